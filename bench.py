@@ -1,0 +1,162 @@
+"""Benchmark of the MI355X MTP E/F/S path (one GPU).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+
+Workload (the metric's configuration): level-16 two-species MTP (radial
+basis size 8, min_dist 1.9 A, cutoff 5.0 A, coefficients U[-0.05, 0.05],
+scaling 0.01) on a 32,000-atom FCC supercell (20x20x20 conventional,
+a = 3.56 A), 75/25 species, symmetric strain +-2 %, Gaussian displacements
+sigma = 0.12 A; synthetic, seeded.
+
+A step is one E/F/S evaluation (energy, forces, stress, site energies) of the
+whole cell with the neighbour lists resident in HBM (the reference fastfit
+"kernel" time).  `value` = atoms * K / wall time of the K timed steps.  The
+roofline entry prices the dominant kernel's algorithmic fp64 flops per launch
+(n_i (8R + 4MR + 4 nu_max + 38B + 24) + 9T + 2S + 2 per atom) against the
+MI355X fp64 peak, over the kernel's mean duration measured with HIP events on
+the library's stream.  The CPU baseline is the oracle's getEFSOMP restatement
+on the host cores.  Prints one JSON line.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "imr-mlp_amd"))
+
+from mtpx import capi  # noqa: E402
+from mtpx import synth as S  # noqa: E402
+
+METRIC = "MTP E/F/S atom-evals/s (lvl16, 32k atoms); train loss+grad configs/s"
+FP64_PEAK_TFLOPS = 78.6
+HBM_PEAK_GBS = 8000.0
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "efs_kernel_lvl16_32k_traffic.json")
+
+
+def efs_flops(model_text: str, n: int, P: int) -> float:
+    t = S.template_topology(model_text)
+    hdr = {k: int(v) for k, v in
+           (l.strip().split(" = ") for l in model_text.splitlines()
+            if l.strip().startswith(("radial_basis_size", "radial_funcs_count")))}
+    R, M = hdr["radial_basis_size"], hdr["radial_funcs_count"]
+    B, T, Sn = len(t["basic"]), len(t["times"]), len(t["map"])
+    nu = int(t["basic"][:, 1:].sum(axis=1).max())
+    per_pair = 8 * R + 4 * M * R + 4 * nu + 32 * B + 6 * B + 24
+    per_site = 9 * T + 2 * Sn + 2
+    return float(P) * per_pair + float(n) * per_site
+
+
+def cpu_baseline(model_text, cell, pbc, pos, types, budget_s: float = 12.0):
+    """The oracle's getEFSOMP restatement timed on the host cores (bounded sample)."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+
+    threads = max(1, min(16, os.cpu_count() or 1))
+    m = O.Model(model_text)
+    nb = O.Neighbors.build(cell, pbc, pos, types, m.cutoff)
+    O.efs(m, nb, threads=threads)  # warm-up
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        O.efs(m, nb, threads=threads)
+        reps += 1
+        el = time.perf_counter() - t0
+        if el > budget_s or reps >= 50:
+            break
+    return {"value": reps * nb.n / el, "unit": "atom-evals/s", "cores": threads, "kind": "port",
+            "sample": "%d full E/F/S evaluations of the 32,000-atom cell (oracle getEFSOMP, "
+                      "prebuilt lists, %d OpenMP threads, %.1f s)" % (reps, threads, el)}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--deterministic", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path "
+              "(see DESIGN.md for how it would shard)", file=sys.stderr)
+        sys.exit(2)
+
+    model_text, s = S.workload_inference(2)
+    pos = capi.wrap(s.cell, s.pbc, s.pos)  # Atoms::wrap, as CalcEFS does before building lists
+    ctx = capi.Context(0)
+    ctx.load_model_text(model_text)
+    cutoff = 5.0
+
+    t0 = time.perf_counter()
+    ctx.build_neighbors(s.cell, s.pbc, pos, s.types, cutoff)
+    nbuild_first = time.perf_counter() - t0
+    n, P = ctx.neighbor_count()
+    det = bool(args.deterministic)
+
+    for _ in range(args.warmup):
+        ctx.efs_device(det)
+    kernel_ms = []
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        ctx.efs_device(det)
+        kernel_ms.append(ctx.last_timings()[1])
+    wall = time.perf_counter() - t0
+    ms_per_step = 1e3 * wall / args.steps
+
+    # "total": neighbour build from host positions + E/F/S (fastfit total_ns_atom)
+    tot = []
+    for _ in range(3):
+        t1 = time.perf_counter()
+        ctx.build_neighbors(s.cell, s.pbc, pos, s.types, cutoff)
+        ctx.efs_device(det)
+        tot.append(time.perf_counter() - t1)
+    E, F, St, _ = ctx.efs(det)
+    ctx.close()
+
+    flops = efs_flops(model_text, n, P)
+    k_ms = float(np.mean(kernel_ms))
+    achieved = flops / (k_ms * 1e-3) / 1e12
+    traffic = None
+    if os.path.exists(TRAFFIC_FILE):
+        traffic = json.load(open(TRAFFIC_FILE)).get("hbm_bytes_per_launch")
+    out = {
+        "metric": METRIC,
+        "value": n * args.steps / wall,
+        "unit": "atom-evals/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f64",
+        "data": "synthetic (seeded FCC supercell and random-coefficient model)",
+        "config": {"workload": "E/F/S, level-16 MTP, 2 species, 32,000-atom FCC 20x20x20 a=3.56, "
+                               "cutoff 5.0, 75/25, strain 2%, sigma 0.12",
+                   "atoms": n, "neighbor_entries": P, "mean_neighbors": P / n,
+                   "deterministic": det},
+        "roofline": {"bound": "mfma", "achieved": achieved, "peak": FP64_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": achieved / FP64_PEAK_TFLOPS, "traffic": traffic,
+                     "kernel": "efs_kernel<4,6,8>", "kernel_ms": k_ms,
+                     "kernel_ms_min": float(np.min(kernel_ms)),
+                     "algorithmic_flops_per_launch": flops,
+                     "note": "fp64 VALU-bound; the MI355X fp64 vector and matrix peaks are both "
+                             "78.6 TFLOP/s"},
+        "extra": {"total_ms_build_plus_efs": 1e3 * float(np.median(tot)),
+                  "neighbor_build_first_ms": 1e3 * nbuild_first,
+                  "energy": E, "max_abs_force": float(np.abs(F).max()),
+                  "train_loss_grad_configs_per_s": None},
+    }
+    if not args.no_cpu:
+        out["cpu_baseline"] = cpu_baseline(model_text, s.cell, s.pbc, pos, s.types)
+    print(json.dumps(out))
+
+
+if __name__ == "__main__":
+    main()

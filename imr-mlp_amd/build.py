@@ -1,0 +1,67 @@
+"""Build libmtpx.so for gfx950 with hipcc (in-tree, no JIT cache).
+
+    python imr-mlp_amd/build.py [-v]
+
+Each translation unit gets its own floating-point contraction policy: the
+neighbour builder and the host geometry are compiled with
+-ffp-contract=off (their results are compared bit for bit with the
+reference), the E/F/S and training kernels with -ffp-contract=fast (FMA).
+"""
+from __future__ import annotations
+
+import os
+import subprocess
+import sys
+import time
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(HERE)
+CSRC = os.path.join(HERE, "csrc")
+LIB_DIR = os.path.join(HERE, "lib")
+LIB = os.path.join(LIB_DIR, "libmtpx.so")
+OBJ_DIR = os.path.join(HERE, "_build")
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+ARCH = "gfx950"
+
+COMMON = ["-O3", "-std=c++17", "-fPIC", "--offload-arch=" + ARCH, "-munsafe-fp-atomics",
+          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+          "-I", os.path.join(ROOT, "include"), "-I", CSRC, "-Wall", "-Wno-unused-function"]
+
+SOURCES = [
+    ("efs_kernel.hip", ["-ffp-contract=fast"]),
+    ("neighbors.hip", ["-ffp-contract=off"]),
+    ("geometry.cpp", ["-ffp-contract=off"]),
+    ("model.cpp", ["-ffp-contract=off"]),
+    ("capi.cpp", ["-ffp-contract=off"]),
+]
+
+
+def sources():
+    return [(s, f) for s, f in SOURCES if os.path.exists(os.path.join(CSRC, s))]
+
+
+def build(verbose: bool = False) -> str:
+    os.makedirs(LIB_DIR, exist_ok=True)
+    os.makedirs(OBJ_DIR, exist_ok=True)
+    objs = []
+    t0 = time.time()
+    for src, flags in sources():
+        obj = os.path.join(OBJ_DIR, src + ".o")
+        cmd = [HIPCC, "-x", "hip", "-c", os.path.join(CSRC, src), "-o", obj] + COMMON + flags
+        if verbose:
+            print(" ".join(cmd), flush=True)
+        subprocess.run(cmd, check=True)
+        objs.append(obj)
+    tmp = LIB + ".tmp"
+    cmd = [HIPCC, "-shared", "-fPIC", "--offload-arch=" + ARCH, "-o", tmp] + objs
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    subprocess.run(cmd, check=True)
+    os.replace(tmp, LIB)
+    if verbose:
+        print("built %s in %.1fs" % (LIB, time.time() - t0), flush=True)
+    return LIB
+
+
+if __name__ == "__main__":
+    build(verbose="-v" in sys.argv)

@@ -1,0 +1,605 @@
+// C ABI (include/mtpx.h): context, device-resident model and neighbour lists,
+// E/F/S launches.  Host code; no exceptions escape.
+#include "mtpx.h"
+#include "mtpx_internal.hpp"
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <new>
+
+using namespace mtpx;
+
+struct mtpx_context {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    std::string err;
+    int num_cus = 256;
+
+    bool has_model = false;
+    Model model;
+    Plan plan;
+    DevModel dm{};
+    // model buffers
+    DBuf radial, species, moment, map, seed, slot_basic, slot_abc, dup, fwd_level, fwd_task,
+        fwd_lr, fwd_c, bwd_level, bwd_task, bwd_oo, bwd_c;
+
+    // neighbour lists
+    bool has_nbh = false;
+    NeighborStore nbh;
+    NeighborScratch scratch;
+    int &n = nbh.n;
+    int64_t &P = nbh.P;
+    DBuf &offsets = nbh.offsets, &idx = nbh.idx, &type = nbh.type, &x = nbh.x, &y = nbh.y,
+         &z = nbh.z, &d = nbh.d, &center_type = nbh.center_type;
+    DBuf rev_offsets, rev_pairs;
+    bool rev_ready = false;
+
+    // outputs
+    DBuf forces, site_energy, partial, pair_ders, out10;
+    int grid = 0;
+
+    hipEvent_t ev[3] = {nullptr, nullptr, nullptr};
+    double timings[4] = {0, 0, 0, 0};
+
+    ~mtpx_context()
+    {
+        for (DBuf *b : {&radial, &species, &moment, &map, &seed, &slot_basic, &slot_abc, &dup,
+                        &fwd_level, &fwd_task, &fwd_lr, &fwd_c, &bwd_level, &bwd_task, &bwd_oo,
+                        &bwd_c, &offsets, &idx, &type, &x, &y, &z, &d, &center_type, &rev_offsets,
+                        &rev_pairs, &forces, &site_energy, &partial, &pair_ders, &out10})
+            b->release();
+        scratch.release_all();
+        for (auto &e : ev)
+            if (e)
+                (void)hipEventDestroy(e);
+        if (stream)
+            (void)hipStreamDestroy(stream);
+    }
+};
+
+namespace {
+
+int set_error(mtpx_context *ctx, int code, const std::string &msg)
+{
+    if (ctx)
+        ctx->err = msg;
+    return code;
+}
+
+int hip_fail(mtpx_context *ctx, hipError_t e, const char *what)
+{
+    return set_error(ctx, e == hipErrorOutOfMemory ? MTPX_E_ALLOC : MTPX_E_DEVICE,
+                     std::string(what) + ": " + hipGetErrorString(e));
+}
+
+#define HIP_TRY(expr, what)                                                                \
+    do {                                                                                   \
+        hipError_t e_ = (expr);                                                            \
+        if (e_ != hipSuccess)                                                              \
+            return hip_fail(ctx, e_, what);                                                \
+    } while (0)
+
+template <class T>
+hipError_t upload(DBuf &b, const std::vector<T> &v, hipStream_t s)
+{
+    hipError_t e = b.ensure(sizeof(T) * std::max<size_t>(v.size(), 1));
+    if (e != hipSuccess || v.empty())
+        return e;
+    return hipMemcpyAsync(b.p, v.data(), sizeof(T) * v.size(), hipMemcpyHostToDevice, s);
+}
+
+// Upload coefficient-dependent arrays: radial, species, moment coefficients
+// and the adjoint seeds (sum of the moment coefficients mapped to a moment,
+// accumulated in scalar order as potential_mtp.cpp:2974-2977 does).
+int upload_coeffs(mtpx_context *ctx)
+{
+    const Model &m = ctx->model;
+    std::vector<double> radial(m.coef.begin(), m.coef.begin() + m.nradial());
+    std::vector<double> species(m.coef.begin() + m.nradial(), m.coef.begin() + m.nradial() + m.Z);
+    std::vector<double> moment(m.coef.begin() + m.nradial() + m.Z, m.coef.end());
+    std::vector<double> seed((size_t)m.K, 0.0);
+    for (int s = 0; s < m.S; ++s)
+        seed[m.map[s]] += moment[s];
+    HIP_TRY(upload(ctx->radial, radial, ctx->stream), "upload radial coefficients");
+    HIP_TRY(upload(ctx->species, species, ctx->stream), "upload species coefficients");
+    HIP_TRY(upload(ctx->moment, moment, ctx->stream), "upload moment coefficients");
+    HIP_TRY(upload(ctx->seed, seed, ctx->stream), "upload adjoint seeds");
+    HIP_TRY(hipStreamSynchronize(ctx->stream), "upload coefficients");
+    ctx->dm.radial = ctx->radial.as<double>();
+    ctx->dm.species = ctx->species.as<double>();
+    ctx->dm.moment = ctx->moment.as<double>();
+    ctx->dm.seed = ctx->seed.as<double>();
+    return MTPX_OK;
+}
+
+int install_model(mtpx_context *ctx, Model &&m)
+{
+    std::string err;
+    if (!validate_model(m, err))
+        return set_error(ctx, MTPX_E_MODEL, err);
+    Plan p;
+    if (!build_plan(m, p, err))
+        return set_error(ctx, MTPX_E_MODEL, err);
+    ctx->model = std::move(m);
+    ctx->plan = std::move(p);
+    const Model &M = ctx->model;
+    const Plan &P = ctx->plan;
+    DevModel &dm = ctx->dm;
+    dm = DevModel{};
+    dm.Z = M.Z;
+    dm.M = M.M;
+    dm.R = M.R;
+    dm.K = M.K;
+    dm.B = M.B;
+    dm.T = M.T;
+    dm.S = M.S;
+    dm.nslots = P.nslots;
+    dm.rmin = M.rmin;
+    dm.rmax = M.rmax;
+    dm.scaling = M.scaling;
+    // RBasis_Chebyshev::setup (basis/basis.cpp:119-125)
+    dm.mult = 2.0 / (M.rmax - M.rmin);
+    dm.su = M.rmax - M.rmin;
+    dm.pu = M.rmax + M.rmin;
+    for (int mu = 0; mu < kMaxMu; ++mu)
+        dm.numax[mu] = P.numax[mu];
+    dm.numax_all = P.numax_all;
+    dm.ndup = (int)P.dup.size() / 2;
+    dm.nfwd = (int)P.fwd_level.size() - 1;
+    dm.nbwd = (int)P.bwd_level.size() - 1;
+    hipStream_t s = ctx->stream;
+    HIP_TRY(upload(ctx->map, M.map, s), "upload model");
+    HIP_TRY(upload(ctx->slot_basic, P.slot_basic, s), "upload model");
+    HIP_TRY(upload(ctx->slot_abc, P.slot_abc, s), "upload model");
+    HIP_TRY(upload(ctx->dup, P.dup, s), "upload model");
+    HIP_TRY(upload(ctx->fwd_level, P.fwd_level, s), "upload model");
+    HIP_TRY(upload(ctx->fwd_task, P.fwd_task, s), "upload model");
+    HIP_TRY(upload(ctx->fwd_lr, P.fwd_lr, s), "upload model");
+    HIP_TRY(upload(ctx->fwd_c, P.fwd_c, s), "upload model");
+    HIP_TRY(upload(ctx->bwd_level, P.bwd_level, s), "upload model");
+    HIP_TRY(upload(ctx->bwd_task, P.bwd_task, s), "upload model");
+    HIP_TRY(upload(ctx->bwd_oo, P.bwd_oo, s), "upload model");
+    HIP_TRY(upload(ctx->bwd_c, P.bwd_c, s), "upload model");
+    dm.map = ctx->map.as<int>();
+    dm.slot_basic = ctx->slot_basic.as<int>();
+    dm.slot_abc = ctx->slot_abc.as<int>();
+    dm.dup = ctx->dup.as<int>();
+    dm.fwd_level = ctx->fwd_level.as<int>();
+    dm.fwd_task = ctx->fwd_task.as<int4>();
+    dm.fwd_lr = ctx->fwd_lr.as<int>();
+    dm.fwd_c = ctx->fwd_c.as<double>();
+    dm.bwd_level = ctx->bwd_level.as<int>();
+    dm.bwd_task = ctx->bwd_task.as<int4>();
+    dm.bwd_oo = ctx->bwd_oo.as<int>();
+    dm.bwd_c = ctx->bwd_c.as<double>();
+    if (efs_lds_bytes(dm) > 160 * 1024)
+        return set_error(ctx, MTPX_E_CAPACITY, "model needs more LDS than a CU provides");
+    int rc = upload_coeffs(ctx);
+    if (rc != MTPX_OK)
+        return rc;
+    ctx->has_model = true;
+    return MTPX_OK;
+}
+
+DevNeighbors dev_neighbors(const mtpx_context *ctx)
+{
+    DevNeighbors nb;
+    nb.n = ctx->n;
+    nb.P = ctx->P;
+    nb.offsets = ctx->offsets.as<int>();
+    nb.idx = ctx->idx.as<int>();
+    nb.type = ctx->type.as<int>();
+    nb.x = ctx->x.as<double>();
+    nb.y = ctx->y.as<double>();
+    nb.z = ctx->z.as<double>();
+    nb.d = ctx->d.as<double>();
+    nb.center_type = ctx->center_type.as<int>();
+    return nb;
+}
+
+// Ordered reverse index: for each atom k, the pairs p with idx[p] == k, in
+// ascending p (used by the deterministic force gather).
+int build_reverse_index(mtpx_context *ctx, const int *idx_host)
+{
+    std::vector<int> roff((size_t)ctx->n + 1, 0), rp((size_t)std::max<int64_t>(ctx->P, 1));
+    for (int64_t p = 0; p < ctx->P; ++p)
+        roff[(size_t)idx_host[p] + 1]++;
+    for (int k = 0; k < ctx->n; ++k)
+        roff[k + 1] += roff[k];
+    std::vector<int> cur(roff.begin(), roff.end() - 1);
+    for (int64_t p = 0; p < ctx->P; ++p)
+        rp[(size_t)cur[idx_host[p]]++] = (int)p;
+    HIP_TRY(upload(ctx->rev_offsets, roff, ctx->stream), "upload reverse index");
+    HIP_TRY(upload(ctx->rev_pairs, rp, ctx->stream), "upload reverse index");
+    HIP_TRY(hipStreamSynchronize(ctx->stream), "upload reverse index");
+    ctx->rev_ready = true;
+    return MTPX_OK;
+}
+
+int run_efs(mtpx_context *ctx, bool deterministic)
+{
+    if (!ctx->has_model)
+        return set_error(ctx, MTPX_E_NO_MODEL, "no model loaded");
+    if (!ctx->has_nbh)
+        return set_error(ctx, MTPX_E_NO_TOPOLOGY, "no neighbour lists");
+    if (deterministic && !ctx->rev_ready) {
+        std::vector<int> idx_host((size_t)std::max<int64_t>(ctx->P, 1));
+        if (ctx->P > 0)
+            HIP_TRY(hipMemcpy(idx_host.data(), ctx->idx.p, sizeof(int) * ctx->P,
+                              hipMemcpyDeviceToHost),
+                    "copy neighbour indices");
+        int rc = build_reverse_index(ctx, idx_host.data());
+        if (rc != MTPX_OK)
+            return rc;
+    }
+    const int n = ctx->n;
+    hipStream_t s = ctx->stream;
+    int per_cu = 0;
+    const size_t lds = efs_lds_bytes(ctx->dm);
+    // workgroups per CU the LDS budget allows; register limits cap it further
+    per_cu = std::max(1, std::min(8, (int)((160 * 1024) / std::max<size_t>(lds, 1))));
+    ctx->grid = std::max(1, std::min(n, ctx->num_cus * per_cu));
+    HIP_TRY(ctx->forces.ensure(sizeof(double) * 3 * std::max(n, 1)), "allocate forces");
+    HIP_TRY(ctx->site_energy.ensure(sizeof(double) * std::max(n, 1)), "allocate site energies");
+    HIP_TRY(ctx->partial.ensure(sizeof(double) * 10 * ctx->grid), "allocate partials");
+    HIP_TRY(ctx->out10.ensure(sizeof(double) * 10), "allocate outputs");
+    if (deterministic)
+        HIP_TRY(ctx->pair_ders.ensure(sizeof(double) * 3 * std::max<int64_t>(ctx->P, 1)),
+                "allocate pair derivatives");
+    EfsOut out;
+    out.forces = ctx->forces.as<double>();
+    out.site_energy = ctx->site_energy.as<double>();
+    out.partial = ctx->partial.as<double>();
+    out.pair_ders = deterministic ? ctx->pair_ders.as<double>() : nullptr;
+    DevNeighbors nb = dev_neighbors(ctx);
+    if (!deterministic && n > 0)
+        HIP_TRY(hipMemsetAsync(out.forces, 0, sizeof(double) * 3 * n, s), "clear forces");
+    HIP_TRY(hipEventRecord(ctx->ev[0], s), "record event");
+    if (n > 0)
+        HIP_TRY(launch_efs(ctx->dm, nb, out, ctx->grid, deterministic, s), "launch efs kernel");
+    HIP_TRY(hipEventRecord(ctx->ev[1], s), "record event");
+    if (n > 0)
+        HIP_TRY(launch_efs_finish(nb, out, ctx->grid, deterministic, ctx->rev_offsets.as<int>(),
+                                  ctx->rev_pairs.as<int>(), ctx->out10.as<double>(), s),
+                "launch efs reductions");
+    else
+        HIP_TRY(hipMemsetAsync(ctx->out10.p, 0, sizeof(double) * 10, s), "clear outputs");
+    HIP_TRY(hipEventRecord(ctx->ev[2], s), "record event");
+    HIP_TRY(hipEventSynchronize(ctx->ev[2]), "efs");
+    float t01 = 0, t12 = 0, t02 = 0;
+    (void)hipEventElapsedTime(&t01, ctx->ev[0], ctx->ev[1]);
+    (void)hipEventElapsedTime(&t12, ctx->ev[1], ctx->ev[2]);
+    (void)hipEventElapsedTime(&t02, ctx->ev[0], ctx->ev[2]);
+    ctx->timings[0] = t02;
+    ctx->timings[1] = t01;
+    ctx->timings[2] = t12;
+    ctx->timings[3] = 0;
+    return MTPX_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char *mtpx_version(void)
+{
+    return "mtpx 0.1 gfx950 fp64 (efs variants: M4/nu6/R8, M5/nu8/R10, M8/nu8/R16)";
+}
+
+int mtpx_create(int device, mtpx_context **out)
+{
+    if (!out)
+        return MTPX_E_INVALID;
+    *out = nullptr;
+    int count = 0;
+    if (hipGetDeviceCount(&count) != hipSuccess || device < 0 || device >= count)
+        return MTPX_E_DEVICE;
+    mtpx_context *ctx = new (std::nothrow) mtpx_context();
+    if (!ctx)
+        return MTPX_E_ALLOC;
+    ctx->device = device;
+    if (hipSetDevice(device) != hipSuccess || hipStreamCreate(&ctx->stream) != hipSuccess) {
+        delete ctx;
+        return MTPX_E_DEVICE;
+    }
+    for (auto &e : ctx->ev)
+        if (hipEventCreate(&e) != hipSuccess) {
+            delete ctx;
+            return MTPX_E_DEVICE;
+        }
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, device) == hipSuccess && prop.multiProcessorCount > 0)
+        ctx->num_cus = prop.multiProcessorCount;
+    *out = ctx;
+    return MTPX_OK;
+}
+
+void mtpx_destroy(mtpx_context *ctx)
+{
+    if (!ctx)
+        return;
+    (void)hipSetDevice(ctx->device);
+    if (ctx->stream)
+        (void)hipStreamSynchronize(ctx->stream);
+    delete ctx;
+}
+
+const char *mtpx_last_error(const mtpx_context *ctx)
+{
+    return ctx ? ctx->err.c_str() : "null context";
+}
+
+int mtpx_load_model(mtpx_context *ctx, const mtpx_model_view *v)
+{
+    if (!ctx || !v)
+        return set_error(ctx, MTPX_E_INVALID, "null argument");
+    if (v->species_count <= 0 || v->radial_func_count <= 0 || v->rb_size <= 0 ||
+        v->alpha_index_basic_count <= 0 || v->alpha_moments_count <= 0 ||
+        v->alpha_index_times_count < 0 || v->alpha_scalar_moments < 0 || !v->alpha_index_basic ||
+        (v->alpha_index_times_count > 0 && !v->alpha_index_times) ||
+        (v->alpha_scalar_moments > 0 && (!v->alpha_moment_mapping || !v->moment_coeffs)) ||
+        !v->radial_coeffs || !v->species_coeffs)
+        return set_error(ctx, MTPX_E_INVALID, "incomplete model view");
+    Model m;
+    m.Z = v->species_count;
+    m.M = v->radial_func_count;
+    m.R = v->rb_size;
+    m.rmin = v->min_dist;
+    m.rmax = v->max_dist;
+    m.scaling = v->scaling;
+    m.K = v->alpha_moments_count;
+    m.B = v->alpha_index_basic_count;
+    m.T = v->alpha_index_times_count;
+    m.S = v->alpha_scalar_moments;
+    m.basic.assign(v->alpha_index_basic, v->alpha_index_basic + 4 * m.B);
+    m.times.assign(v->alpha_index_times, v->alpha_index_times + 4 * m.T);
+    m.map.assign(v->alpha_moment_mapping, v->alpha_moment_mapping + m.S);
+    m.coef.assign(v->radial_coeffs, v->radial_coeffs + m.nradial());
+    m.coef.insert(m.coef.end(), v->species_coeffs, v->species_coeffs + m.Z);
+    m.coef.insert(m.coef.end(), v->moment_coeffs, v->moment_coeffs + m.S);
+    (void)hipSetDevice(ctx->device);
+    return install_model(ctx, std::move(m));
+}
+
+int mtpx_load_model_text(mtpx_context *ctx, const char *text)
+{
+    if (!ctx || !text)
+        return set_error(ctx, MTPX_E_INVALID, "null argument");
+    Model m;
+    std::string err;
+    if (!parse_mtp(text, m, err))
+        return set_error(ctx, MTPX_E_MODEL, err);
+    (void)hipSetDevice(ctx->device);
+    return install_model(ctx, std::move(m));
+}
+
+int mtpx_parse_model_text(const char *text, int out8[8], double *coeffs, char *err, int errlen)
+{
+    if (!text)
+        return MTPX_E_INVALID;
+    Model m;
+    std::string e;
+    if (!parse_mtp(text, m, e)) {
+        if (err && errlen > 0) {
+            std::strncpy(err, e.c_str(), (size_t)errlen - 1);
+            err[errlen - 1] = 0;
+        }
+        return MTPX_E_MODEL;
+    }
+    if (out8) {
+        const int v[8] = {m.Z, m.M, m.R, m.K, m.B, m.T, m.S, m.ncoef()};
+        std::memcpy(out8, v, sizeof v);
+    }
+    if (coeffs)
+        std::memcpy(coeffs, m.coef.data(), sizeof(double) * m.coef.size());
+    return MTPX_OK;
+}
+
+int mtpx_model_info(const mtpx_context *ctx, int out8[8])
+{
+    if (!ctx || !out8)
+        return MTPX_E_INVALID;
+    if (!ctx->has_model)
+        return MTPX_E_NO_MODEL;
+    const Model &m = ctx->model;
+    const int v[8] = {m.Z, m.M, m.R, m.K, m.B, m.T, m.S, m.ncoef()};
+    std::memcpy(out8, v, sizeof v);
+    return MTPX_OK;
+}
+
+int mtpx_get_coeffs(const mtpx_context *ctx, double *coeffs)
+{
+    if (!ctx || !coeffs)
+        return MTPX_E_INVALID;
+    if (!ctx->has_model)
+        return MTPX_E_NO_MODEL;
+    std::memcpy(coeffs, ctx->model.coef.data(), sizeof(double) * ctx->model.coef.size());
+    return MTPX_OK;
+}
+
+int mtpx_set_coeffs(mtpx_context *ctx, const double *coeffs)
+{
+    if (!ctx || !coeffs)
+        return set_error(ctx, MTPX_E_INVALID, "null argument");
+    if (!ctx->has_model)
+        return set_error(ctx, MTPX_E_NO_MODEL, "no model loaded");
+    std::memcpy(ctx->model.coef.data(), coeffs, sizeof(double) * ctx->model.coef.size());
+    (void)hipSetDevice(ctx->device);
+    return upload_coeffs(ctx);
+}
+
+int mtpx_set_neighbors(mtpx_context *ctx, int n, const int *offsets, const int *indices,
+                       const int *types, const double *vecs, const double *dists,
+                       const int *center_types)
+{
+    if (!ctx)
+        return MTPX_E_INVALID;
+    if (n < 0 || !offsets || (n > 0 && !center_types))
+        return set_error(ctx, MTPX_E_INVALID, "invalid neighbour arrays");
+    if (offsets[0] != 0)
+        return set_error(ctx, MTPX_E_INVALID, "offsets must start at 0");
+    for (int i = 0; i < n; ++i)
+        if (offsets[i + 1] < offsets[i])
+            return set_error(ctx, MTPX_E_INVALID, "offsets must be non-decreasing");
+    const int64_t P = offsets[n];
+    if (P > 0 && (!indices || !types || !vecs || !dists))
+        return set_error(ctx, MTPX_E_INVALID, "invalid neighbour arrays");
+    int Z = ctx->has_model ? ctx->model.Z : 1 << 30;
+    for (int64_t p = 0; p < P; ++p) {
+        if (indices[p] < 0 || indices[p] >= n)
+            return set_error(ctx, MTPX_E_INVALID, "neighbour index out of range");
+        if (types[p] < 0 || types[p] >= Z)
+            return set_error(ctx, MTPX_E_INVALID, "neighbour species out of range");
+    }
+    for (int i = 0; i < n; ++i)
+        if (center_types[i] < 0 || center_types[i] >= Z)
+            return set_error(ctx, MTPX_E_INVALID, "centre species out of range");
+    (void)hipSetDevice(ctx->device);
+    ctx->has_nbh = false;
+    ctx->rev_ready = false;
+    std::vector<double> xs((size_t)P), ys((size_t)P), zs((size_t)P);
+    for (int64_t p = 0; p < P; ++p) {
+        xs[p] = vecs[3 * p];
+        ys[p] = vecs[3 * p + 1];
+        zs[p] = vecs[3 * p + 2];
+    }
+    hipStream_t s = ctx->stream;
+    HIP_TRY(upload(ctx->offsets, std::vector<int>(offsets, offsets + n + 1), s), "upload lists");
+    HIP_TRY(upload(ctx->idx, std::vector<int>(indices, indices + P), s), "upload lists");
+    HIP_TRY(upload(ctx->type, std::vector<int>(types, types + P), s), "upload lists");
+    HIP_TRY(upload(ctx->x, xs, s), "upload lists");
+    HIP_TRY(upload(ctx->y, ys, s), "upload lists");
+    HIP_TRY(upload(ctx->z, zs, s), "upload lists");
+    HIP_TRY(upload(ctx->d, std::vector<double>(dists, dists + P), s), "upload lists");
+    HIP_TRY(upload(ctx->center_type, std::vector<int>(center_types, center_types + n), s),
+            "upload lists");
+    HIP_TRY(hipStreamSynchronize(s), "upload lists");
+    ctx->n = n;
+    ctx->P = P;
+    ctx->has_nbh = true;
+    return MTPX_OK;
+}
+
+int mtpx_build_neighbors(mtpx_context *ctx, const double cell[9], const int pbc[3], int n,
+                         const double *pos, const int *types, double cutoff)
+{
+    if (!ctx)
+        return MTPX_E_INVALID;
+    if (!cell || !pbc || n < 0 || (n > 0 && (!pos || !types)) || !(cutoff > 0) ||
+        !std::isfinite(cutoff))
+        return set_error(ctx, MTPX_E_INVALID, "invalid neighbour-build arguments");
+    for (int i = 0; i < 9; ++i)
+        if (!std::isfinite(cell[i]))
+            return set_error(ctx, MTPX_E_INVALID, "non-finite cell");
+    for (int i = 0; i < 3 * n; ++i)
+        if (!std::isfinite(pos[i]))
+            return set_error(ctx, MTPX_E_INVALID, "non-finite position");
+    const int Z = ctx->has_model ? ctx->model.Z : 1 << 30;
+    for (int i = 0; i < n; ++i)
+        if (types[i] < 0 || types[i] >= Z)
+            return set_error(ctx, MTPX_E_INVALID, "species out of range");
+    (void)hipSetDevice(ctx->device);
+    ctx->has_nbh = false;
+    ctx->rev_ready = false;
+    std::string err;
+    int rc = build_neighbors_gpu(cell, pbc, n, pos, types, cutoff, ctx->stream, ctx->nbh,
+                                 ctx->scratch, err);
+    if (rc != MTPX_OK)
+        return set_error(ctx, rc, err);
+    ctx->has_nbh = true;
+    return MTPX_OK;
+}
+
+int mtpx_neighbor_count(const mtpx_context *ctx, int64_t *entries, int *centers)
+{
+    if (!ctx)
+        return MTPX_E_INVALID;
+    if (!ctx->has_nbh)
+        return MTPX_E_NO_TOPOLOGY;
+    if (entries)
+        *entries = ctx->P;
+    if (centers)
+        *centers = ctx->n;
+    return MTPX_OK;
+}
+
+int mtpx_get_neighbors(const mtpx_context *ctx_c, int *offsets, int *indices, int *types,
+                       double *vecs, double *dists, int *center_types)
+{
+    mtpx_context *ctx = const_cast<mtpx_context *>(ctx_c);
+    if (!ctx)
+        return MTPX_E_INVALID;
+    if (!ctx->has_nbh)
+        return set_error(ctx, MTPX_E_NO_TOPOLOGY, "no neighbour lists");
+    (void)hipSetDevice(ctx->device);
+    const int n = ctx->n;
+    const int64_t P = ctx->P;
+    auto d2h = [&](void *dst, const DBuf &src, size_t bytes) {
+        return bytes ? hipMemcpy(dst, src.p, bytes, hipMemcpyDeviceToHost) : hipSuccess;
+    };
+    if (offsets)
+        HIP_TRY(d2h(offsets, ctx->offsets, sizeof(int) * (n + 1)), "copy lists");
+    if (indices)
+        HIP_TRY(d2h(indices, ctx->idx, sizeof(int) * P), "copy lists");
+    if (types)
+        HIP_TRY(d2h(types, ctx->type, sizeof(int) * P), "copy lists");
+    if (dists)
+        HIP_TRY(d2h(dists, ctx->d, sizeof(double) * P), "copy lists");
+    if (center_types)
+        HIP_TRY(d2h(center_types, ctx->center_type, sizeof(int) * n), "copy lists");
+    if (vecs) {
+        std::vector<double> c((size_t)P);
+        for (int a = 0; a < 3; ++a) {
+            const DBuf &b = a == 0 ? ctx->x : a == 1 ? ctx->y : ctx->z;
+            HIP_TRY(d2h(c.data(), b, sizeof(double) * P), "copy lists");
+            for (int64_t p = 0; p < P; ++p)
+                vecs[3 * p + a] = c[p];
+        }
+    }
+    return MTPX_OK;
+}
+
+int mtpx_efs_device(mtpx_context *ctx, int deterministic)
+{
+    if (!ctx)
+        return MTPX_E_INVALID;
+    (void)hipSetDevice(ctx->device);
+    return run_efs(ctx, deterministic != 0);
+}
+
+int mtpx_efs(mtpx_context *ctx, int deterministic, double *energy, double *forces, double *stress,
+             double *site_energies)
+{
+    if (!ctx)
+        return MTPX_E_INVALID;
+    (void)hipSetDevice(ctx->device);
+    int rc = run_efs(ctx, deterministic != 0);
+    if (rc != MTPX_OK)
+        return rc;
+    double o10[10];
+    HIP_TRY(hipMemcpy(o10, ctx->out10.p, sizeof o10, hipMemcpyDeviceToHost), "copy outputs");
+    if (energy)
+        *energy = o10[0];
+    if (stress)
+        std::memcpy(stress, o10 + 1, 9 * sizeof(double));
+    if (forces && ctx->n > 0)
+        HIP_TRY(hipMemcpy(forces, ctx->forces.p, sizeof(double) * 3 * ctx->n,
+                          hipMemcpyDeviceToHost),
+                "copy forces");
+    if (site_energies && ctx->n > 0)
+        HIP_TRY(hipMemcpy(site_energies, ctx->site_energy.p, sizeof(double) * ctx->n,
+                          hipMemcpyDeviceToHost),
+                "copy site energies");
+    return MTPX_OK;
+}
+
+int mtpx_last_timings(const mtpx_context *ctx, double out_ms[4])
+{
+    if (!ctx || !out_ms)
+        return MTPX_E_INVALID;
+    std::memcpy(out_ms, ctx->timings, sizeof ctx->timings);
+    return MTPX_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,428 @@
+// Model I/O and the contraction-graph launch plan (host code).
+//
+// parse_mtp follows the PotMTP::Load grammar (potentials/potential_mtp.cpp:
+// 119-571) for non-split RBChebyshev models: optional potential_name,
+// optional scaling (default 0.01, :155), species_count, optional
+// potential_tag line, radial basis block, optional radial_coeffs (default
+// 1e-5 with 1e-3 + k on the channel diagonal, :335-351), the alpha_* tables,
+// optional species/moment coefficients (default 1e-3, :471-474).
+#include "mtpx_internal.hpp"
+
+#include <algorithm>
+#include <cmath>
+#include <cstdlib>
+#include <cstring>
+#include <sstream>
+
+namespace mtpx {
+
+namespace {
+
+// A cursor with std::istream extraction semantics over the model text.
+class Cursor {
+  public:
+    explicit Cursor(const std::string &t) : s_(t) {}
+    bool ok() const { return ok_; }
+    void clear() { ok_ = true; }
+    std::string line()
+    {
+        size_t e = s_.find('\n', p_);
+        std::string l = s_.substr(p_, e == std::string::npos ? std::string::npos : e - p_);
+        p_ = e == std::string::npos ? s_.size() : e + 1;
+        if (!l.empty() && l.back() == '\r')
+            l.pop_back();
+        return l;
+    }
+    std::string word()
+    {
+        ws();
+        size_t b = p_;
+        while (p_ < s_.size() && !std::isspace((unsigned char)s_[p_]))
+            ++p_;
+        if (p_ == b)
+            ok_ = false;
+        return s_.substr(b, p_ - b);
+    }
+    void skip(int n) { p_ = std::min(s_.size(), p_ + (size_t)n); }
+    void skip_past(char delim, int limit)
+    {
+        while (limit-- > 0 && p_ < s_.size())
+            if (s_[p_++] == delim)
+                return;
+    }
+    double real()
+    {
+        ws();
+        const char *b = s_.c_str() + p_;
+        char *e = nullptr;
+        double v = std::strtod(b, &e);
+        if (e == b)
+            ok_ = false;
+        p_ += (size_t)(e - b);
+        return v;
+    }
+    int integer()
+    {
+        ws();
+        const char *b = s_.c_str() + p_;
+        char *e = nullptr;
+        long v = std::strtol(b, &e, 10);
+        if (e == b)
+            ok_ = false;
+        p_ += (size_t)(e - b);
+        return (int)v;
+    }
+    char ch()
+    {
+        ws();
+        if (p_ >= s_.size()) {
+            ok_ = false;
+            return 0;
+        }
+        return s_[p_++];
+    }
+
+  private:
+    void ws()
+    {
+        while (p_ < s_.size() && std::isspace((unsigned char)s_[p_]))
+            ++p_;
+    }
+    const std::string &s_;
+    size_t p_ = 0;
+    bool ok_ = true;
+};
+
+bool fail(std::string &err, const char *msg)
+{
+    err = msg;
+    return false;
+}
+
+}  // namespace
+
+bool parse_mtp(const std::string &text, Model &m, std::string &err)
+{
+    m = Model();
+    Cursor in(text);
+    if (in.line() != "MTP")
+        return fail(err, "Can only read MTP format potentials");
+    if (in.line() != "version = 1.1.0")
+        return fail(err, "MTP file must have version \"1.1.0\"");
+    std::string key = in.word();
+    if (key == "potential_name") {
+        in.skip(2);
+        in.word();
+        key = in.word();
+    }
+    m.scaling = 0.01;
+    if (key == "scaling") {
+        in.skip(2);
+        m.scaling = in.real();
+        key = in.word();
+    }
+    if (key != "species_count")
+        return fail(err, "Error reading .mtp file, no species_count tag found");
+    in.skip(2);
+    m.Z = in.integer();
+    if (!in.ok() || m.Z <= 0)
+        return fail(err, "Error reading .mtp file, invalid species_count");
+    key = in.word();
+    if (key == "potential_tag") {
+        if (in.line().find('=') == std::string::npos)
+            return fail(err, "Invalid potential_tag assignment");
+        key = in.word();
+    }
+    if (key == "radial_split" || key == "radial_basis_split") {
+        in.skip(2);
+        if (in.integer() != 0)
+            return fail(err, "split radial bases are not supported");
+        key = in.word();
+    }
+    if (key != "radial_basis_type")
+        return fail(err, "Error reading .mtp file");
+    in.skip(2);
+    if (in.word() != "RBChebyshev")
+        return fail(err, "only RBChebyshev radial bases are supported");
+    if (in.word() != "min_dist")
+        return fail(err, "Error in loading basis: min_dist");
+    in.skip(2);
+    m.rmin = in.real();
+    if (in.word() != "max_dist")
+        return fail(err, "Error in loading basis: max_dist");
+    in.skip(2);
+    m.rmax = in.real();
+    if (in.word() != "radial_basis_size")
+        return fail(err, "Error in loading basis: radial_basis_size");
+    in.skip(2);
+    m.R = in.integer();
+    if (!in.ok() || m.R <= 0)
+        return fail(err, "Error in loading basis: radial_basis_size must be positive");
+    if (in.word() != "radial_funcs_count")
+        return fail(err, "Error reading .mtp file");
+    in.skip(2);
+    m.M = in.integer();
+    if (!in.ok() || m.M < 0)
+        return fail(err, "Error reading .mtp file, invalid radial basis dimensions");
+
+    const int Z = m.Z, M = m.M, R = m.R;
+    std::vector<double> radial((size_t)Z * Z * M * R, 0.0);
+    key = in.word();
+    if (key == "radial_coeffs") {
+        for (int p = 0; p < Z * Z; ++p) {
+            int a = in.integer();
+            in.ch();
+            int b = in.integer();
+            if (!in.ok() || a < 0 || a >= Z || b < 0 || b >= Z)
+                return fail(err, "Error reading .mtp file, invalid radial coefficient pair");
+            for (int mu = 0; mu < M; ++mu) {
+                in.ch();
+                for (int k = 0; k < R; ++k) {
+                    double v = in.real();
+                    in.ch();
+                    if (!in.ok())
+                        return fail(err, "Error reading .mtp file, missing radial coefficient");
+                    radial[((size_t)(a * Z + b) * M + mu) * R + k] = v;
+                }
+            }
+        }
+        key = in.word();
+    } else {
+        for (int p = 0; p < Z * Z; ++p)
+            for (int mu = 0; mu < M; ++mu) {
+                for (int k = 0; k < R; ++k)
+                    radial[((size_t)p * M + mu) * R + k] = 1e-5;
+                radial[((size_t)p * M + mu) * R + std::min(mu, R - 1)] = 1e-3 + mu;
+            }
+    }
+    if (key != "alpha_moments_count")
+        return fail(err, "Error reading .mtp file, except: alpha_moments_count");
+    in.skip(2);
+    m.K = in.integer();
+    if (in.word() != "alpha_index_basic_count")
+        return fail(err, "Error reading .mtp file");
+    in.skip(2);
+    m.B = in.integer();
+    if (!in.ok() || in.word() != "alpha_index_basic" || m.B < 0)
+        return fail(err, "Error reading .mtp file");
+    in.skip(4);
+    m.basic.resize((size_t)m.B * 4);
+    int mu_max = -1;
+    for (int i = 0; i < m.B; ++i) {
+        in.skip_past('{', 1000);
+        for (int q = 0; q < 4; ++q) {
+            m.basic[4 * i + q] = in.integer();
+            if (q < 3)
+                in.ch();
+        }
+        if (!in.ok())
+            return fail(err, "Error reading .mtp file");
+        mu_max = std::max(mu_max, m.basic[4 * i]);
+    }
+    if (mu_max != M - 1)
+        return fail(err, "Wrong number of radial functions specified");
+    in.skip_past('\n', 1000);
+    if (in.word() != "alpha_index_times_count")
+        return fail(err, "Error reading .mtp file");
+    in.skip(2);
+    m.T = in.integer();
+    if (!in.ok() || in.word() != "alpha_index_times" || m.T < 0)
+        return fail(err, "Error reading .mtp file");
+    in.skip(4);
+    m.times.resize((size_t)m.T * 4);
+    for (int i = 0; i < m.T; ++i) {
+        in.skip_past('{', 1000);
+        for (int q = 0; q < 4; ++q) {
+            m.times[4 * i + q] = in.integer();
+            if (q < 3)
+                in.ch();
+        }
+        if (!in.ok())
+            return fail(err, "Error reading .mtp file");
+    }
+    in.skip_past('\n', 1000);
+    if (in.word() != "alpha_scalar_moments")
+        return fail(err, "Error reading .mtp file");
+    in.skip(2);
+    m.S = in.integer();
+    if (!in.ok() || in.word() != "alpha_moment_mapping" || m.S < 0)
+        return fail(err, "Error reading .mtp file");
+    in.skip(4);
+    m.map.resize((size_t)m.S);
+    for (int i = 0; i < m.S; ++i) {
+        m.map[i] = in.integer();
+        in.ch();
+        if (!in.ok())
+            return fail(err, "Error reading .mtp file");
+    }
+    in.skip_past('\n', 1000);
+
+    m.coef.assign((size_t)m.ncoef(), 1e-3);
+    std::copy(radial.begin(), radial.end(), m.coef.begin());
+    double *lin = m.coef.data() + m.nradial();
+    key = in.word();
+    in.clear();
+    if (key == "species_coeffs") {
+        in.skip(4);
+        for (int i = 0; i < Z; ++i) {
+            lin[i] = in.real();
+            in.ch();
+            if (!in.ok())
+                return fail(err, "Error reading .mtp file, missing species coefficient");
+        }
+        in.skip_past('\n', 1000);
+        key = in.word();
+        in.clear();
+    }
+    if (key == "moment_coeffs") {
+        in.skip(2);
+        in.skip_past('{', 10);
+        for (int i = 0; i < m.S; ++i) {
+            lin[Z + i] = in.real();
+            in.ch();
+            if (!in.ok())
+                return fail(err, "Error reading .mtp file, missing moment coefficient");
+        }
+    }
+    return validate_model(m, err);
+}
+
+bool validate_model(const Model &m, std::string &err)
+{
+    if (m.Z <= 0 || m.M < 1 || m.R <= 0 || m.B < 1 || m.K < m.B || m.T < 0 || m.S < 0)
+        return fail(err, "invalid model sizes");
+    if (m.M > kMaxMu)
+        return fail(err, "radial_funcs_count exceeds the supported maximum (8)");
+    if (m.R > kMaxR)
+        return fail(err, "radial_basis_size exceeds the supported maximum (16)");
+    if (m.K > 65535)
+        return fail(err, "alpha_moments_count exceeds the supported maximum (65535)");
+    if (!(m.rmax > m.rmin) || !std::isfinite(m.rmin) || !std::isfinite(m.rmax))
+        return fail(err, "invalid radial basis interval");
+    if ((int)m.basic.size() != 4 * m.B || (int)m.times.size() != 4 * m.T ||
+        (int)m.map.size() != m.S || (int)m.coef.size() != m.ncoef())
+        return fail(err, "inconsistent model array sizes");
+    for (int i = 0; i < m.B; ++i) {
+        const int *b = &m.basic[4 * i];
+        if (b[0] < 0 || b[0] >= m.M || b[1] < 0 || b[2] < 0 || b[3] < 0)
+            return fail(err, "basic moment index out of range");
+        if (b[1] + b[2] + b[3] > kMaxNu)
+            return fail(err, "basic moment degree exceeds the supported maximum (8)");
+    }
+    for (int t = 0; t < m.T; ++t) {
+        const int *r = &m.times[4 * t];
+        if (r[0] < 0 || r[0] >= m.K || r[1] < 0 || r[1] >= m.K || r[3] < 0 || r[3] >= m.K)
+            return fail(err, "product rule index out of range");
+        if (r[3] < m.B)
+            return fail(err, "a product rule writes a basic moment");
+    }
+    for (int s = 0; s < m.S; ++s)
+        if (m.map[s] < 0 || m.map[s] >= m.K)
+            return fail(err, "scalar moment mapping out of range");
+    return true;
+}
+
+// Canonical slot order shared with the kernels: for nu ascending, for mu
+// ascending (mu with numax[mu] >= nu), for alpha in the shell of degree nu
+// enumerated a = nu..0, b = nu-a..0, c = nu-a-b.
+bool build_plan(const Model &m, Plan &p, std::string &err)
+{
+    p = Plan();
+    for (int mu = 0; mu < kMaxMu; ++mu)
+        p.numax[mu] = -1;
+    for (int i = 0; i < m.B; ++i) {
+        const int *b = &m.basic[4 * i];
+        p.numax[b[0]] = std::max(p.numax[b[0]], b[1] + b[2] + b[3]);
+    }
+    for (int mu = 0; mu < m.M; ++mu)
+        p.numax_all = std::max(p.numax_all, p.numax[mu]);
+    // (mu, a, b, c) -> first basic index
+    const int dim = kMaxNu + 1;
+    std::vector<int> first((size_t)kMaxMu * dim * dim * dim, -1);
+    auto key = [&](int mu, int a, int b, int c) { return ((mu * dim + a) * dim + b) * dim + c; };
+    for (int i = 0; i < m.B; ++i) {
+        const int *b = &m.basic[4 * i];
+        int &f = first[key(b[0], b[1], b[2], b[3])];
+        if (f < 0)
+            f = i;
+        else {
+            p.dup.push_back(i);
+            p.dup.push_back(f);
+        }
+    }
+    for (int nu = 0; nu <= p.numax_all; ++nu)
+        for (int mu = 0; mu < m.M; ++mu) {
+            if (p.numax[mu] < nu)
+                continue;
+            for (int a = nu; a >= 0; --a)
+                for (int b = nu - a; b >= 0; --b) {
+                    p.slot_basic.push_back(first[key(mu, a, b, nu - a - b)]);
+                    p.slot_abc.push_back(a | (b << 8) | ((nu - a - b) << 16));
+                }
+        }
+    p.nslots = (int)p.slot_basic.size();
+
+    // Dependency levels.  The reference applies the rules in file order
+    // (potential_mtp.cpp:2918-2924), so every operand must be complete before
+    // a rule reads it; a file that violates this is rejected.
+    std::vector<int> last_write((size_t)m.K, -1);
+    for (int t = 0; t < m.T; ++t)
+        last_write[m.times[4 * t + 3]] = t;
+    std::vector<int> level((size_t)m.K, 0);
+    for (int t = 0; t < m.T; ++t) {
+        const int *r = &m.times[4 * t];
+        if (last_write[r[0]] >= t || last_write[r[1]] >= t)
+            return fail(err, "product rules are not in dependency order");
+        level[r[3]] = std::max(level[r[3]], 1 + std::max(level[r[0]], level[r[1]]));
+    }
+    int maxl = 0;
+    for (int x = 0; x < m.K; ++x)
+        maxl = std::max(maxl, level[x]);
+    p.max_level = maxl;
+
+    // Forward tasks: outputs of each level, rules of an output in file order.
+    std::vector<std::vector<int>> by_out((size_t)m.K);
+    for (int t = 0; t < m.T; ++t)
+        by_out[m.times[4 * t + 3]].push_back(t);
+    p.fwd_level.push_back(0);
+    for (int L = 1; L <= maxl; ++L) {
+        for (int o = 0; o < m.K; ++o) {
+            if (level[o] != L || by_out[o].empty())
+                continue;
+            p.fwd_task.insert(p.fwd_task.end(), {o, (int)p.fwd_lr.size(), (int)by_out[o].size(), 0});
+            for (int t : by_out[o]) {
+                const int *r = &m.times[4 * t];
+                p.fwd_lr.push_back(r[0] | (r[1] << 16));
+                p.fwd_c.push_back((double)r[2]);
+            }
+        }
+        p.fwd_level.push_back((int)p.fwd_task.size() / 4);
+    }
+
+    // Reverse tasks: destinations of each level from the top down; entries of
+    // a destination in reverse file order, the right operand's entry first
+    // (backpropagate_moments, potential_mtp.cpp:3292-3305).
+    std::vector<std::vector<int>> ent((size_t)m.K);  // pairs {out, other} and c via index
+    std::vector<std::vector<double>> entc((size_t)m.K);
+    for (int t = m.T - 1; t >= 0; --t) {
+        const int *r = &m.times[4 * t];
+        ent[r[1]].push_back(r[3] | (r[0] << 16));
+        entc[r[1]].push_back((double)r[2]);
+        ent[r[0]].push_back(r[3] | (r[1] << 16));
+        entc[r[0]].push_back((double)r[2]);
+    }
+    p.bwd_level.push_back(0);
+    for (int L = maxl - 1; L >= 0; --L) {
+        for (int x = 0; x < m.K; ++x) {
+            if (level[x] != L || ent[x].empty())
+                continue;
+            p.bwd_task.insert(p.bwd_task.end(), {x, (int)p.bwd_oo.size(), (int)ent[x].size(), 0});
+            p.bwd_oo.insert(p.bwd_oo.end(), ent[x].begin(), ent[x].end());
+            p.bwd_c.insert(p.bwd_c.end(), entc[x].begin(), entc[x].end());
+        }
+        p.bwd_level.push_back((int)p.bwd_task.size() / 4);
+    }
+    return true;
+}
+
+}  // namespace mtpx

@@ -1,0 +1,168 @@
+// Internal types shared by the host runtime and the HIP kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <string>
+#include <vector>
+
+namespace mtpx {
+
+// Compile-time ceilings of the kernel variants; a model is run by the
+// smallest variant whose ceilings it fits.
+constexpr int kMaxMu = 8;       // radial functions
+constexpr int kMaxNu = 8;       // angular degree a+b+c
+constexpr int kMaxR = 16;       // radial basis size
+constexpr int kWave = 64;       // CDNA wavefront
+constexpr int kChunk = 16;      // slots per LDS reduction chunk
+constexpr int kRedStride = 65;  // padded row stride of the reduction buffer
+
+// Growable device allocation owned by a context.
+struct DBuf {
+    void *p = nullptr;
+    size_t bytes = 0;
+    hipError_t ensure(size_t need)
+    {
+        if (need <= bytes && p)
+            return hipSuccess;
+        if (p) {
+            // queued work may still read the old allocation
+            (void)hipDeviceSynchronize();
+            (void)hipFree(p);
+        }
+        p = nullptr;
+        bytes = 0;
+        const size_t want = need < 64 ? 64 : need;
+        hipError_t e = hipMalloc(&p, want);
+        if (e == hipSuccess)
+            bytes = want;
+        return e;
+    }
+    template <class T> T *as() const { return static_cast<T *>(p); }
+    void release()
+    {
+        if (p)
+            (void)hipFree(p);
+        p = nullptr;
+        bytes = 0;
+    }
+};
+
+// Resident neighbour lists (SoA) and the builder's scratch.
+struct NeighborStore {
+    int n = 0;
+    int64_t P = 0;
+    DBuf offsets, idx, type, x, y, z, d, center_type;
+};
+struct NeighborScratch {
+    DBuf pos, types, pts, orig, cand, flags, scan, tmp, minmax, box, box_start, box_cur,
+        box_items, rank, cnt, cursor, key, st_idx, st_type, st_vec, st_d, scalars;
+    void release_all()
+    {
+        for (DBuf *b : {&pos, &types, &pts, &orig, &cand, &flags, &scan, &tmp, &minmax, &box,
+                        &box_start, &box_cur, &box_items, &rank, &cnt, &cursor, &key, &st_idx,
+                        &st_type, &st_vec, &st_d, &scalars})
+            b->release();
+    }
+};
+// Builds the lists on the device (neighbors.hip); returns an MTPX_* code.
+int build_neighbors_gpu(const double cell[9], const int pbc[3], int n, const double *pos,
+                        const int *types, double cutoff, hipStream_t s, NeighborStore &out,
+                        NeighborScratch &w, std::string &err);
+
+// Host-side model: the linear MTP (potentials/potential_mtp.h:93) plus the
+// launch plan derived from its contraction graph.
+struct Model {
+    int Z = 0, M = 0, R = 0, K = 0, B = 0, T = 0, S = 0;
+    double rmin = 0, rmax = 0, scaling = 0.01;
+    std::vector<int> basic;   // [B][4]
+    std::vector<int> times;   // [T][4]
+    std::vector<int> map;     // [S]
+    std::vector<double> coef; // [Z*Z*M*R | Z | S]
+    int nradial() const { return Z * Z * M * R; }
+    int ncoef() const { return nradial() + Z + S; }
+};
+
+// Parses .mtp text (PotMTP::Load grammar, non-split RBChebyshev).
+bool parse_mtp(const std::string &text, Model &m, std::string &err);
+// Validates sizes and index ranges of a model view.
+bool validate_model(const Model &m, std::string &err);
+
+// Launch plan: basic moments in canonical order, the product rules grouped by
+// dependency level and output (forward) or destination (reverse).
+struct Plan {
+    int numax[kMaxMu];        // per mu: max degree present, -1 if absent
+    int numax_all = -1;
+    int nslots = 0;           // canonical (nu, mu, alpha) slots
+    std::vector<int> slot_basic;   // [nslots] basic index or -1 (padding)
+    std::vector<int> slot_abc;     // [nslots] a | b << 8 | c << 16
+    std::vector<int> dup;          // [ndup][2] {duplicate basic, source basic}
+    // forward: level ranges over tasks, task = {out, first, count, 0}
+    std::vector<int> fwd_level;    // [nfwd+1]
+    std::vector<int> fwd_task;     // [ntask][4]
+    std::vector<int> fwd_lr;       // [T] l | r << 16
+    std::vector<double> fwd_c;     // [T]
+    // reverse: level ranges over tasks, task = {dst, first, count, 0}
+    std::vector<int> bwd_level;
+    std::vector<int> bwd_task;
+    std::vector<int> bwd_oo;       // [2T] out | other << 16
+    std::vector<double> bwd_c;     // [2T]
+    int max_level = 0;
+};
+bool build_plan(const Model &m, Plan &p, std::string &err);
+
+// Device view passed to the kernels by value.
+struct DevModel {
+    int Z, M, R, K, B, T, S, nslots;
+    double rmin, rmax, scaling, mult, su, pu;
+    int numax[kMaxMu];
+    int numax_all;
+    int ndup;
+    int nfwd, nbwd;
+    const double *radial;   // [Z*Z*M*R]
+    const double *species;  // [Z]
+    const double *moment;   // [S]
+    const int *map;         // [S]
+    const double *seed;     // [K] sum of moment coefficients mapped to each moment
+    const int *slot_basic;  // [nslots]
+    const int *slot_abc;    // [nslots] a | b << 8 | c << 16
+    const int *dup;         // [ndup][2]
+    const int *fwd_level;
+    const int4 *fwd_task;
+    const int *fwd_lr;
+    const double *fwd_c;
+    const int *bwd_level;
+    const int4 *bwd_task;
+    const int *bwd_oo;
+    const double *bwd_c;
+};
+
+// Neighbour lists resident on the device (SoA).
+struct DevNeighbors {
+    int n;                  // centres
+    int64_t P;              // directed entries
+    const int *offsets;     // [n+1]
+    const int *idx;         // [P]
+    const int *type;        // [P]
+    const double *x, *y, *z, *d;  // [P]
+    const int *center_type; // [n]
+};
+
+struct EfsOut {
+    double *forces;         // [n][3] (zeroed by the caller)
+    double *site_energy;    // [n]
+    double *partial;        // [gridDim.x][10]: energy, stress[9]
+    double *pair_ders;      // [P][3] (deterministic mode) or nullptr
+};
+
+// Kernel launchers (efs_kernel.hip).
+size_t efs_lds_bytes(const DevModel &m);
+int efs_variant(const DevModel &m, int R);
+hipError_t launch_efs(const DevModel &m, const DevNeighbors &nb, const EfsOut &out, int grid,
+                      bool deterministic, hipStream_t s);
+hipError_t launch_efs_finish(const DevNeighbors &nb, const EfsOut &out, int grid,
+                             bool deterministic, const int *rev_offsets, const int *rev_pairs,
+                             double *energy_stress10, hipStream_t s);
+
+}  // namespace mtpx

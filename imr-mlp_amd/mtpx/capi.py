@@ -1,0 +1,209 @@
+"""ctypes binding of libmtpx.so (include/mtpx.h).
+
+The library is loaded from imr-mlp_amd/lib/libmtpx.so (built in-tree by
+imr-mlp_amd/build.py).  There is no fallback: if the HIP library is missing
+or fails to load, every entry point raises.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import re
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.dirname(HERE)
+ROOT = os.path.dirname(PKG)
+LIB_PATH = os.path.join(PKG, "lib", "libmtpx.so")
+HEADER = os.path.join(ROOT, "include", "mtpx.h")
+
+OK = 0
+ERRORS = {-1: "MTPX_E_INVALID", -2: "MTPX_E_MODEL", -3: "MTPX_E_NO_MODEL",
+          -4: "MTPX_E_NO_TOPOLOGY", -5: "MTPX_E_DEVICE", -6: "MTPX_E_ALLOC",
+          -7: "MTPX_E_CAPACITY", -8: "MTPX_E_RANGE"}
+
+_dp = C.POINTER(C.c_double)
+_ip = C.POINTER(C.c_int)
+_lib = None
+
+
+class MtpxError(RuntimeError):
+    def __init__(self, code, msg):
+        super().__init__("%s (%d): %s" % (ERRORS.get(code, "error"), code, msg))
+        self.code = code
+
+
+def declared_symbols() -> list[str]:
+    """Entry points declared in include/mtpx.h."""
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(mtpx_\w+)\s*\(", text, re.M)))
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError("libmtpx.so is not built (run imr-mlp_amd/build.py): " + LIB_PATH)
+        L = C.CDLL(LIB_PATH)
+        L.mtpx_version.restype = C.c_char_p
+        L.mtpx_create.argtypes = [C.c_int, C.POINTER(C.c_void_p)]
+        L.mtpx_destroy.argtypes = [C.c_void_p]
+        L.mtpx_last_error.restype = C.c_char_p
+        L.mtpx_last_error.argtypes = [C.c_void_p]
+        L.mtpx_load_model_text.argtypes = [C.c_void_p, C.c_char_p]
+        L.mtpx_parse_model_text.argtypes = [C.c_char_p, _ip, _dp, C.c_char_p, C.c_int]
+        L.mtpx_model_info.argtypes = [C.c_void_p, _ip]
+        L.mtpx_get_coeffs.argtypes = [C.c_void_p, _dp]
+        L.mtpx_set_coeffs.argtypes = [C.c_void_p, _dp]
+        L.mtpx_wrap.argtypes = [_dp, _ip, C.c_int, _dp]
+        L.mtpx_build_neighbors.argtypes = [C.c_void_p, _dp, _ip, C.c_int, _dp, _ip, C.c_double]
+        L.mtpx_neighbor_count.argtypes = [C.c_void_p, C.POINTER(C.c_int64), _ip]
+        L.mtpx_get_neighbors.argtypes = [C.c_void_p, _ip, _ip, _ip, _dp, _dp, _ip]
+        L.mtpx_set_neighbors.argtypes = [C.c_void_p, C.c_int, _ip, _ip, _ip, _dp, _dp, _ip]
+        L.mtpx_efs.argtypes = [C.c_void_p, C.c_int, _dp, _dp, _dp, _dp]
+        L.mtpx_efs_device.argtypes = [C.c_void_p, C.c_int]
+        L.mtpx_last_timings.argtypes = [C.c_void_p, _dp]
+        _lib = L
+    return _lib
+
+
+def _d(a):
+    return a.ctypes.data_as(_dp)
+
+
+def _i(a):
+    return a.ctypes.data_as(_ip)
+
+
+def f64(a, shape=None):
+    a = np.ascontiguousarray(a, dtype=np.float64)
+    return a if shape is None else a.reshape(shape)
+
+
+def i32(a):
+    return np.ascontiguousarray(a, dtype=np.int32)
+
+
+def version() -> str:
+    return lib().mtpx_version().decode()
+
+
+def wrap(cell, pbc, pos) -> np.ndarray:
+    """Atoms::wrap on host arrays (returns a wrapped copy)."""
+    out = f64(pos, (-1, 3)).copy()
+    cell = f64(cell, (9,))
+    pbc = i32(pbc)
+    rc = lib().mtpx_wrap(_d(cell), _i(pbc), out.shape[0], _d(out))
+    if rc != OK:
+        raise MtpxError(rc, "mtpx_wrap")
+    return out
+
+
+def parse_model_text(text: str):
+    """Host-only .mtp parse: (sizes dict, coefficients)."""
+    info = np.zeros(8, np.int32)
+    err = C.create_string_buffer(512)
+    rc = lib().mtpx_parse_model_text(text.encode(), _i(info), None, err, 512)
+    if rc != OK:
+        raise MtpxError(rc, err.value.decode())
+    coef = np.zeros(int(info[7]))
+    lib().mtpx_parse_model_text(text.encode(), _i(info), _d(coef), err, 512)
+    keys = ["Z", "M", "R", "K", "B", "T", "S", "ncoef"]
+    return dict(zip(keys, [int(v) for v in info])), coef
+
+
+class Context:
+    """One mtpx_context on one device."""
+
+    def __init__(self, device: int = 0):
+        h = C.c_void_p()
+        rc = lib().mtpx_create(device, C.byref(h))
+        if rc != OK:
+            raise MtpxError(rc, "mtpx_create(%d)" % device)
+        self.h = h
+
+    def close(self):
+        if getattr(self, "h", None):
+            lib().mtpx_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.close()
+
+    def _check(self, rc, what):
+        if rc != OK:
+            raise MtpxError(rc, "%s: %s" % (what, lib().mtpx_last_error(self.h).decode()))
+
+    # ---- model ----
+    def load_model_text(self, text: str):
+        self._check(lib().mtpx_load_model_text(self.h, text.encode()), "load_model_text")
+        info = np.zeros(8, np.int32)
+        self._check(lib().mtpx_model_info(self.h, _i(info)), "model_info")
+        self.info = dict(zip(["Z", "M", "R", "K", "B", "T", "S", "ncoef"], [int(v) for v in info]))
+        return self.info
+
+    def get_coeffs(self) -> np.ndarray:
+        x = np.zeros(self.info["ncoef"])
+        self._check(lib().mtpx_get_coeffs(self.h, _d(x)), "get_coeffs")
+        return x
+
+    def set_coeffs(self, x):
+        x = f64(x)
+        assert x.size == self.info["ncoef"]
+        self._check(lib().mtpx_set_coeffs(self.h, _d(x)), "set_coeffs")
+
+    # ---- neighbours ----
+    def build_neighbors(self, cell, pbc, pos, types, cutoff):
+        cell = f64(cell, (9,))
+        pbc = i32(pbc)
+        pos = f64(pos, (-1, 3))
+        types = i32(types)
+        self._check(lib().mtpx_build_neighbors(self.h, _d(cell), _i(pbc), pos.shape[0], _d(pos),
+                                               _i(types), float(cutoff)), "build_neighbors")
+
+    def set_neighbors(self, offsets, idx, types, vec, dist, center_types):
+        offsets, idx, types, ct = i32(offsets), i32(idx), i32(types), i32(center_types)
+        vec, dist = f64(vec, (-1,)), f64(dist)
+        self._check(lib().mtpx_set_neighbors(self.h, len(offsets) - 1, _i(offsets), _i(idx),
+                                             _i(types), _d(vec), _d(dist), _i(ct)),
+                    "set_neighbors")
+
+    def neighbor_count(self):
+        P = C.c_int64()
+        n = C.c_int()
+        self._check(lib().mtpx_neighbor_count(self.h, C.byref(P), C.byref(n)), "neighbor_count")
+        return n.value, P.value
+
+    def get_neighbors(self):
+        n, P = self.neighbor_count()
+        Pz = max(P, 1)
+        offsets = np.zeros(n + 1, np.int32)
+        idx = np.zeros(Pz, np.int32)
+        types = np.zeros(Pz, np.int32)
+        vec = np.zeros((Pz, 3))
+        dist = np.zeros(Pz)
+        ct = np.zeros(max(n, 1), np.int32)
+        self._check(lib().mtpx_get_neighbors(self.h, _i(offsets), _i(idx), _i(types), _d(vec),
+                                             _d(dist), _i(ct)), "get_neighbors")
+        return dict(offsets=offsets, idx=idx[:P], types=types[:P], vec=vec[:P], dist=dist[:P],
+                    center_types=ct[:n])
+
+    # ---- E/F/S ----
+    def efs(self, deterministic: bool = False):
+        n, _ = self.neighbor_count()
+        E = C.c_double()
+        F = np.zeros((max(n, 1), 3))
+        S = np.zeros((3, 3))
+        se = np.zeros(max(n, 1))
+        self._check(lib().mtpx_efs(self.h, int(deterministic), C.byref(E), _d(F), _d(S), _d(se)),
+                    "efs")
+        return E.value, F[:n], S, se[:n]
+
+    def efs_device(self, deterministic: bool = False):
+        self._check(lib().mtpx_efs_device(self.h, int(deterministic)), "efs_device")
+
+    def last_timings(self):
+        t = np.zeros(4)
+        self._check(lib().mtpx_last_timings(self.h, _d(t)), "last_timings")
+        return t

@@ -1,0 +1,106 @@
+"""Device neighbour lists against the oracle's restatement of the reference
+BOXED builder: identical offsets, neighbour indices, species, and
+displacements/distances equal bit for bit."""
+import numpy as np
+import pytest
+
+import oracle as O
+from mtpx import synth as S
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def nctx():
+    """A context without a model: species indices are not range-checked
+    against a model's species count."""
+    from mtpx import capi
+    c = capi.Context(0)
+    yield c
+    c.close()
+
+
+def _structures():
+    out = []
+    _, s = S.workload_inference(1)
+    out.append(("fcc108", s, 5.0))
+    _, s = S.scaled_inference(2, (4, 3, 5))
+    out.append(("fcc-strained-240", s, 5.0))
+    rng = S.rng_for(400)
+    for k in range(6):
+        s = S.lattice("fcc", (2, 2, 2), 3.6)
+        s = S.displace(S.strain(s, rng, 0.15), rng, 0.2)
+        cell = s.cell.copy()
+        cell[1] += 0.37 * cell[0]
+        cell[2] += -0.21 * cell[1] + 0.3 * cell[0]
+        s.cell = cell
+        s.types = (S.uniform(rng, s.n) * 2).astype(np.int32)
+        out.append(("skew%d" % k, s, 3.0 + 2.5 * rng.random()))
+    # cell smaller than the cutoff: many images of the same atom in one list
+    s = S.displace(S.lattice("bcc", (1, 1, 2), 2.87), rng, 0.05)
+    out.append(("tiny-bcc", s, 6.0))
+    for k, st in enumerate(S.training_structures(5, 2)):
+        out.append(("liquid%d" % k, st, 6.0))
+    # slab: periodic in x, y only
+    s = S.displace(S.lattice("fcc", (3, 3, 3), 3.6), rng, 0.1)
+    s.pbc = np.array([1, 1, 0], np.int32)
+    out.append(("slab", s, 5.0))
+    # isolated cluster
+    s = S.displace(S.lattice("fcc", (2, 2, 2), 3.6), rng, 0.1)
+    s.pbc = np.zeros(3, np.int32)
+    out.append(("cluster", s, 5.0))
+    s = S.Structure(np.eye(3) * 10, np.array([[1.0, 2.0, 3.0]]), np.zeros(1, np.int32),
+                    np.ones(3, np.int32))
+    out.append(("single-atom", s, 5.0))
+    return out
+
+
+CASES = _structures()
+
+
+def _compare(got, nb):
+    assert np.array_equal(got["offsets"], nb.offsets)
+    assert np.array_equal(got["idx"], nb.idx)
+    assert np.array_equal(got["types"], nb.types)
+    assert np.array_equal(got["center_types"], nb.center_types)
+    assert np.array_equal(got["vec"].view(np.uint64), nb.vec.view(np.uint64))
+    assert np.array_equal(got["dist"].view(np.uint64), nb.dist.view(np.uint64))
+
+
+@pytest.mark.parametrize("name,s,rc", CASES, ids=[c[0] for c in CASES])
+def test_device_lists_bit_exact(nctx, name, s, rc):
+    pos = O.wrap(s.cell, s.pbc, s.pos) if np.any(s.pbc) else s.pos
+    nb = O.Neighbors.build(s.cell, s.pbc, pos, s.types, rc)
+    nctx.build_neighbors(s.cell, s.pbc, pos, s.types, rc)
+    _compare(nctx.get_neighbors(), nb)
+
+
+def test_empty_structure_lists(nctx):
+    nctx.build_neighbors(np.eye(3) * 5, [1, 1, 1], np.zeros((0, 3)), np.zeros(0), 5.0)
+    got = nctx.get_neighbors()
+    assert got["offsets"].tolist() == [0] and len(got["idx"]) == 0
+
+
+def test_full_size_workload2_lists_bit_exact(nctx):
+    model_text, s = S.workload_inference(2)
+    pos = O.wrap(s.cell, s.pbc, s.pos)
+    nb = O.Neighbors.build(s.cell, s.pbc, pos, s.types, 5.0)
+    nctx.build_neighbors(s.cell, s.pbc, pos, s.types, 5.0)
+    _compare(nctx.get_neighbors(), nb)
+    counts = np.diff(nb.offsets)
+    assert 40 <= counts.mean() <= 55
+
+
+def test_device_lists_drive_efs(ctx):
+    """Build on the device, evaluate on the device, compare with the oracle."""
+    model_text, s = S.scaled_inference(2, (4, 4, 4))
+    m = O.Model(model_text)
+    pos = O.wrap(s.cell, s.pbc, s.pos)
+    nb = O.Neighbors.build(s.cell, s.pbc, pos, s.types, m.cutoff)
+    E, F, St, se = O.efs(m, nb)
+    ctx.load_model_text(model_text)
+    ctx.build_neighbors(s.cell, s.pbc, pos, s.types, m.cutoff)
+    Eg, Fg, Sg, seg = ctx.efs()
+    assert abs(Eg - E) < 1e-10 * abs(E)
+    assert np.abs(Fg - F).max() < 1e-10 * np.abs(F).max()
+    assert np.abs(Sg - St).max() < 1e-10 * np.abs(St).max()
