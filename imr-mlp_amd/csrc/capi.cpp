@@ -21,8 +21,8 @@ struct mtpx_context {
     Plan plan;
     DevModel dm{};
     // model buffers
-    DBuf radial, species, moment, map, seed, slot_basic, slot_abc, dup, fwd_level, fwd_task,
-        fwd_lr, fwd_c, bwd_level, bwd_task, bwd_oo, bwd_c;
+    DBuf radial, species, moment, map, seed, slot_basic, slot_abc, dup, fwd_level, fwd_steps,
+        fwd_lcomb, fwd_comb, bwd_level, bwd_steps, bwd_lcomb, bwd_comb;
 
     // neighbour lists
     bool has_nbh = false;
@@ -45,8 +45,8 @@ struct mtpx_context {
     ~mtpx_context()
     {
         for (DBuf *b : {&radial, &species, &moment, &map, &seed, &slot_basic, &slot_abc, &dup,
-                        &fwd_level, &fwd_task, &fwd_lr, &fwd_c, &bwd_level, &bwd_task, &bwd_oo,
-                        &bwd_c, &offsets, &idx, &type, &x, &y, &z, &d, &center_type, &rev_offsets,
+                        &fwd_level, &fwd_steps, &fwd_lcomb, &fwd_comb, &bwd_level, &bwd_steps,
+                        &bwd_lcomb, &bwd_comb, &offsets, &idx, &type, &x, &y, &z, &d, &center_type, &rev_offsets,
                         &rev_pairs, &forces, &site_energy, &partial, &pair_ders, &out10})
             b->release();
         scratch.release_all();
@@ -146,33 +146,34 @@ int install_model(mtpx_context *ctx, Model &&m)
         dm.numax[mu] = P.numax[mu];
     dm.numax_all = P.numax_all;
     dm.ndup = (int)P.dup.size() / 2;
-    dm.nfwd = (int)P.fwd_level.size() - 1;
-    dm.nbwd = (int)P.bwd_level.size() - 1;
+    dm.nfwd = (int)P.fwd_level_step.size() - 1;
+    dm.nbwd = (int)P.bwd_level_step.size() - 1;
     hipStream_t s = ctx->stream;
     HIP_TRY(upload(ctx->map, M.map, s), "upload model");
     HIP_TRY(upload(ctx->slot_basic, P.slot_basic, s), "upload model");
     HIP_TRY(upload(ctx->slot_abc, P.slot_abc, s), "upload model");
     HIP_TRY(upload(ctx->dup, P.dup, s), "upload model");
-    HIP_TRY(upload(ctx->fwd_level, P.fwd_level, s), "upload model");
-    HIP_TRY(upload(ctx->fwd_task, P.fwd_task, s), "upload model");
-    HIP_TRY(upload(ctx->fwd_lr, P.fwd_lr, s), "upload model");
-    HIP_TRY(upload(ctx->fwd_c, P.fwd_c, s), "upload model");
-    HIP_TRY(upload(ctx->bwd_level, P.bwd_level, s), "upload model");
-    HIP_TRY(upload(ctx->bwd_task, P.bwd_task, s), "upload model");
-    HIP_TRY(upload(ctx->bwd_oo, P.bwd_oo, s), "upload model");
-    HIP_TRY(upload(ctx->bwd_c, P.bwd_c, s), "upload model");
+    HIP_TRY(upload(ctx->fwd_level, P.fwd_level_step, s), "upload model");
+    HIP_TRY(upload(ctx->fwd_steps, P.fwd_steps, s), "upload model");
+    HIP_TRY(upload(ctx->bwd_level, P.bwd_level_step, s), "upload model");
+    HIP_TRY(upload(ctx->bwd_steps, P.bwd_steps, s), "upload model");
+    HIP_TRY(upload(ctx->fwd_lcomb, P.fwd_level_comb, s), "upload model");
+    HIP_TRY(upload(ctx->fwd_comb, P.fwd_comb, s), "upload model");
+    HIP_TRY(upload(ctx->bwd_lcomb, P.bwd_level_comb, s), "upload model");
+    HIP_TRY(upload(ctx->bwd_comb, P.bwd_comb, s), "upload model");
     dm.map = ctx->map.as<int>();
     dm.slot_basic = ctx->slot_basic.as<int>();
     dm.slot_abc = ctx->slot_abc.as<int>();
     dm.dup = ctx->dup.as<int>();
-    dm.fwd_level = ctx->fwd_level.as<int>();
-    dm.fwd_task = ctx->fwd_task.as<int4>();
-    dm.fwd_lr = ctx->fwd_lr.as<int>();
-    dm.fwd_c = ctx->fwd_c.as<double>();
-    dm.bwd_level = ctx->bwd_level.as<int>();
-    dm.bwd_task = ctx->bwd_task.as<int4>();
-    dm.bwd_oo = ctx->bwd_oo.as<int>();
-    dm.bwd_c = ctx->bwd_c.as<double>();
+    dm.fwd_level_step = ctx->fwd_level.as<int>();
+    dm.fwd_steps = ctx->fwd_steps.as<int4>();
+    dm.bwd_level_step = ctx->bwd_level.as<int>();
+    dm.bwd_steps = ctx->bwd_steps.as<int4>();
+    dm.fwd_level_comb = ctx->fwd_lcomb.as<int>();
+    dm.fwd_comb = ctx->fwd_comb.as<int4>();
+    dm.bwd_level_comb = ctx->bwd_lcomb.as<int>();
+    dm.bwd_comb = ctx->bwd_comb.as<int4>();
+    dm.max_partials = P.max_partials;
     if (efs_lds_bytes(dm) > 160 * 1024)
         return set_error(ctx, MTPX_E_CAPACITY, "model needs more LDS than a CU provides");
     int rc = upload_coeffs(ctx);

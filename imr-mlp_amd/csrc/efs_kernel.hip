@@ -10,10 +10,10 @@
 //      vector u = r/d.  Every basic moment (mu, a, b, c) equals
 //      sum_j f_mu(d_j) * Y_abc(u_j) with Y_abc = ux^a uy^b uz^c, so the basics
 //      are produced shell by shell (degree nu = a+b+c, compile-time unrolled)
-//      in registers and reduced over neighbours through a padded LDS
+//      in registers and summed over neighbours through a padded LDS
 //      transpose, 16 slots at a time.
-//   2. the product rules run lane-parallel, one output per lane and level
-//      (forward) and one destination per lane and level (reverse adjoint).
+//   2. the product rules run lane-parallel from lane-major step tables, one
+//      dependency level at a time (forward values, then reverse adjoints).
 //   3. lanes over neighbours again: dE_i/dr_j from the closed form
 //      grad_r[f Y] = (f' - nu f/d) Y u + (f/d) grad_u Y, with the basic
 //      adjoints read as LDS broadcasts.
@@ -21,6 +21,11 @@
 //      fp64 atomics for the neighbour reactions; deterministic mode stores D
 //      per pair for an ordered gather.  Energy and virial are reduced per
 //      workgroup and finished by a single ordered pass.
+//
+// Kernel variants: a "shell profile" fixes, per radial function mu, the
+// highest angular degree of its basic moments.  The level-10/16/20 template
+// profiles are compile-time constants (every (nu, mu) guard folds away); the
+// generic variants read the profile at run time.
 #include "mtpx_internal.hpp"
 
 namespace mtpx {
@@ -38,6 +43,37 @@ constexpr int shell_index(int nu, int a, int b)
     return pos + (nu - a - b);
 }
 
+// ---- shell profiles ---------------------------------------------------
+template <int MM, int NN, int RR, int... NM>
+struct ExactProfile {
+    static constexpr bool exact = true;
+    static constexpr int M = MM, NUMAX = NN, RMAX = RR;
+    static constexpr int nm[MM] = {NM...};
+    static __device__ __forceinline__ bool active(const DevModel &, int mu, int nu)
+    {
+        return nm[mu] >= nu;
+    }
+    static __device__ __forceinline__ bool deeper(const DevModel &, int nu) { return nu < NN; }
+};
+template <int MM, int NN, int RR>
+struct RuntimeProfile {
+    static constexpr bool exact = false;
+    static constexpr int M = MM, NUMAX = NN, RMAX = RR;
+    static __device__ __forceinline__ bool active(const DevModel &m, int mu, int nu)
+    {
+        return mu < m.M && m.numax[mu] >= nu;
+    }
+    static __device__ __forceinline__ bool deeper(const DevModel &m, int nu)
+    {
+        return nu < m.numax_all;
+    }
+};
+using ProfLevel10 = ExactProfile<3, 3, 8, 3, 1, 0>;
+using ProfLevel16 = ExactProfile<4, 6, 8, 6, 4, 2, 0>;
+using ProfLevel20 = ExactProfile<5, 8, 10, 8, 6, 4, 2, 0>;
+using ProfSmall = RuntimeProfile<4, 6, 8>;
+using ProfGeneric = RuntimeProfile<kMaxMu, kMaxNu, kMaxR>;
+
 __device__ __forceinline__ double wave_sum(double v)
 {
 #pragma unroll
@@ -46,25 +82,29 @@ __device__ __forceinline__ double wave_sum(double v)
     return v;
 }
 
+template <int MMAX>
 struct Nbr {
     double x, y, z, d, invd, ux, uy, uz;
-    double f[kMaxMu], fd[kMaxMu];
-    bool in_cutoff;
+    double f[MMAX], fd[MMAX];
 };
 
-template <int MMAX, int RMAX>
+// Neighbour data of list entry p; lanes without an entry keep zeros, so
+// they contribute nothing to the sums below.
+template <class P>
 __device__ __forceinline__ void load_neighbor(const DevModel &m, const DevNeighbors &nb,
                                               const double *coef_lds, int ti, int64_t p,
-                                              Nbr &q)
+                                              bool valid, Nbr<P::M> &q)
 {
-    q.x = nb.x[p];
-    q.y = nb.y[p];
-    q.z = nb.z[p];
-    q.d = nb.d[p];
-    const int tj = nb.type[p];
+    constexpr int RMAX = P::RMAX;
+    q.x = valid ? nb.x[p] : 0.0;
+    q.y = valid ? nb.y[p] : 0.0;
+    q.z = valid ? nb.z[p] : 0.0;
+    const double dd = valid ? nb.d[p] : m.rmax;
+    const int tj = valid ? nb.type[p] : 0;
     // potential_mtp.cpp:2842 -- entries beyond the cutoff are skipped, r == cutoff kept
-    q.in_cutoff = !(q.d > m.rmax);
-    const double d = q.in_cutoff ? q.d : m.rmax;
+    const bool in_cutoff = valid && !(dd > m.rmax);
+    const double d = in_cutoff ? dd : m.rmax;
+    q.d = d;
     q.invd = 1.0 / d;
     q.ux = q.x * q.invd;
     q.uy = q.y * q.invd;
@@ -84,11 +124,12 @@ __device__ __forceinline__ void load_neighbor(const DevModel &m, const DevNeighb
         Q[k] = 2 * ksi * Q[k - 1] - Q[k - 2];
         dQ[k] = 2 * (m.mult * Q[k - 1] + ksi * dQ[k - 1]) - dQ[k - 2];
     }
+    const double w = in_cutoff ? 1.0 : 0.0;
     const double *c = coef_lds + (ti * m.Z + tj) * m.M * m.R;
 #pragma unroll
-    for (int mu = 0; mu < MMAX; ++mu) {
+    for (int mu = 0; mu < P::M; ++mu) {
         double f = 0, fd = 0;
-        if (mu < m.M) {
+        if (P::exact || mu < m.M) {
             const double *cm = c + mu * m.R;
 #pragma unroll
             for (int k = 0; k < RMAX; ++k)
@@ -97,14 +138,13 @@ __device__ __forceinline__ void load_neighbor(const DevModel &m, const DevNeighb
                     fd += cm[k] * dQ[k];
                 }
         }
-        const double w = q.in_cutoff ? 1.0 : 0.0;
         q.f[mu] = f * w;
         q.fd[mu] = fd * w;
     }
 }
 
-template <int NU>
-__device__ __forceinline__ void next_shell(const double *prev, double *cur, const Nbr &q)
+template <int NU, int MMAX>
+__device__ __forceinline__ void next_shell(const double *prev, double *cur, const Nbr<MMAX> &q)
 {
 #pragma unroll
     for (int a = NU; a >= 0; --a)
@@ -120,20 +160,23 @@ __device__ __forceinline__ void next_shell(const double *prev, double *cur, cons
         }
 }
 
-// Sum a chunk of `nrows` slots over the `ncols` neighbour columns of the
-// transpose buffer and add the sums into the moment array.
-__device__ __forceinline__ void reduce_chunk(double *red, int ncols, int nrows, int slot0,
+// Sum `nrows` slots of the transpose buffer over the neighbour columns and
+// add the sums to the moment array.  Rows hold 64 columns; columns of lanes
+// without a neighbour hold zeros.
+__device__ __forceinline__ void reduce_chunk(const double *red, int nrows, int slot0,
                                              const int *slot_basic, double *mom, int lane)
 {
     __syncthreads();
     const int s = lane & (kChunk - 1), qq = lane >> 4;
-    double acc = 0.0;
+    const double2 *row = reinterpret_cast<const double2 *>(red + s * kRedStride + qq * 16);
+    double a0 = 0.0, a1 = 0.0;
 #pragma unroll
-    for (int jj = 0; jj < 16; ++jj) {
-        const int j = qq * 16 + jj;
-        if (j < ncols)
-            acc += red[s * kRedStride + j];
+    for (int jj = 0; jj < 8; ++jj) {
+        const double2 v = row[jj];
+        a0 += v.x;
+        a1 += v.y;
     }
+    double acc = a0 + a1;
     acc += __shfl_xor(acc, 16, kWave);
     acc += __shfl_xor(acc, 32, kWave);
     if (lane < nrows) {
@@ -145,42 +188,40 @@ __device__ __forceinline__ void reduce_chunk(double *red, int ncols, int nrows, 
 }
 
 struct FwdCtx {
-    const DevModel *m;
     double *red, *mom;
-    int ncols, lane;
-    bool active;
-    int slot;
+    const int *slot_basic;
+    int lane, slot;
 };
 
-template <int NU, int NUMAX, int MMAX>
-__device__ __forceinline__ void fwd_shells(FwdCtx &cx, const Nbr &q, const double *prev)
+template <int NU, class P>
+__device__ __forceinline__ void fwd_shells(const DevModel &m, FwdCtx &cx, const Nbr<P::M> &q,
+                                           const double *prev)
 {
     double cur[shell_size(NU)];
     if constexpr (NU == 0)
         cur[0] = 1.0;
     else
-        next_shell<NU>(prev, cur, q);
-    const DevModel &m = *cx.m;
+        next_shell<NU, P::M>(prev, cur, q);
 #pragma unroll
-    for (int mu = 0; mu < MMAX; ++mu) {
-        if (mu < m.M && m.numax[mu] >= NU) {
+    for (int mu = 0; mu < P::M; ++mu) {
+        if (P::active(m, mu, NU)) {
+            __builtin_amdgcn_sched_barrier(0);
             int row = 0;
 #pragma unroll
             for (int i = 0; i < shell_size(NU); ++i) {
-                if (cx.active)
-                    cx.red[row * kRedStride + cx.lane] = q.f[mu] * cur[i];
+                cx.red[row * kRedStride + cx.lane] = q.f[mu] * cur[i];
                 ++row;
                 if (row == kChunk || i == shell_size(NU) - 1) {
-                    reduce_chunk(cx.red, cx.ncols, row, cx.slot, m.slot_basic, cx.mom, cx.lane);
+                    reduce_chunk(cx.red, row, cx.slot, cx.slot_basic, cx.mom, cx.lane);
                     cx.slot += row;
                     row = 0;
                 }
             }
         }
     }
-    if constexpr (NU < NUMAX) {
-        if (NU < m.numax_all)
-            fwd_shells<NU + 1, NUMAX, MMAX>(cx, q, cur);
+    if constexpr (NU < P::NUMAX) {
+        if (P::deeper(m, NU))
+            fwd_shells<NU + 1, P>(m, cx, q, cur);
     }
 }
 
@@ -188,18 +229,21 @@ struct BwdAcc {
     double s, gx, gy, gz;
 };
 
-template <int NU, int NUMAX, int MMAX>
+template <int NU, class P>
 __device__ __forceinline__ void bwd_shells(const DevModel &m, const double4 *A4, int &slot,
-                                           const Nbr &q, const double *prev, BwdAcc &acc)
+                                           const Nbr<P::M> &q, const double *prev, BwdAcc &acc)
 {
     double cur[shell_size(NU)];
     if constexpr (NU == 0)
         cur[0] = 1.0;
     else
-        next_shell<NU>(prev, cur, q);
+        next_shell<NU, P::M>(prev, cur, q);
 #pragma unroll
-    for (int mu = 0; mu < MMAX; ++mu) {
-        if (mu < m.M && m.numax[mu] >= NU) {
+    for (int mu = 0; mu < P::M; ++mu) {
+        if (P::active(m, mu, NU)) {
+            // keep the adjoint loads of one (nu, mu) block from being hoisted
+            // into the previous one: bounds the live registers
+            __builtin_amdgcn_sched_barrier(0);
             double u = 0, Gx = 0, Gy = 0, Gz = 0;
 #pragma unroll
             for (int a = NU; a >= 0; --a)
@@ -225,29 +269,152 @@ __device__ __forceinline__ void bwd_shells(const DevModel &m, const double4 *A4,
             slot += shell_size(NU);
         }
     }
-    if constexpr (NU < NUMAX) {
-        if (NU < m.numax_all)
-            bwd_shells<NU + 1, NUMAX, MMAX>(m, A4, slot, q, cur, acc);
+    if constexpr (NU < P::NUMAX) {
+        if (P::deeper(m, NU))
+            bwd_shells<NU + 1, P>(m, A4, slot, q, cur, acc);
     }
 }
 
-template <int MMAX, int NUMAX, int RMAX>
+// One level of a lane-major step table; entries are prefetched four steps
+// ahead so every step costs one coalesced, already-resident int4.
+template <class Step>
+__device__ __forceinline__ void run_steps(const int4 *steps, int s0, int s1, int lane, Step step)
+{
+    if (s1 <= s0)
+        return;
+    const int4 *tab = steps + (size_t)s0 * kWave + lane;
+    int4 e0 = tab[0], e1 = tab[kWave], e2 = tab[2 * kWave], e3 = tab[3 * kWave];
+    for (int st = s0; st < s1; st += 4) {
+        int4 n0 = e0, n1 = e1, n2 = e2, n3 = e3;
+        if (st + 4 < s1) {
+            const int4 *nt = tab + (size_t)(st + 4 - s0) * kWave;
+            n0 = nt[0];
+            n1 = nt[kWave];
+            n2 = nt[2 * kWave];
+            n3 = nt[3 * kWave];
+        }
+        step(e0);
+        step(e1);
+        step(e2);
+        step(e3);
+        e0 = n0;
+        e1 = n1;
+        e2 = n2;
+        e3 = n3;
+    }
+}
+
+// Product rules, forward (potential_mtp.cpp:2918-2924): one level at a time.
+__device__ __forceinline__ void rules_forward(const DevModel &m, double *mom, double *partial,
+                                              int lane)
+{
+    for (int L = 0; L < m.nfwd; ++L) {
+        double acc = 0.0;
+        run_steps(m.fwd_steps, m.fwd_level_step[L], m.fwd_level_step[L + 1], lane,
+                  [&](const int4 &e) {
+                      acc += (double)e.z * mom[e.x] * mom[e.y];
+                      if (e.w != -1) {
+                          if (e.w >= 0)
+                              mom[e.w] = acc;
+                          else
+                              partial[-e.w - 2] = acc;
+                          acc = 0.0;
+                      }
+                  });
+        const int c0 = m.fwd_level_comb[L], c1 = m.fwd_level_comb[L + 1];
+        if (c1 > c0) {
+            __syncthreads();
+            for (int c = c0 + lane; c < c1; c += kWave) {
+                const int4 t = m.fwd_comb[c];
+                double sum = 0.0;
+                for (int k = 0; k < t.z; ++k)
+                    sum += partial[t.y + k];
+                mom[t.x] = sum;
+            }
+        }
+        __syncthreads();
+    }
+}
+
+// Product rules, reverse (backpropagate_moments, potential_mtp.cpp:3292-3305).
+__device__ __forceinline__ void rules_reverse(const DevModel &m, const double *mom, double *A,
+                                              double *partial, int lane)
+{
+    for (int L = 0; L < m.nbwd; ++L) {
+        double acc = 0.0;
+        run_steps(m.bwd_steps, m.bwd_level_step[L], m.bwd_level_step[L + 1], lane,
+                  [&](const int4 &e) {
+                      acc += (double)e.z * A[e.x] * mom[e.y];
+                      if (e.w != -1) {
+                          if (e.w >= 0)
+                              A[e.w] += acc;
+                          else
+                              partial[-e.w - 2] = acc;
+                          acc = 0.0;
+                      }
+                  });
+        const int c0 = m.bwd_level_comb[L], c1 = m.bwd_level_comb[L + 1];
+        if (c1 > c0) {
+            __syncthreads();
+            for (int c = c0 + lane; c < c1; c += kWave) {
+                const int4 t = m.bwd_comb[c];
+                double sum = 0.0;
+                for (int k = 0; k < t.z; ++k)
+                    sum += partial[t.y + k];
+                A[t.x] += sum;
+            }
+        }
+        __syncthreads();
+    }
+}
+
+struct Lds {
+    double *coef, *mom, *A, *red, *seed, *moment, *partial;
+    int *map, *slot_basic, *slot_abc;
+};
+
+__device__ __forceinline__ Lds lds_layout(const DevModel &m, double *base)
+{
+    const int ncoef_r = m.Z * m.Z * m.M * m.R;
+    const int K4 = (m.K + 3) & ~3, S4 = (m.S + 3) & ~3, N4 = (m.nslots + 3) & ~3;
+    const int P4 = (m.max_partials + 3) & ~3;
+    Lds L;
+    L.coef = base;
+    L.mom = L.coef + ((ncoef_r + 3) & ~3);
+    L.A = L.mom + K4;
+    L.red = L.A + K4;
+    L.seed = L.red + max(kChunk * kRedStride, 4 * N4);
+    L.moment = L.seed + K4;
+    L.partial = L.moment + S4;
+    L.map = reinterpret_cast<int *>(L.partial + P4);
+    L.slot_basic = L.map + S4;
+    L.slot_abc = L.slot_basic + N4;
+    return L;
+}
+
+template <class P>
 __global__ __launch_bounds__(kWave) void efs_kernel(DevModel m, DevNeighbors nb, EfsOut out,
                                                      int deterministic)
 {
     extern __shared__ double lds[];
     const int lane = threadIdx.x;
-    const int ncoef_r = m.Z * m.Z * m.M * m.R;
-    // LDS: radial coefficients | moments | adjoints | transpose buffer, each
-    // region a multiple of 4 doubles so the double4 view stays 32-byte aligned
-    double *coef = lds;
-    double *mom = coef + ((ncoef_r + 3) & ~3);
-    double *A = mom + ((m.K + 3) & ~3);
-    double *red = A + ((m.K + 3) & ~3);
-    const double4 *A4 = reinterpret_cast<const double4 *>(red);
+    const Lds L = lds_layout(m, lds);
+    const double4 *A4 = reinterpret_cast<const double4 *>(L.red);
 
+    // model tables the per-atom phases index, staged once per workgroup
+    const int ncoef_r = m.Z * m.Z * m.M * m.R;
     for (int k = lane; k < ncoef_r; k += kWave)
-        coef[k] = m.radial[k];
+        L.coef[k] = m.radial[k];
+    for (int k = lane; k < m.K; k += kWave)
+        L.seed[k] = m.seed[k];
+    for (int k = lane; k < m.S; k += kWave) {
+        L.moment[k] = m.moment[k];
+        L.map[k] = m.map[k];
+    }
+    for (int k = lane; k < m.nslots; k += kWave) {
+        L.slot_basic[k] = m.slot_basic[k];
+        L.slot_abc[k] = m.slot_abc[k];
+    }
     __syncthreads();
 
     double e_acc = 0.0;  // this lane's share of the block's energy and virial
@@ -258,43 +425,28 @@ __global__ __launch_bounds__(kWave) void efs_kernel(DevModel m, DevNeighbors nb,
         const int beg = nb.offsets[i];
         const int n = nb.offsets[i + 1] - beg;
         for (int k = lane; k < m.K; k += kWave)
-            mom[k] = 0.0;
+            L.mom[k] = 0.0;
         __syncthreads();
 
         // ---- basic moments -------------------------------------------------
         for (int base = 0; base < n; base += kWave) {
-            const int ncols = min(kWave, n - base);
-            FwdCtx cx{&m, red, mom, ncols, lane, lane < ncols, 0};
-            Nbr q;
-            if (cx.active)
-                load_neighbor<MMAX, RMAX>(m, nb, coef, ti, beg + base + lane, q);
-            else
-                q = Nbr{};
-            fwd_shells<0, NUMAX, MMAX>(cx, q, nullptr);
+            FwdCtx cx{L.red, L.mom, L.slot_basic, lane, 0};
+            Nbr<P::M> q;
+            const bool valid = lane < n - base;
+            load_neighbor<P>(m, nb, L.coef, ti, beg + base + lane, valid, q);
+            fwd_shells<0, P>(m, cx, q, nullptr);
         }
         if (lane == 0)
             for (int k = 0; k < m.ndup; ++k)
-                mom[m.dup[2 * k]] = mom[m.dup[2 * k + 1]];
+                L.mom[m.dup[2 * k]] = L.mom[m.dup[2 * k + 1]];
         __syncthreads();
 
-        // ---- product rules, forward ----------------------------------------
-        for (int L = 0; L < m.nfwd; ++L) {
-            for (int t = m.fwd_level[L] + lane; t < m.fwd_level[L + 1]; t += kWave) {
-                const int4 task = m.fwd_task[t];
-                double acc = 0.0;
-                for (int k = 0; k < task.z; ++k) {
-                    const int lr = m.fwd_lr[task.y + k];
-                    acc += m.fwd_c[task.y + k] * mom[lr & 0xffff] * mom[lr >> 16];
-                }
-                mom[task.x] = acc;
-            }
-            __syncthreads();
-        }
+        rules_forward(m, L.mom, L.partial, lane);
 
         // ---- site energy (potential_mtp.cpp:2966-2970) and adjoint seed ----
         double e = 0.0;
         for (int s = lane; s < m.S; s += kWave)
-            e += m.moment[s] * mom[m.map[s]];
+            e += L.moment[s] * L.mom[L.map[s]];
         e = wave_sum(e);
         const double site_energy = m.species[ti] + e;
         if (lane == 0) {
@@ -302,62 +454,50 @@ __global__ __launch_bounds__(kWave) void efs_kernel(DevModel m, DevNeighbors nb,
             e_acc += site_energy;
         }
         for (int k = lane; k < m.K; k += kWave)
-            A[k] = m.seed[k];
+            L.A[k] = L.seed[k];
         __syncthreads();
 
-        // ---- product rules, reverse (backpropagate_moments) -----------------
-        for (int L = 0; L < m.nbwd; ++L) {
-            for (int t = m.bwd_level[L] + lane; t < m.bwd_level[L + 1]; t += kWave) {
-                const int4 task = m.bwd_task[t];
-                double acc = A[task.x];
-                for (int k = 0; k < task.z; ++k) {
-                    const int oo = m.bwd_oo[task.y + k];
-                    acc += m.bwd_c[task.y + k] * A[oo & 0xffff] * mom[oo >> 16];
-                }
-                A[task.x] = acc;
-            }
-            __syncthreads();
-        }
+        rules_reverse(m, L.mom, L.A, L.partial, lane);
         if (lane == 0)
             for (int k = 0; k < m.ndup; ++k)
-                A[m.dup[2 * k + 1]] += A[m.dup[2 * k]];
+                L.A[m.dup[2 * k + 1]] += L.A[m.dup[2 * k]];
         __syncthreads();
         // slot-ordered adjoints {A, aA, bA, cA}
         for (int s = lane; s < m.nslots; s += kWave) {
-            const int b = m.slot_basic[s];
+            const int b = L.slot_basic[s];
             double4 w = {0, 0, 0, 0};
             if (b >= 0) {
-                const double a = A[b];
-                const int abc = m.slot_abc[s];
+                const double a = L.A[b];
+                const int abc = L.slot_abc[s];
                 w = {a, a * (abc & 0xff), a * ((abc >> 8) & 0xff), a * ((abc >> 16) & 0xff)};
             }
-            reinterpret_cast<double4 *>(red)[s] = w;
+            reinterpret_cast<double4 *>(L.red)[s] = w;
         }
         __syncthreads();
 
         // ---- forces and virial ---------------------------------------------
         double fi0 = 0, fi1 = 0, fi2 = 0;
         for (int base = 0; base < n; base += kWave) {
-            const bool active = lane < n - base;
-            if (active) {
-                const int64_t p = beg + base + lane;
-                Nbr q;
-                load_neighbor<MMAX, RMAX>(m, nb, coef, ti, p, q);
-                BwdAcc acc{0, 0, 0, 0};
-                int slot = 0;
-                bwd_shells<0, NUMAX, MMAX>(m, A4, slot, q, nullptr, acc);
-                const double D0 = acc.s * q.ux + acc.gx * q.invd;
-                const double D1 = acc.s * q.uy + acc.gy * q.invd;
-                const double D2 = acc.s * q.uz + acc.gz * q.invd;
-                fi0 += D0;
-                fi1 += D1;
-                fi2 += D2;
-                const double r[3] = {q.x, q.y, q.z}, D[3] = {D0, D1, D2};
+            const bool valid = lane < n - base;
+            const int64_t p = beg + base + lane;
+            Nbr<P::M> q;
+            load_neighbor<P>(m, nb, L.coef, ti, p, valid, q);
+            BwdAcc acc{0, 0, 0, 0};
+            int slot = 0;
+            bwd_shells<0, P>(m, A4, slot, q, nullptr, acc);
+            const double D0 = acc.s * q.ux + acc.gx * q.invd;
+            const double D1 = acc.s * q.uy + acc.gy * q.invd;
+            const double D2 = acc.s * q.uz + acc.gz * q.invd;
+            fi0 += D0;
+            fi1 += D1;
+            fi2 += D2;
+            const double r[3] = {q.x, q.y, q.z}, D[3] = {D0, D1, D2};
 #pragma unroll
-                for (int a = 0; a < 3; ++a)
+            for (int a = 0; a < 3; ++a)
 #pragma unroll
-                    for (int bq = 0; bq < 3; ++bq)
-                        v_acc[3 * a + bq] -= D[a] * r[bq];
+                for (int bq = 0; bq < 3; ++bq)
+                    v_acc[3 * a + bq] -= D[a] * r[bq];
+            if (valid) {
                 if (deterministic) {
                     out.pair_ders[3 * p + 0] = D0;
                     out.pair_ders[3 * p + 1] = D1;
@@ -447,23 +587,44 @@ __global__ __launch_bounds__(256) void force_gather_kernel(DevNeighbors nb, cons
     forces[3 * k + 2] = f2;
 }
 
+template <int... NM>
+bool profile_is(const DevModel &m)
+{
+    constexpr int nm[] = {NM...};
+    constexpr int M = sizeof...(NM);
+    if (m.M != M)
+        return false;
+    for (int mu = 0; mu < M; ++mu)
+        if (m.numax[mu] != nm[mu])
+            return false;
+    return true;
+}
+
 }  // namespace
 
 size_t efs_lds_bytes(const DevModel &m)
 {
-    const size_t ncoef_r = (size_t)m.Z * m.Z * m.M * m.R;
-    const size_t red = std::max<size_t>((size_t)kChunk * kRedStride, 4 * (size_t)m.nslots);
     auto r4 = [](size_t v) { return (v + 3) & ~size_t(3); };
-    return (r4(ncoef_r) + 2 * r4((size_t)m.K) + red) * sizeof(double);
+    const size_t ncoef_r = (size_t)m.Z * m.Z * m.M * m.R;
+    const size_t red = std::max<size_t>((size_t)kChunk * kRedStride, 4 * r4((size_t)m.nslots));
+    const size_t dbl = r4(ncoef_r) + 3 * r4((size_t)m.K) + red + r4((size_t)m.S) +
+                       r4((size_t)m.max_partials);
+    const size_t ints = r4((size_t)m.S) + 2 * r4((size_t)m.nslots);
+    return dbl * sizeof(double) + ints * sizeof(int);
 }
 
+// 0: level-16 profile, 1: level-20, 2: level-10, 3: small runtime, 4: generic
 int efs_variant(const DevModel &m, int R)
 {
-    if (m.M <= 4 && m.numax_all <= 6 && R <= 8)
+    if (profile_is<6, 4, 2, 0>(m) && R <= 8)
         return 0;
-    if (m.M <= 5 && m.numax_all <= 8 && R <= 10)
+    if (profile_is<8, 6, 4, 2, 0>(m) && R <= 10)
         return 1;
-    return 2;
+    if (profile_is<3, 1, 0>(m) && R <= 8)
+        return 2;
+    if (m.M <= 4 && m.numax_all <= 6 && R <= 8)
+        return 3;
+    return 4;
 }
 
 hipError_t launch_efs(const DevModel &m, const DevNeighbors &nb, const EfsOut &out, int grid,
@@ -473,15 +634,24 @@ hipError_t launch_efs(const DevModel &m, const DevNeighbors &nb, const EfsOut &o
     const int det = deterministic ? 1 : 0;
     switch (efs_variant(m, m.R)) {
     case 0:
-        hipLaunchKernelGGL((efs_kernel<4, 6, 8>), dim3(grid), dim3(kWave), lds, s, m, nb, out, det);
+        hipLaunchKernelGGL(efs_kernel<ProfLevel16>, dim3(grid), dim3(kWave), lds, s, m, nb, out,
+                           det);
         break;
     case 1:
-        hipLaunchKernelGGL((efs_kernel<5, 8, 10>), dim3(grid), dim3(kWave), lds, s, m, nb, out,
+        hipLaunchKernelGGL(efs_kernel<ProfLevel20>, dim3(grid), dim3(kWave), lds, s, m, nb, out,
+                           det);
+        break;
+    case 2:
+        hipLaunchKernelGGL(efs_kernel<ProfLevel10>, dim3(grid), dim3(kWave), lds, s, m, nb, out,
+                           det);
+        break;
+    case 3:
+        hipLaunchKernelGGL(efs_kernel<ProfSmall>, dim3(grid), dim3(kWave), lds, s, m, nb, out,
                            det);
         break;
     default:
-        hipLaunchKernelGGL((efs_kernel<kMaxMu, kMaxNu, kMaxR>), dim3(grid), dim3(kWave), lds, s, m,
-                           nb, out, det);
+        hipLaunchKernelGGL(efs_kernel<ProfGeneric>, dim3(grid), dim3(kWave), lds, s, m, nb, out,
+                           det);
         break;
     }
     return hipGetLastError();

@@ -9,6 +9,7 @@
 #include "mtpx_internal.hpp"
 
 #include <algorithm>
+#include <array>
 #include <cmath>
 #include <cstdlib>
 #include <cstring>
@@ -380,47 +381,102 @@ bool build_plan(const Model &m, Plan &p, std::string &err)
         maxl = std::max(maxl, level[x]);
     p.max_level = maxl;
 
-    // Forward tasks: outputs of each level, rules of an output in file order.
+    // Forward: outputs of each level, an output's rules in file order.
     std::vector<std::vector<int>> by_out((size_t)m.K);
     for (int t = 0; t < m.T; ++t)
         by_out[m.times[4 * t + 3]].push_back(t);
-    p.fwd_level.push_back(0);
+    auto emit_level = [&p](std::vector<std::vector<std::array<int, 4>>> &tasks,
+                           std::vector<int> &level_step, std::vector<int> &steps,
+                           std::vector<int> &level_comb, std::vector<int> &comb) {
+        size_t total = 0;
+        for (auto &t : tasks)
+            total += t.size();
+        const size_t cap = std::max<size_t>(4, (total + kWave - 1) / kWave);
+        // split long tasks into pieces that end in partial sums
+        std::vector<std::vector<std::array<int, 4>>> pieces;
+        int npart = 0;
+        for (auto &t : tasks) {
+            if (t.size() <= cap) {
+                pieces.push_back(t);
+                continue;
+            }
+            const int target = t.back()[3];
+            const int first = npart;
+            for (size_t b0 = 0; b0 < t.size(); b0 += cap) {
+                std::vector<std::array<int, 4>> piece(t.begin() + b0,
+                                                      t.begin() + std::min(t.size(), b0 + cap));
+                piece.back()[3] = -2 - npart++;
+                pieces.push_back(std::move(piece));
+            }
+            comb.insert(comb.end(), {target, first, npart - first, 0});
+        }
+        p.max_partials = std::max(p.max_partials, npart);
+        level_comb.push_back((int)comb.size() / 4);
+        // longest-processing-time assignment of pieces to the 64 lanes
+        std::vector<int> order(pieces.size());
+        for (size_t i = 0; i < order.size(); ++i)
+            order[i] = (int)i;
+        std::stable_sort(order.begin(), order.end(),
+                         [&](int a, int b) { return pieces[a].size() > pieces[b].size(); });
+        std::vector<std::vector<std::array<int, 4>>> lane(kWave);
+        std::vector<size_t> load(kWave, 0);
+        for (int t : order) {
+            int q = (int)(std::min_element(load.begin(), load.end()) - load.begin());
+            lane[q].insert(lane[q].end(), pieces[t].begin(), pieces[t].end());
+            load[q] += pieces[t].size();
+        }
+        size_t nst = *std::max_element(load.begin(), load.end());
+        nst = (nst + 3) & ~size_t(3);
+        const size_t base = steps.size() / 4 / kWave;
+        steps.resize((base + nst) * kWave * 4, 0);
+        for (int q = 0; q < kWave; ++q)
+            for (size_t st = 0; st < nst; ++st) {
+                std::array<int, 4> e = st < lane[q].size() ? lane[q][st]
+                                                           : std::array<int, 4>{0, 0, 0, -1};
+                for (int c = 0; c < 4; ++c)
+                    steps[((base + st) * kWave + q) * 4 + c] = e[c];
+            }
+        level_step.push_back((int)(base + nst));
+    };
+    p.fwd_level_comb.push_back(0);
+    p.bwd_level_comb.push_back(0);
+    p.fwd_level_step.push_back(0);
     for (int L = 1; L <= maxl; ++L) {
+        std::vector<std::vector<std::array<int, 4>>> tasks;
         for (int o = 0; o < m.K; ++o) {
             if (level[o] != L || by_out[o].empty())
                 continue;
-            p.fwd_task.insert(p.fwd_task.end(), {o, (int)p.fwd_lr.size(), (int)by_out[o].size(), 0});
+            std::vector<std::array<int, 4>> task;
             for (int t : by_out[o]) {
                 const int *r = &m.times[4 * t];
-                p.fwd_lr.push_back(r[0] | (r[1] << 16));
-                p.fwd_c.push_back((double)r[2]);
+                task.push_back({r[0], r[1], r[2], -1});
             }
+            task.back()[3] = o;
+            tasks.push_back(std::move(task));
         }
-        p.fwd_level.push_back((int)p.fwd_task.size() / 4);
+        emit_level(tasks, p.fwd_level_step, p.fwd_steps, p.fwd_level_comb, p.fwd_comb);
     }
 
-    // Reverse tasks: destinations of each level from the top down; entries of
-    // a destination in reverse file order, the right operand's entry first
-    // (backpropagate_moments, potential_mtp.cpp:3292-3305).
-    std::vector<std::vector<int>> ent((size_t)m.K);  // pairs {out, other} and c via index
-    std::vector<std::vector<double>> entc((size_t)m.K);
+    // Reverse: destinations of each level from the top down; a destination's
+    // entries in reverse file order, the right operand's entry of a rule
+    // first (backpropagate_moments, potential_mtp.cpp:3292-3305).
+    std::vector<std::vector<std::array<int, 4>>> ent((size_t)m.K);
     for (int t = m.T - 1; t >= 0; --t) {
         const int *r = &m.times[4 * t];
-        ent[r[1]].push_back(r[3] | (r[0] << 16));
-        entc[r[1]].push_back((double)r[2]);
-        ent[r[0]].push_back(r[3] | (r[1] << 16));
-        entc[r[0]].push_back((double)r[2]);
+        ent[r[1]].push_back({r[3], r[0], r[2], -1});
+        ent[r[0]].push_back({r[3], r[1], r[2], -1});
     }
-    p.bwd_level.push_back(0);
+    p.bwd_level_step.push_back(0);
     for (int L = maxl - 1; L >= 0; --L) {
+        std::vector<std::vector<std::array<int, 4>>> tasks;
         for (int x = 0; x < m.K; ++x) {
             if (level[x] != L || ent[x].empty())
                 continue;
-            p.bwd_task.insert(p.bwd_task.end(), {x, (int)p.bwd_oo.size(), (int)ent[x].size(), 0});
-            p.bwd_oo.insert(p.bwd_oo.end(), ent[x].begin(), ent[x].end());
-            p.bwd_c.insert(p.bwd_c.end(), entc[x].begin(), entc[x].end());
+            std::vector<std::array<int, 4>> task = ent[x];
+            task.back()[3] = x;
+            tasks.push_back(std::move(task));
         }
-        p.bwd_level.push_back((int)p.bwd_task.size() / 4);
+        emit_level(tasks, p.bwd_level_step, p.bwd_steps, p.bwd_level_comb, p.bwd_comb);
     }
     return true;
 }

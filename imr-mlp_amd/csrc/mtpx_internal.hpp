@@ -16,7 +16,7 @@ constexpr int kMaxNu = 8;       // angular degree a+b+c
 constexpr int kMaxR = 16;       // radial basis size
 constexpr int kWave = 64;       // CDNA wavefront
 constexpr int kChunk = 16;      // slots per LDS reduction chunk
-constexpr int kRedStride = 65;  // padded row stride of the reduction buffer
+constexpr int kRedStride = 66;  // row stride of the reduction buffer (16-byte rows, no bank conflicts)
 
 // Growable device allocation owned by a context.
 struct DBuf {
@@ -98,16 +98,21 @@ struct Plan {
     std::vector<int> slot_basic;   // [nslots] basic index or -1 (padding)
     std::vector<int> slot_abc;     // [nslots] a | b << 8 | c << 16
     std::vector<int> dup;          // [ndup][2] {duplicate basic, source basic}
-    // forward: level ranges over tasks, task = {out, first, count, 0}
-    std::vector<int> fwd_level;    // [nfwd+1]
-    std::vector<int> fwd_task;     // [ntask][4]
-    std::vector<int> fwd_lr;       // [T] l | r << 16
-    std::vector<double> fwd_c;     // [T]
-    // reverse: level ranges over tasks, task = {dst, first, count, 0}
-    std::vector<int> bwd_level;
-    std::vector<int> bwd_task;
-    std::vector<int> bwd_oo;       // [2T] out | other << 16
-    std::vector<double> bwd_c;     // [2T]
+    // Lane-major step tables, one per direction.  Level L owns steps
+    // [level_step[L], level_step[L+1]) (a multiple of 4); step s of lane q is
+    // entry s * 64 + q, an int4:
+    //   forward {l, r, c, w}:      acc += c m_l m_r
+    //   reverse {o, other, c, w}:  acc += c A_o m_other
+    // w == -1 continues; w >= 0 finalises the task (forward m_w = acc,
+    // reverse A_w += acc); w <= -2 stores acc in partial[-w - 2].  A task
+    // longer than the level's fair share (entries / 64) is split into
+    // pieces whose partial sums the level's combine list adds in order:
+    // combine entry {target, first partial, count, 0}.  Tasks and pieces
+    // are spread over the lanes by longest-processing-time assignment;
+    // padding steps have c = 0.
+    std::vector<int> fwd_level_step, fwd_steps, fwd_level_comb, fwd_comb;
+    std::vector<int> bwd_level_step, bwd_steps, bwd_level_comb, bwd_comb;
+    int max_partials = 0;
     int max_level = 0;
 };
 bool build_plan(const Model &m, Plan &p, std::string &err);
@@ -119,7 +124,7 @@ struct DevModel {
     int numax[kMaxMu];
     int numax_all;
     int ndup;
-    int nfwd, nbwd;
+    int nfwd, nbwd;  // levels
     const double *radial;   // [Z*Z*M*R]
     const double *species;  // [Z]
     const double *moment;   // [S]
@@ -128,14 +133,15 @@ struct DevModel {
     const int *slot_basic;  // [nslots]
     const int *slot_abc;    // [nslots] a | b << 8 | c << 16
     const int *dup;         // [ndup][2]
-    const int *fwd_level;
-    const int4 *fwd_task;
-    const int *fwd_lr;
-    const double *fwd_c;
-    const int *bwd_level;
-    const int4 *bwd_task;
-    const int *bwd_oo;
-    const double *bwd_c;
+    int max_partials;
+    const int *fwd_level_step;  // [nfwd+1]
+    const int4 *fwd_steps;
+    const int *fwd_level_comb;  // [nfwd+1]
+    const int4 *fwd_comb;
+    const int *bwd_level_step;  // [nbwd+1]
+    const int4 *bwd_steps;
+    const int *bwd_level_comb;  // [nbwd+1]
+    const int4 *bwd_comb;
 };
 
 // Neighbour lists resident on the device (SoA).
