@@ -240,6 +240,8 @@ int run_efs(mtpx_context *ctx, bool deterministic)
     const size_t lds = efs_lds_bytes(ctx->dm);
     // workgroups per CU the LDS budget allows; register limits cap it further
     per_cu = std::max(1, std::min(8, (int)((160 * 1024) / std::max<size_t>(lds, 1))));
+    if (const char *g = getenv("MTPX_EFS_BLOCKS_PER_CU"))  // tuning
+        per_cu = std::max(1, atoi(g));
     ctx->grid = std::max(1, std::min(n, ctx->num_cus * per_cu));
     HIP_TRY(ctx->forces.ensure(sizeof(double) * 3 * std::max(n, 1)), "allocate forces");
     HIP_TRY(ctx->site_energy.ensure(sizeof(double) * std::max(n, 1)), "allocate site energies");

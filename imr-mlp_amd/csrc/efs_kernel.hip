@@ -28,6 +28,8 @@
 // generic variants read the profile at run time.
 #include "mtpx_internal.hpp"
 
+#include <cstdlib>
+
 namespace mtpx {
 
 namespace {
@@ -74,10 +76,30 @@ using ProfLevel20 = ExactProfile<5, 8, 10, 8, 6, 4, 2, 0>;
 using ProfSmall = RuntimeProfile<4, 6, 8>;
 using ProfGeneric = RuntimeProfile<kMaxMu, kMaxNu, kMaxR>;
 
+// v[l] + v[l ^ 32] and v[l] + v[l ^ 16] with the gfx950 lane swaps (VALU, no
+// LDS crossbar): permlane32_swap exchanges the wave halves, permlane16_swap
+// the odd and even rows of 16 lanes.
+__device__ __forceinline__ double xor32_sum(double v)
+{
+    const unsigned lo = __double2loint(v), hi = __double2hiint(v);
+    const auto l = __builtin_amdgcn_permlane32_swap(lo, lo, false, false);
+    const auto h = __builtin_amdgcn_permlane32_swap(hi, hi, false, false);
+    return __hiloint2double(h[0], l[0]) + __hiloint2double(h[1], l[1]);
+}
+__device__ __forceinline__ double xor16_sum(double v)
+{
+    const unsigned lo = __double2loint(v), hi = __double2hiint(v);
+    const auto l = __builtin_amdgcn_permlane16_swap(lo, lo, false, false);
+    const auto h = __builtin_amdgcn_permlane16_swap(hi, hi, false, false);
+    return __hiloint2double(h[0], l[0]) + __hiloint2double(h[1], l[1]);
+}
+
 __device__ __forceinline__ double wave_sum(double v)
 {
+    v = xor32_sum(v);
+    v = xor16_sum(v);
 #pragma unroll
-    for (int off = 32; off >= 1; off >>= 1)
+    for (int off = 8; off >= 1; off >>= 1)
         v += __shfl_xor(v, off, kWave);
     return v;
 }
@@ -176,9 +198,7 @@ __device__ __forceinline__ void reduce_chunk(const double *red, int nrows, int s
         a0 += v.x;
         a1 += v.y;
     }
-    double acc = a0 + a1;
-    acc += __shfl_xor(acc, 16, kWave);
-    acc += __shfl_xor(acc, 32, kWave);
+    double acc = xor16_sum(xor32_sum(a0 + a1));
     if (lane < nrows) {
         const int b = slot_basic[slot0 + lane];
         if (b >= 0)
@@ -190,7 +210,7 @@ __device__ __forceinline__ void reduce_chunk(const double *red, int nrows, int s
 struct FwdCtx {
     double *red, *mom;
     const int *slot_basic;
-    int lane, slot;
+    int lane, slot;  // slots written so far; rows are packed across (nu, mu) blocks
 };
 
 template <int NU, class P>
@@ -206,16 +226,13 @@ __device__ __forceinline__ void fwd_shells(const DevModel &m, FwdCtx &cx, const 
     for (int mu = 0; mu < P::M; ++mu) {
         if (P::active(m, mu, NU)) {
             __builtin_amdgcn_sched_barrier(0);
-            int row = 0;
 #pragma unroll
             for (int i = 0; i < shell_size(NU); ++i) {
-                cx.red[row * kRedStride + cx.lane] = q.f[mu] * cur[i];
-                ++row;
-                if (row == kChunk || i == shell_size(NU) - 1) {
-                    reduce_chunk(cx.red, row, cx.slot, cx.slot_basic, cx.mom, cx.lane);
-                    cx.slot += row;
-                    row = 0;
-                }
+                cx.red[(cx.slot % kChunk) * kRedStride + cx.lane] = q.f[mu] * cur[i];
+                ++cx.slot;
+                if (cx.slot % kChunk == 0)
+                    reduce_chunk(cx.red, kChunk, cx.slot - kChunk, cx.slot_basic, cx.mom,
+                                 cx.lane);
             }
         }
     }
@@ -392,9 +409,9 @@ __device__ __forceinline__ Lds lds_layout(const DevModel &m, double *base)
     return L;
 }
 
-template <class P>
-__global__ __launch_bounds__(kWave) void efs_kernel(DevModel m, DevNeighbors nb, EfsOut out,
-                                                     int deterministic)
+template <class P, int WPE>
+__global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(WPE))) void efs_kernel(
+    DevModel m, DevNeighbors nb, EfsOut out, int deterministic)
 {
     extern __shared__ double lds[];
     const int lane = threadIdx.x;
@@ -435,6 +452,9 @@ __global__ __launch_bounds__(kWave) void efs_kernel(DevModel m, DevNeighbors nb,
             const bool valid = lane < n - base;
             load_neighbor<P>(m, nb, L.coef, ti, beg + base + lane, valid, q);
             fwd_shells<0, P>(m, cx, q, nullptr);
+            const int rest = cx.slot % kChunk;
+            if (rest)
+                reduce_chunk(L.red, rest, cx.slot - rest, L.slot_basic, L.mom, lane);
         }
         if (lane == 0)
             for (int k = 0; k < m.ndup; ++k)
@@ -632,26 +652,36 @@ hipError_t launch_efs(const DevModel &m, const DevNeighbors &nb, const EfsOut &o
 {
     const size_t lds = efs_lds_bytes(m);
     const int det = deterministic ? 1 : 0;
+    // MTPX_EFS_WAVES_PER_EU (tuning): occupancy the level-16 kernel is
+    // register-allocated for (1 = compiler's choice, 3)
+    static const int wpe = [] {
+        const char *e = getenv("MTPX_EFS_WAVES_PER_EU");
+        return e ? atoi(e) : 1;
+    }();
     switch (efs_variant(m, m.R)) {
     case 0:
-        hipLaunchKernelGGL(efs_kernel<ProfLevel16>, dim3(grid), dim3(kWave), lds, s, m, nb, out,
-                           det);
+        if (wpe == 3)
+            hipLaunchKernelGGL((efs_kernel<ProfLevel16, 3>), dim3(grid), dim3(kWave), lds, s, m, nb,
+                               out, det);
+        else
+            hipLaunchKernelGGL((efs_kernel<ProfLevel16, 1>), dim3(grid), dim3(kWave), lds, s, m, nb,
+                               out, det);
         break;
     case 1:
-        hipLaunchKernelGGL(efs_kernel<ProfLevel20>, dim3(grid), dim3(kWave), lds, s, m, nb, out,
-                           det);
+        hipLaunchKernelGGL((efs_kernel<ProfLevel20, 1>), dim3(grid), dim3(kWave), lds, s, m, nb,
+                           out, det);
         break;
     case 2:
-        hipLaunchKernelGGL(efs_kernel<ProfLevel10>, dim3(grid), dim3(kWave), lds, s, m, nb, out,
-                           det);
+        hipLaunchKernelGGL((efs_kernel<ProfLevel10, 1>), dim3(grid), dim3(kWave), lds, s, m, nb,
+                           out, det);
         break;
     case 3:
-        hipLaunchKernelGGL(efs_kernel<ProfSmall>, dim3(grid), dim3(kWave), lds, s, m, nb, out,
+        hipLaunchKernelGGL((efs_kernel<ProfSmall, 1>), dim3(grid), dim3(kWave), lds, s, m, nb, out,
                            det);
         break;
     default:
-        hipLaunchKernelGGL(efs_kernel<ProfGeneric>, dim3(grid), dim3(kWave), lds, s, m, nb, out,
-                           det);
+        hipLaunchKernelGGL((efs_kernel<ProfGeneric, 1>), dim3(grid), dim3(kWave), lds, s, m, nb,
+                           out, det);
         break;
     }
     return hipGetLastError();
