@@ -15,6 +15,7 @@ struct mtpx_context {
     hipStream_t stream = nullptr;
     std::string err;
     int num_cus = 256;
+    size_t lds_limit = 160 * 1024;  // LDS one workgroup may allocate
 
     bool has_model = false;
     Model model;
@@ -37,7 +38,7 @@ struct mtpx_context {
 
     // outputs
     DBuf forces, site_energy, partial, pair_ders, out10;
-    int grid = 0;
+    EfsLaunch launch{};
 
     hipEvent_t ev[3] = {nullptr, nullptr, nullptr};
     double timings[4] = {0, 0, 0, 0};
@@ -166,15 +167,23 @@ int install_model(mtpx_context *ctx, Model &&m)
     dm.slot_abc = ctx->slot_abc.as<int>();
     dm.dup = ctx->dup.as<int>();
     dm.fwd_level_step = ctx->fwd_level.as<int>();
-    dm.fwd_steps = ctx->fwd_steps.as<int4>();
+    dm.fwd_steps = ctx->fwd_steps.as<int2>();
     dm.bwd_level_step = ctx->bwd_level.as<int>();
-    dm.bwd_steps = ctx->bwd_steps.as<int4>();
+    dm.bwd_steps = ctx->bwd_steps.as<int2>();
     dm.fwd_level_comb = ctx->fwd_lcomb.as<int>();
     dm.fwd_comb = ctx->fwd_comb.as<int4>();
     dm.bwd_level_comb = ctx->bwd_lcomb.as<int>();
     dm.bwd_comb = ctx->bwd_comb.as<int4>();
     dm.max_partials = P.max_partials;
-    if (efs_lds_bytes(dm) > 160 * 1024)
+    dm.K4 = P.K4;
+    dm.dummy = P.dummy;
+    dm.part0 = P.part0;
+    dm.red0 = P.red0;
+    dm.priv_doubles = P.priv_doubles;
+    dm.fwd_nsteps = P.fwd_level_step.back();
+    dm.bwd_nsteps = P.bwd_level_step.back();
+    EfsLaunch probe;
+    if (!efs_configure(dm, 1, 1, 0, ctx->lds_limit, probe))
         return set_error(ctx, MTPX_E_CAPACITY, "model needs more LDS than a CU provides");
     int rc = upload_coeffs(ctx);
     if (rc != MTPX_OK)
@@ -236,16 +245,18 @@ int run_efs(mtpx_context *ctx, bool deterministic)
     }
     const int n = ctx->n;
     hipStream_t s = ctx->stream;
-    int per_cu = 0;
-    const size_t lds = efs_lds_bytes(ctx->dm);
-    // workgroups per CU the LDS budget allows; register limits cap it further
-    per_cu = std::max(1, std::min(8, (int)((160 * 1024) / std::max<size_t>(lds, 1))));
-    if (const char *g = getenv("MTPX_EFS_BLOCKS_PER_CU"))  // tuning
-        per_cu = std::max(1, atoi(g));
-    ctx->grid = std::max(1, std::min(n, ctx->num_cus * per_cu));
+    // MTPX_EFS_WAVES (tuning): cap on the waves per workgroup
+    static const int max_waves = [] {
+        const char *e = getenv("MTPX_EFS_WAVES");
+        return e ? atoi(e) : 0;
+    }();
+    EfsLaunch cfg;
+    if (!efs_configure(ctx->dm, n, ctx->num_cus, max_waves, ctx->lds_limit, cfg))
+        return set_error(ctx, MTPX_E_CAPACITY, "model needs more LDS than a CU provides");
+    ctx->launch = cfg;
     HIP_TRY(ctx->forces.ensure(sizeof(double) * 3 * std::max(n, 1)), "allocate forces");
     HIP_TRY(ctx->site_energy.ensure(sizeof(double) * std::max(n, 1)), "allocate site energies");
-    HIP_TRY(ctx->partial.ensure(sizeof(double) * 10 * ctx->grid), "allocate partials");
+    HIP_TRY(ctx->partial.ensure(sizeof(double) * 10 * cfg.rows), "allocate partials");
     HIP_TRY(ctx->out10.ensure(sizeof(double) * 10), "allocate outputs");
     if (deterministic)
         HIP_TRY(ctx->pair_ders.ensure(sizeof(double) * 3 * std::max<int64_t>(ctx->P, 1)),
@@ -260,10 +271,10 @@ int run_efs(mtpx_context *ctx, bool deterministic)
         HIP_TRY(hipMemsetAsync(out.forces, 0, sizeof(double) * 3 * n, s), "clear forces");
     HIP_TRY(hipEventRecord(ctx->ev[0], s), "record event");
     if (n > 0)
-        HIP_TRY(launch_efs(ctx->dm, nb, out, ctx->grid, deterministic, s), "launch efs kernel");
+        HIP_TRY(launch_efs(ctx->dm, nb, out, cfg, deterministic, s), "launch efs kernel");
     HIP_TRY(hipEventRecord(ctx->ev[1], s), "record event");
     if (n > 0)
-        HIP_TRY(launch_efs_finish(nb, out, ctx->grid, deterministic, ctx->rev_offsets.as<int>(),
+        HIP_TRY(launch_efs_finish(nb, out, cfg.rows, deterministic, ctx->rev_offsets.as<int>(),
                                   ctx->rev_pairs.as<int>(), ctx->out10.as<double>(), s),
                 "launch efs reductions");
     else
@@ -312,8 +323,11 @@ int mtpx_create(int device, mtpx_context **out)
             return MTPX_E_DEVICE;
         }
     hipDeviceProp_t prop;
-    if (hipGetDeviceProperties(&prop, device) == hipSuccess && prop.multiProcessorCount > 0)
+    if (hipGetDeviceProperties(&prop, device) == hipSuccess && prop.multiProcessorCount > 0) {
         ctx->num_cus = prop.multiProcessorCount;
+        if (prop.sharedMemPerBlock > 0)
+            ctx->lds_limit = std::min<size_t>(ctx->lds_limit, prop.sharedMemPerBlock);
+    }
     *out = ctx;
     return MTPX_OK;
 }

@@ -4,7 +4,11 @@
 // (potentials/potential_mtp.cpp:2813-2984, :1899-1933).  The arithmetic is
 // reorganised for a wave64; results agree with the reference to rounding.
 //
-// One workgroup = one wave64, grid-stride over atoms.  Per atom:
+// A workgroup holds up to eight wave64s that share one LDS copy of the model
+// tables (radial coefficients, adjoint seeds, moment coefficients, slot
+// tables and, when they fit, the product-rule step tables).  Each wave owns a
+// private LDS work space and works through its own atoms (grid-stride), so the
+// waves synchronise only at wavefront scope.  Per atom:
 //   1. lanes over neighbours: Chebyshev basis Q_k(d), radial functions
 //      f_mu = sum_k c[ti,tj,mu,k] Q_k (coefficients staged in LDS), unit
 //      vector u = r/d.  Every basic moment (mu, a, b, c) equals
@@ -12,15 +16,16 @@
 //      are produced shell by shell (degree nu = a+b+c, compile-time unrolled)
 //      in registers and summed over neighbours through a padded LDS
 //      transpose, 16 slots at a time.
-//   2. the product rules run lane-parallel from lane-major step tables, one
-//      dependency level at a time (forward values, then reverse adjoints).
+//   2. the product rules run lane-parallel from lane-major step tables of
+//      8-byte entries, one dependency level at a time (forward values, then
+//      reverse adjoints).
 //   3. lanes over neighbours again: dE_i/dr_j from the closed form
 //      grad_r[f Y] = (f' - nu f/d) Y u + (f/d) grad_u Y, with the basic
 //      adjoints read as LDS broadcasts.
 //   4. F_i += sum_j D_j, F_idx(j) -= D_j, S_ab -= D_ja r_jb.  Fast mode uses
 //      fp64 atomics for the neighbour reactions; deterministic mode stores D
 //      per pair for an ordered gather.  Energy and virial are reduced per
-//      workgroup and finished by a single ordered pass.
+//      wave and finished by a single ordered pass.
 //
 // Kernel variants: a "shell profile" fixes, per radial function mu, the
 // highest angular degree of its basic moments.  The level-10/16/20 template
@@ -28,7 +33,7 @@
 // generic variants read the profile at run time.
 #include "mtpx_internal.hpp"
 
-#include <cstdlib>
+#include <algorithm>
 
 namespace mtpx {
 
@@ -102,6 +107,16 @@ __device__ __forceinline__ double wave_sum(double v)
     for (int off = 8; off >= 1; off >>= 1)
         v += __shfl_xor(v, off, kWave);
     return v;
+}
+
+// Orders the LDS accesses of one wave: a wave's LDS operations complete in
+// issue order, so a compiler-level fence at wavefront scope is all that is
+// needed between a lane's store and another lane's load.
+__device__ __forceinline__ void wave_sync()
+{
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
 template <int MMAX>
@@ -188,7 +203,7 @@ __device__ __forceinline__ void next_shell(const double *prev, double *cur, cons
 __device__ __forceinline__ void reduce_chunk(const double *red, int nrows, int slot0,
                                              const int *slot_basic, double *mom, int lane)
 {
-    __syncthreads();
+    wave_sync();
     const int s = lane & (kChunk - 1), qq = lane >> 4;
     const double2 *row = reinterpret_cast<const double2 *>(red + s * kRedStride + qq * 16);
     double a0 = 0.0, a1 = 0.0;
@@ -204,7 +219,7 @@ __device__ __forceinline__ void reduce_chunk(const double *red, int nrows, int s
         if (b >= 0)
             mom[b] += acc;
     }
-    __syncthreads();
+    wave_sync();
 }
 
 struct FwdCtx {
@@ -292,181 +307,177 @@ __device__ __forceinline__ void bwd_shells(const DevModel &m, const double4 *A4,
     }
 }
 
-// One level of a lane-major step table; entries are prefetched four steps
-// ahead so every step costs one coalesced, already-resident int4.
-template <class Step>
-__device__ __forceinline__ void run_steps(const int4 *steps, int s0, int s1, int lane, Step step)
+// Product rules from a lane-major step table (forward: potential_mtp.cpp:
+// 2918-2924; reverse: backpropagate_moments, :3292-3305), one dependency
+// level at a time.  Steps are taken in groups of four: the entries of the
+// next group are loaded while the current one runs, and every operand of a
+// group is read before any of its results is written (a level never reads
+// what it writes).
+__device__ __forceinline__ void run_rules(const int2 *tab, const int *level_step,
+                                          const int *level_comb, const int4 *comb, int nlev,
+                                          double *ws, int lane)
 {
-    if (s1 <= s0)
-        return;
-    const int4 *tab = steps + (size_t)s0 * kWave + lane;
-    int4 e0 = tab[0], e1 = tab[kWave], e2 = tab[2 * kWave], e3 = tab[3 * kWave];
-    for (int st = s0; st < s1; st += 4) {
-        int4 n0 = e0, n1 = e1, n2 = e2, n3 = e3;
-        if (st + 4 < s1) {
-            const int4 *nt = tab + (size_t)(st + 4 - s0) * kWave;
-            n0 = nt[0];
-            n1 = nt[kWave];
-            n2 = nt[2 * kWave];
-            n3 = nt[3 * kWave];
-        }
-        step(e0);
-        step(e1);
-        step(e2);
-        step(e3);
-        e0 = n0;
-        e1 = n1;
-        e2 = n2;
-        e3 = n3;
-    }
-}
-
-// Product rules, forward (potential_mtp.cpp:2918-2924): one level at a time.
-__device__ __forceinline__ void rules_forward(const DevModel &m, double *mom, double *partial,
-                                              int lane)
-{
-    for (int L = 0; L < m.nfwd; ++L) {
+    for (int L = 0; L < nlev; ++L) {
+        const int s0 = level_step[L], s1 = level_step[L + 1];
         double acc = 0.0;
-        run_steps(m.fwd_steps, m.fwd_level_step[L], m.fwd_level_step[L + 1], lane,
-                  [&](const int4 &e) {
-                      acc += (double)e.z * mom[e.x] * mom[e.y];
-                      if (e.w != -1) {
-                          if (e.w >= 0)
-                              mom[e.w] = acc;
-                          else
-                              partial[-e.w - 2] = acc;
-                          acc = 0.0;
-                      }
-                  });
-        const int c0 = m.fwd_level_comb[L], c1 = m.fwd_level_comb[L + 1];
-        if (c1 > c0) {
-            __syncthreads();
-            for (int c = c0 + lane; c < c1; c += kWave) {
-                const int4 t = m.fwd_comb[c];
-                double sum = 0.0;
-                for (int k = 0; k < t.z; ++k)
-                    sum += partial[t.y + k];
-                mom[t.x] = sum;
+        if (s1 > s0) {
+            const int2 *t = tab + (size_t)s0 * kWave + lane;
+            int2 e[4] = {t[0], t[kWave], t[2 * kWave], t[3 * kWave]};
+            for (int st = s0; st < s1; st += 4) {
+                int2 nx[4] = {e[0], e[1], e[2], e[3]};
+                if (st + 4 < s1) {
+                    const int2 *u = t + (size_t)(st + 4 - s0) * kWave;
+                    nx[0] = u[0];
+                    nx[1] = u[kWave];
+                    nx[2] = u[2 * kWave];
+                    nx[3] = u[3 * kWave];
+                }
+                double ml[4], mr[4], init[4], v[4];
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    ml[k] = ws[e[k].x & 0xffff];
+                    mr[k] = ws[(unsigned)e[k].x >> 16];
+                    init[k] = ws[e[k].y & 0xffff];
+                }
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const double c = (double)(e[k].y >> 17);
+                    acc = fma(c * ml[k], mr[k], (e[k].y & 0x10000) ? init[k] : acc);
+                    v[k] = acc;
+                }
+#pragma unroll
+                for (int k = 0; k < 4; ++k)
+                    ws[e[k].y & 0xffff] = v[k];
+#pragma unroll
+                for (int k = 0; k < 4; ++k)
+                    e[k] = nx[k];
             }
         }
-        __syncthreads();
-    }
-}
-
-// Product rules, reverse (backpropagate_moments, potential_mtp.cpp:3292-3305).
-__device__ __forceinline__ void rules_reverse(const DevModel &m, const double *mom, double *A,
-                                              double *partial, int lane)
-{
-    for (int L = 0; L < m.nbwd; ++L) {
-        double acc = 0.0;
-        run_steps(m.bwd_steps, m.bwd_level_step[L], m.bwd_level_step[L + 1], lane,
-                  [&](const int4 &e) {
-                      acc += (double)e.z * A[e.x] * mom[e.y];
-                      if (e.w != -1) {
-                          if (e.w >= 0)
-                              A[e.w] += acc;
-                          else
-                              partial[-e.w - 2] = acc;
-                          acc = 0.0;
-                      }
-                  });
-        const int c0 = m.bwd_level_comb[L], c1 = m.bwd_level_comb[L + 1];
+        const int c0 = level_comb[L], c1 = level_comb[L + 1];
         if (c1 > c0) {
-            __syncthreads();
+            wave_sync();
             for (int c = c0 + lane; c < c1; c += kWave) {
-                const int4 t = m.bwd_comb[c];
-                double sum = 0.0;
-                for (int k = 0; k < t.z; ++k)
-                    sum += partial[t.y + k];
-                A[t.x] += sum;
+                const int4 q = comb[c];
+                double sum = ws[q.x];
+                for (int k = 0; k < q.z; ++k) {
+                    sum += ws[q.y + k];
+                    ws[q.y + k] = 0.0;
+                }
+                ws[q.x] = sum;
             }
         }
-        __syncthreads();
+        wave_sync();
     }
 }
 
-struct Lds {
-    double *coef, *mom, *A, *red, *seed, *moment, *partial;
+// Block-shared LDS tables, in this order (doubles, then ints, then the
+// optional step tables; every part a multiple of 32 bytes).
+struct Shared {
+    double *coef, *seed, *moment;
     int *map, *slot_basic, *slot_abc;
+    int2 *fwd_steps, *bwd_steps;
 };
 
-__device__ __forceinline__ Lds lds_layout(const DevModel &m, double *base)
+__device__ __host__ __forceinline__ size_t shared_doubles(const DevModel &m, bool tables)
 {
-    const int ncoef_r = m.Z * m.Z * m.M * m.R;
-    const int K4 = (m.K + 3) & ~3, S4 = (m.S + 3) & ~3, N4 = (m.nslots + 3) & ~3;
-    const int P4 = (m.max_partials + 3) & ~3;
-    Lds L;
+    const size_t r4c = ((size_t)m.Z * m.Z * m.M * m.R + 3) & ~size_t(3);
+    const size_t S4 = (m.S + 3) & ~3, N4 = (m.nslots + 3) & ~3;
+    size_t d = r4c + m.K4 + S4 + (S4 + 2 * N4) / 2;
+    if (tables)
+        d += (size_t)(m.fwd_nsteps + m.bwd_nsteps) * kWave;
+    return (d + 3) & ~size_t(3);
+}
+
+__device__ __forceinline__ Shared shared_layout(const DevModel &m, double *base)
+{
+    const int r4c = (m.Z * m.Z * m.M * m.R + 3) & ~3;
+    const int S4 = (m.S + 3) & ~3, N4 = (m.nslots + 3) & ~3;
+    Shared L;
     L.coef = base;
-    L.mom = L.coef + ((ncoef_r + 3) & ~3);
-    L.A = L.mom + K4;
-    L.red = L.A + K4;
-    L.seed = L.red + max(kChunk * kRedStride, 4 * N4);
-    L.moment = L.seed + K4;
-    L.partial = L.moment + S4;
-    L.map = reinterpret_cast<int *>(L.partial + P4);
+    L.seed = L.coef + r4c;
+    L.moment = L.seed + m.K4;
+    L.map = reinterpret_cast<int *>(L.moment + S4);
     L.slot_basic = L.map + S4;
     L.slot_abc = L.slot_basic + N4;
+    L.fwd_steps = reinterpret_cast<int2 *>(L.slot_abc + N4);
+    L.bwd_steps = L.fwd_steps + (size_t)m.fwd_nsteps * kWave;
     return L;
 }
 
-template <class P, int WPE>
-__global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(WPE))) void efs_kernel(
-    DevModel m, DevNeighbors nb, EfsOut out, int deterministic)
+template <class P, bool kTabLds, int kMaxWaves>
+__global__ __launch_bounds__(kWave *kMaxWaves) void efs_kernel(DevModel m, DevNeighbors nb,
+                                                               EfsOut out, int deterministic)
 {
     extern __shared__ double lds[];
-    const int lane = threadIdx.x;
-    const Lds L = lds_layout(m, lds);
-    const double4 *A4 = reinterpret_cast<const double4 *>(L.red);
+    const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
+    const int nwaves = blockDim.x / kWave;
+    const Shared L = shared_layout(m, lds);
+    double *ws = lds + shared_doubles(m, kTabLds) + (size_t)wave * m.priv_doubles;
+    double *mom = ws, *A = ws + m.K4, *red = ws + m.red0;
+    const double4 *A4 = reinterpret_cast<const double4 *>(red);
 
     // model tables the per-atom phases index, staged once per workgroup
     const int ncoef_r = m.Z * m.Z * m.M * m.R;
-    for (int k = lane; k < ncoef_r; k += kWave)
+    for (int k = tid; k < ncoef_r; k += blockDim.x)
         L.coef[k] = m.radial[k];
-    for (int k = lane; k < m.K; k += kWave)
+    for (int k = tid; k < m.K; k += blockDim.x)
         L.seed[k] = m.seed[k];
-    for (int k = lane; k < m.S; k += kWave) {
+    for (int k = tid; k < m.S; k += blockDim.x) {
         L.moment[k] = m.moment[k];
         L.map[k] = m.map[k];
     }
-    for (int k = lane; k < m.nslots; k += kWave) {
+    for (int k = tid; k < m.nslots; k += blockDim.x) {
         L.slot_basic[k] = m.slot_basic[k];
         L.slot_abc[k] = m.slot_abc[k];
     }
+    if constexpr (kTabLds) {
+        for (int k = tid; k < m.fwd_nsteps * kWave; k += blockDim.x)
+            L.fwd_steps[k] = m.fwd_steps[k];
+        for (int k = tid; k < m.bwd_nsteps * kWave; k += blockDim.x)
+            L.bwd_steps[k] = m.bwd_steps[k];
+    }
+    // the dummy slot and the partial sums start at zero; the rule phases
+    // leave them zero
+    for (int k = m.dummy + lane; k < m.red0; k += kWave)
+        ws[k] = 0.0;
     __syncthreads();
+    const int2 *fwd_tab = kTabLds ? L.fwd_steps : m.fwd_steps;
+    const int2 *bwd_tab = kTabLds ? L.bwd_steps : m.bwd_steps;
 
-    double e_acc = 0.0;  // this lane's share of the block's energy and virial
+    double e_acc = 0.0;  // this lane's share of the wave's energy and virial
     double v_acc[9] = {0, 0, 0, 0, 0, 0, 0, 0, 0};
 
-    for (int i = blockIdx.x; i < nb.n; i += gridDim.x) {
+    const int row = blockIdx.x * nwaves + wave;
+    for (int i = row; i < nb.n; i += gridDim.x * nwaves) {
         const int ti = nb.center_type[i];
         const int beg = nb.offsets[i];
         const int n = nb.offsets[i + 1] - beg;
         for (int k = lane; k < m.K; k += kWave)
-            L.mom[k] = 0.0;
-        __syncthreads();
+            mom[k] = 0.0;
+        wave_sync();
 
         // ---- basic moments -------------------------------------------------
         for (int base = 0; base < n; base += kWave) {
-            FwdCtx cx{L.red, L.mom, L.slot_basic, lane, 0};
+            FwdCtx cx{red, mom, L.slot_basic, lane, 0};
             Nbr<P::M> q;
             const bool valid = lane < n - base;
             load_neighbor<P>(m, nb, L.coef, ti, beg + base + lane, valid, q);
             fwd_shells<0, P>(m, cx, q, nullptr);
             const int rest = cx.slot % kChunk;
             if (rest)
-                reduce_chunk(L.red, rest, cx.slot - rest, L.slot_basic, L.mom, lane);
+                reduce_chunk(red, rest, cx.slot - rest, L.slot_basic, mom, lane);
         }
         if (lane == 0)
             for (int k = 0; k < m.ndup; ++k)
-                L.mom[m.dup[2 * k]] = L.mom[m.dup[2 * k + 1]];
-        __syncthreads();
+                mom[m.dup[2 * k]] = mom[m.dup[2 * k + 1]];
+        wave_sync();
 
-        rules_forward(m, L.mom, L.partial, lane);
+        run_rules(fwd_tab, m.fwd_level_step, m.fwd_level_comb, m.fwd_comb, m.nfwd, ws, lane);
 
         // ---- site energy (potential_mtp.cpp:2966-2970) and adjoint seed ----
         double e = 0.0;
         for (int s = lane; s < m.S; s += kWave)
-            e += L.moment[s] * L.mom[L.map[s]];
+            e += L.moment[s] * mom[L.map[s]];
         e = wave_sum(e);
         const double site_energy = m.species[ti] + e;
         if (lane == 0) {
@@ -474,26 +485,26 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(WPE))) vo
             e_acc += site_energy;
         }
         for (int k = lane; k < m.K; k += kWave)
-            L.A[k] = L.seed[k];
-        __syncthreads();
+            A[k] = L.seed[k];
+        wave_sync();
 
-        rules_reverse(m, L.mom, L.A, L.partial, lane);
+        run_rules(bwd_tab, m.bwd_level_step, m.bwd_level_comb, m.bwd_comb, m.nbwd, ws, lane);
         if (lane == 0)
             for (int k = 0; k < m.ndup; ++k)
-                L.A[m.dup[2 * k + 1]] += L.A[m.dup[2 * k]];
-        __syncthreads();
+                A[m.dup[2 * k + 1]] += A[m.dup[2 * k]];
+        wave_sync();
         // slot-ordered adjoints {A, aA, bA, cA}
         for (int s = lane; s < m.nslots; s += kWave) {
             const int b = L.slot_basic[s];
             double4 w = {0, 0, 0, 0};
             if (b >= 0) {
-                const double a = L.A[b];
+                const double a = A[b];
                 const int abc = L.slot_abc[s];
                 w = {a, a * (abc & 0xff), a * ((abc >> 8) & 0xff), a * ((abc >> 16) & 0xff)};
             }
-            reinterpret_cast<double4 *>(L.red)[s] = w;
+            reinterpret_cast<double4 *>(red)[s] = w;
         }
-        __syncthreads();
+        wave_sync();
 
         // ---- forces and virial ---------------------------------------------
         double fi0 = 0, fi1 = 0, fi2 = 0;
@@ -540,29 +551,29 @@ __global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(WPE))) vo
                 atomicAdd(&out.forces[3 * i + 2], fi2);
             }
         }
-        __syncthreads();
+        wave_sync();
     }
-    // block partials: energy, stress[9]
+    // per-wave partials: energy, stress[9]
     e_acc = wave_sum(e_acc);
 #pragma unroll
     for (int k = 0; k < 9; ++k)
         v_acc[k] = wave_sum(v_acc[k]);
     if (lane == 0) {
-        out.partial[10 * blockIdx.x] = e_acc;
+        out.partial[10 * row] = e_acc;
 #pragma unroll
         for (int k = 0; k < 9; ++k)
-            out.partial[10 * blockIdx.x + 1 + k] = v_acc[k];
+            out.partial[10 * row + 1 + k] = v_acc[k];
     }
 }
 
-// Ordered reduction of the per-workgroup partials (one workgroup).
-__global__ __launch_bounds__(256) void partial_reduce_kernel(const double *partial, int nblocks,
+// Ordered reduction of the per-wave partials (one workgroup).
+__global__ __launch_bounds__(256) void partial_reduce_kernel(const double *partial, int nrows,
                                                              double *out10)
 {
     __shared__ double buf[256][10];
     const int t = threadIdx.x;
     double acc[10] = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
-    for (int b = t; b < nblocks; b += 256)
+    for (int b = t; b < nrows; b += 256)
 #pragma unroll
         for (int k = 0; k < 10; ++k)
             acc[k] += partial[10 * b + k];
@@ -620,17 +631,72 @@ bool profile_is(const DevModel &m)
     return true;
 }
 
+// Kernel variants: shell profile x table placement.  The profiles whose
+// kernels fit 256 registers run eight waves per workgroup, the larger ones four.
+template <class P>
+struct VariantWaves {
+    static constexpr int value = 8;
+};
+template <>
+struct VariantWaves<ProfLevel20> {
+    static constexpr int value = 4;
+};
+template <>
+struct VariantWaves<ProfGeneric> {
+    static constexpr int value = 4;
+};
+
+template <class P>
+void launch_variant(const DevModel &m, const DevNeighbors &nb, const EfsOut &out,
+                    const EfsLaunch &cfg, int det, hipStream_t s)
+{
+    constexpr int W = VariantWaves<P>::value;
+    if (cfg.lds_tables)
+        hipLaunchKernelGGL((efs_kernel<P, true, W>), dim3(cfg.grid), dim3(kWave * cfg.waves),
+                           cfg.lds_bytes, s, m, nb, out, det);
+    else
+        hipLaunchKernelGGL((efs_kernel<P, false, W>), dim3(cfg.grid), dim3(kWave * cfg.waves),
+                           cfg.lds_bytes, s, m, nb, out, det);
+}
+
+int variant_max_waves(int v)
+{
+    switch (v) {
+    case 0: return VariantWaves<ProfLevel16>::value;
+    case 1: return VariantWaves<ProfLevel20>::value;
+    case 2: return VariantWaves<ProfLevel10>::value;
+    case 3: return VariantWaves<ProfSmall>::value;
+    default: return VariantWaves<ProfGeneric>::value;
+    }
+}
+
 }  // namespace
 
-size_t efs_lds_bytes(const DevModel &m)
+bool efs_configure(const DevModel &m, int n, int num_cus, int max_waves, size_t lds_limit,
+                   EfsLaunch &cfg)
 {
-    auto r4 = [](size_t v) { return (v + 3) & ~size_t(3); };
-    const size_t ncoef_r = (size_t)m.Z * m.Z * m.M * m.R;
-    const size_t red = std::max<size_t>((size_t)kChunk * kRedStride, 4 * r4((size_t)m.nslots));
-    const size_t dbl = r4(ncoef_r) + 3 * r4((size_t)m.K) + red + r4((size_t)m.S) +
-                       r4((size_t)m.max_partials);
-    const size_t ints = r4((size_t)m.S) + 2 * r4((size_t)m.nslots);
-    return dbl * sizeof(double) + ints * sizeof(int);
+    const size_t kLdsPerCu = lds_limit;
+    const size_t priv = (size_t)m.priv_doubles * sizeof(double);
+    const int vmax = variant_max_waves(efs_variant(m, m.R));
+    const int wcap = max_waves > 0 ? std::min(vmax, max_waves) : vmax;
+    auto fit = [&](bool tables) {
+        const size_t sh = shared_doubles(m, tables) * sizeof(double);
+        if (sh + priv > kLdsPerCu)
+            return 0;
+        return (int)std::min<size_t>(wcap, (kLdsPerCu - sh) / priv);
+    };
+    const int wt = fit(true), wg = fit(false);
+    if (wg == 0)
+        return false;
+    // rule tables in LDS unless that costs more than half the waves
+    cfg.lds_tables = wt > 0 && 2 * wt >= wg;
+    cfg.waves = cfg.lds_tables ? wt : wg;
+    cfg.lds_bytes = shared_doubles(m, cfg.lds_tables) * sizeof(double) + cfg.waves * priv;
+    const int per_cu = std::max<int>(1, (int)(kLdsPerCu / cfg.lds_bytes));
+    const int need = (std::max(n, 1) + cfg.waves - 1) / cfg.waves;
+    cfg.grid = std::max(1, std::min(need, num_cus * per_cu));
+    cfg.rows = cfg.grid * cfg.waves;
+    return true;
 }
 
 // 0: level-16 profile, 1: level-20, 2: level-10, 3: small runtime, 4: generic
@@ -647,51 +713,25 @@ int efs_variant(const DevModel &m, int R)
     return 4;
 }
 
-hipError_t launch_efs(const DevModel &m, const DevNeighbors &nb, const EfsOut &out, int grid,
-                      bool deterministic, hipStream_t s)
+hipError_t launch_efs(const DevModel &m, const DevNeighbors &nb, const EfsOut &out,
+                      const EfsLaunch &cfg, bool deterministic, hipStream_t s)
 {
-    const size_t lds = efs_lds_bytes(m);
     const int det = deterministic ? 1 : 0;
-    // MTPX_EFS_WAVES_PER_EU (tuning): occupancy the level-16 kernel is
-    // register-allocated for (1 = compiler's choice, 3)
-    static const int wpe = [] {
-        const char *e = getenv("MTPX_EFS_WAVES_PER_EU");
-        return e ? atoi(e) : 1;
-    }();
     switch (efs_variant(m, m.R)) {
-    case 0:
-        if (wpe == 3)
-            hipLaunchKernelGGL((efs_kernel<ProfLevel16, 3>), dim3(grid), dim3(kWave), lds, s, m, nb,
-                               out, det);
-        else
-            hipLaunchKernelGGL((efs_kernel<ProfLevel16, 1>), dim3(grid), dim3(kWave), lds, s, m, nb,
-                               out, det);
-        break;
-    case 1:
-        hipLaunchKernelGGL((efs_kernel<ProfLevel20, 1>), dim3(grid), dim3(kWave), lds, s, m, nb,
-                           out, det);
-        break;
-    case 2:
-        hipLaunchKernelGGL((efs_kernel<ProfLevel10, 1>), dim3(grid), dim3(kWave), lds, s, m, nb,
-                           out, det);
-        break;
-    case 3:
-        hipLaunchKernelGGL((efs_kernel<ProfSmall, 1>), dim3(grid), dim3(kWave), lds, s, m, nb, out,
-                           det);
-        break;
-    default:
-        hipLaunchKernelGGL((efs_kernel<ProfGeneric, 1>), dim3(grid), dim3(kWave), lds, s, m, nb,
-                           out, det);
-        break;
+    case 0: launch_variant<ProfLevel16>(m, nb, out, cfg, det, s); break;
+    case 1: launch_variant<ProfLevel20>(m, nb, out, cfg, det, s); break;
+    case 2: launch_variant<ProfLevel10>(m, nb, out, cfg, det, s); break;
+    case 3: launch_variant<ProfSmall>(m, nb, out, cfg, det, s); break;
+    default: launch_variant<ProfGeneric>(m, nb, out, cfg, det, s); break;
     }
     return hipGetLastError();
 }
 
-hipError_t launch_efs_finish(const DevNeighbors &nb, const EfsOut &out, int grid,
+hipError_t launch_efs_finish(const DevNeighbors &nb, const EfsOut &out, int rows,
                              bool deterministic, const int *rev_offsets, const int *rev_pairs,
                              double *energy_stress10, hipStream_t s)
 {
-    hipLaunchKernelGGL(partial_reduce_kernel, dim3(1), dim3(256), 0, s, out.partial, grid,
+    hipLaunchKernelGGL(partial_reduce_kernel, dim3(1), dim3(256), 0, s, out.partial, rows,
                        energy_stress10);
     if (deterministic && nb.n > 0)
         hipLaunchKernelGGL(force_gather_kernel, dim3((nb.n + 255) / 256), dim3(256), 0, s, nb,

@@ -381,44 +381,57 @@ bool build_plan(const Model &m, Plan &p, std::string &err)
         maxl = std::max(maxl, level[x]);
     p.max_level = maxl;
 
-    // Forward: outputs of each level, an output's rules in file order.
-    std::vector<std::vector<int>> by_out((size_t)m.K);
-    for (int t = 0; t < m.T; ++t)
-        by_out[m.times[4 * t + 3]].push_back(t);
-    auto emit_level = [&p](std::vector<std::vector<std::array<int, 4>>> &tasks,
-                           std::vector<int> &level_step, std::vector<int> &steps,
-                           std::vector<int> &level_comb, std::vector<int> &comb) {
+    // Private LDS layout of one wave (in doubles): moments, adjoints, a zero
+    // slot that padding steps read and write, then the partial sums.
+    const int K4 = (m.K + 3) & ~3;
+    p.K4 = K4;
+    p.dummy = 2 * K4;
+    p.part0 = 2 * K4 + 4;
+
+    // A step entry before encoding: {l, r, c, w, first}; w >= 0 is the
+    // task's target (moment or adjoint index), w <= -2 partial -w - 2.
+    using Ent = std::array<int, 5>;
+    using Task = std::vector<Ent>;
+    struct Raw {
+        std::vector<Ent> steps;          // lane-major
+        std::vector<int> level_step;     // per level: first step
+        std::vector<std::array<int, 3>> comb;  // {target, first partial, count}
+        std::vector<int> level_comb;
+    };
+    auto emit_level = [&p](std::vector<Task> &tasks, Raw &raw) {
         size_t total = 0;
         for (auto &t : tasks)
             total += t.size();
         const size_t cap = std::max<size_t>(4, (total + kWave - 1) / kWave);
         // split long tasks into pieces that end in partial sums
-        std::vector<std::vector<std::array<int, 4>>> pieces;
+        std::vector<Task> pieces;
         int npart = 0;
         for (auto &t : tasks) {
             if (t.size() <= cap) {
                 pieces.push_back(t);
                 continue;
             }
-            const int target = t.back()[3];
+            const int target = t[0][3];
             const int first = npart;
             for (size_t b0 = 0; b0 < t.size(); b0 += cap) {
-                std::vector<std::array<int, 4>> piece(t.begin() + b0,
-                                                      t.begin() + std::min(t.size(), b0 + cap));
-                piece.back()[3] = -2 - npart++;
+                Task piece(t.begin() + b0, t.begin() + std::min(t.size(), b0 + cap));
+                for (Ent &e : piece)
+                    e[3] = -2 - npart;
+                piece[0][4] = 1;
+                ++npart;
                 pieces.push_back(std::move(piece));
             }
-            comb.insert(comb.end(), {target, first, npart - first, 0});
+            raw.comb.push_back({target, first, npart - first});
         }
         p.max_partials = std::max(p.max_partials, npart);
-        level_comb.push_back((int)comb.size() / 4);
+        raw.level_comb.push_back((int)raw.comb.size());
         // longest-processing-time assignment of pieces to the 64 lanes
         std::vector<int> order(pieces.size());
         for (size_t i = 0; i < order.size(); ++i)
             order[i] = (int)i;
         std::stable_sort(order.begin(), order.end(),
                          [&](int a, int b) { return pieces[a].size() > pieces[b].size(); });
-        std::vector<std::vector<std::array<int, 4>>> lane(kWave);
+        std::vector<Task> lane(kWave);
         std::vector<size_t> load(kWave, 0);
         for (int t : order) {
             int q = (int)(std::min_element(load.begin(), load.end()) - load.begin());
@@ -427,57 +440,101 @@ bool build_plan(const Model &m, Plan &p, std::string &err)
         }
         size_t nst = *std::max_element(load.begin(), load.end());
         nst = (nst + 3) & ~size_t(3);
-        const size_t base = steps.size() / 4 / kWave;
-        steps.resize((base + nst) * kWave * 4, 0);
+        const size_t base = raw.steps.size() / kWave;
+        raw.steps.resize((base + nst) * kWave, Ent{-1, -1, 0, -1, 1});  // padding
         for (int q = 0; q < kWave; ++q)
-            for (size_t st = 0; st < nst; ++st) {
-                std::array<int, 4> e = st < lane[q].size() ? lane[q][st]
-                                                           : std::array<int, 4>{0, 0, 0, -1};
-                for (int c = 0; c < 4; ++c)
-                    steps[((base + st) * kWave + q) * 4 + c] = e[c];
-            }
-        level_step.push_back((int)(base + nst));
+            for (size_t st = 0; st < lane[q].size(); ++st)
+                raw.steps[(base + st) * kWave + q] = lane[q][st];
+        raw.level_step.push_back((int)(base + nst));
     };
-    p.fwd_level_comb.push_back(0);
-    p.bwd_level_comb.push_back(0);
-    p.fwd_level_step.push_back(0);
+
+    // Forward: outputs of each level, an output's rules in file order.
+    std::vector<std::vector<int>> by_out((size_t)m.K);
+    for (int t = 0; t < m.T; ++t)
+        by_out[m.times[4 * t + 3]].push_back(t);
+    Raw fwd, bwd;
+    fwd.level_step.push_back(0);
+    fwd.level_comb.push_back(0);
     for (int L = 1; L <= maxl; ++L) {
-        std::vector<std::vector<std::array<int, 4>>> tasks;
+        std::vector<Task> tasks;
         for (int o = 0; o < m.K; ++o) {
             if (level[o] != L || by_out[o].empty())
                 continue;
-            std::vector<std::array<int, 4>> task;
+            Task task;
             for (int t : by_out[o]) {
                 const int *r = &m.times[4 * t];
-                task.push_back({r[0], r[1], r[2], -1});
+                task.push_back({r[0], r[1], r[2], o, 0});
             }
-            task.back()[3] = o;
+            task[0][4] = 1;
             tasks.push_back(std::move(task));
         }
-        emit_level(tasks, p.fwd_level_step, p.fwd_steps, p.fwd_level_comb, p.fwd_comb);
+        emit_level(tasks, fwd);
     }
 
     // Reverse: destinations of each level from the top down; a destination's
     // entries in reverse file order, the right operand's entry of a rule
-    // first (backpropagate_moments, potential_mtp.cpp:3292-3305).
-    std::vector<std::vector<std::array<int, 4>>> ent((size_t)m.K);
+    // first (backpropagate_moments, potential_mtp.cpp:3292-3305).  Entry
+    // {o, other, c}: A_x += c A_o m_other.
+    std::vector<Task> ent((size_t)m.K);
     for (int t = m.T - 1; t >= 0; --t) {
         const int *r = &m.times[4 * t];
-        ent[r[1]].push_back({r[3], r[0], r[2], -1});
-        ent[r[0]].push_back({r[3], r[1], r[2], -1});
+        ent[r[1]].push_back({r[3], r[0], r[2], r[1], 0});
+        ent[r[0]].push_back({r[3], r[1], r[2], r[0], 0});
     }
-    p.bwd_level_step.push_back(0);
+    bwd.level_step.push_back(0);
+    bwd.level_comb.push_back(0);
     for (int L = maxl - 1; L >= 0; --L) {
-        std::vector<std::vector<std::array<int, 4>>> tasks;
+        std::vector<Task> tasks;
         for (int x = 0; x < m.K; ++x) {
             if (level[x] != L || ent[x].empty())
                 continue;
-            std::vector<std::array<int, 4>> task = ent[x];
-            task.back()[3] = x;
+            Task task = ent[x];
+            task[0][4] = 1;
             tasks.push_back(std::move(task));
         }
-        emit_level(tasks, p.bwd_level_step, p.bwd_steps, p.bwd_level_comb, p.bwd_comb);
+        emit_level(tasks, bwd);
     }
+
+    // Encode against the private layout (indices in doubles).
+    const int P4 = (p.max_partials + 3) & ~3;
+    p.red0 = p.part0 + P4;
+    const int N4 = (p.nslots + 3) & ~3;
+    p.priv_doubles = p.red0 + std::max(kChunk * kRedStride, 4 * N4);
+    if (p.priv_doubles > 0xffff)
+        return fail(err, "model too large: per-atom work space exceeds 65535 doubles");
+    for (int t = 0; t < m.T; ++t)
+        if (m.times[4 * t + 2] < -16384 || m.times[4 * t + 2] > 16383)
+            return fail(err, "product-rule multiplicity outside [-16384, 16383]");
+    auto encode = [&p](const Raw &raw, bool reverse, std::vector<int> &steps,
+                       std::vector<int> &level_step, std::vector<int> &comb,
+                       std::vector<int> &level_comb) {
+        auto target = [&](int w) {
+            if (w <= -2)
+                return p.part0 + (-w - 2);
+            return reverse ? p.K4 + w : w;
+        };
+        steps.assign(raw.steps.size() * 2, 0);
+        for (size_t i = 0; i < raw.steps.size(); ++i) {
+            const Ent &e = raw.steps[i];
+            int l, r, w;
+            if (e[0] < 0) {
+                l = r = w = p.dummy;
+            } else {
+                l = reverse ? p.K4 + e[0] : e[0];
+                r = e[1];
+                w = target(e[3]);
+            }
+            steps[2 * i] = l | (r << 16);
+            steps[2 * i + 1] = w | (e[4] << 16) | (int)((unsigned)e[2] << 17);
+        }
+        level_step = raw.level_step;
+        level_comb = raw.level_comb;
+        comb.clear();
+        for (auto &c : raw.comb)
+            comb.insert(comb.end(), {target(c[0]), p.part0 + c[1], c[2], 0});
+    };
+    encode(fwd, false, p.fwd_steps, p.fwd_level_step, p.fwd_comb, p.fwd_level_comb);
+    encode(bwd, true, p.bwd_steps, p.bwd_level_step, p.bwd_comb, p.bwd_level_comb);
     return true;
 }
 

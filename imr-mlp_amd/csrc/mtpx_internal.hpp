@@ -98,18 +98,24 @@ struct Plan {
     std::vector<int> slot_basic;   // [nslots] basic index or -1 (padding)
     std::vector<int> slot_abc;     // [nslots] a | b << 8 | c << 16
     std::vector<int> dup;          // [ndup][2] {duplicate basic, source basic}
+    // Each wave owns a private LDS work space (indices in doubles):
+    //   [0, K4) moments | [K4, 2 K4) adjoints | dummy (a zero slot) |
+    //   [part0, red0) partial sums | [red0, priv_doubles) transpose buffer.
+    int K4 = 0, dummy = 0, part0 = 0, red0 = 0, priv_doubles = 0;
     // Lane-major step tables, one per direction.  Level L owns steps
     // [level_step[L], level_step[L+1]) (a multiple of 4); step s of lane q is
-    // entry s * 64 + q, an int4:
-    //   forward {l, r, c, w}:      acc += c m_l m_r
-    //   reverse {o, other, c, w}:  acc += c A_o m_other
-    // w == -1 continues; w >= 0 finalises the task (forward m_w = acc,
-    // reverse A_w += acc); w <= -2 stores acc in partial[-w - 2].  A task
-    // longer than the level's fair share (entries / 64) is split into
-    // pieces whose partial sums the level's combine list adds in order:
-    // combine entry {target, first partial, count, 0}.  Tasks and pieces
-    // are spread over the lanes by longest-processing-time assignment;
-    // padding steps have c = 0.
+    // entry s * 64 + q, an int2 of work-space indices:
+    //   x = l | r << 16,  y = w | first << 16 | c << 17  (c signed)
+    //   acc = c * ws[l] * ws[r] + (first ? ws[w] : acc);  ws[w] = acc
+    // Forward entries read two moments and write a rule output; reverse
+    // entries read an adjoint and a moment and write an adjoint (whose
+    // initial value is its seed).  A task (all rules of one output, or all
+    // reverse entries of one destination) longer than the level's fair share
+    // (entries / 64) is split into pieces that write zeroed partial sums; the
+    // level's combine list {target, first partial, count, 0} then adds them
+    // in order to the target and clears them.  Padding steps have c = 0 and
+    // read and write the dummy slot.  Tasks and pieces are spread over the
+    // lanes by longest-processing-time assignment.
     std::vector<int> fwd_level_step, fwd_steps, fwd_level_comb, fwd_comb;
     std::vector<int> bwd_level_step, bwd_steps, bwd_level_comb, bwd_comb;
     int max_partials = 0;
@@ -134,12 +140,14 @@ struct DevModel {
     const int *slot_abc;    // [nslots] a | b << 8 | c << 16
     const int *dup;         // [ndup][2]
     int max_partials;
+    int K4, dummy, part0, red0, priv_doubles;  // per-wave work space (Plan)
+    int fwd_nsteps, bwd_nsteps;                 // steps per lane, all levels
     const int *fwd_level_step;  // [nfwd+1]
-    const int4 *fwd_steps;
+    const int2 *fwd_steps;
     const int *fwd_level_comb;  // [nfwd+1]
     const int4 *fwd_comb;
     const int *bwd_level_step;  // [nbwd+1]
-    const int4 *bwd_steps;
+    const int2 *bwd_steps;
     const int *bwd_level_comb;  // [nbwd+1]
     const int4 *bwd_comb;
 };
@@ -158,16 +166,27 @@ struct DevNeighbors {
 struct EfsOut {
     double *forces;         // [n][3] (zeroed by the caller)
     double *site_energy;    // [n]
-    double *partial;        // [gridDim.x][10]: energy, stress[9]
+    double *partial;        // [rows][10] per wave: energy, stress[9]
     double *pair_ders;      // [P][3] (deterministic mode) or nullptr
 };
 
-// Kernel launchers (efs_kernel.hip).
-size_t efs_lds_bytes(const DevModel &m);
+// Launch shape of the E/F/S kernel (efs_kernel.hip).
+struct EfsLaunch {
+    bool lds_tables;   // product-rule step tables staged in LDS
+    int waves;         // waves per workgroup
+    int grid;          // workgroups
+    int rows;          // per-wave partial rows (grid * waves)
+    size_t lds_bytes;  // dynamic LDS per workgroup
+};
+// Chooses the launch shape; false if one wave's work space does not fit the
+// LDS a workgroup may allocate (lds_limit bytes, which one CU also holds).
+// max_waves > 0 caps the waves per workgroup.
+bool efs_configure(const DevModel &m, int n, int num_cus, int max_waves, size_t lds_limit,
+                   EfsLaunch &cfg);
 int efs_variant(const DevModel &m, int R);
-hipError_t launch_efs(const DevModel &m, const DevNeighbors &nb, const EfsOut &out, int grid,
-                      bool deterministic, hipStream_t s);
-hipError_t launch_efs_finish(const DevNeighbors &nb, const EfsOut &out, int grid,
+hipError_t launch_efs(const DevModel &m, const DevNeighbors &nb, const EfsOut &out,
+                      const EfsLaunch &cfg, bool deterministic, hipStream_t s);
+hipError_t launch_efs_finish(const DevNeighbors &nb, const EfsOut &out, int rows,
                              bool deterministic, const int *rev_offsets, const int *rev_pairs,
                              double *energy_stress10, hipStream_t s);
 
