@@ -29,10 +29,12 @@ COMMON = ["-O3", "-std=c++17", "-fPIC", "--offload-arch=" + ARCH, "-munsafe-fp-a
 
 SOURCES = [
     ("efs_kernel.hip", ["-ffp-contract=fast"]),
+    ("train_kernel.hip", ["-ffp-contract=fast"]),
     ("neighbors.hip", ["-ffp-contract=off"]),
     ("geometry.cpp", ["-ffp-contract=off"]),
     ("model.cpp", ["-ffp-contract=off"]),
     ("capi.cpp", ["-ffp-contract=off"]),
+    ("train_api.cpp", ["-ffp-contract=off"]),
 ]
 
 
@@ -43,15 +45,21 @@ def sources():
 def build(verbose: bool = False) -> str:
     os.makedirs(LIB_DIR, exist_ok=True)
     os.makedirs(OBJ_DIR, exist_ok=True)
-    objs = []
+    objs, cmds = [], []
     t0 = time.time()
     for src, flags in sources():
         obj = os.path.join(OBJ_DIR, src + ".o")
-        cmd = [HIPCC, "-x", "hip", "-c", os.path.join(CSRC, src), "-o", obj] + COMMON + flags
+        cmds.append([HIPCC, "-x", "hip", "-c", os.path.join(CSRC, src), "-o", obj] + COMMON + flags)
+        objs.append(obj)
+    # translation units compile in parallel (the kernel files dominate)
+    procs = []
+    for cmd in cmds:
         if verbose:
             print(" ".join(cmd), flush=True)
-        subprocess.run(cmd, check=True)
-        objs.append(obj)
+        procs.append(subprocess.Popen(cmd))
+    failed = [c for c, p in zip(cmds, procs) if p.wait() != 0]
+    if failed:
+        raise subprocess.CalledProcessError(1, failed[0])
     tmp = LIB + ".tmp"
     cmd = [HIPCC, "-shared", "-fPIC", "--offload-arch=" + ARCH, "-o", tmp] + objs
     if verbose:

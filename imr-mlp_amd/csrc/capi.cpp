@@ -1,94 +1,13 @@
 // C ABI (include/mtpx.h): context, device-resident model and neighbour lists,
 // E/F/S launches.  Host code; no exceptions escape.
-#include "mtpx.h"
-#include "mtpx_internal.hpp"
+#include "context.hpp"
 
 #include <algorithm>
 #include <cmath>
 #include <cstring>
 #include <new>
 
-using namespace mtpx;
-
-struct mtpx_context {
-    int device = 0;
-    hipStream_t stream = nullptr;
-    std::string err;
-    int num_cus = 256;
-    size_t lds_limit = 160 * 1024;  // LDS one workgroup may allocate
-
-    bool has_model = false;
-    Model model;
-    Plan plan;
-    DevModel dm{};
-    // model buffers
-    DBuf radial, species, moment, map, seed, slot_basic, slot_abc, dup, fwd_level, fwd_steps,
-        fwd_lcomb, fwd_comb, bwd_level, bwd_steps, bwd_lcomb, bwd_comb;
-
-    // neighbour lists
-    bool has_nbh = false;
-    NeighborStore nbh;
-    NeighborScratch scratch;
-    int &n = nbh.n;
-    int64_t &P = nbh.P;
-    DBuf &offsets = nbh.offsets, &idx = nbh.idx, &type = nbh.type, &x = nbh.x, &y = nbh.y,
-         &z = nbh.z, &d = nbh.d, &center_type = nbh.center_type;
-    DBuf rev_offsets, rev_pairs;
-    bool rev_ready = false;
-
-    // outputs
-    DBuf forces, site_energy, partial, pair_ders, out10;
-    EfsLaunch launch{};
-
-    hipEvent_t ev[3] = {nullptr, nullptr, nullptr};
-    double timings[4] = {0, 0, 0, 0};
-
-    ~mtpx_context()
-    {
-        for (DBuf *b : {&radial, &species, &moment, &map, &seed, &slot_basic, &slot_abc, &dup,
-                        &fwd_level, &fwd_steps, &fwd_lcomb, &fwd_comb, &bwd_level, &bwd_steps,
-                        &bwd_lcomb, &bwd_comb, &offsets, &idx, &type, &x, &y, &z, &d, &center_type, &rev_offsets,
-                        &rev_pairs, &forces, &site_energy, &partial, &pair_ders, &out10})
-            b->release();
-        scratch.release_all();
-        for (auto &e : ev)
-            if (e)
-                (void)hipEventDestroy(e);
-        if (stream)
-            (void)hipStreamDestroy(stream);
-    }
-};
-
 namespace {
-
-int set_error(mtpx_context *ctx, int code, const std::string &msg)
-{
-    if (ctx)
-        ctx->err = msg;
-    return code;
-}
-
-int hip_fail(mtpx_context *ctx, hipError_t e, const char *what)
-{
-    return set_error(ctx, e == hipErrorOutOfMemory ? MTPX_E_ALLOC : MTPX_E_DEVICE,
-                     std::string(what) + ": " + hipGetErrorString(e));
-}
-
-#define HIP_TRY(expr, what)                                                                \
-    do {                                                                                   \
-        hipError_t e_ = (expr);                                                            \
-        if (e_ != hipSuccess)                                                              \
-            return hip_fail(ctx, e_, what);                                                \
-    } while (0)
-
-template <class T>
-hipError_t upload(DBuf &b, const std::vector<T> &v, hipStream_t s)
-{
-    hipError_t e = b.ensure(sizeof(T) * std::max<size_t>(v.size(), 1));
-    if (e != hipSuccess || v.empty())
-        return e;
-    return hipMemcpyAsync(b.p, v.data(), sizeof(T) * v.size(), hipMemcpyHostToDevice, s);
-}
 
 // Upload coefficient-dependent arrays: radial, species, moment coefficients
 // and the adjoint seeds (sum of the moment coefficients mapped to a moment,
@@ -124,6 +43,8 @@ int install_model(mtpx_context *ctx, Model &&m)
         return set_error(ctx, MTPX_E_MODEL, err);
     ctx->model = std::move(m);
     ctx->plan = std::move(p);
+    ctx->has_batch_out = false;
+    ctx->has_adjoints = false;
     const Model &M = ctx->model;
     const Plan &P = ctx->plan;
     DevModel &dm = ctx->dm;
@@ -180,6 +101,15 @@ int install_model(mtpx_context *ctx, Model &&m)
     dm.part0 = P.part0;
     dm.red0 = P.red0;
     dm.priv_doubles = P.priv_doubles;
+    dm.tr_delta = P.tr_delta;
+    dm.tr_red = P.tr_red;
+    dm.tr_stage = P.tr_stage;
+    dm.tr_grad = P.tr_grad;
+    dm.tr_ctype = P.tr_ctype;
+    dm.tr_priv = P.tr_priv;
+    dm.nradial = M.nradial();
+    dm.ncoef = M.ncoef();
+    std::memcpy(dm.slot_base, P.slot_base, sizeof dm.slot_base);
     dm.fwd_nsteps = P.fwd_level_step.back();
     dm.bwd_nsteps = P.bwd_level_step.back();
     EfsLaunch probe;
@@ -191,6 +121,10 @@ int install_model(mtpx_context *ctx, Model &&m)
     ctx->has_model = true;
     return MTPX_OK;
 }
+
+}  // namespace
+
+namespace mtpx {
 
 DevNeighbors dev_neighbors(const mtpx_context *ctx)
 {
@@ -207,6 +141,8 @@ DevNeighbors dev_neighbors(const mtpx_context *ctx)
     nb.center_type = ctx->center_type.as<int>();
     return nb;
 }
+
+namespace {
 
 // Ordered reverse index: for each atom k, the pairs p with idx[p] == k, in
 // ascending p (used by the deterministic force gather).
@@ -227,12 +163,42 @@ int build_reverse_index(mtpx_context *ctx, const int *idx_host)
     return MTPX_OK;
 }
 
-int run_efs(mtpx_context *ctx, bool deterministic)
+}  // namespace
+
+int set_single_structure(mtpx_context *ctx)
+{
+    ctx->nconf = 1;
+    ctx->soff_host = {0, ctx->n};
+    ctx->has_batch_out = false;
+    ctx->has_adjoints = false;
+    ctx->has_labels = false;
+    HIP_TRY(upload(ctx->soff, ctx->soff_host, ctx->stream), "upload structure offsets");
+    HIP_TRY(ctx->center_structure.ensure(sizeof(int) * std::max(ctx->n, 1)),
+            "allocate structure index");
+    HIP_TRY(hipMemsetAsync(ctx->center_structure.p, 0, sizeof(int) * std::max(ctx->n, 1),
+                           ctx->stream),
+            "clear structure index");
+    HIP_TRY(hipStreamSynchronize(ctx->stream), "upload structure offsets");
+    return MTPX_OK;
+}
+
+int check_species(mtpx_context *ctx)
+{
+    if (ctx->max_species >= ctx->model.Z)
+        return set_error(ctx, MTPX_E_INVALID,
+                         "neighbour lists hold species " + std::to_string(ctx->max_species) +
+                             " but the model has " + std::to_string(ctx->model.Z));
+    return MTPX_OK;
+}
+
+int run_efs(mtpx_context *ctx, bool deterministic, bool site_virial)
 {
     if (!ctx->has_model)
         return set_error(ctx, MTPX_E_NO_MODEL, "no model loaded");
     if (!ctx->has_nbh)
         return set_error(ctx, MTPX_E_NO_TOPOLOGY, "no neighbour lists");
+    if (int rc = check_species(ctx))
+        return rc;
     if (deterministic && !ctx->rev_ready) {
         std::vector<int> idx_host((size_t)std::max<int64_t>(ctx->P, 1));
         if (ctx->P > 0)
@@ -266,6 +232,12 @@ int run_efs(mtpx_context *ctx, bool deterministic)
     out.site_energy = ctx->site_energy.as<double>();
     out.partial = ctx->partial.as<double>();
     out.pair_ders = deterministic ? ctx->pair_ders.as<double>() : nullptr;
+    out.site_virial = nullptr;
+    if (site_virial) {
+        HIP_TRY(ctx->site_virial.ensure(sizeof(double) * 9 * std::max(n, 1)),
+                "allocate site virials");
+        out.site_virial = ctx->site_virial.as<double>();
+    }
     DevNeighbors nb = dev_neighbors(ctx);
     if (!deterministic && n > 0)
         HIP_TRY(hipMemsetAsync(out.forces, 0, sizeof(double) * 3 * n, s), "clear forces");
@@ -292,7 +264,7 @@ int run_efs(mtpx_context *ctx, bool deterministic)
     return MTPX_OK;
 }
 
-}  // namespace
+}  // namespace mtpx
 
 extern "C" {
 
@@ -443,6 +415,8 @@ int mtpx_set_coeffs(mtpx_context *ctx, const double *coeffs)
         return set_error(ctx, MTPX_E_NO_MODEL, "no model loaded");
     std::memcpy(ctx->model.coef.data(), coeffs, sizeof(double) * ctx->model.coef.size());
     (void)hipSetDevice(ctx->device);
+    ctx->has_batch_out = false;
+    ctx->has_adjoints = false;
     return upload_coeffs(ctx);
 }
 
@@ -469,9 +443,14 @@ int mtpx_set_neighbors(mtpx_context *ctx, int n, const int *offsets, const int *
         if (types[p] < 0 || types[p] >= Z)
             return set_error(ctx, MTPX_E_INVALID, "neighbour species out of range");
     }
-    for (int i = 0; i < n; ++i)
+    int maxs = -1;
+    for (int i = 0; i < n; ++i) {
         if (center_types[i] < 0 || center_types[i] >= Z)
             return set_error(ctx, MTPX_E_INVALID, "centre species out of range");
+        maxs = std::max(maxs, center_types[i]);
+    }
+    for (int64_t p = 0; p < P; ++p)
+        maxs = std::max(maxs, types[p]);
     (void)hipSetDevice(ctx->device);
     ctx->has_nbh = false;
     ctx->rev_ready = false;
@@ -494,8 +473,9 @@ int mtpx_set_neighbors(mtpx_context *ctx, int n, const int *offsets, const int *
     HIP_TRY(hipStreamSynchronize(s), "upload lists");
     ctx->n = n;
     ctx->P = P;
+    ctx->max_species = maxs;
     ctx->has_nbh = true;
-    return MTPX_OK;
+    return set_single_structure(ctx);
 }
 
 int mtpx_build_neighbors(mtpx_context *ctx, const double cell[9], const int pbc[3], int n,
@@ -513,9 +493,12 @@ int mtpx_build_neighbors(mtpx_context *ctx, const double cell[9], const int pbc[
         if (!std::isfinite(pos[i]))
             return set_error(ctx, MTPX_E_INVALID, "non-finite position");
     const int Z = ctx->has_model ? ctx->model.Z : 1 << 30;
-    for (int i = 0; i < n; ++i)
+    int maxs = -1;
+    for (int i = 0; i < n; ++i) {
         if (types[i] < 0 || types[i] >= Z)
             return set_error(ctx, MTPX_E_INVALID, "species out of range");
+        maxs = std::max(maxs, types[i]);
+    }
     (void)hipSetDevice(ctx->device);
     ctx->has_nbh = false;
     ctx->rev_ready = false;
@@ -524,8 +507,9 @@ int mtpx_build_neighbors(mtpx_context *ctx, const double cell[9], const int pbc[
                                  ctx->scratch, err);
     if (rc != MTPX_OK)
         return set_error(ctx, rc, err);
+    ctx->max_species = maxs;
     ctx->has_nbh = true;
-    return MTPX_OK;
+    return set_single_structure(ctx);
 }
 
 int mtpx_neighbor_count(const mtpx_context *ctx, int64_t *entries, int *centers)

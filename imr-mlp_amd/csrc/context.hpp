@@ -1,0 +1,127 @@
+// The C-ABI context (include/mtpx.h) and helpers shared by the host files.
+#pragma once
+
+#include "mtpx.h"
+#include "mtpx_internal.hpp"
+
+#include <string>
+#include <vector>
+
+using namespace mtpx;
+
+struct mtpx_context {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    std::string err;
+    int num_cus = 256;
+    size_t lds_limit = 160 * 1024;  // LDS one workgroup may allocate
+
+    bool has_model = false;
+    Model model;
+    Plan plan;
+    DevModel dm{};
+    // model buffers
+    DBuf radial, species, moment, map, seed, slot_basic, slot_abc, dup, fwd_level, fwd_steps,
+        fwd_lcomb, fwd_comb, bwd_level, bwd_steps, bwd_lcomb, bwd_comb;
+
+    // neighbour lists
+    bool has_nbh = false;
+    NeighborStore nbh;
+    NeighborScratch scratch;
+    int &n = nbh.n;
+    int64_t &P = nbh.P;
+    DBuf &offsets = nbh.offsets, &idx = nbh.idx, &type = nbh.type, &x = nbh.x, &y = nbh.y,
+         &z = nbh.z, &d = nbh.d, &center_type = nbh.center_type;
+    DBuf rev_offsets, rev_pairs;
+    bool rev_ready = false;
+    int max_species = -1;  // largest species index in the lists
+
+    // structures of the resident topology (one unless a batch is set)
+    int nconf = 0;
+    std::vector<int> soff_host;          // [nconf+1] first atom of each structure
+    DBuf soff, center_structure;         // device copies; [N] structure of each atom
+
+    // outputs
+    DBuf forces, site_energy, partial, pair_ders, out10;
+    DBuf site_virial, benergy, bstress;  // batch: [N][9], [nconf], [nconf][9]
+    EfsLaunch launch{};
+    bool has_batch_out = false;          // compute_batch outputs match model and topology
+
+    // training: labels, adjoints, gradient rows
+    bool has_labels = false, has_adjoints = false;
+    DBuf active, tE, wE, tF, wF, tS, wS;
+    DBuf dLdE, dLdF, dLdS, metric_rows, metrics, grad_rows, grad;
+    NeighborStore nbh_tmp;
+    double train_timings[4] = {0, 0, 0, 0};
+    hipEvent_t tev[4] = {nullptr, nullptr, nullptr, nullptr};
+
+    hipEvent_t ev[3] = {nullptr, nullptr, nullptr};
+    double timings[4] = {0, 0, 0, 0};
+
+    ~mtpx_context()
+    {
+        for (DBuf *b : {&radial, &species, &moment, &map, &seed, &slot_basic, &slot_abc, &dup,
+                        &fwd_level, &fwd_steps, &fwd_lcomb, &fwd_comb, &bwd_level, &bwd_steps,
+                        &bwd_lcomb, &bwd_comb, &offsets, &idx, &type, &x, &y, &z, &d,
+                        &center_type, &rev_offsets, &rev_pairs, &forces, &site_energy, &partial,
+                        &pair_ders, &out10, &soff, &center_structure, &site_virial, &benergy,
+                        &bstress, &active, &tE, &wE, &tF, &wF, &tS, &wS, &dLdE, &dLdF, &dLdS,
+                        &metric_rows, &metrics, &grad_rows, &grad, &nbh_tmp.offsets,
+                        &nbh_tmp.idx, &nbh_tmp.type, &nbh_tmp.x, &nbh_tmp.y, &nbh_tmp.z,
+                        &nbh_tmp.d, &nbh_tmp.center_type})
+            b->release();
+        scratch.release_all();
+        for (auto &e : ev)
+            if (e)
+                (void)hipEventDestroy(e);
+        for (auto &e : tev)
+            if (e)
+                (void)hipEventDestroy(e);
+        if (stream)
+            (void)hipStreamDestroy(stream);
+    }
+};
+
+namespace mtpx {
+
+
+inline int set_error(mtpx_context *ctx, int code, const std::string &msg)
+{
+    if (ctx)
+        ctx->err = msg;
+    return code;
+}
+
+inline int hip_fail(mtpx_context *ctx, hipError_t e, const char *what)
+{
+    return set_error(ctx, e == hipErrorOutOfMemory ? MTPX_E_ALLOC : MTPX_E_DEVICE,
+                     std::string(what) + ": " + hipGetErrorString(e));
+}
+
+#define HIP_TRY(expr, what)                                                                \
+    do {                                                                                   \
+        hipError_t e_ = (expr);                                                            \
+        if (e_ != hipSuccess)                                                              \
+            return hip_fail(ctx, e_, what);                                                \
+    } while (0)
+
+template <class T>
+hipError_t upload(DBuf &b, const std::vector<T> &v, hipStream_t s)
+{
+    hipError_t e = b.ensure(sizeof(T) * std::max<size_t>(v.size(), 1));
+    if (e != hipSuccess || v.empty())
+        return e;
+    return hipMemcpyAsync(b.p, v.data(), sizeof(T) * v.size(), hipMemcpyHostToDevice, s);
+}
+
+// Runs the E/F/S kernel over the resident topology (capi.cpp); with
+// site_virial the per-atom virials are written too.
+int run_efs(mtpx_context *ctx, bool deterministic, bool site_virial = false);
+// Marks the topology as one structure of all atoms.
+int set_single_structure(mtpx_context *ctx);
+// MTPX_E_INVALID when the lists hold a species the model does not have.
+int check_species(mtpx_context *ctx);
+// Device view of the resident lists.
+DevNeighbors dev_neighbors(const mtpx_context *ctx);
+
+}  // namespace mtpx

@@ -31,378 +31,13 @@
 // highest angular degree of its basic moments.  The level-10/16/20 template
 // profiles are compile-time constants (every (nu, mu) guard folds away); the
 // generic variants read the profile at run time.
-#include "mtpx_internal.hpp"
+#include "mtp_device.hpp"
 
 #include <algorithm>
 
 namespace mtpx {
 
 namespace {
-
-constexpr int shell_size(int nu) { return (nu + 1) * (nu + 2) / 2; }
-
-// Position of (a, b, c = nu-a-b) in the shell enumeration a = nu..0, b = nu-a..0.
-constexpr int shell_index(int nu, int a, int b)
-{
-    int pos = 0;
-    for (int ap = nu; ap > a; --ap)
-        pos += nu - ap + 1;
-    return pos + (nu - a - b);
-}
-
-// ---- shell profiles ---------------------------------------------------
-template <int MM, int NN, int RR, int... NM>
-struct ExactProfile {
-    static constexpr bool exact = true;
-    static constexpr int M = MM, NUMAX = NN, RMAX = RR;
-    static constexpr int nm[MM] = {NM...};
-    static __device__ __forceinline__ bool active(const DevModel &, int mu, int nu)
-    {
-        return nm[mu] >= nu;
-    }
-    static __device__ __forceinline__ bool deeper(const DevModel &, int nu) { return nu < NN; }
-};
-template <int MM, int NN, int RR>
-struct RuntimeProfile {
-    static constexpr bool exact = false;
-    static constexpr int M = MM, NUMAX = NN, RMAX = RR;
-    static __device__ __forceinline__ bool active(const DevModel &m, int mu, int nu)
-    {
-        return mu < m.M && m.numax[mu] >= nu;
-    }
-    static __device__ __forceinline__ bool deeper(const DevModel &m, int nu)
-    {
-        return nu < m.numax_all;
-    }
-};
-using ProfLevel10 = ExactProfile<3, 3, 8, 3, 1, 0>;
-using ProfLevel16 = ExactProfile<4, 6, 8, 6, 4, 2, 0>;
-using ProfLevel20 = ExactProfile<5, 8, 10, 8, 6, 4, 2, 0>;
-using ProfSmall = RuntimeProfile<4, 6, 8>;
-using ProfGeneric = RuntimeProfile<kMaxMu, kMaxNu, kMaxR>;
-
-// v[l] + v[l ^ 32] and v[l] + v[l ^ 16] with the gfx950 lane swaps (VALU, no
-// LDS crossbar): permlane32_swap exchanges the wave halves, permlane16_swap
-// the odd and even rows of 16 lanes.
-__device__ __forceinline__ double xor32_sum(double v)
-{
-    const unsigned lo = __double2loint(v), hi = __double2hiint(v);
-    const auto l = __builtin_amdgcn_permlane32_swap(lo, lo, false, false);
-    const auto h = __builtin_amdgcn_permlane32_swap(hi, hi, false, false);
-    return __hiloint2double(h[0], l[0]) + __hiloint2double(h[1], l[1]);
-}
-__device__ __forceinline__ double xor16_sum(double v)
-{
-    const unsigned lo = __double2loint(v), hi = __double2hiint(v);
-    const auto l = __builtin_amdgcn_permlane16_swap(lo, lo, false, false);
-    const auto h = __builtin_amdgcn_permlane16_swap(hi, hi, false, false);
-    return __hiloint2double(h[0], l[0]) + __hiloint2double(h[1], l[1]);
-}
-
-__device__ __forceinline__ double wave_sum(double v)
-{
-    v = xor32_sum(v);
-    v = xor16_sum(v);
-#pragma unroll
-    for (int off = 8; off >= 1; off >>= 1)
-        v += __shfl_xor(v, off, kWave);
-    return v;
-}
-
-// Orders the LDS accesses of one wave: a wave's LDS operations complete in
-// issue order, so a compiler-level fence at wavefront scope is all that is
-// needed between a lane's store and another lane's load.
-__device__ __forceinline__ void wave_sync()
-{
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
-
-template <int MMAX>
-struct Nbr {
-    double x, y, z, d, invd, ux, uy, uz;
-    double f[MMAX], fd[MMAX];
-};
-
-// Neighbour data of list entry p; lanes without an entry keep zeros, so
-// they contribute nothing to the sums below.
-template <class P>
-__device__ __forceinline__ void load_neighbor(const DevModel &m, const DevNeighbors &nb,
-                                              const double *coef_lds, int ti, int64_t p,
-                                              bool valid, Nbr<P::M> &q)
-{
-    constexpr int RMAX = P::RMAX;
-    q.x = valid ? nb.x[p] : 0.0;
-    q.y = valid ? nb.y[p] : 0.0;
-    q.z = valid ? nb.z[p] : 0.0;
-    const double dd = valid ? nb.d[p] : m.rmax;
-    const int tj = valid ? nb.type[p] : 0;
-    // potential_mtp.cpp:2842 -- entries beyond the cutoff are skipped, r == cutoff kept
-    const bool in_cutoff = valid && !(dd > m.rmax);
-    const double d = in_cutoff ? dd : m.rmax;
-    q.d = d;
-    q.invd = 1.0 / d;
-    q.ux = q.x * q.invd;
-    q.uy = q.y * q.invd;
-    q.uz = q.z * q.invd;
-    // RBasis_Chebyshev::calc_der (basis/basis.cpp:148-164)
-    double Q[RMAX], dQ[RMAX];
-    const double ksi = (2 * d - m.pu) / m.su;
-    const double ru = d - m.rmax;
-    Q[0] = m.scaling * (ru * ru);
-    dQ[0] = m.scaling * (2 * ru);
-    if (RMAX > 1) {
-        Q[1] = m.scaling * (ksi * ru * ru);
-        dQ[1] = m.scaling * (m.mult * ru * ru + 2 * ksi * ru);
-    }
-#pragma unroll
-    for (int k = 2; k < RMAX; ++k) {
-        Q[k] = 2 * ksi * Q[k - 1] - Q[k - 2];
-        dQ[k] = 2 * (m.mult * Q[k - 1] + ksi * dQ[k - 1]) - dQ[k - 2];
-    }
-    const double w = in_cutoff ? 1.0 : 0.0;
-    const double *c = coef_lds + (ti * m.Z + tj) * m.M * m.R;
-#pragma unroll
-    for (int mu = 0; mu < P::M; ++mu) {
-        double f = 0, fd = 0;
-        if (P::exact || mu < m.M) {
-            const double *cm = c + mu * m.R;
-#pragma unroll
-            for (int k = 0; k < RMAX; ++k)
-                if (k < m.R) {
-                    f += cm[k] * Q[k];
-                    fd += cm[k] * dQ[k];
-                }
-        }
-        q.f[mu] = f * w;
-        q.fd[mu] = fd * w;
-    }
-}
-
-template <int NU, int MMAX>
-__device__ __forceinline__ void next_shell(const double *prev, double *cur, const Nbr<MMAX> &q)
-{
-#pragma unroll
-    for (int a = NU; a >= 0; --a)
-#pragma unroll
-        for (int b = NU - a; b >= 0; --b) {
-            const int i = shell_index(NU, a, b);
-            if (a > 0)
-                cur[i] = prev[shell_index(NU - 1, a - 1, b)] * q.ux;
-            else if (b > 0)
-                cur[i] = prev[shell_index(NU - 1, 0, b - 1)] * q.uy;
-            else
-                cur[i] = prev[shell_index(NU - 1, 0, 0)] * q.uz;
-        }
-}
-
-// Sum `nrows` slots of the transpose buffer over the neighbour columns and
-// add the sums to the moment array.  Rows hold 64 columns; columns of lanes
-// without a neighbour hold zeros.
-__device__ __forceinline__ void reduce_chunk(const double *red, int nrows, int slot0,
-                                             const int *slot_basic, double *mom, int lane)
-{
-    wave_sync();
-    const int s = lane & (kChunk - 1), qq = lane >> 4;
-    const double2 *row = reinterpret_cast<const double2 *>(red + s * kRedStride + qq * 16);
-    double a0 = 0.0, a1 = 0.0;
-#pragma unroll
-    for (int jj = 0; jj < 8; ++jj) {
-        const double2 v = row[jj];
-        a0 += v.x;
-        a1 += v.y;
-    }
-    double acc = xor16_sum(xor32_sum(a0 + a1));
-    if (lane < nrows) {
-        const int b = slot_basic[slot0 + lane];
-        if (b >= 0)
-            mom[b] += acc;
-    }
-    wave_sync();
-}
-
-struct FwdCtx {
-    double *red, *mom;
-    const int *slot_basic;
-    int lane, slot;  // slots written so far; rows are packed across (nu, mu) blocks
-};
-
-template <int NU, class P>
-__device__ __forceinline__ void fwd_shells(const DevModel &m, FwdCtx &cx, const Nbr<P::M> &q,
-                                           const double *prev)
-{
-    double cur[shell_size(NU)];
-    if constexpr (NU == 0)
-        cur[0] = 1.0;
-    else
-        next_shell<NU, P::M>(prev, cur, q);
-#pragma unroll
-    for (int mu = 0; mu < P::M; ++mu) {
-        if (P::active(m, mu, NU)) {
-            __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-            for (int i = 0; i < shell_size(NU); ++i) {
-                cx.red[(cx.slot % kChunk) * kRedStride + cx.lane] = q.f[mu] * cur[i];
-                ++cx.slot;
-                if (cx.slot % kChunk == 0)
-                    reduce_chunk(cx.red, kChunk, cx.slot - kChunk, cx.slot_basic, cx.mom,
-                                 cx.lane);
-            }
-        }
-    }
-    if constexpr (NU < P::NUMAX) {
-        if (P::deeper(m, NU))
-            fwd_shells<NU + 1, P>(m, cx, q, cur);
-    }
-}
-
-struct BwdAcc {
-    double s, gx, gy, gz;
-};
-
-template <int NU, class P>
-__device__ __forceinline__ void bwd_shells(const DevModel &m, const double4 *A4, int &slot,
-                                           const Nbr<P::M> &q, const double *prev, BwdAcc &acc)
-{
-    double cur[shell_size(NU)];
-    if constexpr (NU == 0)
-        cur[0] = 1.0;
-    else
-        next_shell<NU, P::M>(prev, cur, q);
-#pragma unroll
-    for (int mu = 0; mu < P::M; ++mu) {
-        if (P::active(m, mu, NU)) {
-            // keep the adjoint loads of one (nu, mu) block from being hoisted
-            // into the previous one: bounds the live registers
-            __builtin_amdgcn_sched_barrier(0);
-            double u = 0, Gx = 0, Gy = 0, Gz = 0;
-#pragma unroll
-            for (int a = NU; a >= 0; --a)
-#pragma unroll
-                for (int b = NU - a; b >= 0; --b) {
-                    const int i = shell_index(NU, a, b);
-                    const double4 w = A4[slot + i];  // {A, aA, bA, cA}, LDS broadcast
-                    u += w.x * cur[i];
-                    if constexpr (NU > 0) {
-                        if (a > 0)
-                            Gx += w.y * prev[shell_index(NU - 1, a - 1, b)];
-                        if (b > 0)
-                            Gy += w.z * prev[shell_index(NU - 1, a, b - 1)];
-                        if (NU - a - b > 0)
-                            Gz += w.w * prev[shell_index(NU - 1, a, b)];
-                    }
-                }
-            const double h = q.fd[mu] - NU * q.f[mu] * q.invd;
-            acc.s += h * u;
-            acc.gx += q.f[mu] * Gx;
-            acc.gy += q.f[mu] * Gy;
-            acc.gz += q.f[mu] * Gz;
-            slot += shell_size(NU);
-        }
-    }
-    if constexpr (NU < P::NUMAX) {
-        if (P::deeper(m, NU))
-            bwd_shells<NU + 1, P>(m, A4, slot, q, cur, acc);
-    }
-}
-
-// Product rules from a lane-major step table (forward: potential_mtp.cpp:
-// 2918-2924; reverse: backpropagate_moments, :3292-3305), one dependency
-// level at a time.  Steps are taken in groups of four: the entries of the
-// next group are loaded while the current one runs, and every operand of a
-// group is read before any of its results is written (a level never reads
-// what it writes).
-__device__ __forceinline__ void run_rules(const int2 *tab, const int *level_step,
-                                          const int *level_comb, const int4 *comb, int nlev,
-                                          double *ws, int lane)
-{
-    for (int L = 0; L < nlev; ++L) {
-        const int s0 = level_step[L], s1 = level_step[L + 1];
-        double acc = 0.0;
-        if (s1 > s0) {
-            const int2 *t = tab + (size_t)s0 * kWave + lane;
-            int2 e[4] = {t[0], t[kWave], t[2 * kWave], t[3 * kWave]};
-            for (int st = s0; st < s1; st += 4) {
-                int2 nx[4] = {e[0], e[1], e[2], e[3]};
-                if (st + 4 < s1) {
-                    const int2 *u = t + (size_t)(st + 4 - s0) * kWave;
-                    nx[0] = u[0];
-                    nx[1] = u[kWave];
-                    nx[2] = u[2 * kWave];
-                    nx[3] = u[3 * kWave];
-                }
-                double ml[4], mr[4], init[4], v[4];
-#pragma unroll
-                for (int k = 0; k < 4; ++k) {
-                    ml[k] = ws[e[k].x & 0xffff];
-                    mr[k] = ws[(unsigned)e[k].x >> 16];
-                    init[k] = ws[e[k].y & 0xffff];
-                }
-#pragma unroll
-                for (int k = 0; k < 4; ++k) {
-                    const double c = (double)(e[k].y >> 17);
-                    acc = fma(c * ml[k], mr[k], (e[k].y & 0x10000) ? init[k] : acc);
-                    v[k] = acc;
-                }
-#pragma unroll
-                for (int k = 0; k < 4; ++k)
-                    ws[e[k].y & 0xffff] = v[k];
-#pragma unroll
-                for (int k = 0; k < 4; ++k)
-                    e[k] = nx[k];
-            }
-        }
-        const int c0 = level_comb[L], c1 = level_comb[L + 1];
-        if (c1 > c0) {
-            wave_sync();
-            for (int c = c0 + lane; c < c1; c += kWave) {
-                const int4 q = comb[c];
-                double sum = ws[q.x];
-                for (int k = 0; k < q.z; ++k) {
-                    sum += ws[q.y + k];
-                    ws[q.y + k] = 0.0;
-                }
-                ws[q.x] = sum;
-            }
-        }
-        wave_sync();
-    }
-}
-
-// Block-shared LDS tables, in this order (doubles, then ints, then the
-// optional step tables; every part a multiple of 32 bytes).
-struct Shared {
-    double *coef, *seed, *moment;
-    int *map, *slot_basic, *slot_abc;
-    int2 *fwd_steps, *bwd_steps;
-};
-
-__device__ __host__ __forceinline__ size_t shared_doubles(const DevModel &m, bool tables)
-{
-    const size_t r4c = ((size_t)m.Z * m.Z * m.M * m.R + 3) & ~size_t(3);
-    const size_t S4 = (m.S + 3) & ~3, N4 = (m.nslots + 3) & ~3;
-    size_t d = r4c + m.K4 + S4 + (S4 + 2 * N4) / 2;
-    if (tables)
-        d += (size_t)(m.fwd_nsteps + m.bwd_nsteps) * kWave;
-    return (d + 3) & ~size_t(3);
-}
-
-__device__ __forceinline__ Shared shared_layout(const DevModel &m, double *base)
-{
-    const int r4c = (m.Z * m.Z * m.M * m.R + 3) & ~3;
-    const int S4 = (m.S + 3) & ~3, N4 = (m.nslots + 3) & ~3;
-    Shared L;
-    L.coef = base;
-    L.seed = L.coef + r4c;
-    L.moment = L.seed + m.K4;
-    L.map = reinterpret_cast<int *>(L.moment + S4);
-    L.slot_basic = L.map + S4;
-    L.slot_abc = L.slot_basic + N4;
-    L.fwd_steps = reinterpret_cast<int2 *>(L.slot_abc + N4);
-    L.bwd_steps = L.fwd_steps + (size_t)m.fwd_nsteps * kWave;
-    return L;
-}
 
 template <class P, bool kTabLds, int kMaxWaves>
 __global__ __launch_bounds__(kWave *kMaxWaves) void efs_kernel(DevModel m, DevNeighbors nb,
@@ -417,25 +52,7 @@ __global__ __launch_bounds__(kWave *kMaxWaves) void efs_kernel(DevModel m, DevNe
     const double4 *A4 = reinterpret_cast<const double4 *>(red);
 
     // model tables the per-atom phases index, staged once per workgroup
-    const int ncoef_r = m.Z * m.Z * m.M * m.R;
-    for (int k = tid; k < ncoef_r; k += blockDim.x)
-        L.coef[k] = m.radial[k];
-    for (int k = tid; k < m.K; k += blockDim.x)
-        L.seed[k] = m.seed[k];
-    for (int k = tid; k < m.S; k += blockDim.x) {
-        L.moment[k] = m.moment[k];
-        L.map[k] = m.map[k];
-    }
-    for (int k = tid; k < m.nslots; k += blockDim.x) {
-        L.slot_basic[k] = m.slot_basic[k];
-        L.slot_abc[k] = m.slot_abc[k];
-    }
-    if constexpr (kTabLds) {
-        for (int k = tid; k < m.fwd_nsteps * kWave; k += blockDim.x)
-            L.fwd_steps[k] = m.fwd_steps[k];
-        for (int k = tid; k < m.bwd_nsteps * kWave; k += blockDim.x)
-            L.bwd_steps[k] = m.bwd_steps[k];
-    }
+    stage_shared(m, L, kTabLds, tid, blockDim.x);
     // the dummy slot and the partial sums start at zero; the rule phases
     // leave them zero
     for (int k = m.dummy + lane; k < m.red0; k += kWave)
@@ -472,7 +89,7 @@ __global__ __launch_bounds__(kWave *kMaxWaves) void efs_kernel(DevModel m, DevNe
                 mom[m.dup[2 * k]] = mom[m.dup[2 * k + 1]];
         wave_sync();
 
-        run_rules(fwd_tab, m.fwd_level_step, m.fwd_level_comb, m.fwd_comb, m.nfwd, ws, lane);
+        run_rules<false>(fwd_tab, m.fwd_level_step, m.fwd_level_comb, m.fwd_comb, m.nfwd, ws, lane, 0);
 
         // ---- site energy (potential_mtp.cpp:2966-2970) and adjoint seed ----
         double e = 0.0;
@@ -488,7 +105,7 @@ __global__ __launch_bounds__(kWave *kMaxWaves) void efs_kernel(DevModel m, DevNe
             A[k] = L.seed[k];
         wave_sync();
 
-        run_rules(bwd_tab, m.bwd_level_step, m.bwd_level_comb, m.bwd_comb, m.nbwd, ws, lane);
+        run_rules<false>(bwd_tab, m.bwd_level_step, m.bwd_level_comb, m.bwd_comb, m.nbwd, ws, lane, 0);
         if (lane == 0)
             for (int k = 0; k < m.ndup; ++k)
                 A[m.dup[2 * k + 1]] += A[m.dup[2 * k]];
@@ -508,6 +125,7 @@ __global__ __launch_bounds__(kWave *kMaxWaves) void efs_kernel(DevModel m, DevNe
 
         // ---- forces and virial ---------------------------------------------
         double fi0 = 0, fi1 = 0, fi2 = 0;
+        double vs[9] = {0, 0, 0, 0, 0, 0, 0, 0, 0};  // this atom's virial share
         for (int base = 0; base < n; base += kWave) {
             const bool valid = lane < n - base;
             const int64_t p = beg + base + lane;
@@ -527,7 +145,7 @@ __global__ __launch_bounds__(kWave *kMaxWaves) void efs_kernel(DevModel m, DevNe
             for (int a = 0; a < 3; ++a)
 #pragma unroll
                 for (int bq = 0; bq < 3; ++bq)
-                    v_acc[3 * a + bq] -= D[a] * r[bq];
+                    vs[3 * a + bq] -= D[a] * r[bq];
             if (valid) {
                 if (deterministic) {
                     out.pair_ders[3 * p + 0] = D0;
@@ -540,6 +158,18 @@ __global__ __launch_bounds__(kWave *kMaxWaves) void efs_kernel(DevModel m, DevNe
                     atomicAdd(&out.forces[3 * j + 2], -D2);
                 }
             }
+        }
+#pragma unroll
+        for (int k = 0; k < 9; ++k)
+            v_acc[k] += vs[k];
+        if (out.site_virial) {
+#pragma unroll
+            for (int k = 0; k < 9; ++k)
+                vs[k] = wave_sum(vs[k]);
+            if (lane == 0)
+#pragma unroll
+                for (int k = 0; k < 9; ++k)
+                    out.site_virial[9 * (size_t)i + k] = vs[k];
         }
         if (!deterministic) {
             fi0 = wave_sum(fi0);
@@ -618,19 +248,6 @@ __global__ __launch_bounds__(256) void force_gather_kernel(DevNeighbors nb, cons
     forces[3 * k + 2] = f2;
 }
 
-template <int... NM>
-bool profile_is(const DevModel &m)
-{
-    constexpr int nm[] = {NM...};
-    constexpr int M = sizeof...(NM);
-    if (m.M != M)
-        return false;
-    for (int mu = 0; mu < M; ++mu)
-        if (m.numax[mu] != nm[mu])
-            return false;
-    return true;
-}
-
 // Kernel variants: shell profile x table placement.  The profiles whose
 // kernels fit 256 registers run eight waves per workgroup, the larger ones four.
 template <class P>
@@ -675,38 +292,20 @@ int variant_max_waves(int v)
 bool efs_configure(const DevModel &m, int n, int num_cus, int max_waves, size_t lds_limit,
                    EfsLaunch &cfg)
 {
-    const size_t kLdsPerCu = lds_limit;
-    const size_t priv = (size_t)m.priv_doubles * sizeof(double);
     const int vmax = variant_max_waves(efs_variant(m, m.R));
     const int wcap = max_waves > 0 ? std::min(vmax, max_waves) : vmax;
-    auto fit = [&](bool tables) {
-        const size_t sh = shared_doubles(m, tables) * sizeof(double);
-        if (sh + priv > kLdsPerCu)
-            return 0;
-        return (int)std::min<size_t>(wcap, (kLdsPerCu - sh) / priv);
-    };
-    const int wt = fit(true), wg = fit(false);
-    if (wg == 0)
-        return false;
-    // rule tables in LDS unless that costs more than half the waves
-    cfg.lds_tables = wt > 0 && 2 * wt >= wg;
-    cfg.waves = cfg.lds_tables ? wt : wg;
-    cfg.lds_bytes = shared_doubles(m, cfg.lds_tables) * sizeof(double) + cfg.waves * priv;
-    const int per_cu = std::max<int>(1, (int)(kLdsPerCu / cfg.lds_bytes));
-    const int need = (std::max(n, 1) + cfg.waves - 1) / cfg.waves;
-    cfg.grid = std::max(1, std::min(need, num_cus * per_cu));
-    cfg.rows = cfg.grid * cfg.waves;
-    return true;
+    return configure_launch(m, n, num_cus, wcap, lds_limit, m.priv_doubles, cfg);
 }
 
-// 0: level-16 profile, 1: level-20, 2: level-10, 3: small runtime, 4: generic
+// 0: level-16 profile, 1: level-20, 2: level-10 (each with its template's
+// radial basis size), 3: small runtime, 4: generic
 int efs_variant(const DevModel &m, int R)
 {
-    if (profile_is<6, 4, 2, 0>(m) && R <= 8)
+    if (profile_is<6, 4, 2, 0>(m) && R == 8)
         return 0;
-    if (profile_is<8, 6, 4, 2, 0>(m) && R <= 10)
+    if (profile_is<8, 6, 4, 2, 0>(m) && R == 10)
         return 1;
-    if (profile_is<3, 1, 0>(m) && R <= 8)
+    if (profile_is<3, 1, 0>(m) && R == 8)
         return 2;
     if (m.M <= 4 && m.numax_all <= 6 && R <= 8)
         return 3;

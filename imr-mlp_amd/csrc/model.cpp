@@ -362,6 +362,17 @@ bool build_plan(const Model &m, Plan &p, std::string &err)
                 }
         }
     p.nslots = (int)p.slot_basic.size();
+    for (int k = 0; k < (kMaxNu + 1) * kMaxMu; ++k)
+        p.slot_base[k] = -1;
+    {
+        int s = 0;
+        for (int nu = 0; nu <= p.numax_all; ++nu)
+            for (int mu = 0; mu < m.M; ++mu)
+                if (p.numax[mu] >= nu) {
+                    p.slot_base[nu * kMaxMu + mu] = s;
+                    s += (nu + 1) * (nu + 2) / 2;
+                }
+    }
 
     // Dependency levels.  The reference applies the rules in file order
     // (potential_mtp.cpp:2918-2924), so every operand must be complete before
@@ -535,6 +546,17 @@ bool build_plan(const Model &m, Plan &p, std::string &err)
     };
     encode(fwd, false, p.fwd_steps, p.fwd_level_step, p.fwd_comb, p.fwd_level_comb);
     encode(bwd, true, p.bwd_steps, p.bwd_level_step, p.bwd_comb, p.bwd_level_comb);
+
+    // Training work space: the E/F/S work space, its dual copy (tangents and
+    // second adjoints), a transpose buffer, the slot-ordered adjoint staging
+    // {A, aA, bA, cA} + G, the wave's gradient accumulator and the species
+    // of the neighbours in flight.
+    p.tr_delta = p.red0;
+    p.tr_red = 2 * p.red0;
+    p.tr_stage = p.tr_red + kChunk * kRedStride;
+    p.tr_grad = p.tr_stage + 5 * N4;
+    p.tr_ctype = p.tr_grad + ((m.ncoef() + 3) & ~3);
+    p.tr_priv = p.tr_ctype + kWave / 2;  // 64 ints: neighbour species of a batch
     return true;
 }
 

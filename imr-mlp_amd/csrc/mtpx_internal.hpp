@@ -71,6 +71,13 @@ int build_neighbors_gpu(const double cell[9], const int pbc[3], int n, const dou
                         const int *types, double cutoff, hipStream_t s, NeighborStore &out,
                         NeighborScratch &w, std::string &err);
 
+// Builds the lists of nconf structures (atoms atom_offsets[c] .. [c+1]) one
+// after the other and concatenates them: atom and entry indices are global.
+int build_neighbors_batch_gpu(int nconf, const int *atom_offsets, const double *cells,
+                              const int *pbc, const double *pos, const int *types, double cutoff,
+                              hipStream_t s, NeighborStore &out, NeighborStore &tmp,
+                              NeighborScratch &w, std::string &err);
+
 // Host-side model: the linear MTP (potentials/potential_mtp.h:93) plus the
 // launch plan derived from its contraction graph.
 struct Model {
@@ -102,6 +109,14 @@ struct Plan {
     //   [0, K4) moments | [K4, 2 K4) adjoints | dummy (a zero slot) |
     //   [part0, red0) partial sums | [red0, priv_doubles) transpose buffer.
     int K4 = 0, dummy = 0, part0 = 0, red0 = 0, priv_doubles = 0;
+    // Training work space (doubles): [0, tr_delta) the E/F/S work space,
+    // [tr_delta, tr_red) its dual copy, then a transpose buffer, the staged
+    // slot adjoints (tr_stage: 4 x nslots4 of {A, aA, bA, cA}, then nslots4
+    // of G), the gradient accumulator (tr_grad, ncoef) and 64 neighbour
+    // species (tr_ctype, as ints).
+    int tr_delta = 0, tr_red = 0, tr_stage = 0, tr_grad = 0, tr_ctype = 0, tr_priv = 0;
+    // first slot of each (nu, mu) block, -1 where absent: [nu * kMaxMu + mu]
+    int slot_base[(kMaxNu + 1) * kMaxMu];
     // Lane-major step tables, one per direction.  Level L owns steps
     // [level_step[L], level_step[L+1]) (a multiple of 4); step s of lane q is
     // entry s * 64 + q, an int2 of work-space indices:
@@ -141,6 +156,9 @@ struct DevModel {
     const int *dup;         // [ndup][2]
     int max_partials;
     int K4, dummy, part0, red0, priv_doubles;  // per-wave work space (Plan)
+    int tr_delta, tr_red, tr_stage, tr_grad, tr_ctype, tr_priv;
+    int nradial, ncoef;
+    int slot_base[(kMaxNu + 1) * kMaxMu];
     int fwd_nsteps, bwd_nsteps;                 // steps per lane, all levels
     const int *fwd_level_step;  // [nfwd+1]
     const int2 *fwd_steps;
@@ -168,6 +186,7 @@ struct EfsOut {
     double *site_energy;    // [n]
     double *partial;        // [rows][10] per wave: energy, stress[9]
     double *pair_ders;      // [P][3] (deterministic mode) or nullptr
+    double *site_virial;    // [n][9] per-atom -sum_j D_j r_j^T, or nullptr
 };
 
 // Launch shape of the E/F/S kernel (efs_kernel.hip).
@@ -186,6 +205,33 @@ bool efs_configure(const DevModel &m, int n, int num_cus, int max_waves, size_t 
 int efs_variant(const DevModel &m, int R);
 hipError_t launch_efs(const DevModel &m, const DevNeighbors &nb, const EfsOut &out,
                       const EfsLaunch &cfg, bool deterministic, hipStream_t s);
+// Training (train_kernel.hip).
+struct LossArgs {
+    const int *soff;     // [nconf+1] first atom of each structure
+    int nconf;
+    const int *active;   // [nconf][3] energy, force, stress terms present
+    const double *E, *F, *S;      // model: [nconf], [n][3], [nconf][9]
+    const double *tE, *wE;        // targets and weights: [nconf]
+    const double *tF, *wF;        // [n][3], [n]
+    const double *tS, *wS;        // [nconf][9], [nconf]
+    double *dLdE, *dLdF, *dLdS;   // adjoints: [nconf], [n][3], [nconf][9]
+    double *metric_rows;          // [nconf][7]
+};
+struct TrainArgs {
+    const int *center_structure;  // [n]
+    const double *dLdE, *dLdF, *dLdS;
+    double *grad_rows;            // [rows][ncoef]
+};
+bool grad_configure(const DevModel &m, int n, int num_cus, size_t lds_limit, EfsLaunch &cfg);
+hipError_t launch_structure_reduce(const int *soff, int nconf, const double *site_energy,
+                                   const double *site_virial, double *energy, double *stress,
+                                   hipStream_t s);
+hipError_t launch_loss(const LossArgs &a, hipStream_t s);
+hipError_t launch_rows_reduce(const double *rows, int nrows, int cols, double *out, bool accumulate,
+                              hipStream_t s);
+hipError_t launch_grad(const DevModel &m, const DevNeighbors &nb, const TrainArgs &t,
+                       const EfsLaunch &cfg, hipStream_t s);
+
 hipError_t launch_efs_finish(const DevNeighbors &nb, const EfsOut &out, int rows,
                              bool deterministic, const int *rev_offsets, const int *rev_pairs,
                              double *energy_stress10, hipStream_t s);

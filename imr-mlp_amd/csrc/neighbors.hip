@@ -754,4 +754,103 @@ int build_neighbors_gpu(const double cell[9], const int pbc[3], int n, const dou
     return MTPX_OK;
 }
 
+namespace {
+
+// Append one structure's lists (atoms from a0, entries from p0) to a batch.
+__global__ void append_lists_kernel(const int *offsets, const int *idx, int n, int64_t P, int a0,
+                                    int64_t p0, int *out_offsets, int *out_idx)
+{
+    const int64_t k = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (k <= n)
+        out_offsets[a0 + k] = (int)(p0 + offsets[k]);
+    if (k < P)
+        out_idx[p0 + k] = a0 + idx[k];
+}
+
+// Grows a device buffer to `need` bytes, keeping its first `keep` bytes.
+hipError_t grow_keep(DBuf &b, size_t need, size_t keep, hipStream_t s)
+{
+    if (need <= b.bytes && b.p)
+        return hipSuccess;
+    size_t want = std::max<size_t>(need, 2 * b.bytes);
+    void *np = nullptr;
+    hipError_t e = hipMalloc(&np, want);
+    if (e != hipSuccess)
+        return e;
+    if (keep && b.p)
+        e = hipMemcpyAsync(np, b.p, keep, hipMemcpyDeviceToDevice, s);
+    if (e == hipSuccess)
+        e = hipStreamSynchronize(s);
+    if (e != hipSuccess) {
+        (void)hipFree(np);
+        return e;
+    }
+    if (b.p)
+        (void)hipFree(b.p);
+    b.p = np;
+    b.bytes = want;
+    return hipSuccess;
+}
+
+}  // namespace
+
+int build_neighbors_batch_gpu(int nconf, const int *atom_offsets, const double *cells,
+                              const int *pbc, const double *pos, const int *types, double cutoff,
+                              hipStream_t s, NeighborStore &out, NeighborStore &tmp,
+                              NeighborScratch &w, std::string &err)
+{
+    const int ntot = atom_offsets[nconf];
+    out.n = ntot;
+    out.P = 0;
+    DTRY(out.offsets.ensure(sizeof(int) * ((size_t)ntot + 1)));
+    DTRY(out.center_type.ensure(sizeof(int) * std::max(ntot, 1)));
+    DTRY(hipMemsetAsync(out.offsets.p, 0, sizeof(int) * ((size_t)ntot + 1), s));
+    int64_t P = 0;
+    for (int c = 0; c < nconf; ++c) {
+        const int a0 = atom_offsets[c], nc = atom_offsets[c + 1] - a0;
+        int rc = build_neighbors_gpu(cells + 9 * (size_t)c, pbc + 3 * (size_t)c, nc,
+                                     pos + 3 * (size_t)a0, types + a0, cutoff, s, tmp, w, err);
+        if (rc != MTPX_OK) {
+            err = "structure " + std::to_string(c) + ": " + err;
+            return rc;
+        }
+        const int64_t Pc = tmp.P, Pn = P + Pc;
+        if (Pn > INT32_MAX) {
+            err = "batch has more than 2^31 - 1 neighbour entries";
+            return MTPX_E_CAPACITY;
+        }
+        const size_t keep = (size_t)P, need = (size_t)std::max<int64_t>(Pn, 1);
+        DTRY(grow_keep(out.idx, sizeof(int) * need, sizeof(int) * keep, s));
+        DTRY(grow_keep(out.type, sizeof(int) * need, sizeof(int) * keep, s));
+        DTRY(grow_keep(out.x, sizeof(double) * need, sizeof(double) * keep, s));
+        DTRY(grow_keep(out.y, sizeof(double) * need, sizeof(double) * keep, s));
+        DTRY(grow_keep(out.z, sizeof(double) * need, sizeof(double) * keep, s));
+        DTRY(grow_keep(out.d, sizeof(double) * need, sizeof(double) * keep, s));
+        if (nc > 0)
+            DTRY(hipMemcpyAsync(out.center_type.as<int>() + a0, tmp.center_type.p,
+                                sizeof(int) * nc, hipMemcpyDeviceToDevice, s));
+        if (Pc > 0) {
+            DTRY(hipMemcpyAsync(out.type.as<int>() + P, tmp.type.p, sizeof(int) * Pc,
+                                hipMemcpyDeviceToDevice, s));
+            DTRY(hipMemcpyAsync(out.x.as<double>() + P, tmp.x.p, sizeof(double) * Pc,
+                                hipMemcpyDeviceToDevice, s));
+            DTRY(hipMemcpyAsync(out.y.as<double>() + P, tmp.y.p, sizeof(double) * Pc,
+                                hipMemcpyDeviceToDevice, s));
+            DTRY(hipMemcpyAsync(out.z.as<double>() + P, tmp.z.p, sizeof(double) * Pc,
+                                hipMemcpyDeviceToDevice, s));
+            DTRY(hipMemcpyAsync(out.d.as<double>() + P, tmp.d.p, sizeof(double) * Pc,
+                                hipMemcpyDeviceToDevice, s));
+        }
+        const int64_t work = std::max<int64_t>(Pc, (int64_t)nc + 1);
+        hipLaunchKernelGGL(append_lists_kernel, dim3((unsigned)((work + 255) / 256)), dim3(256),
+                           0, s, tmp.offsets.as<int>(), tmp.idx.as<int>(), nc, Pc, a0, P,
+                           out.offsets.as<int>(), out.idx.as<int>());
+        DTRY(hipGetLastError());
+        P = Pn;
+    }
+    DTRY(hipStreamSynchronize(s));
+    out.P = P;
+    return MTPX_OK;
+}
+
 }  // namespace mtpx

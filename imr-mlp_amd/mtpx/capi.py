@@ -64,16 +64,43 @@ def lib():
         L.mtpx_efs.argtypes = [C.c_void_p, C.c_int, _dp, _dp, _dp, _dp]
         L.mtpx_efs_device.argtypes = [C.c_void_p, C.c_int]
         L.mtpx_last_timings.argtypes = [C.c_void_p, _dp]
+        L.mtpx_set_structures.argtypes = [C.c_void_p, C.c_int, _ip, _dp, _ip, _dp, _ip,
+                                          C.c_double]
+        L.mtpx_structure_count.argtypes = [C.c_void_p, _ip]
+        L.mtpx_compute_batch.argtypes = [C.c_void_p, C.c_int, _dp, _dp, _dp, _dp]
+        L.mtpx_loss_weights.argtypes = [C.POINTER(LossSettings), C.c_int, _ip, _ip, _dp, _dp,
+                                        _dp, _ip, _dp, _dp, _dp]
+        L.mtpx_set_labels.argtypes = [C.c_void_p, _ip, _dp, _dp, _dp, _dp, _dp, _dp]
+        L.mtpx_prepare_loss.argtypes = [C.c_void_p, _dp]
+        L.mtpx_accumulate_gradient.argtypes = [C.c_void_p, _dp, _dp, _dp, C.c_int, _dp]
+        L.mtpx_penalty.argtypes = [C.c_void_p, C.c_double, C.c_double, C.c_double, _dp, _dp]
+        L.mtpx_loss_grad.argtypes = [C.c_void_p, C.c_int, C.c_double, C.c_double, C.c_double,
+                                     _dp, _dp, _dp]
+        L.mtpx_last_train_timings.argtypes = [C.c_void_p, _dp]
         _lib = L
     return _lib
 
 
+class LossSettings(C.Structure):
+    """mtpx_loss_settings; defaults are Trainer_MTP's (train_mtp.cpp:2552-2568)."""
+    _fields_ = [(k, C.c_double) for k in
+                ("weight_energy", "weight_forces", "weight_stress", "energy_pow", "force_pow",
+                 "stress_pow", "force_norm_d", "force_norm_f", "force_norm_p")]
+
+    @classmethod
+    def make(cls, weight_energy=1.0, weight_forces=0.01, weight_stress=1e-4, energy_pow=1.0,
+             force_pow=0.0, stress_pow=1.0, force_norm_d=0.1, force_norm_f=0.0,
+             force_norm_p=1.0):
+        return cls(weight_energy, weight_forces, weight_stress, energy_pow, force_pow,
+                   stress_pow, force_norm_d, force_norm_f, force_norm_p)
+
+
 def _d(a):
-    return a.ctypes.data_as(_dp)
+    return None if a is None else a.ctypes.data_as(_dp)
 
 
 def _i(a):
-    return a.ctypes.data_as(_ip)
+    return None if a is None else a.ctypes.data_as(_ip)
 
 
 def f64(a, shape=None):
@@ -98,6 +125,25 @@ def wrap(cell, pbc, pos) -> np.ndarray:
     if rc != OK:
         raise MtpxError(rc, "mtpx_wrap")
     return out
+
+
+def loss_weights(settings: LossSettings, atom_offsets, has, target_forces=None, fitness=None,
+                 atomic_fitness=None):
+    """Per-structure loss weights (host): (active [nconf][3], wE, wF, wS)."""
+    off = i32(atom_offsets)
+    nconf = len(off) - 1
+    N = int(off[-1])
+    has = i32(has).reshape(-1)
+    active = np.zeros(3 * max(nconf, 1), np.int32)
+    wE, wS, wF = np.zeros(max(nconf, 1)), np.zeros(max(nconf, 1)), np.zeros(max(N, 1))
+    tf = None if target_forces is None else f64(target_forces, (-1,))
+    fit = None if fitness is None else f64(fitness)
+    af = None if atomic_fitness is None else f64(atomic_fitness)
+    rc = lib().mtpx_loss_weights(C.byref(settings), nconf, _i(off), _i(has), _d(tf), _d(fit),
+                                 _d(af), _i(active), _d(wE), _d(wF), _d(wS))
+    if rc != OK:
+        raise MtpxError(rc, "mtpx_loss_weights")
+    return active[:3 * nconf].reshape(nconf, 3), wE[:nconf], wF[:N], wS[:nconf]
 
 
 def parse_model_text(text: str):
@@ -206,4 +252,78 @@ class Context:
     def last_timings(self):
         t = np.zeros(4)
         self._check(lib().mtpx_last_timings(self.h, _d(t)), "last_timings")
+        return t
+
+    # ---- training batches ----
+    def set_structures(self, structures, cutoff):
+        """structures: objects with cell (3x3), pbc (3), pos (n x 3), types (n)."""
+        off = np.zeros(len(structures) + 1, np.int32)
+        for c, st in enumerate(structures):
+            off[c + 1] = off[c] + len(st.types)
+        cells = f64(np.array([f64(st.cell, (9,)) for st in structures]).reshape(-1))
+        pbc = i32(np.array([i32(st.pbc) for st in structures]).reshape(-1))
+        pos = f64(np.concatenate([f64(st.pos, (-1, 3)) for st in structures]) if len(structures)
+                  else np.zeros((0, 3)), (-1,))
+        types = i32(np.concatenate([i32(st.types) for st in structures]) if len(structures)
+                    else np.zeros(0))
+        self._check(lib().mtpx_set_structures(self.h, len(structures), _i(off), _d(cells),
+                                              _i(pbc), _d(pos), _i(types), float(cutoff)),
+                    "set_structures")
+        self.atom_offsets = off
+        return off
+
+    def structure_count(self):
+        n = C.c_int()
+        self._check(lib().mtpx_structure_count(self.h, C.byref(n)), "structure_count")
+        return n.value
+
+    def compute_batch(self, deterministic: bool = False):
+        n, _ = self.neighbor_count()
+        nc = self.structure_count()
+        E, S = np.zeros(max(nc, 1)), np.zeros((max(nc, 1), 3, 3))
+        F, se = np.zeros((max(n, 1), 3)), np.zeros(max(n, 1))
+        self._check(lib().mtpx_compute_batch(self.h, int(deterministic), _d(E), _d(F), _d(S),
+                                             _d(se)), "compute_batch")
+        return E[:nc], F[:n], S[:nc], se[:n]
+
+    def set_labels(self, active, tE=None, wE=None, tF=None, wF=None, tS=None, wS=None):
+        conv = lambda a, shape=None: None if a is None else f64(a, shape)
+        self._labels = [i32(active).reshape(-1), conv(tE), conv(wE), conv(tF, (-1,)), conv(wF),
+                        conv(tS, (-1,)), conv(wS)]
+        a = self._labels
+        self._check(lib().mtpx_set_labels(self.h, _i(a[0]), _d(a[1]), _d(a[2]), _d(a[3]),
+                                          _d(a[4]), _d(a[5]), _d(a[6])), "set_labels")
+
+    def prepare_loss(self):
+        m = np.zeros(7)
+        self._check(lib().mtpx_prepare_loss(self.h, _d(m)), "prepare_loss")
+        return m
+
+    def accumulate_gradient(self, dLdE=None, dLdF=None, dLdS=None, gradient=None):
+        g = np.zeros(self.info["ncoef"]) if gradient is None else f64(gradient).copy()
+        conv = lambda a: None if a is None else f64(a, (-1,))
+        a = [conv(dLdE), conv(dLdF), conv(dLdS)]
+        self._check(lib().mtpx_accumulate_gradient(self.h, _d(a[0]), _d(a[1]), _d(a[2]),
+                                                   int(gradient is not None), _d(g)),
+                    "accumulate_gradient")
+        return g
+
+    def penalty(self, weight, reg_l2, reg_l1):
+        loss = C.c_double(0.0)
+        g = np.zeros(self.info["ncoef"])
+        self._check(lib().mtpx_penalty(self.h, weight, reg_l2, reg_l1, C.byref(loss), _d(g)),
+                    "penalty")
+        return loss.value, g
+
+    def loss_grad(self, penalty_weight=0.0, reg_l2=0.0, reg_l1=0.0, deterministic=False):
+        loss = C.c_double()
+        g = np.zeros(self.info["ncoef"])
+        m = np.zeros(7)
+        self._check(lib().mtpx_loss_grad(self.h, int(deterministic), penalty_weight, reg_l2,
+                                         reg_l1, C.byref(loss), _d(g), _d(m)), "loss_grad")
+        return loss.value, g, m
+
+    def last_train_timings(self):
+        t = np.zeros(4)
+        self._check(lib().mtpx_last_train_timings(self.h, _d(t)), "last_train_timings")
         return t

@@ -125,6 +125,84 @@ int mtpx_efs_device(mtpx_context *ctx, int deterministic);
  * {E/F/S kernel + reductions, E/F/S kernel alone, reductions, 0}. */
 int mtpx_last_timings(const mtpx_context *ctx, double out_ms[4]);
 
+/* ---- training batches -------------------------------------------------
+ * A batch is nconf structures stored one after the other: structure c owns
+ * atoms atom_offsets[c] .. atom_offsets[c+1]-1 of pos [N][3] and types [N],
+ * its cell is cells[9c .. 9c+8] and its periodicity pbc[3c .. 3c+2].  The
+ * lists of every structure are built on the device as by
+ * mtpx_build_neighbors and concatenated into one CSR with global atom
+ * indices: the flattened topology of MTPGpuBatchRequest
+ * (mtp_gpu_direct.h:452-517) and MTPGpuBatch::build
+ * (potentials/mtp_gpu_adapter.cpp:1011-1200).  Replaces the resident lists;
+ * mtpx_build_neighbors / mtpx_set_neighbors make a batch of one. */
+int mtpx_set_structures(mtpx_context *ctx, int nconf, const int *atom_offsets,
+                        const double *cells, const int *pbc, const double *pos, const int *types,
+                        double cutoff);
+/* Number of structures of the resident topology. */
+int mtpx_structure_count(const mtpx_context *ctx, int *nconf);
+/* MTPGpuDirect::compute_batch (mtp_gpu_direct.h:892) over the batch: per
+ * structure energy [nconf] and stress [nconf][9] (as mtpx_efs), forces
+ * [N][3] and site energies [N].  Any output may be NULL; the outputs stay
+ * resident for mtpx_prepare_loss. */
+int mtpx_compute_batch(mtpx_context *ctx, int deterministic, double *energy, double *forces,
+                       double *stress, double *site_energies);
+
+/* Loss settings of Trainer_MTP (train/train_mtp.cpp:2552-2568; the
+ * defaults 1, 0.01, 1e-4, 1, 0, 1, 0.1, 0, 1 are the reference's). */
+typedef struct mtpx_loss_settings {
+    double weight_energy, weight_forces, weight_stress;
+    double energy_pow, force_pow, stress_pow;   /* weights divided by N^pow */
+    double force_norm_d, force_norm_f, force_norm_p;
+} mtpx_loss_settings;
+/* Host-only: the per-structure weights Trainer_MTP::AddLossGard applies
+ * (train/train_mtp.cpp:3839-3996).  has [nconf][3] flags labels present
+ * (energy, forces, stress); target_forces [N][3] (used by the force
+ * normalisation), fitness [nconf] and atomic_fitness [N] may be NULL
+ * (weight 1).  Out: active [nconf][3] (the term is part of the loss),
+ * energy_weight [nconf], force_weight [N], stress_weight [nconf]. */
+int mtpx_loss_weights(const mtpx_loss_settings *s, int nconf, const int *atom_offsets,
+                      const int *has, const double *target_forces, const double *fitness,
+                      const double *atomic_fitness, int *active, double *energy_weight,
+                      double *force_weight, double *stress_weight);
+/* MTPGpuLossRequest labels (mtp_gpu_direct.h:561-579): active [nconf][3],
+ * target_energy [nconf], energy_weight [nconf], target_forces [N][3],
+ * force_weight [N], target_stress [nconf][9], stress_weight [nconf].  Arrays
+ * of inactive terms may be NULL. */
+int mtpx_set_labels(mtpx_context *ctx, const int *active, const double *target_energy,
+                    const double *energy_weight, const double *target_forces,
+                    const double *force_weight, const double *target_stress,
+                    const double *stress_weight);
+/* MTPGpuDirect::prepare_loss: the weighted loss of the last
+ * mtpx_compute_batch outputs against the labels, summed over structures;
+ * the adjoints dL/dE, dL/dF, dL/dS stay resident.  metrics [7]: total,
+ * energy, force and stress loss, squared per-atom energy error, squared
+ * force error, squared stress error (mtp_gpu_direct.h:561-566). */
+int mtpx_prepare_loss(mtpx_context *ctx, double metrics[7]);
+/* MTPGpuDirect::accumulate_gradient / PotMTP::AccumulateEFSCombinationGard
+ * (mtp_gpu_direct.h:523-555; potentials/potential_mtp.cpp:6896-6923): the
+ * coefficient gradient [ncoef] of sum_c (dLdE_c E_c + sum_i dLdF_i . F_i +
+ * dLdS_c : S_c), in the flat order [radial | species | moment].  dLdE
+ * [nconf], dLdF [N][3], dLdS [nconf][9] (row-major 3x3); all three NULL use
+ * the adjoints of mtpx_prepare_loss.  accumulate != 0 adds to gradient.
+ * The sum is ordered: repeatable bit for bit. */
+int mtpx_accumulate_gradient(mtpx_context *ctx, const double *dLdE, const double *dLdF,
+                             const double *dLdS, int accumulate, double *gradient);
+/* PotMTP::AddPenaltyGard, radial_mode 0 (potentials/potential_mtp.cpp:
+ * 6568-6742), on the current coefficients: adds the orthonormality penalty
+ * of the radial functions and L2/L1 regularisation of the moment
+ * coefficients to *loss and grad [ncoef]. */
+int mtpx_penalty(const mtpx_context *ctx, double weight, double reg_l2, double reg_l1,
+                 double *loss, double *grad);
+/* Trainer_MTP::AccumulateGard / operator() (train/train_mtp.cpp:3039-3094,
+ * :4256-4297) over the resident batch and labels: loss = sum_c L_c / nconf
+ * + penalty, grad = sum_c g_c / nconf + penalty gradient; metrics [7] as
+ * mtpx_prepare_loss (may be NULL). */
+int mtpx_loss_grad(mtpx_context *ctx, int deterministic, double penalty_weight, double reg_l2,
+                   double reg_l1, double *loss, double *grad, double metrics[7]);
+/* Device-side timing of the last mtpx_loss_grad, milliseconds:
+ * {whole call, E/F/S, loss, gradient}. */
+int mtpx_last_train_timings(const mtpx_context *ctx, double out_ms[4]);
+
 #ifdef __cplusplus
 }
 #endif

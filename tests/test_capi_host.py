@@ -1,0 +1,132 @@
+"""Host-side C-ABI checks that need no GPU: the library loads and exports
+every entry point include/mtpx.h declares; the host-only functions (wrap,
+the .mtp parser, the loss weights) agree with the oracle; context creation
+fails cleanly without a device."""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+import oracle as O
+from helpers import rel_err
+from mtpx import capi
+from mtpx import synth as S
+
+
+def test_library_exports_every_declared_symbol():
+    L = capi.lib()
+    names = capi.declared_symbols()
+    assert len(names) >= 28
+    for name in names:
+        assert hasattr(L, name), name
+
+
+def test_create_without_device_fails_cleanly():
+    import torch
+    if torch.cuda.is_available():
+        pytest.skip("a device is present")
+    h = C.c_void_p()
+    rc = capi.lib().mtpx_create(0, C.byref(h))
+    assert rc == -5 and not h.value
+
+
+def test_wrap_is_bit_exact_against_oracle():
+    rng = S.rng_for(900)
+    for k in range(20):
+        s = S.lattice("fcc" if k % 2 else "bcc", (2, 3, 2), 3.6)
+        s = S.displace(S.strain(s, rng, 0.2), rng, 2.0)
+        cell = s.cell.copy()
+        cell[1] += 0.3 * cell[0]
+        cell[2] -= 0.2 * cell[1]
+        pos = s.pos * (1.0 + 3 * rng.random())
+        pbc = np.array([1, 1, 1], np.int32) if k % 3 else np.array([1, 0, 1], np.int32)
+        a = capi.wrap(cell, pbc, pos)
+        b = O.wrap(cell, pbc, pos)
+        assert np.array_equal(a.view(np.uint64), b.view(np.uint64))
+
+
+@pytest.mark.parametrize("name", ["shapeev-10.mtp", "shapeev-16.mtp", "shapeev-20.mtp",
+                                  "shapeev-20-t.mtp", "shapeev-06.mtp"])
+def test_parser_matches_oracle(name):
+    text = S.random_model(name, 3, 8, 2.0, 5.0, -0.1, 0.1, S.rng_for(3))
+    info, coef = capi.parse_model_text(text)
+    m = O.Model(text)
+    assert (info["Z"], info["M"], info["R"], info["K"], info["B"], info["T"], info["S"]) == \
+        (m.Z, m.M, m.R, m.K, m.B, m.T, m.S)
+    assert np.array_equal(coef, m.coeffs)
+
+
+def test_parser_defaults_match_oracle():
+    """No scaling line (default 0.01) and no coefficient lines (defaults)."""
+    text = S.read_template("shapeev-06.mtp")
+    info, coef = capi.parse_model_text(text)
+    m = O.Model(text)
+    assert np.array_equal(coef, m.coeffs)
+
+
+@pytest.mark.parametrize("bad", ["", "MTP\nversion = 1.1.0\nspecies_count = x\n",
+                                 "not an mtp file"])
+def test_parser_rejects_malformed_text(bad):
+    with pytest.raises(capi.MtpxError):
+        capi.parse_model_text(bad)
+
+
+SETTINGS = [O.LossSettings.make(),
+            O.LossSettings.make(eng_pow=2.0, force_pow=1.0, stress_pow=0.0),
+            O.LossSettings.make(force_norm_f=1.0, force_norm_p=1.5, force_norm_d=0.1)]
+
+
+@pytest.mark.parametrize("k", range(len(SETTINGS)))
+def test_loss_weights_reproduce_oracle_loss(k):
+    """mtpx_loss_weights applied to the oracle's own residuals gives the loss
+    the oracle's AddLossGard computes, structure by structure."""
+    st = SETTINGS[k]
+    text = S.random_model("shapeev-10.mtp", 2, 8, 2.0, 5.0, -0.1, 0.1, S.rng_for(31))
+    m = O.Model(text)
+    rng = S.rng_for(32)
+    structs, labels, nbs = [], [], []
+    for j in range(5):
+        s = S.displace(S.lattice("fcc", (2, 2, 1 + j % 2), 3.6), rng, 0.15)
+        s.types = (S.uniform(rng, s.n) * 2).astype(np.int32)
+        s.pos = O.wrap(s.cell, s.pbc, s.pos)
+        nb = O.Neighbors.build(s.cell, s.pbc, s.pos, s.types, m.cutoff)
+        E, F, St, _ = O.efs(m, nb)
+        lb = O.Labels(s.n, energy=E + 0.1 * (rng.random() - 0.5),
+                      forces=F + 0.05 * (rng.random((s.n, 3)) - 0.5),
+                      stress=St + 0.2 * (rng.random((3, 3)) - 0.5), fitness=0.5 + rng.random())
+        if j == 1:
+            lb.forces = None
+        if j == 2:
+            lb.stress = None
+        if j == 3:
+            lb.atomic_fitness = rng.random(s.n)
+        structs.append((s, E, F, St))
+        labels.append(lb)
+        nbs.append(nb)
+    off = np.cumsum([0] + [lb.n for lb in labels]).astype(np.int32)
+    has = np.array([[lb.energy is not None, lb.forces is not None, lb.stress is not None]
+                    for lb in labels], np.int32)
+    tf = np.concatenate([lb.forces if lb.forces is not None else np.zeros((lb.n, 3))
+                         for lb in labels])
+    af = np.concatenate([lb.atomic_fitness if lb.atomic_fitness is not None else np.ones(lb.n)
+                         for lb in labels])
+    fit = np.array([lb.fitness for lb in labels])
+    cs = capi.LossSettings.make(*[getattr(st, f[0]) for f in st._fields_])
+    active, wE, wF, wS = capi.loss_weights(cs, off, has, tf, fit, af)
+    for c, ((s, E, F, St), lb, nb) in enumerate(zip(structs, labels, nbs)):
+        loss_o, _, _ = O.add_loss_grad(m, nb, st, lb)
+        loss = 0.0
+        if active[c, 1]:
+            loss += np.sum(wF[off[c]:off[c + 1]] * np.sum((F - lb.forces) ** 2, axis=1))
+        if active[c, 2]:
+            loss += wS[c] * np.sum((St - lb.stress) ** 2)
+        if active[c, 0]:
+            loss += wE[c] * (E - lb.energy) ** 2
+        assert rel_err(loss, loss_o) < 1e-12
+
+
+def test_loss_weights_flags():
+    cs = capi.LossSettings.make(weight_stress=0.0)
+    active, wE, wF, wS = capi.loss_weights(cs, [0, 3, 3, 5], [[1, 1, 1], [1, 1, 1], [0, 1, 0]])
+    assert active.tolist() == [[1, 1, 0], [0, 0, 0], [0, 1, 0]]
+    assert wS.tolist() == [0.0, 0.0, 0.0] and wE[1] == 0.0 and wE[2] == 0.0
