@@ -1,6 +1,6 @@
 """Benchmark of the MI355X MTP E/F/S path (one GPU).
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-train]
 
 Workload (the metric's configuration): level-16 two-species MTP (radial
 basis size 8, min_dist 1.9 A, cutoff 5.0 A, coefficients U[-0.05, 0.05],
@@ -52,6 +52,109 @@ def efs_flops(model_text: str, n: int, P: int) -> float:
     return float(P) * per_pair + float(n) * per_site
 
 
+def train_flops(model_text: str, n: int, P: int) -> float:
+    """Loss+gradient per atom: E/F/S + n_i (30B + 4MR + 24) + 18T + 4S."""
+    t = S.template_topology(model_text)
+    hdr = {k: int(v) for k, v in
+           (l.strip().split(" = ") for l in model_text.splitlines()
+            if l.strip().startswith(("radial_basis_size", "radial_funcs_count")))}
+    R, M = hdr["radial_basis_size"], hdr["radial_funcs_count"]
+    B, T, Sn = len(t["basic"]), len(t["times"]), len(t["map"])
+    return efs_flops(model_text, n, P) + float(P) * (30 * B + 4 * M * R + 24) + \
+        float(n) * (18 * T + 4 * Sn)
+
+
+def training_set(nconf: int):
+    """Workload: level-20 three-species model (radial basis 10, cutoff 6.0),
+    nconf liquid configurations of 108-216 atoms at 0.06 atoms/A^3 (minimum
+    distance 1.5 A); labels are a seeded reference model's E/F/S (computed
+    by this library) plus Gaussian noise (1 meV/atom, 0.05 eV/A)."""
+    ref_text, start_text = S.training_models(5)
+    structs = S.training_structures(5, nconf)
+    for st in structs:
+        st.pos = capi.wrap(st.cell, st.pbc, st.pos)
+    return ref_text, start_text, structs
+
+
+def train_bench(ctx, steps: int, warmup: int, nconf: int):
+    ref_text, start_text, structs = training_set(nconf)
+    cutoff = 6.0
+    ctx.load_model_text(ref_text)
+    off = ctx.set_structures(structs, cutoff)
+    E, F, St, _ = ctx.compute_batch()
+    rng = S.rng_for(5, 3)
+    tE, tF, tS = [], [], []
+    for c, st in enumerate(structs):
+        e, f, sv = S.noisy_labels(rng, st.n, E[c], F[off[c]:off[c + 1]], St[c])
+        tE.append(e)
+        tF.append(f)
+        tS.append(sv)
+    tE, tF, tS = np.array(tE), np.concatenate(tF), np.array(tS)
+    ctx.load_model_text(start_text)
+    has = np.ones((nconf, 3), np.int32)
+    active, wE, wF, wS = capi.loss_weights(capi.LossSettings.make(), off, has, tF)
+    ctx.set_labels(active, tE, wE, tF, wF, tS, wS)
+    for _ in range(warmup):
+        ctx.loss_grad(penalty_weight=1e-6, reg_l2=1e-10)
+    tims = []
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        f, g, met = ctx.loss_grad(penalty_weight=1e-6, reg_l2=1e-10)
+        tims.append(ctx.last_train_timings())
+    wall = time.perf_counter() - t0
+    tims = np.array(tims)
+    n, P = ctx.neighbor_count()
+    flops = train_flops(start_text, n, P)
+    dev_ms = float(np.mean(tims[:, 0]))
+    grad_ms = float(np.mean(tims[:, 3]))
+    return {
+        "metric": "train loss+grad configs/s (lvl20, 3 species, %d liquid configs)" % nconf,
+        "value": nconf * steps / wall, "unit": "configs/s", "steps": steps, "warmup": warmup,
+        "ms_per_step": 1e3 * wall / steps,
+        "config": {"workload": "loss+gradient, level-20 MTP, 3 species, R=10, cutoff 6.0, "
+                               "%d liquid configs of 108-216 atoms, rho 0.06, d_min 1.5" % nconf,
+                   "atoms": n, "neighbor_entries": P},
+        "roofline": {"bound": "mfma", "achieved": flops / (dev_ms * 1e-3) / 1e12,
+                     "peak": FP64_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": flops / (dev_ms * 1e-3) / 1e12 / FP64_PEAK_TFLOPS, "traffic": None,
+                     "kernel": "loss+grad step (efs_kernel, loss_kernel, grad_kernel)",
+                     "device_ms": dev_ms, "efs_ms": float(np.mean(tims[:, 1])),
+                     "loss_ms": float(np.mean(tims[:, 2])), "grad_ms": grad_ms,
+                     "algorithmic_flops_per_step": flops},
+        "loss": f,
+    }, (start_text, structs, off, tE, tF, tS, cutoff)
+
+
+def train_cpu_baseline(data, budget_s: float = 12.0):
+    """The oracle's AccumulateGard restatement on the host cores, on the
+    first structures of the same batch (bounded sample)."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+
+    text, structs, off, tE, tF, tS, cutoff = data
+    threads = max(1, min(16, os.cpu_count() or 1))
+    m = O.Model(text)
+    sample = min(16, len(structs))
+    nbs, labels = [], []
+    for k in range(sample):
+        st = structs[k]
+        nbs.append(O.Neighbors.build(st.cell, st.pbc, st.pos, st.types, cutoff))
+        labels.append(O.Labels(st.n, energy=tE[k], forces=tF[off[k]:off[k + 1]], stress=tS[k]))
+    st = O.LossSettings.make()
+    O.loss_grad_batch(m, nbs, labels, st, 1e-6, 1e-10, 0.0, threads)  # warm-up
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        O.loss_grad_batch(m, nbs, labels, st, 1e-6, 1e-10, 0.0, threads)
+        reps += 1
+        el = time.perf_counter() - t0
+        if el > budget_s or reps >= 1000:
+            break
+    return {"value": reps * len(nbs) / el, "unit": "configs/s", "cores": threads, "kind": "port",
+            "sample": "%d loss+gradient passes over the first %d structures of the batch "
+                      "(oracle AccumulateGard, %d OpenMP threads, %.1f s)"
+                      % (reps, len(nbs), threads, el)}
+
+
 def cpu_baseline(model_text, cell, pbc, pos, types, budget_s: float = 12.0):
     """The oracle's getEFSOMP restatement timed on the host cores (bounded sample)."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
@@ -66,7 +169,7 @@ def cpu_baseline(model_text, cell, pbc, pos, types, budget_s: float = 12.0):
         O.efs(m, nb, threads=threads)
         reps += 1
         el = time.perf_counter() - t0
-        if el > budget_s or reps >= 50:
+        if el > budget_s or reps >= 2000:
             break
     return {"value": reps * nb.n / el, "unit": "atom-evals/s", "cores": threads, "kind": "port",
             "sample": "%d full E/F/S evaluations of the 32,000-atom cell (oracle getEFSOMP, "
@@ -80,7 +183,23 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--deterministic", action="store_true")
+    ap.add_argument("--no-train", action="store_true")
+    ap.add_argument("--train-steps", type=int, default=5)
+    ap.add_argument("--train-configs", type=int, default=1000)
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
+                    help="only copy a MIB-MiB device buffer 3 times (calibrates the HBM "
+                         "byte counters against a plain copy of known size)")
     args = ap.parse_args()
+    if args.copy_probe:
+        import torch
+        nbytes = args.copy_probe << 20
+        a = torch.ones(nbytes, dtype=torch.uint8, device="cuda")
+        b = torch.empty_like(a)
+        for _ in range(3):
+            b.copy_(a)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_probe_bytes": nbytes, "copies": 3}))
+        return
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path "
               "(see DESIGN.md for how it would shard)", file=sys.stderr)
@@ -116,6 +235,9 @@ def main():
         ctx.efs_device(det)
         tot.append(time.perf_counter() - t1)
     E, F, St, _ = ctx.efs(det)
+    train = None
+    if not args.no_train:
+        train, tdata = train_bench(ctx, args.train_steps, 1, args.train_configs)
     ctx.close()
 
     flops = efs_flops(model_text, n, P)
@@ -150,11 +272,14 @@ def main():
                              "78.6 TFLOP/s"},
         "extra": {"total_ms_build_plus_efs": 1e3 * float(np.median(tot)),
                   "neighbor_build_first_ms": 1e3 * nbuild_first,
-                  "energy": E, "max_abs_force": float(np.abs(F).max()),
-                  "train_loss_grad_configs_per_s": None},
+                  "energy": E, "max_abs_force": float(np.abs(F).max())},
     }
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(model_text, s.cell, s.pbc, pos, s.types)
+    if train is not None:
+        if not args.no_cpu:
+            train["cpu_baseline"] = train_cpu_baseline(tdata)
+        out["train"] = train
     print(json.dumps(out))
 
 
