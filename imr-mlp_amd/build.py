@@ -30,11 +30,13 @@ COMMON = ["-O3", "-std=c++17", "-fPIC", "--offload-arch=" + ARCH, "-munsafe-fp-a
 SOURCES = [
     ("efs_kernel.hip", ["-ffp-contract=fast"]),
     ("train_kernel.hip", ["-ffp-contract=fast"]),
+    ("lin_kernel.hip", ["-ffp-contract=fast"]),
     ("neighbors.hip", ["-ffp-contract=off"]),
     ("geometry.cpp", ["-ffp-contract=off"]),
     ("model.cpp", ["-ffp-contract=off"]),
     ("capi.cpp", ["-ffp-contract=off"]),
     ("train_api.cpp", ["-ffp-contract=off"]),
+    ("linear_api.cpp", ["-ffp-contract=off"]),
 ]
 
 

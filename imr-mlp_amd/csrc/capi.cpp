@@ -115,6 +115,33 @@ int install_model(mtpx_context *ctx, Model &&m)
     EfsLaunch probe;
     if (!efs_configure(dm, 1, 1, 0, ctx->lds_limit, probe))
         return set_error(ctx, MTPX_E_CAPACITY, "model needs more LDS than a CU provides");
+    // linear-fit plan: optional (the linear entry points report its error)
+    ctx->has_lin = build_lin_plan(M, P, ctx->lin, ctx->lin_err);
+    if (ctx->has_lin) {
+        const LinPlan &lp = ctx->lin;
+        HIP_TRY(upload(ctx->lin_level, lp.level_step, s), "upload model");
+        HIP_TRY(upload(ctx->lin_steps, lp.steps, s), "upload model");
+        HIP_TRY(upload(ctx->lin_lcomb, lp.level_comb, s), "upload model");
+        HIP_TRY(upload(ctx->lin_comb, lp.comb, s), "upload model");
+        HIP_TRY(upload(ctx->lin_ent, lp.ent, s), "upload model");
+        HIP_TRY(upload(ctx->lin_estart, lp.ent_start, s), "upload model");
+        DevLin &L = ctx->dl;
+        L.nL = lp.nL;
+        L.one = lp.one;
+        L.L0 = lp.L0;
+        L.part0 = lp.part0;
+        L.acc = lp.acc;
+        L.priv = lp.priv;
+        L.CH = lp.CH;
+        L.nchunks = lp.nchunks;
+        L.nlev = (int)lp.level_step.size() - 1;
+        L.level_step = ctx->lin_level.as<int>();
+        L.level_comb = ctx->lin_lcomb.as<int>();
+        L.steps = ctx->lin_steps.as<int2>();
+        L.comb = ctx->lin_comb.as<int4>();
+        L.ent = ctx->lin_ent.as<int2>();
+        L.ent_start = ctx->lin_estart.as<int>();
+    }
     int rc = upload_coeffs(ctx);
     if (rc != MTPX_OK)
         return rc;

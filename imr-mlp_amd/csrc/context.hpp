@@ -52,6 +52,18 @@ struct mtpx_context {
     DBuf active, tE, wE, tF, wF, tS, wS;
     DBuf dLdE, dLdF, dLdS, metric_rows, metrics, grad_rows, grad;
     NeighborStore nbh_tmp;
+    // host copies of the labels (linear-fit rows)
+    std::vector<int> active_h;
+    std::vector<double> tE_h, wE_h, tF_h, wF_h, tS_h, wS_h;
+
+    // linear fit: plan, components [fc | sc | ec], row descriptors, Gram
+    bool has_lin = false;
+    std::string lin_err;
+    LinPlan lin;
+    DevLin dl{};
+    DBuf lin_level, lin_steps, lin_lcomb, lin_comb, lin_ent, lin_estart;
+    DBuf comp, row_src, row_sw, row_y, rowsA, rowsY, gram_part, gram_out;
+    double lin_timings[4] = {0, 0, 0, 0};
     double train_timings[4] = {0, 0, 0, 0};
     hipEvent_t tev[4] = {nullptr, nullptr, nullptr, nullptr};
 
@@ -68,7 +80,9 @@ struct mtpx_context {
                         &bstress, &active, &tE, &wE, &tF, &wF, &tS, &wS, &dLdE, &dLdF, &dLdS,
                         &metric_rows, &metrics, &grad_rows, &grad, &nbh_tmp.offsets,
                         &nbh_tmp.idx, &nbh_tmp.type, &nbh_tmp.x, &nbh_tmp.y, &nbh_tmp.z,
-                        &nbh_tmp.d, &nbh_tmp.center_type})
+                        &nbh_tmp.d, &nbh_tmp.center_type, &lin_level, &lin_steps, &lin_lcomb,
+                        &lin_comb, &lin_ent, &lin_estart, &comp, &row_src, &row_sw, &row_y,
+                        &rowsA, &rowsY, &gram_part, &gram_out})
             b->release();
         scratch.release_all();
         for (auto &e : ev)

@@ -1,0 +1,294 @@
+// C ABI, linear-fit part (include/mtpx.h): E/F/S components of the linear
+// coefficients, the weighted design rows and the normal equations of the
+// linear fit, and the orthogonalisation of the radial functions.  Host
+// code; no exceptions escape.
+#include "context.hpp"
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+
+namespace {
+
+struct CompLayout {
+    int p;
+    size_t fc, sc, ec, total;  // offsets in doubles
+};
+
+CompLayout comp_layout(const mtpx_context *ctx)
+{
+    CompLayout l;
+    l.p = ctx->model.Z + ctx->model.S;
+    l.fc = 0;
+    l.sc = (size_t)ctx->n * 3 * l.p;
+    l.ec = l.sc + (size_t)ctx->nconf * 9 * l.p;
+    l.total = l.ec + (size_t)ctx->nconf * l.p;
+    return l;
+}
+
+// Components of every structure of the resident topology into ctx->comp.
+int run_lin(mtpx_context *ctx)
+{
+    if (!ctx->has_model)
+        return set_error(ctx, MTPX_E_NO_MODEL, "no model loaded");
+    if (!ctx->has_nbh)
+        return set_error(ctx, MTPX_E_NO_TOPOLOGY, "no neighbour lists");
+    if (int rc = check_species(ctx))
+        return rc;
+    if (!ctx->has_lin)
+        return set_error(ctx, MTPX_E_MODEL, "linear fit unavailable: " + ctx->lin_err);
+    const CompLayout cl = comp_layout(ctx);
+    hipStream_t s = ctx->stream;
+    HIP_TRY(ctx->comp.ensure(sizeof(double) * std::max<size_t>(cl.total, 1)),
+            "allocate components");
+    if (cl.total)
+        HIP_TRY(hipMemsetAsync(ctx->comp.p, 0, sizeof(double) * cl.total, s), "clear components");
+    if (ctx->n == 0)
+        return MTPX_OK;
+    EfsLaunch cfg;
+    if (!lin_configure(ctx->dm, ctx->dl, ctx->n, ctx->num_cus, ctx->lds_limit, cfg))
+        return set_error(ctx, MTPX_E_CAPACITY,
+                         "model needs more LDS than a CU provides for the linear fit");
+    LinOut out;
+    double *comp = ctx->comp.as<double>();
+    out.center_structure = ctx->center_structure.as<int>();
+    out.fc = comp + cl.fc;
+    out.sc = comp + cl.sc;
+    out.ec = comp + cl.ec;
+    HIP_TRY(launch_lin_site(ctx->dm, ctx->dl, dev_neighbors(ctx), out, cfg, s),
+            "launch linear-fit kernel");
+    return MTPX_OK;
+}
+
+// AddLinearFast (train/train_mtp.cpp:1289-1395) row order per structure:
+// force rows of the atoms with a positive weight (x, y, z), the 9 stress
+// rows, the energy row; each scaled by sqrt(w), targets likewise.
+int build_rows(mtpx_context *ctx, int64_t &R)
+{
+    if (!ctx->has_labels)
+        return set_error(ctx, MTPX_E_INVALID, "no labels");
+    const CompLayout cl = comp_layout(ctx);
+    std::vector<int64_t> src;
+    std::vector<double> sw, yw;
+    for (int c = 0; c < ctx->nconf; ++c) {
+        const int a0 = ctx->soff_host[c], a1 = ctx->soff_host[c + 1];
+        const int *act = &ctx->active_h[3 * (size_t)c];
+        if (act[1])
+            for (int i = a0; i < a1; ++i) {
+                if (!(ctx->wF_h[i] > 0))
+                    continue;
+                const double w = std::sqrt(ctx->wF_h[i]);
+                for (int a = 0; a < 3; ++a) {
+                    src.push_back((int64_t)(cl.fc + ((size_t)i * 3 + a) * cl.p));
+                    sw.push_back(w);
+                    yw.push_back(w * ctx->tF_h[3 * (size_t)i + a]);
+                }
+            }
+        if (act[2]) {
+            const double w = std::sqrt(ctx->wS_h[c]);
+            for (int q = 0; q < 9; ++q) {
+                src.push_back((int64_t)(cl.sc + ((size_t)c * 9 + q) * cl.p));
+                sw.push_back(w);
+                yw.push_back(w * ctx->tS_h[9 * (size_t)c + q]);
+            }
+        }
+        if (act[0]) {
+            const double w = std::sqrt(ctx->wE_h[c]);
+            src.push_back((int64_t)(cl.ec + (size_t)c * cl.p));
+            sw.push_back(w);
+            yw.push_back(w * ctx->tE_h[c]);
+        }
+    }
+    R = (int64_t)src.size();
+    HIP_TRY(upload(ctx->row_src, src, ctx->stream), "upload rows");
+    HIP_TRY(upload(ctx->row_sw, sw, ctx->stream), "upload rows");
+    HIP_TRY(upload(ctx->row_y, yw, ctx->stream), "upload rows");
+    return MTPX_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int mtpx_efs_components(mtpx_context *ctx, double *energy_cmpts, double *force_cmpts,
+                        double *stress_cmpts)
+{
+    if (!ctx)
+        return MTPX_E_INVALID;
+    (void)hipSetDevice(ctx->device);
+    int rc = run_lin(ctx);
+    if (rc != MTPX_OK)
+        return rc;
+    const CompLayout cl = comp_layout(ctx);
+    const double *comp = ctx->comp.as<double>();
+    HIP_TRY(hipStreamSynchronize(ctx->stream), "components");
+    if (force_cmpts && cl.sc > cl.fc)
+        HIP_TRY(hipMemcpy(force_cmpts, comp + cl.fc, sizeof(double) * (cl.sc - cl.fc),
+                          hipMemcpyDeviceToHost),
+                "copy force components");
+    if (stress_cmpts && cl.ec > cl.sc)
+        HIP_TRY(hipMemcpy(stress_cmpts, comp + cl.sc, sizeof(double) * (cl.ec - cl.sc),
+                          hipMemcpyDeviceToHost),
+                "copy stress components");
+    if (energy_cmpts && cl.total > cl.ec)
+        HIP_TRY(hipMemcpy(energy_cmpts, comp + cl.ec, sizeof(double) * (cl.total - cl.ec),
+                          hipMemcpyDeviceToHost),
+                "copy energy components");
+    return MTPX_OK;
+}
+
+int mtpx_linear_rows(mtpx_context *ctx, int64_t *nrows, double *A, double *y)
+{
+    if (!ctx || !nrows)
+        return set_error(ctx, MTPX_E_INVALID, "null argument");
+    if (!ctx->has_nbh)
+        return set_error(ctx, MTPX_E_NO_TOPOLOGY, "no structures");
+    if (!ctx->has_model)
+        return set_error(ctx, MTPX_E_NO_MODEL, "no model loaded");
+    (void)hipSetDevice(ctx->device);
+    int64_t R = 0;
+    int rc = build_rows(ctx, R);
+    if (rc != MTPX_OK)
+        return rc;
+    if (!A && !y) {
+        *nrows = R;
+        return MTPX_OK;
+    }
+    if (!A || !y)
+        return set_error(ctx, MTPX_E_INVALID, "A and y are both needed");
+    if (*nrows < R)
+        return set_error(ctx, MTPX_E_RANGE, "row buffer too small");
+    rc = run_lin(ctx);
+    if (rc != MTPX_OK)
+        return rc;
+    const int p = ctx->model.Z + ctx->model.S;
+    HIP_TRY(ctx->rowsA.ensure(sizeof(double) * std::max<int64_t>(R * p, 1)), "allocate rows");
+    HIP_TRY(ctx->rowsY.ensure(sizeof(double) * std::max<int64_t>(R, 1)), "allocate rows");
+    HIP_TRY(launch_lin_rows(ctx->comp.as<double>(), ctx->row_src.as<int64_t>(),
+                            ctx->row_sw.as<double>(), ctx->row_y.as<double>(), R, p,
+                            ctx->rowsA.as<double>(), ctx->rowsY.as<double>(), ctx->stream),
+            "launch rows");
+    HIP_TRY(hipStreamSynchronize(ctx->stream), "rows");
+    if (R > 0) {
+        HIP_TRY(hipMemcpy(A, ctx->rowsA.p, sizeof(double) * R * p, hipMemcpyDeviceToHost),
+                "copy rows");
+        HIP_TRY(hipMemcpy(y, ctx->rowsY.p, sizeof(double) * R, hipMemcpyDeviceToHost),
+                "copy targets");
+    }
+    *nrows = R;
+    return MTPX_OK;
+}
+
+int mtpx_linear_system(mtpx_context *ctx, double *G, double *b)
+{
+    if (!ctx || !G || !b)
+        return set_error(ctx, MTPX_E_INVALID, "null argument");
+    if (!ctx->has_nbh)
+        return set_error(ctx, MTPX_E_NO_TOPOLOGY, "no structures");
+    if (!ctx->has_model)
+        return set_error(ctx, MTPX_E_NO_MODEL, "no model loaded");
+    (void)hipSetDevice(ctx->device);
+    int64_t R = 0;
+    int rc = build_rows(ctx, R);
+    if (rc != MTPX_OK)
+        return rc;
+    hipStream_t s = ctx->stream;
+    for (auto &e : ctx->tev)
+        if (!e)
+            HIP_TRY(hipEventCreate(&e), "create events");
+    HIP_TRY(hipEventRecord(ctx->tev[0], s), "record event");
+    rc = run_lin(ctx);
+    if (rc != MTPX_OK)
+        return rc;
+    HIP_TRY(hipEventRecord(ctx->tev[1], s), "record event");
+    const int p = ctx->model.Z + ctx->model.S;
+    const int pp = gram_padded(p);
+    HIP_TRY(ctx->gram_out.ensure(sizeof(double) * pp * pp), "allocate Gram");
+    if (R == 0) {
+        HIP_TRY(hipMemsetAsync(ctx->gram_out.p, 0, sizeof(double) * pp * pp, s), "clear Gram");
+    } else {
+        const int nblocks =
+            (int)std::max<int64_t>(1, std::min<int64_t>((R + 255) / 256, 4LL * ctx->num_cus));
+        HIP_TRY(ctx->gram_part.ensure(sizeof(double) * (size_t)nblocks * pp * pp),
+                "allocate Gram partials");
+        HIP_TRY(launch_gram(ctx->comp.as<double>(), ctx->row_src.as<int64_t>(),
+                            ctx->row_sw.as<double>(), ctx->row_y.as<double>(), R, p, nblocks,
+                            ctx->gram_part.as<double>(), s),
+                "launch Gram");
+        HIP_TRY(hipEventRecord(ctx->tev[2], s), "record event");
+        HIP_TRY(launch_rows_reduce(ctx->gram_part.as<double>(), nblocks, pp * pp,
+                                   ctx->gram_out.as<double>(), false, s),
+                "launch Gram reduction");
+    }
+    std::vector<double> g((size_t)pp * pp);
+    HIP_TRY(hipMemcpyAsync(g.data(), ctx->gram_out.p, sizeof(double) * pp * pp,
+                           hipMemcpyDeviceToHost, s),
+            "copy Gram");
+    HIP_TRY(hipEventRecord(ctx->tev[3], s), "record event");
+    HIP_TRY(hipStreamSynchronize(s), "Gram");
+    float t03 = 0, t01 = 0, t12 = 0;
+    (void)hipEventElapsedTime(&t03, ctx->tev[0], ctx->tev[3]);
+    (void)hipEventElapsedTime(&t01, ctx->tev[0], ctx->tev[1]);
+    if (R > 0)
+        (void)hipEventElapsedTime(&t12, ctx->tev[1], ctx->tev[2]);
+    ctx->lin_timings[0] = t03;
+    ctx->lin_timings[1] = t01;
+    ctx->lin_timings[2] = t12;
+    ctx->lin_timings[3] = (double)R;
+    for (int i = 0; i < p; ++i) {
+        for (int j = 0; j < p; ++j)
+            G[(size_t)i * p + j] = g[(size_t)i * pp + j];
+        b[i] = g[(size_t)i * pp + p];
+    }
+    return MTPX_OK;
+}
+
+// PotMTP::Orthogonalize (potentials/potential_mtp.cpp:3849-3930): for each
+// radial function k, subtract from c_k its projection on every earlier c_k2
+// -- divided by |c_k|^2, the reference's choice, not |c_k2|^2 -- then
+// normalise with sqrt(sum (c^2 + 1e-10)).  Vectors run over (ti, tj, k).
+int mtpx_orthogonalize(mtpx_context *ctx)
+{
+    if (!ctx)
+        return MTPX_E_INVALID;
+    if (!ctx->has_model)
+        return set_error(ctx, MTPX_E_NO_MODEL, "no model loaded");
+    Model &m = ctx->model;
+    const int Z = m.Z, M = m.M, R = m.R;
+    std::vector<double> x(m.coef);
+    double *c = x.data();
+    auto at = [&](int pair, int mu, int k) { return (size_t)pair * M * R + (size_t)mu * R + k; };
+    for (int k = 0; k < M; ++k) {
+        for (int k2 = 0; k2 < k; ++k2) {
+            double norm = 0.0, scal = 0.0;
+            for (int pr = 0; pr < Z * Z; ++pr)
+                for (int l = 0; l < R; ++l)
+                    norm += c[at(pr, k, l)] * c[at(pr, k, l)];
+            for (int pr = 0; pr < Z * Z; ++pr)
+                for (int l = 0; l < R; ++l)
+                    scal += c[at(pr, k, l)] * c[at(pr, k2, l)];
+            for (int pr = 0; pr < Z * Z; ++pr)
+                for (int l = 0; l < R; ++l)
+                    c[at(pr, k, l)] -= c[at(pr, k2, l)] * scal / norm;
+        }
+        double norm = 0.0;
+        for (int pr = 0; pr < Z * Z; ++pr)
+            for (int l = 0; l < R; ++l)
+                norm += c[at(pr, k, l)] * c[at(pr, k, l)] + 1e-10;
+        norm = std::sqrt(norm);
+        for (int pr = 0; pr < Z * Z; ++pr)
+            for (int l = 0; l < R; ++l)
+                c[at(pr, k, l)] /= norm;
+    }
+    return mtpx_set_coeffs(ctx, x.data());
+}
+
+int mtpx_last_linear_timings(const mtpx_context *ctx, double out[4])
+{
+    if (!ctx || !out)
+        return MTPX_E_INVALID;
+    std::memcpy(out, ctx->lin_timings, sizeof ctx->lin_timings);
+    return MTPX_OK;
+}
+
+}  // extern "C"

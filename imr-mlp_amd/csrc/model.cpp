@@ -8,6 +8,8 @@
 // optional species/moment coefficients (default 1e-3, :471-474).
 #include "mtpx_internal.hpp"
 
+#include <iterator>
+
 #include <algorithm>
 #include <array>
 #include <cmath>
@@ -98,6 +100,103 @@ bool fail(std::string &err, const char *msg)
 {
     err = msg;
     return false;
+}
+
+// ---- lane-major step tables (shared by the rule plans) -------------------
+// A step entry before encoding: {l, r, c, w, first}; w >= 0 is the task's
+// target, w <= -2 partial -w - 2.
+using Ent = std::array<int, 5>;
+using Task = std::vector<Ent>;
+struct RawTables {
+    std::vector<Ent> steps;                 // lane-major
+    std::vector<int> level_step;            // per level: first step
+    std::vector<std::array<int, 3>> comb;   // {target, first partial, count}
+    std::vector<int> level_comb;
+    int max_partials = 0;
+    RawTables() : level_step{0}, level_comb{0} {}
+};
+
+// One dependency level: split tasks longer than the fair share (entries /
+// 64) into pieces ending in partial sums, spread the pieces over the 64
+// lanes by longest-processing-time, pad to a multiple of 4 steps.
+void emit_level(std::vector<Task> &tasks, RawTables &raw)
+{
+    size_t total = 0;
+    for (auto &t : tasks)
+        total += t.size();
+    const size_t cap = std::max<size_t>(4, (total + kWave - 1) / kWave);
+    std::vector<Task> pieces;
+    int npart = 0;
+    for (auto &t : tasks) {
+        if (t.size() <= cap) {
+            pieces.push_back(t);
+            continue;
+        }
+        const int target = t[0][3];
+        const int first = npart;
+        for (size_t b0 = 0; b0 < t.size(); b0 += cap) {
+            Task piece(t.begin() + b0, t.begin() + std::min(t.size(), b0 + cap));
+            for (Ent &e : piece)
+                e[3] = -2 - npart;
+            piece[0][4] = 1;
+            ++npart;
+            pieces.push_back(std::move(piece));
+        }
+        raw.comb.push_back({target, first, npart - first});
+    }
+    raw.max_partials = std::max(raw.max_partials, npart);
+    raw.level_comb.push_back((int)raw.comb.size());
+    std::vector<int> order(pieces.size());
+    for (size_t i = 0; i < order.size(); ++i)
+        order[i] = (int)i;
+    std::stable_sort(order.begin(), order.end(),
+                     [&](int a, int b) { return pieces[a].size() > pieces[b].size(); });
+    std::vector<Task> lane(kWave);
+    std::vector<size_t> load(kWave, 0);
+    for (int t : order) {
+        int q = (int)(std::min_element(load.begin(), load.end()) - load.begin());
+        lane[q].insert(lane[q].end(), pieces[t].begin(), pieces[t].end());
+        load[q] += pieces[t].size();
+    }
+    size_t nst = *std::max_element(load.begin(), load.end());
+    nst = (nst + 3) & ~size_t(3);
+    const size_t base = raw.steps.size() / kWave;
+    raw.steps.resize((base + nst) * kWave, Ent{-1, -1, 0, -1, 1});  // padding
+    for (int q = 0; q < kWave; ++q)
+        for (size_t st = 0; st < lane[q].size(); ++st)
+            raw.steps[(base + st) * kWave + q] = lane[q][st];
+    raw.level_step.push_back((int)(base + nst));
+}
+
+// Encodes raw entries into int2 work-space steps: x = l | r << 16,
+// y = w | first << 16 | c << 17.  map_l / map_r / map_w translate raw
+// operands and targets to work-space indices; partial p goes to part0 + p
+// and padding reads and writes `dummy`.
+template <class ML, class MR, class MW>
+void encode_tables(const RawTables &raw, int part0, int dummy, ML map_l, MR map_r, MW map_w,
+                   std::vector<int> &steps, std::vector<int> &level_step, std::vector<int> &comb,
+                   std::vector<int> &level_comb)
+{
+    auto target = [&](int w) { return w <= -2 ? part0 + (-w - 2) : map_w(w); };
+    steps.assign(raw.steps.size() * 2, 0);
+    for (size_t i = 0; i < raw.steps.size(); ++i) {
+        const Ent &e = raw.steps[i];
+        int l, r, w;
+        if (e[0] < 0) {
+            l = r = w = dummy;
+        } else {
+            l = map_l(e[0]);
+            r = map_r(e[1]);
+            w = target(e[3]);
+        }
+        steps[2 * i] = l | (r << 16);
+        steps[2 * i + 1] = w | (e[4] << 16) | (int)((unsigned)e[2] << 17);
+    }
+    level_step = raw.level_step;
+    level_comb = raw.level_comb;
+    comb.clear();
+    for (auto &c : raw.comb)
+        comb.insert(comb.end(), {target(c[0]), part0 + c[1], c[2], 0});
 }
 
 }  // namespace
@@ -399,73 +498,11 @@ bool build_plan(const Model &m, Plan &p, std::string &err)
     p.dummy = 2 * K4;
     p.part0 = 2 * K4 + 4;
 
-    // A step entry before encoding: {l, r, c, w, first}; w >= 0 is the
-    // task's target (moment or adjoint index), w <= -2 partial -w - 2.
-    using Ent = std::array<int, 5>;
-    using Task = std::vector<Ent>;
-    struct Raw {
-        std::vector<Ent> steps;          // lane-major
-        std::vector<int> level_step;     // per level: first step
-        std::vector<std::array<int, 3>> comb;  // {target, first partial, count}
-        std::vector<int> level_comb;
-    };
-    auto emit_level = [&p](std::vector<Task> &tasks, Raw &raw) {
-        size_t total = 0;
-        for (auto &t : tasks)
-            total += t.size();
-        const size_t cap = std::max<size_t>(4, (total + kWave - 1) / kWave);
-        // split long tasks into pieces that end in partial sums
-        std::vector<Task> pieces;
-        int npart = 0;
-        for (auto &t : tasks) {
-            if (t.size() <= cap) {
-                pieces.push_back(t);
-                continue;
-            }
-            const int target = t[0][3];
-            const int first = npart;
-            for (size_t b0 = 0; b0 < t.size(); b0 += cap) {
-                Task piece(t.begin() + b0, t.begin() + std::min(t.size(), b0 + cap));
-                for (Ent &e : piece)
-                    e[3] = -2 - npart;
-                piece[0][4] = 1;
-                ++npart;
-                pieces.push_back(std::move(piece));
-            }
-            raw.comb.push_back({target, first, npart - first});
-        }
-        p.max_partials = std::max(p.max_partials, npart);
-        raw.level_comb.push_back((int)raw.comb.size());
-        // longest-processing-time assignment of pieces to the 64 lanes
-        std::vector<int> order(pieces.size());
-        for (size_t i = 0; i < order.size(); ++i)
-            order[i] = (int)i;
-        std::stable_sort(order.begin(), order.end(),
-                         [&](int a, int b) { return pieces[a].size() > pieces[b].size(); });
-        std::vector<Task> lane(kWave);
-        std::vector<size_t> load(kWave, 0);
-        for (int t : order) {
-            int q = (int)(std::min_element(load.begin(), load.end()) - load.begin());
-            lane[q].insert(lane[q].end(), pieces[t].begin(), pieces[t].end());
-            load[q] += pieces[t].size();
-        }
-        size_t nst = *std::max_element(load.begin(), load.end());
-        nst = (nst + 3) & ~size_t(3);
-        const size_t base = raw.steps.size() / kWave;
-        raw.steps.resize((base + nst) * kWave, Ent{-1, -1, 0, -1, 1});  // padding
-        for (int q = 0; q < kWave; ++q)
-            for (size_t st = 0; st < lane[q].size(); ++st)
-                raw.steps[(base + st) * kWave + q] = lane[q][st];
-        raw.level_step.push_back((int)(base + nst));
-    };
-
     // Forward: outputs of each level, an output's rules in file order.
     std::vector<std::vector<int>> by_out((size_t)m.K);
     for (int t = 0; t < m.T; ++t)
         by_out[m.times[4 * t + 3]].push_back(t);
-    Raw fwd, bwd;
-    fwd.level_step.push_back(0);
-    fwd.level_comb.push_back(0);
+    RawTables fwd, bwd;
     for (int L = 1; L <= maxl; ++L) {
         std::vector<Task> tasks;
         for (int o = 0; o < m.K; ++o) {
@@ -492,8 +529,6 @@ bool build_plan(const Model &m, Plan &p, std::string &err)
         ent[r[1]].push_back({r[3], r[0], r[2], r[1], 0});
         ent[r[0]].push_back({r[3], r[1], r[2], r[0], 0});
     }
-    bwd.level_step.push_back(0);
-    bwd.level_comb.push_back(0);
     for (int L = maxl - 1; L >= 0; --L) {
         std::vector<Task> tasks;
         for (int x = 0; x < m.K; ++x) {
@@ -507,6 +542,7 @@ bool build_plan(const Model &m, Plan &p, std::string &err)
     }
 
     // Encode against the private layout (indices in doubles).
+    p.max_partials = std::max(fwd.max_partials, bwd.max_partials);
     const int P4 = (p.max_partials + 3) & ~3;
     p.red0 = p.part0 + P4;
     const int N4 = (p.nslots + 3) & ~3;
@@ -516,36 +552,12 @@ bool build_plan(const Model &m, Plan &p, std::string &err)
     for (int t = 0; t < m.T; ++t)
         if (m.times[4 * t + 2] < -16384 || m.times[4 * t + 2] > 16383)
             return fail(err, "product-rule multiplicity outside [-16384, 16383]");
-    auto encode = [&p](const Raw &raw, bool reverse, std::vector<int> &steps,
-                       std::vector<int> &level_step, std::vector<int> &comb,
-                       std::vector<int> &level_comb) {
-        auto target = [&](int w) {
-            if (w <= -2)
-                return p.part0 + (-w - 2);
-            return reverse ? p.K4 + w : w;
-        };
-        steps.assign(raw.steps.size() * 2, 0);
-        for (size_t i = 0; i < raw.steps.size(); ++i) {
-            const Ent &e = raw.steps[i];
-            int l, r, w;
-            if (e[0] < 0) {
-                l = r = w = p.dummy;
-            } else {
-                l = reverse ? p.K4 + e[0] : e[0];
-                r = e[1];
-                w = target(e[3]);
-            }
-            steps[2 * i] = l | (r << 16);
-            steps[2 * i + 1] = w | (e[4] << 16) | (int)((unsigned)e[2] << 17);
-        }
-        level_step = raw.level_step;
-        level_comb = raw.level_comb;
-        comb.clear();
-        for (auto &c : raw.comb)
-            comb.insert(comb.end(), {target(c[0]), p.part0 + c[1], c[2], 0});
-    };
-    encode(fwd, false, p.fwd_steps, p.fwd_level_step, p.fwd_comb, p.fwd_level_comb);
-    encode(bwd, true, p.bwd_steps, p.bwd_level_step, p.bwd_comb, p.bwd_level_comb);
+    auto same = [](int x) { return x; };
+    auto adj = [&p](int x) { return p.K4 + x; };
+    encode_tables(fwd, p.part0, p.dummy, same, same, same, p.fwd_steps, p.fwd_level_step,
+                  p.fwd_comb, p.fwd_level_comb);
+    encode_tables(bwd, p.part0, p.dummy, adj, same, adj, p.bwd_steps, p.bwd_level_step,
+                  p.bwd_comb, p.bwd_level_comb);
 
     // Training work space: the E/F/S work space, its dual copy (tangents and
     // second adjoints), a transpose buffer, the slot-ordered adjoint staging
@@ -557,6 +569,135 @@ bool build_plan(const Model &m, Plan &p, std::string &err)
     p.tr_grad = p.tr_stage + 5 * N4;
     p.tr_ctype = p.tr_grad + ((m.ncoef() + 3) & ~3);
     p.tr_priv = p.tr_ctype + kWave / 2;  // 64 ints: neighbour species of a batch
+    return true;
+}
+
+// Linear-fit plan.  The scalar moments are polynomials in the basic moments,
+// so dm_s/dr_j = sum_b L[s][b] grad_r(f_b Y_b)(r_j) with the sparse site
+// Jacobian L[x][b] = dm_x/dm_b.  Its support follows the rules:
+// supp(o) = union of supp(l), supp(r); its values follow
+//   L[o][b] = sum_rules c (m_r L[l][b] + m_l L[r][b]),
+// which is a step table of the same form as the rule tables (each entry adds
+// c * ws[m index] * ws[L index]).  Duplicated basics count as their first
+// occurrence.
+bool build_lin_plan(const Model &m, const Plan &p, LinPlan &lp, std::string &err)
+{
+    lp = LinPlan();
+    const int K = m.K, B = m.B;
+    std::vector<int> canon((size_t)B);
+    for (int b = 0; b < B; ++b)
+        canon[b] = b;
+    for (size_t k = 0; k + 1 < p.dup.size(); k += 2)
+        canon[p.dup[k]] = p.dup[k + 1];
+    std::vector<int> slot_of((size_t)B, -1);
+    for (int s = 0; s < p.nslots; ++s)
+        if (p.slot_basic[s] >= 0)
+            slot_of[p.slot_basic[s]] = s;
+    std::vector<std::vector<int>> supp((size_t)K);
+    for (int b = 0; b < B; ++b)
+        supp[b] = {canon[b]};
+    std::vector<int> level((size_t)K, 0);
+    for (int t = 0; t < m.T; ++t) {
+        const int *r = &m.times[4 * t];
+        std::vector<int> u;
+        std::set_union(supp[r[0]].begin(), supp[r[0]].end(), supp[r[1]].begin(),
+                       supp[r[1]].end(), std::back_inserter(u));
+        std::vector<int> v;
+        std::set_union(supp[r[3]].begin(), supp[r[3]].end(), u.begin(), u.end(),
+                       std::back_inserter(v));
+        supp[r[3]].swap(v);
+        level[r[3]] = std::max(level[r[3]], 1 + std::max(level[r[0]], level[r[1]]));
+    }
+    // moments the scalars depend on
+    std::vector<char> need((size_t)K, 0);
+    for (int s = 0; s < m.S; ++s)
+        need[m.map[s]] = 1;
+    for (int t = m.T - 1; t >= 0; --t) {
+        const int *r = &m.times[4 * t];
+        if (need[r[3]])
+            need[r[0]] = need[r[1]] = 1;
+    }
+    // work-space layout (doubles): E/F/S block, transpose buffer, one, L
+    lp.one = p.red0 + kChunk * kRedStride;
+    lp.L0 = lp.one + 4;
+    std::vector<int> lbase((size_t)K, -1);
+    int nL = 0;
+    for (int x = B; x < K; ++x)
+        if (need[x]) {
+            lbase[x] = nL;
+            nL += (int)supp[x].size();
+        }
+    lp.nL = nL;
+    auto lws = [&](int x, int b) {  // work-space index of L[x][b], -1 outside the support
+        if (x < B)
+            return canon[x] == b ? lp.one : -1;
+        const auto &sx = supp[x];
+        auto it = std::lower_bound(sx.begin(), sx.end(), b);
+        if (it == sx.end() || *it != b)
+            return -1;
+        return lp.L0 + lbase[x] + (int)(it - sx.begin());
+    };
+    std::vector<std::vector<int>> by_out((size_t)K);
+    for (int t = 0; t < m.T; ++t)
+        by_out[m.times[4 * t + 3]].push_back(t);
+    RawTables raw;
+    for (int L = 1; L <= p.max_level; ++L) {
+        std::vector<Task> tasks;
+        for (int o = B; o < K; ++o) {
+            if (level[o] != L || !need[o] || by_out[o].empty())
+                continue;
+            for (int b : supp[o]) {
+                Task task;
+                for (int t : by_out[o]) {
+                    const int *r = &m.times[4 * t];
+                    const int ll = lws(r[0], b), lr = lws(r[1], b);
+                    if (ll >= 0)
+                        task.push_back({r[1], ll, r[2], lws(o, b), 0});
+                    if (lr >= 0)
+                        task.push_back({r[0], lr, r[2], lws(o, b), 0});
+                }
+                if (task.empty())
+                    continue;
+                task[0][4] = 1;
+                tasks.push_back(std::move(task));
+            }
+        }
+        emit_level(tasks, raw);
+    }
+    lp.part0 = lp.L0 + ((nL + 3) & ~3);
+    const int P4 = (raw.max_partials + 3) & ~3;
+    lp.acc = lp.part0 + P4;
+    lp.CH = 16;
+    lp.acc_rows = 3 * lp.CH;
+    lp.priv = lp.acc + lp.acc_rows * kRedStride;
+    lp.priv = (lp.priv + 3) & ~3;
+    if (lp.acc > 0xffff)
+        return fail(err, "model too large for the linear-fit work space");
+    auto same = [](int x) { return x; };
+    encode_tables(raw, lp.part0, p.dummy, same, same, same, lp.steps, lp.level_step, lp.comb,
+                  lp.level_comb);
+    // per chunk of scalars: {slot | s_local << 16, L index}, sorted by slot
+    lp.nchunks = (m.S + lp.CH - 1) / lp.CH;
+    lp.ent_start.assign(1, 0);
+    for (int c = 0; c < lp.nchunks; ++c) {
+        std::vector<std::array<int, 3>> e;
+        for (int s = c * lp.CH; s < std::min(m.S, (c + 1) * lp.CH); ++s) {
+            const int x = m.map[s];
+            for (int b : supp[x])
+                e.push_back({slot_of[b], s - c * lp.CH, lws(x, b)});
+        }
+        std::stable_sort(e.begin(), e.end(),
+                         [](const std::array<int, 3> &a, const std::array<int, 3> &b) {
+                             return a[0] < b[0];
+                         });
+        for (auto &v : e) {
+            if (v[0] < 0 || v[2] < 0)
+                return fail(err, "internal error: linear-fit support outside the slots");
+            lp.ent.push_back(v[0] | (v[1] << 16));
+            lp.ent.push_back(v[2]);
+        }
+        lp.ent_start.push_back((int)lp.ent.size() / 2);
+    }
     return true;
 }
 

@@ -138,6 +138,20 @@ struct Plan {
 };
 bool build_plan(const Model &m, Plan &p, std::string &err);
 
+// Linear-fit plan (sparse Jacobian of the scalar moments w.r.t. the basic
+// moments, see build_lin_plan).  Work space per wave (doubles): the E/F/S
+// block [0, red0), the transpose buffer, `one` (1.0), the Jacobian values
+// [L0, L0 + nL), the step partials [part0, acc), the per-lane accumulators
+// acc_rows x kRedStride.
+struct LinPlan {
+    int nL = 0, one = 0, L0 = 0, part0 = 0, acc = 0, acc_rows = 0, priv = 0;
+    int CH = 16, nchunks = 0;   // scalars per chunk
+    std::vector<int> level_step, steps, level_comb, comb;  // as Plan's rule tables
+    std::vector<int> ent;        // int2 {slot | s_local << 16, L index} per chunk, by slot
+    std::vector<int> ent_start;  // [nchunks + 1]
+};
+bool build_lin_plan(const Model &m, const Plan &p, LinPlan &lp, std::string &err);
+
 // Device view passed to the kernels by value.
 struct DevModel {
     int Z, M, R, K, B, T, S, nslots;
@@ -205,6 +219,32 @@ bool efs_configure(const DevModel &m, int n, int num_cus, int max_waves, size_t 
 int efs_variant(const DevModel &m, int R);
 hipError_t launch_efs(const DevModel &m, const DevNeighbors &nb, const EfsOut &out,
                       const EfsLaunch &cfg, bool deterministic, hipStream_t s);
+// Linear fit (lin_kernel.hip).
+struct DevLin {
+    int nL, one, L0, part0, acc, priv, CH, nchunks, nlev;
+    const int *level_step, *level_comb;  // [nlev + 1]
+    const int2 *steps;
+    const int4 *comb;
+    const int2 *ent;        // {slot | s_local << 16, L index}
+    const int *ent_start;   // [nchunks + 1]
+};
+struct LinOut {
+    const int *center_structure;  // [n]
+    double *ec;  // [nconf][p] energy components (p = Z + S)
+    double *fc;  // [n][3][p] force components
+    double *sc;  // [nconf][9][p] stress components
+};
+bool lin_configure(const DevModel &m, const DevLin &L, int n, int num_cus, size_t lds_limit,
+                   EfsLaunch &cfg);
+hipError_t launch_lin_site(const DevModel &m, const DevLin &L, const DevNeighbors &nb,
+                           const LinOut &out, const EfsLaunch &cfg, hipStream_t s);
+hipError_t launch_lin_rows(const double *comp, const int64_t *src, const double *sw,
+                           const double *yw, int64_t R, int p, double *A, double *y, hipStream_t s);
+// Gram columns padded to a multiple of 16 (p coefficients plus the target).
+int gram_padded(int p);
+hipError_t launch_gram(const double *comp, const int64_t *src, const double *sw, const double *yw,
+                       int64_t R, int p, int nblocks, double *partial, hipStream_t s);
+
 // Training (train_kernel.hip).
 struct LossArgs {
     const int *soff;     // [nconf+1] first atom of each structure

@@ -350,6 +350,19 @@ int mtpx_set_labels(mtpx_context *ctx, const int *active, const double *target_e
             "upload labels");
     HIP_TRY(upload_or_zero(ctx->wS, any[2] ? stress_weight : nullptr, nc, s), "upload labels");
     HIP_TRY(hipStreamSynchronize(s), "upload labels");
+    auto keep = [](std::vector<double> &dst, const double *src, size_t len) {
+        if (src)
+            dst.assign(src, src + len);
+        else
+            dst.assign(len, 0.0);
+    };
+    ctx->active_h.assign(active ? active : nullptr, active ? active + 3 * (size_t)nc : nullptr);
+    keep(ctx->tE_h, any[0] ? target_energy : nullptr, nc);
+    keep(ctx->wE_h, any[0] ? energy_weight : nullptr, nc);
+    keep(ctx->tF_h, any[1] ? target_forces : nullptr, 3 * (size_t)n);
+    keep(ctx->wF_h, any[1] ? force_weight : nullptr, n);
+    keep(ctx->tS_h, any[2] ? target_stress : nullptr, 9 * (size_t)nc);
+    keep(ctx->wS_h, any[2] ? stress_weight : nullptr, nc);
     ctx->has_labels = true;
     ctx->has_adjoints = false;
     return MTPX_OK;

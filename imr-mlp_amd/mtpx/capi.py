@@ -77,6 +77,11 @@ def lib():
         L.mtpx_loss_grad.argtypes = [C.c_void_p, C.c_int, C.c_double, C.c_double, C.c_double,
                                      _dp, _dp, _dp]
         L.mtpx_last_train_timings.argtypes = [C.c_void_p, _dp]
+        L.mtpx_efs_components.argtypes = [C.c_void_p, _dp, _dp, _dp]
+        L.mtpx_linear_rows.argtypes = [C.c_void_p, C.POINTER(C.c_int64), _dp, _dp]
+        L.mtpx_linear_system.argtypes = [C.c_void_p, _dp, _dp]
+        L.mtpx_orthogonalize.argtypes = [C.c_void_p]
+        L.mtpx_last_linear_timings.argtypes = [C.c_void_p, _dp]
         _lib = L
     return _lib
 
@@ -326,4 +331,39 @@ class Context:
     def last_train_timings(self):
         t = np.zeros(4)
         self._check(lib().mtpx_last_train_timings(self.h, _d(t)), "last_train_timings")
+        return t
+
+    # ---- linear fit ----
+    def efs_components(self):
+        n, _ = self.neighbor_count()
+        nc = self.structure_count()
+        p = self.info["Z"] + self.info["S"]
+        ec = np.zeros((max(nc, 1), p))
+        fc = np.zeros((max(n, 1), 3, p))
+        sc = np.zeros((max(nc, 1), 9, p))
+        self._check(lib().mtpx_efs_components(self.h, _d(ec), _d(fc), _d(sc)), "efs_components")
+        return ec[:nc], fc[:n], sc[:nc].reshape(nc, 3, 3, p)
+
+    def linear_rows(self):
+        R = C.c_int64(0)
+        self._check(lib().mtpx_linear_rows(self.h, C.byref(R), None, None), "linear_rows")
+        p = self.info["Z"] + self.info["S"]
+        A = np.zeros((max(R.value, 1), p))
+        y = np.zeros(max(R.value, 1))
+        self._check(lib().mtpx_linear_rows(self.h, C.byref(R), _d(A), _d(y)), "linear_rows")
+        return A[:R.value], y[:R.value]
+
+    def linear_system(self):
+        p = self.info["Z"] + self.info["S"]
+        G = np.zeros((p, p))
+        b = np.zeros(p)
+        self._check(lib().mtpx_linear_system(self.h, _d(G), _d(b)), "linear_system")
+        return G, b
+
+    def orthogonalize(self):
+        self._check(lib().mtpx_orthogonalize(self.h), "orthogonalize")
+
+    def last_linear_timings(self):
+        t = np.zeros(4)
+        self._check(lib().mtpx_last_linear_timings(self.h, _d(t)), "last_linear_timings")
         return t

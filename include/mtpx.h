@@ -203,6 +203,33 @@ int mtpx_loss_grad(mtpx_context *ctx, int deterministic, double penalty_weight, 
  * {whole call, E/F/S, loss, gradient}. */
 int mtpx_last_train_timings(const mtpx_context *ctx, double out_ms[4]);
 
+/* ---- linear fit -------------------------------------------------------
+ * PotMTP::CalcEFSCmpt_R (potentials/potential_mtp.cpp:2675-2707, over
+ * CalcSiteBasisDers :3163-3280; potential_mtp.h:1609) for every structure of
+ * the resident topology: the energy [nconf][p], force [N][3][p] and stress
+ * [nconf][9][p] of each linear coefficient (p = Z + S: species, then moment
+ * coefficients), so that E = sum_q x_q energy_cmpts[q] etc.  Outputs may be
+ * NULL. */
+int mtpx_efs_components(mtpx_context *ctx, double *energy_cmpts, double *force_cmpts,
+                        double *stress_cmpts);
+/* Trainer_MTP::AddLinearFast rows (train/train_mtp.cpp:1289-1395) for the
+ * resident batch and labels: per structure the force rows of the atoms with
+ * a positive force weight (x, y, z), the 9 stress rows, the energy row, each
+ * scaled by sqrt(weight); y the scaled targets.  A [nrows][p], y [nrows];
+ * with A and y NULL only *nrows is set, otherwise *nrows is the capacity on
+ * entry and the count on return. */
+int mtpx_linear_rows(mtpx_context *ctx, int64_t *nrows, double *A, double *y);
+/* Trainer_MTP::TrainLinearFast assembly (train/train_mtp.cpp:2383-2427):
+ * G = A^T A [p][p] and b = A^T y [p] over the rows of mtpx_linear_rows,
+ * summed on the fp64 matrix cores in a fixed order. */
+int mtpx_linear_system(mtpx_context *ctx, double *G, double *b);
+/* PotMTP::Orthogonalize (potentials/potential_mtp.cpp:3849-3930) of the
+ * radial coefficients; TrainLinearFast calls it before the assembly. */
+int mtpx_orthogonalize(mtpx_context *ctx);
+/* Device-side timing of the last mtpx_linear_system, milliseconds:
+ * {whole call, components kernel, Gram kernel, rows}. */
+int mtpx_last_linear_timings(const mtpx_context *ctx, double out[4]);
+
 #ifdef __cplusplus
 }
 #endif

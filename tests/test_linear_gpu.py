@@ -1,0 +1,184 @@
+"""Linear fit on the device against the oracle's restatement of
+CalcEFSCmpt_R / CalcSiteBasisDers (potentials/potential_mtp.cpp:2675-2707,
+3163-3280), AddLinearFast (train/train_mtp.cpp:1289-1395), the Gram of
+TrainLinearFast (:2426-2427) and Orthogonalize (:3849-3930).
+
+Tolerances: components, rows and the normal equations 1e-10 relative
+(largest absolute difference over the largest magnitude)."""
+import numpy as np
+import pytest
+
+import oracle as O
+from helpers import rel_err
+from mtpx import capi
+from mtpx import synth as S
+
+pytestmark = pytest.mark.gpu
+
+
+def _crystals(count, seed, drop=False):
+    ref_text, start_text = S.training_models(4)
+    mref = O.Model(ref_text)
+    rng = S.rng_for(900 + seed)
+    structs, nbs, labels = [], [], []
+    for k, s in enumerate(S.training_structures(4, count)):
+        s.pos = O.wrap(s.cell, s.pbc, s.pos)
+        nb = O.Neighbors.build(s.cell, s.pbc, s.pos, s.types, 5.0)
+        E, F, St, _ = O.efs(mref, nb)
+        e, f, st = S.noisy_labels(rng, s.n, E, F, St)
+        lb = O.Labels(s.n, energy=e, forces=f, stress=st, fitness=0.5 + rng.random())
+        if drop:
+            if k % 4 == 1:
+                lb.forces = None
+            if k % 4 == 2:
+                lb.stress = None
+            if k % 4 == 3:
+                lb.energy = None
+            if k % 3 == 0:
+                af = 0.5 + rng.random(s.n)
+                af[::5] = 0.0  # atoms excluded from the force rows
+                lb.atomic_fitness = af
+        structs.append(s)
+        nbs.append(nb)
+        labels.append(lb)
+    return start_text, structs, nbs, labels
+
+
+def _upload(ctx, text, structs, labels, settings, cutoff=5.0):
+    ctx.load_model_text(text)
+    off = ctx.set_structures(structs, cutoff)
+    has = np.array([[lb.energy is not None, lb.forces is not None, lb.stress is not None]
+                    for lb in labels], np.int32)
+    tf = np.concatenate([lb.forces if lb.forces is not None else np.zeros((lb.n, 3))
+                         for lb in labels])
+    fit = np.array([lb.fitness for lb in labels])
+    af = np.concatenate([lb.atomic_fitness if lb.atomic_fitness is not None else np.ones(lb.n)
+                         for lb in labels])
+    st = capi.LossSettings.make(*[getattr(settings, f[0]) for f in settings._fields_])
+    active, wE, wF, wS = capi.loss_weights(st, off, has, tf, fit, af)
+    tE = np.array([lb.energy if lb.energy is not None else 0.0 for lb in labels])
+    tS = np.array([lb.stress if lb.stress is not None else np.zeros((3, 3)) for lb in labels])
+    ctx.set_labels(active, tE, wE, tf, wF, tS, wS)
+    return off
+
+
+@pytest.fixture(scope="module")
+def crystal_set():
+    return _crystals(6, 1, drop=True)
+
+
+SETTINGS = {"linear": O.LossSettings.make(weight_eng=1.0, weight_force=0.01, weight_stress=0.001),
+            "per-atom": O.LossSettings.make(weight_eng=1.0, weight_force=0.01,
+                                            weight_stress=0.001, eng_pow=2.0, force_pow=1.0,
+                                            stress_pow=0.0),
+            "force-norm": O.LossSettings.make(force_norm_f=1.0, force_norm_p=1.5)}
+
+
+def test_components_match_oracle(ctx, crystal_set):
+    text, structs, nbs, labels = crystal_set
+    off = _upload(ctx, text, structs, labels, SETTINGS["linear"])
+    m = O.Model(text)
+    ec, fc, sc = ctx.efs_components()
+    for c, nb in enumerate(nbs):
+        eo, fo, so = O.efs_components(m, nb)
+        assert rel_err(ec[c], eo) < 1e-10
+        assert rel_err(fc[off[c]:off[c + 1]], fo) < 1e-10
+        assert rel_err(sc[c], so) < 1e-10
+
+
+def test_components_reproduce_efs(ctx, crystal_set):
+    """sum_q x_q components_q equals the device E/F/S."""
+    text, structs, nbs, labels = crystal_set
+    _upload(ctx, text, structs, labels, SETTINGS["linear"])
+    ec, fc, sc = ctx.efs_components()
+    x = ctx.get_coeffs()
+    info = ctx.info
+    lin = x[info["Z"] * info["Z"] * info["M"] * info["R"]:]
+    E, F, St, _ = ctx.compute_batch()
+    assert rel_err(ec @ lin, E) < 1e-10
+    assert rel_err(fc @ lin, F) < 1e-10
+    assert rel_err(sc @ lin, St) < 1e-10
+
+
+@pytest.mark.parametrize("name", list(SETTINGS))
+def test_linear_rows_match_oracle(ctx, crystal_set, name):
+    text, structs, nbs, labels = crystal_set
+    st = SETTINGS[name]
+    _upload(ctx, text, structs, labels, st)
+    m = O.Model(text)
+    A, y = ctx.linear_rows()
+    Ao = np.concatenate([O.linear_rows(m, nb, st, lb)[0] for nb, lb in zip(nbs, labels)])
+    yo = np.concatenate([O.linear_rows(m, nb, st, lb)[1] for nb, lb in zip(nbs, labels)])
+    assert A.shape == Ao.shape
+    assert rel_err(A, Ao) < 1e-10 and rel_err(y, yo) < 1e-10
+
+
+@pytest.mark.parametrize("name", list(SETTINGS))
+def test_linear_system_matches_oracle(ctx, crystal_set, name):
+    text, structs, nbs, labels = crystal_set
+    st = SETTINGS[name]
+    _upload(ctx, text, structs, labels, st)
+    m = O.Model(text)
+    G, b = ctx.linear_system()
+    Go, bo = O.linear_system_batch(m, nbs, labels, st, threads=8)
+    assert rel_err(G, Go) < 1e-10 and rel_err(b, bo) < 1e-10
+    assert np.array_equal(G, G.T)
+
+
+def test_gram_of_the_device_rows(ctx, crystal_set):
+    """The matrix-core Gram equals the textbook sum over the returned rows."""
+    text, structs, nbs, labels = crystal_set
+    _upload(ctx, text, structs, labels, SETTINGS["per-atom"])
+    A, y = ctx.linear_rows()
+    G, b = ctx.linear_system()
+    Gt, bt = O.gram(A, y)
+    assert rel_err(G, Gt) < 1e-12 and rel_err(b, bt) < 1e-12
+
+
+def test_orthogonalize_matches_oracle(ctx):
+    text, _ = S.training_models(4)
+    m = O.Model(text)
+    ctx.load_model_text(text)
+    ctx.orthogonalize()
+    m.orthogonalize()
+    assert rel_err(ctx.get_coeffs(), m.coeffs) < 1e-14
+
+
+def test_linear_after_orthogonalize(ctx, crystal_set):
+    """The TrainLinearFast order: orthogonalise, then assemble."""
+    text, structs, nbs, labels = crystal_set
+    st = SETTINGS["linear"]
+    _upload(ctx, text, structs, labels, st)
+    ctx.orthogonalize()
+    m = O.Model(text)
+    m.orthogonalize()
+    G, b = ctx.linear_system()
+    Go, bo = O.linear_system_batch(m, nbs, labels, st, threads=8)
+    assert rel_err(G, Go) < 1e-10 and rel_err(b, bo) < 1e-10
+
+
+def test_level10_and_runtime_profile_models(ctx):
+    """Level-10 (compile-time profile) and a model on the runtime profile."""
+    rng = S.rng_for(77)
+    for name, R in [("shapeev-10.mtp", 8), ("shapeev-16.mtp", 6)]:
+        text = S.random_model(name, 2, R, 1.9, 5.0, -0.1, 0.1, rng)
+        m = O.Model(text)
+        s = S.displace(S.lattice("fcc", (3, 3, 3), 3.56), rng, 0.1)
+        s.types = (S.uniform(rng, s.n) * 2).astype(np.int32)
+        s.pos = O.wrap(s.cell, s.pbc, s.pos)
+        nb = O.Neighbors.build(s.cell, s.pbc, s.pos, s.types, 5.0)
+        ctx.load_model_text(text)
+        ctx.set_structures([s], 5.0)
+        ec, fc, sc = ctx.efs_components()
+        eo, fo, so = O.efs_components(m, nb)
+        assert rel_err(ec[0], eo) < 1e-10 and rel_err(fc, fo) < 1e-10
+        assert rel_err(sc[0], so) < 1e-10
+
+
+def test_empty_batch_linear_system(ctx):
+    text, _ = S.training_models(4)
+    ctx.load_model_text(text)
+    ctx.set_structures([], 5.0)
+    ctx.set_labels(np.zeros((0, 3), np.int32))
+    G, b = ctx.linear_system()
+    assert not G.any() and not b.any()
