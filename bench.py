@@ -125,6 +125,107 @@ def train_bench(ctx, steps: int, warmup: int, nconf: int):
     }, (start_text, structs, off, tE, tF, tS, cutoff)
 
 
+def linear_flops(model_text: str, n: int, P: int, rows: int) -> float:
+    """Linear step: sum_i [n_i (8R + 4MR + 4nu + 32B + 12T + 24S) + 3T + 2S]
+    + rows p (p + 1) + 2 rows p, p = Z + S."""
+    t = S.template_topology(model_text)
+    hdr = {k: int(v) for k, v in
+           (l.strip().split(" = ") for l in model_text.splitlines()
+            if l.strip().startswith(("radial_basis_size", "radial_funcs_count",
+                                     "species_count")))}
+    R, M, Z = hdr["radial_basis_size"], hdr["radial_funcs_count"], hdr["species_count"]
+    B, T, Sn = len(t["basic"]), len(t["times"]), len(t["map"])
+    nu = int(t["basic"][:, 1:].sum(axis=1).max())
+    p = Z + Sn
+    per_pair = 8 * R + 4 * M * R + 4 * nu + 32 * B + 12 * T + 24 * Sn
+    return float(P) * per_pair + float(n) * (3 * T + 2 * Sn) + rows * p * (p + 1) + 2.0 * rows * p
+
+
+def linear_bench(ctx, steps: int, nconf: int):
+    """Workload: level-16 two-species model (radial basis 8, cutoff 5.0),
+    nconf FCC/BCC structures of 64-256 atoms (strain 3 %, displacements
+    0.1-0.3 A); labels from a seeded reference model (this library) plus
+    noise; weights energy/force/stress 1/0.01/0.001.  A step is
+    TrainLinearFast's assembly: design rows, AddLinearFast rows, Gram."""
+    ref_text, start_text = S.training_models(4)
+    structs = S.training_structures(4, nconf)
+    for st in structs:
+        st.pos = capi.wrap(st.cell, st.pbc, st.pos)
+    ctx.load_model_text(ref_text)
+    off = ctx.set_structures(structs, 5.0)
+    E, F, St, _ = ctx.compute_batch()
+    rng = S.rng_for(4, 3)
+    tE, tF, tS = [], [], []
+    for c, st in enumerate(structs):
+        e, f, sv = S.noisy_labels(rng, st.n, E[c], F[off[c]:off[c + 1]], St[c])
+        tE.append(e)
+        tF.append(f)
+        tS.append(sv)
+    tE, tF, tS = np.array(tE), np.concatenate(tF), np.array(tS)
+    ctx.load_model_text(start_text)
+    has = np.ones((nconf, 3), np.int32)
+    sets = capi.LossSettings.make(weight_energy=1.0, weight_forces=0.01, weight_stress=0.001)
+    active, wE, wF, wS = capi.loss_weights(sets, off, has, tF)
+    ctx.set_labels(active, tE, wE, tF, wF, tS, wS)
+    ctx.linear_system()  # warm-up
+    tims = []
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        G, b = ctx.linear_system()
+        tims.append(ctx.last_linear_timings())
+    wall = time.perf_counter() - t0
+    tims = np.array(tims)
+    n, P = ctx.neighbor_count()
+    rows = int(tims[0, 3])
+    flops = linear_flops(start_text, n, P, rows)
+    dev_ms = float(np.mean(tims[:, 0]))
+    return {
+        "metric": "linear-fit assembly configs/s (lvl16, 2 species, %d FCC/BCC configs)" % nconf,
+        "value": nconf * steps / wall, "unit": "configs/s", "steps": steps,
+        "ms_per_step": 1e3 * wall / steps,
+        "config": {"workload": "linear fit, level-16 MTP, 2 species, R=8, cutoff 5.0, %d FCC/BCC "
+                               "configs of 64-256 atoms, weights 1/0.01/0.001" % nconf,
+                   "atoms": n, "neighbor_entries": P, "rows": rows, "p": int(G.shape[0])},
+        "roofline": {"bound": "mfma", "achieved": flops / (dev_ms * 1e-3) / 1e12,
+                     "peak": FP64_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": flops / (dev_ms * 1e-3) / 1e12 / FP64_PEAK_TFLOPS, "traffic": None,
+                     "kernel": "lin_site_kernel + gram_kernel (MFMA)", "device_ms": dev_ms,
+                     "components_ms": float(np.mean(tims[:, 1])),
+                     "gram_ms": float(np.mean(tims[:, 2])),
+                     "algorithmic_flops_per_step": flops},
+    }, (start_text, structs, off, tE, tF, tS)
+
+
+def linear_cpu_baseline(data, budget_s: float = 12.0):
+    """The oracle's CalcEFSCmpt_R + AddLinearFast + Gram on the host cores,
+    on the first structures of the same batch (bounded sample)."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+
+    text, structs, off, tE, tF, tS = data
+    threads = max(1, min(16, os.cpu_count() or 1))
+    m = O.Model(text)
+    sample = min(32, len(structs))
+    nbs, labels = [], []
+    for k in range(sample):
+        st = structs[k]
+        nbs.append(O.Neighbors.build(st.cell, st.pbc, st.pos, st.types, 5.0))
+        labels.append(O.Labels(st.n, energy=tE[k], forces=tF[off[k]:off[k + 1]], stress=tS[k]))
+    sets = O.LossSettings.make(weight_eng=1.0, weight_force=0.01, weight_stress=0.001)
+    O.linear_system_batch(m, nbs, labels, sets, threads)  # warm-up
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        O.linear_system_batch(m, nbs, labels, sets, threads)
+        reps += 1
+        el = time.perf_counter() - t0
+        if el > budget_s or reps >= 1000:
+            break
+    return {"value": reps * len(nbs) / el, "unit": "configs/s", "cores": threads, "kind": "port",
+            "sample": "%d assemblies over the first %d structures of the batch (oracle "
+                      "CalcEFSCmpt_R + AddLinearFast + Gram, %d OpenMP threads, %.1f s)"
+                      % (reps, len(nbs), threads, el)}
+
+
 def train_cpu_baseline(data, budget_s: float = 12.0):
     """The oracle's AccumulateGard restatement on the host cores, on the
     first structures of the same batch (bounded sample)."""
@@ -186,6 +287,9 @@ def main():
     ap.add_argument("--no-train", action="store_true")
     ap.add_argument("--train-steps", type=int, default=5)
     ap.add_argument("--train-configs", type=int, default=1000)
+    ap.add_argument("--no-linear", action="store_true")
+    ap.add_argument("--linear-steps", type=int, default=3)
+    ap.add_argument("--linear-configs", type=int, default=2000)
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="only copy a MIB-MiB device buffer 3 times (calibrates the HBM "
                          "byte counters against a plain copy of known size)")
@@ -238,6 +342,9 @@ def main():
     train = None
     if not args.no_train:
         train, tdata = train_bench(ctx, args.train_steps, 1, args.train_configs)
+    linear = None
+    if not args.no_linear:
+        linear, ldata = linear_bench(ctx, args.linear_steps, args.linear_configs)
     ctx.close()
 
     flops = efs_flops(model_text, n, P)
@@ -280,6 +387,10 @@ def main():
         if not args.no_cpu:
             train["cpu_baseline"] = train_cpu_baseline(tdata)
         out["train"] = train
+    if linear is not None:
+        if not args.no_cpu:
+            linear["cpu_baseline"] = linear_cpu_baseline(ldata)
+        out["linear"] = linear
     print(json.dumps(out))
 
 

@@ -1,6 +1,6 @@
 """Build libmtpx.so for gfx950 with hipcc (in-tree, no JIT cache).
 
-    python imr-mlp_amd/build.py [-v]
+    python imr-mlp_amd/build.py [-v] [--changed]
 
 Each translation unit gets its own floating-point contraction policy: the
 neighbour builder and the host geometry are compiled with
@@ -44,15 +44,28 @@ def sources():
     return [(s, f) for s, f in SOURCES if os.path.exists(os.path.join(CSRC, s))]
 
 
-def build(verbose: bool = False) -> str:
+def _newest_header() -> float:
+    hs = [os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".hpp")]
+    hs.append(os.path.join(ROOT, "include", "mtpx.h"))
+    return max(os.path.getmtime(h) for h in hs)
+
+
+def build(verbose: bool = False, changed_only: bool = False) -> str:
+    """Compile every translation unit (changed_only: those older than their
+    source or a header) and link the library."""
     os.makedirs(LIB_DIR, exist_ok=True)
     os.makedirs(OBJ_DIR, exist_ok=True)
     objs, cmds = [], []
     t0 = time.time()
+    newest_h = _newest_header()
     for src, flags in sources():
         obj = os.path.join(OBJ_DIR, src + ".o")
-        cmds.append([HIPCC, "-x", "hip", "-c", os.path.join(CSRC, src), "-o", obj] + COMMON + flags)
         objs.append(obj)
+        if changed_only and os.path.exists(obj):
+            t_obj = os.path.getmtime(obj)
+            if t_obj > os.path.getmtime(os.path.join(CSRC, src)) and t_obj > newest_h:
+                continue
+        cmds.append([HIPCC, "-x", "hip", "-c", os.path.join(CSRC, src), "-o", obj] + COMMON + flags)
     # translation units compile in parallel (the kernel files dominate)
     procs = []
     for cmd in cmds:
@@ -74,4 +87,4 @@ def build(verbose: bool = False) -> str:
 
 
 if __name__ == "__main__":
-    build(verbose="-v" in sys.argv)
+    build(verbose="-v" in sys.argv, changed_only="--changed" in sys.argv)

@@ -123,8 +123,8 @@ int install_model(mtpx_context *ctx, Model &&m)
         HIP_TRY(upload(ctx->lin_steps, lp.steps, s), "upload model");
         HIP_TRY(upload(ctx->lin_lcomb, lp.level_comb, s), "upload model");
         HIP_TRY(upload(ctx->lin_comb, lp.comb, s), "upload model");
-        HIP_TRY(upload(ctx->lin_ent, lp.ent, s), "upload model");
-        HIP_TRY(upload(ctx->lin_estart, lp.ent_start, s), "upload model");
+        HIP_TRY(upload(ctx->lin_ent, lp.slot_L, s), "upload model");
+        HIP_TRY(upload(ctx->lin_estart, lp.slot_mask, s), "upload model");
         DevLin &L = ctx->dl;
         L.nL = lp.nL;
         L.one = lp.one;
@@ -139,8 +139,8 @@ int install_model(mtpx_context *ctx, Model &&m)
         L.level_comb = ctx->lin_lcomb.as<int>();
         L.steps = ctx->lin_steps.as<int2>();
         L.comb = ctx->lin_comb.as<int4>();
-        L.ent = ctx->lin_ent.as<int2>();
-        L.ent_start = ctx->lin_estart.as<int>();
+        L.slot_L = ctx->lin_ent.as<int>();
+        L.slot_mask = ctx->lin_estart.as<int>();
     }
     int rc = upload_coeffs(ctx);
     if (rc != MTPX_OK)

@@ -30,10 +30,15 @@ typedef double d4v __attribute__((ext_vector_type(4)));
 // Walk of the slots (nu, mu, alpha) with the chunk's entries: for a slot
 // that has entries, grad_r(f Y) = (f' - nu f/d) Y u + (f/d) grad_u Y is
 // formed once and added, times L, to each of the slot's scalars.
+// Walk of the slots (nu, mu, alpha) for one chunk of scalars: where the
+// chunk's mask of the slot is set, grad_r(f Y) = (f' - nu f/d) Y u +
+// (f/d) grad_u Y is formed once and added, times L, to those scalars'
+// derivatives (registers; the mask and its bits are wave-uniform).
 template <int NU, class P>
 __device__ __forceinline__ void lin_shells(const DevModel &m, const DevLin &L, const Nbr<P::M> &q,
-                                           const double *prev, int &slot, int &ptr, int end,
-                                           double *ws, int lane)
+                                           const double *prev, int &slot, const int *mask,
+                                           const int *lidx, const double *ws,
+                                           double (&acc)[3 * kLinChunk])
 {
     double cur[shell_size(NU)];
     if constexpr (NU == 0)
@@ -52,32 +57,27 @@ __device__ __forceinline__ void lin_shells(const DevModel &m, const DevLin &L, c
                 for (int b = NU - a; b >= 0; --b) {
                     const int i = shell_index(NU, a, b);
                     const int sl = slot + i;
-                    if (ptr < end) {
-                        int2 e = L.ent[ptr];
-                        if ((e.x & 0xffff) == sl) {
-                            const double hy = h * cur[i];
-                            double gx = hy * q.ux, gy = hy * q.uy, gz = hy * q.uz;
-                            if constexpr (NU > 0) {
-                                if (a > 0)
-                                    gx += (a * fdi) * prev[shell_index(NU - 1, a - 1, b)];
-                                if (b > 0)
-                                    gy += (b * fdi) * prev[shell_index(NU - 1, a, b - 1)];
-                                if (NU - a - b > 0)
-                                    gz += ((NU - a - b) * fdi) * prev[shell_index(NU - 1, a, b)];
-                            }
-                            while (true) {
-                                const double lv = ws[e.y];
-                                double *ar = ws + L.acc + (e.x >> 16) * 3 * kRedStride + lane;
-                                ar[0] += lv * gx;
-                                ar[kRedStride] += lv * gy;
-                                ar[2 * kRedStride] += lv * gz;
-                                if (++ptr >= end)
-                                    break;
-                                e = L.ent[ptr];
-                                if ((e.x & 0xffff) != sl)
-                                    break;
-                            }
+                    const int mk = mask[sl];
+                    if (mk) {
+                        const double hy = h * cur[i];
+                        double gx = hy * q.ux, gy = hy * q.uy, gz = hy * q.uz;
+                        if constexpr (NU > 0) {
+                            if (a > 0)
+                                gx += (a * fdi) * prev[shell_index(NU - 1, a - 1, b)];
+                            if (b > 0)
+                                gy += (b * fdi) * prev[shell_index(NU - 1, a, b - 1)];
+                            if (NU - a - b > 0)
+                                gz += ((NU - a - b) * fdi) * prev[shell_index(NU - 1, a, b)];
                         }
+                        const int *li = lidx + (size_t)sl * kLinChunk;
+#pragma unroll
+                        for (int k = 0; k < kLinChunk; ++k)
+                            if (mk & (1 << k)) {
+                                const double lv = ws[li[k]];
+                                acc[3 * k] += lv * gx;
+                                acc[3 * k + 1] += lv * gy;
+                                acc[3 * k + 2] += lv * gz;
+                            }
                     }
                 }
             slot += shell_size(NU);
@@ -85,7 +85,7 @@ __device__ __forceinline__ void lin_shells(const DevModel &m, const DevLin &L, c
     }
     if constexpr (NU < P::NUMAX) {
         if (P::deeper(m, NU))
-            lin_shells<NU + 1, P>(m, L, q, cur, slot, ptr, end, ws, lane);
+            lin_shells<NU + 1, P>(m, L, q, cur, slot, mask, lidx, ws, acc);
     }
 }
 
@@ -118,7 +118,7 @@ __global__ __launch_bounds__(kWave *kMaxWaves) void lin_site_kernel(DevModel m, 
     const int nwaves = blockDim.x / kWave;
     const Shared Ls = shared_layout(m, lds);
     double *ws = lds + shared_doubles(m, false) + (size_t)wave * L.priv;
-    double *mom = ws, *red = ws + m.red0, *acc = ws + L.acc;
+    double *mom = ws, *red = ws + m.red0;
     const int p = m.Z + m.S;
 
     stage_shared(m, Ls, false, tid, blockDim.x);
@@ -171,52 +171,65 @@ __global__ __launch_bounds__(kWave *kMaxWaves) void lin_site_kernel(DevModel m, 
         // ---- force and stress components, CH scalars at a time ------------
         for (int ch = 0; ch < L.nchunks; ++ch) {
             const int s0 = ch * L.CH, nch = min(L.CH, m.S - s0);
-            const int e0 = L.ent_start[ch], e1 = L.ent_start[ch + 1];
+            const int *mask = L.slot_mask + (size_t)ch * m.nslots;
+            const int *lidx = L.slot_L + (size_t)ch * m.nslots * kLinChunk;
             for (int base = 0; base < n; base += kWave) {
-                for (int r = 0; r < 3 * nch; ++r)
-                    acc[r * kRedStride + lane] = 0.0;
+                double acc[3 * kLinChunk];
+#pragma unroll
+                for (int r = 0; r < 3 * kLinChunk; ++r)
+                    acc[r] = 0.0;
                 const bool valid = lane < n - base;
                 const int64_t pe = beg + base + lane;
                 Nbr<P::M> q;
                 load_neighbor<P>(m, nb, Ls.coef, ti, pe, valid, q);
-                int slot = 0, ptr = e0;
-                lin_shells<0, P>(m, L, q, nullptr, slot, ptr, e1, ws, lane);
+                int slot = 0;
+                lin_shells<0, P>(m, L, q, nullptr, slot, mask, lidx, ws, acc);
                 // the site's own rows: + sum_j dm/dr_j
-                for (int r0 = 0; r0 < 3 * nch; r0 += kChunk)
-                    reduce_rows_lin(acc + r0 * kRedStride, min(kChunk, 3 * nch - r0), r0, lane,
-                                    [&](int r, double v) {
-                                        atomicAdd(&out.fc[((size_t)i * 3 + r % 3) * p + m.Z + s0 +
-                                                          r / 3],
-                                                  v);
-                                    });
+                int row = 0;
+                auto flush_self = [&](int nrows) {
+                    reduce_rows_lin(red, nrows, row - nrows, lane, [&](int r, double v) {
+                        atomicAdd(&out.fc[((size_t)i * 3 + r % 3) * p + m.Z + s0 + r / 3], v);
+                    });
+                };
+#pragma unroll
+                for (int r = 0; r < 3 * kLinChunk; ++r)
+                    if (r < 3 * nch) {
+                        red[(row % kChunk) * kRedStride + lane] = acc[r];
+                        ++row;
+                        if (row % kChunk == 0)
+                            flush_self(kChunk);
+                    }
+                if (row % kChunk)
+                    flush_self(row % kChunk);
                 // the neighbours' rows: - dm/dr_j
                 if (valid) {
                     const int j = nb.idx[pe];
-                    for (int sl = 0; sl < nch; ++sl)
-                        for (int a = 0; a < 3; ++a)
-                            atomicAdd(&out.fc[((size_t)j * 3 + a) * p + m.Z + s0 + sl],
-                                      -acc[(sl * 3 + a) * kRedStride + lane]);
+#pragma unroll
+                    for (int r = 0; r < 3 * kLinChunk; ++r)
+                        if (r < 3 * nch)
+                            atomicAdd(&out.fc[((size_t)j * 3 + r % 3) * p + m.Z + s0 + r / 3],
+                                      -acc[r]);
                 }
                 // stress rows: - sum_j (dm/dr_j)_a r_jb
                 const double rv[3] = {q.x, q.y, q.z};
-                int row = 0;
+                row = 0;
                 auto flush = [&](int nrows) {
                     reduce_rows_lin(red, nrows, row - nrows, lane, [&](int r, double v) {
                         atomicAdd(&out.sc[((size_t)c * 9 + r % 9) * p + m.Z + s0 + r / 9], v);
                     });
                 };
-                for (int sl = 0; sl < nch; ++sl)
 #pragma unroll
-                    for (int a = 0; a < 3; ++a) {
-                        const double d = acc[(sl * 3 + a) * kRedStride + lane];
+                for (int sl = 0; sl < kLinChunk; ++sl)
+                    if (sl < nch)
 #pragma unroll
-                        for (int b = 0; b < 3; ++b) {
-                            red[(row % kChunk) * kRedStride + lane] = -d * rv[b];
-                            ++row;
-                            if (row % kChunk == 0)
-                                flush(kChunk);
-                        }
-                    }
+                        for (int a = 0; a < 3; ++a)
+#pragma unroll
+                            for (int b = 0; b < 3; ++b) {
+                                red[(row % kChunk) * kRedStride + lane] = -acc[3 * sl + a] * rv[b];
+                                ++row;
+                                if (row % kChunk == 0)
+                                    flush(kChunk);
+                            }
                 if (row % kChunk)
                     flush(row % kChunk);
             }
@@ -314,9 +327,15 @@ __global__ __launch_bounds__(256) void gram_kernel(const double *comp, const int
     }
 }
 
+// Waves per workgroup: the level-10 kernel fits 256 registers (eight waves);
+// the others use up to 512 (one wave per SIMD).
 template <class P>
 struct LinWaves {
     static constexpr int value = 4;
+};
+template <>
+struct LinWaves<ProfLevel10> {
+    static constexpr int value = 8;
 };
 
 template <class P>
@@ -338,7 +357,8 @@ bool lin_configure(const DevModel &m, const DevLin &L, int n, int num_cus, size_
     if (sh + priv > lds_limit)
         return false;
     cfg.lds_tables = false;
-    cfg.waves = (int)std::min<size_t>(4, (lds_limit - sh) / priv);
+    const int wcap = efs_variant(m, m.R) == 2 ? 8 : 4;
+    cfg.waves = (int)std::min<size_t>(wcap, (lds_limit - sh) / priv);
     cfg.lds_bytes = sh + cfg.waves * priv;
     const int per_cu = std::max<int>(1, (int)(lds_limit / cfg.lds_bytes));
     const int need = (std::max(n, 1) + cfg.waves - 1) / cfg.waves;

@@ -667,36 +667,29 @@ bool build_lin_plan(const Model &m, const Plan &p, LinPlan &lp, std::string &err
     lp.part0 = lp.L0 + ((nL + 3) & ~3);
     const int P4 = (raw.max_partials + 3) & ~3;
     lp.acc = lp.part0 + P4;
-    lp.CH = 16;
-    lp.acc_rows = 3 * lp.CH;
-    lp.priv = lp.acc + lp.acc_rows * kRedStride;
-    lp.priv = (lp.priv + 3) & ~3;
+    lp.CH = kLinChunk;
+    lp.priv = lp.acc;
     if (lp.acc > 0xffff)
         return fail(err, "model too large for the linear-fit work space");
     auto same = [](int x) { return x; };
     encode_tables(raw, lp.part0, p.dummy, same, same, same, lp.steps, lp.level_step, lp.comb,
                   lp.level_comb);
-    // per chunk of scalars: {slot | s_local << 16, L index}, sorted by slot
+    // per chunk of kLinChunk scalars and per slot: a mask of the chunk's
+    // scalars whose support holds the slot's basic, and their L indices
+    // (`one` where the bit is clear)
     lp.nchunks = (m.S + lp.CH - 1) / lp.CH;
-    lp.ent_start.assign(1, 0);
-    for (int c = 0; c < lp.nchunks; ++c) {
-        std::vector<std::array<int, 3>> e;
-        for (int s = c * lp.CH; s < std::min(m.S, (c + 1) * lp.CH); ++s) {
-            const int x = m.map[s];
-            for (int b : supp[x])
-                e.push_back({slot_of[b], s - c * lp.CH, lws(x, b)});
-        }
-        std::stable_sort(e.begin(), e.end(),
-                         [](const std::array<int, 3> &a, const std::array<int, 3> &b) {
-                             return a[0] < b[0];
-                         });
-        for (auto &v : e) {
-            if (v[0] < 0 || v[2] < 0)
+    lp.slot_mask.assign((size_t)lp.nchunks * p.nslots, 0);
+    lp.slot_L.assign((size_t)lp.nchunks * p.nslots * kLinChunk, lp.one);
+    for (int s = 0; s < m.S; ++s) {
+        const int c = s / lp.CH, k = s % lp.CH, x = m.map[s];
+        for (int b : supp[x]) {
+            const int sl = slot_of[b], li = lws(x, b);
+            if (sl < 0 || li < 0)
                 return fail(err, "internal error: linear-fit support outside the slots");
-            lp.ent.push_back(v[0] | (v[1] << 16));
-            lp.ent.push_back(v[2]);
+            const size_t at = (size_t)c * p.nslots + sl;
+            lp.slot_mask[at] |= 1 << k;
+            lp.slot_L[at * kLinChunk + k] = li;
         }
-        lp.ent_start.push_back((int)lp.ent.size() / 2);
     }
     return true;
 }

@@ -141,14 +141,14 @@ bool build_plan(const Model &m, Plan &p, std::string &err);
 // Linear-fit plan (sparse Jacobian of the scalar moments w.r.t. the basic
 // moments, see build_lin_plan).  Work space per wave (doubles): the E/F/S
 // block [0, red0), the transpose buffer, `one` (1.0), the Jacobian values
-// [L0, L0 + nL), the step partials [part0, acc), the per-lane accumulators
-// acc_rows x kRedStride.
+// [L0, L0 + nL), the step partials [part0, acc); priv = acc.
+constexpr int kLinChunk = 8;  // scalars per pass (their derivatives live in registers)
 struct LinPlan {
-    int nL = 0, one = 0, L0 = 0, part0 = 0, acc = 0, acc_rows = 0, priv = 0;
-    int CH = 16, nchunks = 0;   // scalars per chunk
+    int nL = 0, one = 0, L0 = 0, part0 = 0, acc = 0, priv = 0;
+    int CH = kLinChunk, nchunks = 0;
     std::vector<int> level_step, steps, level_comb, comb;  // as Plan's rule tables
-    std::vector<int> ent;        // int2 {slot | s_local << 16, L index} per chunk, by slot
-    std::vector<int> ent_start;  // [nchunks + 1]
+    std::vector<int> slot_mask;  // [nchunks][nslots] bit k: scalar k of the chunk uses the slot
+    std::vector<int> slot_L;     // [nchunks][nslots][kLinChunk] L index of each bit
 };
 bool build_lin_plan(const Model &m, const Plan &p, LinPlan &lp, std::string &err);
 
@@ -225,8 +225,8 @@ struct DevLin {
     const int *level_step, *level_comb;  // [nlev + 1]
     const int2 *steps;
     const int4 *comb;
-    const int2 *ent;        // {slot | s_local << 16, L index}
-    const int *ent_start;   // [nchunks + 1]
+    const int *slot_mask;   // [nchunks][nslots]
+    const int *slot_L;      // [nchunks][nslots][kLinChunk]
 };
 struct LinOut {
     const int *center_structure;  // [n]
