@@ -89,7 +89,7 @@ __global__ __launch_bounds__(kWave *kMaxWaves) void efs_kernel(DevModel m, DevNe
                 mom[m.dup[2 * k]] = mom[m.dup[2 * k + 1]];
         wave_sync();
 
-        run_rules<false>(fwd_tab, m.fwd_level_step, m.fwd_level_comb, m.fwd_comb, m.nfwd, ws, lane, 0);
+        run_rules<false, false>(fwd_tab, m.fwd_level_step, m.fwd_level_comb, m.fwd_comb, m.nfwd, ws, lane, 0);
 
         // ---- site energy (potential_mtp.cpp:2966-2970) and adjoint seed ----
         double e = 0.0;
@@ -105,7 +105,7 @@ __global__ __launch_bounds__(kWave *kMaxWaves) void efs_kernel(DevModel m, DevNe
             A[k] = L.seed[k];
         wave_sync();
 
-        run_rules<false>(bwd_tab, m.bwd_level_step, m.bwd_level_comb, m.bwd_comb, m.nbwd, ws, lane, 0);
+        run_rules<false, true>(bwd_tab, m.bwd_level_step, m.bwd_level_comb, m.bwd_comb, m.nbwd, ws, lane, 0);
         if (lane == 0)
             for (int k = 0; k < m.ndup; ++k)
                 A[m.dup[2 * k + 1]] += A[m.dup[2 * k]];

@@ -94,16 +94,7 @@ __device__ __forceinline__ void reduce_rows_lin(const double *red, int nrows, in
                                                 Tgt tgt)
 {
     wave_sync();
-    const int s = lane & (kChunk - 1), qq = lane >> 4;
-    const double2 *row = reinterpret_cast<const double2 *>(red + s * kRedStride + qq * 16);
-    double a0 = 0.0, a1 = 0.0;
-#pragma unroll
-    for (int jj = 0; jj < 8; ++jj) {
-        const double2 v = row[jj];
-        a0 += v.x;
-        a1 += v.y;
-    }
-    const double acc = xor16_sum(xor32_sum(a0 + a1));
+    const double acc = chunk_row_sum(red, lane);
     if (lane < nrows)
         tgt(row0 + lane, acc);
     wave_sync();
@@ -153,7 +144,7 @@ __global__ __launch_bounds__(kWave *kMaxWaves) void lin_site_kernel(DevModel m, 
             for (int k = 0; k < m.ndup; ++k)
                 mom[m.dup[2 * k]] = mom[m.dup[2 * k + 1]];
         wave_sync();
-        run_rules<false>(m.fwd_steps, m.fwd_level_step, m.fwd_level_comb, m.fwd_comb, m.nfwd, ws,
+        run_rules<false, false>(m.fwd_steps, m.fwd_level_step, m.fwd_level_comb, m.fwd_comb, m.nfwd, ws,
                          lane, 0);
 
         // ---- energy components -------------------------------------------
@@ -166,7 +157,7 @@ __global__ __launch_bounds__(kWave *kMaxWaves) void lin_site_kernel(DevModel m, 
         for (int k = L.L0 + lane; k < L.L0 + L.nL; k += kWave)
             ws[k] = 0.0;
         wave_sync();
-        run_rules<false>(L.steps, L.level_step, L.level_comb, L.comb, L.nlev, ws, lane, 0);
+        run_rules<false, false>(L.steps, L.level_step, L.level_comb, L.comb, L.nlev, ws, lane, 0);
 
         // ---- force and stress components, CH scalars at a time ------------
         for (int ch = 0; ch < L.nchunks; ++ch) {

@@ -169,9 +169,9 @@ void emit_level(std::vector<Task> &tasks, RawTables &raw)
 }
 
 // Encodes raw entries into int2 work-space steps: x = l | r << 16,
-// y = w | first << 16 | c << 17.  map_l / map_r / map_w translate raw
-// operands and targets to work-space indices; partial p goes to part0 + p
-// and padding reads and writes `dummy`.
+// y = w | first << 16 | last << 17 | c << 18.  map_l / map_r / map_w
+// translate raw operands and targets to work-space indices; partial p goes
+// to part0 + p and padding reads `dummy` and writes nothing.
 template <class ML, class MR, class MW>
 void encode_tables(const RawTables &raw, int part0, int dummy, ML map_l, MR map_r, MW map_w,
                    std::vector<int> &steps, std::vector<int> &level_step, std::vector<int> &comb,
@@ -179,18 +179,31 @@ void encode_tables(const RawTables &raw, int part0, int dummy, ML map_l, MR map_
 {
     auto target = [&](int w) { return w <= -2 ? part0 + (-w - 2) : map_w(w); };
     steps.assign(raw.steps.size() * 2, 0);
+    const size_t nst = raw.steps.size() / kWave;
     for (size_t i = 0; i < raw.steps.size(); ++i) {
         const Ent &e = raw.steps[i];
-        int l, r, w;
+        int l, r, w, last = 0;
         if (e[0] < 0) {
             l = r = w = dummy;
         } else {
             l = map_l(e[0]);
             r = map_r(e[1]);
             w = target(e[3]);
+            // last entry of its task or piece: the lane's next step starts
+            // another one, is padding, or the level ends
+            const size_t st = i / kWave, q = i % kWave;
+            const bool level_end =
+                std::find(raw.level_step.begin(), raw.level_step.end(), (int)(st + 1)) !=
+                raw.level_step.end();
+            if (st + 1 >= nst || level_end)
+                last = 1;
+            else {
+                const Ent &nx = raw.steps[(st + 1) * kWave + q];
+                last = nx[0] < 0 || nx[4] != 0;
+            }
         }
         steps[2 * i] = l | (r << 16);
-        steps[2 * i + 1] = w | (e[4] << 16) | (int)((unsigned)e[2] << 17);
+        steps[2 * i + 1] = w | (e[4] << 16) | (last << 17) | (int)((unsigned)e[2] << 18);
     }
     level_step = raw.level_step;
     level_comb = raw.level_comb;
@@ -550,8 +563,8 @@ bool build_plan(const Model &m, Plan &p, std::string &err)
     if (p.priv_doubles > 0xffff)
         return fail(err, "model too large: per-atom work space exceeds 65535 doubles");
     for (int t = 0; t < m.T; ++t)
-        if (m.times[4 * t + 2] < -16384 || m.times[4 * t + 2] > 16383)
-            return fail(err, "product-rule multiplicity outside [-16384, 16383]");
+        if (m.times[4 * t + 2] < -8192 || m.times[4 * t + 2] > 8191)
+            return fail(err, "product-rule multiplicity outside [-8192, 8191]");
     auto same = [](int x) { return x; };
     auto adj = [&p](int x) { return p.K4 + x; };
     encode_tables(fwd, p.part0, p.dummy, same, same, same, p.fwd_steps, p.fwd_level_step,

@@ -69,6 +69,24 @@ __device__ __forceinline__ double xor16_sum(double v)
     return __hiloint2double(h[0], l[0]) + __hiloint2double(h[1], l[1]);
 }
 
+// Sum of one row of a reduction chunk (kChunk = 16 rows of 64 columns,
+// stride kRedStride): lane l sums row l & 15 over columns 16 (l >> 4) .. +15
+// with 16-byte reads, then the four column groups are combined (lanes l ^ 32,
+// l ^ 16); every lane of the row's group ends with the row total.
+__device__ __forceinline__ double chunk_row_sum(const double *red, int lane)
+{
+    const double2 *row =
+        reinterpret_cast<const double2 *>(red + (lane & (kChunk - 1)) * kRedStride + (lane >> 4) * 16);
+    double a0 = 0.0, a1 = 0.0;
+#pragma unroll
+    for (int jj = 0; jj < 8; ++jj) {
+        const double2 v = row[jj];
+        a0 += v.x;
+        a1 += v.y;
+    }
+    return xor16_sum(xor32_sum(a0 + a1));
+}
+
 __device__ __forceinline__ double wave_sum(double v)
 {
     v = xor32_sum(v);
@@ -188,21 +206,12 @@ __device__ __forceinline__ void next_shell(const double *prev, double *cur, cons
 
 // Sum `nrows` slots of the transpose buffer over the neighbour columns and
 // add the sums to the moment array.  Rows hold 64 columns; columns of lanes
-// without a neighbour hold zeros.
+// without a neighbour hold zeros.  Lanes 0 .. nrows-1 hold the row sums.
 __device__ __forceinline__ void reduce_chunk(const double *red, int nrows, int slot0,
                                              const int *slot_basic, double *mom, int lane)
 {
     wave_sync();
-    const int s = lane & (kChunk - 1), qq = lane >> 4;
-    const double2 *row = reinterpret_cast<const double2 *>(red + s * kRedStride + qq * 16);
-    double a0 = 0.0, a1 = 0.0;
-#pragma unroll
-    for (int jj = 0; jj < 8; ++jj) {
-        const double2 v = row[jj];
-        a0 += v.x;
-        a1 += v.y;
-    }
-    double acc = xor16_sum(xor32_sum(a0 + a1));
+    const double acc = chunk_row_sum(red, lane);
     if (lane < nrows) {
         const int b = slot_basic[slot0 + lane];
         if (b >= 0)
@@ -301,14 +310,16 @@ __device__ __forceinline__ void bwd_shells(const DevModel &m, const double4 *A4,
 // level at a time.  Steps are taken in groups of four: the entries of the
 // next group are loaded while the current one runs, and every operand of a
 // group is read before any of its results is written (a level never reads
-// what it writes).
+// what it writes).  A task's sum starts from its target's value (kInit:
+// adjoints, which start from their seeds) or from zero (outputs and partial
+// sums, which start at zero), and is written on the task's last entry.
 //
 // kDual also carries a second copy of the work space `delta` doubles further
 // on: for a step  x_w += c x_l x_r  it adds  c (x'_l x_r + x_l x'_r)  to x'_w.
 // Forward entries then propagate tangents (Q_o += c (Q_l m_r + m_l Q_r));
 // reverse entries, whose l is an adjoint and r a moment, propagate the
 // adjoint of the tangent computation (G_x += c (G_o m_r + A_o Q_r)).
-template <bool kDual>
+template <bool kDual, bool kInit>
 __device__ __forceinline__ void run_rules(const int2 *tab, const int *level_step,
                                           const int *level_comb, const int4 *comb, int nlev,
                                           double *ws, int lane, int delta)
@@ -329,36 +340,32 @@ __device__ __forceinline__ void run_rules(const int2 *tab, const int *level_step
                     nx[2] = u[2 * kWave];
                     nx[3] = u[3 * kWave];
                 }
-                double ml[4], mr[4], init[4], v[4];
-                double dl[4], dr[4], dinit[4], dv[4];
+                double ml[4], mr[4], init[4];
+                double dl[4], dr[4], dinit[4];
 #pragma unroll
                 for (int k = 0; k < 4; ++k) {
                     const int l = e[k].x & 0xffff, r = (unsigned)e[k].x >> 16, w = e[k].y & 0xffff;
                     ml[k] = ws[l];
                     mr[k] = ws[r];
-                    init[k] = ws[w];
+                    init[k] = kInit ? ws[w] : 0.0;
                     if constexpr (kDual) {
                         dl[k] = wd[l];
                         dr[k] = wd[r];
-                        dinit[k] = wd[w];
+                        dinit[k] = kInit ? wd[w] : 0.0;
                     }
                 }
 #pragma unroll
                 for (int k = 0; k < 4; ++k) {
-                    const double c = (double)(e[k].y >> 17);
+                    const double c = (double)(e[k].y >> 18);
                     const bool first = e[k].y & 0x10000;
                     acc = fma(c * ml[k], mr[k], first ? init[k] : acc);
-                    v[k] = acc;
-                    if constexpr (kDual) {
-                        acd = fma(c * ml[k], dr[k], fma(c * dl[k], mr[k], first ? dinit[k] : acd));
-                        dv[k] = acd;
-                    }
-                }
-#pragma unroll
-                for (int k = 0; k < 4; ++k) {
-                    ws[e[k].y & 0xffff] = v[k];
                     if constexpr (kDual)
-                        wd[e[k].y & 0xffff] = dv[k];
+                        acd = fma(c * ml[k], dr[k], fma(c * dl[k], mr[k], first ? dinit[k] : acd));
+                    if (e[k].y & 0x20000) {
+                        ws[e[k].y & 0xffff] = acc;
+                        if constexpr (kDual)
+                            wd[e[k].y & 0xffff] = acd;
+                    }
                 }
 #pragma unroll
                 for (int k = 0; k < 4; ++k)

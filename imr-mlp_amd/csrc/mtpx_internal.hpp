@@ -120,8 +120,10 @@ struct Plan {
     // Lane-major step tables, one per direction.  Level L owns steps
     // [level_step[L], level_step[L+1]) (a multiple of 4); step s of lane q is
     // entry s * 64 + q, an int2 of work-space indices:
-    //   x = l | r << 16,  y = w | first << 16 | c << 17  (c signed)
-    //   acc = c * ws[l] * ws[r] + (first ? ws[w] : acc);  ws[w] = acc
+    //   x = l | r << 16,  y = w | first << 16 | last << 17 | c << 18  (c signed)
+    //   acc = c * ws[l] * ws[r] + (first ? init : acc);  if (last) ws[w] = acc
+    // with init = ws[w] for targets that start from a value (adjoints and
+    // their seeds) and 0 otherwise.
     // Forward entries read two moments and write a rule output; reverse
     // entries read an adjoint and a moment and write an adjoint (whose
     // initial value is its seed).  A task (all rules of one output, or all

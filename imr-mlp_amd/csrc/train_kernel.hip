@@ -168,16 +168,7 @@ __device__ __forceinline__ void reduce_rows(const double *red, int nrows, int ro
                                             Tgt tgt)
 {
     wave_sync();
-    const int s = lane & (kChunk - 1), qq = lane >> 4;
-    const double2 *row = reinterpret_cast<const double2 *>(red + s * kRedStride + qq * 16);
-    double a0 = 0.0, a1 = 0.0;
-#pragma unroll
-    for (int jj = 0; jj < 8; ++jj) {
-        const double2 v = row[jj];
-        a0 += v.x;
-        a1 += v.y;
-    }
-    const double acc = xor16_sum(xor32_sum(a0 + a1));
+    const double acc = chunk_row_sum(red, lane);
     if (lane < nrows)
         tgt(row0 + lane, acc);
     wave_sync();
@@ -190,9 +181,9 @@ __device__ __forceinline__ void reduce_rows_typed(const double *red, int nrows, 
                                                   int lane, const int *ctype, int Z, Tgt tgt)
 {
     wave_sync();
-    const int s = lane & (kChunk - 1), qq = lane >> 4;
-    const double2 *row = reinterpret_cast<const double2 *>(red + s * kRedStride + qq * 16);
-    const int4 *ty = reinterpret_cast<const int4 *>(ctype + qq * 16);
+    const double2 *row = reinterpret_cast<const double2 *>(red + (lane & (kChunk - 1)) * kRedStride +
+                                                           (lane >> 4) * 16);
+    const int4 *ty = reinterpret_cast<const int4 *>(ctype + (lane >> 4) * 16);
     double v[16];
     int t[16];
 #pragma unroll
@@ -434,7 +425,7 @@ __global__ __launch_bounds__(kWave *kMaxWaves) void grad_kernel(DevModel m, DevN
         wave_sync();
 
         // ---- 2. rules forward with tangents; moment and species gradient ----
-        run_rules<true>(fwd_tab, m.fwd_level_step, m.fwd_level_comb, m.fwd_comb, m.nfwd, ws, lane,
+        run_rules<true, false>(fwd_tab, m.fwd_level_step, m.fwd_level_comb, m.fwd_comb, m.nfwd, ws, lane,
                         m.tr_delta);
         for (int s = lane; s < m.S; s += kWave) {
             const int x = L.map[s];
@@ -450,7 +441,7 @@ __global__ __launch_bounds__(kWave *kMaxWaves) void grad_kernel(DevModel m, DevN
             wd[m.K4 + k] = se * sd;
         }
         wave_sync();
-        run_rules<true>(bwd_tab, m.bwd_level_step, m.bwd_level_comb, m.bwd_comb, m.nbwd, ws, lane,
+        run_rules<true, true>(bwd_tab, m.bwd_level_step, m.bwd_level_comb, m.bwd_comb, m.nbwd, ws, lane,
                         m.tr_delta);
         if (lane == 0)
             for (int k = 0; k < m.ndup; ++k) {
