@@ -218,8 +218,10 @@ int check_species(mtpx_context *ctx)
     return MTPX_OK;
 }
 
-int run_efs(mtpx_context *ctx, bool deterministic, bool site_virial)
+int run_efs(mtpx_context *ctx, bool deterministic, bool site_virial, bool energy_only)
 {
+    if (energy_only)
+        deterministic = false;
     if (!ctx->has_model)
         return set_error(ctx, MTPX_E_NO_MODEL, "no model loaded");
     if (!ctx->has_nbh)
@@ -266,11 +268,15 @@ int run_efs(mtpx_context *ctx, bool deterministic, bool site_virial)
         out.site_virial = ctx->site_virial.as<double>();
     }
     DevNeighbors nb = dev_neighbors(ctx);
-    if (!deterministic && n > 0)
+    if (!deterministic && !energy_only && n > 0)
         HIP_TRY(hipMemsetAsync(out.forces, 0, sizeof(double) * 3 * n, s), "clear forces");
     HIP_TRY(hipEventRecord(ctx->ev[0], s), "record event");
     if (n > 0)
-        HIP_TRY(launch_efs(ctx->dm, nb, out, cfg, deterministic, s), "launch efs kernel");
+        HIP_TRY(launch_efs(ctx->dm, nb, out, cfg,
+                           (deterministic ? kEfsDeterministic : 0) |
+                               (energy_only ? kEfsEnergyOnly : 0),
+                           s),
+                "launch efs kernel");
     HIP_TRY(hipEventRecord(ctx->ev[1], s), "record event");
     if (n > 0)
         HIP_TRY(launch_efs_finish(nb, out, cfg.rows, deterministic, ctx->rev_offsets.as<int>(),
@@ -619,6 +625,37 @@ int mtpx_efs(mtpx_context *ctx, int deterministic, double *energy, double *force
         HIP_TRY(hipMemcpy(site_energies, ctx->site_energy.p, sizeof(double) * ctx->n,
                           hipMemcpyDeviceToHost),
                 "copy site energies");
+    return MTPX_OK;
+}
+
+int mtpx_energy(mtpx_context *ctx, double *energies, double *site_energies)
+{
+    if (!ctx)
+        return MTPX_E_INVALID;
+    (void)hipSetDevice(ctx->device);
+    int rc = run_efs(ctx, false, false, true);
+    if (rc != MTPX_OK)
+        return rc;
+    const int nc = ctx->nconf, n = ctx->n;
+    if (energies && nc > 0) {
+        HIP_TRY(ctx->benergy.ensure(sizeof(double) * nc), "allocate energies");
+        if (n > 0)
+            HIP_TRY(launch_structure_reduce(ctx->soff.as<int>(), nc, ctx->site_energy.as<double>(),
+                                            nullptr, ctx->benergy.as<double>(), nullptr,
+                                            ctx->stream),
+                    "launch structure reduction");
+        else
+            HIP_TRY(hipMemsetAsync(ctx->benergy.p, 0, sizeof(double) * nc, ctx->stream), "clear");
+        HIP_TRY(hipMemcpyAsync(energies, ctx->benergy.p, sizeof(double) * nc,
+                               hipMemcpyDeviceToHost, ctx->stream),
+                "copy energies");
+    }
+    if (site_energies && n > 0)
+        HIP_TRY(hipMemcpyAsync(site_energies, ctx->site_energy.p, sizeof(double) * n,
+                               hipMemcpyDeviceToHost, ctx->stream),
+                "copy site energies");
+    HIP_TRY(hipStreamSynchronize(ctx->stream), "energy");
+    ctx->has_batch_out = false;
     return MTPX_OK;
 }
 

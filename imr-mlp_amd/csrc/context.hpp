@@ -129,8 +129,10 @@ hipError_t upload(DBuf &b, const std::vector<T> &v, hipStream_t s)
 }
 
 // Runs the E/F/S kernel over the resident topology (capi.cpp); with
-// site_virial the per-atom virials are written too.
-int run_efs(mtpx_context *ctx, bool deterministic, bool site_virial = false);
+// site_virial the per-atom virials are written too; energy_only skips the
+// gradient (site energies and the total only).
+int run_efs(mtpx_context *ctx, bool deterministic, bool site_virial = false,
+            bool energy_only = false);
 // Marks the topology as one structure of all atoms.
 int set_single_structure(mtpx_context *ctx);
 // MTPX_E_INVALID when the lists hold a species the model does not have.

@@ -41,8 +41,9 @@ namespace {
 
 template <class P, bool kTabLds, int kMaxWaves>
 __global__ __launch_bounds__(kWave *kMaxWaves) void efs_kernel(DevModel m, DevNeighbors nb,
-                                                               EfsOut out, int deterministic)
+                                                               EfsOut out, int flags)
 {
+    const bool deterministic = flags & kEfsDeterministic;
     extern __shared__ double lds[];
     const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
     const int nwaves = blockDim.x / kWave;
@@ -101,6 +102,8 @@ __global__ __launch_bounds__(kWave *kMaxWaves) void efs_kernel(DevModel m, DevNe
             out.site_energy[i] = site_energy;
             e_acc += site_energy;
         }
+        if (flags & kEfsEnergyOnly)  // getE (potential_mtp.cpp:2604-2621): no gradient
+            continue;
         for (int k = lane; k < m.K; k += kWave)
             A[k] = L.seed[k];
         wave_sync();
@@ -313,9 +316,9 @@ int efs_variant(const DevModel &m, int R)
 }
 
 hipError_t launch_efs(const DevModel &m, const DevNeighbors &nb, const EfsOut &out,
-                      const EfsLaunch &cfg, bool deterministic, hipStream_t s)
+                      const EfsLaunch &cfg, int flags, hipStream_t s)
 {
-    const int det = deterministic ? 1 : 0;
+    const int det = flags;
     switch (efs_variant(m, m.R)) {
     case 0: launch_variant<ProfLevel16>(m, nb, out, cfg, det, s); break;
     case 1: launch_variant<ProfLevel20>(m, nb, out, cfg, det, s); break;

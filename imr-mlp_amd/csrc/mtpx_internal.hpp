@@ -219,8 +219,11 @@ struct EfsLaunch {
 bool efs_configure(const DevModel &m, int n, int num_cus, int max_waves, size_t lds_limit,
                    EfsLaunch &cfg);
 int efs_variant(const DevModel &m, int R);
+// launch_efs flags: ordered force assembly; site energies and energy only.
+constexpr int kEfsDeterministic = 1;
+constexpr int kEfsEnergyOnly = 2;
 hipError_t launch_efs(const DevModel &m, const DevNeighbors &nb, const EfsOut &out,
-                      const EfsLaunch &cfg, bool deterministic, hipStream_t s);
+                      const EfsLaunch &cfg, int flags, hipStream_t s);
 // Linear fit (lin_kernel.hip).
 struct DevLin {
     int nL, one, L0, part0, acc, priv, CH, nchunks, nlev;

@@ -1,6 +1,7 @@
 // Training kernels for gfx950 (fp64).
 //
 //   structure_reduce_kernel  per-structure energy and virial from site values
+//                            (the virial when per-atom virials are given)
 //   loss_kernel              weighted E/F/S loss, its adjoints dL/dE, dL/dF,
 //                            dL/dS and the seven metrics, one wave per
 //                            structure (Trainer_MTP::AddLossGard,
@@ -50,9 +51,10 @@ __global__ __launch_bounds__(kWave) void structure_reduce_kernel(const int *soff
     double e = 0.0, v[9] = {0, 0, 0, 0, 0, 0, 0, 0, 0};
     for (int i = soff[c] + lane; i < soff[c + 1]; i += kWave) {
         e += site_energy[i];
+        if (site_virial)
 #pragma unroll
-        for (int k = 0; k < 9; ++k)
-            v[k] += site_virial[9 * (size_t)i + k];
+            for (int k = 0; k < 9; ++k)
+                v[k] += site_virial[9 * (size_t)i + k];
     }
     e = wave_sum(e);
 #pragma unroll
@@ -60,9 +62,10 @@ __global__ __launch_bounds__(kWave) void structure_reduce_kernel(const int *soff
         v[k] = wave_sum(v[k]);
     if (lane == 0) {
         energy[c] = e;
+        if (stress)
 #pragma unroll
-        for (int k = 0; k < 9; ++k)
-            stress[9 * (size_t)c + k] = v[k];
+            for (int k = 0; k < 9; ++k)
+                stress[9 * (size_t)c + k] = v[k];
     }
 }
 

@@ -63,6 +63,7 @@ def lib():
         L.mtpx_set_neighbors.argtypes = [C.c_void_p, C.c_int, _ip, _ip, _ip, _dp, _dp, _ip]
         L.mtpx_efs.argtypes = [C.c_void_p, C.c_int, _dp, _dp, _dp, _dp]
         L.mtpx_efs_device.argtypes = [C.c_void_p, C.c_int]
+        L.mtpx_energy.argtypes = [C.c_void_p, _dp, _dp]
         L.mtpx_last_timings.argtypes = [C.c_void_p, _dp]
         L.mtpx_set_structures.argtypes = [C.c_void_p, C.c_int, _ip, _dp, _ip, _dp, _ip,
                                           C.c_double]
@@ -250,6 +251,18 @@ class Context:
         self._check(lib().mtpx_efs(self.h, int(deterministic), C.byref(E), _d(F), _d(S), _d(se)),
                     "efs")
         return E.value, F[:n], S, se[:n]
+
+    def energy(self):
+        """getE: per-structure energies and site energies."""
+        n, _ = self.neighbor_count()
+        try:
+            nc = self.structure_count()
+        except MtpxError:
+            nc = 1
+        E = np.zeros(max(nc, 1))
+        se = np.zeros(max(n, 1))
+        self._check(lib().mtpx_energy(self.h, _d(E), _d(se)), "energy")
+        return E[:nc], se[:n]
 
     def efs_device(self, deterministic: bool = False):
         self._check(lib().mtpx_efs_device(self.h, int(deterministic)), "efs_device")

@@ -118,6 +118,11 @@ int mtpx_set_neighbors(mtpx_context *ctx, int n, const int *offsets, const int *
  * orders every reduction (no floating-point atomics): byte-repeatable. */
 int mtpx_efs(mtpx_context *ctx, int deterministic, double *energy, double *forces,
              double *stress, double *site_energies);
+/* PotMTP::getE (potentials/potential_mtp.cpp:2604-2621, over
+ * CalcSiteBasisImpl :3024-3122): energies only, no gradient.  energies
+ * [nconf] (one per structure of the resident topology), site_energies [N];
+ * either may be NULL. */
+int mtpx_energy(mtpx_context *ctx, double *energies, double *site_energies);
 /* Same computation, outputs left on the device (benchmarking). */
 int mtpx_efs_device(mtpx_context *ctx, int deterministic);
 /* Device-side timing of the last mtpx_efs_device / mtpx_efs call, measured

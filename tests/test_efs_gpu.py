@@ -149,3 +149,34 @@ def test_full_size_workload2_matches_oracle(ctx):
     assert abs(Eg - seg.sum()) <= 1e-12 * np.abs(seg).sum()
     assert np.abs(Fg.sum(axis=0)).max() < 1e-9 * np.abs(Fg).max() * np.sqrt(len(Fg))
     assert np.abs(Sg - Sg.T).max() < 1e-9 * np.abs(Sg).max()
+
+
+@pytest.mark.parametrize("name,model_text,s", CASES[:4], ids=[c[0] for c in CASES[:4]])
+def test_energy_only_matches_oracle_get_e(ctx, name, model_text, s):
+    """getE: energies without the gradient, the same numbers as mtpx_efs."""
+    m = O.Model(model_text)
+    pos = O.wrap(s.cell, s.pbc, s.pos)
+    nb = O.Neighbors.build(s.cell, s.pbc, pos, s.types, m.cutoff)
+    Eo, seo = O.energy(m, nb)
+    ctx.load_model_text(model_text)
+    ctx.build_neighbors(s.cell, s.pbc, pos, s.types, m.cutoff)
+    E, se = ctx.energy()
+    assert rel_err(E[0], Eo) < 1e-10 and rel_err(se, seo) < 1e-10
+    E2, _, _, se2 = ctx.efs()
+    assert np.array_equal(se, se2)
+
+
+def test_energy_only_per_structure(ctx):
+    text, _ = S.training_models(4)
+    m = O.Model(text)
+    structs = S.training_structures(4, 5)
+    for st in structs:
+        st.pos = O.wrap(st.cell, st.pbc, st.pos)
+    ctx.load_model_text(text)
+    off = ctx.set_structures(structs, 5.0)
+    E, se = ctx.energy()
+    for c, st in enumerate(structs):
+        nb = O.Neighbors.build(st.cell, st.pbc, st.pos, st.types, 5.0)
+        Eo, seo = O.energy(m, nb)
+        assert rel_err(E[c], Eo) < 1e-10
+        assert rel_err(se[off[c]:off[c + 1]], seo) < 1e-10
