@@ -125,7 +125,21 @@ int install_model(mtpx_context *ctx, Model &&m)
         HIP_TRY(upload(ctx->lin_comb, lp.comb, s), "upload model");
         HIP_TRY(upload(ctx->lin_ent, lp.slot_L, s), "upload model");
         HIP_TRY(upload(ctx->lin_estart, lp.slot_mask, s), "upload model");
+        HIP_TRY(upload(ctx->lin_chunk, lp.chunk_s0, s), "upload model");
+        HIP_TRY(upload(ctx->lin_maskw, lp.maskw, s), "upload model");
+        HIP_TRY(upload(ctx->lin_clist, lp.clist, s), "upload model");
+        HIP_TRY(upload(ctx->lin_flevel, lp.fwd_level_step, s), "upload model");
+        HIP_TRY(upload(ctx->lin_fsteps, lp.fwd_steps, s), "upload model");
+        HIP_TRY(upload(ctx->lin_flcomb, lp.fwd_level_comb, s), "upload model");
+        HIP_TRY(upload(ctx->lin_fcomb, lp.fwd_comb, s), "upload model");
         DevLin &L = ctx->dl;
+        L.dummy = lp.dummy;
+        L.red0 = lp.red0;
+        L.nfwd = (int)lp.fwd_level_step.size() - 1;
+        L.fwd_level_step = ctx->lin_flevel.as<int>();
+        L.fwd_level_comb = ctx->lin_flcomb.as<int>();
+        L.fwd_steps = ctx->lin_fsteps.as<int2>();
+        L.fwd_comb = ctx->lin_fcomb.as<int4>();
         L.nL = lp.nL;
         L.one = lp.one;
         L.L0 = lp.L0;
@@ -141,6 +155,10 @@ int install_model(mtpx_context *ctx, Model &&m)
         L.comb = ctx->lin_comb.as<int4>();
         L.slot_L = ctx->lin_ent.as<int>();
         L.slot_mask = ctx->lin_estart.as<int>();
+        L.chunk_s0 = ctx->lin_chunk.as<int>();
+        L.maskw = ctx->lin_maskw.as<int>();
+        L.clist = ctx->lin_clist.as<int>();
+        L.lane_walk = lp.lane_walk ? 1 : 0;
     }
     int rc = upload_coeffs(ctx);
     if (rc != MTPX_OK)
@@ -169,12 +187,23 @@ DevNeighbors dev_neighbors(const mtpx_context *ctx)
     return nb;
 }
 
-namespace {
-
 // Ordered reverse index: for each atom k, the pairs p with idx[p] == k, in
-// ascending p (used by the deterministic force gather).
-int build_reverse_index(mtpx_context *ctx, const int *idx_host)
+// ascending p (the deterministic force gather and the linear-fit gather);
+// also keeps the list offsets on the host.
+int ensure_reverse_index(mtpx_context *ctx)
 {
+    if (ctx->rev_ready)
+        return MTPX_OK;
+    std::vector<int> idx_host((size_t)std::max<int64_t>(ctx->P, 1));
+    ctx->offsets_host.assign((size_t)ctx->n + 1, 0);
+    if (ctx->P > 0)
+        HIP_TRY(hipMemcpy(idx_host.data(), ctx->idx.p, sizeof(int) * ctx->P,
+                          hipMemcpyDeviceToHost),
+                "copy neighbour indices");
+    if (ctx->n > 0)
+        HIP_TRY(hipMemcpy(ctx->offsets_host.data(), ctx->offsets.p, sizeof(int) * (ctx->n + 1),
+                          hipMemcpyDeviceToHost),
+                "copy neighbour offsets");
     std::vector<int> roff((size_t)ctx->n + 1, 0), rp((size_t)std::max<int64_t>(ctx->P, 1));
     for (int64_t p = 0; p < ctx->P; ++p)
         roff[(size_t)idx_host[p] + 1]++;
@@ -189,8 +218,6 @@ int build_reverse_index(mtpx_context *ctx, const int *idx_host)
     ctx->rev_ready = true;
     return MTPX_OK;
 }
-
-}  // namespace
 
 int set_single_structure(mtpx_context *ctx)
 {
@@ -228,16 +255,9 @@ int run_efs(mtpx_context *ctx, bool deterministic, bool site_virial, bool energy
         return set_error(ctx, MTPX_E_NO_TOPOLOGY, "no neighbour lists");
     if (int rc = check_species(ctx))
         return rc;
-    if (deterministic && !ctx->rev_ready) {
-        std::vector<int> idx_host((size_t)std::max<int64_t>(ctx->P, 1));
-        if (ctx->P > 0)
-            HIP_TRY(hipMemcpy(idx_host.data(), ctx->idx.p, sizeof(int) * ctx->P,
-                              hipMemcpyDeviceToHost),
-                    "copy neighbour indices");
-        int rc = build_reverse_index(ctx, idx_host.data());
-        if (rc != MTPX_OK)
+    if (deterministic)
+        if (int rc = ensure_reverse_index(ctx))
             return rc;
-    }
     const int n = ctx->n;
     hipStream_t s = ctx->stream;
     // MTPX_EFS_WAVES (tuning): cap on the waves per workgroup

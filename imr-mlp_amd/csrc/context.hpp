@@ -33,6 +33,7 @@ struct mtpx_context {
     DBuf &offsets = nbh.offsets, &idx = nbh.idx, &type = nbh.type, &x = nbh.x, &y = nbh.y,
          &z = nbh.z, &d = nbh.d, &center_type = nbh.center_type;
     DBuf rev_offsets, rev_pairs;
+    std::vector<int> offsets_host;  // [n+1], kept with the reverse index
     bool rev_ready = false;
     int max_species = -1;  // largest species index in the lists
 
@@ -55,14 +56,19 @@ struct mtpx_context {
     // host copies of the labels (linear-fit rows)
     std::vector<int> active_h;
     std::vector<double> tE_h, wE_h, tF_h, wF_h, tS_h, wS_h;
+    long label_gen = 0;  // bumped by every set_labels
 
     // linear fit: plan, components [fc | sc | ec], row descriptors, Gram
     bool has_lin = false;
     std::string lin_err;
     LinPlan lin;
     DevLin dl{};
-    DBuf lin_level, lin_steps, lin_lcomb, lin_comb, lin_ent, lin_estart;
-    DBuf comp, row_src, row_sw, row_y, rowsA, rowsY, gram_part, gram_out;
+    DBuf lin_level, lin_steps, lin_lcomb, lin_comb, lin_ent, lin_estart, lin_chunk, lin_maskw,
+        lin_clist, lin_flevel, lin_fsteps, lin_flcomb, lin_fcomb;
+    DBuf comp, row_src, row_sw, row_y, rowsA, rowsY, gram_part, gram_out, lin_pair, lin_site;
+    long rows_gen = -1;  // label_gen and p of the uploaded row descriptors
+    int rows_p = -1;
+    int64_t rows_R = 0;
     double lin_timings[4] = {0, 0, 0, 0};
     double train_timings[4] = {0, 0, 0, 0};
     hipEvent_t tev[4] = {nullptr, nullptr, nullptr, nullptr};
@@ -81,8 +87,10 @@ struct mtpx_context {
                         &metric_rows, &metrics, &grad_rows, &grad, &nbh_tmp.offsets,
                         &nbh_tmp.idx, &nbh_tmp.type, &nbh_tmp.x, &nbh_tmp.y, &nbh_tmp.z,
                         &nbh_tmp.d, &nbh_tmp.center_type, &lin_level, &lin_steps, &lin_lcomb,
-                        &lin_comb, &lin_ent, &lin_estart, &comp, &row_src, &row_sw, &row_y,
-                        &rowsA, &rowsY, &gram_part, &gram_out})
+                        &lin_comb, &lin_ent, &lin_estart, &lin_chunk, &lin_maskw, &lin_clist,
+                        &comp, &row_src, &row_sw, &row_y, &rowsA, &rowsY, &gram_part, &gram_out,
+                        &lin_pair, &lin_site, &lin_flevel, &lin_fsteps, &lin_flcomb,
+                        &lin_fcomb})
             b->release();
         scratch.release_all();
         for (auto &e : ev)
@@ -135,6 +143,8 @@ int run_efs(mtpx_context *ctx, bool deterministic, bool site_virial = false,
             bool energy_only = false);
 // Marks the topology as one structure of all atoms.
 int set_single_structure(mtpx_context *ctx);
+// Reverse index of the resident lists (and their offsets on the host).
+int ensure_reverse_index(mtpx_context *ctx);
 // MTPX_E_INVALID when the lists hold a species the model does not have.
 int check_species(mtpx_context *ctx);
 // Device view of the resident lists.

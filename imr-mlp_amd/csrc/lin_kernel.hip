@@ -1,12 +1,15 @@
 // Linear-fit kernels for gfx950 (fp64).
 //
-//   lin_site_kernel   E/F/S components of every linear coefficient
-//                     (PotMTP::CalcEFSCmpt_R, potentials/potential_mtp.cpp:
-//                     2675-2707, over CalcSiteBasisDers, :3163-3280): for a
-//                     species column, the atom count; for a moment column
-//                     s, sum_i m_map(s), dm/dr_j scattered into the force
-//                     rows of i and of its neighbours, and -sum dm/dr_j r_j
-//                     into the stress rows.
+//   lin_site_kernel   per site: the scalar moments (energy components) and,
+//                     for every neighbour entry, dm_s/dr_j of every scalar s
+//                     into a pair buffer (PotMTP::CalcEFSCmpt_R,
+//                     potentials/potential_mtp.cpp:2675-2707, over
+//                     CalcSiteBasisDers, :3163-3280)
+//   lin_gather_kernel force rows sum_j dm/dr_j - sum_{i: j of i} dm_i/dr_j
+//                     and per-atom stress partials -sum_j dm/dr_j r_j, read
+//                     from the pair buffer through the lists and the
+//                     reverse index (fixed order, no atomics)
+//   lin_reduce_kernel energy and stress components per structure, ordered
 //   rows_kernel       AddLinearFast rows (train/train_mtp.cpp:1289-1395):
 //                     component rows scaled by sqrt(w), targets sqrt(w) y
 //   gram_kernel       [A y]^T [A y] on the fp64 matrix cores
@@ -17,9 +20,12 @@
 // Here the scalar moments are differentiated through the sparse site
 // Jacobian L[s][b] = dm_map(s)/dm_b instead: L is computed once per site by
 // a step table (the rule-table machinery), then lanes take neighbours and
-// accumulate dm_s/dr_j = sum_b L[s][b] grad_r(f_b Y_b)(r_j) for a chunk of
-// scalars at a time.
+// form dm_s/dr_j = sum_b L[s][b] grad_r(f_b Y_b)(r_j) for a chunk of
+// scalars at a time.  Structures are processed in groups whose pair buffer
+// fits a fixed budget.
 #include "mtp_device.hpp"
+
+#include <type_traits>
 
 namespace mtpx {
 
@@ -27,38 +33,154 @@ namespace {
 
 typedef double d4v __attribute__((ext_vector_type(4)));
 
-// Walk of the slots (nu, mu, alpha) with the chunk's entries: for a slot
-// that has entries, grad_r(f Y) = (f' - nu f/d) Y u + (f/d) grad_u Y is
-// formed once and added, times L, to each of the slot's scalars.
-// Walk of the slots (nu, mu, alpha) for one chunk of scalars: where the
-// chunk's mask of the slot is set, grad_r(f Y) = (f' - nu f/d) Y u +
-// (f/d) grad_u Y is formed once and added, times L, to those scalars'
-// derivatives (registers; the mask and its bits are wave-uniform).
+// The tables of one chunk for a walk.  Compile-time walks (exact
+// profiles) hold the chunk's slot masks (4 per word) and its L values in
+// walk order in two lane registers each and read them with readlane: no
+// memory access and no dependent load in the walk.  Runtime walks read the
+// per-slot mask and L-index tables.
+struct LinWalk {
+    const int *mask;  // [nslots]
+    const int *lidx;  // [nslots][kLinChunk]
+    int mw0, mw1;     // lane l: mask words l and 64 + l
+    double lc0, lc1;  // lane l: L values of entries l and 64 + l
+    int pos;          // next entry (uniform)
+};
+
+__device__ __forceinline__ double readlane_d(double v, int l)
+{
+    const long long b = __double_as_longlong(v);
+    const int lo = __builtin_amdgcn_readlane((int)b, l);
+    const int hi = __builtin_amdgcn_readlane((int)(b >> 32), l);
+    return __longlong_as_double(((long long)hi << 32) | (unsigned)lo);
+}
+
+// Compile-time loop: f(integral_constant<int, I>) for I in [B, E).
+template <int B, int E, class F>
+__device__ __forceinline__ void static_for(F &&f)
+{
+    if constexpr (B < E) {
+        f(std::integral_constant<int, B>{});
+        static_for<B + 1, E>(f);
+    }
+}
+
+// Inverse of shell_index: the (a, b) of the i-th monomial of shell nu.
+constexpr int shell_a(int nu, int i)
+{
+    int a = nu;
+    while (i > nu - a) {
+        i -= nu - a + 1;
+        --a;
+    }
+    return a;
+}
+constexpr int shell_b(int nu, int i)
+{
+    int a = nu;
+    while (i > nu - a) {
+        i -= nu - a + 1;
+        --a;
+    }
+    return nu - a - i;
+}
+constexpr bool shell_inverse_ok()
+{
+    for (int nu = 0; nu <= kMaxNu; ++nu)
+        for (int i = 0; i < shell_size(nu); ++i)
+            if (shell_index(nu, shell_a(nu, i), shell_b(nu, i)) != i || shell_b(nu, i) < 0)
+                return false;
+    return true;
+}
+static_assert(shell_inverse_ok(), "shell_a/shell_b must invert shell_index");
+
+// The entries of one slot of the chunk: each scalar k whose bit is set in
+// the slot's mask gets L[k][slot] * grad_r(f Y) added to its derivative
+// (registers; the mask and its bits are wave-uniform).
+template <class P>
+__device__ __forceinline__ void lin_apply(int mk, int sl, double gx, double gy, double gz,
+                                          LinWalk &w, const double *ws,
+                                          double (&acc)[3 * kLinChunk])
+{
+    static_for<0, kLinChunk>([&](auto K) __attribute__((always_inline)) {
+        constexpr int k = decltype(K)::value;
+        if (mk & (1 << k)) {
+            double lv;
+            if constexpr (P::exact) {
+                const int e = w.pos++;
+                lv = readlane_d(e < 64 ? w.lc0 : w.lc1, e & 63);
+            } else {
+                lv = ws[w.lidx[(size_t)sl * kLinChunk + k]];
+            }
+            acc[3 * k] += lv * gx;
+            acc[3 * k + 1] += lv * gy;
+            acc[3 * k + 2] += lv * gz;
+        }
+    });
+}
+
+// Walk of the slots (nu, mu, alpha) in slot order for one chunk.  Where the
+// chunk's mask of a slot is set, grad_r(f Y) = (f' - nu f/d) Y u + (f/d)
+// grad_u Y is formed once and applied to the slot's entries.  The exact
+// profiles walk at compile time (constant slot and monomial indices, masks
+// read from lane registers); the runtime profiles loop and read the mask
+// table.
 template <int NU, class P>
-__device__ __forceinline__ void lin_shells(const DevModel &m, const DevLin &L, const Nbr<P::M> &q,
-                                           const double *prev, int &slot, const int *mask,
-                                           const int *lidx, const double *ws,
-                                           double (&acc)[3 * kLinChunk])
+__device__ __forceinline__ void lin_shells(const DevModel &m, const Nbr<P::M> &q,
+                                           const double *prev, int &slot, LinWalk &w,
+                                           const double *ws, double (&acc)[3 * kLinChunk])
 {
     double cur[shell_size(NU)];
     if constexpr (NU == 0)
         cur[0] = 1.0;
     else
         next_shell<NU, P::M>(prev, cur, q);
-#pragma unroll
-    for (int mu = 0; mu < P::M; ++mu) {
-        if (P::active(m, mu, NU)) {
-            __builtin_amdgcn_sched_barrier(0);
-            const double h = q.fd[mu] - NU * q.f[mu] * q.invd;
-            const double fdi = q.f[mu] * q.invd;
-#pragma unroll
-            for (int a = NU; a >= 0; --a)
-#pragma unroll
-                for (int b = NU - a; b >= 0; --b) {
-                    const int i = shell_index(NU, a, b);
+    if constexpr (P::exact) {
+        static_for<0, P::M>([&](auto MU) __attribute__((always_inline)) {
+            constexpr int mu = decltype(MU)::value;
+            if (P::active(m, mu, NU)) {
+                __builtin_amdgcn_sched_barrier(0);
+                const double h = q.fd[mu] - NU * q.f[mu] * q.invd;
+                const double fdi = q.f[mu] * q.invd;
+                static_for<0, shell_size(NU)>([&](auto I) __attribute__((always_inline)) {
+                    constexpr int i = decltype(I)::value;
+                    constexpr int a = shell_a(NU, i), b = shell_b(NU, i), c = NU - a - b;
                     const int sl = slot + i;
-                    const int mk = mask[sl];
+                    const int word = sl / 4 < 64 ? __builtin_amdgcn_readlane(w.mw0, sl / 4)
+                                                 : __builtin_amdgcn_readlane(w.mw1, sl / 4 - 64);
+                    const int mk = (word >> (8 * (sl % 4))) & 0xff;
                     if (mk) {
+                        const double hy = h * cur[i];
+                        double gx = hy * q.ux, gy = hy * q.uy, gz = hy * q.uz;
+                        if constexpr (a > 0) {
+                            constexpr int ix = shell_index(NU - 1, a - 1, b);
+                            gx += (a * fdi) * prev[ix];
+                        }
+                        if constexpr (b > 0) {
+                            constexpr int iy = shell_index(NU - 1, a, b - 1);
+                            gy += (b * fdi) * prev[iy];
+                        }
+                        if constexpr (c > 0) {
+                            constexpr int iz = shell_index(NU - 1, a, b);
+                            gz += (c * fdi) * prev[iz];
+                        }
+                        lin_apply<P>(mk, sl, gx, gy, gz, w, ws, acc);
+                    }
+                });
+                slot += shell_size(NU);
+            }
+        });
+    } else {
+#pragma unroll
+        for (int mu = 0; mu < P::M; ++mu) {
+            if (P::active(m, mu, NU)) {
+                const double h = q.fd[mu] - NU * q.f[mu] * q.invd;
+                const double fdi = q.f[mu] * q.invd;
+                for (int a = NU; a >= 0; --a)
+                    for (int b = NU - a; b >= 0; --b) {
+                        const int i = shell_index(NU, a, b), sl = slot + i;
+                        const int mk = w.mask[sl];
+                        if (!mk)
+                            continue;
                         const double hy = h * cur[i];
                         double gx = hy * q.ux, gy = hy * q.uy, gz = hy * q.uz;
                         if constexpr (NU > 0) {
@@ -69,63 +191,50 @@ __device__ __forceinline__ void lin_shells(const DevModel &m, const DevLin &L, c
                             if (NU - a - b > 0)
                                 gz += ((NU - a - b) * fdi) * prev[shell_index(NU - 1, a, b)];
                         }
-                        const int *li = lidx + (size_t)sl * kLinChunk;
-#pragma unroll
-                        for (int k = 0; k < kLinChunk; ++k)
-                            if (mk & (1 << k)) {
-                                const double lv = ws[li[k]];
-                                acc[3 * k] += lv * gx;
-                                acc[3 * k + 1] += lv * gy;
-                                acc[3 * k + 2] += lv * gz;
-                            }
+                        lin_apply<P>(mk, sl, gx, gy, gz, w, ws, acc);
                     }
-                }
-            slot += shell_size(NU);
+                slot += shell_size(NU);
+            }
         }
     }
     if constexpr (NU < P::NUMAX) {
         if (P::deeper(m, NU))
-            lin_shells<NU + 1, P>(m, L, q, cur, slot, mask, lidx, ws, acc);
+            lin_shells<NU + 1, P>(m, q, cur, slot, w, ws, acc);
     }
 }
 
-template <class Tgt>
-__device__ __forceinline__ void reduce_rows_lin(const double *red, int nrows, int row0, int lane,
-                                                Tgt tgt)
+// Makes the neighbour's values opaque to the optimiser (no instruction):
+// the shell values of a chunk walk are then recomputed per chunk instead of
+// being hoisted out of the chunk loop, which would keep all of them live.
+template <int MMAX>
+__device__ __forceinline__ void opaque(Nbr<MMAX> &q)
 {
-    wave_sync();
-    const double acc = chunk_row_sum(red, lane);
-    if (lane < nrows)
-        tgt(row0 + lane, acc);
-    wave_sync();
+    asm volatile("" : "+v"(q.d), "+v"(q.invd), "+v"(q.ux), "+v"(q.uy), "+v"(q.uz));
+#pragma unroll
+    for (int mu = 0; mu < MMAX; ++mu)
+        asm volatile("" : "+v"(q.f[mu]), "+v"(q.fd[mu]));
 }
 
 template <class P, int kMaxWaves>
 __global__ __launch_bounds__(kWave *kMaxWaves) void lin_site_kernel(DevModel m, DevLin L,
-                                                                    DevNeighbors nb, LinOut out)
+                                                                    DevNeighbors nb, LinGroup g)
 {
     extern __shared__ double lds[];
     const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
     const int nwaves = blockDim.x / kWave;
     const Shared Ls = shared_layout(m, lds);
     double *ws = lds + shared_doubles(m, false) + (size_t)wave * L.priv;
-    double *mom = ws, *red = ws + m.red0;
-    const int p = m.Z + m.S;
+    double *mom = ws, *red = ws + L.red0;
 
     stage_shared(m, Ls, false, tid, blockDim.x);
-    for (int k = m.dummy + lane; k < m.red0; k += kWave)
-        ws[k] = 0.0;
-    for (int k = L.one + lane; k < L.L0; k += kWave)
-        ws[k] = k == L.one ? 1.0 : 0.0;
-    for (int k = L.part0 + lane; k < L.acc; k += kWave)
+    for (int k = L.dummy + lane; k < L.red0; k += kWave)
         ws[k] = 0.0;
     __syncthreads();
 
-    for (int i = blockIdx.x * nwaves + wave; i < nb.n; i += gridDim.x * nwaves) {
+    for (int i = g.a0 + blockIdx.x * nwaves + wave; i < g.a1; i += gridDim.x * nwaves) {
         const int ti = nb.center_type[i];
         const int beg = nb.offsets[i];
         const int n = nb.offsets[i + 1] - beg;
-        const int c = out.center_structure[i];
         for (int k = lane; k < m.K; k += kWave)
             mom[k] = 0.0;
         wave_sync();
@@ -144,88 +253,157 @@ __global__ __launch_bounds__(kWave *kMaxWaves) void lin_site_kernel(DevModel m, 
             for (int k = 0; k < m.ndup; ++k)
                 mom[m.dup[2 * k]] = mom[m.dup[2 * k + 1]];
         wave_sync();
-        run_rules<false, false>(m.fwd_steps, m.fwd_level_step, m.fwd_level_comb, m.fwd_comb, m.nfwd, ws,
-                         lane, 0);
+        run_rules<false, false>(L.fwd_steps, L.fwd_level_step, L.fwd_level_comb, L.fwd_comb,
+                                L.nfwd, ws, lane, 0);
 
-        // ---- energy components -------------------------------------------
+        // ---- the site's scalar moments (energy components) ---------------
+        double *srow = g.site + (size_t)(i - g.a0) * 10 * m.S + 9 * m.S;
         for (int s = lane; s < m.S; s += kWave)
-            atomicAdd(&out.ec[(size_t)c * p + m.Z + s], mom[Ls.map[s]]);
-        if (lane == 0)
-            atomicAdd(&out.ec[(size_t)c * p + ti], 1.0);
+            srow[s] = mom[Ls.map[s]];
 
-        // ---- site Jacobian of the scalars w.r.t. the basics ----------------
-        for (int k = L.L0 + lane; k < L.L0 + L.nL; k += kWave)
-            ws[k] = 0.0;
+        // ---- site Jacobian of the scalars w.r.t. the basics (its space lies
+        // over the transpose buffer of the moments) ------------------------
+        for (int k = L.one + lane; k < L.L0 + L.nL; k += kWave)
+            ws[k] = k == L.one ? 1.0 : 0.0;
         wave_sync();
         run_rules<false, false>(L.steps, L.level_step, L.level_comb, L.comb, L.nlev, ws, lane, 0);
 
-        // ---- force and stress components, CH scalars at a time ------------
-        for (int ch = 0; ch < L.nchunks; ++ch) {
-            const int s0 = ch * L.CH, nch = min(L.CH, m.S - s0);
-            const int *mask = L.slot_mask + (size_t)ch * m.nslots;
-            const int *lidx = L.slot_L + (size_t)ch * m.nslots * kLinChunk;
-            for (int base = 0; base < n; base += kWave) {
+        // ---- dm_s/dr_j of every entry, a chunk of scalars at a time, into
+        // the pair buffer [entry][3][Sp] (the lane's entry)
+        for (int base = 0; base < n; base += kWave) {
+            const bool valid = lane < n - base;
+            const int64_t pe = beg + base + lane;
+            Nbr<P::M> q;
+            load_neighbor<P>(m, nb, Ls.coef, ti, pe, valid, q);
+            double *dst = g.pair + (size_t)(pe - g.e0) * 3 * g.Sp;
+            for (int ch = 0; ch < L.nchunks; ++ch) {
+                const int s0 = L.chunk_s0[ch], nch = L.chunk_s0[ch + 1] - s0;
+                LinWalk w;
+                w.pos = 0;
+                if constexpr (P::exact) {
+                    const int *mwp = L.maskw + (size_t)ch * kLinMaskWords;
+                    const int *clp = L.clist + (size_t)ch * kLinEntries;
+                    w.mw0 = mwp[lane];
+                    w.mw1 = mwp[kWave + lane];
+                    w.lc0 = ws[clp[lane]];
+                    w.lc1 = ws[clp[kWave + lane]];
+                } else {
+                    w.mask = L.slot_mask + (size_t)ch * m.nslots;
+                    w.lidx = L.slot_L + (size_t)ch * m.nslots * kLinChunk;
+                }
                 double acc[3 * kLinChunk];
 #pragma unroll
                 for (int r = 0; r < 3 * kLinChunk; ++r)
                     acc[r] = 0.0;
-                const bool valid = lane < n - base;
-                const int64_t pe = beg + base + lane;
-                Nbr<P::M> q;
-                load_neighbor<P>(m, nb, Ls.coef, ti, pe, valid, q);
+                opaque(q);
                 int slot = 0;
-                lin_shells<0, P>(m, L, q, nullptr, slot, mask, lidx, ws, acc);
-                // the site's own rows: + sum_j dm/dr_j
-                int row = 0;
-                auto flush_self = [&](int nrows) {
-                    reduce_rows_lin(red, nrows, row - nrows, lane, [&](int r, double v) {
-                        atomicAdd(&out.fc[((size_t)i * 3 + r % 3) * p + m.Z + s0 + r / 3], v);
-                    });
-                };
-#pragma unroll
-                for (int r = 0; r < 3 * kLinChunk; ++r)
-                    if (r < 3 * nch) {
-                        red[(row % kChunk) * kRedStride + lane] = acc[r];
-                        ++row;
-                        if (row % kChunk == 0)
-                            flush_self(kChunk);
-                    }
-                if (row % kChunk)
-                    flush_self(row % kChunk);
-                // the neighbours' rows: - dm/dr_j
+                lin_shells<0, P>(m, q, nullptr, slot, w, ws, acc);
                 if (valid) {
-                    const int j = nb.idx[pe];
 #pragma unroll
-                    for (int r = 0; r < 3 * kLinChunk; ++r)
-                        if (r < 3 * nch)
-                            atomicAdd(&out.fc[((size_t)j * 3 + r % 3) * p + m.Z + s0 + r / 3],
-                                      -acc[r]);
+                    for (int a = 0; a < 3; ++a)
+#pragma unroll
+                        for (int k = 0; k < kLinChunk; ++k)
+                            if (k < nch)
+                                dst[a * g.Sp + s0 + k] = acc[3 * k + a];
                 }
-                // stress rows: - sum_j (dm/dr_j)_a r_jb
-                const double rv[3] = {q.x, q.y, q.z};
-                row = 0;
-                auto flush = [&](int nrows) {
-                    reduce_rows_lin(red, nrows, row - nrows, lane, [&](int r, double v) {
-                        atomicAdd(&out.sc[((size_t)c * 9 + r % 9) * p + m.Z + s0 + r / 9], v);
-                    });
-                };
-#pragma unroll
-                for (int sl = 0; sl < kLinChunk; ++sl)
-                    if (sl < nch)
-#pragma unroll
-                        for (int a = 0; a < 3; ++a)
-#pragma unroll
-                            for (int b = 0; b < 3; ++b) {
-                                red[(row % kChunk) * kRedStride + lane] = -acc[3 * sl + a] * rv[b];
-                                ++row;
-                                if (row % kChunk == 0)
-                                    flush(kChunk);
-                            }
-                if (row % kChunk)
-                    flush(row % kChunk);
             }
         }
         wave_sync();
+    }
+}
+
+// Force rows and per-atom stress partials of a group from the pair buffer,
+// one thread per (atom, scalar), in a fixed order:
+//   fc[i][a][Z+s] = sum_{e in list(i)} D_e[a][s] - sum_{e: idx[e] = i} D_e[a][s]
+//   site[i][3a+b][s] = -sum_{e in list(i)} D_e[a][s] r_e[b]
+__global__ __launch_bounds__(256) void lin_gather_kernel(int S, int Z, int p, DevNeighbors nb,
+                                                         const int *rev_off, const int *rev_pairs,
+                                                         LinGroup g, double *fc)
+{
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= (int64_t)(g.a1 - g.a0) * S)
+        return;
+    const int il = (int)(t / S), s = (int)(t % S);
+    const int i = g.a0 + il;
+    const size_t st = 3 * (size_t)g.Sp;
+    const double *D = g.pair - (size_t)g.e0 * st + s;
+    double f0 = 0.0, f1 = 0.0, f2 = 0.0;
+    double sv[9];
+#pragma unroll
+    for (int q = 0; q < 9; ++q)
+        sv[q] = 0.0;
+#pragma unroll 4
+    for (int e = nb.offsets[i], e1 = nb.offsets[i + 1]; e < e1; ++e) {
+        const double *d = D + (size_t)e * st;
+        const double dx = d[0], dy = d[g.Sp], dz = d[2 * g.Sp];
+        const double r[3] = {nb.x[e], nb.y[e], nb.z[e]};
+        f0 += dx;
+        f1 += dy;
+        f2 += dz;
+#pragma unroll
+        for (int b = 0; b < 3; ++b) {
+            sv[b] -= dx * r[b];
+            sv[3 + b] -= dy * r[b];
+            sv[6 + b] -= dz * r[b];
+        }
+    }
+#pragma unroll 4
+    for (int k = rev_off[i], k1 = rev_off[i + 1]; k < k1; ++k) {
+        const double *d = D + (size_t)rev_pairs[k] * st;
+        f0 -= d[0];
+        f1 -= d[g.Sp];
+        f2 -= d[2 * g.Sp];
+    }
+    double *f = fc + (size_t)i * 3 * p + Z + s;
+    f[0] = f0;
+    f[p] = f1;
+    f[2 * p] = f2;
+    double *srow = g.site + (size_t)il * 10 * S + s;
+#pragma unroll
+    for (int q = 0; q < 9; ++q)
+        srow[q * S] = sv[q];
+}
+
+// Energy and stress components of a group's structures: ordered sums of the
+// site rows over each structure's atoms, and the species counts.
+__global__ __launch_bounds__(256) void lin_reduce_kernel(int S, int Z, int p, const int *soff,
+                                                         const int *center_type, LinGroup g,
+                                                         double *ec, double *sc)
+{
+    const int w = 10 * S + Z;
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= (int64_t)(g.c1 - g.c0) * w)
+        return;
+    const int c = g.c0 + (int)(t / w), r = (int)(t % w);
+    const int i0 = soff[c], i1 = soff[c + 1];
+    if (r < 10 * S) {
+        const int q = r / S, s = r % S;
+        // loads of several atoms in flight; the sum stays in atom order
+        const double *src = g.site + (size_t)(i0 - g.a0) * 10 * S + r;
+        const size_t st = 10 * (size_t)S;
+        double acc = 0.0;
+        int i = i0;
+        for (; i + 8 <= i1; i += 8, src += 8 * st) {
+            double v[8];
+#pragma unroll
+            for (int k = 0; k < 8; ++k)
+                v[k] = src[k * st];
+#pragma unroll
+            for (int k = 0; k < 8; ++k)
+                acc += v[k];
+        }
+        for (; i < i1; ++i, src += st)
+            acc += *src;
+        if (q < 9)
+            sc[((size_t)c * 9 + q) * p + Z + s] = acc;
+        else
+            ec[(size_t)c * p + Z + s] = acc;
+    } else {
+        const int sp = r - 10 * S;
+        int cnt = 0;
+        for (int i = i0; i < i1; ++i)
+            cnt += center_type[i] == sp;
+        ec[(size_t)c * p + sp] = (double)cnt;
     }
 }
 
@@ -331,14 +509,22 @@ struct LinWaves<ProfLevel10> {
 
 template <class P>
 void launch_lin_variant(const DevModel &m, const DevLin &L, const DevNeighbors &nb,
-                        const LinOut &out, const EfsLaunch &cfg, hipStream_t s)
+                        const LinGroup &g, const EfsLaunch &cfg, hipStream_t s)
 {
     constexpr int W = LinWaves<P>::value;
     hipLaunchKernelGGL((lin_site_kernel<P, W>), dim3(cfg.grid), dim3(kWave * cfg.waves),
-                       cfg.lds_bytes, s, m, L, nb, out);
+                       cfg.lds_bytes, s, m, L, nb, g);
 }
 
 }  // namespace
+
+// The E/F/S variant, or the generic one where the compile-time walk's
+// tables do not hold the plan.
+int lin_variant(const DevModel &m, const DevLin &L)
+{
+    const int v = efs_variant(m, m.R);
+    return v <= 2 && !L.lane_walk ? 4 : v;
+}
 
 bool lin_configure(const DevModel &m, const DevLin &L, int n, int num_cus, size_t lds_limit,
                    EfsLaunch &cfg)
@@ -348,7 +534,7 @@ bool lin_configure(const DevModel &m, const DevLin &L, int n, int num_cus, size_
     if (sh + priv > lds_limit)
         return false;
     cfg.lds_tables = false;
-    const int wcap = efs_variant(m, m.R) == 2 ? 8 : 4;
+    const int wcap = lin_variant(m, L) == 2 ? 8 : 4;
     cfg.waves = (int)std::min<size_t>(wcap, (lds_limit - sh) / priv);
     cfg.lds_bytes = sh + cfg.waves * priv;
     const int per_cu = std::max<int>(1, (int)(lds_limit / cfg.lds_bytes));
@@ -359,15 +545,37 @@ bool lin_configure(const DevModel &m, const DevLin &L, int n, int num_cus, size_
 }
 
 hipError_t launch_lin_site(const DevModel &m, const DevLin &L, const DevNeighbors &nb,
-                           const LinOut &out, const EfsLaunch &cfg, hipStream_t s)
+                           const LinGroup &g, const EfsLaunch &cfg, hipStream_t s)
 {
-    switch (efs_variant(m, m.R)) {
-    case 0: launch_lin_variant<ProfLevel16>(m, L, nb, out, cfg, s); break;
-    case 1: launch_lin_variant<ProfLevel20>(m, L, nb, out, cfg, s); break;
-    case 2: launch_lin_variant<ProfLevel10>(m, L, nb, out, cfg, s); break;
-    case 3: launch_lin_variant<ProfSmall>(m, L, nb, out, cfg, s); break;
-    default: launch_lin_variant<ProfGeneric>(m, L, nb, out, cfg, s); break;
+    if (g.a1 <= g.a0)
+        return hipSuccess;
+    switch (lin_variant(m, L)) {
+    case 0: launch_lin_variant<ProfLevel16>(m, L, nb, g, cfg, s); break;
+    case 1: launch_lin_variant<ProfLevel20>(m, L, nb, g, cfg, s); break;
+    case 2: launch_lin_variant<ProfLevel10>(m, L, nb, g, cfg, s); break;
+    case 3: launch_lin_variant<ProfSmall>(m, L, nb, g, cfg, s); break;
+    default: launch_lin_variant<ProfGeneric>(m, L, nb, g, cfg, s); break;
     }
+    return hipGetLastError();
+}
+
+hipError_t launch_lin_gather(const DevModel &m, const DevNeighbors &nb, const int *rev_off,
+                             const int *rev_pairs, const LinGroup &g, double *fc, hipStream_t s)
+{
+    const int64_t work = (int64_t)(g.a1 - g.a0) * m.S;
+    if (work > 0)
+        hipLaunchKernelGGL(lin_gather_kernel, dim3((unsigned)((work + 255) / 256)), dim3(256), 0,
+                           s, m.S, m.Z, m.Z + m.S, nb, rev_off, rev_pairs, g, fc);
+    return hipGetLastError();
+}
+
+hipError_t launch_lin_reduce(const DevModel &m, const int *soff, const int *center_type,
+                             const LinGroup &g, double *ec, double *sc, hipStream_t s)
+{
+    const int64_t work = (int64_t)(g.c1 - g.c0) * (10 * m.S + m.Z);
+    if (work > 0)
+        hipLaunchKernelGGL(lin_reduce_kernel, dim3((unsigned)((work + 255) / 256)), dim3(256), 0,
+                           s, m.S, m.Z, m.Z + m.S, soff, center_type, g, ec, sc);
     return hipGetLastError();
 }
 

@@ -6,6 +6,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
 
 namespace {
@@ -26,7 +27,18 @@ CompLayout comp_layout(const mtpx_context *ctx)
     return l;
 }
 
-// Components of every structure of the resident topology into ctx->comp.
+// Pair-buffer budget of one group of structures (MTPX_LIN_PAIR_MB, tuning);
+// a structure larger than the budget forms a group of its own.
+size_t pair_budget()
+{
+    const char *e = getenv("MTPX_LIN_PAIR_MB");
+    const long v = e ? atol(e) : 0;
+    return (v > 0 ? (size_t)v : (size_t)1024) << 20;
+}
+
+// Components of every structure of the resident topology into ctx->comp,
+// group by group: site kernel (pair buffer and scalar moments), gather
+// (force rows, per-atom stress partials), ordered per-structure reduction.
 int run_lin(mtpx_context *ctx)
 {
     if (!ctx->has_model)
@@ -45,18 +57,63 @@ int run_lin(mtpx_context *ctx)
         HIP_TRY(hipMemsetAsync(ctx->comp.p, 0, sizeof(double) * cl.total, s), "clear components");
     if (ctx->n == 0)
         return MTPX_OK;
-    EfsLaunch cfg;
-    if (!lin_configure(ctx->dm, ctx->dl, ctx->n, ctx->num_cus, ctx->lds_limit, cfg))
-        return set_error(ctx, MTPX_E_CAPACITY,
-                         "model needs more LDS than a CU provides for the linear fit");
-    LinOut out;
+    if (int rc = ensure_reverse_index(ctx))
+        return rc;
+    const DevModel &m = ctx->dm;
+    const int S = m.S;
+    const int Sp = (S + kLinChunk - 1) / kLinChunk * kLinChunk;
+    const size_t per_entry = sizeof(double) * 3 * (size_t)Sp;
+    const std::vector<int> &off = ctx->offsets_host;
+    const size_t budget = pair_budget();
+
+    // groups of whole structures
+    struct Range {
+        int c0, c1;
+    };
+    std::vector<Range> groups;
+    size_t max_entries = 1, max_atoms = 1;
+    for (int c0 = 0; c0 < ctx->nconf;) {
+        int c1 = c0 + 1;
+        auto entries = [&](int cb, int ce) {
+            return (size_t)(off[ctx->soff_host[ce]] - off[ctx->soff_host[cb]]);
+        };
+        while (c1 < ctx->nconf && entries(c0, c1 + 1) * per_entry <= budget)
+            ++c1;
+        groups.push_back({c0, c1});
+        max_entries = std::max(max_entries, entries(c0, c1));
+        max_atoms = std::max(max_atoms, (size_t)(ctx->soff_host[c1] - ctx->soff_host[c0]));
+        c0 = c1;
+    }
+    HIP_TRY(ctx->lin_pair.ensure(per_entry * max_entries), "allocate pair buffer");
+    HIP_TRY(ctx->lin_site.ensure(sizeof(double) * 10 * (size_t)S * max_atoms),
+            "allocate site rows");
+
     double *comp = ctx->comp.as<double>();
-    out.center_structure = ctx->center_structure.as<int>();
-    out.fc = comp + cl.fc;
-    out.sc = comp + cl.sc;
-    out.ec = comp + cl.ec;
-    HIP_TRY(launch_lin_site(ctx->dm, ctx->dl, dev_neighbors(ctx), out, cfg, s),
-            "launch linear-fit kernel");
+    const DevNeighbors nb = dev_neighbors(ctx);
+    for (const Range &r : groups) {
+        LinGroup g;
+        g.c0 = r.c0;
+        g.c1 = r.c1;
+        g.a0 = ctx->soff_host[r.c0];
+        g.a1 = ctx->soff_host[r.c1];
+        g.e0 = off[g.a0];
+        g.Sp = Sp;
+        g.pair = ctx->lin_pair.as<double>();
+        g.site = ctx->lin_site.as<double>();
+        if (g.a1 > g.a0) {
+            EfsLaunch cfg;
+            if (!lin_configure(m, ctx->dl, g.a1 - g.a0, ctx->num_cus, ctx->lds_limit, cfg))
+                return set_error(ctx, MTPX_E_CAPACITY,
+                                 "model needs more LDS than a CU provides for the linear fit");
+            HIP_TRY(launch_lin_site(m, ctx->dl, nb, g, cfg, s), "launch linear-fit site kernel");
+            HIP_TRY(launch_lin_gather(m, nb, ctx->rev_offsets.as<int>(),
+                                      ctx->rev_pairs.as<int>(), g, comp + cl.fc, s),
+                    "launch linear-fit gather");
+        }
+        HIP_TRY(launch_lin_reduce(m, ctx->soff.as<int>(), ctx->center_type.as<int>(), g,
+                                  comp + cl.ec, comp + cl.sc, s),
+                "launch linear-fit reduction");
+    }
     return MTPX_OK;
 }
 
@@ -68,6 +125,10 @@ int build_rows(mtpx_context *ctx, int64_t &R)
     if (!ctx->has_labels)
         return set_error(ctx, MTPX_E_INVALID, "no labels");
     const CompLayout cl = comp_layout(ctx);
+    if (ctx->rows_gen == ctx->label_gen && ctx->rows_p == cl.p) {
+        R = ctx->rows_R;  // descriptors of these labels are resident
+        return MTPX_OK;
+    }
     std::vector<int64_t> src;
     std::vector<double> sw, yw;
     for (int c = 0; c < ctx->nconf; ++c) {
@@ -103,6 +164,9 @@ int build_rows(mtpx_context *ctx, int64_t &R)
     HIP_TRY(upload(ctx->row_src, src, ctx->stream), "upload rows");
     HIP_TRY(upload(ctx->row_sw, sw, ctx->stream), "upload rows");
     HIP_TRY(upload(ctx->row_y, yw, ctx->stream), "upload rows");
+    ctx->rows_gen = ctx->label_gen;
+    ctx->rows_p = cl.p;
+    ctx->rows_R = R;
     return MTPX_OK;
 }
 

@@ -435,6 +435,34 @@ bool validate_model(const Model &m, std::string &err)
     return true;
 }
 
+namespace {
+
+// Forward rule tasks: outputs of each level, an output's rules in file
+// order.
+void forward_tables(const Model &m, const std::vector<int> &level, int maxl, RawTables &fwd)
+{
+    std::vector<std::vector<int>> by_out((size_t)m.K);
+    for (int t = 0; t < m.T; ++t)
+        by_out[m.times[4 * t + 3]].push_back(t);
+    for (int L = 1; L <= maxl; ++L) {
+        std::vector<Task> tasks;
+        for (int o = 0; o < m.K; ++o) {
+            if (level[o] != L || by_out[o].empty())
+                continue;
+            Task task;
+            for (int t : by_out[o]) {
+                const int *r = &m.times[4 * t];
+                task.push_back({r[0], r[1], r[2], o, 0});
+            }
+            task[0][4] = 1;
+            tasks.push_back(std::move(task));
+        }
+        emit_level(tasks, fwd);
+    }
+}
+
+}  // namespace
+
 // Canonical slot order shared with the kernels: for nu ascending, for mu
 // ascending (mu with numax[mu] >= nu), for alpha in the shell of degree nu
 // enumerated a = nu..0, b = nu-a..0, c = nu-a-b.
@@ -511,26 +539,8 @@ bool build_plan(const Model &m, Plan &p, std::string &err)
     p.dummy = 2 * K4;
     p.part0 = 2 * K4 + 4;
 
-    // Forward: outputs of each level, an output's rules in file order.
-    std::vector<std::vector<int>> by_out((size_t)m.K);
-    for (int t = 0; t < m.T; ++t)
-        by_out[m.times[4 * t + 3]].push_back(t);
     RawTables fwd, bwd;
-    for (int L = 1; L <= maxl; ++L) {
-        std::vector<Task> tasks;
-        for (int o = 0; o < m.K; ++o) {
-            if (level[o] != L || by_out[o].empty())
-                continue;
-            Task task;
-            for (int t : by_out[o]) {
-                const int *r = &m.times[4 * t];
-                task.push_back({r[0], r[1], r[2], o, 0});
-            }
-            task[0][4] = 1;
-            tasks.push_back(std::move(task));
-        }
-        emit_level(tasks, fwd);
-    }
+    forward_tables(m, level, maxl, fwd);
 
     // Reverse: destinations of each level from the top down; a destination's
     // entries in reverse file order, the right operand's entry of a rule
@@ -630,8 +640,16 @@ bool build_lin_plan(const Model &m, const Plan &p, LinPlan &lp, std::string &err
         if (need[r[3]])
             need[r[0]] = need[r[1]] = 1;
     }
-    // work-space layout (doubles): E/F/S block, transpose buffer, one, L
-    lp.one = p.red0 + kChunk * kRedStride;
+    // Work-space layout (doubles): moments, a zero slot, the forward
+    // partials, then the transpose buffer of the moment reduction, with
+    // {one, L, L partials} over it (they are set after the moments).  The
+    // forward rules are encoded again for this layout (no adjoint block).
+    RawTables fwd;
+    forward_tables(m, level, p.max_level, fwd);
+    lp.dummy = p.K4;
+    lp.fpart0 = lp.dummy + 4;
+    lp.red0 = lp.fpart0 + ((fwd.max_partials + 3) & ~3);
+    lp.one = lp.red0;
     lp.L0 = lp.one + 4;
     std::vector<int> lbase((size_t)K, -1);
     int nL = 0;
@@ -681,29 +699,63 @@ bool build_lin_plan(const Model &m, const Plan &p, LinPlan &lp, std::string &err
     const int P4 = (raw.max_partials + 3) & ~3;
     lp.acc = lp.part0 + P4;
     lp.CH = kLinChunk;
-    lp.priv = lp.acc;
-    if (lp.acc > 0xffff)
+    lp.priv = std::max(lp.acc, lp.red0 + kChunk * kRedStride);
+    if (lp.priv > 0xffff)
         return fail(err, "model too large for the linear-fit work space");
     auto same = [](int x) { return x; };
-    encode_tables(raw, lp.part0, p.dummy, same, same, same, lp.steps, lp.level_step, lp.comb,
+    encode_tables(fwd, lp.fpart0, lp.dummy, same, same, same, lp.fwd_steps, lp.fwd_level_step,
+                  lp.fwd_comb, lp.fwd_level_comb);
+    encode_tables(raw, lp.part0, lp.dummy, same, same, same, lp.steps, lp.level_step, lp.comb,
                   lp.level_comb);
-    // per chunk of kLinChunk scalars and per slot: a mask of the chunk's
+    // Chunks of consecutive scalars: at most kLinChunk scalars and at most
+    // kLinEntries (slot, scalar) entries each (a scalar with more entries
+    // makes a chunk of its own).  Per chunk and slot: a mask of the chunk's
     // scalars whose support holds the slot's basic, and their L indices
-    // (`one` where the bit is clear)
-    lp.nchunks = (m.S + lp.CH - 1) / lp.CH;
+    // (`one` where the bit is clear); for the compile-time walks also the
+    // masks packed four per word and the L indices in walk order (slot
+    // ascending, then scalar).
+    lp.chunk_s0.assign(1, 0);
+    for (int s = 0, cnt = 0, ent = 0; s < m.S; ++s) {
+        const int e = (int)supp[m.map[s]].size();
+        if (cnt > 0 && (cnt == kLinChunk || ent + e > kLinEntries)) {
+            lp.chunk_s0.push_back(s);
+            cnt = ent = 0;
+        }
+        ++cnt;
+        ent += e;
+        lp.max_chunk_entries = std::max(lp.max_chunk_entries, ent);
+    }
+    lp.chunk_s0.push_back(m.S);
+    lp.nchunks = (int)lp.chunk_s0.size() - 1;
     lp.slot_mask.assign((size_t)lp.nchunks * p.nslots, 0);
     lp.slot_L.assign((size_t)lp.nchunks * p.nslots * kLinChunk, lp.one);
-    for (int s = 0; s < m.S; ++s) {
-        const int c = s / lp.CH, k = s % lp.CH, x = m.map[s];
-        for (int b : supp[x]) {
-            const int sl = slot_of[b], li = lws(x, b);
-            if (sl < 0 || li < 0)
-                return fail(err, "internal error: linear-fit support outside the slots");
-            const size_t at = (size_t)c * p.nslots + sl;
-            lp.slot_mask[at] |= 1 << k;
-            lp.slot_L[at * kLinChunk + k] = li;
+    for (int c = 0; c < lp.nchunks; ++c)
+        for (int s = lp.chunk_s0[c]; s < lp.chunk_s0[c + 1]; ++s) {
+            const int k = s - lp.chunk_s0[c], x = m.map[s];
+            for (int b : supp[x]) {
+                const int sl = slot_of[b], li = lws(x, b);
+                if (sl < 0 || li < 0)
+                    return fail(err, "internal error: linear-fit support outside the slots");
+                const size_t at = (size_t)c * p.nslots + sl;
+                lp.slot_mask[at] |= 1 << k;
+                lp.slot_L[at * kLinChunk + k] = li;
+            }
         }
-    }
+    lp.lane_walk = p.nslots <= 4 * kLinMaskWords && lp.max_chunk_entries <= kLinEntries;
+    lp.maskw.assign((size_t)lp.nchunks * kLinMaskWords, 0);
+    lp.clist.assign((size_t)lp.nchunks * kLinEntries, lp.one);
+    if (lp.lane_walk)
+        for (int c = 0; c < lp.nchunks; ++c) {
+            int e = 0;
+            for (int sl = 0; sl < p.nslots; ++sl) {
+                const size_t at = (size_t)c * p.nslots + sl;
+                const int mk = lp.slot_mask[at];
+                lp.maskw[(size_t)c * kLinMaskWords + sl / 4] |= mk << (8 * (sl % 4));
+                for (int k = 0; k < kLinChunk; ++k)
+                    if (mk & (1 << k))
+                        lp.clist[(size_t)c * kLinEntries + e++] = lp.slot_L[at * kLinChunk + k];
+            }
+        }
     return true;
 }
 

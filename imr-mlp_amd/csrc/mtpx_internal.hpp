@@ -145,12 +145,20 @@ bool build_plan(const Model &m, Plan &p, std::string &err);
 // block [0, red0), the transpose buffer, `one` (1.0), the Jacobian values
 // [L0, L0 + nL), the step partials [part0, acc); priv = acc.
 constexpr int kLinChunk = 8;  // scalars per pass (their derivatives live in registers)
+constexpr int kLinEntries = 128;   // (slot, scalar) entries per pass: two lane registers
+constexpr int kLinMaskWords = 128; // slot masks of a pass, 4 per word: two lane registers
 struct LinPlan {
+    int dummy = 0, fpart0 = 0, red0 = 0;  // zero slot, forward partials, transpose buffer
     int nL = 0, one = 0, L0 = 0, part0 = 0, acc = 0, priv = 0;
-    int CH = kLinChunk, nchunks = 0;
-    std::vector<int> level_step, steps, level_comb, comb;  // as Plan's rule tables
+    int CH = kLinChunk, nchunks = 0, max_chunk_entries = 0;
+    bool lane_walk = false;  // maskw/clist valid (nslots <= 4 kLinMaskWords)
+    std::vector<int> level_step, steps, level_comb, comb;  // L rules, as Plan's rule tables
+    std::vector<int> fwd_level_step, fwd_steps, fwd_level_comb, fwd_comb;  // forward rules
+    std::vector<int> chunk_s0;   // [nchunks+1] first scalar of each chunk
     std::vector<int> slot_mask;  // [nchunks][nslots] bit k: scalar k of the chunk uses the slot
     std::vector<int> slot_L;     // [nchunks][nslots][kLinChunk] L index of each bit
+    std::vector<int> maskw;      // [nchunks][kLinMaskWords] slot masks, 4 per word
+    std::vector<int> clist;      // [nchunks][kLinEntries] L indices in walk order
 };
 bool build_lin_plan(const Model &m, const Plan &p, LinPlan &lp, std::string &err);
 
@@ -226,23 +234,40 @@ hipError_t launch_efs(const DevModel &m, const DevNeighbors &nb, const EfsOut &o
                       const EfsLaunch &cfg, int flags, hipStream_t s);
 // Linear fit (lin_kernel.hip).
 struct DevLin {
+    int dummy, red0, nfwd;
     int nL, one, L0, part0, acc, priv, CH, nchunks, nlev;
+    int lane_walk;
+    const int *fwd_level_step, *fwd_level_comb;  // [nfwd + 1]
+    const int2 *fwd_steps;
+    const int4 *fwd_comb;
     const int *level_step, *level_comb;  // [nlev + 1]
     const int2 *steps;
     const int4 *comb;
+    const int *chunk_s0;    // [nchunks + 1]
     const int *slot_mask;   // [nchunks][nslots]
     const int *slot_L;      // [nchunks][nslots][kLinChunk]
+    const int *maskw;       // [nchunks][kLinMaskWords]
+    const int *clist;       // [nchunks][kLinEntries]
 };
-struct LinOut {
-    const int *center_structure;  // [n]
-    double *ec;  // [nconf][p] energy components (p = Z + S)
-    double *fc;  // [n][3][p] force components
-    double *sc;  // [nconf][9][p] stress components
+// One group of whole structures for the linear-fit kernels: atoms
+// [a0, a1), structures [c0, c1), entries from e0; pair buffer
+// [entries][3][Sp] (Sp = S rounded up to the chunk), site rows
+// [a1 - a0][10][S] (9 stress partials, then the scalar moments).
+struct LinGroup {
+    int a0, a1, c0, c1;
+    int64_t e0;
+    int Sp;
+    double *pair;
+    double *site;
 };
 bool lin_configure(const DevModel &m, const DevLin &L, int n, int num_cus, size_t lds_limit,
                    EfsLaunch &cfg);
 hipError_t launch_lin_site(const DevModel &m, const DevLin &L, const DevNeighbors &nb,
-                           const LinOut &out, const EfsLaunch &cfg, hipStream_t s);
+                           const LinGroup &g, const EfsLaunch &cfg, hipStream_t s);
+hipError_t launch_lin_gather(const DevModel &m, const DevNeighbors &nb, const int *rev_off,
+                             const int *rev_pairs, const LinGroup &g, double *fc, hipStream_t s);
+hipError_t launch_lin_reduce(const DevModel &m, const int *soff, const int *center_type,
+                             const LinGroup &g, double *ec, double *sc, hipStream_t s);
 hipError_t launch_lin_rows(const double *comp, const int64_t *src, const double *sw,
                            const double *yw, int64_t R, int p, double *A, double *y, hipStream_t s);
 // Gram columns padded to a multiple of 16 (p coefficients plus the target).

@@ -364,6 +364,7 @@ int mtpx_set_labels(mtpx_context *ctx, const int *active, const double *target_e
     keep(ctx->tS_h, any[2] ? target_stress : nullptr, 9 * (size_t)nc);
     keep(ctx->wS_h, any[2] ? stress_weight : nullptr, nc);
     ctx->has_labels = true;
+    ++ctx->label_gen;
     ctx->has_adjoints = false;
     return MTPX_OK;
 }

@@ -125,6 +125,22 @@ def test_linear_system_matches_oracle(ctx, crystal_set, name):
     assert np.array_equal(G, G.T)
 
 
+def test_components_independent_of_grouping(ctx, crystal_set, monkeypatch):
+    """Structures are processed in groups bounded by a pair-buffer budget
+    (MTPX_LIN_PAIR_MB): a 1 MB budget puts every structure in a group of
+    its own; the components are bitwise those of one group (fixed-order
+    sums, no atomics)."""
+    text, structs, nbs, labels = crystal_set
+    _upload(ctx, text, structs, labels, SETTINGS["linear"])
+    monkeypatch.setenv("MTPX_LIN_PAIR_MB", "1")
+    small = ctx.efs_components()
+    monkeypatch.setenv("MTPX_LIN_PAIR_MB", "4096")
+    big = ctx.efs_components()
+    again = ctx.efs_components()
+    for a, b, c in zip(small, big, again):
+        assert np.array_equal(a, b) and np.array_equal(b, c)
+
+
 def test_gram_of_the_device_rows(ctx, crystal_set):
     """The matrix-core Gram equals the textbook sum over the returned rows."""
     text, structs, nbs, labels = crystal_set
