@@ -102,7 +102,8 @@ int install_model(mtpx_context *ctx, Model &&m)
     dm.red0 = P.red0;
     dm.priv_doubles = P.priv_doubles;
     dm.tr_delta = P.tr_delta;
-    dm.tr_red = P.tr_red;
+    dm.tr_red1 = P.tr_red1;
+    dm.tr_red4 = P.tr_red4;
     dm.tr_stage = P.tr_stage;
     dm.tr_grad = P.tr_grad;
     dm.tr_ctype = P.tr_ctype;
@@ -265,8 +266,13 @@ int run_efs(mtpx_context *ctx, bool deterministic, bool site_virial, bool energy
         const char *e = getenv("MTPX_EFS_WAVES");
         return e ? atoi(e) : 0;
     }();
+    // MTPX_EFS_TABLES (tuning): "lds" or "global" step-table placement
+    static const int table_pref = [] {
+        const char *e = getenv("MTPX_EFS_TABLES");
+        return !e ? -1 : std::string(e) == "lds" ? 1 : std::string(e) == "global" ? 0 : -1;
+    }();
     EfsLaunch cfg;
-    if (!efs_configure(ctx->dm, n, ctx->num_cus, max_waves, ctx->lds_limit, cfg))
+    if (!efs_configure(ctx->dm, n, ctx->num_cus, max_waves, ctx->lds_limit, cfg, table_pref))
         return set_error(ctx, MTPX_E_CAPACITY, "model needs more LDS than a CU provides");
     ctx->launch = cfg;
     HIP_TRY(ctx->forces.ensure(sizeof(double) * 3 * std::max(n, 1)), "allocate forces");

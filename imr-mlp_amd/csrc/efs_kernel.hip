@@ -293,11 +293,11 @@ int variant_max_waves(int v)
 }  // namespace
 
 bool efs_configure(const DevModel &m, int n, int num_cus, int max_waves, size_t lds_limit,
-                   EfsLaunch &cfg)
+                   EfsLaunch &cfg, int table_pref)
 {
     const int vmax = variant_max_waves(efs_variant(m, m.R));
     const int wcap = max_waves > 0 ? std::min(vmax, max_waves) : vmax;
-    return configure_launch(m, n, num_cus, wcap, lds_limit, m.priv_doubles, cfg);
+    return configure_launch(m, n, num_cus, wcap, lds_limit, m.priv_doubles, cfg, table_pref);
 }
 
 // 0: level-16 profile, 1: level-20, 2: level-10 (each with its template's

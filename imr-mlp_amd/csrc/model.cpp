@@ -586,12 +586,34 @@ bool build_plan(const Model &m, Plan &p, std::string &err)
     // second adjoints), a transpose buffer, the slot-ordered adjoint staging
     // {A, aA, bA, cA} + G, the wave's gradient accumulator and the species
     // of the neighbours in flight.
+    // Regions are laid over blocks that are dead in the phase that uses them
+    // where they fit: the first neighbour pass's transpose buffer over the
+    // adjoint block (written with the seeds later), the slot-ordered {A, G}
+    // stage over the moments (dead after the reverse rules) and the last
+    // pass's transpose buffer over the tangents (dead after the staging).
+    // Otherwise they get room of their own after the gradient accumulator.
+    const int RB = kChunk * kRedStride;
     p.tr_delta = p.red0;
-    p.tr_red = 2 * p.red0;
-    p.tr_stage = p.tr_red + kChunk * kRedStride;
-    p.tr_grad = p.tr_stage + 5 * N4;
+    p.tr_grad = 2 * p.red0;
     p.tr_ctype = p.tr_grad + ((m.ncoef() + 3) & ~3);
-    p.tr_priv = p.tr_ctype + kWave / 2;  // 64 ints: neighbour species of a batch
+    int end = p.tr_ctype + kWave / 2;  // 64 ints: neighbour species of a batch
+    int own_red = -1;
+    auto red_region = [&] {
+        if (own_red < 0) {
+            own_red = end;
+            end += RB;
+        }
+        return own_red;
+    };
+    p.tr_red1 = p.red0 - K4 >= RB ? K4 : red_region();
+    p.tr_red4 = p.red0 >= RB ? p.tr_delta : red_region();
+    if (2 * N4 <= K4) {
+        p.tr_stage = 0;
+    } else {
+        p.tr_stage = end;
+        end += 2 * N4;
+    }
+    p.tr_priv = end;
     return true;
 }
 

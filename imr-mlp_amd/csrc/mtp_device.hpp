@@ -457,8 +457,10 @@ __device__ __forceinline__ void stage_shared(const DevModel &m, const Shared &L,
 // Launch shape for a kernel whose waves each own `priv_doubles` of LDS work
 // space next to the block-shared model tables: rule tables in LDS unless that
 // costs more than half the waves; false if a single wave does not fit.
+// table_pref: -1 chooses the step-table placement, 0 keeps the tables in
+// global memory, 1 in LDS where they fit.
 inline bool configure_launch(const DevModel &m, int n, int num_cus, int wcap, size_t lds_limit,
-                             int priv_doubles, EfsLaunch &cfg)
+                             int priv_doubles, EfsLaunch &cfg, int table_pref = -1)
 {
     const size_t priv = (size_t)priv_doubles * sizeof(double);
     auto fit = [&](bool tables) {
@@ -470,7 +472,7 @@ inline bool configure_launch(const DevModel &m, int n, int num_cus, int wcap, si
     const int wt = fit(true), wg = fit(false);
     if (wg == 0)
         return false;
-    cfg.lds_tables = wt > 0 && 2 * wt >= wg;
+    cfg.lds_tables = table_pref < 0 ? wt > 0 && 2 * wt >= wg : table_pref == 1 && wt > 0;
     cfg.waves = cfg.lds_tables ? wt : wg;
     cfg.lds_bytes = shared_doubles(m, cfg.lds_tables) * sizeof(double) + cfg.waves * priv;
     const int per_cu = std::max<int>(1, (int)(lds_limit / cfg.lds_bytes));

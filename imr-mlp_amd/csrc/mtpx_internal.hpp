@@ -109,12 +109,15 @@ struct Plan {
     //   [0, K4) moments | [K4, 2 K4) adjoints | dummy (a zero slot) |
     //   [part0, red0) partial sums | [red0, priv_doubles) transpose buffer.
     int K4 = 0, dummy = 0, part0 = 0, red0 = 0, priv_doubles = 0;
-    // Training work space (doubles): [0, tr_delta) the E/F/S work space,
-    // [tr_delta, tr_red) its dual copy, then a transpose buffer, the staged
-    // slot adjoints (tr_stage: 4 x nslots4 of {A, aA, bA, cA}, then nslots4
-    // of G), the gradient accumulator (tr_grad, ncoef) and 64 neighbour
-    // species (tr_ctype, as ints).
-    int tr_delta = 0, tr_red = 0, tr_stage = 0, tr_grad = 0, tr_ctype = 0, tr_priv = 0;
+    // Training work space (doubles): [0, tr_delta) the E/F/S work space
+    // without its transpose buffer, [tr_delta, tr_grad) its dual copy, the
+    // gradient accumulator (tr_grad, ncoef) and 64 neighbour species
+    // (tr_ctype, as ints).  The transpose buffers of the first and the last
+    // neighbour pass (tr_red1, tr_red4) and the slot-ordered {A, G} pairs
+    // (tr_stage, nslots4) lie over blocks that are dead in their phase, or
+    // after the species where they do not fit there.
+    int tr_delta = 0, tr_red1 = 0, tr_red4 = 0, tr_stage = 0, tr_grad = 0, tr_ctype = 0,
+        tr_priv = 0;
     // first slot of each (nu, mu) block, -1 where absent: [nu * kMaxMu + mu]
     int slot_base[(kMaxNu + 1) * kMaxMu];
     // Lane-major step tables, one per direction.  Level L owns steps
@@ -180,7 +183,7 @@ struct DevModel {
     const int *dup;         // [ndup][2]
     int max_partials;
     int K4, dummy, part0, red0, priv_doubles;  // per-wave work space (Plan)
-    int tr_delta, tr_red, tr_stage, tr_grad, tr_ctype, tr_priv;
+    int tr_delta, tr_red1, tr_red4, tr_stage, tr_grad, tr_ctype, tr_priv;
     int nradial, ncoef;
     int slot_base[(kMaxNu + 1) * kMaxMu];
     int fwd_nsteps, bwd_nsteps;                 // steps per lane, all levels
@@ -225,7 +228,7 @@ struct EfsLaunch {
 // LDS a workgroup may allocate (lds_limit bytes, which one CU also holds).
 // max_waves > 0 caps the waves per workgroup.
 bool efs_configure(const DevModel &m, int n, int num_cus, int max_waves, size_t lds_limit,
-                   EfsLaunch &cfg);
+                   EfsLaunch &cfg, int table_pref = -1);
 int efs_variant(const DevModel &m, int R);
 // launch_efs flags: ordered force assembly; site energies and energy only.
 constexpr int kEfsDeterministic = 1;

@@ -310,7 +310,7 @@ __device__ __forceinline__ void fwd_dual_shells(const DevModel &m, DualCtx &cx,
 // pass): per mu, alpha_mu (without its beta-like term) and U_mu.
 //   alpha += Gb Y - nu (w_u/d) A Y + (W/d) . (aA Y_a-1, bA Y_b-1, cA Y_c-1)
 template <int NU, class P>
-__device__ __forceinline__ void rad_shells(const DevModel &m, const double4 *A4, const double *Gs,
+__device__ __forceinline__ void rad_shells(const DevModel &m, const double2 *AG,
                                            const Nbr<P::M> &q, const GradNbr &g,
                                            const double *prev, double *alpha, double *U)
 {
@@ -332,16 +332,17 @@ __device__ __forceinline__ void rad_shells(const DevModel &m, const double4 *A4,
 #pragma unroll
                 for (int b = NU - a; b >= 0; --b) {
                     const int i = shell_index(NU, a, b);
-                    const double4 w = A4[base + i];
+                    const double2 w = AG[base + i];  // {A, G}, LDS broadcast
                     uu = fma(w.x, cur[i], uu);
-                    al = fma(Gs[base + i], cur[i], al);
+                    al = fma(w.y, cur[i], al);
                     if constexpr (NU > 0) {
                         if (a > 0)
-                            al = fma(w.y * wxd, prev[shell_index(NU - 1, a - 1, b)], al);
+                            al = fma(w.x * (a * wxd), prev[shell_index(NU - 1, a - 1, b)], al);
                         if (b > 0)
-                            al = fma(w.z * wyd, prev[shell_index(NU - 1, a, b - 1)], al);
+                            al = fma(w.x * (b * wyd), prev[shell_index(NU - 1, a, b - 1)], al);
                         if (NU - a - b > 0)
-                            al = fma(w.w * wzd, prev[shell_index(NU - 1, a, b)], al);
+                            al = fma(w.x * ((NU - a - b) * wzd), prev[shell_index(NU - 1, a, b)],
+                                     al);
                     }
                 }
             alpha[mu] += fma(uu, ncw, al);
@@ -350,7 +351,7 @@ __device__ __forceinline__ void rad_shells(const DevModel &m, const double4 *A4,
     }
     if constexpr (NU < P::NUMAX) {
         if (P::deeper(m, NU))
-            rad_shells<NU + 1, P>(m, A4, Gs, q, g, cur, alpha, U);
+            rad_shells<NU + 1, P>(m, AG, q, g, cur, alpha, U);
     }
 }
 
@@ -364,10 +365,8 @@ __global__ __launch_bounds__(kWave *kMaxWaves) void grad_kernel(DevModel m, DevN
     const Shared L = shared_layout(m, lds);
     double *ws = lds + shared_doubles(m, kTabLds) + (size_t)wave * m.tr_priv;
     double *wd = ws + m.tr_delta;  // tangents Q, second adjoints G
-    double *red = ws + m.tr_red;
-    const double4 *A4 = reinterpret_cast<const double4 *>(ws + m.tr_stage);
-    const int N4 = (m.nslots + 3) & ~3;
-    double *Gs = ws + m.tr_stage + 4 * N4;
+    double *red1 = ws + m.tr_red1, *red4 = ws + m.tr_red4;
+    double2 *AG = reinterpret_cast<double2 *>(ws + m.tr_stage);
     double *grad = ws + m.tr_grad;
     int *ctype = reinterpret_cast<int *>(ws + m.tr_ctype);
 
@@ -405,7 +404,7 @@ __global__ __launch_bounds__(kWave *kMaxWaves) void grad_kernel(DevModel m, DevN
 
         // ---- 1. basic moments and their tangents ----------------------------
         for (int base = 0; base < n; base += kWave) {
-            DualCtx cx{red, ws, L.slot_basic, lane, 0, m.tr_delta};
+            DualCtx cx{red1, ws, L.slot_basic, lane, 0, m.tr_delta};
             Nbr<P::M> q;
             const bool valid = lane < n - base;
             const int64_t p = beg + base + lane;
@@ -414,7 +413,7 @@ __global__ __launch_bounds__(kWave *kMaxWaves) void grad_kernel(DevModel m, DevN
             fwd_dual_shells<0, P>(m, cx, q, g, nullptr);
             const int rest = cx.row % kChunk;
             if (rest)
-                reduce_rows(red, rest, cx.row - rest, lane, [&](int r, double acc) {
+                reduce_rows(red1, rest, cx.row - rest, lane, [&](int r, double acc) {
                     const int b = L.slot_basic[r >> 1];
                     if (b >= 0)
                         ws[b + ((r & 1) ? m.tr_delta : 0)] += acc;
@@ -425,6 +424,11 @@ __global__ __launch_bounds__(kWave *kMaxWaves) void grad_kernel(DevModel m, DevN
                 ws[m.dup[2 * k]] = ws[m.dup[2 * k + 1]];
                 wd[m.dup[2 * k]] = wd[m.dup[2 * k + 1]];
             }
+        // the zero slots and partial sums may lie under a transpose buffer
+        for (int k = m.dummy + lane; k < m.red0; k += kWave) {
+            ws[k] = 0.0;
+            wd[k] = 0.0;
+        }
         wave_sync();
 
         // ---- 2. rules forward with tangents; moment and species gradient ----
@@ -452,18 +456,11 @@ __global__ __launch_bounds__(kWave *kMaxWaves) void grad_kernel(DevModel m, DevN
                 wd[m.K4 + m.dup[2 * k + 1]] += wd[m.K4 + m.dup[2 * k]];
             }
         wave_sync();
+        // slot-ordered {A, G} (the stage may lie over the moments, which are
+        // no longer read; A and G are not under it)
         for (int s = lane; s < m.nslots; s += kWave) {
             const int b = L.slot_basic[s];
-            double4 w = {0, 0, 0, 0};
-            double gb = 0.0;
-            if (b >= 0) {
-                const double a = ws[m.K4 + b];
-                const int abc = L.slot_abc[s];
-                w = {a, a * (abc & 0xff), a * ((abc >> 8) & 0xff), a * ((abc >> 16) & 0xff)};
-                gb = wd[m.K4 + b];
-            }
-            reinterpret_cast<double4 *>(ws + m.tr_stage)[s] = w;
-            Gs[s] = gb;
+            AG[s] = b >= 0 ? double2{ws[m.K4 + b], wd[m.K4 + b]} : double2{0.0, 0.0};
         }
         wave_sync();
 
@@ -481,12 +478,12 @@ __global__ __launch_bounds__(kWave *kMaxWaves) void grad_kernel(DevModel m, DevN
 #pragma unroll
             for (int mu = 0; mu < P::M; ++mu)
                 alpha[mu] = U[mu] = 0.0;
-            rad_shells<0, P>(m, A4, Gs, q, g, nullptr, alpha, U);
+            rad_shells<0, P>(m, AG, q, g, nullptr, alpha, U);
             double Q[P::RMAX], dQ[P::RMAX];
             chebyshev<P::RMAX>(m, q.d, Q, dQ);
             int row = 0;
             auto flush = [&](int nrows) {
-                reduce_rows_typed(red, nrows, row - nrows, lane, ctype, m.Z,
+                reduce_rows_typed(red4, nrows, row - nrows, lane, ctype, m.Z,
                                   [&](int r, int tj2, double acc) {
                                       grad[gbase + tj2 * MR + r] += acc;
                                   });
@@ -498,7 +495,7 @@ __global__ __launch_bounds__(kWave *kMaxWaves) void grad_kernel(DevModel m, DevN
 #pragma unroll
                     for (int k = 0; k < P::RMAX; ++k)
                         if (P::exact || k < m.R) {
-                            red[(row % kChunk) * kRedStride + lane] = al * Q[k] + be * dQ[k];
+                            red4[(row % kChunk) * kRedStride + lane] = al * Q[k] + be * dQ[k];
                             ++row;
                             if (row % kChunk == 0)
                                 flush(kChunk);
