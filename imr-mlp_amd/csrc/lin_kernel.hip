@@ -222,8 +222,8 @@ __global__ __launch_bounds__(kWave *kMaxWaves) void lin_site_kernel(DevModel m, 
     extern __shared__ double lds[];
     const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
     const int nwaves = blockDim.x / kWave;
-    const Shared Ls = shared_layout(m, lds);
-    double *ws = lds + shared_doubles(m, false) + (size_t)wave * L.priv;
+    const Shared Ls = shared_layout(m, lds, false);  // no adjoint seeds
+    double *ws = lds + shared_doubles(m, false, false) + (size_t)wave * L.priv;
     double *mom = ws, *red = ws + L.red0;
 
     stage_shared(m, Ls, false, tid, blockDim.x);
@@ -529,7 +529,7 @@ int lin_variant(const DevModel &m, const DevLin &L)
 bool lin_configure(const DevModel &m, const DevLin &L, int n, int num_cus, size_t lds_limit,
                    EfsLaunch &cfg)
 {
-    const size_t sh = shared_doubles(m, false) * sizeof(double);
+    const size_t sh = shared_doubles(m, false, false) * sizeof(double);
     const size_t priv = (size_t)L.priv * sizeof(double);
     if (sh + priv > lds_limit)
         return false;

@@ -595,7 +595,7 @@ bool build_plan(const Model &m, Plan &p, std::string &err)
     const int RB = kChunk * kRedStride;
     p.tr_delta = p.red0;
     p.tr_grad = 2 * p.red0;
-    p.tr_ctype = p.tr_grad + ((m.ncoef() + 3) & ~3);
+    p.tr_ctype = p.tr_grad + ((m.nradial() + 3) & ~3);
     int end = p.tr_ctype + kWave / 2;  // 64 ints: neighbour species of a batch
     int own_red = -1;
     auto red_region = [&] {

@@ -403,24 +403,29 @@ struct Shared {
     int2 *fwd_steps, *bwd_steps;
 };
 
-__device__ __host__ __forceinline__ size_t shared_doubles(const DevModel &m, bool tables)
+// The block-shared model tables in LDS: radial coefficients, the adjoint
+// seeds (kernels that run the reverse rules from LDS), moment coefficients,
+// map, slot tables and optionally the rule step tables.
+__device__ __host__ __forceinline__ size_t shared_doubles(const DevModel &m, bool tables,
+                                                          bool seeds = true)
 {
     const size_t r4c = ((size_t)m.Z * m.Z * m.M * m.R + 3) & ~size_t(3);
     const size_t S4 = (m.S + 3) & ~3, N4 = (m.nslots + 3) & ~3;
-    size_t d = r4c + m.K4 + S4 + (S4 + 2 * N4) / 2;
+    size_t d = r4c + (seeds ? m.K4 : 0) + S4 + (S4 + 2 * N4) / 2;
     if (tables)
         d += (size_t)(m.fwd_nsteps + m.bwd_nsteps) * kWave;
     return (d + 3) & ~size_t(3);
 }
 
-__device__ __forceinline__ Shared shared_layout(const DevModel &m, double *base)
+__device__ __forceinline__ Shared shared_layout(const DevModel &m, double *base,
+                                                bool seeds = true)
 {
     const int r4c = (m.Z * m.Z * m.M * m.R + 3) & ~3;
     const int S4 = (m.S + 3) & ~3, N4 = (m.nslots + 3) & ~3;
     Shared L;
     L.coef = base;
-    L.seed = L.coef + r4c;
-    L.moment = L.seed + m.K4;
+    L.seed = seeds ? L.coef + r4c : nullptr;
+    L.moment = L.coef + r4c + (seeds ? m.K4 : 0);
     L.map = reinterpret_cast<int *>(L.moment + S4);
     L.slot_basic = L.map + S4;
     L.slot_abc = L.slot_basic + N4;
@@ -436,8 +441,9 @@ __device__ __forceinline__ void stage_shared(const DevModel &m, const Shared &L,
     const int ncoef_r = m.Z * m.Z * m.M * m.R;
     for (int k = tid; k < ncoef_r; k += nthreads)
         L.coef[k] = m.radial[k];
-    for (int k = tid; k < m.K; k += nthreads)
-        L.seed[k] = m.seed[k];
+    if (L.seed)
+        for (int k = tid; k < m.K; k += nthreads)
+            L.seed[k] = m.seed[k];
     for (int k = tid; k < m.S; k += nthreads) {
         L.moment[k] = m.moment[k];
         L.map[k] = m.map[k];
@@ -460,11 +466,12 @@ __device__ __forceinline__ void stage_shared(const DevModel &m, const Shared &L,
 // table_pref: -1 chooses the step-table placement, 0 keeps the tables in
 // global memory, 1 in LDS where they fit.
 inline bool configure_launch(const DevModel &m, int n, int num_cus, int wcap, size_t lds_limit,
-                             int priv_doubles, EfsLaunch &cfg, int table_pref = -1)
+                             int priv_doubles, EfsLaunch &cfg, int table_pref = -1,
+                             bool seeds = true)
 {
     const size_t priv = (size_t)priv_doubles * sizeof(double);
     auto fit = [&](bool tables) {
-        const size_t sh = shared_doubles(m, tables) * sizeof(double);
+        const size_t sh = shared_doubles(m, tables, seeds) * sizeof(double);
         if (sh + priv > lds_limit)
             return 0;
         return (int)std::min<size_t>(wcap, (lds_limit - sh) / priv);
@@ -474,7 +481,7 @@ inline bool configure_launch(const DevModel &m, int n, int num_cus, int wcap, si
         return false;
     cfg.lds_tables = table_pref < 0 ? wt > 0 && 2 * wt >= wg : table_pref == 1 && wt > 0;
     cfg.waves = cfg.lds_tables ? wt : wg;
-    cfg.lds_bytes = shared_doubles(m, cfg.lds_tables) * sizeof(double) + cfg.waves * priv;
+    cfg.lds_bytes = shared_doubles(m, cfg.lds_tables, seeds) * sizeof(double) + cfg.waves * priv;
     const int per_cu = std::max<int>(1, (int)(lds_limit / cfg.lds_bytes));
     const int need = (std::max(n, 1) + cfg.waves - 1) / cfg.waves;
     cfg.grid = std::max(1, std::min(need, num_cus * per_cu));

@@ -111,7 +111,7 @@ struct Plan {
     int K4 = 0, dummy = 0, part0 = 0, red0 = 0, priv_doubles = 0;
     // Training work space (doubles): [0, tr_delta) the E/F/S work space
     // without its transpose buffer, [tr_delta, tr_grad) its dual copy, the
-    // gradient accumulator (tr_grad, ncoef) and 64 neighbour species
+    // radial gradient accumulator (tr_grad, nradial) and 64 neighbour species
     // (tr_ctype, as ints).  The transpose buffers of the first and the last
     // neighbour pass (tr_red1, tr_red4) and the slot-ordered {A, G} pairs
     // (tr_stage, nslots4) lie over blocks that are dead in their phase, or

@@ -362,12 +362,15 @@ __global__ __launch_bounds__(kWave *kMaxWaves) void grad_kernel(DevModel m, DevN
     extern __shared__ double lds[];
     const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
     const int nwaves = blockDim.x / kWave;
-    const Shared L = shared_layout(m, lds);
-    double *ws = lds + shared_doubles(m, kTabLds) + (size_t)wave * m.tr_priv;
+    const Shared L = shared_layout(m, lds, false);  // seeds are read from global memory
+    double *ws = lds + shared_doubles(m, kTabLds, false) + (size_t)wave * m.tr_priv;
     double *wd = ws + m.tr_delta;  // tangents Q, second adjoints G
     double *red1 = ws + m.tr_red1, *red4 = ws + m.tr_red4;
     double2 *AG = reinterpret_cast<double2 *>(ws + m.tr_stage);
-    double *grad = ws + m.tr_grad;
+    double *grad = ws + m.tr_grad;  // radial part of the gradient
+    const int rowid = blockIdx.x * nwaves + wave;
+    // species and moment part: accumulated in the wave's own gradient row
+    double *grow = t.grad_rows + (size_t)rowid * m.ncoef;
     int *ctype = reinterpret_cast<int *>(ws + m.tr_ctype);
 
     stage_shared(m, L, kTabLds, tid, blockDim.x);
@@ -375,14 +378,15 @@ __global__ __launch_bounds__(kWave *kMaxWaves) void grad_kernel(DevModel m, DevN
         ws[k] = 0.0;
         wd[k] = 0.0;
     }
-    for (int k = lane; k < m.ncoef; k += kWave)
+    for (int k = lane; k < m.nradial; k += kWave)
         grad[k] = 0.0;
+    for (int k = m.nradial + lane; k < m.ncoef; k += kWave)
+        grow[k] = 0.0;
     __syncthreads();
     const int2 *fwd_tab = kTabLds ? L.fwd_steps : m.fwd_steps;
     const int2 *bwd_tab = kTabLds ? L.bwd_steps : m.bwd_steps;
     const int MR = P::exact ? P::M * P::RMAX : m.M * m.R;
 
-    const int rowid = blockIdx.x * nwaves + wave;
     for (int i = rowid; i < nb.n; i += gridDim.x * nwaves) {
         const int ti = nb.center_type[i];
         const int beg = nb.offsets[i];
@@ -436,14 +440,14 @@ __global__ __launch_bounds__(kWave *kMaxWaves) void grad_kernel(DevModel m, DevN
                         m.tr_delta);
         for (int s = lane; s < m.S; s += kWave) {
             const int x = L.map[s];
-            grad[m.nradial + m.Z + s] += se * ws[x] + wd[x];
+            grow[m.nradial + m.Z + s] += se * ws[x] + wd[x];
         }
         if (lane == 0)
-            grad[m.nradial + ti] += se;
+            grow[m.nradial + ti] += se;
 
         // ---- 3. reverse rules: A with seeds xi, G with seeds dLdE xi --------
         for (int k = lane; k < m.K; k += kWave) {
-            const double sd = L.seed[k];
+            const double sd = m.seed[k];
             ws[m.K4 + k] = sd;
             wd[m.K4 + k] = se * sd;
         }
@@ -507,9 +511,9 @@ __global__ __launch_bounds__(kWave *kMaxWaves) void grad_kernel(DevModel m, DevN
         }
         wave_sync();
     }
-    // this wave's gradient row
-    for (int k = lane; k < m.ncoef; k += kWave)
-        t.grad_rows[(size_t)rowid * m.ncoef + k] = grad[k];
+    // the radial part of this wave's gradient row
+    for (int k = lane; k < m.nradial; k += kWave)
+        grow[k] = grad[k];
 }
 
 template <class P>
@@ -534,7 +538,7 @@ void launch_grad_variant(const DevModel &m, const DevNeighbors &nb, const TrainA
 
 bool grad_configure(const DevModel &m, int n, int num_cus, size_t lds_limit, EfsLaunch &cfg)
 {
-    return configure_launch(m, n, num_cus, 4, lds_limit, m.tr_priv, cfg);
+    return configure_launch(m, n, num_cus, 4, lds_limit, m.tr_priv, cfg, -1, false);
 }
 
 hipError_t launch_structure_reduce(const int *soff, int nconf, const double *site_energy,
