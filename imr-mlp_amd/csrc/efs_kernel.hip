@@ -50,7 +50,7 @@ __global__ __launch_bounds__(kWave *kMaxWaves) void efs_kernel(DevModel m, DevNe
     const Shared L = shared_layout(m, lds);
     double *ws = lds + shared_doubles(m, kTabLds) + (size_t)wave * m.priv_doubles;
     double *mom = ws, *A = ws + m.K4, *red = ws + m.red0;
-    const double4 *A4 = reinterpret_cast<const double4 *>(red);
+    const double *As = red;  // slot-ordered adjoints (force pass)
 
     // model tables the per-atom phases index, staged once per workgroup
     stage_shared(m, L, kTabLds, tid, blockDim.x);
@@ -113,16 +113,10 @@ __global__ __launch_bounds__(kWave *kMaxWaves) void efs_kernel(DevModel m, DevNe
             for (int k = 0; k < m.ndup; ++k)
                 A[m.dup[2 * k + 1]] += A[m.dup[2 * k]];
         wave_sync();
-        // slot-ordered adjoints {A, aA, bA, cA}
+        // slot-ordered adjoints
         for (int s = lane; s < m.nslots; s += kWave) {
             const int b = L.slot_basic[s];
-            double4 w = {0, 0, 0, 0};
-            if (b >= 0) {
-                const double a = A[b];
-                const int abc = L.slot_abc[s];
-                w = {a, a * (abc & 0xff), a * ((abc >> 8) & 0xff), a * ((abc >> 16) & 0xff)};
-            }
-            reinterpret_cast<double4 *>(red)[s] = w;
+            red[s] = b >= 0 ? A[b] : 0.0;
         }
         wave_sync();
 
@@ -136,7 +130,7 @@ __global__ __launch_bounds__(kWave *kMaxWaves) void efs_kernel(DevModel m, DevNe
             load_neighbor<P>(m, nb, L.coef, ti, p, valid, q);
             BwdAcc acc{0, 0, 0, 0};
             int slot = 0;
-            bwd_shells<0, P>(m, A4, slot, q, nullptr, acc);
+            bwd_shells<0, P>(m, As, slot, q, nullptr, acc);
             const double D0 = acc.s * q.ux + acc.gx * q.invd;
             const double D1 = acc.s * q.uy + acc.gy * q.invd;
             const double D2 = acc.s * q.uz + acc.gz * q.invd;

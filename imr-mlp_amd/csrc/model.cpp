@@ -569,7 +569,7 @@ bool build_plan(const Model &m, Plan &p, std::string &err)
     const int P4 = (p.max_partials + 3) & ~3;
     p.red0 = p.part0 + P4;
     const int N4 = (p.nslots + 3) & ~3;
-    p.priv_doubles = p.red0 + std::max(kChunk * kRedStride, 4 * N4);
+    p.priv_doubles = p.red0 + std::max(kChunk * kRedStride, N4);  // transpose buffer | slot A
     if (p.priv_doubles > 0xffff)
         return fail(err, "model too large: per-atom work space exceeds 65535 doubles");
     for (int t = 0; t < m.T; ++t)
@@ -582,15 +582,15 @@ bool build_plan(const Model &m, Plan &p, std::string &err)
     encode_tables(bwd, p.part0, p.dummy, adj, same, adj, p.bwd_steps, p.bwd_level_step,
                   p.bwd_comb, p.bwd_level_comb);
 
-    // Training work space: the E/F/S work space, its dual copy (tangents and
-    // second adjoints), a transpose buffer, the slot-ordered adjoint staging
-    // {A, aA, bA, cA} + G, the wave's gradient accumulator and the species
-    // of the neighbours in flight.
-    // Regions are laid over blocks that are dead in the phase that uses them
-    // where they fit: the first neighbour pass's transpose buffer over the
-    // adjoint block (written with the seeds later), the slot-ordered {A, G}
-    // stage over the moments (dead after the reverse rules) and the last
-    // pass's transpose buffer over the tangents (dead after the staging).
+    // Training work space: the E/F/S work space (without its transpose
+    // buffer), its dual copy (tangents and second adjoints), the wave's radial
+    // gradient accumulator and the species of the neighbours in flight.
+    // Three more buffers lie over blocks that are dead in the phase that
+    // uses them, where they fit: the first neighbour pass's transpose buffer
+    // over the adjoint block (written with the seeds later), the
+    // slot-ordered {A, G} stage over the moments (dead after the reverse
+    // rules) and the last pass's transpose buffer over the tangents (dead
+    // after the staging).
     // Otherwise they get room of their own after the gradient accumulator.
     const int RB = kChunk * kRedStride;
     p.tr_delta = p.red0;

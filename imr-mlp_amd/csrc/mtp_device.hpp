@@ -259,8 +259,11 @@ struct BwdAcc {
     double s, gx, gy, gz;
 };
 
+// Force pass over the slots: u = sum A Y, G = sum (a A, b A, c A) . Y_{-1}
+// with the slot-ordered adjoints A (an 8-byte LDS broadcast per slot; the
+// integer factors are applied in registers).
 template <int NU, class P>
-__device__ __forceinline__ void bwd_shells(const DevModel &m, const double4 *A4, int &slot,
+__device__ __forceinline__ void bwd_shells(const DevModel &m, const double *As, int &slot,
                                            const Nbr<P::M> &q, const double *prev, BwdAcc &acc)
 {
     double cur[shell_size(NU)];
@@ -280,15 +283,15 @@ __device__ __forceinline__ void bwd_shells(const DevModel &m, const double4 *A4,
 #pragma unroll
                 for (int b = NU - a; b >= 0; --b) {
                     const int i = shell_index(NU, a, b);
-                    const double4 w = A4[slot + i];  // {A, aA, bA, cA}, LDS broadcast
-                    u += w.x * cur[i];
+                    const double w = As[slot + i];  // LDS broadcast
+                    u += w * cur[i];
                     if constexpr (NU > 0) {
                         if (a > 0)
-                            Gx += w.y * prev[shell_index(NU - 1, a - 1, b)];
+                            Gx += (w * a) * prev[shell_index(NU - 1, a - 1, b)];
                         if (b > 0)
-                            Gy += w.z * prev[shell_index(NU - 1, a, b - 1)];
+                            Gy += (w * b) * prev[shell_index(NU - 1, a, b - 1)];
                         if (NU - a - b > 0)
-                            Gz += w.w * prev[shell_index(NU - 1, a, b)];
+                            Gz += (w * (NU - a - b)) * prev[shell_index(NU - 1, a, b)];
                     }
                 }
             const double h = q.fd[mu] - NU * q.f[mu] * q.invd;
@@ -301,7 +304,7 @@ __device__ __forceinline__ void bwd_shells(const DevModel &m, const double4 *A4,
     }
     if constexpr (NU < P::NUMAX) {
         if (P::deeper(m, NU))
-            bwd_shells<NU + 1, P>(m, A4, slot, q, cur, acc);
+            bwd_shells<NU + 1, P>(m, As, slot, q, cur, acc);
     }
 }
 
