@@ -102,6 +102,9 @@ int install_model(mtpx_context *ctx, Model &&m)
     dm.red0 = P.red0;
     dm.priv_doubles = P.priv_doubles;
     dm.tr_delta = P.tr_delta;
+    dm.efs_red = P.efs_red;
+    dm.efs_stage = P.efs_stage;
+    dm.efs_acc = P.efs_acc;
     dm.tr_red1 = P.tr_red1;
     dm.tr_red4 = P.tr_red4;
     dm.tr_stage = P.tr_stage;

@@ -4,10 +4,12 @@
 // (potentials/potential_mtp.cpp:2813-2984, :1899-1933).  The arithmetic is
 // reorganised for a wave64; results agree with the reference to rounding.
 //
-// A workgroup holds up to eight wave64s that share one LDS copy of the model
-// tables (radial coefficients, adjoint seeds, moment coefficients, slot
-// tables and, when they fit, the product-rule step tables).  Each wave owns a
-// private LDS work space and works through its own atoms (grid-stride), so the
+// A workgroup holds up to twelve wave64s (level 16: three per SIMD) that
+// share one LDS copy of the model tables (radial coefficients, adjoint seeds,
+// moment coefficients, slot tables and, when that costs no waves, the
+// product-rule step tables).  Each wave owns a private LDS work space (the
+// transpose buffer lies over the adjoint block, the force pass's adjoints
+// over the moments) and works through its own atoms (grid-stride), so the
 // waves synchronise only at wavefront scope.  Per atom:
 //   1. lanes over neighbours: Chebyshev basis Q_k(d), radial functions
 //      f_mu = sum_k c[ti,tj,mu,k] Q_k (coefficients staged in LDS), unit
@@ -24,8 +26,9 @@
 //      adjoints read as LDS broadcasts.
 //   4. F_i += sum_j D_j, F_idx(j) -= D_j, S_ab -= D_ja r_jb.  Fast mode uses
 //      fp64 atomics for the neighbour reactions; deterministic mode stores D
-//      per pair for an ordered gather.  Energy and virial are reduced per
-//      wave and finished by a single ordered pass.
+//      per pair for an ordered gather.  Each atom's energy and virial are
+//      summed over the lanes (lane swaps and DPP moves) into the wave's
+//      sums in LDS, which a single ordered pass finishes.
 //
 // Kernel variants: a "shell profile" fixes, per radial function mu, the
 // highest angular degree of its basic moments.  The level-10/16/20 template
@@ -49,8 +52,9 @@ __global__ __launch_bounds__(kWave *kMaxWaves) void efs_kernel(DevModel m, DevNe
     const int nwaves = blockDim.x / kWave;
     const Shared L = shared_layout(m, lds);
     double *ws = lds + shared_doubles(m, kTabLds) + (size_t)wave * m.priv_doubles;
-    double *mom = ws, *A = ws + m.K4, *red = ws + m.red0;
-    const double *As = red;  // slot-ordered adjoints (force pass)
+    double *mom = ws, *A = ws + m.K4, *red = ws + m.efs_red;
+    double *As = ws + m.efs_stage;  // slot-ordered adjoints (force pass)
+    double *sums = ws + m.efs_acc;  // the wave's energy and virial[9] (lane 0)
 
     // model tables the per-atom phases index, staged once per workgroup
     stage_shared(m, L, kTabLds, tid, blockDim.x);
@@ -58,12 +62,11 @@ __global__ __launch_bounds__(kWave *kMaxWaves) void efs_kernel(DevModel m, DevNe
     // leave them zero
     for (int k = m.dummy + lane; k < m.red0; k += kWave)
         ws[k] = 0.0;
+    if (lane < 10)
+        sums[lane] = 0.0;
     __syncthreads();
     const int2 *fwd_tab = kTabLds ? L.fwd_steps : m.fwd_steps;
     const int2 *bwd_tab = kTabLds ? L.bwd_steps : m.bwd_steps;
-
-    double e_acc = 0.0;  // this lane's share of the wave's energy and virial
-    double v_acc[9] = {0, 0, 0, 0, 0, 0, 0, 0, 0};
 
     const int row = blockIdx.x * nwaves + wave;
     for (int i = row; i < nb.n; i += gridDim.x * nwaves) {
@@ -88,6 +91,9 @@ __global__ __launch_bounds__(kWave *kMaxWaves) void efs_kernel(DevModel m, DevNe
         if (lane == 0)
             for (int k = 0; k < m.ndup; ++k)
                 mom[m.dup[2 * k]] = mom[m.dup[2 * k + 1]];
+        // the zero slot and the partial sums may lie under the transpose buffer
+        for (int k = m.dummy + lane; k < m.red0; k += kWave)
+            ws[k] = 0.0;
         wave_sync();
 
         run_rules<false, false>(fwd_tab, m.fwd_level_step, m.fwd_level_comb, m.fwd_comb, m.nfwd, ws, lane, 0);
@@ -100,7 +106,7 @@ __global__ __launch_bounds__(kWave *kMaxWaves) void efs_kernel(DevModel m, DevNe
         const double site_energy = m.species[ti] + e;
         if (lane == 0) {
             out.site_energy[i] = site_energy;
-            e_acc += site_energy;
+            sums[0] += site_energy;
         }
         if (flags & kEfsEnergyOnly)  // getE (potential_mtp.cpp:2604-2621): no gradient
             continue;
@@ -116,13 +122,13 @@ __global__ __launch_bounds__(kWave *kMaxWaves) void efs_kernel(DevModel m, DevNe
         // slot-ordered adjoints
         for (int s = lane; s < m.nslots; s += kWave) {
             const int b = L.slot_basic[s];
-            red[s] = b >= 0 ? A[b] : 0.0;
+            As[s] = b >= 0 ? A[b] : 0.0;
         }
         wave_sync();
 
         // ---- forces and virial ---------------------------------------------
         double fi0 = 0, fi1 = 0, fi2 = 0;
-        double vs[9] = {0, 0, 0, 0, 0, 0, 0, 0, 0};  // this atom's virial share
+        double vs[9] = {0, 0, 0, 0, 0, 0, 0, 0, 0};  // this lane's share of the virial
         for (int base = 0; base < n; base += kWave) {
             const bool valid = lane < n - base;
             const int64_t p = beg + base + lane;
@@ -134,15 +140,15 @@ __global__ __launch_bounds__(kWave *kMaxWaves) void efs_kernel(DevModel m, DevNe
             const double D0 = acc.s * q.ux + acc.gx * q.invd;
             const double D1 = acc.s * q.uy + acc.gy * q.invd;
             const double D2 = acc.s * q.uz + acc.gz * q.invd;
-            fi0 += D0;
-            fi1 += D1;
-            fi2 += D2;
             const double r[3] = {q.x, q.y, q.z}, D[3] = {D0, D1, D2};
 #pragma unroll
             for (int a = 0; a < 3; ++a)
 #pragma unroll
                 for (int bq = 0; bq < 3; ++bq)
                     vs[3 * a + bq] -= D[a] * r[bq];
+            fi0 += D0;
+            fi1 += D1;
+            fi2 += D2;
             if (valid) {
                 if (deterministic) {
                     out.pair_ders[3 * p + 0] = D0;
@@ -156,18 +162,6 @@ __global__ __launch_bounds__(kWave *kMaxWaves) void efs_kernel(DevModel m, DevNe
                 }
             }
         }
-#pragma unroll
-        for (int k = 0; k < 9; ++k)
-            v_acc[k] += vs[k];
-        if (out.site_virial) {
-#pragma unroll
-            for (int k = 0; k < 9; ++k)
-                vs[k] = wave_sum(vs[k]);
-            if (lane == 0)
-#pragma unroll
-                for (int k = 0; k < 9; ++k)
-                    out.site_virial[9 * (size_t)i + k] = vs[k];
-        }
         if (!deterministic) {
             fi0 = wave_sum(fi0);
             fi1 = wave_sum(fi1);
@@ -178,19 +172,25 @@ __global__ __launch_bounds__(kWave *kMaxWaves) void efs_kernel(DevModel m, DevNe
                 atomicAdd(&out.forces[3 * i + 2], fi2);
             }
         }
+        // this atom's virial: summed over the lanes, added to the wave's sums
+#pragma unroll
+        for (int k = 0; k < 9; ++k)
+            vs[k] = wave_sum(vs[k]);
+        if (lane == 0) {
+#pragma unroll
+            for (int k = 0; k < 9; ++k)
+                sums[1 + k] += vs[k];
+            if (out.site_virial)
+#pragma unroll
+                for (int k = 0; k < 9; ++k)
+                    out.site_virial[9 * (size_t)i + k] = vs[k];
+        }
         wave_sync();
     }
     // per-wave partials: energy, stress[9]
-    e_acc = wave_sum(e_acc);
-#pragma unroll
-    for (int k = 0; k < 9; ++k)
-        v_acc[k] = wave_sum(v_acc[k]);
-    if (lane == 0) {
-        out.partial[10 * row] = e_acc;
-#pragma unroll
-        for (int k = 0; k < 9; ++k)
-            out.partial[10 * row + 1 + k] = v_acc[k];
-    }
+    wave_sync();
+    if (lane < 10)
+        out.partial[10 * row + lane] = sums[lane];
 }
 
 // Ordered reduction of the per-wave partials (one workgroup).
@@ -249,7 +249,7 @@ __global__ __launch_bounds__(256) void force_gather_kernel(DevNeighbors nb, cons
 // kernels fit 256 registers run eight waves per workgroup, the larger ones four.
 template <class P>
 struct VariantWaves {
-    static constexpr int value = 8;
+    static constexpr int value = 12;
 };
 template <>
 struct VariantWaves<ProfLevel20> {

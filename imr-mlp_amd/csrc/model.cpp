@@ -569,7 +569,23 @@ bool build_plan(const Model &m, Plan &p, std::string &err)
     const int P4 = (p.max_partials + 3) & ~3;
     p.red0 = p.part0 + P4;
     const int N4 = (p.nslots + 3) & ~3;
-    p.priv_doubles = p.red0 + std::max(kChunk * kRedStride, N4);  // transpose buffer | slot A
+    // The moment reduction's transpose buffer lies over the adjoint block
+    // (unused until the seeds are written; the zero slot and the partial sums
+    // under it are cleared again after the neighbour pass) and the force
+    // pass's slot-ordered adjoints over the moments (not read after the
+    // reverse rules), where they fit; then the wave's energy/virial sums.
+    const int RB = kChunk * kRedStride;
+    int end;
+    if (N4 <= p.K4) {
+        p.efs_red = p.K4;
+        p.efs_stage = 0;
+        end = std::max(p.red0, p.K4 + RB);
+    } else {
+        p.efs_red = p.efs_stage = p.red0;
+        end = p.red0 + std::max(RB, N4);
+    }
+    p.efs_acc = (end + 3) & ~3;
+    p.priv_doubles = p.efs_acc + 12;  // energy, virial[9], padding
     if (p.priv_doubles > 0xffff)
         return fail(err, "model too large: per-atom work space exceeds 65535 doubles");
     for (int t = 0; t < m.T; ++t)
@@ -592,11 +608,10 @@ bool build_plan(const Model &m, Plan &p, std::string &err)
     // rules) and the last pass's transpose buffer over the tangents (dead
     // after the staging).
     // Otherwise they get room of their own after the gradient accumulator.
-    const int RB = kChunk * kRedStride;
     p.tr_delta = p.red0;
     p.tr_grad = 2 * p.red0;
     p.tr_ctype = p.tr_grad + ((m.nradial() + 3) & ~3);
-    int end = p.tr_ctype + kWave / 2;  // 64 ints: neighbour species of a batch
+    end = p.tr_ctype + kWave / 2;  // 64 ints: neighbour species of a batch
     int own_red = -1;
     auto red_region = [&] {
         if (own_red < 0) {

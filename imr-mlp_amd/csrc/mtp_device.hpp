@@ -87,13 +87,28 @@ __device__ __forceinline__ double chunk_row_sum(const double *red, int lane)
     return xor16_sum(xor32_sum(a0 + a1));
 }
 
+// v plus the value of the lane that the DPP control kCtrl selects within the
+// lane's row of 16 (VALU lane move, no LDS crossbar).
+template <int kCtrl>
+__device__ __forceinline__ double dpp_add(double v)
+{
+    const int lo = __builtin_amdgcn_update_dpp(0, (int)__double2loint(v), kCtrl, 0xf, 0xf, false);
+    const int hi = __builtin_amdgcn_update_dpp(0, (int)__double2hiint(v), kCtrl, 0xf, 0xf, false);
+    return v + __hiloint2double(hi, lo);
+}
+
+// Sum over the whole wave, in every lane: the two lane swaps, then within
+// each row of 16 the quad permutations [1,0,3,2] and [2,3,0,1], the
+// half-row mirror and the row mirror (each pairs lanes holding disjoint
+// partial sums).
 __device__ __forceinline__ double wave_sum(double v)
 {
     v = xor32_sum(v);
     v = xor16_sum(v);
-#pragma unroll
-    for (int off = 8; off >= 1; off >>= 1)
-        v += __shfl_xor(v, off, kWave);
+    v = dpp_add<0xB1>(v);   // quad_perm [1,0,3,2]
+    v = dpp_add<0x4E>(v);   // quad_perm [2,3,0,1]
+    v = dpp_add<0x141>(v);  // row_half_mirror
+    v = dpp_add<0x140>(v);  // row_mirror
     return v;
 }
 
@@ -465,7 +480,7 @@ __device__ __forceinline__ void stage_shared(const DevModel &m, const Shared &L,
 
 // Launch shape for a kernel whose waves each own `priv_doubles` of LDS work
 // space next to the block-shared model tables: rule tables in LDS unless that
-// costs more than half the waves; false if a single wave does not fit.
+// costs waves; false if a single wave does not fit.
 // table_pref: -1 chooses the step-table placement, 0 keeps the tables in
 // global memory, 1 in LDS where they fit.
 inline bool configure_launch(const DevModel &m, int n, int num_cus, int wcap, size_t lds_limit,
@@ -482,7 +497,7 @@ inline bool configure_launch(const DevModel &m, int n, int num_cus, int wcap, si
     const int wt = fit(true), wg = fit(false);
     if (wg == 0)
         return false;
-    cfg.lds_tables = table_pref < 0 ? wt > 0 && 2 * wt >= wg : table_pref == 1 && wt > 0;
+    cfg.lds_tables = table_pref < 0 ? wt > 0 && wt >= wg : table_pref == 1 && wt > 0;
     cfg.waves = cfg.lds_tables ? wt : wg;
     cfg.lds_bytes = shared_doubles(m, cfg.lds_tables, seeds) * sizeof(double) + cfg.waves * priv;
     const int per_cu = std::max<int>(1, (int)(lds_limit / cfg.lds_bytes));

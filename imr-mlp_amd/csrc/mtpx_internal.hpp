@@ -118,6 +118,9 @@ struct Plan {
     // after the species where they do not fit there.
     int tr_delta = 0, tr_red1 = 0, tr_red4 = 0, tr_stage = 0, tr_grad = 0, tr_ctype = 0,
         tr_priv = 0;
+    // E/F/S kernel: transpose buffer, slot-ordered adjoints and the wave's
+    // energy/virial sums (offsets in doubles).
+    int efs_red = 0, efs_stage = 0, efs_acc = 0;
     // first slot of each (nu, mu) block, -1 where absent: [nu * kMaxMu + mu]
     int slot_base[(kMaxNu + 1) * kMaxMu];
     // Lane-major step tables, one per direction.  Level L owns steps
@@ -184,6 +187,7 @@ struct DevModel {
     int max_partials;
     int K4, dummy, part0, red0, priv_doubles;  // per-wave work space (Plan)
     int tr_delta, tr_red1, tr_red4, tr_stage, tr_grad, tr_ctype, tr_priv;
+    int efs_red, efs_stage, efs_acc;
     int nradial, ncoef;
     int slot_base[(kMaxNu + 1) * kMaxMu];
     int fwd_nsteps, bwd_nsteps;                 // steps per lane, all levels
