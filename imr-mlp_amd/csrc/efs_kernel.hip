@@ -253,7 +253,7 @@ struct VariantWaves {
 };
 template <>
 struct VariantWaves<ProfLevel20> {
-    static constexpr int value = 4;
+    static constexpr int value = 8;
 };
 template <>
 struct VariantWaves<ProfGeneric> {
