@@ -116,55 +116,78 @@ struct RawTables {
     RawTables() : level_step{0}, level_comb{0} {}
 };
 
-// One dependency level: split tasks longer than the fair share (entries /
-// 64) into pieces ending in partial sums, spread the pieces over the 64
-// lanes by longest-processing-time, pad to a multiple of 4 steps.
+// One dependency level: tasks longer than a cap are split into pieces
+// ending in partial sums, the pieces are spread over the 64 lanes by
+// longest-processing-time, and the level is padded to a multiple of 4 steps.
+// The cap is the one, from the fair share (entries / 64) up to the longest
+// task, that gives the fewest steps and then the fewest partial sums: a
+// split that does not shorten the padded level only adds combine work.
 void emit_level(std::vector<Task> &tasks, RawTables &raw)
 {
-    size_t total = 0;
-    for (auto &t : tasks)
-        total += t.size();
-    const size_t cap = std::max<size_t>(4, (total + kWave - 1) / kWave);
-    std::vector<Task> pieces;
-    int npart = 0;
+    size_t total = 0, longest = 0;
     for (auto &t : tasks) {
-        if (t.size() <= cap) {
-            pieces.push_back(t);
-            continue;
-        }
-        const int target = t[0][3];
-        const int first = npart;
-        for (size_t b0 = 0; b0 < t.size(); b0 += cap) {
-            Task piece(t.begin() + b0, t.begin() + std::min(t.size(), b0 + cap));
-            for (Ent &e : piece)
-                e[3] = -2 - npart;
-            piece[0][4] = 1;
-            ++npart;
-            pieces.push_back(std::move(piece));
-        }
-        raw.comb.push_back({target, first, npart - first});
+        total += t.size();
+        longest = std::max(longest, t.size());
     }
-    raw.max_partials = std::max(raw.max_partials, npart);
+    struct Layout {
+        std::vector<Task> pieces;
+        std::vector<std::array<int, 3>> comb;  // target, first partial, count
+        int npart = 0;
+        std::vector<Task> lane;
+        size_t nst = 0;
+    };
+    auto layout = [&](size_t cap) {
+        Layout L;
+        for (auto &t : tasks) {
+            if (t.size() <= cap) {
+                L.pieces.push_back(t);
+                continue;
+            }
+            const int target = t[0][3];
+            const int first = L.npart;
+            for (size_t b0 = 0; b0 < t.size(); b0 += cap) {
+                Task piece(t.begin() + b0, t.begin() + std::min(t.size(), b0 + cap));
+                for (Ent &e : piece)
+                    e[3] = -2 - L.npart;
+                piece[0][4] = 1;
+                ++L.npart;
+                L.pieces.push_back(std::move(piece));
+            }
+            L.comb.push_back({target, first, L.npart - first});
+        }
+        std::vector<int> order(L.pieces.size());
+        for (size_t i = 0; i < order.size(); ++i)
+            order[i] = (int)i;
+        std::stable_sort(order.begin(), order.end(), [&](int a, int b) {
+            return L.pieces[a].size() > L.pieces[b].size();
+        });
+        L.lane.assign(kWave, Task());
+        std::vector<size_t> load(kWave, 0);
+        for (int t : order) {
+            int q = (int)(std::min_element(load.begin(), load.end()) - load.begin());
+            L.lane[q].insert(L.lane[q].end(), L.pieces[t].begin(), L.pieces[t].end());
+            load[q] += L.pieces[t].size();
+        }
+        L.nst = (*std::max_element(load.begin(), load.end()) + 3) & ~size_t(3);
+        return L;
+    };
+    const size_t cap0 = std::max<size_t>(4, (total + kWave - 1) / kWave);
+    Layout best = layout(cap0);
+    for (size_t cap = cap0 + 1; cap <= longest; ++cap) {
+        Layout L = layout(cap);
+        if (L.nst < best.nst || (L.nst == best.nst && L.npart < best.npart))
+            best = std::move(L);
+    }
+    for (const auto &c : best.comb)
+        raw.comb.push_back(c);
+    raw.max_partials = std::max(raw.max_partials, best.npart);
     raw.level_comb.push_back((int)raw.comb.size());
-    std::vector<int> order(pieces.size());
-    for (size_t i = 0; i < order.size(); ++i)
-        order[i] = (int)i;
-    std::stable_sort(order.begin(), order.end(),
-                     [&](int a, int b) { return pieces[a].size() > pieces[b].size(); });
-    std::vector<Task> lane(kWave);
-    std::vector<size_t> load(kWave, 0);
-    for (int t : order) {
-        int q = (int)(std::min_element(load.begin(), load.end()) - load.begin());
-        lane[q].insert(lane[q].end(), pieces[t].begin(), pieces[t].end());
-        load[q] += pieces[t].size();
-    }
-    size_t nst = *std::max_element(load.begin(), load.end());
-    nst = (nst + 3) & ~size_t(3);
+    const size_t nst = best.nst;
     const size_t base = raw.steps.size() / kWave;
     raw.steps.resize((base + nst) * kWave, Ent{-1, -1, 0, -1, 1});  // padding
     for (int q = 0; q < kWave; ++q)
-        for (size_t st = 0; st < lane[q].size(); ++st)
-            raw.steps[(base + st) * kWave + q] = lane[q][st];
+        for (size_t st = 0; st < best.lane[q].size(); ++st)
+            raw.steps[(base + st) * kWave + q] = best.lane[q][st];
     raw.level_step.push_back((int)(base + nst));
 }
 
