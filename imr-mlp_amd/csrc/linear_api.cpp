@@ -27,13 +27,14 @@ CompLayout comp_layout(const mtpx_context *ctx)
     return l;
 }
 
-// Pair-buffer budget of one group of structures (MTPX_LIN_PAIR_MB, tuning);
-// a structure larger than the budget forms a group of its own.
+// Pair-buffer budget of one group of structures (MTPX_LIN_PAIR_MB, tuning;
+// 8 GiB by default: fewer, larger groups keep the site kernel's launches
+// full); a structure larger than the budget forms a group of its own.
 size_t pair_budget()
 {
     const char *e = getenv("MTPX_LIN_PAIR_MB");
     const long v = e ? atol(e) : 0;
-    return (v > 0 ? (size_t)v : (size_t)1024) << 20;
+    return (v > 0 ? (size_t)v : (size_t)8192) << 20;
 }
 
 // Components of every structure of the resident topology into ctx->comp,
