@@ -33,17 +33,21 @@ namespace {
 
 typedef double d4v __attribute__((ext_vector_type(4)));
 
+// Read-only model table in the constant address space: wave-uniform
+// indices compile to scalar loads (SGPRs, no VALU work).
+typedef const int __attribute__((address_space(4))) const_int;
+
 // The tables of one chunk for a walk.  Compile-time walks (exact
-// profiles) hold the chunk's slot masks (4 per word) and its L values in
-// walk order in two lane registers each and read them with readlane: no
-// memory access and no dependent load in the walk.  Runtime walks read the
+// profiles) read the chunk's slot masks (4 per word) with scalar loads and
+// hold its L values in walk order in two lane registers, read with
+// readlane: no dependent vector load in the walk.  Runtime walks read the
 // per-slot mask and L-index tables.
 struct LinWalk {
-    const int *mask;  // [nslots]
-    const int *lidx;  // [nslots][kLinChunk]
-    int mw0, mw1;     // lane l: mask words l and 64 + l
-    double lc0, lc1;  // lane l: L values of entries l and 64 + l
-    int pos;          // next entry (uniform)
+    const int *mask;      // [nslots]
+    const int *lidx;      // [nslots][kLinChunk]
+    const const_int *mw;  // [kLinMaskWords] slot masks of the chunk, 4 per word
+    double lc0, lc1;      // lane l: L values of entries l and 64 + l
+    int pos;              // next entry (uniform)
 };
 
 __device__ __forceinline__ double readlane_d(double v, int l)
@@ -145,8 +149,7 @@ __device__ __forceinline__ void lin_shells(const DevModel &m, const Nbr<P::M> &q
                     constexpr int i = decltype(I)::value;
                     constexpr int a = shell_a(NU, i), b = shell_b(NU, i), c = NU - a - b;
                     const int sl = slot + i;
-                    const int word = sl / 4 < 64 ? __builtin_amdgcn_readlane(w.mw0, sl / 4)
-                                                 : __builtin_amdgcn_readlane(w.mw1, sl / 4 - 64);
+                    const int word = w.mw[sl / 4];
                     const int mk = (word >> (8 * (sl % 4))) & 0xff;
                     if (mk) {
                         const double hy = h * cur[i];
@@ -281,10 +284,8 @@ __global__ __launch_bounds__(kWave *kMaxWaves) void lin_site_kernel(DevModel m, 
                 LinWalk w;
                 w.pos = 0;
                 if constexpr (P::exact) {
-                    const int *mwp = L.maskw + (size_t)ch * kLinMaskWords;
+                    w.mw = (const const_int *)(L.maskw + (size_t)ch * kLinMaskWords);
                     const int *clp = L.clist + (size_t)ch * kLinEntries;
-                    w.mw0 = mwp[lane];
-                    w.mw1 = mwp[kWave + lane];
                     w.lc0 = ws[clp[lane]];
                     w.lc1 = ws[clp[kWave + lane]];
                 } else {
