@@ -163,6 +163,12 @@ int install_model(mtpx_context *ctx, Model &&m)
         L.maskw = ctx->lin_maskw.as<int>();
         L.clist = ctx->lin_clist.as<int>();
         L.lane_walk = lp.lane_walk ? 1 : 0;
+        // MTPX_LIN_WALK=runtime (tuning): keep the run-time walk
+        static const bool runtime_walk = [] {
+            const char *e = getenv("MTPX_LIN_WALK");
+            return e && std::string(e) == "runtime";
+        }();
+        L.compiled_walk = !runtime_walk && lin_walk_compiled(lp, P.nslots) ? 1 : 0;
     }
     int rc = upload_coeffs(ctx);
     if (rc != MTPX_OK)

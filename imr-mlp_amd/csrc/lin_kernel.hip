@@ -28,6 +28,12 @@
 #include <type_traits>
 
 namespace mtpx {
+namespace {
+#include "lin_plan_level16.inc"
+}  // namespace
+}  // namespace mtpx
+
+namespace mtpx {
 
 namespace {
 
@@ -206,6 +212,115 @@ __device__ __forceinline__ void lin_shells(const DevModel &m, const Nbr<P::M> &q
     }
 }
 
+// ---- walk of a compiled plan ---------------------------------------------
+// For a model whose plan equals a generated table (lin_plan_*.inc) every
+// mask, walk position and L index is a compile-time constant: the walk is
+// straight-line code over the chunk's used slots only, with each L value an
+// LDS broadcast read at a constant offset (no mask tests, no readlane).
+
+constexpr int popc(int x)
+{
+    int n = 0;
+    for (; x; x &= x - 1)
+        ++n;
+    return n;
+}
+
+// First slot of the (nu, mu) block of an exact profile: degree ascending,
+// then mu ascending over the functions that reach the degree.
+template <class P>
+constexpr int exact_slot_base(int nu, int mu)
+{
+    int s = 0;
+    for (int v = 0; v < nu; ++v)
+        for (int u = 0; u < P::M; ++u)
+            if (P::nm[u] >= v)
+                s += shell_size(v);
+    for (int u = 0; u < mu; ++u)
+        if (P::nm[u] >= nu)
+            s += shell_size(nu);
+    return s;
+}
+
+template <class P>
+constexpr int exact_slot_count()
+{
+    return exact_slot_base<P>(P::NUMAX + 1, 0);
+}
+
+// Walk position of the first entry of slot `sl` in chunk `c`.
+template <class CP>
+constexpr int walk_pos(int c, int sl)
+{
+    int e = 0;
+    for (int s = 0; s < sl; ++s)
+        e += popc(CP::mask[c][s]);
+    return e;
+}
+
+template <class CP, int C, int NU, class P>
+__device__ __forceinline__ void lin_shells_cp(const Nbr<P::M> &q, const double *prev,
+                                              const double *ws, double (&acc)[3 * kLinChunk])
+{
+    double cur[shell_size(NU)];
+    if constexpr (NU == 0)
+        cur[0] = 1.0;
+    else
+        next_shell<NU, P::M>(prev, cur, q);
+    static_for<0, P::M>([&](auto MU) __attribute__((always_inline)) {
+        constexpr int mu = decltype(MU)::value;
+        if constexpr (P::nm[mu] >= NU) {
+            __builtin_amdgcn_sched_barrier(0);
+            const double h = q.fd[mu] - NU * q.f[mu] * q.invd;
+            const double fdi = q.f[mu] * q.invd;
+            static_for<0, shell_size(NU)>([&](auto I) __attribute__((always_inline)) {
+                constexpr int i = decltype(I)::value;
+                constexpr int sl = exact_slot_base<P>(NU, mu) + i;
+                constexpr int mk = CP::mask[C][sl];
+                if constexpr (mk != 0) {
+                    // one slot at a time: bounds the L values in flight
+                    __builtin_amdgcn_sched_barrier(0);
+                    constexpr int a = shell_a(NU, i), b = shell_b(NU, i), c = NU - a - b;
+                    const double hy = h * cur[i];
+                    double gx = hy * q.ux, gy = hy * q.uy, gz = hy * q.uz;
+                    if constexpr (a > 0)
+                        gx += (a * fdi) * prev[shell_index(NU - 1, a - 1, b)];
+                    if constexpr (b > 0)
+                        gy += (b * fdi) * prev[shell_index(NU - 1, a, b - 1)];
+                    if constexpr (c > 0)
+                        gz += (c * fdi) * prev[shell_index(NU - 1, a, b)];
+                    constexpr int e0 = walk_pos<CP>(C, sl);
+                    static_for<0, kLinChunk>([&](auto K) __attribute__((always_inline)) {
+                        constexpr int k = decltype(K)::value;
+                        if constexpr ((mk >> k) & 1) {
+                            constexpr int e = e0 + popc(mk & ((1 << k) - 1));
+                            const double lv = ws[CP::clist[C][e]];  // LDS broadcast
+                            acc[3 * k] += lv * gx;
+                            acc[3 * k + 1] += lv * gy;
+                            acc[3 * k + 2] += lv * gz;
+                        }
+                    });
+                }
+            });
+        }
+    });
+    if constexpr (NU < P::NUMAX)
+        lin_shells_cp<CP, C, NU + 1, P>(q, cur, ws, acc);
+}
+
+// The compiled walk of chunk `ch` (a chain of uniform compares).
+template <class CP, int C, class P>
+__device__ __forceinline__ void lin_chunk_cp(int ch, const Nbr<P::M> &q, const double *ws,
+                                             double (&acc)[3 * kLinChunk])
+{
+    if (ch == C) {
+        lin_shells_cp<CP, C, 0, P>(q, nullptr, ws, acc);
+        return;
+    }
+    if constexpr (C + 1 < CP::nchunks)
+        lin_chunk_cp<CP, C + 1, P>(ch, q, ws, acc);
+}
+
 // Makes the neighbour's values opaque to the optimiser (no instruction):
 // the shell values of a chunk walk are then recomputed per chunk instead of
 // being hoisted out of the chunk loop, which would keep all of them live.
@@ -218,7 +333,7 @@ __device__ __forceinline__ void opaque(Nbr<MMAX> &q)
         asm volatile("" : "+v"(q.f[mu]), "+v"(q.fd[mu]));
 }
 
-template <class P, int kMaxWaves>
+template <class P, int kMaxWaves, class CP = void>
 __global__ __launch_bounds__(kWave *kMaxWaves) void lin_site_kernel(DevModel m, DevLin L,
                                                                     DevNeighbors nb, LinGroup g)
 {
@@ -279,6 +394,28 @@ __global__ __launch_bounds__(kWave *kMaxWaves) void lin_site_kernel(DevModel m, 
             Nbr<P::M> q;
             load_neighbor<P>(m, nb, Ls.coef, ti, pe, valid, q);
             double *dst = g.pair + (size_t)(pe - g.e0) * 3 * g.Sp;
+            if constexpr (!std::is_void_v<CP>) {
+                // a run-time loop over the chunks (each chunk's walk is its
+                // own block: registers are allocated chunk by chunk)
+                for (int ch = 0; ch < CP::nchunks; ++ch) {
+                    const int s0 = L.chunk_s0[ch], nch = L.chunk_s0[ch + 1] - s0;
+                    double acc[3 * kLinChunk];
+#pragma unroll
+                    for (int r = 0; r < 3 * kLinChunk; ++r)
+                        acc[r] = 0.0;
+                    opaque(q);
+                    lin_chunk_cp<CP, 0, P>(ch, q, ws, acc);
+                    if (valid) {
+#pragma unroll
+                        for (int a = 0; a < 3; ++a)
+#pragma unroll
+                            for (int k = 0; k < kLinChunk; ++k)
+                                if (k < nch)
+                                    dst[a * g.Sp + s0 + k] = acc[3 * k + a];
+                    }
+                }
+                continue;
+            }
             for (int ch = 0; ch < L.nchunks; ++ch) {
                 const int s0 = L.chunk_s0[ch], nch = L.chunk_s0[ch + 1] - s0;
                 LinWalk w;
@@ -508,23 +645,50 @@ struct LinWaves<ProfLevel10> {
     static constexpr int value = 8;
 };
 
-template <class P>
+template <class P, class CP = void>
 void launch_lin_variant(const DevModel &m, const DevLin &L, const DevNeighbors &nb,
                         const LinGroup &g, const EfsLaunch &cfg, hipStream_t s)
 {
     constexpr int W = LinWaves<P>::value;
-    hipLaunchKernelGGL((lin_site_kernel<P, W>), dim3(cfg.grid), dim3(kWave * cfg.waves),
+    hipLaunchKernelGGL((lin_site_kernel<P, W, CP>), dim3(cfg.grid), dim3(kWave * cfg.waves),
                        cfg.lds_bytes, s, m, L, nb, g);
 }
+
+static_assert(exact_slot_count<ProfLevel16>() == LinPlanLevel16::nslots,
+              "the compiled level-16 walk must cover the level-16 profile's slots");
 
 }  // namespace
 
 // The E/F/S variant, or the generic one where the compile-time walk's
-// tables do not hold the plan.
+// tables do not hold the plan; 5: the level-16 profile with the compiled
+// level-16 walk.
 int lin_variant(const DevModel &m, const DevLin &L)
 {
     const int v = efs_variant(m, m.R);
+    if (v == 0 && L.compiled_walk)
+        return 5;
     return v <= 2 && !L.lane_walk ? 4 : v;
+}
+
+// True when the plan equals the compiled level-16 walk (same chunks, masks
+// and L indices), so that walk computes exactly what the run-time walk would.
+bool lin_walk_compiled(const LinPlan &lp, int nslots)
+{
+    using CP = LinPlanLevel16;
+    if (!lp.lane_walk || lp.nchunks != CP::nchunks || nslots != CP::nslots)
+        return false;
+    for (int c = 0; c <= CP::nchunks; ++c)
+        if (lp.chunk_s0[c] != CP::chunk_s0[c])
+            return false;
+    for (int c = 0; c < CP::nchunks; ++c) {
+        for (int s = 0; s < CP::nslots; ++s)
+            if (lp.slot_mask[(size_t)c * nslots + s] != CP::mask[c][s])
+                return false;
+        for (int e = 0; e < kLinEntries; ++e)
+            if (lp.clist[(size_t)c * kLinEntries + e] != CP::clist[c][e])
+                return false;
+    }
+    return true;
 }
 
 bool lin_configure(const DevModel &m, const DevLin &L, int n, int num_cus, size_t lds_limit,
@@ -552,6 +716,7 @@ hipError_t launch_lin_site(const DevModel &m, const DevLin &L, const DevNeighbor
         return hipSuccess;
     switch (lin_variant(m, L)) {
     case 0: launch_lin_variant<ProfLevel16>(m, L, nb, g, cfg, s); break;
+    case 5: launch_lin_variant<ProfLevel16, LinPlanLevel16>(m, L, nb, g, cfg, s); break;
     case 1: launch_lin_variant<ProfLevel20>(m, L, nb, g, cfg, s); break;
     case 2: launch_lin_variant<ProfLevel10>(m, L, nb, g, cfg, s); break;
     case 3: launch_lin_variant<ProfSmall>(m, L, nb, g, cfg, s); break;

@@ -244,6 +244,7 @@ struct DevLin {
     int dummy, red0, nfwd;
     int nL, one, L0, part0, acc, priv, CH, nchunks, nlev;
     int lane_walk;
+    int compiled_walk;  // the plan equals the compiled level-16 walk (lin_walk_compiled)
     const int *fwd_level_step, *fwd_level_comb;  // [nfwd + 1]
     const int2 *fwd_steps;
     const int4 *fwd_comb;
@@ -269,6 +270,7 @@ struct LinGroup {
 };
 bool lin_configure(const DevModel &m, const DevLin &L, int n, int num_cus, size_t lds_limit,
                    EfsLaunch &cfg);
+bool lin_walk_compiled(const LinPlan &lp, int nslots);
 hipError_t launch_lin_site(const DevModel &m, const DevLin &L, const DevNeighbors &nb,
                            const LinGroup &g, const EfsLaunch &cfg, hipStream_t s);
 hipError_t launch_lin_gather(const DevModel &m, const DevNeighbors &nb, const int *rev_off,

@@ -130,3 +130,30 @@ def test_loss_weights_flags():
     active, wE, wF, wS = capi.loss_weights(cs, [0, 3, 3, 5], [[1, 1, 1], [1, 1, 1], [0, 1, 0]])
     assert active.tolist() == [[1, 1, 0], [0, 0, 0], [0, 1, 0]]
     assert wS.tolist() == [0.0, 0.0, 0.0] and wE[1] == 0.0 and wE[2] == 0.0
+
+
+def test_compiled_linear_walk_is_current(tmp_path):
+    """The level-16 walk compiled into the linear-fit kernel
+    (csrc/lin_plan_level16.inc) equals what the library's plan code computes
+    for the level-16 template today (regenerated with gen_lin_plan.cpp)."""
+    import os
+    import shutil
+    import subprocess
+    hipcc = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+    if not os.path.exists(hipcc):
+        pytest.skip("hipcc is not available")
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    pkg = os.path.join(root, "imr-mlp_amd")
+    exe = str(tmp_path / "gen_lin_plan")
+    subprocess.run([hipcc, "-O1", "-std=c++17", "-w", "-I", os.path.join(root, "include"),
+                    "-I", os.path.join(pkg, "csrc"), os.path.join(pkg, "gen_lin_plan.cpp"),
+                    os.path.join(pkg, "csrc", "model.cpp"), "-o", exe], check=True)
+    rel = "tests/golden/templates/shapeev-16.mtp"
+    out = subprocess.run([exe, rel, "LinPlanLevel16"], cwd=root, check=True,
+                         capture_output=True, text=True).stdout
+    with open(os.path.join(pkg, "csrc", "lin_plan_level16.inc")) as f:
+        assert f.read() == out
+    # another structure gives another plan (the kernel keeps the run-time walk)
+    other = subprocess.run([exe, "tests/golden/templates/shapeev-20.mtp", "LinPlanLevel16"],
+                           cwd=root, check=True, capture_output=True, text=True).stdout
+    assert other.split("struct", 1)[1] != out.split("struct", 1)[1]
