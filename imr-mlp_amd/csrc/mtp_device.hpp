@@ -328,9 +328,10 @@ __device__ __forceinline__ void bwd_shells(const DevModel &m, const double *As, 
 // level at a time.  Steps are taken in groups of four: the entries of the
 // next group are loaded while the current one runs, and every operand of a
 // group is read before any of its results is written (a level never reads
-// what it writes).  A task's sum starts from its target's value (kInit:
-// adjoints, which start from their seeds) or from zero (outputs and partial
-// sums, which start at zero), and is written on the task's last entry.
+// what it writes).  A task's sum starts from zero and is stored on the
+// task's last entry: added to its target (kInit: adjoints, which start from
+// their seeds) or written over it (outputs and partial sums, which start at
+// zero).  No task reads or writes another task's target within a level.
 //
 // kDual also carries a second copy of the work space `delta` doubles further
 // on: for a step  x_w += c x_l x_r  it adds  c (x'_l x_r + x_l x'_r)  to x'_w.
@@ -358,31 +359,32 @@ __device__ __forceinline__ void run_rules(const int2 *tab, const int *level_step
                     nx[2] = u[2 * kWave];
                     nx[3] = u[3 * kWave];
                 }
-                double ml[4], mr[4], init[4];
-                double dl[4], dr[4], dinit[4];
+                double ml[4], mr[4];
+                double dl[4], dr[4];
 #pragma unroll
                 for (int k = 0; k < 4; ++k) {
-                    const int l = e[k].x & 0xffff, r = (unsigned)e[k].x >> 16, w = e[k].y & 0xffff;
+                    const int l = e[k].x & 0xffff, r = (unsigned)e[k].x >> 16;
                     ml[k] = ws[l];
                     mr[k] = ws[r];
-                    init[k] = kInit ? ws[w] : 0.0;
                     if constexpr (kDual) {
                         dl[k] = wd[l];
                         dr[k] = wd[r];
-                        dinit[k] = kInit ? wd[w] : 0.0;
                     }
                 }
 #pragma unroll
                 for (int k = 0; k < 4; ++k) {
                     const double c = (double)(e[k].y >> 18);
-                    const bool first = e[k].y & 0x10000;
-                    acc = fma(c * ml[k], mr[k], first ? init[k] : acc);
+                    acc = fma(c * ml[k], mr[k], acc);
                     if constexpr (kDual)
-                        acd = fma(c * ml[k], dr[k], fma(c * dl[k], mr[k], first ? dinit[k] : acd));
+                        acd = fma(c * ml[k], dr[k], fma(c * dl[k], mr[k], acd));
                     if (e[k].y & 0x20000) {
-                        ws[e[k].y & 0xffff] = acc;
-                        if constexpr (kDual)
-                            wd[e[k].y & 0xffff] = acd;
+                        const int w = e[k].y & 0xffff;
+                        ws[w] = kInit ? ws[w] + acc : acc;
+                        acc = 0.0;
+                        if constexpr (kDual) {
+                            wd[w] = kInit ? wd[w] + acd : acd;
+                            acd = 0.0;
+                        }
                     }
                 }
 #pragma unroll

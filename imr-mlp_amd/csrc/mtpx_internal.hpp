@@ -127,9 +127,10 @@ struct Plan {
     // [level_step[L], level_step[L+1]) (a multiple of 4); step s of lane q is
     // entry s * 64 + q, an int2 of work-space indices:
     //   x = l | r << 16,  y = w | first << 16 | last << 17 | c << 18  (c signed)
-    //   acc = c * ws[l] * ws[r] + (first ? init : acc);  if (last) ws[w] = acc
+    //   acc += c * ws[l] * ws[r];  if (last) { ws[w] = init + acc; acc = 0; }
     // with init = ws[w] for targets that start from a value (adjoints and
-    // their seeds) and 0 otherwise.
+    // their seeds) and 0 otherwise (a task's sum starts from zero; the first
+    // flag marks a task's first entry and is not needed by the kernels).
     // Forward entries read two moments and write a rule output; reverse
     // entries read an adjoint and a moment and write an adjoint (whose
     // initial value is its seed).  A task (all rules of one output, or all
@@ -137,7 +138,7 @@ struct Plan {
     // (entries / 64) is split into pieces that write zeroed partial sums; the
     // level's combine list {target, first partial, count, 0} then adds them
     // in order to the target and clears them.  Padding steps have c = 0 and
-    // read and write the dummy slot.  Tasks and pieces are spread over the
+    // read the dummy slot and write nothing.  Tasks and pieces are spread over the
     // lanes by longest-processing-time assignment.
     std::vector<int> fwd_level_step, fwd_steps, fwd_level_comb, fwd_comb;
     std::vector<int> bwd_level_step, bwd_steps, bwd_level_comb, bwd_comb;
