@@ -254,64 +254,81 @@ struct Construct {
     double cutoffsq;
 };
 
-// construct() (neighborhood.cpp:89-141) for one centre.  MODE 0 counts the
-// entries of every list, MODE 1 writes them with their keys.
+// construct() (neighborhood.cpp:89-141) for one centre per wave.  MODE 0
+// counts the entries of every list, MODE 1 writes them with their keys.
+// The lanes test 64 candidates of a box at a time; an accepted candidate's
+// event number (its rank among the centre's accepted candidates in the
+// reference's traversal order) is the count so far plus the accepted lanes
+// below it, so the keys, and the lists they order, are those of the serial
+// traversal.
 template <int MODE>
-__global__ void construct_kernel(Construct c, int *cnt, int *cursor, uint64_t *key, int *st_idx,
-                                 int *st_type, double *st_vec, double *st_d)
+__global__ __launch_bounds__(256) void construct_kernel(Construct c, int *cnt, int *cursor,
+                                                        uint64_t *key, int *st_idx, int *st_type,
+                                                        double *st_vec, double *st_d)
 {
-    const int indi = blockIdx.x * blockDim.x + threadIdx.x;
+    const int lane = threadIdx.x & 63;
+    const int indi = blockIdx.x * (blockDim.x / 64) + threadIdx.x / 64;
     if (indi >= c.n)
-        return;
+        return;  // uniform over the wave
     const int b = c.centre_box[indi];
     const int bi = b / (c.bl1 * c.bl2), bj = (b / c.bl2) % c.bl1, bk = b % c.bl2;
     const double pi0 = c.pts[3 * indi], pi1 = c.pts[3 * indi + 1], pi2 = c.pts[3 * indi + 2];
     const uint64_t krank = (uint64_t)(unsigned)c.rank[indi] << 32;
+    const uint64_t below = (1ull << lane) - 1;
     unsigned ev = 0;
     int own = 0;
     for (int l1 = -1; l1 <= 1; l1++)
         for (int l2 = -1; l2 <= 1; l2++)
             for (int l3 = -1; l3 <= 1; l3++) {
                 const int nb = ((bi + l1) * c.bl1 + (bj + l2)) * c.bl2 + (bk + l3);
-                for (int t = c.box_start[nb]; t < c.box_start[nb + 1]; ++t) {
-                    const int indj = c.items[t];
-                    const double r0 = c.pts[3 * indj] - pi0;
-                    const double r1 = c.pts[3 * indj + 1] - pi1;
-                    const double r2 = c.pts[3 * indj + 2] - pi2;
-                    const double dijsq = r0 * r0 + r1 * r1 + r2 * r2;
-                    const int oj = c.orig[indj];
-                    if (!(dijsq < c.cutoffsq && indi != indj && indi <= oj))
-                        continue;
-                    if (MODE == 0) {
-                        ++own;
-                        if (indi != oj)
-                            atomicAdd(&cnt[oj], 1);
-                    } else {
-                        const double dij = sqrt(dijsq);
-                        const uint64_t k = krank | ev;
-                        int q = atomicAdd(&cursor[indi], 1);
-                        key[q] = k;
-                        st_idx[q] = oj;
-                        st_type[q] = c.types[oj];
-                        st_vec[3 * (int64_t)q] = r0;
-                        st_vec[3 * (int64_t)q + 1] = r1;
-                        st_vec[3 * (int64_t)q + 2] = r2;
-                        st_d[q] = dij;
-                        if (indi != oj) {
-                            q = atomicAdd(&cursor[oj], 1);
+                const int t0 = c.box_start[nb], t1 = c.box_start[nb + 1];
+                for (int tb = t0; tb < t1; tb += 64) {
+                    const int t = tb + lane;
+                    bool ok = false;
+                    double r0 = 0.0, r1 = 0.0, r2 = 0.0, dijsq = 0.0;
+                    int oj = 0;
+                    if (t < t1) {
+                        const int indj = c.items[t];
+                        r0 = c.pts[3 * indj] - pi0;
+                        r1 = c.pts[3 * indj + 1] - pi1;
+                        r2 = c.pts[3 * indj + 2] - pi2;
+                        dijsq = r0 * r0 + r1 * r1 + r2 * r2;
+                        oj = c.orig[indj];
+                        ok = dijsq < c.cutoffsq && indi != indj && indi <= oj;
+                    }
+                    const uint64_t acc = __ballot(ok);
+                    if (ok) {
+                        if (MODE == 0) {
+                            if (indi != oj)
+                                atomicAdd(&cnt[oj], 1);
+                        } else {
+                            const double dij = sqrt(dijsq);
+                            const uint64_t k = krank | (ev + (unsigned)__popcll(acc & below));
+                            int q = atomicAdd(&cursor[indi], 1);
                             key[q] = k;
-                            st_idx[q] = indi;
-                            st_type[q] = c.types[indi];
-                            st_vec[3 * (int64_t)q] = -r0;
-                            st_vec[3 * (int64_t)q + 1] = -r1;
-                            st_vec[3 * (int64_t)q + 2] = -r2;
+                            st_idx[q] = oj;
+                            st_type[q] = c.types[oj];
+                            st_vec[3 * (int64_t)q] = r0;
+                            st_vec[3 * (int64_t)q + 1] = r1;
+                            st_vec[3 * (int64_t)q + 2] = r2;
                             st_d[q] = dij;
+                            if (indi != oj) {
+                                q = atomicAdd(&cursor[oj], 1);
+                                key[q] = k;
+                                st_idx[q] = indi;
+                                st_type[q] = c.types[indi];
+                                st_vec[3 * (int64_t)q] = -r0;
+                                st_vec[3 * (int64_t)q + 1] = -r1;
+                                st_vec[3 * (int64_t)q + 2] = -r2;
+                                st_d[q] = dij;
+                            }
                         }
                     }
-                    ++ev;
+                    ev += (unsigned)__popcll(acc);
+                    own += __popcll(acc);
                 }
             }
-    if (MODE == 0)
+    if (MODE == 0 && lane == 0)
         atomicAdd(&cnt[indi], own);
 }
 
@@ -713,7 +730,8 @@ int build_neighbors_gpu(const double cell[9], const int pbc[3], int n, const dou
     DTRY(w.cursor.ensure(sizeof(int) * ((size_t)n + 1)));
     int *cnt = w.cursor.as<int>();
     DTRY(hipMemsetAsync(cnt, 0, sizeof(int) * ((size_t)n + 1), s));
-    hipLaunchKernelGGL(construct_kernel<0>, dim3(blocks(n, 128)), dim3(128), 0, s, cs, cnt,
+    // one wave per centre, four per workgroup
+    hipLaunchKernelGGL(construct_kernel<0>, dim3((n + 3) / 4), dim3(256), 0, s, cs, cnt,
                        nullptr, nullptr, nullptr, nullptr, nullptr, nullptr);
     DTRY(scan_exclusive(cnt, (int64_t)n + 1, out.offsets.as<int>(), w.tmp, w.scalars.as<int>(), s));
     int Pi = 0;
@@ -736,7 +754,7 @@ int build_neighbors_gpu(const double cell[9], const int pbc[3], int n, const dou
     DTRY(w.st_vec.ensure(sizeof(double) * 3 * Pz));
     DTRY(w.st_d.ensure(sizeof(double) * Pz));
     DTRY(hipMemcpyAsync(cnt, out.offsets.p, sizeof(int) * n, hipMemcpyDeviceToDevice, s));
-    hipLaunchKernelGGL(construct_kernel<1>, dim3(blocks(n, 128)), dim3(128), 0, s, cs, nullptr, cnt,
+    hipLaunchKernelGGL(construct_kernel<1>, dim3((n + 3) / 4), dim3(256), 0, s, cs, nullptr, cnt,
                        w.key.as<uint64_t>(), w.st_idx.as<int>(), w.st_type.as<int>(),
                        w.st_vec.as<double>(), w.st_d.as<double>());
     DTRY(w.flags.ensure(sizeof(int) * Pz));
