@@ -195,19 +195,20 @@ __global__ void box_place_kernel(const int *box, int npts, int *box_cur, int *it
     items[q] = i;
 }
 
-__global__ void box_rank_kernel(const int *box_start, int nbox, const int *unsorted, int *items)
+// One thread per point: its slot in its box is the number of the box's
+// points with a smaller index (a box of a small cell can hold every point).
+__global__ void box_rank_kernel(const int *box, const int *box_start, int npts,
+                                const int *unsorted, int *items)
 {
-    const int b = blockIdx.x * blockDim.x + threadIdx.x;
-    if (b >= nbox)
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= npts)
         return;
+    const int b = box[i];
     const int s = box_start[b], e = box_start[b + 1];
-    for (int q = s; q < e; ++q) {
-        const int v = unsorted[q];
-        int r = 0;
-        for (int u = s; u < e; ++u)
-            r += unsorted[u] < v;
-        items[s + r] = v;
-    }
+    int r = 0;
+    for (int u = s; u < e; ++u)
+        r += unsorted[u] < i;
+    items[s + r] = i;
 }
 
 // Originals per interior box, in the lexicographic walk order of construct().
@@ -697,8 +698,9 @@ int build_neighbors_gpu(const double cell[9], const int pbc[3], int n, const dou
     int *unsorted = w.flags.as<int>();
     hipLaunchKernelGGL(box_place_kernel, dim3(blocks(npts, 256)), dim3(256), 0, s,
                        w.box.as<int>(), npts, w.box_cur.as<int>(), unsorted);
-    hipLaunchKernelGGL(box_rank_kernel, dim3(blocks(nbox, 256)), dim3(256), 0, s,
-                       w.box_start.as<int>(), (int)nbox, unsorted, w.box_items.as<int>());
+    hipLaunchKernelGGL(box_rank_kernel, dim3(blocks(npts, 256)), dim3(256), 0, s,
+                       w.box.as<int>(), w.box_start.as<int>(), (int)npts, unsorted,
+                       w.box_items.as<int>());
 
     // processing ranks of the centres
     const int64_t ninterior = (int64_t)(g.bl[0] - 2) * (g.bl[1] - 2) * (g.bl[2] - 2);
