@@ -270,7 +270,6 @@ __device__ __forceinline__ void lin_shells_cp(const Nbr<P::M> &q, const double *
     static_for<0, P::M>([&](auto MU) __attribute__((always_inline)) {
         constexpr int mu = decltype(MU)::value;
         if constexpr (P::nm[mu] >= NU) {
-            __builtin_amdgcn_sched_barrier(0);
             const double h = q.fd[mu] - NU * q.f[mu] * q.invd;
             const double fdi = q.f[mu] * q.invd;
             static_for<0, shell_size(NU)>([&](auto I) __attribute__((always_inline)) {
@@ -278,8 +277,6 @@ __device__ __forceinline__ void lin_shells_cp(const Nbr<P::M> &q, const double *
                 constexpr int sl = exact_slot_base<P>(NU, mu) + i;
                 constexpr int mk = CP::mask[C][sl];
                 if constexpr (mk != 0) {
-                    // one slot at a time: bounds the L values in flight
-                    __builtin_amdgcn_sched_barrier(0);
                     constexpr int a = shell_a(NU, i), b = shell_b(NU, i), c = NU - a - b;
                     const double hy = h * cur[i];
                     double gx = hy * q.ux, gy = hy * q.uy, gz = hy * q.uz;
