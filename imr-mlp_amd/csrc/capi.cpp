@@ -33,22 +33,9 @@ int upload_coeffs(mtpx_context *ctx)
     return MTPX_OK;
 }
 
-int install_model(mtpx_context *ctx, Model &&m)
+// Sizes and work-space offsets of the device view (no device pointers).
+void fill_model_sizes(const Model &M, const Plan &P, DevModel &dm)
 {
-    std::string err;
-    if (!validate_model(m, err))
-        return set_error(ctx, MTPX_E_MODEL, err);
-    Plan p;
-    if (!build_plan(m, p, err))
-        return set_error(ctx, MTPX_E_MODEL, err);
-    ctx->model = std::move(m);
-    ctx->plan = std::move(p);
-    ctx->has_batch_out = false;
-    ctx->has_adjoints = false;
-    const Model &M = ctx->model;
-    const Plan &P = ctx->plan;
-    DevModel &dm = ctx->dm;
-    dm = DevModel{};
     dm.Z = M.Z;
     dm.M = M.M;
     dm.R = M.R;
@@ -70,6 +57,55 @@ int install_model(mtpx_context *ctx, Model &&m)
     dm.ndup = (int)P.dup.size() / 2;
     dm.nfwd = (int)P.fwd_level_step.size() - 1;
     dm.nbwd = (int)P.bwd_level_step.size() - 1;
+    dm.max_partials = P.max_partials;
+    dm.K4 = P.K4;
+    dm.dummy = P.dummy;
+    dm.part0 = P.part0;
+    dm.red0 = P.red0;
+    dm.priv_doubles = P.priv_doubles;
+    dm.tr_delta = P.tr_delta;
+    dm.efs_red = P.efs_red;
+    dm.efs_stage = P.efs_stage;
+    dm.efs_acc = P.efs_acc;
+    dm.tr_red1 = P.tr_red1;
+    dm.tr_red4 = P.tr_red4;
+    dm.tr_stage = P.tr_stage;
+    dm.tr_grad = P.tr_grad;
+    dm.tr_ctype = P.tr_ctype;
+    dm.tr_priv = P.tr_priv;
+    dm.nradial = M.nradial();
+    dm.ncoef = M.ncoef();
+    std::memcpy(dm.slot_base, P.slot_base, sizeof dm.slot_base);
+    dm.fwd_nsteps = P.fwd_level_step.back();
+    dm.bwd_nsteps = P.bwd_level_step.back();
+}
+
+int install_model(mtpx_context *ctx, Model &&m)
+{
+    std::string err;
+    if (!validate_model(m, err))
+        return set_error(ctx, MTPX_E_MODEL, err);
+    Plan p;
+    if (!build_plan(m, p, err))
+        return set_error(ctx, MTPX_E_MODEL, err);
+    // Sizes first, in a local view: a model whose work space does not fit a
+    // CU's LDS is refused before anything of the context changes.
+    DevModel dm{};
+    fill_model_sizes(m, p, dm);
+    EfsLaunch probe;
+    if (!efs_configure(dm, 1, 1, 0, ctx->lds_limit, probe))
+        return set_error(ctx, MTPX_E_CAPACITY, "model needs more LDS than a CU provides");
+    // From here on the old model is gone: until every upload has succeeded the
+    // context holds no model (a failed upload leaves MTPX_E_NO_MODEL behind,
+    // never tables of two models).
+    ctx->has_model = false;
+    ctx->has_lin = false;
+    ctx->has_batch_out = false;
+    ctx->has_adjoints = false;
+    ctx->model = std::move(m);
+    ctx->plan = std::move(p);
+    const Model &M = ctx->model;
+    const Plan &P = ctx->plan;
     hipStream_t s = ctx->stream;
     HIP_TRY(upload(ctx->map, M.map, s), "upload model");
     HIP_TRY(upload(ctx->slot_basic, P.slot_basic, s), "upload model");
@@ -95,33 +131,9 @@ int install_model(mtpx_context *ctx, Model &&m)
     dm.fwd_comb = ctx->fwd_comb.as<int4>();
     dm.bwd_level_comb = ctx->bwd_lcomb.as<int>();
     dm.bwd_comb = ctx->bwd_comb.as<int4>();
-    dm.max_partials = P.max_partials;
-    dm.K4 = P.K4;
-    dm.dummy = P.dummy;
-    dm.part0 = P.part0;
-    dm.red0 = P.red0;
-    dm.priv_doubles = P.priv_doubles;
-    dm.tr_delta = P.tr_delta;
-    dm.efs_red = P.efs_red;
-    dm.efs_stage = P.efs_stage;
-    dm.efs_acc = P.efs_acc;
-    dm.tr_red1 = P.tr_red1;
-    dm.tr_red4 = P.tr_red4;
-    dm.tr_stage = P.tr_stage;
-    dm.tr_grad = P.tr_grad;
-    dm.tr_ctype = P.tr_ctype;
-    dm.tr_priv = P.tr_priv;
-    dm.nradial = M.nradial();
-    dm.ncoef = M.ncoef();
-    std::memcpy(dm.slot_base, P.slot_base, sizeof dm.slot_base);
-    dm.fwd_nsteps = P.fwd_level_step.back();
-    dm.bwd_nsteps = P.bwd_level_step.back();
-    EfsLaunch probe;
-    if (!efs_configure(dm, 1, 1, 0, ctx->lds_limit, probe))
-        return set_error(ctx, MTPX_E_CAPACITY, "model needs more LDS than a CU provides");
     // linear-fit plan: optional (the linear entry points report its error)
-    ctx->has_lin = build_lin_plan(M, P, ctx->lin, ctx->lin_err);
-    if (ctx->has_lin) {
+    const bool lin_ok = build_lin_plan(M, P, ctx->lin, ctx->lin_err);
+    if (lin_ok) {
         const LinPlan &lp = ctx->lin;
         HIP_TRY(upload(ctx->lin_level, lp.level_step, s), "upload model");
         HIP_TRY(upload(ctx->lin_steps, lp.steps, s), "upload model");
@@ -170,9 +182,11 @@ int install_model(mtpx_context *ctx, Model &&m)
         }();
         L.compiled_walk = !runtime_walk && lin_walk_compiled(lp, P.nslots) ? 1 : 0;
     }
+    ctx->dm = dm;
     int rc = upload_coeffs(ctx);
     if (rc != MTPX_OK)
         return rc;
+    ctx->has_lin = lin_ok;
     ctx->has_model = true;
     return MTPX_OK;
 }

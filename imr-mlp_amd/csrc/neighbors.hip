@@ -452,6 +452,27 @@ __global__ __launch_bounds__(kScanBlock) void scan_tiles(const int *in, int64_t 
     }
 }
 
+// 64-bit sum of n non-negative ints into *total (zeroed by the caller): the
+// list-length total, checked against the int32 entry indices before any
+// offset is trusted.
+__global__ __launch_bounds__(256) void sum64_kernel(const int *in, int64_t n,
+                                                    unsigned long long *total)
+{
+    __shared__ unsigned long long buf[256];
+    unsigned long long s = 0;
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256)
+        s += (unsigned)in[i];
+    buf[threadIdx.x] = s;
+    __syncthreads();
+    for (int w = 128; w >= 1; w >>= 1) {
+        if ((int)threadIdx.x < w)
+            buf[threadIdx.x] += buf[threadIdx.x + w];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0)
+        atomicAdd(total, buf[0]);
+}
+
 // Exclusive scan; *total receives the sum (device), returns the error.
 hipError_t scan_exclusive(const int *in, int64_t n, int *out, DBuf &tmp, int *total,
                           hipStream_t s)
@@ -602,7 +623,7 @@ int build_neighbors_gpu(const double cell[9], const int pbc[3], int n, const dou
     DTRY(w.pos.ensure(sizeof(double) * 3 * n));
     DTRY(w.types.ensure(sizeof(int) * n));
     DTRY(w.minmax.ensure(sizeof(double) * 8));
-    DTRY(w.scalars.ensure(sizeof(int) * 8));
+    DTRY(w.scalars.ensure(sizeof(int) * 16));
     DTRY(hipMemcpyAsync(w.pos.p, pos, sizeof(double) * 3 * n, hipMemcpyHostToDevice, s));
     DTRY(hipMemcpyAsync(w.types.p, types, sizeof(int) * n, hipMemcpyHostToDevice, s));
     hipLaunchKernelGGL(gather_types_kernel, dim3(blocks(n, 256)), dim3(256), 0, s,
@@ -735,11 +756,20 @@ int build_neighbors_gpu(const double cell[9], const int pbc[3], int n, const dou
     // one wave per centre, four per workgroup
     hipLaunchKernelGGL(construct_kernel<0>, dim3((n + 3) / 4), dim3(256), 0, s, cs, cnt,
                        nullptr, nullptr, nullptr, nullptr, nullptr, nullptr);
+    // the entry total in 64 bits: offsets and entry indices are int32
+    unsigned long long *total64 = reinterpret_cast<unsigned long long *>(w.scalars.as<int>() + 8);
+    DTRY(hipMemsetAsync(total64, 0, sizeof *total64, s));
+    hipLaunchKernelGGL(sum64_kernel, dim3(std::min<unsigned>(blocks(n, 256), 1024)), dim3(256), 0,
+                       s, cnt, (int64_t)n, total64);
     DTRY(scan_exclusive(cnt, (int64_t)n + 1, out.offsets.as<int>(), w.tmp, w.scalars.as<int>(), s));
-    int Pi = 0;
-    DTRY(hipMemcpyAsync(&Pi, out.offsets.as<int>() + n, sizeof(int), hipMemcpyDeviceToHost, s));
+    unsigned long long P64 = 0;
+    DTRY(hipMemcpyAsync(&P64, total64, sizeof P64, hipMemcpyDeviceToHost, s));
     DTRY(hipStreamSynchronize(s));
-    const int64_t P = Pi;
+    if (P64 > (unsigned long long)INT32_MAX) {
+        err = "structure has more than 2^31 - 1 neighbour entries";
+        return MTPX_E_CAPACITY;
+    }
+    const int64_t P = (int64_t)P64;
     out.P = P;
     const size_t Pz = (size_t)std::max<int64_t>(P, 1);
     DTRY(out.idx.ensure(sizeof(int) * Pz));

@@ -37,6 +37,10 @@ def _cases():
     # dense: > 64 neighbours per atom exercises the multi-chunk neighbour loop
     dense = S.random_model("shapeev-16.mtp", 3, 8, 1.5, 7.5, -0.05, 0.05, S.rng_for(300))
     out.append(("lvl16-dense-liquid", dense, liq))
+    # duplicate scalar mapping {0, 4, 5, 6, 4} and rules with l == r
+    # (runtime/mtp/cpu/tests/test_mtp_cpu.cpp:30-33)
+    dup = S.random_model("dup-scalar.mtp", 2, 6, 1.8, 4.6, -0.5, 0.5, S.rng_for(700))
+    out.append(("dup-scalar-map", dup, s))
     return out
 
 
@@ -55,7 +59,7 @@ def test_efs_matches_oracle(ctx, name, model_text, s):
 
 
 def test_dense_case_has_long_lists():
-    name, model_text, s = CASES[-1]
+    name, model_text, s = CASES[-2]
     ref = oracle_case(model_text, s)
     counts = np.diff(ref["nb"].offsets)
     assert counts.max() > 64
@@ -180,3 +184,34 @@ def test_energy_only_per_structure(ctx):
         Eo, seo = O.energy(m, nb)
         assert rel_err(E[c], Eo) < 1e-10
         assert rel_err(se[off[c]:off[c + 1]], seo) < 1e-10
+
+
+def _oversized_model(K=12001):
+    """One basic moment and K-1 product rules m_k = m_0 m_0: a per-wave work
+    space far beyond a CU's 160 KB of LDS."""
+    times = ", ".join("{0, 0, 1, %d}" % k for k in range(1, K))
+    return ("MTP\nversion = 1.1.0\npotential_name = MTP1m\nscaling = 0.01\nspecies_count = 1\n"
+            "potential_tag = \nradial_basis_type = RBChebyshev\n\tmin_dist = 2\n\tmax_dist = 5\n"
+            "\tradial_basis_size = 8\n\tradial_funcs_count = 1\n"
+            "alpha_moments_count = %d\nalpha_index_basic_count = 1\n"
+            "alpha_index_basic = {{0, 0, 0, 0}}\nalpha_index_times_count = %d\n"
+            "alpha_index_times = {%s}\nalpha_scalar_moments = 1\nalpha_moment_mapping = {%d}\n"
+            % (K, K - 1, times, K - 1))
+
+
+def test_failed_model_load_leaves_previous_model(ctx):
+    """A model refused for capacity changes nothing: the loaded model, its
+    tables and results stay as they were (no half-installed model)."""
+    from mtpx import capi
+    model_text, s = S.scaled_inference(2, (3, 3, 3))
+    ref = oracle_case(model_text, s)
+    ctx.load_model_text(model_text)
+    upload_oracle_lists(ctx, ref["nb"])
+    before = ctx.efs()
+    with pytest.raises(capi.MtpxError) as e:
+        ctx.load_model_text(_oversized_model())
+    assert e.value.code == -7  # MTPX_E_CAPACITY
+    after = ctx.efs()
+    for x, y in zip(before, after):
+        assert np.allclose(x, y, rtol=1e-13, atol=0)
+    assert_efs_close(after, ref, TOL)

@@ -198,3 +198,31 @@ def test_empty_batch_linear_system(ctx):
     ctx.set_labels(np.zeros((0, 3), np.int32))
     G, b = ctx.linear_system()
     assert not G.any() and not b.any()
+
+
+def test_orthogonalize_known_answer(ctx):
+    """mtpx_orthogonalize on the hand-worked three-channel case (see
+    test_oracle_math.ORTHO_MTP): the reference's projection by the norm of
+    the channel being projected, not textbook Gram-Schmidt."""
+    from test_oracle_math import ORTHO_EXPECTED, ORTHO_MTP
+    ctx.load_model_text(ORTHO_MTP)
+    ctx.orthogonalize()
+    got = ctx.get_coeffs()[:6].reshape(3, 2)
+    assert np.abs(got - ORTHO_EXPECTED).max() < 1e-9
+
+
+def test_duplicate_scalar_mapping_rows(ctx):
+    """Duplicate mapping entries give identical design columns."""
+    text = S.random_model("dup-scalar.mtp", 2, 6, 1.8, 4.6, -0.5, 0.5, S.rng_for(700))
+    m = O.Model(text)
+    rng = S.rng_for(704)
+    s = S.displace(S.strain(S.lattice("bcc", (2, 2, 3), 2.87), rng, 0.03), rng, 0.15)
+    s.types = (S.uniform(rng, s.n) * 2).astype(np.int32)
+    s.pos = O.wrap(s.cell, s.pbc, s.pos)
+    nb = O.Neighbors.build(s.cell, s.pbc, s.pos, s.types, m.cutoff)
+    ctx.load_model_text(text)
+    ctx.set_structures([s], m.cutoff)
+    ec, fc, sc = ctx.efs_components()
+    eo, fo, so = O.efs_components(m, nb)
+    assert rel_err(ec[0], eo) < 1e-10 and rel_err(fc, fo) < 1e-10 and rel_err(sc[0], so) < 1e-10
+    assert np.array_equal(fc[..., m.Z + 1], fc[..., m.Z + 4])

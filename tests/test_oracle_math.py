@@ -296,3 +296,235 @@ def test_orthogonalize_normalises_first_channel():
     for k in range(M):
         assert abs(np.sum(out[:, k, :] ** 2) - 1) < 1e-6
     assert np.array_equal(m.coeffs[m.nradial:], c[m.nradial:])
+
+
+# A three-function, two-term radial basis whose Orthogonalize result was
+# worked out by hand.  Channels c0 = (3, 4), c1 = (2, 0), c2 = (0, 5) (one
+# species pair).  potential_mtp.cpp:3849-3930 projects channel k on an
+# earlier channel k2 with scal / |c_k|^2 -- the squared norm of the channel
+# being projected, recomputed before each projection -- not |c_k2|^2:
+#   c0 -> (3, 4) / 5                                     = (0.6, 0.8)
+#   c1: |c1|^2 = 4, scal = 2 * 0.6 = 1.2, c1 -= 0.3 c0    = (1.82, -0.24)
+#       |c1|^2 = 3.37                                    -> c1 / sqrt(3.37)
+#   c2: |c2|^2 = 25, scal = 5 * 0.8 = 4, c2 -= 0.16 c0    = (-0.096, 4.872)
+#       |c2|^2 = 23.7456, scal = c2 . c1 = -1.344 / sqrt(3.37),
+#       c2 -= c1 scal / 23.7456 = c2 - (1.82, -0.24) (-1.344) / (3.37 * 23.7456)
+#          = (-0.0654326627833672, 4.86796914234506), |c2|^2 = 23.7014050041826
+# The 1e-10 added per term to the final norms moves these by ~1e-10.
+# Textbook Gram-Schmidt (divide by |c_k2|^2 = 1) gives c1 = (0.8, -0.6) and
+# c2 = (0, 0) instead.
+ORTHO_MTP = """MTP
+version = 1.1.0
+potential_name = MTP1m
+scaling = 1.0
+species_count = 1
+potential_tag = 
+radial_basis_type = RBChebyshev
+\tmin_dist = 2.0
+\tmax_dist = 5.0
+\tradial_basis_size = 2
+\tradial_funcs_count = 3
+\tradial_coeffs
+\t\t0-0
+\t\t\t{3, 4}
+\t\t\t{2, 0}
+\t\t\t{0, 5}
+alpha_moments_count = 3
+alpha_index_basic_count = 3
+alpha_index_basic = {{0, 0, 0, 0}, {1, 0, 0, 0}, {2, 0, 0, 0}}
+alpha_index_times_count = 0
+alpha_index_times = {}
+alpha_scalar_moments = 3
+alpha_moment_mapping = {0, 1, 2}
+species_coeffs = {0.5}
+moment_coeffs = {1, 2, 3}
+"""
+ORTHO_EXPECTED = np.array([[0.6, 0.8],
+                           [0.9914171734791749, -0.1307363305686824],
+                           [-0.013440256236068761, 0.9999096756769127]])
+ORTHO_TEXTBOOK = np.array([[0.6, 0.8], [0.8, -0.6], [0.0, 0.0]])
+
+
+def _textbook_gram_schmidt(c):
+    """Classical Gram-Schmidt with unit-norm earlier channels (the planted
+    alternative the known answer must reject)."""
+    out = []
+    for v in c:
+        v = v.astype(float).copy()
+        for u in out:
+            v -= u * (v @ u) / (u @ u) if (u @ u) > 0 else 0.0
+        nv = np.sqrt(v @ v + 1e-10 * v.size)
+        out.append(v / nv)
+    return np.array(out)
+
+
+def test_orthogonalize_known_answer():
+    m = O.Model(ORTHO_MTP)
+    assert (m.Z, m.M, m.R) == (1, 3, 2)
+    m.orthogonalize()
+    got = m.coeffs[: m.nradial].reshape(3, 2)
+    assert np.abs(got - ORTHO_EXPECTED).max() < 1e-9
+    # the known answer rejects textbook Gram-Schmidt
+    tb = _textbook_gram_schmidt(np.array([[3, 4], [2, 0], [0, 5]]))
+    assert np.abs(tb - ORTHO_TEXTBOOK).max() < 1e-6
+    assert np.abs(tb - ORTHO_EXPECTED).max() > 0.1
+
+
+def test_orthogonalize_first_projection_closed_form():
+    """After one projection c1' = c1 - c0 (c1.c0) / |c1|^2 with |c0| = 1, so
+    c1'.c0 = s (1 - 1 / |c1|^2) with s = c1.c0: nonzero unless |c1| = 1
+    (textbook Gram-Schmidt leaves 0)."""
+    rng = S.rng_for(31)
+    for trial in range(5):
+        M, R = 2, 4
+        v0 = rng.random(R) - 0.5
+        v1 = 2.0 * (rng.random(R) - 0.5)
+        text = ORTHO_MTP.replace("\tradial_basis_size = 2", "\tradial_basis_size = 4")
+        text = text.replace("\tradial_funcs_count = 3", "\tradial_funcs_count = 2")
+        body = "\t\t\t{%s}\n\t\t\t{%s}\n" % (", ".join(repr(float(x)) for x in v0),
+                                                  ", ".join(repr(float(x)) for x in v1))
+        start = text.index("\t\t\t{3, 4}")
+        end = text.index("alpha_moments_count")
+        text = text[:start] + body + text[end:]
+        text = text.replace("{{0, 0, 0, 0}, {1, 0, 0, 0}, {2, 0, 0, 0}}",
+                            "{{0, 0, 0, 0}, {1, 0, 0, 0}, {1, 0, 0, 0}}")
+        m = O.Model(text)
+        assert (m.M, m.R) == (M, R)
+        m.orthogonalize()
+        out = m.coeffs[: m.nradial].reshape(M, R)
+        c0 = v0 / np.sqrt(v0 @ v0 + 1e-10 * R)
+        sc = v1 @ c0
+        v1p = v1 - c0 * sc / (v1 @ v1)
+        assert abs(v1p @ c0 - sc * (1 - (c0 @ c0) / (v1 @ v1))) < 1e-13
+        assert np.abs(out[1] - v1p / np.sqrt(v1p @ v1p + 1e-10 * R)).max() < 1e-12
+        assert abs(out[1] @ out[0]) > 1e-3 * abs(sc)
+
+
+# --------------------------------------------------- loss weight factors --
+
+def _loss_parts(m, nb, lab, **kw):
+    st = O.LossSettings.make(**kw)
+    loss, g, met = O.add_loss_grad(m, nb, st, lab)
+    return loss, met
+
+
+def test_force_normalisation_scales_every_term():
+    """fit:force_wgt_d/f/p (train_mtp.cpp:3868-3880): with the label forces
+    scaled so that mean_i |F*_i|^2 = 4, d = 0.1, f = 0.025, p = 2 the factor is
+    0.1 / (0.1 + (0.025 * 4)^2) = 10/11, and it multiplies the energy, force
+    and stress terms alike (never the predicted forces' norm)."""
+    m, nb, lab = _config()
+    F = lab.forces
+    lab.forces = F * np.sqrt(4.0 / np.mean(np.sum(F * F, axis=1)))
+    assert abs(np.mean(np.sum(lab.forces ** 2, axis=1)) - 4.0) < 1e-12
+    for w in [(1.0, 0.0, 0.0), (0.0, 0.05, 0.0), (0.0, 0.0, 0.1), (1.0, 0.01, 1e-3)]:
+        kw = dict(weight_eng=w[0], weight_force=w[1], weight_stress=w[2], force_norm_d=0.1,
+                  force_norm_p=2.0)
+        base, mb = _loss_parts(m, nb, lab, force_norm_f=0.0, **kw)
+        norm, mn = _loss_parts(m, nb, lab, force_norm_f=0.025, **kw)
+        assert abs(norm - base * 10.0 / 11.0) < 1e-13 * abs(base), w
+        # metrics: [loss_e, loss_f, loss_s] scale, the squared errors do not
+        assert np.allclose(mn[0:3], mb[0:3] * 10.0 / 11.0, rtol=1e-13, atol=0)
+        assert np.array_equal(mn[3:6], mb[3:6])
+    # the factor depends on the labels only: the same predicted forces with a
+    # label set of half the norm give d / (d + (f * 1)^2) = 0.1 / 0.100625
+    lab.forces = lab.forces * 0.5
+    kw = dict(weight_eng=1.0, weight_force=0.0, weight_stress=0.0, force_norm_d=0.1,
+              force_norm_p=2.0)
+    base, _ = _loss_parts(m, nb, lab, force_norm_f=0.0, **kw)
+    norm, _ = _loss_parts(m, nb, lab, force_norm_f=0.025, **kw)
+    assert abs(norm - base * 0.1 / 0.100625) < 1e-13 * abs(base)
+
+
+def test_fitness_scales_energy_only_and_atomic_fitness_forces_per_atom():
+    """Atoms::fitness multiplies the energy weight only (train_mtp.cpp:2552-2556);
+    atomic_fitness_i multiplies the force weight of atom i only (:3888-3893)."""
+    m, nb, lab = _config()
+    n = lab.n
+    E, F, St, _ = O.efs(m, nb)
+    for w in [(1.0, 0.0, 0.0), (0.0, 0.05, 0.0), (0.0, 0.0, 0.1)]:
+        kw = dict(weight_eng=w[0], weight_force=w[1], weight_stress=w[2])
+        base, _ = _loss_parts(m, nb, lab, **kw)
+        lab.fitness = 3.0
+        fit, _ = _loss_parts(m, nb, lab, **kw)
+        lab.fitness = 1.0
+        assert abs(fit - (3.0 if w[0] > 0 else 1.0) * base) < 1e-13 * abs(base), w
+    # atomic fitness: an indicator of atom k leaves W_F |F_k - F*_k|^2
+    kw = dict(weight_eng=0.0, weight_force=0.05, weight_stress=0.0)
+    total = _loss_parts(m, nb, lab, **kw)[0]
+    parts = []
+    for k in [0, 3, n - 1]:
+        a = np.zeros(n)
+        a[k] = 1.0
+        lab.atomic_fitness = a
+        parts.append(_loss_parts(m, nb, lab, **kw)[0])
+        assert abs(parts[-1] - 0.05 * np.sum((F[k] - lab.forces[k]) ** 2)) < 1e-15 + 1e-13 * parts[-1]
+    lab.atomic_fitness = np.full(n, 2.5)
+    assert abs(_loss_parts(m, nb, lab, **kw)[0] - 2.5 * total) < 1e-13 * total
+    # energy and stress terms ignore atomic fitness
+    kw = dict(weight_eng=1.0, weight_force=0.0, weight_stress=0.1)
+    with_af = _loss_parts(m, nb, lab, **kw)[0]
+    lab.atomic_fitness = None
+    assert abs(with_af - _loss_parts(m, nb, lab, **kw)[0]) < 1e-13 * abs(with_af)
+
+
+def test_energy_and_stress_powers():
+    """W_X = w_X / N^p_X with the configured powers (train_mtp.cpp:2552-2568)."""
+    m, nb, lab = _config()
+    n = lab.n
+    for key, pw in [("eng_pow", 0.0), ("eng_pow", 2.0), ("stress_pow", 0.5), ("force_pow", 1.5)]:
+        kw = dict(weight_eng=1.0 if key == "eng_pow" else 0.0,
+                  weight_force=0.05 if key == "force_pow" else 0.0,
+                  weight_stress=0.1 if key == "stress_pow" else 0.0)
+        default = {"eng_pow": 1.0, "stress_pow": 1.0, "force_pow": 0.0}[key]
+        base, _ = _loss_parts(m, nb, lab, **kw)
+        kw[key] = pw
+        got, _ = _loss_parts(m, nb, lab, **kw)
+        assert abs(got - base * n ** (default - pw)) < 1e-12 * abs(got), key
+
+
+# --------------------------------------------- duplicate scalar mapping --
+
+def _dup_case():
+    text = S.random_model("dup-scalar.mtp", 2, 6, 1.8, 4.6, -0.5, 0.5, S.rng_for(700))
+    rng = S.rng_for(701)
+    s = S.displace(S.strain(S.lattice("bcc", (2, 2, 3), 2.87), rng, 0.03), rng, 0.15)
+    s.types = (S.uniform(rng, s.n) * 2).astype(np.int32)
+    return text, s
+
+
+def test_duplicate_scalar_mapping_accumulates():
+    """alpha_moment_mapping {0, 4, 5, 6, 4} (the moment graph of
+    runtime/mtp/cpu/tests/test_mtp_cpu.cpp:30-33, with rules whose two
+    operands are the same moment): the energy counts moment 4 with
+    xi_1 + xi_4, and so must the adjoint seed (potential_mtp.cpp:2976, +=).
+    Forces are minus the energy gradient."""
+    text, s = _dup_case()
+    m = O.Model(text)
+    assert list(m.tables()[2]) == [0, 4, 5, 6, 4]
+    E, F, St, se = _efs_of(m, s)
+    # energy: replacing the duplicate by a single entry with the summed
+    # coefficient leaves every output unchanged
+    x = m.coeffs.copy()
+    base = m.nradial + m.Z
+    single = text.replace("alpha_scalar_moments = 5", "alpha_scalar_moments = 4")
+    single = single.replace("alpha_moment_mapping = {0, 4, 5, 6, 4}",
+                            "alpha_moment_mapping = {0, 4, 5, 6}")
+    mc = x[base:]
+    lines = single.splitlines()
+    for i, l in enumerate(lines):
+        if l.startswith("moment_coeffs"):
+            merged = [mc[0], mc[1] + mc[4], mc[2], mc[3]]
+            lines[i] = "moment_coeffs = {%s}" % ", ".join(repr(float(v)) for v in merged)
+    m1 = O.Model("\n".join(lines) + "\n")
+    E1, F1, S1, se1 = _efs_of(m1, s)
+    assert rel_err(E, E1) < 1e-13 and rel_err(F, F1) < 1e-12 and rel_err(St, S1) < 1e-12
+    h = 1e-5
+    for i in range(0, s.n, 5):
+        for a in range(3):
+            p1 = s.pos.copy()
+            p1[i, a] += h
+            p2 = s.pos.copy()
+            p2[i, a] -= h
+            fd = -(_efs_of(m, s, p1)[0] - _efs_of(m, s, p2)[0]) / (2 * h)
+            assert abs(F[i, a] - fd) < 1e-7 * max(1.0, np.abs(F).max())

@@ -104,6 +104,27 @@ def test_oracle_efs_matches_reference_binary(workdir):
         assert rel_err(se, ser) < 1e-12
 
 
+@needs_ref
+def test_duplicate_mapping_energy_matches_reference_binary(workdir):
+    """The duplicate-mapping model (alpha_moment_mapping {0, 4, 5, 6, 4}):
+    energies and site energies agree with the reference core to 1e-12.
+    Forces are not compared with it: runtime/mtp/mlip.cpp:1101 assigns the
+    adjoint seed of a scalar's moment (=) where PotMTP adds it
+    (potential_mtp.cpp:2976, +=), so that core's forces for this model are
+    not minus its own energy gradient; the oracle's are
+    (test_oracle_math.test_duplicate_scalar_mapping_accumulates)."""
+    from test_oracle_math import _dup_case
+    text, s = _dup_case()
+    m = O.Model(text)
+    pos = O.wrap(s.cell, s.pbc, s.pos)
+    nb = O.Neighbors.build(s.cell, s.pbc, pos, s.types, m.cutoff)
+    E, F, St, se = O.efs(m, nb)
+    Er, ser, Fr, vr = O.ref_mlip_efs(text, nb, s.types, m.cutoff, workdir, m.Z)
+    assert rel_err(E, Er) < 1e-12 and rel_err(se, ser) < 1e-12
+    # the reference core's forces miss the first duplicate's coefficient
+    assert rel_err(F, Fr) > 1e-6
+
+
 def test_level10_template_inventory():
     """sources.json records shapeev/10 as 41 moments, 25 basic, 42 products,
     16 scalars; the carved template must reproduce it."""

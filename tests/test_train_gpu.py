@@ -231,3 +231,35 @@ def test_empty_batch_and_empty_structure(ctx):
     E, F, St, _ = ctx.compute_batch()
     assert E[1] == 0.0 and not St[1].any()
     assert E[0] == pytest.approx(E[2], rel=1e-14)
+
+
+def test_loss_grad_duplicate_scalar_mapping(ctx):
+    """A repeated alpha_moment_mapping entry: both scalars count in the
+    energy and in the adjoint seed, and each gets its own gradient entry."""
+    text = S.random_model("dup-scalar.mtp", 2, 6, 1.8, 4.6, -0.5, 0.5, S.rng_for(700))
+    ref = S.random_model("dup-scalar.mtp", 2, 6, 1.8, 4.6, -0.5, 0.5, S.rng_for(702))
+    m, mref = O.Model(text), O.Model(ref)
+    rng = S.rng_for(703)
+    structs, nbs, labels = [], [], []
+    for k in range(4):
+        s = S.displace(S.strain(S.lattice("bcc", (2, 2, 2 + k % 2), 2.87), rng, 0.03), rng, 0.15)
+        s.types = (S.uniform(rng, s.n) * 2).astype(np.int32)
+        s.pos = O.wrap(s.cell, s.pbc, s.pos)
+        nb = O.Neighbors.build(s.cell, s.pbc, s.pos, s.types, mref.cutoff)
+        E, F, St, _ = O.efs(mref, nb)
+        e, f, st = S.noisy_labels(rng, s.n, E, F, St)
+        structs.append(s)
+        nbs.append(nb)
+        labels.append(O.Labels(s.n, energy=e, forces=f, stress=st))
+    st = SETTINGS["default"]
+    _upload(ctx, text, mref.cutoff, structs, labels, st)
+    f_o, g_o = O.loss_grad_batch(m, nbs, labels, st, penalty_weight=1e-3, reg_l2=1e-4, threads=4)
+    f, g, _ = ctx.loss_grad(penalty_weight=1e-3, reg_l2=1e-4)
+    assert rel_err(f, f_o) < 1e-9
+    assert rel_err(g, g_o) < 1e-9
+    # the two scalars mapped to moment 4 see the same moment: equal energy
+    # derivatives (dL/dE m_4 + q_4) up to the L2 term of their own coefficient
+    base = m.nradial + m.Z
+    x = m.coeffs
+    assert abs((g[base + 1] - 2e-4 * x[base + 1]) - (g[base + 4] - 2e-4 * x[base + 4])) \
+        < 1e-12 * np.abs(g).max()
