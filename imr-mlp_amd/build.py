@@ -37,6 +37,7 @@ SOURCES = [
     ("capi.cpp", ["-ffp-contract=off"]),
     ("train_api.cpp", ["-ffp-contract=off"]),
     ("linear_api.cpp", ["-ffp-contract=off"]),
+    ("sites.cpp", ["-ffp-contract=off"]),
 ]
 
 

@@ -208,6 +208,7 @@ DevNeighbors dev_neighbors(const mtpx_context *ctx)
     nb.z = ctx->z.as<double>();
     nb.d = ctx->d.as<double>();
     nb.center_type = ctx->center_type.as<int>();
+    nb.center = nullptr;
     return nb;
 }
 
@@ -257,6 +258,22 @@ int set_single_structure(mtpx_context *ctx)
                            ctx->stream),
             "clear structure index");
     HIP_TRY(hipStreamSynchronize(ctx->stream), "upload structure offsets");
+    return MTPX_OK;
+}
+
+int copy_out(mtpx_context *ctx, double *dst, const void *src, size_t count, bool add,
+             const char *what)
+{
+    if (!count)
+        return MTPX_OK;
+    if (!add) {
+        HIP_TRY(hipMemcpy(dst, src, sizeof(double) * count, hipMemcpyDeviceToHost), what);
+        return MTPX_OK;
+    }
+    std::vector<double> tmp(count);
+    HIP_TRY(hipMemcpy(tmp.data(), src, sizeof(double) * count, hipMemcpyDeviceToHost), what);
+    for (size_t k = 0; k < count; ++k)
+        dst[k] += tmp[k];
     return MTPX_OK;
 }
 
@@ -311,6 +328,7 @@ int run_efs(mtpx_context *ctx, bool deterministic, bool site_virial, bool energy
     out.partial = ctx->partial.as<double>();
     out.pair_ders = deterministic ? ctx->pair_ders.as<double>() : nullptr;
     out.site_virial = nullptr;
+    out.site_virial6 = nullptr;
     if (site_virial) {
         HIP_TRY(ctx->site_virial.ensure(sizeof(double) * 9 * std::max(n, 1)),
                 "allocate site virials");
@@ -660,20 +678,29 @@ int mtpx_efs(mtpx_context *ctx, int deterministic, double *energy, double *force
     int rc = run_efs(ctx, deterministic != 0);
     if (rc != MTPX_OK)
         return rc;
+    const bool add = ctx->add_efs;
     double o10[10];
     HIP_TRY(hipMemcpy(o10, ctx->out10.p, sizeof o10, hipMemcpyDeviceToHost), "copy outputs");
     if (energy)
-        *energy = o10[0];
+        *energy = add ? *energy + o10[0] : o10[0];
     if (stress)
-        std::memcpy(stress, o10 + 1, 9 * sizeof(double));
-    if (forces && ctx->n > 0)
-        HIP_TRY(hipMemcpy(forces, ctx->forces.p, sizeof(double) * 3 * ctx->n,
-                          hipMemcpyDeviceToHost),
-                "copy forces");
-    if (site_energies && ctx->n > 0)
-        HIP_TRY(hipMemcpy(site_energies, ctx->site_energy.p, sizeof(double) * ctx->n,
-                          hipMemcpyDeviceToHost),
-                "copy site energies");
+        for (int k = 0; k < 9; ++k)
+            stress[k] = add ? stress[k] + o10[1 + k] : o10[1 + k];
+    if (forces)
+        if (int rc2 = copy_out(ctx, forces, ctx->forces.p, 3 * (size_t)ctx->n, add, "copy forces"))
+            return rc2;
+    if (site_energies)
+        if (int rc2 = copy_out(ctx, site_energies, ctx->site_energy.p, (size_t)ctx->n, add,
+                               "copy site energies"))
+            return rc2;
+    return MTPX_OK;
+}
+
+int mtpx_set_add_efs(mtpx_context *ctx, int add_efs)
+{
+    if (!ctx)
+        return MTPX_E_INVALID;
+    ctx->add_efs = add_efs != 0;
     return MTPX_OK;
 }
 

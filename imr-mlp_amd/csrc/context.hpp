@@ -76,6 +76,30 @@ struct mtpx_context {
     hipEvent_t ev[3] = {nullptr, nullptr, nullptr};
     double timings[4] = {0, 0, 0, 0};
 
+    // PotMTP::add_efs: E/F/S outputs are added onto the caller's arrays
+    bool add_efs = false;
+
+    // CSR site requests (mtpx_compute_sites): their own topology, kept for
+    // reuse_topology; independent of the resident lists above
+    struct Sites {
+        bool valid = false;
+        int center_count = 0, nlocal = 0, ntotal = 0, rows = 0;
+        int64_t P_in = 0;            // entries of the request (before dropped centres)
+        std::vector<int> row_atom;   // atom of each kept centre row
+        std::vector<int> row_src;    // request centre index of each kept row
+        NeighborStore nb;            // offsets, idx, type, x, y, z, d, center_type
+        DBuf center_atom, atom_type, pos, vec, atom_row, rev_offsets, rev_pairs, forces,
+            site_virial6, site_energy, partial, out10, pair_ders;
+        void release()
+        {
+            for (DBuf *b : {&nb.offsets, &nb.idx, &nb.type, &nb.x, &nb.y, &nb.z, &nb.d,
+                            &nb.center_type, &center_atom, &atom_type, &pos, &vec, &atom_row,
+                            &rev_offsets, &rev_pairs, &forces, &site_virial6, &site_energy,
+                            &partial, &out10, &pair_ders})
+                b->release();
+        }
+    } sites;
+
     ~mtpx_context()
     {
         for (DBuf *b : {&radial, &species, &moment, &map, &seed, &slot_basic, &slot_abc, &dup,
@@ -93,6 +117,7 @@ struct mtpx_context {
                         &lin_fcomb})
             b->release();
         scratch.release_all();
+        sites.release();
         for (auto &e : ev)
             if (e)
                 (void)hipEventDestroy(e);
@@ -135,6 +160,11 @@ hipError_t upload(DBuf &b, const std::vector<T> &v, hipStream_t s)
         return e;
     return hipMemcpyAsync(b.p, v.data(), sizeof(T) * v.size(), hipMemcpyHostToDevice, s);
 }
+
+// Copies `count` doubles from the device to dst; with add, adds them onto
+// what dst holds (PotMTP::add_efs, the reference's accumulate_force).
+int copy_out(mtpx_context *ctx, double *dst, const void *src, size_t count, bool add,
+             const char *what);
 
 // Runs the E/F/S kernel over the resident topology (capi.cpp); with
 // site_virial the per-atom virials are written too; energy_only skips the

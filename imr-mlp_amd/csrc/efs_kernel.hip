@@ -71,6 +71,7 @@ __global__ __launch_bounds__(kWave *kMaxWaves) void efs_kernel(DevModel m, DevNe
     const int row = blockIdx.x * nwaves + wave;
     for (int i = row; i < nb.n; i += gridDim.x * nwaves) {
         const int ti = nb.center_type[i];
+        const int ai = nb.center ? nb.center[i] : i;  // the centre's atom
         const int beg = nb.offsets[i];
         const int n = nb.offsets[i + 1] - beg;
         for (int k = lane; k < m.K; k += kWave)
@@ -159,6 +160,16 @@ __global__ __launch_bounds__(kWave *kMaxWaves) void efs_kernel(DevModel m, DevNe
                     atomicAdd(&out.forces[3 * j + 0], -D0);
                     atomicAdd(&out.forces[3 * j + 1], -D1);
                     atomicAdd(&out.forces[3 * j + 2], -D2);
+                    if (out.site_virial6) {
+                        // the neighbour's half (runtime/mtp/mlip.cpp:1181-1189)
+                        double *v = out.site_virial6 + 6 * (size_t)j;
+                        atomicAdd(v + 0, -0.5 * D0 * q.x);
+                        atomicAdd(v + 1, -0.5 * D1 * q.y);
+                        atomicAdd(v + 2, -0.5 * D2 * q.z);
+                        atomicAdd(v + 3, -0.25 * (D1 * q.x + D0 * q.y));
+                        atomicAdd(v + 4, -0.25 * (D2 * q.x + D0 * q.z));
+                        atomicAdd(v + 5, -0.25 * (D2 * q.y + D1 * q.z));
+                    }
                 }
             }
         }
@@ -167,9 +178,9 @@ __global__ __launch_bounds__(kWave *kMaxWaves) void efs_kernel(DevModel m, DevNe
             fi1 = wave_sum(fi1);
             fi2 = wave_sum(fi2);
             if (lane == 0) {
-                atomicAdd(&out.forces[3 * i + 0], fi0);
-                atomicAdd(&out.forces[3 * i + 1], fi1);
-                atomicAdd(&out.forces[3 * i + 2], fi2);
+                atomicAdd(&out.forces[3 * ai + 0], fi0);
+                atomicAdd(&out.forces[3 * ai + 1], fi1);
+                atomicAdd(&out.forces[3 * ai + 2], fi2);
             }
         }
         // this atom's virial: summed over the lanes, added to the wave's sums
@@ -184,6 +195,16 @@ __global__ __launch_bounds__(kWave *kMaxWaves) void efs_kernel(DevModel m, DevNe
 #pragma unroll
                 for (int k = 0; k < 9; ++k)
                     out.site_virial[9 * (size_t)i + k] = vs[k];
+            if (out.site_virial6 && !deterministic) {
+                // the centre's half of its entries (mlip.cpp:1164-1180)
+                double *v = out.site_virial6 + 6 * (size_t)ai;
+                atomicAdd(v + 0, 0.5 * vs[0]);
+                atomicAdd(v + 1, 0.5 * vs[4]);
+                atomicAdd(v + 2, 0.5 * vs[8]);
+                atomicAdd(v + 3, 0.25 * (vs[3] + vs[1]));
+                atomicAdd(v + 4, 0.25 * (vs[6] + vs[2]));
+                atomicAdd(v + 5, 0.25 * (vs[7] + vs[5]));
+            }
         }
         wave_sync();
     }
@@ -243,6 +264,63 @@ __global__ __launch_bounds__(256) void force_gather_kernel(DevNeighbors nb, cons
     forces[3 * k] = f0;
     forces[3 * k + 1] = f1;
     forces[3 * k + 2] = f2;
+}
+
+// -1/2 D r^T, symmetrised off the diagonal, as (xx, yy, zz, xy, xz, yz): one
+// endpoint's share of an entry in the LAMMPS per-atom virial
+// (runtime/mtp/mlip.cpp:1164-1190).
+__device__ __forceinline__ void half_virial(const double *D, double rx, double ry, double rz,
+                                            double v[6])
+{
+    v[0] += -0.5 * D[0] * rx;
+    v[1] += -0.5 * D[1] * ry;
+    v[2] += -0.5 * D[2] * rz;
+    v[3] += -0.25 * (D[1] * rx + D[0] * ry);
+    v[4] += -0.25 * (D[2] * rx + D[0] * rz);
+    v[5] += -0.25 * (D[2] * ry + D[1] * rz);
+}
+
+// Deterministic assembly of a site request over every atom k (owned and
+// ghost): F_k = sum over k's own entries (when k is a centre) of D minus the
+// sum over the entries whose neighbour is k, both in ascending entry order;
+// the per-atom virial takes half of each of those entries.
+__global__ __launch_bounds__(256) void site_gather_kernel(DevNeighbors nb, int ntotal,
+                                                          const int *atom_row, const double *D,
+                                                          const int *rev_offsets,
+                                                          const int *rev_pairs, double *forces,
+                                                          double *site_virial6)
+{
+    const int k = blockIdx.x * blockDim.x + threadIdx.x;
+    if (k >= ntotal)
+        return;
+    double f[3] = {0, 0, 0}, v[6] = {0, 0, 0, 0, 0, 0};
+    const int row = atom_row[k];
+    if (row >= 0)
+        for (int p = nb.offsets[row]; p < nb.offsets[row + 1]; ++p) {
+            const double *Dp = D + 3 * (int64_t)p;
+            f[0] += Dp[0];
+            f[1] += Dp[1];
+            f[2] += Dp[2];
+            if (site_virial6)
+                half_virial(Dp, nb.x[p], nb.y[p], nb.z[p], v);
+        }
+    for (int q = rev_offsets[k]; q < rev_offsets[k + 1]; ++q) {
+        const int64_t p = rev_pairs[q];
+        const double *Dp = D + 3 * p;
+        f[0] -= Dp[0];
+        f[1] -= Dp[1];
+        f[2] -= Dp[2];
+        if (site_virial6)
+            half_virial(Dp, nb.x[p], nb.y[p], nb.z[p], v);
+    }
+    if (forces) {
+        forces[3 * (int64_t)k] = f[0];
+        forces[3 * (int64_t)k + 1] = f[1];
+        forces[3 * (int64_t)k + 2] = f[2];
+    }
+    if (site_virial6)
+        for (int c = 0; c < 6; ++c)
+            site_virial6[6 * (int64_t)k + c] = v[c];
 }
 
 // Kernel variants: shell profile x table placement.  The profiles whose
@@ -320,6 +398,18 @@ hipError_t launch_efs(const DevModel &m, const DevNeighbors &nb, const EfsOut &o
     case 3: launch_variant<ProfSmall>(m, nb, out, cfg, det, s); break;
     default: launch_variant<ProfGeneric>(m, nb, out, cfg, det, s); break;
     }
+    return hipGetLastError();
+}
+
+hipError_t launch_site_gather(const DevNeighbors &nb, int ntotal, const int *atom_row,
+                              const double *pair_ders, const int *rev_offsets,
+                              const int *rev_pairs, double *forces, double *site_virial6,
+                              hipStream_t s)
+{
+    if (ntotal > 0)
+        hipLaunchKernelGGL(site_gather_kernel, dim3((ntotal + 255) / 256), dim3(256), 0, s, nb,
+                           ntotal, atom_row, pair_ders, rev_offsets, rev_pairs, forces,
+                           site_virial6);
     return hipGetLastError();
 }
 

@@ -211,6 +211,7 @@ struct DevNeighbors {
     const int *type;        // [P]
     const double *x, *y, *z, *d;  // [P]
     const int *center_type; // [n]
+    const int *center;      // [n] atom of each centre row; nullptr: row i is atom i
 };
 
 struct EfsOut {
@@ -219,6 +220,8 @@ struct EfsOut {
     double *partial;        // [rows][10] per wave: energy, stress[9]
     double *pair_ders;      // [P][3] (deterministic mode) or nullptr
     double *site_virial;    // [n][9] per-atom -sum_j D_j r_j^T, or nullptr
+    double *site_virial6;   // [atoms][6] LAMMPS per-atom virial (half of each entry's
+                            // -D r^T to the centre, half to the neighbour), or nullptr
 };
 
 // Launch shape of the E/F/S kernel (efs_kernel.hip).
@@ -311,6 +314,21 @@ hipError_t launch_rows_reduce(const double *rows, int nrows, int cols, double *o
                               hipStream_t s);
 hipError_t launch_grad(const DevModel &m, const DevNeighbors &nb, const TrainArgs &t,
                        const EfsLaunch &cfg, hipStream_t s);
+
+// Site requests (mtpx_compute_sites): per-entry geometry from positions or
+// given vectors (neighbors.hip), skipped entries get d = +inf and type 0.
+hipError_t launch_site_prepare(int nrows, const int *offsets, const int *center_atom,
+                               const int *idx, const int *atom_type, const double *pos,
+                               const double *vec, double cutoffsq, int *center_type, int *type,
+                               double *x, double *y, double *z, double *d, hipStream_t s);
+// Ordered assembly over every atom of a site request (efs_kernel.hip): forces
+// and, when site_virial6 is set, the LAMMPS per-atom virial; atom_row [ntotal]
+// is the centre row of each atom or -1, rev_offsets/rev_pairs the entries
+// whose neighbour is the atom, in ascending order.
+hipError_t launch_site_gather(const DevNeighbors &nb, int ntotal, const int *atom_row,
+                              const double *pair_ders, const int *rev_offsets,
+                              const int *rev_pairs, double *forces, double *site_virial6,
+                              hipStream_t s);
 
 hipError_t launch_efs_finish(const DevNeighbors &nb, const EfsOut &out, int rows,
                              bool deterministic, const int *rev_offsets, const int *rev_pairs,

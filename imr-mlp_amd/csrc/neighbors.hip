@@ -806,6 +806,52 @@ int build_neighbors_gpu(const double cell[9], const int pbc[3], int n, const dou
 
 namespace {
 
+// Entry geometry of a site request, one wave per centre row: r = x[j] - x[i]
+// (or the caller's vector) and d = sqrt(r.r) as MLIPCore::compute forms them
+// (runtime/mtp/mlip.cpp:949-968, no contraction in this file).  Entries the
+// reference skips (r.r == 0, r.r >= cutoff^2, a neighbour of negative type)
+// get d = +inf, beyond every cutoff, and type 0.
+__global__ __launch_bounds__(256) void site_prepare_kernel(
+    int nrows, const int *offsets, const int *center_atom, const int *idx, const int *atom_type,
+    const double *pos, const double *vec, double cutoffsq, int *center_type, int *type,
+    double *x, double *y, double *z, double *d)
+{
+    const int row = blockIdx.x * (blockDim.x / 64) + threadIdx.x / 64;
+    const int lane = threadIdx.x & 63;
+    if (row >= nrows)
+        return;
+    const int ai = center_atom[row];
+    if (lane == 0)
+        center_type[row] = atom_type[ai];
+    double xi0 = 0, xi1 = 0, xi2 = 0;
+    if (!vec) {
+        xi0 = pos[3 * (int64_t)ai];
+        xi1 = pos[3 * (int64_t)ai + 1];
+        xi2 = pos[3 * (int64_t)ai + 2];
+    }
+    for (int p = offsets[row] + lane; p < offsets[row + 1]; p += 64) {
+        const int j = idx[p];
+        double r0, r1, r2;
+        if (vec) {
+            r0 = vec[3 * (int64_t)p];
+            r1 = vec[3 * (int64_t)p + 1];
+            r2 = vec[3 * (int64_t)p + 2];
+        } else {
+            r0 = pos[3 * (int64_t)j] - xi0;
+            r1 = pos[3 * (int64_t)j + 1] - xi1;
+            r2 = pos[3 * (int64_t)j + 2] - xi2;
+        }
+        const double rr = r0 * r0 + r1 * r1 + r2 * r2;
+        const int tj = atom_type[j];
+        const bool keep = tj >= 0 && rr > 0.0 && rr < cutoffsq;
+        x[p] = r0;
+        y[p] = r1;
+        z[p] = r2;
+        d[p] = keep ? sqrt(rr) : __builtin_inf();
+        type[p] = keep ? tj : 0;
+    }
+}
+
 // Append one structure's lists (atoms from a0, entries from p0) to a batch.
 __global__ void append_lists_kernel(const int *offsets, const int *idx, int n, int64_t P, int a0,
                                     int64_t p0, int *out_offsets, int *out_idx)
@@ -843,6 +889,18 @@ hipError_t grow_keep(DBuf &b, size_t need, size_t keep, hipStream_t s)
 }
 
 }  // namespace
+
+hipError_t launch_site_prepare(int nrows, const int *offsets, const int *center_atom,
+                               const int *idx, const int *atom_type, const double *pos,
+                               const double *vec, double cutoffsq, int *center_type, int *type,
+                               double *x, double *y, double *z, double *d, hipStream_t s)
+{
+    if (nrows > 0)
+        hipLaunchKernelGGL(site_prepare_kernel, dim3((nrows + 3) / 4), dim3(256), 0, s, nrows,
+                           offsets, center_atom, idx, atom_type, pos, vec, cutoffsq, center_type,
+                           type, x, y, z, d);
+    return hipGetLastError();
+}
 
 int build_neighbors_batch_gpu(int nconf, const int *atom_offsets, const double *cells,
                               const int *pbc, const double *pos, const int *types, double cutoff,

@@ -252,23 +252,18 @@ int mtpx_compute_batch(mtpx_context *ctx, int deterministic, double *energy, dou
         rc = batch_forward(ctx, deterministic != 0);
     if (rc != MTPX_OK)
         return rc;
-    const int nc = ctx->nconf, n = ctx->n;
+    const size_t nc = (size_t)ctx->nconf, n = (size_t)ctx->n;
+    const bool add = ctx->add_efs;
     HIP_TRY(hipStreamSynchronize(ctx->stream), "compute batch");
-    if (energy && nc > 0)
-        HIP_TRY(hipMemcpy(energy, ctx->benergy.p, sizeof(double) * nc, hipMemcpyDeviceToHost),
-                "copy energies");
-    if (stress && nc > 0)
-        HIP_TRY(hipMemcpy(stress, ctx->bstress.p, sizeof(double) * 9 * nc,
-                          hipMemcpyDeviceToHost),
-                "copy stresses");
-    if (forces && n > 0)
-        HIP_TRY(hipMemcpy(forces, ctx->forces.p, sizeof(double) * 3 * n, hipMemcpyDeviceToHost),
-                "copy forces");
-    if (site_energies && n > 0)
-        HIP_TRY(hipMemcpy(site_energies, ctx->site_energy.p, sizeof(double) * n,
-                          hipMemcpyDeviceToHost),
-                "copy site energies");
-    return MTPX_OK;
+    if (energy)
+        rc = copy_out(ctx, energy, ctx->benergy.p, nc, add, "copy energies");
+    if (rc == MTPX_OK && stress)
+        rc = copy_out(ctx, stress, ctx->bstress.p, 9 * nc, add, "copy stresses");
+    if (rc == MTPX_OK && forces)
+        rc = copy_out(ctx, forces, ctx->forces.p, 3 * n, add, "copy forces");
+    if (rc == MTPX_OK && site_energies)
+        rc = copy_out(ctx, site_energies, ctx->site_energy.p, n, add, "copy site energies");
+    return rc;
 }
 
 int mtpx_loss_weights(const mtpx_loss_settings *s, int nconf, const int *atom_offsets,

@@ -83,8 +83,20 @@ def lib():
         L.mtpx_linear_system.argtypes = [C.c_void_p, _dp, _dp]
         L.mtpx_orthogonalize.argtypes = [C.c_void_p]
         L.mtpx_last_linear_timings.argtypes = [C.c_void_p, _dp]
+        L.mtpx_set_add_efs.argtypes = [C.c_void_p, C.c_int]
+        L.mtpx_compute_sites.argtypes = [C.c_void_p, C.POINTER(SiteRequest)]
         _lib = L
     return _lib
+
+
+class SiteRequest(C.Structure):
+    """mtpx_site_request (MTPGpuBatchRequest / MTPGpuComputeRequest)."""
+    _fields_ = [("center_count", C.c_int), ("nlocal", C.c_int), ("ntotal", C.c_int),
+                ("centers", _ip), ("offsets", _ip), ("neighbors", _ip),
+                ("neighbor_index_mask", C.c_int), ("neighbor_vectors", _dp), ("type", _ip),
+                ("x", _dp), ("force", _dp), ("total_energy", _dp), ("global_virial", _dp),
+                ("site_energy", _dp), ("site_virial", _dp), ("accumulate_force", C.c_int),
+                ("reuse_topology", C.c_int), ("deterministic", C.c_int)]
 
 
 class LossSettings(C.Structure):
@@ -242,15 +254,55 @@ class Context:
                     center_types=ct[:n])
 
     # ---- E/F/S ----
-    def efs(self, deterministic: bool = False):
+    def efs(self, deterministic: bool = False, init=None):
+        """getEFS; init = (E, F, S, site energies) start values, which the
+        outputs are added onto when add_efs is set."""
         n, _ = self.neighbor_count()
         E = C.c_double()
         F = np.zeros((max(n, 1), 3))
         S = np.zeros((3, 3))
         se = np.zeros(max(n, 1))
+        if init is not None:
+            E.value = float(init[0])
+            F[:n] = init[1]
+            S[:] = init[2]
+            se[:n] = init[3]
         self._check(lib().mtpx_efs(self.h, int(deterministic), C.byref(E), _d(F), _d(S), _d(se)),
                     "efs")
         return E.value, F[:n], S, se[:n]
+
+    def set_add_efs(self, flag: bool):
+        self._check(lib().mtpx_set_add_efs(self.h, int(bool(flag))), "set_add_efs")
+
+    def compute_sites(self, offsets, neighbors, types, x=None, vectors=None, centers=None,
+                      nlocal=None, mask=-1, force=None, accumulate=True, reuse=False,
+                      deterministic=False, site_virial=True):
+        """mtpx_compute_sites over a CSR with ghost atoms.  types [ntotal];
+        force (optional start values, [ntotal][3]) is added onto when
+        accumulate.  Returns dict(energy, virial6, force, site_energy,
+        site_virial)."""
+        offsets, neighbors, types = i32(offsets), i32(neighbors), i32(types)
+        ntotal = int(types.size)
+        nc = len(offsets) - 1
+        nlocal = ntotal if nlocal is None else int(nlocal)
+        cen = None if centers is None else i32(centers)
+        xs = None if x is None else f64(x, (-1,))
+        vs = None if vectors is None else f64(vectors, (-1,))
+        F = np.zeros((max(ntotal, 1), 3))
+        if force is not None:
+            F[:ntotal] = force
+        E = np.zeros(1)
+        V6 = np.zeros(6)
+        se = np.zeros(max(nlocal, 1))
+        sv = np.zeros((max(ntotal, 1), 6)) if site_virial else None
+        r = SiteRequest(nc, nlocal, ntotal, None if cen is None else _i(cen), _i(offsets),
+                        _i(neighbors), int(mask), None if vs is None else _d(vs), _i(types),
+                        None if xs is None else _d(xs), _d(F), _d(E), _d(V6), _d(se),
+                        None if sv is None else _d(sv), int(bool(accumulate)), int(bool(reuse)),
+                        int(bool(deterministic)))
+        self._check(lib().mtpx_compute_sites(self.h, C.byref(r)), "compute_sites")
+        return dict(energy=float(E[0]), virial6=V6, force=F[:ntotal], site_energy=se[:nlocal],
+                    site_virial=None if sv is None else sv[:ntotal])
 
     def energy(self):
         """getE: per-structure energies and site energies."""

@@ -130,6 +130,64 @@ int mtpx_efs_device(mtpx_context *ctx, int deterministic);
  * {E/F/S kernel + reductions, E/F/S kernel alone, reductions, 0}. */
 int mtpx_last_timings(const mtpx_context *ctx, double out_ms[4]);
 
+/* PotMTP's add_efs member (potentials/potential.h:188; getEFS
+ * potentials/potential_mtp.cpp:1904-1907): 0 (the default) makes mtpx_efs
+ * and mtpx_compute_batch overwrite energy, forces, stress and site energies;
+ * 1 adds the results onto what the caller's arrays hold. */
+int mtpx_set_add_efs(mtpx_context *ctx, int add_efs);
+
+/* ---- CSR site requests with ghost atoms ------------------------------
+ * MTPGpuBatchRequest / MTPGpuComputeRequest
+ * (runtime/mtp/gpu-direct/mtp_gpu_direct.h:359-440, :455-517) as driven by
+ * the LAMMPS pair style mlip/gpudirect
+ * (LAMMPS/USER-MLIP/pair_MLIP_gpu_direct.cpp:577-603) and computed on the
+ * CPU by MLIPCore::compute (runtime/mtp/mlip.cpp:907-1191).  Atoms 0 ..
+ * ntotal-1 are owned (< nlocal) or ghosts; centre c is atom centers[c]
+ * (< nlocal) with neighbours neighbors[offsets[c] .. offsets[c+1]-1] & mask,
+ * atom indices < ntotal (ghosts allowed).  Per entry r = x[j] - x[i] (or the
+ * given neighbor_vectors); entries with r.r == 0, r.r >= cutoff^2 or a
+ * neighbour of negative type are skipped, and so are centres of negative
+ * type (the reference's species map returning -1).
+ *
+ * Outputs (each may be NULL):
+ *   force [ntotal][3]: f_i += sum_j D_j, f_j -= D_j; added onto the array
+ *     when accumulate_force (the reference default and LAMMPS semantics),
+ *     overwritten otherwise;
+ *   total_energy; global_virial [6] xx yy zz xy xz yz (symmetric part of
+ *     -sum D r^T); both overwritten;
+ *   site_energy [nlocal]: E_i of each centre at its atom index, 0 for owned
+ *     atoms that are not centres; overwritten;
+ *   site_virial [ntotal][6]: per entry -1/2 D r^T (symmetrised for the
+ *     off-diagonal terms) to the centre and half to the neighbour (ghosts
+ *     included), the LAMMPS per-atom virial of mlip.cpp:1164-1190;
+ *     overwritten.
+ * reuse_topology keeps the centres, offsets and neighbour indices of the
+ * previous request (the counts must match) and refreshes types and
+ * positions.  deterministic orders every sum (no floating-point atomics).
+ * Independent of the resident lists of mtpx_build_neighbors /
+ * mtpx_set_structures, which stay as they are. */
+typedef struct mtpx_site_request {
+    int center_count;              /* centres (LAMMPS inum) */
+    int nlocal;                    /* owned atoms */
+    int ntotal;                    /* owned + ghost atoms */
+    const int *centers;            /* [center_count] atom of each centre; NULL: 0 .. center_count-1 */
+    const int *offsets;            /* [center_count + 1] */
+    const int *neighbors;          /* [offsets[center_count]] atom indices (before the mask) */
+    int neighbor_index_mask;       /* LAMMPS NEIGHMASK; -1 keeps every bit */
+    const double *neighbor_vectors;/* [P][3] r_j - r_i, or NULL to take x[j] - x[i] */
+    const int *type;               /* [ntotal] species 0 .. Z-1, negative: skipped */
+    const double *x;               /* [ntotal][3]; may be NULL with neighbor_vectors */
+    double *force;                 /* [ntotal][3] */
+    double *total_energy;
+    double *global_virial;         /* [6] */
+    double *site_energy;           /* [nlocal] */
+    double *site_virial;           /* [ntotal][6] */
+    int accumulate_force;
+    int reuse_topology;
+    int deterministic;
+} mtpx_site_request;
+int mtpx_compute_sites(mtpx_context *ctx, const mtpx_site_request *req);
+
 /* ---- training batches -------------------------------------------------
  * A batch is nconf structures stored one after the other: structure c owns
  * atoms atom_offsets[c] .. atom_offsets[c+1]-1 of pos [N][3] and types [N],

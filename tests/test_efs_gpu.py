@@ -155,6 +155,36 @@ def test_full_size_workload2_matches_oracle(ctx):
     assert np.abs(Sg - Sg.T).max() < 1e-9 * np.abs(Sg).max()
 
 
+@pytest.mark.timeout(600)
+def test_full_size_workload3_matches_oracle(ctx):
+    """The 256,000-atom level-20 four-species cell (about 14.8M directed
+    entries): device lists bit-exact against the oracle's BOXED lists, E/F/S
+    against the oracle's getEFSOMP at 1e-10, and the size-independent sums."""
+    model_text, s = S.workload_inference(3)
+    m = O.Model(model_text)
+    pos = O.wrap(s.cell, s.pbc, s.pos)
+    nb = O.Neighbors.build(s.cell, s.pbc, pos, s.types, m.cutoff)
+    assert s.n == 256000 and nb.P > 14_000_000
+    ctx.load_model_text(model_text)
+    ctx.build_neighbors(s.cell, s.pbc, pos, s.types, m.cutoff)
+    got = ctx.get_neighbors()
+    assert np.array_equal(got["offsets"], nb.offsets)
+    assert np.array_equal(got["idx"], nb.idx)
+    assert np.array_equal(got["types"], nb.types)
+    assert np.array_equal(got["vec"].view(np.uint64), nb.vec.view(np.uint64))
+    assert np.array_equal(got["dist"].view(np.uint64), nb.dist.view(np.uint64))
+    del got
+    E, F, St, se = O.efs(m, nb, threads=16)
+    res = ctx.efs()
+    assert_efs_close(res, dict(E=E, F=F, S=St, se=se), TOL)
+    Eg, Fg, Sg, seg = res
+    assert abs(Eg - seg.sum()) <= 1e-12 * np.abs(seg).sum()
+    assert np.abs(Fg.sum(axis=0)).max() < 1e-9 * np.abs(Fg).max() * np.sqrt(len(Fg))
+    assert np.abs(Sg - Sg.T).max() < 1e-9 * np.abs(Sg).max()
+    # the deterministic path at this size too
+    assert_efs_close(ctx.efs(deterministic=True), dict(E=E, F=F, S=St, se=se), TOL)
+
+
 @pytest.mark.parametrize("name,model_text,s", CASES[:4], ids=[c[0] for c in CASES[:4]])
 def test_energy_only_matches_oracle_get_e(ctx, name, model_text, s):
     """getE: energies without the gradient, the same numbers as mtpx_efs."""
