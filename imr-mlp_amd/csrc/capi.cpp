@@ -394,6 +394,11 @@ int mtpx_create(int device, mtpx_context **out)
             delete ctx;
             return MTPX_E_DEVICE;
         }
+    // the allocation-free entry point's scratch: this device's copy
+    if (noalloc_scratch_address(&ctx->noalloc_scratch) != hipSuccess || !ctx->noalloc_scratch) {
+        delete ctx;
+        return MTPX_E_DEVICE;
+    }
     hipDeviceProp_t prop;
     if (hipGetDeviceProperties(&prop, device) == hipSuccess && prop.multiProcessorCount > 0) {
         ctx->num_cus = prop.multiProcessorCount;
@@ -693,6 +698,55 @@ int mtpx_efs(mtpx_context *ctx, int deterministic, double *energy, double *force
         if (int rc2 = copy_out(ctx, site_energies, ctx->site_energy.p, (size_t)ctx->n, add,
                                "copy site energies"))
             return rc2;
+    return MTPX_OK;
+}
+
+int mtpx_efs_noalloc(mtpx_context *ctx, double *forces, double *site_energies,
+                     double *energy_stress)
+{
+    if (!ctx)
+        return MTPX_E_INVALID;
+    if (!ctx->has_model)
+        return set_error(ctx, MTPX_E_NO_MODEL, "no model loaded");
+    if (!ctx->has_nbh)
+        return set_error(ctx, MTPX_E_NO_TOPOLOGY, "no neighbour lists");
+    if (int rc = check_species(ctx))
+        return rc;
+    const int n = ctx->n;
+    if (!energy_stress || (n > 0 && (!forces || !site_energies)))
+        return set_error(ctx, MTPX_E_INVALID, "null device output");
+    if (!ctx->noalloc_scratch)
+        return set_error(ctx, MTPX_E_DEVICE, "no scratch address for this device");
+    (void)hipSetDevice(ctx->device);
+    hipStream_t s = ctx->stream;
+    EfsLaunch cfg;
+    if (!efs_configure(ctx->dm, n, ctx->num_cus, 0, ctx->lds_limit, cfg))
+        return set_error(ctx, MTPX_E_CAPACITY, "model needs more LDS than a CU provides");
+    // the per-wave partial rows must fit the scratch: fewer workgroups walk
+    // the atoms with a longer stride when they would not
+    const int cap_rows = (int)(kNoAllocScratchDoubles / 10);
+    if (cfg.waves > cap_rows)
+        return set_error(ctx, MTPX_E_CAPACITY,
+                         "per-wave partial rows exceed the allocation-free scratch");
+    cfg.grid = std::min(cfg.grid, cap_rows / cfg.waves);
+    cfg.rows = cfg.grid * cfg.waves;
+    if (n > 0) {
+        EfsOut out;
+        out.forces = forces;
+        out.site_energy = site_energies;
+        out.partial = ctx->noalloc_scratch;
+        out.pair_ders = nullptr;
+        out.site_virial = nullptr;
+        out.site_virial6 = nullptr;
+        const DevNeighbors nb = dev_neighbors(ctx);
+        HIP_TRY(launch_fill_zero(forces, 3 * (size_t)n, s), "clear forces");
+        HIP_TRY(launch_efs(ctx->dm, nb, out, cfg, 0, s), "launch efs kernel");
+        HIP_TRY(launch_efs_finish(nb, out, cfg.rows, false, nullptr, nullptr, energy_stress, s),
+                "launch efs reduction");
+    } else {
+        HIP_TRY(launch_fill_zero(energy_stress, 10, s), "clear outputs");
+    }
+    HIP_TRY(hipStreamSynchronize(s), "efs");
     return MTPX_OK;
 }
 

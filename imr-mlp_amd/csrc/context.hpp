@@ -79,6 +79,10 @@ struct mtpx_context {
     // PotMTP::add_efs: E/F/S outputs are added onto the caller's arrays
     bool add_efs = false;
 
+    // device address of this GPU's static scratch array (mtpx_efs_noalloc),
+    // taken once at mtpx_create with the device current
+    double *noalloc_scratch = nullptr;
+
     // CSR site requests (mtpx_compute_sites): their own topology, kept for
     // reuse_topology; independent of the resident lists above
     struct Sites {

@@ -323,6 +323,18 @@ __global__ __launch_bounds__(256) void site_gather_kernel(DevNeighbors nb, int n
             site_virial6[6 * (int64_t)k + c] = v[c];
 }
 
+// Scratch of the allocation-free entry point: the per-wave partial rows.
+// Host code never names this array; it takes the device address from
+// noalloc_scratch_address once per device.
+static __device__ __align__(256) double scratch[kNoAllocScratchDoubles];
+
+__global__ __launch_bounds__(256) void fill_zero_kernel(double *p, size_t count)
+{
+    for (size_t k = (size_t)blockIdx.x * blockDim.x + threadIdx.x; k < count;
+         k += (size_t)gridDim.x * blockDim.x)
+        p[k] = 0.0;
+}
+
 // Kernel variants: shell profile x table placement.  The profiles whose
 // kernels fit 256 registers run eight waves per workgroup, the larger ones four.
 template <class P>
@@ -398,6 +410,20 @@ hipError_t launch_efs(const DevModel &m, const DevNeighbors &nb, const EfsOut &o
     case 3: launch_variant<ProfSmall>(m, nb, out, cfg, det, s); break;
     default: launch_variant<ProfGeneric>(m, nb, out, cfg, det, s); break;
     }
+    return hipGetLastError();
+}
+
+hipError_t noalloc_scratch_address(double **ptr)
+{
+    return hipGetSymbolAddress(reinterpret_cast<void **>(ptr), HIP_SYMBOL(scratch));
+}
+
+hipError_t launch_fill_zero(double *p, size_t count, hipStream_t s)
+{
+    if (count)
+        hipLaunchKernelGGL(fill_zero_kernel,
+                           dim3((unsigned)std::min<size_t>((count + 255) / 256, 4096)), dim3(256),
+                           0, s, p, count);
     return hipGetLastError();
 }
 

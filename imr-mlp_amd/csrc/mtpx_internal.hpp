@@ -330,6 +330,15 @@ hipError_t launch_site_gather(const DevNeighbors &nb, int ntotal, const int *ato
                               const int *rev_pairs, double *forces, double *site_virial6,
                               hipStream_t s);
 
+// Allocation-free E/F/S (mtpx_efs_noalloc): the per-wave partial rows live
+// in a file-scope device array of this many doubles (efs_kernel.hip), one
+// copy per GPU, shared by every call on that GPU.
+constexpr size_t kNoAllocScratchDoubles = size_t(1) << 16;  // 512 KiB
+// Device address of that array on the current device (hipGetSymbolAddress).
+hipError_t noalloc_scratch_address(double **ptr);
+// Zero-fill kernel (used where a caller may capture the launches).
+hipError_t launch_fill_zero(double *p, size_t count, hipStream_t s);
+
 hipError_t launch_efs_finish(const DevNeighbors &nb, const EfsOut &out, int rows,
                              bool deterministic, const int *rev_offsets, const int *rev_pairs,
                              double *energy_stress10, hipStream_t s);

@@ -84,6 +84,7 @@ def lib():
         L.mtpx_orthogonalize.argtypes = [C.c_void_p]
         L.mtpx_last_linear_timings.argtypes = [C.c_void_p, _dp]
         L.mtpx_set_add_efs.argtypes = [C.c_void_p, C.c_int]
+        L.mtpx_efs_noalloc.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p]
         L.mtpx_compute_sites.argtypes = [C.c_void_p, C.POINTER(SiteRequest)]
         _lib = L
     return _lib
@@ -270,6 +271,12 @@ class Context:
         self._check(lib().mtpx_efs(self.h, int(deterministic), C.byref(E), _d(F), _d(S), _d(se)),
                     "efs")
         return E.value, F[:n], S, se[:n]
+
+    def efs_noalloc(self, forces_ptr: int, site_energies_ptr: int, energy_stress_ptr: int):
+        """mtpx_efs_noalloc on caller-owned device buffers (raw addresses)."""
+        self._check(lib().mtpx_efs_noalloc(self.h, C.c_void_p(forces_ptr),
+                                           C.c_void_p(site_energies_ptr),
+                                           C.c_void_p(energy_stress_ptr)), "efs_noalloc")
 
     def set_add_efs(self, flag: bool):
         self._check(lib().mtpx_set_add_efs(self.h, int(bool(flag))), "set_add_efs")

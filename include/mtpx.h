@@ -130,6 +130,22 @@ int mtpx_efs_device(mtpx_context *ctx, int deterministic);
  * {E/F/S kernel + reductions, E/F/S kernel alone, reductions, 0}. */
 int mtpx_last_timings(const mtpx_context *ctx, double out_ms[4]);
 
+/* No counterpart in the reference: an allocation-free mtpx_efs for callers
+ * that cannot allocate device memory (HIP graph capture, serving loops,
+ * harnesses that forbid hipMalloc).  The fast (non-deterministic) E/F/S of
+ * the resident model and lists, written to the caller's device buffers on
+ * the context's device: forces [n][3] (overwritten), site_energies [n],
+ * energy_stress [10] (energy, then the 3x3 stress row-major).  The per-wave
+ * partial sums live in one static device array of 65,536 doubles (512 KiB)
+ * per GPU, held until the process ends; a launch whose partial rows would
+ * exceed it runs fewer workgroups instead, and a model whose single
+ * workgroup would exceed it is refused with MTPX_E_CAPACITY.  Calls on one
+ * GPU share that array: calls that overlap in time on one GPU (from several
+ * contexts or threads) race.  Allocates nothing; returns after the results
+ * are in the caller's buffers. */
+int mtpx_efs_noalloc(mtpx_context *ctx, double *forces, double *site_energies,
+                     double *energy_stress);
+
 /* PotMTP's add_efs member (potentials/potential.h:188; getEFS
  * potentials/potential_mtp.cpp:1904-1907): 0 (the default) makes mtpx_efs
  * and mtpx_compute_batch overwrite energy, forces, stress and site energies;
