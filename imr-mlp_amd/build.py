@@ -38,6 +38,8 @@ SOURCES = [
     ("train_api.cpp", ["-ffp-contract=off"]),
     ("linear_api.cpp", ["-ffp-contract=off"]),
     ("sites.cpp", ["-ffp-contract=off"]),
+    ("metadata.cpp", ["-ffp-contract=off"]),
+    ("lbfgs.cpp", ["-ffp-contract=off"]),
 ]
 
 

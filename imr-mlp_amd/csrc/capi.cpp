@@ -75,6 +75,8 @@ void fill_model_sizes(const Model &M, const Plan &P, DevModel &dm)
     dm.tr_priv = P.tr_priv;
     dm.nradial = M.nradial();
     dm.ncoef = M.ncoef();
+    dm.rb_general = M.general_basis() ? 1 : 0;
+    dm.rb_table = nullptr;
     std::memcpy(dm.slot_base, P.slot_base, sizeof dm.slot_base);
     dm.fwd_nsteps = P.fwd_level_step.back();
     dm.bwd_nsteps = P.bwd_level_step.back();
@@ -119,6 +121,29 @@ int install_model(mtpx_context *ctx, Model &&m)
     HIP_TRY(upload(ctx->fwd_comb, P.fwd_comb, s), "upload model");
     HIP_TRY(upload(ctx->bwd_lcomb, P.bwd_level_comb, s), "upload model");
     HIP_TRY(upload(ctx->bwd_comb, P.bwd_comb, s), "upload model");
+    if (dm.rb_general) {
+        // per ordered pair: kind, min, max, scaling and the setup constants
+        // of the basis (basis/basis.cpp setup(): mult, su, pu, pi / max,
+        // and b, 1 / su for Poly4 / Poly5)
+        std::vector<double> t((size_t)M.Z * M.Z * kRbStride);
+        for (int q = 0; q < M.Z * M.Z; ++q) {
+            const RadialBasis &b = M.pair_basis(q / M.Z, q % M.Z);
+            double *r = &t[(size_t)q * kRbStride];
+            const double su = b.rmax - b.rmin;
+            r[0] = b.kind;
+            r[1] = b.rmin;
+            r[2] = b.rmax;
+            r[3] = b.scaling;
+            r[4] = 2.0 / (b.rmax - b.rmin);
+            r[5] = su;
+            r[6] = b.rmax + b.rmin;
+            r[7] = M_PI / b.rmax;
+            r[8] = b.b;
+            r[9] = 1.0 / su;
+        }
+        HIP_TRY(upload(ctx->rb_table, t, s), "upload model");
+        dm.rb_table = ctx->rb_table.as<double>();
+    }
     dm.map = ctx->map.as<int>();
     dm.slot_basic = ctx->slot_basic.as<int>();
     dm.slot_abc = ctx->slot_abc.as<int>();
@@ -442,6 +467,11 @@ int mtpx_load_model(mtpx_context *ctx, const mtpx_model_view *v)
     m.rmin = v->min_dist;
     m.rmax = v->max_dist;
     m.scaling = v->scaling;
+    RadialBasis rb;
+    rb.rmin = v->min_dist;
+    rb.rmax = v->max_dist;
+    rb.scaling = v->scaling;
+    m.bases.assign(1, rb);
     m.K = v->alpha_moments_count;
     m.B = v->alpha_index_basic_count;
     m.T = v->alpha_index_times_count;
@@ -488,6 +518,46 @@ int mtpx_parse_model_text(const char *text, int out8[8], double *coeffs, char *e
     if (coeffs)
         std::memcpy(coeffs, m.coef.data(), sizeof(double) * m.coef.size());
     return MTPX_OK;
+}
+
+namespace {
+int copy_text(const std::string &t, char *buf, size_t cap, size_t *len)
+{
+    if (len)
+        *len = t.size();
+    if (!buf)
+        return MTPX_OK;
+    if (cap <= t.size())
+        return MTPX_E_CAPACITY;
+    std::memcpy(buf, t.c_str(), t.size() + 1);
+    return MTPX_OK;
+}
+}  // namespace
+
+int mtpx_save_model_text(const mtpx_context *ctx, char *buf, size_t cap, size_t *len)
+{
+    if (!ctx)
+        return MTPX_E_INVALID;
+    if (!ctx->has_model)
+        return MTPX_E_NO_MODEL;
+    return copy_text(save_mtp(ctx->model), buf, cap, len);
+}
+
+int mtpx_format_model_text(const char *text, char *buf, size_t cap, size_t *len, char *err,
+                           int errlen)
+{
+    if (!text)
+        return MTPX_E_INVALID;
+    Model m;
+    std::string e;
+    if (!parse_mtp(text, m, e)) {
+        if (err && errlen > 0) {
+            std::strncpy(err, e.c_str(), (size_t)errlen - 1);
+            err[errlen - 1] = 0;
+        }
+        return MTPX_E_MODEL;
+    }
+    return copy_text(save_mtp(m), buf, cap, len);
 }
 
 int mtpx_model_info(const mtpx_context *ctx, int out8[8])

@@ -22,7 +22,7 @@ struct mtpx_context {
     DevModel dm{};
     // model buffers
     DBuf radial, species, moment, map, seed, slot_basic, slot_abc, dup, fwd_level, fwd_steps,
-        fwd_lcomb, fwd_comb, bwd_level, bwd_steps, bwd_lcomb, bwd_comb;
+        fwd_lcomb, fwd_comb, bwd_level, bwd_steps, bwd_lcomb, bwd_comb, rb_table;
 
     // neighbour lists
     bool has_nbh = false;
@@ -108,7 +108,7 @@ struct mtpx_context {
     {
         for (DBuf *b : {&radial, &species, &moment, &map, &seed, &slot_basic, &slot_abc, &dup,
                         &fwd_level, &fwd_steps, &fwd_lcomb, &fwd_comb, &bwd_level, &bwd_steps,
-                        &bwd_lcomb, &bwd_comb, &offsets, &idx, &type, &x, &y, &z, &d,
+                        &bwd_lcomb, &bwd_comb, &rb_table, &offsets, &idx, &type, &x, &y, &z, &d,
                         &center_type, &rev_offsets, &rev_pairs, &forces, &site_energy, &partial,
                         &pair_ders, &out10, &soff, &center_structure, &site_virial, &benergy,
                         &bstress, &active, &tE, &wE, &tF, &wF, &tS, &wS, &dLdE, &dLdF, &dLdS,

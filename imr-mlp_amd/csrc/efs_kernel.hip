@@ -388,6 +388,9 @@ bool efs_configure(const DevModel &m, int n, int num_cus, int max_waves, size_t 
 // radial basis size), 3: small runtime, 4: generic
 int efs_variant(const DevModel &m, int R)
 {
+    // general radial bases are evaluated by the run-time profiles only
+    if (m.rb_general)
+        return m.M <= 4 && m.numax_all <= 6 && R <= 8 ? 3 : 4;
     if (profile_is<6, 4, 2, 0>(m) && R == 8)
         return 0;
     if (profile_is<8, 6, 4, 2, 0>(m) && R == 10)

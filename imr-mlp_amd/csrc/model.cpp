@@ -1,9 +1,10 @@
 // Model I/O and the contraction-graph launch plan (host code).
 //
 // parse_mtp follows the PotMTP::Load grammar (potentials/potential_mtp.cpp:
-// 119-571) for non-split RBChebyshev models: optional potential_name,
-// optional scaling (default 0.01, :155), species_count, optional
-// potential_tag line, radial basis block, optional radial_coeffs (default
+// 119-571): optional potential_name, optional scaling (default 0.01, :155),
+// species_count, optional potential_tag line (metadata.cpp), one radial
+// basis block or, split, one per ordered species pair (RBChebyshev,
+// RBChebyCos, RBChebyshevPoly4, RBChebyshevPoly5), optional radial_coeffs (default
 // 1e-5 with 1e-3 + k on the channel diagonal, :335-351), the alpha_* tables,
 // optional species/moment coefficients (default 1e-3, :471-474).
 #include "mtpx_internal.hpp"
@@ -14,6 +15,7 @@
 #include <array>
 #include <cmath>
 #include <cstdlib>
+#include <cstdio>
 #include <cstring>
 #include <sstream>
 
@@ -264,36 +266,96 @@ bool parse_mtp(const std::string &text, Model &m, std::string &err)
     if (!in.ok() || m.Z <= 0)
         return fail(err, "Error reading .mtp file, invalid species_count");
     key = in.word();
-    if (key == "potential_tag") {
-        if (in.line().find('=') == std::string::npos)
+    if (key == "potential_tag") {  // :171-187
+        const std::string rest = in.line();
+        const size_t eq = rest.find('=');
+        if (eq == std::string::npos)
             return fail(err, "Invalid potential_tag assignment");
+        if (!tag_parse(rest.substr(eq + 1), m.Z, m.tag, err))
+            return false;
         key = in.word();
     }
-    if (key == "radial_split" || key == "radial_basis_split") {
+    if (key == "radial_split" || key == "radial_basis_split") {  // :190-204
         in.skip(2);
-        if (in.integer() != 0)
-            return fail(err, "split radial bases are not supported");
-        key = in.word();
+        m.split = in.integer() != 0;
+        if (!m.split)
+            key = in.word();
     }
-    if (key != "radial_basis_type")
-        return fail(err, "Error reading .mtp file");
-    in.skip(2);
-    if (in.word() != "RBChebyshev")
-        return fail(err, "only RBChebyshev radial bases are supported");
-    if (in.word() != "min_dist")
-        return fail(err, "Error in loading basis: min_dist");
-    in.skip(2);
-    m.rmin = in.real();
-    if (in.word() != "max_dist")
-        return fail(err, "Error in loading basis: max_dist");
-    in.skip(2);
-    m.rmax = in.real();
-    if (in.word() != "radial_basis_size")
-        return fail(err, "Error in loading basis: radial_basis_size");
-    in.skip(2);
-    m.R = in.integer();
-    if (!in.ok() || m.R <= 0)
-        return fail(err, "Error in loading basis: radial_basis_size must be positive");
+    // basis_name_to_code and AnyBasis::LoadFromStream (basis/basis.cpp:10-27,
+    // :73-117), with the rb_b line of Poly4 / Poly5 (:543-558, :716-731)
+    auto read_basis = [&](RadialBasis &b, int &size, const std::string &first) {
+        if (first != "radial_basis_type")
+            return fail(err, m.split ? "Error reading .mtp file, incorrect pair setting"
+                                     : "Error reading .mtp file");
+        in.skip(2);
+        const std::string name = in.word();
+        if (name == "RBChebyshev")
+            b.kind = kRBChebyshev;
+        else if (name == "RBChebyCos")
+            b.kind = kRBChebyCos;
+        else if (name == "RBChebyshevPoly4")
+            b.kind = kRBChebyshevPoly4;
+        else if (name == "RBChebyshevPoly5")
+            b.kind = kRBChebyshevPoly5;
+        else
+            return fail(err, ("unsupported radial basis type: " + name).c_str());
+        b.scaling = m.scaling;
+        if (in.word() != "min_dist")
+            return fail(err, "Error in loading basis: min_dist");
+        in.skip(2);
+        b.rmin = in.real();
+        if (in.word() != "max_dist")
+            return fail(err, "Error in loading basis: max_dist");
+        in.skip(2);
+        b.rmax = in.real();
+        if (in.word() != "radial_basis_size")
+            return fail(err, "Error in loading basis: radial_basis_size");
+        in.skip(2);
+        size = in.integer();
+        if (!in.ok() || size <= 0)
+            return fail(err, "Error in loading basis: radial_basis_size must be positive");
+        if (b.kind == kRBChebyshevPoly4 || b.kind == kRBChebyshevPoly5) {
+            if (in.word() != "rb_b")
+                return fail(err, "Error in loading basis: rb_b");
+            in.skip(2);
+            b.b = in.real();
+            if (!in.ok())
+                return fail(err, "Error in loading basis: rb_b");
+        }
+        if (!std::isfinite(b.rmin) || !std::isfinite(b.rmax) || !(b.rmin < b.rmax))
+            return fail(err, "Error in loading basis: min_dist < max_dist is required");
+        return true;
+    };
+    if (m.split) {  // :206-265, one basis per ordered species pair
+        m.bases.assign((size_t)m.Z * m.Z, RadialBasis());
+        std::vector<char> seen((size_t)m.Z * m.Z, 0);
+        int last = 0;
+        for (int q = 0; q < m.Z * m.Z; ++q) {
+            if (in.word() != "pair")
+                return fail(err, "Error reading .mtp file, incorrect pair setting");
+            const int ci = in.integer(), cj = in.integer();
+            if (!in.ok() || ci < 0 || ci >= m.Z || cj < 0 || cj >= m.Z)
+                return fail(err, "Error reading .mtp file, invalid radial basis pair");
+            if (seen[ci * m.Z + cj]++)
+                return fail(err, "Error reading .mtp file, duplicate radial basis pair");
+            int size = 0;
+            if (!read_basis(m.bases[ci * m.Z + cj], size, in.word()))
+                return false;
+            if (last && size != last)
+                return fail(err, "Error reading .mtp file, split radial bases must have the same "
+                                 "radial_basis_size");
+            last = size;
+        }
+        m.R = last;
+    } else {
+        m.bases.assign(1, RadialBasis());
+        if (!read_basis(m.bases[0], m.R, key))
+            return false;
+    }
+    m.rmin = m.bases[0].rmin;
+    m.rmax = 0;
+    for (const RadialBasis &b : m.bases)
+        m.rmax = std::max(m.rmax, b.rmax);
     if (in.word() != "radial_funcs_count")
         return fail(err, "Error reading .mtp file");
     in.skip(2);
@@ -423,6 +485,118 @@ bool parse_mtp(const std::string &text, Model &m, std::string &err)
     return validate_model(m, err);
 }
 
+// PotMTP::Save (potentials/potential_mtp.cpp:1052-1061): write_header
+// (:656-671), write_radial_info (:673-690; AnyBasis::SaveToStream,
+// basis/basis.h:50-56, and the rb_b line of Poly4 / Poly5, basis.cpp:560-564,
+// :733-737), write_radial_coeff (:692-714), write_rules (:716-752) and
+// write_linear_coeff (:754-785), on a stream in std::scientific notation
+// with max_digits10 (17) digits: printf "%.17e" for every double.
+std::string save_mtp(const Model &m)
+{
+    std::string o;
+    char buf[64];
+    auto num = [&](double v) {
+        std::snprintf(buf, sizeof buf, "%.17e", v);
+        o += buf;
+    };
+    auto integer = [&](long v) { o += std::to_string(v); };
+    static const char *kind_names[] = {"RBChebyshev", "RBChebyCos", "RBChebyshevPoly4",
+                                       "RBChebyshevPoly5"};
+    o += "MTP\nversion = 1.1.0\npotential_name = MTP1m\nscaling = ";
+    num(m.bases.empty() ? m.scaling : m.bases[0].scaling);
+    o += "\nspecies_count = ";
+    integer(m.Z);
+    o += "\npotential_tag = " + tag_output(m.tag) + "\n";
+    if (m.split)
+        o += "radial_basis_split = 1\n";
+    for (size_t q = 0; q < m.bases.size(); ++q) {
+        const RadialBasis &b = m.bases[q];
+        if (m.split) {
+            o += "pair ";
+            integer((long)q / m.Z);
+            o += ' ';
+            integer((long)q % m.Z);
+            o += '\n';
+        }
+        o += "radial_basis_type = ";
+        o += kind_names[b.kind];
+        o += "\n\tmin_dist = ";
+        num(b.rmin);
+        o += "\n\tmax_dist = ";
+        num(b.rmax);
+        o += "\n\tradial_basis_size = ";
+        integer(m.R);
+        o += '\n';
+        if (b.kind == kRBChebyshevPoly4 || b.kind == kRBChebyshevPoly5) {
+            o += "\trb_b = ";
+            num(b.b);
+            o += '\n';
+        }
+    }
+    o += "radial_funcs_count = ";
+    integer(m.M);
+    o += "\nradial_coeffs\n";
+    size_t q = 0;
+    for (int i = 0; i < m.Z; ++i)
+        for (int j = 0; j < m.Z; ++j) {
+            o += '\t';
+            integer(i);
+            o += '-';
+            integer(j);
+            o += '\n';
+            for (int k = 0; k < m.M; ++k) {
+                o += "\t\t{";
+                for (int l = 0; l < m.R; ++l) {
+                    num(m.coef[q++]);
+                    o += l != m.R - 1 ? ", " : "}\n";
+                }
+            }
+        }
+    o += "alpha_moments_count = ";
+    integer(m.K);
+    o += "\nalpha_index_basic_count = ";
+    integer(m.B);
+    o += "\nalpha_index_basic = {";
+    auto quad = [&](const int *v, bool last) {
+        o += '{';
+        for (int k = 0; k < 4; ++k) {
+            integer(v[k]);
+            if (k < 3)
+                o += ", ";
+        }
+        o += last ? "}" : "}, ";
+    };
+    for (int i = 0; i < m.B; ++i)
+        quad(&m.basic[4 * i], i == m.B - 1);
+    o += "}\nalpha_index_times_count = ";
+    integer(m.T);
+    o += "\nalpha_index_times = {";
+    for (int i = 0; i < m.T; ++i)
+        quad(&m.times[4 * i], i == m.T - 1);
+    o += "}\nalpha_scalar_moments = ";
+    integer(m.S);
+    o += "\nalpha_moment_mapping = {";
+    for (int i = 0; i < m.S; ++i) {
+        if (i)
+            o += ", ";
+        integer(m.map[i]);
+    }
+    o += "}\nspecies_coeffs = {";
+    for (int i = 0; i < m.Z; ++i) {
+        if (i)
+            o += ", ";
+        num(m.coef[m.nradial() + i]);
+    }
+    o += "}\nmoment_coeffs = {";
+    for (int i = 0; i < m.S; ++i) {
+        if (i)
+            o += ", ";
+        num(m.coef[m.nradial() + m.Z + i]);
+    }
+    o += "}\n";
+    return o;
+}
+
 bool validate_model(const Model &m, std::string &err)
 {
     if (m.Z <= 0 || m.M < 1 || m.R <= 0 || m.B < 1 || m.K < m.B || m.T < 0 || m.S < 0)
@@ -433,6 +607,13 @@ bool validate_model(const Model &m, std::string &err)
         return fail(err, "radial_basis_size exceeds the supported maximum (16)");
     if (m.K > 65535)
         return fail(err, "alpha_moments_count exceeds the supported maximum (65535)");
+    if (m.bases.size() != (m.split ? (size_t)m.Z * m.Z : 1))
+        return fail(err, "radial basis table does not match species_count");
+    for (const RadialBasis &b : m.bases)
+        if (!(b.rmax > b.rmin) || !std::isfinite(b.rmin) || !std::isfinite(b.rmax) ||
+            !std::isfinite(b.scaling) || !std::isfinite(b.b) || b.kind < kRBChebyshev ||
+            b.kind > kRBChebyshevPoly5)
+            return fail(err, "invalid radial basis");
     if (!(m.rmax > m.rmin) || !std::isfinite(m.rmin) || !std::isfinite(m.rmax))
         return fail(err, "invalid radial basis interval");
     if ((int)m.basic.size() != 4 * m.B || (int)m.times.size() != 4 * m.T ||

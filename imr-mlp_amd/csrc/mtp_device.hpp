@@ -128,21 +128,36 @@ struct Nbr {
     double f[MMAX], fd[MMAX];
 };
 
+// The cutoff of the pair (ti, tj): the model's, or with general radial bases
+// the pair basis's max_dist (cutoffs(itype, jtype), potential_mtp.cpp:2842).
+template <bool kGeneral>
+__device__ __forceinline__ double pair_cutoff(const DevModel &m, int ti, int tj)
+{
+    if constexpr (kGeneral)
+        if (m.rb_general)
+            return m.rb_table[(ti * m.Z + tj) * kRbStride + 2];
+    return m.rmax;
+}
+
 // Geometry of list entry p; lanes without an entry keep zeros, so they
 // contribute nothing to the sums below.  Returns 1 for an entry inside the
 // cutoff and 0 otherwise (potential_mtp.cpp:2842 skips entries beyond the
-// cutoff and keeps r == cutoff); such entries get d = cutoff.
-template <int MMAX>
+// cutoff and keeps r == cutoff); such entries get d = cutoff.  kGeneral
+// (run-time profiles) reads the pair's cutoff when the model has general
+// radial bases.
+template <int MMAX, bool kGeneral = false>
 __device__ __forceinline__ double load_geometry(const DevModel &m, const DevNeighbors &nb,
-                                                int64_t p, bool valid, Nbr<MMAX> &q, int &tj)
+                                                int64_t p, bool valid, Nbr<MMAX> &q, int &tj,
+                                                int ti = 0)
 {
     q.x = valid ? nb.x[p] : 0.0;
     q.y = valid ? nb.y[p] : 0.0;
     q.z = valid ? nb.z[p] : 0.0;
-    const double dd = valid ? nb.d[p] : m.rmax;
     tj = valid ? nb.type[p] : 0;
-    const bool in_cutoff = valid && !(dd > m.rmax);
-    const double d = in_cutoff ? dd : m.rmax;
+    const double rc = pair_cutoff<kGeneral>(m, ti, tj);
+    const double dd = valid ? nb.d[p] : rc;
+    const bool in_cutoff = valid && !(dd > rc);
+    const double d = in_cutoff ? dd : rc;
     q.d = d;
     q.invd = 1.0 / d;
     q.ux = q.x * q.invd;
@@ -170,6 +185,74 @@ __device__ __forceinline__ void chebyshev(const DevModel &m, double d, double *Q
     }
 }
 
+// A general radial basis (basis/basis.cpp): Chebyshev polynomials of
+// xi = (2d - (min + max)) / (max - min) times an envelope rc(d), by the same
+// recurrence as RBChebyshev -- Q_0 = s rc, Q_1 = s xi rc,
+// Q_k = 2 xi Q_(k-1) - Q_(k-2), and the derivative recurrence with
+// mult = 2 / (max - min) -- for the envelopes
+//   RBChebyshev       (d - max)^2                              (:148-164)
+//   RBChebyCos        (1 + cos(pi d / max)) / 2                (:242-271)
+//   RBChebyshevPoly4  (1 - x)^3 (1 + (3 + b) x), x = (d - min) / (max - min),
+//                     zero outside [min, max]                  (:585-619)
+//   RBChebyshevPoly5  (1 - x)^4 (1 + (4 + b) x), likewise      (:776-805)
+// t is the pair's row of the basis table (kRbStride doubles).
+template <int RMAX>
+__device__ __forceinline__ void general_basis(const double *t, double d, double *Q, double *dQ)
+{
+    const int kind = (int)t[0];
+    const double rmin = t[1], rmax = t[2], s = t[3], mult = t[4], su = t[5], pu = t[6];
+    const double ksi = (2 * d - pu) / su;
+    double rc, drc;
+    if (kind == kRBChebyshev) {
+        const double ru = d - rmax;
+        rc = ru * ru;
+        drc = 2 * ru;
+    } else if (kind == kRBChebyCos) {
+        const double irpi = t[7];
+        rc = 0.5 * (1.0 + cos(d * irpi));
+        drc = -0.5 * irpi * sin(d * irpi);
+    } else {
+        const double b = t[8], dxdr = t[9];
+        const bool inside = !(d < rmin || d > rmax);
+        const double x = (d - rmin) / su;
+        const double vx = 1.0 - x, vxx = vx * vx, vxxx = vxx * vx;
+        if (kind == kRBChebyshevPoly4) {
+            rc = vxxx * (1 + (3 + b) * x);
+            drc = vxx * (b * (1. - 4.0 * x) - 12.0 * x) * dxdr;
+        } else {
+            rc = vxx * vxx * (1 + (4 + b) * x);
+            drc = -vxxx * (20 * x + b * (5 * x - 1)) * dxdr;
+        }
+        rc = inside ? rc : 0.0;
+        drc = inside ? drc : 0.0;
+    }
+    Q[0] = s * rc;
+    dQ[0] = s * drc;
+    if (RMAX > 1) {
+        Q[1] = s * (ksi * rc);
+        dQ[1] = s * (mult * rc + ksi * drc);
+    }
+#pragma unroll
+    for (int k = 2; k < RMAX; ++k) {
+        Q[k] = 2 * ksi * Q[k - 1] - Q[k - 2];
+        dQ[k] = 2 * (mult * Q[k - 1] + ksi * dQ[k - 1]) - dQ[k - 2];
+    }
+}
+
+// The radial basis of the pair (ti, tj) at distance d: the model's shared
+// RBChebyshev basis, or (run-time profiles only) the pair's general basis.
+template <class P>
+__device__ __forceinline__ void radial_basis(const DevModel &m, int ti, int tj, double d,
+                                             double *Q, double *dQ)
+{
+    if constexpr (!P::exact)
+        if (m.rb_general) {
+            general_basis<P::RMAX>(m.rb_table + (ti * m.Z + tj) * kRbStride, d, Q, dQ);
+            return;
+        }
+    chebyshev<P::RMAX>(m, d, Q, dQ);
+}
+
 // Geometry plus the radial functions f_mu = sum_k c[ti,tj,mu,k] Q_k and
 // their derivatives (coefficients staged in LDS), zero beyond the cutoff.
 template <class P>
@@ -179,9 +262,9 @@ __device__ __forceinline__ void load_neighbor(const DevModel &m, const DevNeighb
 {
     constexpr int RMAX = P::RMAX;
     int tj;
-    const double w = load_geometry(m, nb, p, valid, q, tj);
+    const double w = load_geometry<P::M, !P::exact>(m, nb, p, valid, q, tj, ti);
     double Q[RMAX], dQ[RMAX];
-    chebyshev<RMAX>(m, q.d, Q, dQ);
+    radial_basis<P>(m, ti, tj, q.d, Q, dQ);
     // exact profiles fix M and R at compile time
     const int R = P::exact ? RMAX : m.R;
     const double *c = coef_lds + (ti * m.Z + tj) * (P::exact ? P::M : m.M) * R;

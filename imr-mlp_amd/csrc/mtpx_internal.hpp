@@ -4,6 +4,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <map>
 #include <string>
 #include <vector>
 
@@ -78,11 +79,50 @@ int build_neighbors_batch_gpu(int nconf, const int *atom_offsets, const double *
                               hipStream_t s, NeighborStore &out, NeighborStore &tmp,
                               NeighborScratch &w, std::string &err);
 
+// A JSON value (the potential_tag metadata, metadata.cpp).
+struct Json {
+    enum Kind { Null, Bool, Num, Str, Arr, Obj } kind = Null;
+    bool b = false;
+    double num = 0;
+    std::string str;
+    std::vector<Json> arr;
+    std::map<std::string, Json> obj;
+};
+bool json_parse(const std::string &text, Json &out, std::string &err);
+std::string json_serialize(const Json &v);
+// potential_tag of an .mtp file: the fields of a structured tag, or the plain
+// text of a legacy one (MTPMetadata::Tag, tools/mtp_metadata.h:93-370).
+struct MetaTag {
+    std::map<std::string, Json> fields;
+    std::string legacy;
+};
+bool tag_parse(const std::string &raw, int Z, MetaTag &tag, std::string &err);
+std::string tag_output(const MetaTag &tag);
+
+// Radial basis kinds (basis/basis.h:19-29): the Chebyshev polynomials of
+// xi = (2r - (min + max)) / (max - min) times an envelope.
+enum RadialKind { kRBChebyshev = 0, kRBChebyCos = 1, kRBChebyshevPoly4 = 2, kRBChebyshevPoly5 = 3 };
+struct RadialBasis {
+    int kind = kRBChebyshev;
+    double rmin = 0, rmax = 0, scaling = 0.01;
+    double b = 0;  // rb_b of the Poly4 / Poly5 envelopes
+};
+// Per-pair basis table on the device: kRbStride doubles per ordered species
+// pair {kind, min, max, scaling, mult, su, pu, pi / max, b, 1 / su}.
+constexpr int kRbStride = 10;
+
 // Host-side model: the linear MTP (potentials/potential_mtp.h:93) plus the
 // launch plan derived from its contraction graph.
 struct Model {
     int Z = 0, M = 0, R = 0, K = 0, B = 0, T = 0, S = 0;
+    // rmin / scaling of the first basis, rmax the largest cutoff of any pair
     double rmin = 0, rmax = 0, scaling = 0.01;
+    bool split = false;                // radial_basis_split: one basis per ordered pair
+    std::vector<RadialBasis> bases;    // [1] or [Z*Z]
+    MetaTag tag;
+    // true unless every pair uses the one shared RBChebyshev basis
+    bool general_basis() const { return split || (!bases.empty() && bases[0].kind != kRBChebyshev); }
+    const RadialBasis &pair_basis(int ti, int tj) const { return split ? bases[ti * Z + tj] : bases[0]; }
     std::vector<int> basic;   // [B][4]
     std::vector<int> times;   // [T][4]
     std::vector<int> map;     // [S]
@@ -91,8 +131,11 @@ struct Model {
     int ncoef() const { return nradial() + Z + S; }
 };
 
-// Parses .mtp text (PotMTP::Load grammar, non-split RBChebyshev).
+// Parses .mtp text (PotMTP::Load grammar).
 bool parse_mtp(const std::string &text, Model &m, std::string &err);
+// .mtp text of a model in PotMTP::Save layout (potentials/potential_mtp.cpp:
+// 647-785, 1052-1061).
+std::string save_mtp(const Model &m);
 // Validates sizes and index ranges of a model view.
 bool validate_model(const Model &m, std::string &err);
 
@@ -173,6 +216,11 @@ bool build_lin_plan(const Model &m, const Plan &p, LinPlan &lp, std::string &err
 struct DevModel {
     int Z, M, R, K, B, T, S, nslots;
     double rmin, rmax, scaling, mult, su, pu;
+    // general radial bases (split, or another kind than RBChebyshev): per
+    // ordered pair kRbStride doubles (RadialBasis); 0 and nullptr for the
+    // shared RBChebyshev basis of the scalar fields above
+    int rb_general;
+    const double *rb_table;
     int numax[kMaxMu];
     int numax_all;
     int ndup;

@@ -486,7 +486,7 @@ __global__ __launch_bounds__(kWave *kMaxWaves) void grad_kernel(DevModel m, DevN
             int tj;
             const bool valid = lane < n - base;
             const int64_t p = beg + base + lane;
-            const double win = load_geometry(m, nb, p, valid, q, tj);
+            const double win = load_geometry<P::M, !P::exact>(m, nb, p, valid, q, tj, ti);
             const GradNbr g = pair_weight<P>(nb, t, fi, S, p, valid, q);
             ctype[lane] = win != 0.0 ? tj : -1;
             double alpha[P::M], U[P::M];
@@ -495,7 +495,7 @@ __global__ __launch_bounds__(kWave *kMaxWaves) void grad_kernel(DevModel m, DevN
                 alpha[mu] = U[mu] = 0.0;
             rad_shells<0, P>(m, AG, q, g, nullptr, alpha, U);
             double Q[P::RMAX], dQ[P::RMAX];
-            chebyshev<P::RMAX>(m, q.d, Q, dQ);
+            radial_basis<P>(m, ti, tj, q.d, Q, dQ);
             int row = 0;
             auto flush = [&](int nrows) {
                 reduce_rows_typed(red4, nrows, row - nrows, lane, ctype, m.Z,

@@ -21,7 +21,8 @@ HEADER = os.path.join(ROOT, "include", "mtpx.h")
 OK = 0
 ERRORS = {-1: "MTPX_E_INVALID", -2: "MTPX_E_MODEL", -3: "MTPX_E_NO_MODEL",
           -4: "MTPX_E_NO_TOPOLOGY", -5: "MTPX_E_DEVICE", -6: "MTPX_E_ALLOC",
-          -7: "MTPX_E_CAPACITY", -8: "MTPX_E_RANGE"}
+          -7: "MTPX_E_CAPACITY", -8: "MTPX_E_RANGE", -9: "MTPX_E_SOLVER"}
+ERRORS_BY_NAME = {v: k for k, v in ERRORS.items()}
 
 _dp = C.POINTER(C.c_double)
 _ip = C.POINTER(C.c_int)
@@ -84,6 +85,17 @@ def lib():
         L.mtpx_orthogonalize.argtypes = [C.c_void_p]
         L.mtpx_last_linear_timings.argtypes = [C.c_void_p, _dp]
         L.mtpx_set_add_efs.argtypes = [C.c_void_p, C.c_int]
+        L.mtpx_lbfgs_default_params.argtypes = [C.POINTER(LbfgsParams)]
+        L.mtpx_lbfgs_default_params.restype = None
+        L.mtpx_train_lbfgs.argtypes = [C.c_void_p, C.POINTER(LbfgsParams), _dp, _dp, C.c_int,
+                                       C.c_double, C.c_double, C.c_double, _ip, _dp, _dp,
+                                       C.c_int, _ip]
+        L.mtpx_lbfgs_minimize.argtypes = [C.POINTER(LbfgsParams), C.c_int, _dp, LBFGS_OBJECTIVE,
+                                          C.c_void_p, _ip, _dp, _ip, C.c_char_p, C.c_int]
+        L.mtpx_save_model_text.argtypes = [C.c_void_p, C.c_char_p, C.c_size_t,
+                                           C.POINTER(C.c_size_t)]
+        L.mtpx_format_model_text.argtypes = [C.c_char_p, C.c_char_p, C.c_size_t,
+                                             C.POINTER(C.c_size_t), C.c_char_p, C.c_int]
         L.mtpx_efs_noalloc.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p]
         L.mtpx_compute_sites.argtypes = [C.c_void_p, C.POINTER(SiteRequest)]
         _lib = L
@@ -98,6 +110,60 @@ class SiteRequest(C.Structure):
                 ("x", _dp), ("force", _dp), ("total_energy", _dp), ("global_virial", _dp),
                 ("site_energy", _dp), ("site_virial", _dp), ("accumulate_force", C.c_int),
                 ("reuse_topology", C.c_int), ("deterministic", C.c_int)]
+
+
+class LbfgsParams(C.Structure):
+    """mtpx_lbfgs_params (LBFGSpp::LBFGSParam)."""
+    _fields_ = [("m", C.c_int), ("epsilon", C.c_double), ("epsilon_rel", C.c_double),
+                ("epsgmax", C.c_double), ("past", C.c_int), ("delta", C.c_double),
+                ("max_iterations", C.c_int), ("max_linesearch", C.c_int),
+                ("min_step", C.c_double), ("max_step", C.c_double), ("f_dec_coeff", C.c_double),
+                ("s_curv_coeff", C.c_double), ("max_step_move", C.c_double),
+                ("machine_prec", C.c_double), ("initial_step", C.c_double),
+                ("first_initial_step", C.c_double), ("unscale_iterate", C.c_int)]
+
+    @classmethod
+    def default(cls, **kw):
+        p = cls()
+        lib().mtpx_lbfgs_default_params(C.byref(p))
+        for k, v in kw.items():
+            setattr(p, k, v)
+        return p
+
+
+LBFGS_OBJECTIVE = C.CFUNCTYPE(C.c_int, C.c_void_p, C.POINTER(C.c_double),
+                              C.POINTER(C.c_double), C.c_int, C.POINTER(C.c_double))
+
+
+def lbfgs_minimize(fg, x0, params=None):
+    """mtpx_lbfgs_minimize over a Python objective fg(x) -> (f, grad); fg may
+    return a third value, the point to leave in the solver's iterate.
+    Returns (status, x, iterations, f, evaluations, message)."""
+    p = params if params is not None else LbfgsParams.default()
+    x = f64(x0).copy()
+    n = x.size
+
+    def cb(_user, xp, gp, nn, fp):
+        try:
+            xa = np.ctypeslib.as_array(xp, shape=(nn,))
+            res = fg(xa.copy())
+            f, g = res[0], res[1]
+            np.ctypeslib.as_array(gp, shape=(nn,))[:] = g
+            if len(res) > 2:
+                xa[:] = res[2]
+            fp[0] = f
+            return 0
+        except Exception:  # noqa: BLE001 -- reported to the solver as a status
+            return 1
+
+    cfn = LBFGS_OBJECTIVE(cb)
+    it = C.c_int()
+    ev = C.c_int()
+    fx = C.c_double()
+    msg = C.create_string_buffer(256)
+    rc = lib().mtpx_lbfgs_minimize(C.byref(p), n, _d(x), cfn, None, C.byref(it), C.byref(fx),
+                                   C.byref(ev), msg, 256)
+    return rc, x, it.value, fx.value, ev.value, msg.value.decode()
 
 
 class LossSettings(C.Structure):
@@ -129,6 +195,20 @@ def f64(a, shape=None):
 
 def i32(a):
     return np.ascontiguousarray(a, dtype=np.int32)
+
+
+def format_model_text(text: str) -> str:
+    """PotMTP::Load then PotMTP::Save on the host (mtpx_format_model_text)."""
+    n = C.c_size_t()
+    err = C.create_string_buffer(512)
+    rc = lib().mtpx_format_model_text(text.encode(), None, 0, C.byref(n), err, 512)
+    if rc != OK:
+        raise MtpxError(rc, err.value.decode())
+    buf = C.create_string_buffer(n.value + 1)
+    rc = lib().mtpx_format_model_text(text.encode(), buf, n.value + 1, C.byref(n), err, 512)
+    if rc != OK:
+        raise MtpxError(rc, err.value.decode())
+    return buf.value.decode()
 
 
 def version() -> str:
@@ -207,6 +287,14 @@ class Context:
         self._check(lib().mtpx_model_info(self.h, _i(info)), "model_info")
         self.info = dict(zip(["Z", "M", "R", "K", "B", "T", "S", "ncoef"], [int(v) for v in info]))
         return self.info
+
+    def save_model_text(self) -> str:
+        n = C.c_size_t()
+        self._check(lib().mtpx_save_model_text(self.h, None, 0, C.byref(n)), "save_model_text")
+        buf = C.create_string_buffer(n.value + 1)
+        self._check(lib().mtpx_save_model_text(self.h, buf, n.value + 1, C.byref(n)),
+                    "save_model_text")
+        return buf.value.decode()
 
     def get_coeffs(self) -> np.ndarray:
         x = np.zeros(self.info["ncoef"])
@@ -399,6 +487,32 @@ class Context:
         self._check(lib().mtpx_loss_grad(self.h, int(deterministic), penalty_weight, reg_l2,
                                          reg_l1, C.byref(loss), _d(g), _d(m)), "loss_grad")
         return loss.value, g, m
+
+    def train_lbfgs(self, params=None, scaling=None, x=None, deterministic=True,
+                    penalty_weight=0.0, reg_l2=0.0, reg_l1=0.0, history_cap=256,
+                    raise_on_error=True):
+        """Trainer_MTP::TrainNonLinearLBFGS: returns (iterations, loss,
+        objective values of the evaluations, evaluations, final iterate); with
+        raise_on_error False, (status, message) come first and a solver
+        failure returns what the run reached."""
+        p = params if params is not None else LbfgsParams.default()
+        sc = None if scaling is None else f64(scaling)
+        xv = f64(x).copy() if x is not None else np.zeros(self.info["ncoef"])
+        it = C.c_int()
+        ev = C.c_int()
+        loss = C.c_double()
+        hist = np.zeros(history_cap)
+        if x is None:
+            xv[:] = self.get_coeffs() * (1.0 if sc is None else sc)
+        rc = lib().mtpx_train_lbfgs(self.h, C.byref(p), _d(sc), _d(xv), int(bool(deterministic)),
+                                    penalty_weight, reg_l2, reg_l1, C.byref(it), C.byref(loss),
+                                    _d(hist), history_cap, C.byref(ev))
+        out = (it.value, loss.value, hist[:min(ev.value, history_cap)], ev.value, xv)
+        if raise_on_error:
+            self._check(rc, "train_lbfgs")
+            return out
+        msg = lib().mtpx_last_error(self.h).decode() if rc != OK else ""
+        return (rc, msg) + out
 
     def last_train_timings(self):
         t = np.zeros(4)

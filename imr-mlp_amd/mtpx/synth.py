@@ -149,16 +149,42 @@ def fmt(x: float) -> str:
     return "%.17e" % x
 
 
-def write_mtp(topo, Z, R, rmin, rmax, scaling, coeffs) -> str:
-    """PotMTP::Save layout (potentials/potential_mtp.cpp:647-785)."""
+BASIS_TYPES = ("RBChebyshev", "RBChebyCos", "RBChebyshevPoly4", "RBChebyshevPoly5")
+
+
+def basis_lines(kind: str, rmin: float, rmax: float, R: int, b: float = -1.0 / 3.0):
+    """AnyBasis::SaveToStream (basis/basis.h:50-56), plus rb_b for the
+    Poly4 / Poly5 bases (basis/basis.cpp:560-564, :733-737)."""
+    out = ["radial_basis_type = " + kind, "\tmin_dist = " + fmt(rmin),
+           "\tmax_dist = " + fmt(rmax), "\tradial_basis_size = %d" % R]
+    if kind in ("RBChebyshevPoly4", "RBChebyshevPoly5"):
+        out.append("\trb_b = " + fmt(b))
+    return out
+
+
+def write_mtp(topo, Z, R, rmin, rmax, scaling, coeffs, basis="RBChebyshev", pair_bases=None,
+              tag=None) -> str:
+    """PotMTP::Save layout (potentials/potential_mtp.cpp:647-785).  basis
+    names the shared radial basis; pair_bases, a list of Z*Z (kind, rmin,
+    rmax[, b]) in pair order, writes a split file (radial_basis_split = 1)
+    instead; tag is an optional potential_tag value."""
     M = topo["M"]
     nrad = Z * Z * M * R
     S = len(topo["map"])
     assert len(coeffs) == nrad + Z + S
     out = ["MTP", "version = 1.1.0", "potential_name = MTP1m", "scaling = " + fmt(scaling),
-           "species_count = %d" % Z, "radial_basis_type = RBChebyshev",
-           "\tmin_dist = " + fmt(rmin), "\tmax_dist = " + fmt(rmax),
-           "\tradial_basis_size = %d" % R, "radial_funcs_count = %d" % M, "radial_coeffs"]
+           "species_count = %d" % Z]
+    if tag is not None:
+        out.append("potential_tag = " + tag)
+    if pair_bases is None:
+        out += basis_lines(basis, rmin, rmax, R)
+    else:
+        assert len(pair_bases) == Z * Z
+        out.append("radial_basis_split = 1")
+        for q, pb in enumerate(pair_bases):
+            out.append("pair %d %d" % (q // Z, q % Z))
+            out += basis_lines(pb[0], pb[1], pb[2], R, *pb[3:])
+    out += ["radial_funcs_count = %d" % M, "radial_coeffs"]
     q = 0
     for i in range(Z):
         for j in range(Z):
@@ -181,10 +207,12 @@ def write_mtp(topo, Z, R, rmin, rmax, scaling, coeffs) -> str:
 
 
 def random_model(template: str, Z: int, R: int, rmin: float, rmax: float, lo: float, hi: float,
-                 rng, scaling: float = 0.01) -> str:
+                 rng, scaling: float = 0.01, **kw) -> str:
+    """A template's moment structure with U[lo, hi] coefficients; kw are
+    write_mtp's basis, pair_bases and tag."""
     topo = template_topology(read_template(template))
     n = Z * Z * topo["M"] * R + Z + len(topo["map"])
-    return write_mtp(topo, Z, R, rmin, rmax, scaling, uniform(rng, n, lo, hi))
+    return write_mtp(topo, Z, R, rmin, rmax, scaling, uniform(rng, n, lo, hi), **kw)
 
 
 # ------------------------------------------------------------ workloads --

@@ -31,6 +31,7 @@ extern "C" {
 #define MTPX_E_ALLOC -6       /* device or host allocation failed */
 #define MTPX_E_CAPACITY -7    /* size beyond a documented limit */
 #define MTPX_E_RANGE -8       /* neighbour image/box range not representable */
+#define MTPX_E_SOLVER -9      /* the L-BFGS solver stopped on an error (its text) */
 
 typedef struct mtpx_context mtpx_context;
 
@@ -69,13 +70,27 @@ const char *mtpx_version(void);
  * MTPGpuDirect::initialize(const MTPGpuPotentialView&)
  * (mtp_gpu_direct.h:800-806). */
 int mtpx_load_model(mtpx_context *ctx, const mtpx_model_view *view);
-/* PotMTP::Load (potentials/potential_mtp.cpp:119-571): .mtp text, non-split
- * RBChebyshev grammar, scaling defaulting to 0.01. */
+/* PotMTP::Load (potentials/potential_mtp.cpp:119-571): .mtp text with a
+ * shared radial basis or one per ordered species pair (radial_basis_split),
+ * of the kinds RBChebyshev, RBChebyCos, RBChebyshevPoly4 and
+ * RBChebyshevPoly5 (basis/basis.h:19-29); scaling defaults to 0.01; the
+ * potential_tag is read as the reference's metadata (a structured tag must
+ * declare a linear MTP). */
 int mtpx_load_model_text(mtpx_context *ctx, const char *text);
 /* Host-only parse of .mtp text (no device needed): sizes Z M R K B T S ncoef
  * into out8, the flat coefficients into coeffs (may be NULL), the first
  * error into err.  Same grammar and defaults as mtpx_load_model_text. */
 int mtpx_parse_model_text(const char *text, int out8[8], double *coeffs, char *err, int errlen);
+/* PotMTP::Save (potentials/potential_mtp.cpp:647-785, 1052-1061) of the
+ * loaded model with its current coefficients: the .mtp text, numbers in
+ * "%.17e", the potential_tag as the reference's metadata JSON.  buf may be
+ * NULL (only *len, the text length without the terminating 0, is set);
+ * otherwise cap must exceed that length (MTPX_E_CAPACITY if not). */
+int mtpx_save_model_text(const mtpx_context *ctx, char *buf, size_t cap, size_t *len);
+/* Host-only PotMTP::Load then PotMTP::Save of .mtp text (no device needed);
+ * buf / cap / len as mtpx_save_model_text, the parse error into err. */
+int mtpx_format_model_text(const char *text, char *buf, size_t cap, size_t *len, char *err,
+                           int errlen);
 /* Sizes: Z M R K B T S ncoef (ncoef = Z*Z*M*R + Z + S). */
 int mtpx_model_info(const mtpx_context *ctx, int out8[8]);
 /* PotMTP::get_coeffs / set_coeffs (potential_mtp.cpp:4160-4245) in the flat
@@ -278,6 +293,63 @@ int mtpx_penalty(const mtpx_context *ctx, double weight, double reg_l2, double r
  * mtpx_prepare_loss (may be NULL). */
 int mtpx_loss_grad(mtpx_context *ctx, int deterministic, double penalty_weight, double reg_l2,
                    double reg_l1, double *loss, double *grad, double metrics[7]);
+/* LBFGSpp::LBFGSParam of the trainer's L-BFGS (deplibs/LBFGSpp/include/
+ * LBFGSpp/Param.h:99-243), the fields the Lewis-Overton line search reads;
+ * the trainer's options lbfgspp:* (train/train_mtp.cpp:59,144-163) set them. */
+typedef struct mtpx_lbfgs_params {
+    int m;                     /* corrections kept (6) */
+    double epsilon;            /* stop when |g| <= epsilon (1e-5) */
+    double epsilon_rel;        /* ... or |g| <= epsilon_rel |x| (1e-5) */
+    double epsgmax;            /* ... or max |g_i| <= epsgmax (0) */
+    int past;                  /* relative-decrease test over `past` iterations (0: off) */
+    double delta;              /* its tolerance (0) */
+    int max_iterations;        /* 0: no limit */
+    int max_linesearch;        /* evaluations per line search (20) */
+    double min_step, max_step; /* 1e-20, 1e20 */
+    double f_dec_coeff;        /* sufficient decrease (1e-4) */
+    double s_curv_coeff;       /* curvature (0.9) */
+    double max_step_move;      /* largest move of one coordinate (1e20) */
+    double machine_prec;       /* bracket width limit (1e-16) */
+    double initial_step;       /* step of later iterations; < 0: 1 */
+    double first_initial_step; /* first step; < 0: 1 / |g| */
+    /* mtpx_train_lbfgs only.  1 (the trainer's behaviour): every evaluation
+     * leaves the solver's iterate at the coefficients x / scaling, because
+     * Trainer_MTP::operator() divides the vector it is given -- the solver's
+     * own iterate -- in place (train_mtp.cpp:4260-4264, 4336).  0: the
+     * iterate stays in the scaled coordinates. */
+    int unscale_iterate;
+} mtpx_lbfgs_params;
+/* The LBFGSParam defaults of the reference's vendored LBFGSpp, with the
+ * trainer's epsgmax = 0 (train_mtp.cpp:59) and unscale_iterate = 1. */
+void mtpx_lbfgs_default_params(mtpx_lbfgs_params *p);
+/* The objective of mtpx_lbfgs_minimize: writes f(x) to *f and its gradient to
+ * grad[n]; may overwrite x, as the trainer's objective does.  A nonzero
+ * return stops the solver with MTPX_E_INVALID. */
+typedef int (*mtpx_lbfgs_objective)(void *user, double *x, double *grad, int n, double *f);
+/* LBFGSSolver<double, LineSearchLewisOverton>::minimize (deplibs/LBFGSpp/
+ * include/LBFGS.h:81-190, LBFGSpp/LineSearchLewisOverton.h:47-133) over a
+ * caller's objective; host only.  x [n]: in, the starting point; out, the
+ * final iterate.  iterations, fx, evaluations and message may be NULL.  The
+ * solver's exceptions (bad parameters, "exceed max linesearch", "width too
+ * small", "inf or nan", ...) return MTPX_E_INVALID (parameters, objective
+ * status) or MTPX_E_SOLVER with LBFGSpp's text in message[message_cap]. */
+int mtpx_lbfgs_minimize(const mtpx_lbfgs_params *params, int n, double *x,
+                        mtpx_lbfgs_objective objective, void *user, int *iterations, double *fx,
+                        int *evaluations, char *message, int message_cap);
+/* Trainer_MTP::TrainNonLinearLBFGS (train/train_mtp.cpp:4300-4339): the
+ * solver above over Trainer_MTP::operator() (:4256-4295) -- coefficients
+ * x / scaling, the objective and gradient of mtpx_loss_grad on the resident
+ * batch and labels, the gradient times scaling.  scaling [ncoef] or NULL for
+ * ones.  x [ncoef] (Trainer_MTP::x_in) or NULL: in, the starting point in
+ * scaled coordinates (NULL: the context's coefficients times scaling); out,
+ * the final iterate.  The context keeps the coefficients of the last
+ * evaluation.  iterations, loss (the last objective value), history (the
+ * objective of the first history_cap evaluations) and evaluations may be
+ * NULL.  A failed line search returns MTPX_E_SOLVER with the solver's text. */
+int mtpx_train_lbfgs(mtpx_context *ctx, const mtpx_lbfgs_params *params, const double *scaling,
+                     double *x, int deterministic, double penalty_weight, double reg_l2,
+                     double reg_l1, int *iterations, double *loss, double *history,
+                     int history_cap, int *evaluations);
 /* Device-side timing of the last mtpx_loss_grad, milliseconds:
  * {whole call, E/F/S, loss, gradient}. */
 int mtpx_last_train_timings(const mtpx_context *ctx, double out_ms[4]);

@@ -148,7 +148,65 @@ void orc_model_free(orc_model *m)
     free(m->map);
     free(m->nu);
     free(m->coef);
+    free(m->bases);
+    free(m->tag);
     free(m);
+}
+
+/* basis_name_to_code (basis/basis.cpp:10-27), the four types restated here */
+static int basis_code(const char *name)
+{
+    if (strcmp(name, "RBChebyshev") == 0)
+        return 0;
+    if (strcmp(name, "RBChebyCos") == 0)
+        return 1;
+    if (strcmp(name, "RBChebyshevPoly4") == 0)
+        return 2;
+    if (strcmp(name, "RBChebyshevPoly5") == 0)
+        return 3;
+    return -1;
+}
+static const char *basis_name(int code)
+{
+    static const char *names[] = {"RBChebyshev", "RBChebyCos", "RBChebyshevPoly4",
+                                  "RBChebyshevPoly5"};
+    return names[code];
+}
+
+/* AnyBasis::LoadFromStream (basis/basis.cpp:73-117) and, for Poly4/Poly5,
+ * the rb_b line of their LoadFromStream (:543-558, :716-731).  0 on success,
+ * else an error message. */
+static const char *load_basis(rd_t *r, int code, double scaling, orc_basis *b)
+{
+    char tok[256];
+    b->type = code;
+    b->scaling = scaling;
+    b->b = 0;
+    rd_word(r, tok, sizeof tok);
+    if (strcmp(tok, "min_dist") != 0)
+        return "Error in loading basis: min_dist";
+    rd_ignore(r, 2);
+    b->rmin = rd_double(r);
+    rd_word(r, tok, sizeof tok);
+    if (strcmp(tok, "max_dist") != 0)
+        return "Error in loading basis: max_dist";
+    rd_ignore(r, 2);
+    b->rmax = rd_double(r);
+    return 0;
+}
+static const char *load_basis_tail(rd_t *r, orc_basis *b)
+{
+    char tok[256];
+    if (b->type == 2 || b->type == 3) {
+        rd_word(r, tok, sizeof tok);
+        if (strcmp(tok, "rb_b") != 0)
+            return "Error in loading basis: rb_b";
+        rd_ignore(r, 2);
+        b->b = rd_double(r);
+        if (r->fail)
+            return "Error in loading basis: rb_b";
+    }
+    return 0;
 }
 
 #define LOAD_FAIL(msg)                                                                     \
@@ -190,44 +248,133 @@ orc_model *orc_model_load_text(const char *text, char *err, int errlen)
     if (r.fail || m->Z <= 0)
         LOAD_FAIL("Error reading .mtp file, invalid species_count");
 
-    rd_word(&r, tok, sizeof tok); /* :171-187, metadata is carried, not interpreted */
+    rd_word(&r, tok, sizeof tok); /* :171-187 */
+    m->tag = (char *)calloc(1, 1);
     if (strcmp(tok, "potential_tag") == 0) {
-        rd_line(&r, line, sizeof line);
-        if (!strchr(line, '='))
+        const char *nl = strchr(r.p, '\n');
+        size_t len = nl ? (size_t)(nl - r.p) : strlen(r.p);
+        char *raw = (char *)malloc(len + 1);
+        memcpy(raw, r.p, len);
+        raw[len] = 0;
+        r.p += len + (nl ? 1 : 0);
+        char *eq = strchr(raw, '=');
+        if (!eq) {
+            free(raw);
             LOAD_FAIL("Invalid potential_tag assignment");
+        }
+        /* MTPMetadata::Tag::parse trims the text after '=' (tools/mtp_metadata.h:208-212) */
+        char *b0 = eq + 1, *e0 = raw + len;
+        while (*b0 && strchr(" \t\r\n", *b0))
+            ++b0;
+        while (e0 > b0 && strchr(" \t\r\n", e0[-1]))
+            --e0;
+        free(m->tag);
+        m->tag = (char *)malloc((size_t)(e0 - b0) + 1);
+        memcpy(m->tag, b0, (size_t)(e0 - b0));
+        m->tag[e0 - b0] = 0;
+        free(raw);
+        if (m->tag[0] != '{' && strstr(m->tag, "imrmlp_meta_v"))
+            LOAD_FAIL("imrmlp_meta_v1 potential tags are not supported");
         rd_word(&r, tok, sizeof tok);
     }
+    m->split = 0;
     if (strcmp(tok, "radial_split") == 0 || strcmp(tok, "radial_basis_split") == 0) {
         rd_ignore(&r, 2); /* :190-204 */
-        int split = rd_int(&r);
-        if (split)
-            LOAD_FAIL("split radial bases are not supported");
-        rd_word(&r, tok, sizeof tok);
+        m->split = rd_int(&r) != 0;
+        if (!m->split)
+            rd_word(&r, tok, sizeof tok);
     }
-    if (strcmp(tok, "radial_basis_type") != 0) /* :267-272 */
-        LOAD_FAIL("Error reading .mtp file");
-    rd_ignore(&r, 2);
-    rd_word(&r, tok, sizeof tok);
-    if (strcmp(tok, "RBChebyshev") != 0)
-        LOAD_FAIL("only RBChebyshev radial bases are supported");
-    /* AnyBasis::LoadFromStream, basis/basis.cpp:73-117 */
-    rd_word(&r, tok, sizeof tok);
-    if (strcmp(tok, "min_dist") != 0)
-        LOAD_FAIL("Error in loading basis: min_dist");
-    rd_ignore(&r, 2);
-    m->rmin = rd_double(&r);
-    rd_word(&r, tok, sizeof tok);
-    if (strcmp(tok, "max_dist") != 0)
-        LOAD_FAIL("Error in loading basis: max_dist");
-    rd_ignore(&r, 2);
-    m->rmax = rd_double(&r);
-    rd_word(&r, tok, sizeof tok);
-    if (strcmp(tok, "radial_basis_size") != 0)
-        LOAD_FAIL("Error in loading basis: radial_basis_size");
-    rd_ignore(&r, 2);
-    m->R = rd_int(&r);
-    if (r.fail || m->R <= 0)
-        LOAD_FAIL("Error in loading basis: radial_basis_size must be positive");
+    const char *berr = 0;
+    if (m->split) { /* :206-265: one basis per ordered species pair */
+        const int P = m->Z * m->Z;
+        m->bases = (orc_basis *)calloc((size_t)P, sizeof(orc_basis));
+        char *seen = (char *)calloc((size_t)P, 1);
+        int rb_last = 0;
+        m->cutoff = 0;
+        for (int q = 0; q < P; ++q) {
+            rd_word(&r, tok, sizeof tok);
+            if (strcmp(tok, "pair") != 0) {
+                free(seen);
+                LOAD_FAIL("Error reading .mtp file, incorrect pair setting");
+            }
+            int ci = rd_int(&r), cj = rd_int(&r);
+            if (r.fail || ci < 0 || ci >= m->Z || cj < 0 || cj >= m->Z) {
+                free(seen);
+                LOAD_FAIL("Error reading .mtp file, invalid radial basis pair");
+            }
+            if (seen[ci * m->Z + cj]) {
+                free(seen);
+                LOAD_FAIL("Error reading .mtp file, duplicate radial basis pair");
+            }
+            seen[ci * m->Z + cj] = 1;
+            rd_word(&r, tok, sizeof tok);
+            if (strcmp(tok, "radial_basis_type") != 0) {
+                free(seen);
+                LOAD_FAIL("Error reading .mtp file, incorrect pair setting");
+            }
+            rd_ignore(&r, 2);
+            rd_word(&r, tok, sizeof tok);
+            const int code = basis_code(tok);
+            if (code < 0) {
+                free(seen);
+                LOAD_FAIL("unsupported radial basis type");
+            }
+            orc_basis *bb = &m->bases[ci * m->Z + cj];
+            berr = load_basis(&r, code, scaling, bb);
+            int size = 0;
+            if (!berr) {
+                rd_word(&r, tok, sizeof tok);
+                if (strcmp(tok, "radial_basis_size") != 0)
+                    berr = "Error in loading basis: radial_basis_size";
+                rd_ignore(&r, 2);
+                size = rd_int(&r);
+                if (!berr && (r.fail || size <= 0))
+                    berr = "Error in loading basis: radial_basis_size must be positive";
+            }
+            if (!berr)
+                berr = load_basis_tail(&r, bb);
+            if (berr) {
+                free(seen);
+                LOAD_FAIL(berr);
+            }
+            if (rb_last == 0)
+                rb_last = size;
+            else if (size != rb_last) {
+                free(seen);
+                LOAD_FAIL("Error reading .mtp file, split radial bases must have the same "
+                          "radial_basis_size");
+            }
+            if (m->cutoff < bb->rmax)
+                m->cutoff = bb->rmax;
+        }
+        free(seen);
+        m->R = rb_last;
+    } else {
+        if (strcmp(tok, "radial_basis_type") != 0) /* :267-272 */
+            LOAD_FAIL("Error reading .mtp file");
+        rd_ignore(&r, 2);
+        rd_word(&r, tok, sizeof tok);
+        const int code = basis_code(tok);
+        if (code < 0)
+            LOAD_FAIL("unsupported radial basis type");
+        m->bases = (orc_basis *)calloc(1, sizeof(orc_basis));
+        berr = load_basis(&r, code, scaling, m->bases);
+        if (berr)
+            LOAD_FAIL(berr);
+        rd_word(&r, tok, sizeof tok);
+        if (strcmp(tok, "radial_basis_size") != 0)
+            LOAD_FAIL("Error in loading basis: radial_basis_size");
+        rd_ignore(&r, 2);
+        m->R = rd_int(&r);
+        if (r.fail || m->R <= 0)
+            LOAD_FAIL("Error in loading basis: radial_basis_size must be positive");
+        berr = load_basis_tail(&r, m->bases);
+        if (berr)
+            LOAD_FAIL(berr);
+        m->cutoff = m->bases[0].rmax;
+    }
+    m->rmin = m->bases[0].rmin;
+    m->rmax = m->cutoff;
     m->scaling = scaling;
 
     rd_word(&r, tok, sizeof tok); /* :291-297 */
@@ -463,8 +610,53 @@ void orc_model_tables(const orc_model *m, int *basic, int *times, int *map, doub
 /* PotMTP::write_header / write_radial_info / write_radial_coeff / write_rules /
  * write_linear_coeff (potentials/potential_mtp.cpp:647-785), scientific
  * notation with max_digits10 (17) significant digits. */
+/* picojson's serialize_str (tools/picojson.h:484-519): the escapes of a JSON
+ * string as the reference's metadata writer emits them. */
+static size_t json_escape(const char *in, char *out)
+{
+    size_t k = 0;
+    out[k++] = '"';
+    for (const unsigned char *c = (const unsigned char *)in; *c; ++c) {
+        const char *rep = 0;
+        switch (*c) {
+        case '"': rep = "\\\""; break;
+        case '\\': rep = "\\\\"; break;
+        case '/': rep = "\\/"; break;
+        case '\b': rep = "\\b"; break;
+        case '\f': rep = "\\f"; break;
+        case '\n': rep = "\\n"; break;
+        case '\r': rep = "\\r"; break;
+        case '\t': rep = "\\t"; break;
+        default: break;
+        }
+        if (rep) {
+            memcpy(out + k, rep, strlen(rep));
+            k += strlen(rep);
+        } else if (*c < 0x20 || *c == 0x7f) {
+            k += (size_t)sprintf(out + k, "\\u%04x", *c & 0xff);
+        } else {
+            out[k++] = (char)*c;
+        }
+    }
+    out[k++] = '"';
+    out[k] = 0;
+    return k;
+}
+
+/* PotMTP::Save (potentials/potential_mtp.cpp:1052-1061): write_header
+ * (:656-671), write_radial_info (:673-690, AnyBasis::SaveToStream
+ * basis/basis.h:50-56 and the rb_b line of Poly4/Poly5, basis.cpp:560-564,
+ * :733-737), write_radial_coeff (:692-714), write_rules (:716-752),
+ * write_linear_coeff (:754-785), on a stream set to std::scientific with
+ * max_digits10 = 17 digits (printf "%.17e").  The potential_tag line is
+ * MTPMetadata::Tag::output(model_metadata()) serialised
+ * (tools/mtp_metadata.h:353-370): this restatement covers an absent tag and
+ * a plain-text (legacy) tag, kept as "legacy_tag"; it returns -1 for a tag
+ * in JSON form. */
 int orc_model_save_text(const orc_model *m, char *buf, int buflen)
 {
+    if (m->tag[0] == '{')
+        return -1;
     size_t cap = 1 << 16, len = 0;
     char *out = (char *)malloc(cap);
 #define EMIT(...)                                                                          \
@@ -478,11 +670,31 @@ int orc_model_save_text(const orc_model *m, char *buf, int buflen)
         len += (size_t)need_;                                                              \
     } while (0)
     EMIT("MTP\nversion = 1.1.0\npotential_name = MTP1m\n");
-    EMIT("scaling = %.16e\n", m->scaling);
+    EMIT("scaling = %.17e\n", m->scaling);
     EMIT("species_count = %d\n", m->Z);
-    EMIT("radial_basis_type = RBChebyshev\n");
-    EMIT("\tmin_dist = %.16e\n\tmax_dist = %.16e\n\tradial_basis_size = %d\n", m->rmin, m->rmax,
-         m->R);
+    if (m->tag[0]) {
+        char *esc = (char *)malloc(6 * strlen(m->tag) + 3);
+        json_escape(m->tag, esc);
+        EMIT("potential_tag = {\"legacy_tag\":%s,\"model\":\"linear\",\"schema\":\"gpml.mtp.metadata\","
+             "\"type\":\"MTP\",\"version\":1}\n", esc);
+        free(esc);
+    } else {
+        EMIT("potential_tag = {\"model\":\"linear\",\"schema\":\"gpml.mtp.metadata\","
+             "\"type\":\"MTP\",\"version\":1}\n");
+    }
+    if (m->split)
+        EMIT("radial_basis_split = 1\n");
+    const int nb = m->split ? m->Z * m->Z : 1;
+    for (int q = 0; q < nb; ++q) {
+        const orc_basis *bb = &m->bases[q];
+        if (m->split)
+            EMIT("pair %d %d\n", q / m->Z, q % m->Z);
+        EMIT("radial_basis_type = %s\n", basis_name(bb->type));
+        EMIT("\tmin_dist = %.17e\n\tmax_dist = %.17e\n\tradial_basis_size = %d\n", bb->rmin,
+             bb->rmax, m->R);
+        if (bb->type == 2 || bb->type == 3)
+            EMIT("\trb_b = %.17e\n", bb->b);
+    }
     EMIT("radial_funcs_count = %d\n", m->M);
     EMIT("radial_coeffs\n");
     int q = 0;
@@ -491,8 +703,8 @@ int orc_model_save_text(const orc_model *m, char *buf, int buflen)
             EMIT("\t%d-%d\n", i, j);
             for (int k = 0; k < m->M; ++k) {
                 EMIT("\t\t{");
-                for (int l = 0; l < m->R; ++l)
-                    EMIT("%.16e%s", m->coef[q++], l != m->R - 1 ? ", " : "}\n");
+                for (int l = 0; l < m->R; ++l, ++q)  /* EMIT evaluates its arguments twice */
+                    EMIT("%.17e%s", m->coef[q], l != m->R - 1 ? ", " : "}\n");
             }
         }
     EMIT("alpha_moments_count = %d\n", m->K);
@@ -515,11 +727,11 @@ int orc_model_save_text(const orc_model *m, char *buf, int buflen)
     EMIT("}\n");
     EMIT("species_coeffs = {");
     for (int i = 0; i < m->Z; ++i)
-        EMIT("%s%.16e", i ? ", " : "", m->coef[m->nradial + i]);
+        EMIT("%s%.17e", i ? ", " : "", m->coef[m->nradial + i]);
     EMIT("}\n");
     EMIT("moment_coeffs = {");
     for (int i = 0; i < m->S; ++i)
-        EMIT("%s%.16e", i ? ", " : "", m->coef[m->nradial + m->Z + i]);
+        EMIT("%s%.17e", i ? ", " : "", m->coef[m->nradial + m->Z + i]);
     EMIT("}\n");
 #undef EMIT
     int ret = (int)len;
@@ -578,26 +790,97 @@ void orc_orthogonalize(orc_model *m)
 }
 
 /* ======================================================================
- * RBasis_Chebyshev::calc_der (basis/basis.cpp:119-164)
+ * Radial bases, calc_der of basis/basis.cpp: RBasis_Chebyshev (:119-164,
+ * setup :119-125), RBasis_ChebyCos (:242-271, setup :228-235),
+ * RBasis_ChebyshevPoly4 (:585-619, setup :533-540) and
+ * RBasis_ChebyshevPoly5 (:776-805, setup :706-713).
  * ====================================================================== */
+/* ksi = (2 r - (min + max)) / (max - min), the Chebyshev argument of all four */
+static double ksi_of(const orc_basis *bs, double value)
+{
+    return (2 * value - (bs->rmax + bs->rmin)) / (bs->rmax - bs->rmin);
+}
+
+static void basis_calc_der(const orc_basis *bs, int R, double value, double *val, double *der)
+{
+    const double min_val = bs->rmin, max_val = bs->rmax, scaling = bs->scaling;
+    const double mult = 2.0 / (max_val - min_val);
+    const double su = max_val - min_val;
+    const double pu = max_val + min_val;
+    if (bs->type == 0) {
+        double ksi = (2 * value - pu) / su;
+        double ru = value - max_val;
+        val[0] = scaling * (1 * ru * ru);
+        der[0] = scaling * (0 * ru * ru + 2 * ru);
+        if (R == 1)
+            return;
+        val[1] = scaling * (ksi * ru * ru);
+        der[1] = scaling * (mult * ru * ru + 2 * ksi * ru);
+    } else if (bs->type == 1) {
+        const double irpi = M_PI / max_val;
+        double ksi = (2 * value - pu) / su;
+        double rc = 0.5 * (1.0 + cos(value * irpi));
+        double drc = -0.5 * irpi * sin(value * irpi);
+        val[0] = scaling * (1 * rc);
+        der[0] = scaling * (0 * rc + drc);
+        if (R == 1)
+            return;
+        val[1] = scaling * (ksi * rc);
+        der[1] = scaling * (mult * rc + ksi * drc);
+    } else {
+        if (value < min_val || value > max_val) {
+            for (int i = 0; i < R; i++)
+                val[i] = der[i] = 0;
+            return;
+        }
+        const double dxdr = 1.0 / su;
+        double ksi = (2 * value - pu) / su;
+        double x = (value - min_val) / su;
+        double vx = 1.0 - x;
+        double vxx = vx * vx;
+        double vxxx = vxx * vx;
+        double rc, drc;
+        if (bs->type == 2) {
+            rc = vxxx * (1 + (3 + bs->b) * x);
+            drc = vxx * (bs->b * (1. - 4.0 * x) - 12.0 * x) * dxdr;
+        } else {
+            double vxxxx = vxx * vxx;
+            rc = vxxxx * (1 + (4 + bs->b) * x);
+            drc = -vxxx * (20 * x + bs->b * (5 * x - 1)) * dxdr;
+        }
+        val[0] = scaling * rc;
+        der[0] = scaling * drc;
+        if (R == 1)
+            return;
+        val[1] = scaling * (ksi * rc);
+        der[1] = scaling * (mult * rc + ksi * drc);
+    }
+    for (int i = 2; i < R; i++) {
+        val[i] = 2 * ksi_of(bs, value) * val[i - 1] - val[i - 2];
+        der[i] = 2 * (mult * val[i - 1] + ksi_of(bs, value) * der[i - 1]) - der[i - 2];
+    }
+}
+
+/* the shared basis, or the pair's own (PotMTP::rb_calcder(itype, jtype, r)) */
+static const orc_basis *pair_basis(const orc_model *m, int ti, int tj)
+{
+    return m->split ? &m->bases[ti * m->Z + tj] : &m->bases[0];
+}
+/* cutoffs(itype, jtype) of the site loop (potential_mtp.cpp:2842) */
+static double pair_cutoff(const orc_model *m, int ti, int tj)
+{
+    return pair_basis(m, ti, tj)->rmax;
+}
+
 void orc_rb_calc_der(const orc_model *m, double value, double *val, double *der)
 {
-    const double mult = 2.0 / (m->rmax - m->rmin);
-    const double su = m->rmax - m->rmin;
-    const double pu = m->rmax + m->rmin;
-    const double s = m->scaling;
-    double ksi = (2 * value - pu) / su;
-    double ru = value - m->rmax;
-    val[0] = s * (1 * ru * ru);
-    der[0] = s * (0 * ru * ru + 2 * ru);
-    if (m->R == 1)
-        return;
-    val[1] = s * (ksi * ru * ru);
-    der[1] = s * (mult * ru * ru + 2 * ksi * ru);
-    for (int i = 2; i < m->R; i++) {
-        val[i] = 2 * ksi * val[i - 1] - val[i - 2];
-        der[i] = 2 * (mult * val[i - 1] + ksi * der[i - 1]) - der[i - 2];
-    }
+    basis_calc_der(&m->bases[0], m->R, value, val, der);
+}
+
+void orc_rb_calc_der_pair(const orc_model *m, int ti, int tj, double value, double *val,
+                          double *der)
+{
+    basis_calc_der(pair_basis(m, ti, tj), m->R, value, val, der);
 }
 
 /* ======================================================================
@@ -1142,10 +1425,10 @@ static void site_descriptors(const orc_model *m, const orc_nbh *h, int i, ws_t *
         const double rij = h->dist[off + jj];
         const int jtype = h->types[off + jj];
         const double *pos = h->vec + 3 * (size_t)(off + jj);
-        if (rij > m->rmax) /* :2842, r == cutoff is kept */
+        if (rij > pair_cutoff(m, itype, jtype)) /* :2842, r == cutoff is kept */
             continue;
         const double rijinv = 1.0 / rij;
-        orc_rb_calc_der(m, rij, w->rv, w->rd);
+        orc_rb_calc_der_pair(m, itype, jtype, rij, w->rv, w->rd);
         w->dp[0] = 1;
         for (int k = 1; k < m->max_nu1; ++k) {
             w->dp[k] = w->dp[k - 1] * rijinv;
@@ -1404,10 +1687,10 @@ static void site_parameter_gradient(const orc_model *m, const orc_nbh *h, int i,
         const double rij = h->dist[off + jj];
         const int jtype = h->types[off + jj];
         const double *pos = h->vec + 3 * (size_t)(off + jj);
-        if (rij > m->rmax)
+        if (rij > pair_cutoff(m, itype, jtype))
             continue;
         const double rijinv = 1.0 / rij;
-        orc_rb_calc_der(m, rij, w->rv, w->rd);
+        orc_rb_calc_der_pair(m, itype, jtype, rij, w->rv, w->rd);
         w->dp[0] = 1;
         for (int k = 1; k < m->max_nu1; ++k) {
             w->dp[k] = w->dp[k - 1] * rijinv;
@@ -1799,10 +2082,10 @@ static void site_basis_ders(const orc_model *m, const orc_nbh *h, int i, ws_t *w
         const double rij = h->dist[off + jj];
         const int jtype = h->types[off + jj];
         const double *pos = h->vec + 3 * (size_t)(off + jj);
-        if (rij > m->rmax)
+        if (rij > pair_cutoff(m, itype, jtype))
             continue;
         const double rijinv = 1.0 / rij;
-        orc_rb_calc_der(m, rij, w->rv, w->rd);
+        orc_rb_calc_der_pair(m, itype, jtype, rij, w->rv, w->rd);
         w->dp[0] = 1;
         for (int k = 1; k < m->max_nu1; ++k) {
             w->dp[k] = w->dp[k - 1] * rijinv;

@@ -18,11 +18,24 @@
 extern "C" {
 #endif
 
-/* Linear MTP with an RBChebyshev radial basis (potentials/potential_mtp.h:93,
- * coefficient layout potentials/potential_mtp.h:170-176). */
+/* One radial basis (basis/basis.h:104-278): RBChebyshev (0), RBChebyCos (1),
+ * RBChebyshevPoly4 (2), RBChebyshevPoly5 (3). */
+typedef struct orc_basis {
+    int type;
+    double rmin, rmax, scaling;   /* min_val, max_val, scaling */
+    double b;                     /* rb_b of the Poly4/Poly5 bases */
+} orc_basis;
+
+/* Linear MTP (potentials/potential_mtp.h:93, coefficient layout
+ * potentials/potential_mtp.h:170-176); one shared radial basis, or one per
+ * ordered species pair when split (potential_mtp.cpp:188-265). */
 typedef struct orc_model {
     int Z, M, R;                  /* species_count, radial_funcs_count, rb_size */
-    double rmin, rmax, scaling;   /* min_dist, max_dist, scaling */
+    double rmin, rmax, scaling;   /* the first basis; rmax is replaced by the cutoff below */
+    double cutoff;                /* max over the pair bases of max_dist */
+    int split;                    /* radial_basis_split */
+    orc_basis *bases;             /* [1] or [Z*Z] (pair ti * Z + tj) */
+    char *tag;                    /* potential_tag text after '=', trimmed ("" if none) */
     int K, B, T, S;               /* alpha_moments_count, basic, times, scalar moments */
     int *basic;                   /* [B][4] {mu, a, b, c} */
     int *times;                   /* [T][4] {l, r, c, out} */
@@ -80,6 +93,8 @@ void orc_orthogonalize(orc_model *m);
 
 /* ---- radial basis --------------------------------------------------- */
 void orc_rb_calc_der(const orc_model *m, double r, double *val, double *der);
+void orc_rb_calc_der_pair(const orc_model *m, int ti, int tj, double r, double *val,
+                          double *der);
 
 /* ---- structures and neighbours -------------------------------------- */
 void orc_wrap(const double *cell, const int *pbc, int n, double *pos);

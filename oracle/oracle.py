@@ -30,6 +30,16 @@ def build(force: bool = False) -> None:
         subprocess.run(["make", "-C", HERE, "-B" if force else "-s", "liboracle.so"], check=True)
 
 
+def use_library(path: str) -> None:
+    """Load the oracle from another build of the same source (the timing
+    build of the CPU baseline, `make -C oracle fast`); call before any other
+    oracle function."""
+    global LIB_PATH, _lib
+    if _lib is not None and LIB_PATH != path:
+        raise RuntimeError("oracle library already loaded from " + LIB_PATH)
+    LIB_PATH = path
+
+
 def lib():
     global _lib
     if _lib is None:
@@ -47,6 +57,7 @@ def lib():
         L.orc_model_save_text.argtypes = [C.c_void_p, C.c_char_p, C.c_int]
         L.orc_orthogonalize.argtypes = [C.c_void_p]
         L.orc_rb_calc_der.argtypes = [C.c_void_p, C.c_double, _dp, _dp]
+        L.orc_rb_calc_der_pair.argtypes = [C.c_void_p, C.c_int, C.c_int, C.c_double, _dp, _dp]
         L.orc_wrap.argtypes = [_dp, _ip, C.c_int, _dp]
         L.orc_cell_inverse.argtypes = [_dp, _dp]
         L.orc_build_neighbors.restype = C.c_void_p
@@ -194,7 +205,10 @@ class Model:
         return basic[:self.B], times[:self.T], mp[:self.S], rb
 
     def save_text(self) -> str:
+        """PotMTP::Save text (a JSON potential_tag is not restated: ValueError)."""
         n = lib().orc_model_save_text(self.h, None, 0)
+        if n < 0:
+            raise ValueError("the oracle does not restate JSON potential tags")
         buf = C.create_string_buffer(n + 1)
         lib().orc_model_save_text(self.h, buf, n + 1)
         return buf.value.decode()
@@ -202,10 +216,15 @@ class Model:
     def orthogonalize(self):
         lib().orc_orthogonalize(self.h)
 
-    def rb_calc_der(self, r: float):
+    def rb_calc_der(self, r: float, ti: int | None = None, tj: int | None = None):
+        """Radial basis values and derivatives at r: the shared basis, or the
+        basis of the ordered species pair (ti, tj)."""
         v = np.zeros(self.R)
         d = np.zeros(self.R)
-        lib().orc_rb_calc_der(self.h, float(r), _d(v), _d(d))
+        if ti is None:
+            lib().orc_rb_calc_der(self.h, float(r), _d(v), _d(d))
+        else:
+            lib().orc_rb_calc_der_pair(self.h, int(ti), int(tj), float(r), _d(v), _d(d))
         return v, d
 
     @property
@@ -469,3 +488,73 @@ def ref_mlip_efs(model_text, nb: Neighbors, point_types, cutoff, workdir, Z):
     raw = np.frombuffer(open(fout, "rb").read(), np.float64)
     n = nb.n
     return raw[0], raw[1:1 + n], raw[1 + n:1 + 4 * n].reshape(n, 3), raw[1 + 4 * n:7 + 4 * n]
+
+
+class RefLbfgsParams(C.Structure):
+    """The parameter block of oracle/_ref/liblbfgs_ref.so (LBFGSpp::LBFGSParam
+    fields of the Lewis-Overton solver)."""
+    _fields_ = [("m", C.c_int), ("epsilon", C.c_double), ("epsilon_rel", C.c_double),
+                ("epsgmax", C.c_double), ("past", C.c_int), ("delta", C.c_double),
+                ("max_iterations", C.c_int), ("max_linesearch", C.c_int),
+                ("min_step", C.c_double), ("max_step", C.c_double), ("f_dec_coeff", C.c_double),
+                ("s_curv_coeff", C.c_double), ("max_step_move", C.c_double),
+                ("machine_prec", C.c_double), ("initial_step", C.c_double),
+                ("first_initial_step", C.c_double), ("unscale_iterate", C.c_int)]
+
+    @classmethod
+    def default(cls, **kw):
+        """LBFGSParam() defaults (deplibs/LBFGSpp/include/LBFGSpp/Param.h:224-243)
+        with the trainer's epsgmax = 0 (train/train_mtp.cpp:59)."""
+        p = cls(m=6, epsilon=1e-5, epsilon_rel=1e-5, epsgmax=0.0, past=0, delta=0.0,
+                max_iterations=0, max_linesearch=20, min_step=1e-20, max_step=1e20,
+                f_dec_coeff=1e-4, s_curv_coeff=0.9, max_step_move=1e20, machine_prec=1e-16,
+                initial_step=-1.0, first_initial_step=-1.0, unscale_iterate=1)
+        for k, v in kw.items():
+            setattr(p, k, v)
+        return p
+
+
+_REF_OBJECTIVE = C.CFUNCTYPE(C.c_int, C.c_void_p, C.POINTER(C.c_double),
+                             C.POINTER(C.c_double), C.c_int, C.POINTER(C.c_double))
+_ref_lbfgs_lib = None
+
+
+def ref_lbfgs(fg, x0, params=None):
+    """LBFGSSolver<double, LineSearchLewisOverton>::minimize of the reference's
+    vendored LBFGSpp (oracle/_ref/liblbfgs_ref.so) over fg(x) -> (f, grad[,
+    point to leave in the solver's iterate]).  Returns (ok, x, iterations, f,
+    evaluations, message)."""
+    global _ref_lbfgs_lib
+    if _ref_lbfgs_lib is None:
+        L = C.CDLL(os.path.join(REF_DIR, "liblbfgs_ref.so"))
+        L.ref_lbfgs_minimize.argtypes = [C.POINTER(RefLbfgsParams), C.c_int,
+                                         C.POINTER(C.c_double), _REF_OBJECTIVE, C.c_void_p,
+                                         C.POINTER(C.c_int), C.POINTER(C.c_double), C.c_char_p,
+                                         C.c_int]
+        L.ref_lbfgs_minimize.restype = C.c_int
+        _ref_lbfgs_lib = L
+    p = params if params is not None else RefLbfgsParams.default()
+    x = np.array(x0, dtype=np.float64)
+    n = x.size
+    count = [0]
+
+    def cb(_user, xp, gp, nn, fp):
+        try:
+            xa = np.ctypeslib.as_array(xp, shape=(nn,))
+            res = fg(xa.copy())
+            np.ctypeslib.as_array(gp, shape=(nn,))[:] = res[1]
+            if len(res) > 2:
+                xa[:] = res[2]
+            fp[0] = res[0]
+            count[0] += 1
+            return 0
+        except Exception:  # noqa: BLE001 -- reported to the solver as a failure
+            return 1
+
+    cfn = _REF_OBJECTIVE(cb)
+    it = C.c_int()
+    fx = C.c_double()
+    msg = C.create_string_buffer(256)
+    rc = _ref_lbfgs_lib.ref_lbfgs_minimize(C.byref(p), n, x.ctypes.data_as(C.POINTER(C.c_double)),
+                                           cfn, None, C.byref(it), C.byref(fx), msg, 256)
+    return rc == 0, x, it.value, fx.value, count[0], msg.value.decode()

@@ -147,7 +147,8 @@ def test_compiled_linear_walk_is_current(tmp_path):
     exe = str(tmp_path / "gen_lin_plan")
     subprocess.run([hipcc, "-O1", "-std=c++17", "-w", "-I", os.path.join(root, "include"),
                     "-I", os.path.join(pkg, "csrc"), os.path.join(pkg, "gen_lin_plan.cpp"),
-                    os.path.join(pkg, "csrc", "model.cpp"), "-o", exe], check=True)
+                    os.path.join(pkg, "csrc", "model.cpp"), os.path.join(pkg, "csrc", "metadata.cpp"),
+                    "-o", exe], check=True)
     rel = "tests/golden/templates/shapeev-16.mtp"
     out = subprocess.run([exe, rel, "LinPlanLevel16"], cwd=root, check=True,
                          capture_output=True, text=True).stdout
