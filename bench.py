@@ -1,6 +1,7 @@
 """Benchmark of the MI355X MTP E/F/S path (one GPU).
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-train]
+                    [--no-linear] [--no-large]
 
 Workload (the metric's configuration): level-16 two-species MTP (radial
 basis size 8, min_dist 1.9 A, cutoff 5.0 A, coefficients U[-0.05, 0.05],
@@ -14,8 +15,16 @@ whole cell with the neighbour lists resident in HBM (the reference fastfit
 roofline entry prices the dominant kernel's algorithmic fp64 flops per launch
 (n_i (8R + 4MR + 4 nu_max + 38B + 24) + 9T + 2S + 2 per atom) against the
 MI355X fp64 peak, over the kernel's mean duration measured with HIP events on
-the library's stream.  The CPU baseline is the oracle's getEFSOMP restatement
-on the host cores.  Prints one JSON line.
+the library's stream.  Further legs (same JSON line): the 256,000-atom
+level-20 four-species cell ("large"), the nonlinear training loss+gradient
+("train") and the linear-fit assembly ("linear").
+
+The CPU baselines time the oracle's restatement of the reference CPU path
+(getEFSOMP, AccumulateGard, CalcEFSCmpt_R + AddLinearFast + Gram) built
+with the reference's release flags (-O3 -march=native -fopenmp) on the host
+that runs the benchmark, on the cores allotted to the job (OMP_NUM_THREADS)
+and on one core; medians of timed rounds with their interquartile range.
+Prints one JSON line.
 """
 from __future__ import annotations
 
@@ -36,7 +45,6 @@ from mtpx import synth as S  # noqa: E402
 METRIC = "MTP E/F/S atom-evals/s (lvl16, 32k atoms); train loss+grad configs/s"
 FP64_PEAK_TFLOPS = 78.6
 HBM_PEAK_GBS = 8000.0
-TRAFFIC_FILE = os.path.join(ROOT, "profiles", "efs_kernel_lvl16_32k_traffic.json")
 
 
 def efs_flops(model_text: str, n: int, P: int) -> float:
@@ -50,6 +58,87 @@ def efs_flops(model_text: str, n: int, P: int) -> float:
     per_pair = 8 * R + 4 * M * R + 4 * nu + 32 * B + 6 * B + 24
     per_site = 9 * T + 2 * Sn + 2
     return float(P) * per_pair + float(n) * per_site
+
+
+def traffic_of(key: str):
+    """HBM bytes per launch of a kernel on a workload, from the calibrated
+    FETCH_SIZE / WRITE_SIZE summaries under profiles/ (None if absent)."""
+    path = os.path.join(ROOT, "profiles", key + "_traffic.json")
+    if os.path.exists(path):
+        return json.load(open(path)).get("hbm_bytes_per_launch")
+    return None
+
+
+def compute_roofline(flops: float, ms: float, kernel: str, traffic_key: str, pipe="fp64 VALU",
+                     **extra):
+    """Roofline of an fp64 compute-bound kernel: algorithmic flops per launch
+    over its mean duration against the MI355X fp64 peak (78.6 TFLOP/s for
+    the vector and the matrix pipe alike; "mfma" names the compute roof)."""
+    achieved = flops / (ms * 1e-3) / 1e12
+    r = {"bound": "mfma", "achieved": achieved, "peak": FP64_PEAK_TFLOPS, "unit": "TFLOP/s",
+         "frac": achieved / FP64_PEAK_TFLOPS, "traffic": traffic_of(traffic_key),
+         "kernel": kernel, "pipe": pipe, "kernel_ms": ms, "algorithmic_flops_per_launch": flops}
+    r.update(extra)
+    return r
+
+
+def copy_probe(mib: int):
+    """A plain device-to-device copy of MIB MiB, three times (calibrates the
+    HBM byte counters against traffic of known size); HIP runtime only."""
+    import ctypes as C
+    hip = C.CDLL("libamdhip64.so.7")
+    hip.hipMalloc.argtypes = [C.POINTER(C.c_void_p), C.c_size_t]
+    hip.hipMemcpy.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int]
+    hip.hipMemset.argtypes = [C.c_void_p, C.c_int, C.c_size_t]
+    hip.hipFree.argtypes = [C.c_void_p]
+    nbytes = mib << 20
+    a, b = C.c_void_p(), C.c_void_p()
+    assert hip.hipMalloc(C.byref(a), nbytes) == 0 and hip.hipMalloc(C.byref(b), nbytes) == 0
+    assert hip.hipMemset(a, 1, nbytes) == 0
+    for _ in range(3):
+        assert hip.hipMemcpy(b, a, nbytes, 3) == 0  # device to device
+    assert hip.hipDeviceSynchronize() == 0
+    hip.hipFree(a)
+    hip.hipFree(b)
+    print(json.dumps({"copy_probe_bytes": nbytes, "copies": 3}))
+
+
+def large_bench(ctx, steps: int, warmup: int):
+    """The 256,000-atom level-20 four-species cell (40x40x40 FCC, a = 3.6 A,
+    equiatomic, sigma 0.15 A, radial basis 10, cutoff 5.5 A): E/F/S with the
+    lists resident, and list build + E/F/S from host positions."""
+    model_text, s = S.workload_inference(3)
+    pos = capi.wrap(s.cell, s.pbc, s.pos)
+    ctx.load_model_text(model_text)
+    cutoff = 5.5
+    ctx.build_neighbors(s.cell, s.pbc, pos, s.types, cutoff)
+    n, P = ctx.neighbor_count()
+    for _ in range(warmup):
+        ctx.efs_device(False)
+    kms = []
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        ctx.efs_device(False)
+        kms.append(ctx.last_timings()[1])
+    wall = time.perf_counter() - t0
+    tot = []
+    for _ in range(3):
+        t1 = time.perf_counter()
+        ctx.build_neighbors(s.cell, s.pbc, pos, s.types, cutoff)
+        ctx.efs_device(False)
+        tot.append(time.perf_counter() - t1)
+    flops = efs_flops(model_text, n, P)
+    k_ms = float(np.mean(kms))
+    return {
+        "metric": "MTP E/F/S atom-evals/s (lvl20, 4 species, 256k atoms)",
+        "value": n * steps / wall, "unit": "atom-evals/s", "steps": steps,
+        "ms_per_step": 1e3 * wall / steps,
+        "config": {"workload": "E/F/S, level-20 MTP, 4 species, R=10, cutoff 5.5, 256,000-atom "
+                               "FCC 40x40x40 a=3.6, equiatomic, sigma 0.15",
+                   "atoms": n, "neighbor_entries": P, "mean_neighbors": P / n},
+        "roofline": compute_roofline(flops, k_ms, "efs_kernel<level 20>", "efs_lvl20_256k"),
+        "total_ms_build_plus_efs": 1e3 * float(np.median(tot)),
+    }, (model_text, s.cell, s.pbc, pos, s.types)
 
 
 def train_flops(model_text: str, n: int, P: int) -> float:
@@ -116,13 +205,11 @@ def train_bench(ctx, steps: int, warmup: int, nconf: int):
         "config": {"workload": "loss+gradient, level-20 MTP, 3 species, R=10, cutoff 6.0, "
                                "%d liquid configs of 108-216 atoms, rho 0.06, d_min 1.5" % nconf,
                    "atoms": n, "neighbor_entries": P},
-        "roofline": {"bound": "mfma", "achieved": flops / (dev_ms * 1e-3) / 1e12,
-                     "peak": FP64_PEAK_TFLOPS, "unit": "TFLOP/s",
-                     "frac": flops / (dev_ms * 1e-3) / 1e12 / FP64_PEAK_TFLOPS, "traffic": None,
-                     "kernel": "loss+grad step (efs_kernel, loss_kernel, grad_kernel)",
-                     "device_ms": dev_ms, "efs_ms": float(np.mean(tims[:, 1])),
-                     "loss_ms": float(np.mean(tims[:, 2])), "grad_ms": grad_ms,
-                     "algorithmic_flops_per_step": flops},
+        "roofline": compute_roofline(
+            flops, dev_ms, "loss+grad step (efs_kernel, loss_kernel, grad_kernel)",
+            "grad_lvl20_1000", efs_ms=float(np.mean(tims[:, 1])),
+            loss_ms=float(np.mean(tims[:, 2])), grad_ms=grad_ms,
+            traffic_kernel="grad_kernel (the step's largest kernel)"),
         "loss": f,
         "list_build_ms": build_ms,
     }, (start_text, structs, off, tE, tF, tS, cutoff)
@@ -191,96 +278,176 @@ def linear_bench(ctx, steps: int, nconf: int):
         "config": {"workload": "linear fit, level-16 MTP, 2 species, R=8, cutoff 5.0, %d FCC/BCC "
                                "configs of 64-256 atoms, weights 1/0.01/0.001" % nconf,
                    "atoms": n, "neighbor_entries": P, "rows": rows, "p": int(G.shape[0])},
-        "roofline": {"bound": "mfma", "achieved": flops / (dev_ms * 1e-3) / 1e12,
-                     "peak": FP64_PEAK_TFLOPS, "unit": "TFLOP/s",
-                     "frac": flops / (dev_ms * 1e-3) / 1e12 / FP64_PEAK_TFLOPS, "traffic": None,
-                     "kernel": "lin_site_kernel + gram_kernel (MFMA)", "device_ms": dev_ms,
-                     "components_ms": float(np.mean(tims[:, 1])),
-                     "gram_ms": float(np.mean(tims[:, 2])),
-                     "algorithmic_flops_per_step": flops},
+        "roofline": compute_roofline(
+            flops, dev_ms, "linear-fit step (lin_site_kernel, lin_gather_kernel, gram_kernel)",
+            "lin_site_lvl16_2000", pipe="fp64 VALU (design rows) + fp64 MFMA (Gram)",
+            components_ms=float(np.mean(tims[:, 1])), gram_ms=float(np.mean(tims[:, 2])),
+            traffic_kernel="lin_site_kernel (the step's largest kernel)"),
         "list_build_ms": build_ms,
     }, (start_text, structs, off, tE, tF, tS)
 
 
-def linear_cpu_baseline(data, budget_s: float = 12.0):
-    """The oracle's CalcEFSCmpt_R + AddLinearFast + Gram on the host cores,
-    on the first structures of the same batch (bounded sample)."""
-    sys.path.insert(0, os.path.join(ROOT, "oracle"))
-    import oracle as O
+# ------------------------------------------------------------ CPU baselines --
 
-    text, structs, off, tE, tF, tS = data
-    threads = max(1, min(16, os.cpu_count() or 1))
-    m = O.Model(text)
-    sample = min(32, len(structs))
-    nbs, labels = [], []
-    for k in range(sample):
-        st = structs[k]
-        nbs.append(O.Neighbors.build(st.cell, st.pbc, st.pos, st.types, 5.0))
-        labels.append(O.Labels(st.n, energy=tE[k], forces=tF[off[k]:off[k + 1]], stress=tS[k]))
-    sets = O.LossSettings.make(weight_eng=1.0, weight_force=0.01, weight_stress=0.001)
-    O.linear_system_batch(m, nbs, labels, sets, threads)  # warm-up
-    reps, t0 = 0, time.perf_counter()
-    while True:
-        O.linear_system_batch(m, nbs, labels, sets, threads)
-        reps += 1
-        el = time.perf_counter() - t0
-        if el > budget_s or reps >= 1000:
-            break
-    return {"value": reps * len(nbs) / el, "unit": "configs/s", "cores": threads, "kind": "port",
-            "sample": "%d assemblies over the first %d structures of the batch (oracle "
-                      "CalcEFSCmpt_R + AddLinearFast + Gram, %d OpenMP threads, %.1f s)"
-                      % (reps, len(nbs), threads, el)}
+_ORACLE = None
 
 
-def train_cpu_baseline(data, budget_s: float = 12.0):
-    """The oracle's AccumulateGard restatement on the host cores, on the
-    first structures of the same batch (bounded sample)."""
-    sys.path.insert(0, os.path.join(ROOT, "oracle"))
-    import oracle as O
-
-    text, structs, off, tE, tF, tS, cutoff = data
-    threads = max(1, min(16, os.cpu_count() or 1))
-    m = O.Model(text)
-    sample = min(16, len(structs))
-    nbs, labels = [], []
-    for k in range(sample):
-        st = structs[k]
-        nbs.append(O.Neighbors.build(st.cell, st.pbc, st.pos, st.types, cutoff))
-        labels.append(O.Labels(st.n, energy=tE[k], forces=tF[off[k]:off[k + 1]], stress=tS[k]))
-    st = O.LossSettings.make()
-    O.loss_grad_batch(m, nbs, labels, st, 1e-6, 1e-10, 0.0, threads)  # warm-up
-    reps, t0 = 0, time.perf_counter()
-    while True:
-        O.loss_grad_batch(m, nbs, labels, st, 1e-6, 1e-10, 0.0, threads)
-        reps += 1
-        el = time.perf_counter() - t0
-        if el > budget_s or reps >= 1000:
-            break
-    return {"value": reps * len(nbs) / el, "unit": "configs/s", "cores": threads, "kind": "port",
-            "sample": "%d loss+gradient passes over the first %d structures of the batch "
-                      "(oracle AccumulateGard, %d OpenMP threads, %.1f s)"
-                      % (reps, len(nbs), threads, el)}
+def oracle_module():
+    """The oracle's timing build (make -C oracle fast: -O3 -march=native
+    -fopenmp, compiled here, on the host that runs the baseline); the parity
+    build if that compile fails."""
+    global _ORACLE
+    if _ORACLE is None:
+        import subprocess
+        sys.path.insert(0, os.path.join(ROOT, "oracle"))
+        import oracle as O
+        fast = os.path.join(ROOT, "oracle", "_fast", "liboracle_fast.so")
+        r = subprocess.run(["make", "-s", "-B", "-C", os.path.join(ROOT, "oracle"), "fast"],
+                           capture_output=True, text=True)
+        if r.returncode == 0 and os.path.exists(fast):
+            O.use_library(fast)
+            O.BUILD_FLAGS = "-O3 -march=native -fopenmp (oracle/Makefile fast)"
+        else:
+            O.BUILD_FLAGS = "-O2 -ffp-contract=off -fopenmp (parity build; fast build failed)"
+        _ORACLE = O
+    return _ORACLE
 
 
-def cpu_baseline(model_text, cell, pbc, pos, types, budget_s: float = 12.0):
-    """The oracle's getEFSOMP restatement timed on the host cores (bounded sample)."""
-    sys.path.insert(0, os.path.join(ROOT, "oracle"))
-    import oracle as O
+def host_info():
+    model = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    try:
+        affinity = len(os.sched_getaffinity(0))
+    except AttributeError:
+        affinity = os.cpu_count()
+    return {"nproc": os.cpu_count(), "affinity_cpus": affinity, "cpu_model": model,
+            "omp_num_threads": os.environ.get("OMP_NUM_THREADS")}
 
-    threads = max(1, min(16, os.cpu_count() or 1))
+
+def job_threads() -> int:
+    """The cores allotted to this job: OMP_NUM_THREADS where the scheduler
+    sets it (16 per GPU on the MI355X pool), else the affinity mask."""
+    env = os.environ.get("OMP_NUM_THREADS")
+    if env and env.isdigit() and int(env) > 0:
+        return int(env)
+    return host_info()["affinity_cpus"] or 1
+
+
+def timed(fn, budget_s: float, min_reps: int = 5, max_reps: int = 1000, warmup: int = 1):
+    """Median and interquartile range of per-round wall times (warm-up
+    rounds first; at least min_reps rounds, then until the budget is used)."""
+    for _ in range(warmup):
+        fn()
+    t = []
+    t0 = time.perf_counter()
+    while len(t) < max_reps and (len(t) < min_reps or time.perf_counter() - t0 < budget_s):
+        t1 = time.perf_counter()
+        fn()
+        t.append(time.perf_counter() - t1)
+    q1, med, q3 = np.percentile(t, [25, 50, 75])
+    return float(med), float(q3 - q1), len(t)
+
+
+def _leg(units: float, unit: str, med: float, iqr: float, reps: int, cores: int, what: str):
+    return {"value": units / med, "unit": unit, "cores": cores, "kind": "port",
+            "median_s": med, "iqr_s": iqr, "rounds": reps,
+            "sample": "%s; median of %d rounds (IQR %.3g s), %d thread%s"
+                      % (what, reps, iqr, cores, "" if cores == 1 else "s")}
+
+
+def efs_cpu_baseline(model_text, cell, pbc, pos, types, label: str, budget_s: float = 6.0,
+                     single: bool = True, total: bool = True):
+    """The oracle's getEFSOMP (atom-parallel, per-thread buffers, serial
+    merge; potential_mtp.cpp:2416-2486) on the job's cores and on one core,
+    lists prebuilt ("kernel"); plus list build + E/F/S ("total", the BOXED
+    build is serial in the reference)."""
+    O = oracle_module()
+    t = job_threads()
     m = O.Model(model_text)
     nb = O.Neighbors.build(cell, pbc, pos, types, m.cutoff)
-    O.efs(m, nb, threads=threads)  # warm-up
-    reps, t0 = 0, time.perf_counter()
-    while True:
-        O.efs(m, nb, threads=threads)
-        reps += 1
-        el = time.perf_counter() - t0
-        if el > budget_s or reps >= 2000:
-            break
-    return {"value": reps * nb.n / el, "unit": "atom-evals/s", "cores": threads, "kind": "port",
-            "sample": "%d full E/F/S evaluations of the 32,000-atom cell (oracle getEFSOMP, "
-                      "prebuilt lists, %d OpenMP threads, %.1f s)" % (reps, threads, el)}
+    n = nb.n
+    med, iqr, reps = timed(lambda: O.efs(m, nb, threads=t), budget_s, min_reps=3)
+    out = _leg(n, "atom-evals/s", med, iqr, reps, t, "E/F/S of the %s, prebuilt lists" % label)
+    if single:
+        med1, iqr1, reps1 = timed(lambda: O.efs(m, nb, threads=1), budget_s, min_reps=3)
+        out["single_core"] = _leg(n, "atom-evals/s", med1, iqr1, reps1, 1,
+                                  "E/F/S of the %s, prebuilt lists" % label)
+    if total:
+        def build_and_efs():
+            b = O.Neighbors.build(cell, pbc, pos, types, m.cutoff)
+            O.efs(m, b, threads=t)
+        medt, iqrt, repst = timed(build_and_efs, budget_s / 2, min_reps=3)
+        out["total"] = _leg(n, "atom-evals/s", medt, iqrt, repst, t,
+                            "BOXED list build (serial) + E/F/S of the %s" % label)
+    out["host"] = host_info()
+    out["build"] = O.BUILD_FLAGS
+    return out
+
+
+def train_cpu_baseline(data, budget_s: float = 6.0):
+    """The oracle's AccumulateGard (per-thread loss/gradient accumulators
+    merged in thread order) on the job's cores and on one core."""
+    O = oracle_module()
+    text, structs, off, tE, tF, tS, cutoff = data
+    t = job_threads()
+    m = O.Model(text)
+
+    def sample(k):
+        nbs, labels = [], []
+        for c in range(min(k, len(structs))):
+            st = structs[c]
+            nbs.append(O.Neighbors.build(st.cell, st.pbc, st.pos, st.types, cutoff))
+            labels.append(O.Labels(st.n, energy=tE[c], forces=tF[off[c]:off[c + 1]],
+                                   stress=tS[c]))
+        return nbs, labels
+
+    st = O.LossSettings.make()
+    nbs, labels = sample(250)
+    med, iqr, reps = timed(lambda: O.loss_grad_batch(m, nbs, labels, st, 1e-6, 1e-10, 0.0, t),
+                           budget_s, min_reps=3)
+    out = _leg(len(nbs), "configs/s", med, iqr, reps, t,
+               "loss+gradient pass over the first %d structures of the batch" % len(nbs))
+    nb1, lb1 = nbs[:24], labels[:24]
+    med1, iqr1, reps1 = timed(lambda: O.loss_grad_batch(m, nb1, lb1, st, 1e-6, 1e-10, 0.0, 1),
+                              budget_s, min_reps=3)
+    out["single_core"] = _leg(len(nb1), "configs/s", med1, iqr1, reps1, 1,
+                              "loss+gradient pass over the first %d structures" % len(nb1))
+    out["host"] = host_info()
+    out["build"] = O.BUILD_FLAGS
+    return out
+
+
+def linear_cpu_baseline(data, budget_s: float = 6.0):
+    """The oracle's CalcEFSCmpt_R + AddLinearFast + Gram (per-thread normal
+    equations merged in thread order) on the job's cores and on one core."""
+    O = oracle_module()
+    text, structs, off, tE, tF, tS = data
+    t = job_threads()
+    m = O.Model(text)
+    nbs, labels = [], []
+    for c in range(min(1000, len(structs))):
+        st = structs[c]
+        nbs.append(O.Neighbors.build(st.cell, st.pbc, st.pos, st.types, 5.0))
+        labels.append(O.Labels(st.n, energy=tE[c], forces=tF[off[c]:off[c + 1]], stress=tS[c]))
+    sets = O.LossSettings.make(weight_eng=1.0, weight_force=0.01, weight_stress=0.001)
+    med, iqr, reps = timed(lambda: O.linear_system_batch(m, nbs, labels, sets, t), budget_s,
+                           min_reps=3)
+    out = _leg(len(nbs), "configs/s", med, iqr, reps, t,
+               "normal-equation assembly over the first %d structures of the batch" % len(nbs))
+    nb1, lb1 = nbs[:64], labels[:64]
+    med1, iqr1, reps1 = timed(lambda: O.linear_system_batch(m, nb1, lb1, sets, 1), budget_s,
+                              min_reps=3)
+    out["single_core"] = _leg(len(nb1), "configs/s", med1, iqr1, reps1, 1,
+                              "normal-equation assembly over the first %d structures" % len(nb1))
+    out["host"] = host_info()
+    out["build"] = O.BUILD_FLAGS
+    return out
 
 
 def main():
@@ -299,16 +466,11 @@ def main():
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="only copy a MIB-MiB device buffer 3 times (calibrates the HBM "
                          "byte counters against a plain copy of known size)")
+    ap.add_argument("--no-large", action="store_true")
+    ap.add_argument("--large-steps", type=int, default=20)
     args = ap.parse_args()
     if args.copy_probe:
-        import torch
-        nbytes = args.copy_probe << 20
-        a = torch.ones(nbytes, dtype=torch.uint8, device="cuda")
-        b = torch.empty_like(a)
-        for _ in range(3):
-            b.copy_(a)
-        torch.cuda.synchronize()
-        print(json.dumps({"copy_probe_bytes": nbytes, "copies": 3}))
+        copy_probe(args.copy_probe)
         return
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path "
@@ -339,12 +501,15 @@ def main():
 
     # "total": neighbour build from host positions + E/F/S (fastfit total_ns_atom)
     tot = []
-    for _ in range(3):
+    for _ in range(5):
         t1 = time.perf_counter()
         ctx.build_neighbors(s.cell, s.pbc, pos, s.types, cutoff)
         ctx.efs_device(det)
         tot.append(time.perf_counter() - t1)
     E, F, St, _ = ctx.efs(det)
+    large = None
+    if not args.no_large:
+        large, large_data = large_bench(ctx, args.large_steps, 3)
     train = None
     if not args.no_train:
         train, tdata = train_bench(ctx, args.train_steps, 1, args.train_configs)
@@ -356,9 +521,6 @@ def main():
     flops = efs_flops(model_text, n, P)
     k_ms = float(np.mean(kernel_ms))
     achieved = flops / (k_ms * 1e-3) / 1e12
-    traffic = None
-    if os.path.exists(TRAFFIC_FILE):
-        traffic = json.load(open(TRAFFIC_FILE)).get("hbm_bytes_per_launch")
     out = {
         "metric": METRIC,
         "value": n * args.steps / wall,
@@ -376,19 +538,20 @@ def main():
                                "cutoff 5.0, 75/25, strain 2%, sigma 0.12",
                    "atoms": n, "neighbor_entries": P, "mean_neighbors": P / n,
                    "deterministic": det},
-        "roofline": {"bound": "mfma", "achieved": achieved, "peak": FP64_PEAK_TFLOPS,
-                     "unit": "TFLOP/s", "frac": achieved / FP64_PEAK_TFLOPS, "traffic": traffic,
-                     "kernel": "efs_kernel<4,6,8>", "kernel_ms": k_ms,
-                     "kernel_ms_min": float(np.min(kernel_ms)),
-                     "algorithmic_flops_per_launch": flops,
-                     "note": "fp64 VALU-bound; the MI355X fp64 vector and matrix peaks are both "
-                             "78.6 TFLOP/s"},
+        "roofline": compute_roofline(flops, k_ms, "efs_kernel<level 16>", "efs_lvl16_32k",
+                                     kernel_ms_min=float(np.min(kernel_ms))),
         "extra": {"total_ms_build_plus_efs": 1e3 * float(np.median(tot)),
                   "neighbor_build_first_ms": 1e3 * nbuild_first,
                   "energy": E, "max_abs_force": float(np.abs(F).max())},
     }
     if not args.no_cpu:
-        out["cpu_baseline"] = cpu_baseline(model_text, s.cell, s.pbc, pos, s.types)
+        out["cpu_baseline"] = efs_cpu_baseline(model_text, s.cell, s.pbc, pos, s.types,
+                                               "32,000-atom level-16 cell")
+    if large is not None:
+        if not args.no_cpu:
+            large["cpu_baseline"] = efs_cpu_baseline(*large_data, "256,000-atom level-20 cell",
+                                                     single=False, total=False)
+        out["large"] = large
     if train is not None:
         if not args.no_cpu:
             train["cpu_baseline"] = train_cpu_baseline(tdata)

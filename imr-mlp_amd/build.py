@@ -19,6 +19,8 @@ ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 LIB_DIR = os.path.join(HERE, "lib")
 LIB = os.path.join(LIB_DIR, "libmtpx.so")
+CALC_EFS = os.path.join(LIB_DIR, "mtpx_calc_efs")
+CXX = os.environ.get("CXX", "g++")
 OBJ_DIR = os.path.join(HERE, "_build")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
@@ -31,6 +33,7 @@ SOURCES = [
     ("efs_kernel.hip", ["-ffp-contract=fast"]),
     ("train_kernel.hip", ["-ffp-contract=fast"]),
     ("lin_kernel.hip", ["-ffp-contract=fast"]),
+    ("gram_kernel.hip", ["-ffp-contract=fast"]),
     ("neighbors.hip", ["-ffp-contract=off"]),
     ("geometry.cpp", ["-ffp-contract=off"]),
     ("model.cpp", ["-ffp-contract=off"]),
@@ -84,6 +87,15 @@ def build(verbose: bool = False, changed_only: bool = False) -> str:
         print(" ".join(cmd), flush=True)
     subprocess.run(cmd, check=True)
     os.replace(tmp, LIB)
+    # the calc_efs front end over the C ABI (host code, links the library)
+    tmp = CALC_EFS + ".tmp"
+    cmd = [CXX, "-O2", "-std=c++17", "-Wall", "-I", os.path.join(ROOT, "include"),
+           os.path.join(HERE, "calc_efs.cpp"), "-o", tmp, "-L", LIB_DIR, "-lmtpx",
+           "-Wl,-rpath,$ORIGIN"]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    subprocess.run(cmd, check=True)
+    os.replace(tmp, CALC_EFS)
     if verbose:
         print("built %s in %.1fs" % (LIB, time.time() - t0), flush=True)
     return LIB

@@ -1,0 +1,407 @@
+// mtpx_calc_efs: the calc_efs front end (apps/calc_efs.cpp:179-389, the
+// --device=hip branch) over the C ABI.  Reads structures in the text MLIP
+// configuration format (io/gpio_read_cfg.cpp:319-615), evaluates energy,
+// forces, stress and site energies on the device in structure-preserving
+// chunks (mtpx_set_structures + mtpx_compute_batch, or mtpx_energy with
+// --energy-only), and writes the configurations back
+// (GPIO::write_next_mlpcfg, io/gpio_write.cpp:224-380).
+//
+//   mtpx_calc_efs --pot potential.mtp --in input.cfg --out output-efs.cfg
+//       [--energy-only] [--no-site-energy] [--lossless] [--show-progress]
+//       [--gpu-id K] [--gpu-batch-atoms N] [--gpu-batch-structures N]
+//       [--deterministic]
+//
+// Read: BEGIN_CFG, Size, an optional Supercell of three rows (periodic in
+// all three directions; without it the structure is a cluster), AtomData
+// with the columns id, type, cartes_x/y/z (or x/y/z) and any others (kept
+// by name), Energy, PlusStress (xx yy zz yz xz xy), Feature lines (kept
+// verbatim), END_CFG.  Types are species indices 0 .. Z-1.
+// Written: the reference's fixed-width form ({:>15.8g}, printf "%15.8g"),
+// or with --lossless numbers that read back to the same doubles ("%.17g";
+// the reference prints the shortest such form).  Energy, forces, stress and
+// site energies are replaced by the computed ones; --energy-only writes the
+// energy and drops forces, stress and site energies, --no-site-energy drops
+// the site energies.
+#include "mtpx.h"
+
+#include <algorithm>
+#include <cmath>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <fstream>
+#include <iostream>
+#include <sstream>
+#include <string>
+#include <vector>
+
+namespace {
+
+struct Config {
+    int n = 0;
+    bool periodic = false;
+    double cell[9] = {0, 0, 0, 0, 0, 0, 0, 0, 0};
+    std::vector<int> type;
+    std::vector<double> pos;              // [n][3]
+    std::vector<std::string> extra_names; // other AtomData columns
+    std::vector<double> extra;            // [n][extra]
+    std::vector<std::string> features;    // "Feature ..." lines, verbatim
+    double energy = 0;
+    double stress[9] = {0, 0, 0, 0, 0, 0, 0, 0, 0};
+    std::vector<double> force, site;      // computed
+};
+
+[[noreturn]] void die(const std::string &msg)
+{
+    std::fprintf(stderr, "mtpx_calc_efs: %s\n", msg.c_str());
+    std::exit(1);
+}
+
+std::vector<std::string> split(const std::string &line)
+{
+    std::istringstream is(line);
+    std::vector<std::string> out;
+    std::string t;
+    while (is >> t)
+        out.push_back(t);
+    return out;
+}
+
+bool number(const std::string &s, double &v)
+{
+    char *end = nullptr;
+    v = std::strtod(s.c_str(), &end);
+    return end && *end == 0 && end != s.c_str() && std::isfinite(v);
+}
+
+// GPIO::load_next_from_mlpcfg: false at a clean end of input, dies on a
+// malformed configuration.
+bool read_config(std::istream &is, Config &c, int index)
+{
+    std::string line;
+    bool begin = false;
+    while (std::getline(is, line))
+        if (line.find("BEGIN_CFG") != std::string::npos) {
+            begin = true;
+            break;
+        }
+    if (!begin)
+        return false;
+    const std::string where = "configuration " + std::to_string(index) + ": ";
+    double v = 0;
+    if (!std::getline(is, line) || !std::getline(is, line))
+        die(where + "missing Size");
+    {
+        auto t = split(line);
+        if (t.empty() || !number(t[0], v) || v < 0 || v != std::floor(v))
+            die(where + "invalid Size");
+        c.n = (int)v;
+    }
+    if (!std::getline(is, line))
+        die(where + "truncated");
+    if (line.find("Supercell") != std::string::npos) {
+        c.periodic = true;
+        for (int a = 0; a < 3; ++a) {
+            if (!std::getline(is, line))
+                die(where + "truncated Supercell");
+            auto t = split(line);
+            if (t.size() < 3)
+                die(where + "invalid Supercell row");
+            for (int b = 0; b < 3; ++b)
+                if (!number(t[b], c.cell[3 * a + b]))
+                    die(where + "invalid Supercell row");
+        }
+        if (!std::getline(is, line))
+            die(where + "truncated");
+    }
+    auto head = split(line);
+    if (head.empty() || head[0] != "AtomData:")
+        die(where + "missing AtomData");
+    int col_id = -1, col_type = -1, col_x = -1, col_y = -1, col_z = -1;
+    std::vector<int> extra_cols;
+    const std::vector<std::string> computed = {"fx", "fy", "fz", "site_en"};
+    for (size_t k = 1; k < head.size(); ++k) {
+        const std::string &h = head[k];
+        const int col = (int)k - 1;
+        if (h == "id")
+            col_id = col;
+        else if (h == "type")
+            col_type = col;
+        else if (h == "cartes_x" || h == "x")
+            col_x = col;
+        else if (h == "cartes_y" || h == "y")
+            col_y = col;
+        else if (h == "cartes_z" || h == "z")
+            col_z = col;
+        else if (std::find(computed.begin(), computed.end(), h) == computed.end()) {
+            c.extra_names.push_back(h);
+            extra_cols.push_back(col);
+        }
+    }
+    if (col_x < 0 || col_y < 0 || col_z < 0)
+        die(where + "AtomData needs cartes_x cartes_y cartes_z");
+    const int ncol = (int)head.size() - 1;
+    c.type.assign(c.n, 0);
+    c.pos.assign(3 * (size_t)c.n, 0.0);
+    c.extra.assign((size_t)c.n * extra_cols.size(), 0.0);
+    std::vector<char> seen(c.n, 0);
+    for (int i = 0; i < c.n; ++i) {
+        if (!std::getline(is, line))
+            die(where + "truncated AtomData");
+        auto t = split(line);
+        if ((int)t.size() < ncol)
+            die(where + "short AtomData row");
+        std::vector<double> val(ncol);
+        for (int k = 0; k < ncol; ++k)
+            if (!number(t[k], val[k]))
+                die(where + "invalid AtomData value");
+        int id = i;
+        if (col_id >= 0) {
+            const double d = val[col_id];
+            if (d != std::floor(d) || d < 1 || d > c.n || seen[(int)d - 1])
+                die(where + "invalid atom id");
+            id = (int)d - 1;
+        }
+        seen[id] = 1;
+        if (col_type >= 0) {
+            const double d = val[col_type];
+            if (d != std::floor(d) || d < 0 || d > 1e9)
+                die(where + "invalid atom type");
+            c.type[id] = (int)d;
+        }
+        c.pos[3 * (size_t)id] = val[col_x];
+        c.pos[3 * (size_t)id + 1] = val[col_y];
+        c.pos[3 * (size_t)id + 2] = val[col_z];
+        for (size_t e = 0; e < extra_cols.size(); ++e)
+            c.extra[(size_t)id * extra_cols.size() + e] = val[extra_cols[e]];
+    }
+    while (std::getline(is, line)) {
+        auto t = split(line);
+        if (t.empty())
+            continue;
+        if (t[0] == "END_CFG")
+            return true;
+        if (t[0] == "Energy" || t[0] == "energy" || t[0] == "PlusStress:" ||
+            t[0] == "plusstress:" || t[0] == "Stress:" || t[0] == "stress:") {
+            if (!std::getline(is, line))  // the label values are replaced
+                die(where + "truncated");
+        } else if (t[0] == "Feature" || t[0] == "feature") {
+            c.features.push_back(line);
+        }
+    }
+    die(where + "missing END_CFG");
+}
+
+void write_num(std::ostream &os, double v, bool lossless, bool lead_space = true)
+{
+    char buf[64];
+    std::snprintf(buf, sizeof buf, lossless ? "%.17g" : "%15.8g", v);
+    if (lead_space)
+        os << ' ';
+    os << buf;
+}
+
+// GPIO::write_next_mlpcfg (io/gpio_write.cpp:224-380).
+void write_config(std::ostream &os, const Config &c, bool lossless, bool energy_only,
+                  bool site_energy)
+{
+    os << "BEGIN_CFG\nSize\n" << c.n << "\nSupercell\n";
+    for (int a = 0; a < 3; ++a) {
+        for (int b = 0; b < 3; ++b)
+            write_num(os, c.cell[3 * a + b], lossless, b > 0);
+        os << '\n';
+    }
+    const bool forces = !energy_only, site = !energy_only && site_energy;
+    os << "AtomData: id type  cartes_x cartes_y cartes_z";
+    if (site)
+        os << " site_en";
+    if (forces)
+        os << " fx fy fz";
+    for (const auto &name : c.extra_names)
+        os << ' ' << name;
+    os << '\n';
+    const size_t ne = c.extra_names.size();
+    for (int i = 0; i < c.n; ++i) {
+        char buf[64];
+        if (lossless)
+            std::snprintf(buf, sizeof buf, "%d %d", i + 1, c.type[i]);
+        else
+            std::snprintf(buf, sizeof buf, " %-6d %-6d", i + 1, c.type[i]);
+        os << buf;
+        for (int a = 0; a < 3; ++a)
+            write_num(os, c.pos[3 * (size_t)i + a], lossless);
+        if (site)
+            write_num(os, c.site[i], lossless);
+        if (forces)
+            for (int a = 0; a < 3; ++a)
+                write_num(os, c.force[3 * (size_t)i + a], lossless);
+        for (size_t e = 0; e < ne; ++e)
+            write_num(os, c.extra[(size_t)i * ne + e], lossless);
+        os << '\n';
+    }
+    os << "Energy\n";
+    write_num(os, c.energy, lossless, !lossless);
+    os << '\n';
+    if (!energy_only) {
+        os << "PlusStress: xx yy zz yz xz xy\n";
+        const int order[6] = {0, 4, 8, 5, 2, 1};
+        for (int k = 0; k < 6; ++k)
+            write_num(os, c.stress[order[k]], lossless, k > 0 || !lossless);
+        os << '\n';
+    }
+    for (const auto &f : c.features)
+        os << f << '\n';
+    os << "END_CFG\n\n";
+}
+
+void check(mtpx_context *ctx, int rc, const char *what)
+{
+    if (rc != MTPX_OK)
+        die(std::string(what) + ": " + (ctx ? mtpx_last_error(ctx) : "error"));
+}
+
+}  // namespace
+
+int main(int argc, char **argv)
+{
+    std::string pot = "potential.mtp", in = "POSCAR", out = "output-efs.cfg";
+    bool energy_only = false, site_energy = true, lossless = false, progress = false;
+    bool deterministic = false;
+    int gpu = 0;
+    long batch_atoms = 0, batch_structures = 0;
+    for (int k = 1; k < argc; ++k) {
+        const std::string a = argv[k];
+        auto value = [&]() -> std::string {
+            if (k + 1 >= argc)
+                die("missing value for " + a);
+            return argv[++k];
+        };
+        if (a == "--pot" || a == "--potfile")
+            pot = value();
+        else if (a == "--in" || a == "--input")
+            in = value();
+        else if (a == "--out" || a == "--output")
+            out = value();
+        else if (a == "--energy-only")
+            energy_only = true;
+        else if (a == "--no-site-energy")
+            site_energy = false;
+        else if (a == "--lossless")
+            lossless = true;
+        else if (a == "--show-progress")
+            progress = true;
+        else if (a == "--deterministic")
+            deterministic = true;
+        else if (a == "--gpu-id")
+            gpu = std::atoi(value().c_str());
+        else if (a == "--gpu-batch-atoms")
+            batch_atoms = std::atol(value().c_str());
+        else if (a == "--gpu-batch-structures")
+            batch_structures = std::atol(value().c_str());
+        else if (a == "-h" || a == "--help") {
+            std::puts("mtpx_calc_efs --pot F.mtp --in F.cfg --out F.cfg [--energy-only] "
+                      "[--no-site-energy] [--lossless] [--show-progress] [--deterministic] "
+                      "[--gpu-id K] [--gpu-batch-atoms N] [--gpu-batch-structures N]");
+            return 0;
+        } else
+            die("unknown option " + a);
+    }
+    if (batch_atoms < 0 || batch_structures < 0)
+        die("GPU batch limits must be zero (automatic) or positive");
+    if (gpu < 0)
+        gpu = 0;
+
+    std::ifstream pf(pot);
+    if (!pf)
+        die("cannot read " + pot);
+    const std::string text((std::istreambuf_iterator<char>(pf)), {});
+    std::ifstream inf(in);
+    if (!inf)
+        die("cannot read " + in);
+    std::vector<Config> cfgs;
+    for (;;) {
+        Config c;
+        if (!read_config(inf, c, (int)cfgs.size()))
+            break;
+        cfgs.push_back(std::move(c));
+    }
+
+    mtpx_context *ctx = nullptr;
+    check(nullptr, mtpx_create(gpu, &ctx), "mtpx_create");
+    check(ctx, mtpx_load_model_text(ctx, text.c_str()), "load potential");
+    int info[8];
+    check(ctx, mtpx_model_info(ctx, info), "model info");
+    double cutoff = 0;
+    check(ctx, mtpx_model_cutoff(ctx, &cutoff), "model cutoff");
+    for (size_t c = 0; c < cfgs.size(); ++c)
+        for (int t : cfgs[c].type)
+            if (t >= info[0])
+                die("configuration " + std::to_string(c) + ": type " + std::to_string(t) +
+                    " but the potential has " + std::to_string(info[0]) + " species");
+
+    // structure-preserving chunks: at most batch_atoms atoms (2^21 by
+    // default) and batch_structures structures
+    const long max_atoms = batch_atoms > 0 ? batch_atoms : (1L << 21);
+    size_t done = 0, chunks = 0, total_atoms = 0;
+    for (size_t c0 = 0; c0 < cfgs.size();) {
+        size_t c1 = c0;
+        long atoms = 0;
+        while (c1 < cfgs.size() && (c1 == c0 || atoms + cfgs[c1].n <= max_atoms) &&
+               (batch_structures == 0 || (long)(c1 - c0) < batch_structures))
+            atoms += cfgs[c1++].n;
+        const int nconf = (int)(c1 - c0);
+        std::vector<int> off(nconf + 1, 0), pbc(3 * (size_t)nconf), types;
+        std::vector<double> cells(9 * (size_t)nconf), pos;
+        for (int k = 0; k < nconf; ++k) {
+            Config &c = cfgs[c0 + k];
+            off[k + 1] = off[k] + c.n;
+            for (int q = 0; q < 9; ++q)
+                cells[9 * (size_t)k + q] = c.cell[q];
+            for (int a = 0; a < 3; ++a)
+                pbc[3 * (size_t)k + a] = c.periodic ? 1 : 0;
+            // Atoms::wrap before the lists (calc_efs.cpp:195), as the
+            // reference writes the wrapped positions back
+            if (c.periodic)
+                check(ctx, mtpx_wrap(c.cell, &pbc[3 * (size_t)k], c.n, c.pos.data()), "wrap");
+            pos.insert(pos.end(), c.pos.begin(), c.pos.end());
+            types.insert(types.end(), c.type.begin(), c.type.end());
+        }
+        check(ctx, mtpx_set_structures(ctx, nconf, off.data(), cells.data(), pbc.data(),
+                                       pos.data(), types.data(), cutoff),
+              "neighbour lists");
+        std::vector<double> E(nconf), F(3 * (size_t)atoms), S(9 * (size_t)nconf), se(atoms);
+        if (energy_only)
+            check(ctx, mtpx_energy(ctx, E.data(), nullptr), "energy");
+        else
+            check(ctx, mtpx_compute_batch(ctx, deterministic ? 1 : 0, E.data(), F.data(),
+                                          S.data(), se.data()),
+                  "evaluation");
+        for (int k = 0; k < nconf; ++k) {
+            Config &c = cfgs[c0 + k];
+            c.energy = E[k];
+            if (!energy_only) {
+                c.force.assign(F.begin() + 3 * (size_t)off[k], F.begin() + 3 * (size_t)off[k + 1]);
+                c.site.assign(se.begin() + off[k], se.begin() + off[k + 1]);
+                std::memcpy(c.stress, &S[9 * (size_t)k], sizeof c.stress);
+            }
+        }
+        total_atoms += (size_t)atoms;
+        ++chunks;
+        done += nconf;
+        if (progress)
+            std::fprintf(stderr, "Calculated EFS %zu/%zu\n", done, cfgs.size());
+        c0 = c1;
+    }
+    std::ofstream of(out);
+    if (!of)
+        die("cannot write " + out);
+    for (const Config &c : cfgs)
+        write_config(of, c, lossless, energy_only, site_energy);
+    of.close();
+    if (!of)
+        die("error writing " + out);
+    std::fprintf(stderr, "mtpx_calc_efs: %zu structures, %zu atoms in %zu chunk(s)\n",
+                 cfgs.size(), total_atoms, chunks);
+    mtpx_destroy(ctx);
+    return 0;
+}

@@ -560,6 +560,16 @@ int mtpx_format_model_text(const char *text, char *buf, size_t cap, size_t *len,
     return copy_text(save_mtp(m), buf, cap, len);
 }
 
+int mtpx_model_cutoff(const mtpx_context *ctx, double *cutoff)
+{
+    if (!ctx || !cutoff)
+        return MTPX_E_INVALID;
+    if (!ctx->has_model)
+        return MTPX_E_NO_MODEL;
+    *cutoff = ctx->model.rmax;
+    return MTPX_OK;
+}
+
 int mtpx_model_info(const mtpx_context *ctx, int out8[8])
 {
     if (!ctx || !out8)

@@ -69,6 +69,11 @@ struct mtpx_context {
     long rows_gen = -1;  // label_gen and p of the uploaded row descriptors
     int rows_p = -1;
     int64_t rows_R = 0;
+    // Trainer_MTP::fix_species_coeffs: rows without the species columns,
+    // energy targets less the species part (the coefficients the rows
+    // were built with are kept to know when to rebuild them)
+    bool fix_species = false, rows_fix = false;
+    std::vector<double> rows_species;
     double lin_timings[4] = {0, 0, 0, 0};
     double train_timings[4] = {0, 0, 0, 0};
     hipEvent_t tev[4] = {nullptr, nullptr, nullptr, nullptr};

@@ -12,8 +12,6 @@
 //   lin_reduce_kernel energy and stress components per structure, ordered
 //   rows_kernel       AddLinearFast rows (train/train_mtp.cpp:1289-1395):
 //                     component rows scaled by sqrt(w), targets sqrt(w) y
-//   gram_kernel       [A y]^T [A y] on the fp64 matrix cores
-//                     (v_mfma_f64_16x16x4f64), partial per workgroup
 //
 // lin_site_kernel runs one wave per site.  The reference propagates the
 // Jacobian of every moment w.r.t. all 3 n_i coordinates through the rules.
@@ -36,8 +34,6 @@ namespace {
 namespace mtpx {
 
 namespace {
-
-typedef double d4v __attribute__((ext_vector_type(4)));
 
 // Read-only model table in the constant address space: wave-uniform
 // indices compile to scalar loads (SGPRs, no VALU work).
@@ -557,80 +553,6 @@ __global__ __launch_bounds__(256) void rows_kernel(const double *comp, const int
         y[r] = yw[r];
 }
 
-// Gram of the extended rows e_r = [sw_r comp[src_r + q] (q < p), y_r, 0...]
-// (length pp, a multiple of 16).  Workgroup (x, y) sums e_r e_r^T over row
-// range x for the 16 output tiles of group y (4 per wave) on the matrix cores
-// and writes them into partial x (pp x pp).
-//
-// v_mfma_f64_16x16x4f64: A operand 16x4 (lane l holds A[l%16][l/16]), B
-// operand 4x16 (lane l holds B[l/16][l%16]), result 16x16 with lane l
-// holding D[l/16 + 4v][l%16], v = 0..3.  For the tile (I, J) of the Gram,
-// A[i][k] = e_{r+k}[16I+i] and B[k][j] = e_{r+k}[16J+j].
-constexpr int kGramRows = 32;   // rows staged per step
-constexpr int kGramPad = 2;     // LDS row padding (doubles)
-constexpr int kTilesPerWave = 4;
-
-__global__ __launch_bounds__(256) void gram_kernel(const double *comp, const int64_t *src,
-                                                   const double *sw, const double *yw, int64_t R,
-                                                   int p, int pp, int64_t rows_per_block,
-                                                   double *partial)
-{
-    extern __shared__ double tile[];  // [kGramRows][pp + kGramPad]
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int ld = pp + kGramPad;
-    const int nt = pp / 16;
-    const int ntiles = nt * nt;
-    const int tile0 = blockIdx.y * 4 * kTilesPerWave + wave * kTilesPerWave;
-    d4v accv[kTilesPerWave];
-#pragma unroll
-    for (int k = 0; k < kTilesPerWave; ++k)
-        accv[k] = d4v{0.0, 0.0, 0.0, 0.0};
-    const int64_t r0 = (int64_t)blockIdx.x * rows_per_block;
-    const int64_t r1 = min(R, r0 + rows_per_block);
-    for (int64_t rb = r0; rb < r1; rb += kGramRows) {
-        __syncthreads();
-        for (int t = tid; t < kGramRows * pp; t += blockDim.x) {
-            const int rr = t / pp, q = t % pp;
-            const int64_t r = rb + rr;
-            double v = 0.0;
-            if (r < r1) {
-                if (q < p)
-                    v = sw[r] * comp[src[r] + q];
-                else if (q == p)
-                    v = yw[r];
-            }
-            tile[rr * ld + q] = v;
-        }
-        __syncthreads();
-#pragma unroll
-        for (int k = 0; k < kTilesPerWave; ++k) {
-            const int t = tile0 + k;
-            if (t < ntiles) {
-                const int I = t / nt, J = t % nt;
-                d4v cacc = accv[k];
-#pragma unroll
-                for (int k4 = 0; k4 < kGramRows; k4 += 4) {
-                    const double a = tile[(k4 + lane / 16) * ld + 16 * I + lane % 16];
-                    const double b = tile[(k4 + lane / 16) * ld + 16 * J + lane % 16];
-                    cacc = __builtin_amdgcn_mfma_f64_16x16x4f64(a, b, cacc, 0, 0, 0);
-                }
-                accv[k] = cacc;
-            }
-        }
-    }
-    double *out = partial + (size_t)blockIdx.x * pp * pp;
-#pragma unroll
-    for (int k = 0; k < kTilesPerWave; ++k) {
-        const int t = tile0 + k;
-        if (t < ntiles) {
-            const int I = t / nt, J = t % nt;
-#pragma unroll
-            for (int v = 0; v < 4; ++v)
-                out[(size_t)(16 * I + lane / 16 + 4 * v) * pp + 16 * J + lane % 16] = accv[k][v];
-        }
-    }
-}
-
 // Waves per workgroup: the level-10 kernel fits 256 registers (eight waves);
 // the others use up to 512 (one wave per SIMD).
 template <class P>
@@ -749,21 +671,6 @@ hipError_t launch_lin_rows(const double *comp, const int64_t *src, const double 
     if (work > 0)
         hipLaunchKernelGGL(rows_kernel, dim3((unsigned)((work + 255) / 256)), dim3(256), 0, s,
                            comp, src, sw, yw, R, p, A, y);
-    return hipGetLastError();
-}
-
-int gram_padded(int p) { return (p + 1 + 15) / 16 * 16; }
-
-hipError_t launch_gram(const double *comp, const int64_t *src, const double *sw, const double *yw,
-                       int64_t R, int p, int nblocks, double *partial, hipStream_t s)
-{
-    const int pp = gram_padded(p);
-    const int64_t per = ((R + nblocks - 1) / nblocks + kGramRows - 1) / kGramRows * kGramRows;
-    const size_t lds = sizeof(double) * kGramRows * (pp + kGramPad);
-    const int nt = pp / 16;
-    const int groups = (nt * nt + 4 * kTilesPerWave - 1) / (4 * kTilesPerWave);
-    hipLaunchKernelGGL(gram_kernel, dim3(nblocks, groups), dim3(256), lds, s, comp, src, sw, yw, R,
-                       p, pp, std::max<int64_t>(per, kGramRows), partial);
     return hipGetLastError();
 }
 

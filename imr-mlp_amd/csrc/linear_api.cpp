@@ -126,9 +126,33 @@ int build_rows(mtpx_context *ctx, int64_t &R)
     if (!ctx->has_labels)
         return set_error(ctx, MTPX_E_INVALID, "no labels");
     const CompLayout cl = comp_layout(ctx);
-    if (ctx->rows_gen == ctx->label_gen && ctx->rows_p == cl.p) {
+    const Model &M = ctx->model;
+    const bool fix = ctx->fix_species;
+    std::vector<double> csp;
+    if (fix)
+        csp.assign(M.coef.begin() + M.nradial(), M.coef.begin() + M.nradial() + M.Z);
+    if (ctx->rows_gen == ctx->label_gen && ctx->rows_p == cl.p && ctx->rows_fix == fix &&
+        (!fix || ctx->rows_species == csp)) {
         R = ctx->rows_R;  // descriptors of these labels are resident
         return MTPX_OK;
+    }
+    // fix_species_coeffs (train/train_mtp.cpp:1300-1302, 1381-1392): rows
+    // start at the moment columns; energy targets less sum_s n_s c_s
+    const size_t off = fix ? (size_t)M.Z : 0;
+    std::vector<double> esub((size_t)ctx->nconf, 0.0);
+    if (fix && ctx->n > 0) {
+        std::vector<int> ct((size_t)ctx->n);
+        HIP_TRY(hipMemcpyAsync(ct.data(), ctx->center_type.p, sizeof(int) * ct.size(),
+                               hipMemcpyDeviceToHost, ctx->stream),
+                "copy species");
+        HIP_TRY(hipStreamSynchronize(ctx->stream), "copy species");
+        for (int c = 0; c < ctx->nconf; ++c) {
+            std::vector<double> cnt((size_t)M.Z, 0.0);
+            for (int i = ctx->soff_host[c]; i < ctx->soff_host[c + 1]; ++i)
+                cnt[(size_t)ct[i]] += 1.0;
+            for (int t = 0; t < M.Z; ++t)
+                esub[c] += cnt[t] * csp[t];
+        }
     }
     std::vector<int64_t> src;
     std::vector<double> sw, yw;
@@ -141,7 +165,7 @@ int build_rows(mtpx_context *ctx, int64_t &R)
                     continue;
                 const double w = std::sqrt(ctx->wF_h[i]);
                 for (int a = 0; a < 3; ++a) {
-                    src.push_back((int64_t)(cl.fc + ((size_t)i * 3 + a) * cl.p));
+                    src.push_back((int64_t)(cl.fc + ((size_t)i * 3 + a) * cl.p + off));
                     sw.push_back(w);
                     yw.push_back(w * ctx->tF_h[3 * (size_t)i + a]);
                 }
@@ -149,16 +173,16 @@ int build_rows(mtpx_context *ctx, int64_t &R)
         if (act[2]) {
             const double w = std::sqrt(ctx->wS_h[c]);
             for (int q = 0; q < 9; ++q) {
-                src.push_back((int64_t)(cl.sc + ((size_t)c * 9 + q) * cl.p));
+                src.push_back((int64_t)(cl.sc + ((size_t)c * 9 + q) * cl.p + off));
                 sw.push_back(w);
                 yw.push_back(w * ctx->tS_h[9 * (size_t)c + q]);
             }
         }
         if (act[0]) {
             const double w = std::sqrt(ctx->wE_h[c]);
-            src.push_back((int64_t)(cl.ec + (size_t)c * cl.p));
+            src.push_back((int64_t)(cl.ec + (size_t)c * cl.p + off));
             sw.push_back(w);
-            yw.push_back(w * ctx->tE_h[c]);
+            yw.push_back(w * (ctx->tE_h[c] - esub[c]));
         }
     }
     R = (int64_t)src.size();
@@ -168,7 +192,15 @@ int build_rows(mtpx_context *ctx, int64_t &R)
     ctx->rows_gen = ctx->label_gen;
     ctx->rows_p = cl.p;
     ctx->rows_R = R;
+    ctx->rows_fix = fix;
+    ctx->rows_species = csp;
     return MTPX_OK;
+}
+
+// Columns of a linear-fit row: Z + S, or S with the species coefficients fixed.
+int row_width(const mtpx_context *ctx)
+{
+    return ctx->model.S + (ctx->fix_species ? 0 : ctx->model.Z);
 }
 
 }  // namespace
@@ -226,7 +258,7 @@ int mtpx_linear_rows(mtpx_context *ctx, int64_t *nrows, double *A, double *y)
     rc = run_lin(ctx);
     if (rc != MTPX_OK)
         return rc;
-    const int p = ctx->model.Z + ctx->model.S;
+    const int p = row_width(ctx);
     HIP_TRY(ctx->rowsA.ensure(sizeof(double) * std::max<int64_t>(R * p, 1)), "allocate rows");
     HIP_TRY(ctx->rowsY.ensure(sizeof(double) * std::max<int64_t>(R, 1)), "allocate rows");
     HIP_TRY(launch_lin_rows(ctx->comp.as<double>(), ctx->row_src.as<int64_t>(),
@@ -252,6 +284,8 @@ int mtpx_linear_system(mtpx_context *ctx, double *G, double *b)
         return set_error(ctx, MTPX_E_NO_TOPOLOGY, "no structures");
     if (!ctx->has_model)
         return set_error(ctx, MTPX_E_NO_MODEL, "no model loaded");
+    if (!gram_fits(row_width(ctx)))
+        return set_error(ctx, MTPX_E_CAPACITY, "linear system of more than 1007 coefficients");
     (void)hipSetDevice(ctx->device);
     int64_t R = 0;
     int rc = build_rows(ctx, R);
@@ -266,24 +300,20 @@ int mtpx_linear_system(mtpx_context *ctx, double *G, double *b)
     if (rc != MTPX_OK)
         return rc;
     HIP_TRY(hipEventRecord(ctx->tev[1], s), "record event");
-    const int p = ctx->model.Z + ctx->model.S;
+    const int p = row_width(ctx);
     const int pp = gram_padded(p);
     HIP_TRY(ctx->gram_out.ensure(sizeof(double) * pp * pp), "allocate Gram");
     if (R == 0) {
         HIP_TRY(hipMemsetAsync(ctx->gram_out.p, 0, sizeof(double) * pp * pp, s), "clear Gram");
     } else {
-        const int nblocks =
-            (int)std::max<int64_t>(1, std::min<int64_t>((R + 255) / 256, 4LL * ctx->num_cus));
-        HIP_TRY(ctx->gram_part.ensure(sizeof(double) * (size_t)nblocks * pp * pp),
+        const int nblocks = gram_blocks(R, p, ctx->num_cus);
+        HIP_TRY(ctx->gram_part.ensure(sizeof(double) * gram_partial_doubles(p, nblocks)),
                 "allocate Gram partials");
         HIP_TRY(launch_gram(ctx->comp.as<double>(), ctx->row_src.as<int64_t>(),
                             ctx->row_sw.as<double>(), ctx->row_y.as<double>(), R, p, nblocks,
-                            ctx->gram_part.as<double>(), s),
+                            ctx->gram_part.as<double>(), ctx->gram_out.as<double>(), s),
                 "launch Gram");
         HIP_TRY(hipEventRecord(ctx->tev[2], s), "record event");
-        HIP_TRY(launch_rows_reduce(ctx->gram_part.as<double>(), nblocks, pp * pp,
-                                   ctx->gram_out.as<double>(), false, s),
-                "launch Gram reduction");
     }
     std::vector<double> g((size_t)pp * pp);
     HIP_TRY(hipMemcpyAsync(g.data(), ctx->gram_out.p, sizeof(double) * pp * pp,
@@ -312,6 +342,14 @@ int mtpx_linear_system(mtpx_context *ctx, double *G, double *b)
 // radial function k, subtract from c_k its projection on every earlier c_k2
 // -- divided by |c_k|^2, the reference's choice, not |c_k2|^2 -- then
 // normalise with sqrt(sum (c^2 + 1e-10)).  Vectors run over (ti, tj, k).
+int mtpx_set_fix_species_coeffs(mtpx_context *ctx, int fix)
+{
+    if (!ctx)
+        return MTPX_E_INVALID;
+    ctx->fix_species = fix != 0;
+    return MTPX_OK;
+}
+
 int mtpx_orthogonalize(mtpx_context *ctx)
 {
     if (!ctx)

@@ -333,8 +333,15 @@ hipError_t launch_lin_rows(const double *comp, const int64_t *src, const double 
                            const double *yw, int64_t R, int p, double *A, double *y, hipStream_t s);
 // Gram columns padded to a multiple of 16 (p coefficients plus the target).
 int gram_padded(int p);
+// Whether the Gram kernel stages rows of p + 1 values (p <= 1007).
+bool gram_fits(int p);
+// Row ranges of the Gram for R rows, and the partial buffer they need.
+int gram_blocks(int64_t R, int p, int num_cus);
+size_t gram_partial_doubles(int p, int nblocks);
+// [A y]^T [A y] of the R extended rows into out (pp x pp), through the
+// partials; the sums run in a fixed order for a given R and nblocks.
 hipError_t launch_gram(const double *comp, const int64_t *src, const double *sw, const double *yw,
-                       int64_t R, int p, int nblocks, double *partial, hipStream_t s);
+                       int64_t R, int p, int nblocks, double *partial, double *out, hipStream_t s);
 
 // Training (train_kernel.hip).
 struct LossArgs {

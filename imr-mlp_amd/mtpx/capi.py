@@ -85,6 +85,7 @@ def lib():
         L.mtpx_orthogonalize.argtypes = [C.c_void_p]
         L.mtpx_last_linear_timings.argtypes = [C.c_void_p, _dp]
         L.mtpx_set_add_efs.argtypes = [C.c_void_p, C.c_int]
+        L.mtpx_set_fix_species_coeffs.argtypes = [C.c_void_p, C.c_int]
         L.mtpx_lbfgs_default_params.argtypes = [C.POINTER(LbfgsParams)]
         L.mtpx_lbfgs_default_params.restype = None
         L.mtpx_train_lbfgs.argtypes = [C.c_void_p, C.POINTER(LbfgsParams), _dp, _dp, C.c_int,
@@ -530,17 +531,25 @@ class Context:
         self._check(lib().mtpx_efs_components(self.h, _d(ec), _d(fc), _d(sc)), "efs_components")
         return ec[:nc], fc[:n], sc[:nc].reshape(nc, 3, 3, p)
 
+    def set_fix_species_coeffs(self, fix: bool):
+        self._check(lib().mtpx_set_fix_species_coeffs(self.h, int(bool(fix))),
+                    "set_fix_species_coeffs")
+        self.fix_species = bool(fix)
+
+    def _row_width(self):
+        return self.info["S"] + (0 if getattr(self, "fix_species", False) else self.info["Z"])
+
     def linear_rows(self):
         R = C.c_int64(0)
         self._check(lib().mtpx_linear_rows(self.h, C.byref(R), None, None), "linear_rows")
-        p = self.info["Z"] + self.info["S"]
+        p = self._row_width()
         A = np.zeros((max(R.value, 1), p))
         y = np.zeros(max(R.value, 1))
         self._check(lib().mtpx_linear_rows(self.h, C.byref(R), _d(A), _d(y)), "linear_rows")
         return A[:R.value], y[:R.value]
 
     def linear_system(self):
-        p = self.info["Z"] + self.info["S"]
+        p = self._row_width()
         G = np.zeros((p, p))
         b = np.zeros(p)
         self._check(lib().mtpx_linear_system(self.h, _d(G), _d(b)), "linear_system")

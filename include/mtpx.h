@@ -93,6 +93,9 @@ int mtpx_format_model_text(const char *text, char *buf, size_t cap, size_t *len,
                            int errlen);
 /* Sizes: Z M R K B T S ncoef (ncoef = Z*Z*M*R + Z + S). */
 int mtpx_model_info(const mtpx_context *ctx, int out8[8]);
+/* PotMTP::cutoff (potentials/potential_mtp.cpp:300-310): the largest
+ * max_dist of the radial bases, the list cutoff of the model. */
+int mtpx_model_cutoff(const mtpx_context *ctx, double *cutoff);
 /* PotMTP::get_coeffs / set_coeffs (potential_mtp.cpp:4160-4245) in the flat
  * order [radial | species | moment]; MTPGpuDirect::update_coefficients
  * (mtp_gpu_direct.h:813-818). */
@@ -370,9 +373,16 @@ int mtpx_efs_components(mtpx_context *ctx, double *energy_cmpts, double *force_c
  * with A and y NULL only *nrows is set, otherwise *nrows is the capacity on
  * entry and the count on return. */
 int mtpx_linear_rows(mtpx_context *ctx, int64_t *nrows, double *A, double *y);
+/* Trainer_MTP::fix_species_coeffs (train/train_mtp.cpp:1300-1302,
+ * 1381-1392): 1 makes mtpx_linear_rows and mtpx_linear_system leave out the
+ * Z species columns (rows of S values, p = S) and subtract
+ * sum_s n_s species_coeffs[s] (the model's current species coefficients)
+ * from each energy target; 0 (the default) keeps p = Z + S. */
+int mtpx_set_fix_species_coeffs(mtpx_context *ctx, int fix);
 /* Trainer_MTP::TrainLinearFast assembly (train/train_mtp.cpp:2383-2427):
  * G = A^T A [p][p] and b = A^T y [p] over the rows of mtpx_linear_rows,
- * summed on the fp64 matrix cores in a fixed order. */
+ * summed on the fp64 matrix cores in a fixed order; p <= 1007
+ * (MTPX_E_CAPACITY beyond). */
 int mtpx_linear_system(mtpx_context *ctx, double *G, double *b);
 /* PotMTP::Orthogonalize (potentials/potential_mtp.cpp:3849-3930) of the
  * radial coefficients; TrainLinearFast calls it before the assembly. */

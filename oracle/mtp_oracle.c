@@ -2212,7 +2212,18 @@ int64_t orc_linear_row_count(const orc_loss_settings *s, const orc_config *c)
 int64_t orc_linear_rows(const orc_model *m, const orc_nbh *h, const orc_loss_settings *s,
                         const orc_config *c, double *A, double *y)
 {
+    return orc_linear_rows_ex(m, h, s, c, 0, A, y);
+}
+
+/* With fix_species (Trainer_MTP::fix_species_coeffs, train_mtp.cpp:1300-1302,
+ * 1381-1392) every row drops the Z species columns (soffset = Z, rows of
+ * n_size_mat = S values) and the energy target becomes
+ * E - sum_s energy_cmpts[s] species_coeffs[s]. */
+int64_t orc_linear_rows_ex(const orc_model *m, const orc_nbh *h, const orc_loss_settings *s,
+                           const orc_config *c, int fix_species, double *A, double *y)
+{
     const int p = m->Z + m->S, N = c->n;
+    const int off = fix_species ? m->Z : 0, w = p - off;
     double *ec = (double *)calloc((size_t)p, sizeof(double));
     double *fc = (double *)calloc((size_t)N * 3 * p + 1, sizeof(double));
     double *sc = (double *)calloc(9 * (size_t)p, sizeof(double));
@@ -2227,8 +2238,8 @@ int64_t orc_linear_rows(const orc_model *m, const orc_nbh *h, const orc_loss_set
                 continue;
             double sw = sqrt(wi);
             for (int a = 0; a < 3; ++a) {
-                for (int q = 0; q < p; ++q)
-                    A[row * p + q] = fc[((size_t)iat * 3 + a) * p + q] * sw;
+                for (int q = 0; q < w; ++q)
+                    A[row * w + q] = fc[((size_t)iat * 3 + a) * p + off + q] * sw;
                 y[row] = sw * c->forces[3 * iat + a];
                 row++;
             }
@@ -2237,17 +2248,21 @@ int64_t orc_linear_rows(const orc_model *m, const orc_nbh *h, const orc_loss_set
     if (s->weight_stress > 0 && c->has_stress) {
         double sw = sqrt(s->weight_stress / pow(N, s->stress_pow) * cc);
         for (int q9 = 0; q9 < 9; ++q9) {
-            for (int q = 0; q < p; ++q)
-                A[row * p + q] = sc[(size_t)q9 * p + q] * sw;
+            for (int q = 0; q < w; ++q)
+                A[row * w + q] = sc[(size_t)q9 * p + off + q] * sw;
             y[row] = sw * c->stress[q9];
             row++;
         }
     }
     if (s->weight_eng > 0 && c->has_energy) {
         double sw = sqrt(s->weight_eng / pow(N, s->eng_pow) * c->fitness * cc);
-        for (int q = 0; q < p; ++q)
-            A[row * p + q] = ec[q] * sw;
-        y[row] = sw * c->energy;
+        for (int q = 0; q < w; ++q)
+            A[row * w + q] = ec[off + q] * sw;
+        double sub = 0;
+        if (fix_species)
+            for (int t = 0; t < m->Z; ++t)
+                sub += ec[t] * m->coef[m->nradial + t];
+        y[row] = sw * (c->energy - sub);
         row++;
     }
     free(ec);
@@ -2282,13 +2297,20 @@ int orc_linear_system_batch(const orc_model *m, int nconf, orc_nbh *const *hs,
                             const orc_config *cs, const orc_loss_settings *s, int nthreads,
                             double *G, double *b)
 {
+    return orc_linear_system_batch_ex(m, nconf, hs, cs, s, 0, nthreads, G, b);
+}
+
+int orc_linear_system_batch_ex(const orc_model *m, int nconf, orc_nbh *const *hs,
+                               const orc_config *cs, const orc_loss_settings *s, int fix_species,
+                               int nthreads, double *G, double *b)
+{
 #ifdef _OPENMP
     if (nthreads <= 0)
         nthreads = omp_get_max_threads();
 #else
     nthreads = 1;
 #endif
-    const int p = m->Z + m->S;
+    const int p = m->Z + m->S - (fix_species ? m->Z : 0);
     double *tG = (double *)calloc((size_t)nthreads * p * p, sizeof(double));
     double *tb = (double *)calloc((size_t)nthreads * p, sizeof(double));
     int actual = 1;
@@ -2309,7 +2331,7 @@ int orc_linear_system_batch(const orc_model *m, int nconf, orc_nbh *const *hs,
             int64_t rows = orc_linear_row_count(s, cs + c);
             double *A = (double *)calloc((size_t)(rows > 0 ? rows : 1) * p, sizeof(double));
             double *y = (double *)calloc((size_t)(rows > 0 ? rows : 1), sizeof(double));
-            orc_linear_rows(m, hs[c], s, cs + c, A, y);
+            orc_linear_rows_ex(m, hs[c], s, cs + c, fix_species, A, y);
             orc_gram(rows, p, A, y, tG + (size_t)it * p * p, tb + (size_t)it * p);
             free(A);
             free(y);

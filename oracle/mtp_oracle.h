@@ -137,11 +137,18 @@ void orc_efs_components(const orc_model *m, const orc_nbh *h, double *energy_cmp
                         double *force_cmpts /* [n][3][p] */, double *stress_cmpts /* [3][3][p] */);
 int64_t orc_linear_rows(const orc_model *m, const orc_nbh *h, const orc_loss_settings *s,
                         const orc_config *c, double *A, double *y);
+/* orc_linear_rows with Trainer_MTP::fix_species_coeffs: rows of S values
+ * (the species columns dropped), energy targets less the species part. */
+int64_t orc_linear_rows_ex(const orc_model *m, const orc_nbh *h, const orc_loss_settings *s,
+                           const orc_config *c, int fix_species, double *A, double *y);
 int64_t orc_linear_row_count(const orc_loss_settings *s, const orc_config *c);
 void orc_gram(int64_t rows, int p, const double *A, const double *y, double *G, double *b);
 int orc_linear_system_batch(const orc_model *m, int nconf, orc_nbh *const *hs,
                             const orc_config *cs, const orc_loss_settings *s, int nthreads,
                             double *G, double *b);
+int orc_linear_system_batch_ex(const orc_model *m, int nconf, orc_nbh *const *hs,
+                               const orc_config *cs, const orc_loss_settings *s, int fix_species,
+                               int nthreads, double *G, double *b);
 
 /* ---- flop convention shared with the benchmark ---------------------- */
 double orc_efs_flops(const orc_model *m, const orc_nbh *h);

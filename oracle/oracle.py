@@ -89,6 +89,12 @@ def lib():
         L.orc_efs_components.argtypes = [C.c_void_p, C.c_void_p, _dp, _dp, _dp]
         L.orc_linear_rows.restype = C.c_int64
         L.orc_linear_rows.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, _dp, _dp]
+        L.orc_linear_rows_ex.restype = C.c_int64
+        L.orc_linear_rows_ex.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int,
+                                         _dp, _dp]
+        L.orc_linear_system_batch_ex.argtypes = [C.c_void_p, C.c_int, C.POINTER(C.c_void_p),
+                                                 C.c_void_p, C.c_void_p, C.c_int, C.c_int, _dp,
+                                                 _dp]
         L.orc_linear_row_count.restype = C.c_int64
         L.orc_linear_row_count.argtypes = [C.c_void_p, C.c_void_p]
         L.orc_gram.argtypes = [C.c_int64, C.c_int, _dp, _dp, _dp, _dp]
@@ -397,14 +403,16 @@ def efs_components(model, nb):
     return ec, fc[:nb.n], sc
 
 
-def linear_rows(model, nb, settings, labels: Labels):
-    """AddLinearFast rows (train/train_mtp.cpp:1289-1395): F, S, E, scaled by sqrt(w)."""
+def linear_rows(model, nb, settings, labels: Labels, fix_species=False):
+    """AddLinearFast rows (train/train_mtp.cpp:1289-1395): F, S, E, scaled by
+    sqrt(w); fix_species drops the species columns (fix_species_coeffs)."""
     cfg = labels.cstruct()
     rows = int(lib().orc_linear_row_count(C.byref(settings), C.byref(cfg)))
-    p = model.Z + model.S
+    p = model.S if fix_species else model.Z + model.S
     A = np.zeros((max(rows, 1), p))
     y = np.zeros(max(rows, 1))
-    got = lib().orc_linear_rows(model.h, nb.h, C.byref(settings), C.byref(cfg), _d(A), _d(y))
+    got = lib().orc_linear_rows_ex(model.h, nb.h, C.byref(settings), C.byref(cfg),
+                                   int(bool(fix_species)), _d(A), _d(y))
     assert got == rows
     return A[:rows], y[:rows]
 
@@ -419,14 +427,15 @@ def gram(A, y):
     return G, b
 
 
-def linear_system_batch(model, nbs, labels, settings, threads=0):
+def linear_system_batch(model, nbs, labels, settings, threads=0, fix_species=False):
     arr = (C.c_void_p * len(nbs))(*[nb.h for nb in nbs])
     cfgs = (_Config * len(labels))(*[lb.cstruct() for lb in labels])
-    p = model.Z + model.S
+    p = model.S if fix_species else model.Z + model.S
     G = np.zeros((p, p))
     b = np.zeros(p)
-    lib().orc_linear_system_batch(model.h, len(nbs), arr, C.cast(cfgs, C.c_void_p),
-                                  C.byref(settings), int(threads), _d(G), _d(b))
+    lib().orc_linear_system_batch_ex(model.h, len(nbs), arr, C.cast(cfgs, C.c_void_p),
+                                     C.byref(settings), int(bool(fix_species)), int(threads),
+                                     _d(G), _d(b))
     return G, b
 
 

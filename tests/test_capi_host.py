@@ -45,6 +45,62 @@ def test_wrap_is_bit_exact_against_oracle():
         assert np.array_equal(a.view(np.uint64), b.view(np.uint64))
 
 
+def _lattice_offsets(delta, basis):
+    """Least-squares coefficients of delta over the rows of basis."""
+    k, *_ = np.linalg.lstsq(basis.T, delta.T, rcond=None)
+    return k.T
+
+
+def test_singular_cell_wrap_known_answers():
+    """wrap_singular_cell (base/structures.cpp:97-130): a line (rank 1) wraps
+    x into [0, L); the non-periodic coordinates are untouched."""
+    cell = np.array([[3.0, 0, 0], [0, 0, 0], [0, 0, 0]])
+    pos = np.array([[7.5, 1.0, -2.0], [-0.5, 4.0, 9.0], [0.0, 0.0, 0.0], [3.0, 1.0, 1.0]])
+    out = capi.wrap(cell, [1, 0, 0], pos)
+    assert np.array_equal(out[:, 1:], pos[:, 1:])
+    assert np.array_equal(out[:, 0], [1.5, 2.5, 0.0, 0.0])
+    # nothing periodic: unchanged
+    assert np.array_equal(capi.wrap(cell, [0, 0, 0], pos), pos)
+
+
+@pytest.mark.parametrize("seed", range(4))
+def test_singular_cell_wrap_slab(seed):
+    """A slab: two periodic rows and a zero (or dependent) third row.  Every
+    position moves by an integer combination of the periodic rows and lands
+    with dual coordinates in [0, 1)."""
+    rng = np.random.default_rng(seed)
+    a1 = rng.standard_normal(3) * 3
+    a2 = rng.standard_normal(3) * 3
+    third = np.zeros(3) if seed % 2 == 0 else a1 + a2  # singular either way
+    cell = np.array([a1, a2, third])
+    pos = rng.standard_normal((50, 3)) * 10
+    out = capi.wrap(cell, [1, 1, 0], pos)
+    basis = np.array([a1, a2])
+    k = _lattice_offsets(pos - out, basis)
+    assert np.abs(k - np.round(k)).max() < 1e-9
+    # the component normal to the plane is kept
+    nrm = np.cross(a1, a2)
+    assert np.abs((out - pos) @ nrm).max() < 1e-9 * np.abs(pos @ nrm).max()
+    dual = np.linalg.solve(basis @ basis.T, basis)
+    c = out @ dual.T
+    assert c.min() > -1e-12 and c.max() < 1 + 1e-12
+    # a second pass moves nothing by more than rounding
+    assert np.abs(capi.wrap(cell, [1, 1, 0], out) - out).max() < 1e-12
+
+
+def test_singular_cell_wrap_refusals():
+    """Dependent periodic rows and non-finite rows raise, as the reference
+    throws."""
+    a = np.array([2.0, 0.5, 0.0])
+    pos = np.zeros((1, 3))
+    with pytest.raises(capi.MtpxError):
+        capi.wrap(np.array([a, 2 * a, [0, 0, 0]]), [1, 1, 0], pos)
+    with pytest.raises(capi.MtpxError):
+        capi.wrap(np.array([a, [np.inf, 0, 0], [0, 0, 0]]), [1, 1, 0], pos)
+    with pytest.raises(capi.MtpxError):  # all three periodic and singular
+        capi.wrap(np.array([a, [0, 1.0, 0], a]), [1, 1, 1], pos)
+
+
 @pytest.mark.parametrize("name", ["shapeev-10.mtp", "shapeev-16.mtp", "shapeev-20.mtp",
                                   "shapeev-20-t.mtp", "shapeev-06.mtp"])
 def test_parser_matches_oracle(name):

@@ -151,6 +151,74 @@ def test_gram_of_the_device_rows(ctx, crystal_set):
     assert rel_err(G, Gt) < 1e-12 and rel_err(b, bt) < 1e-12
 
 
+@pytest.mark.parametrize("name", ["shapeev-20.mtp", "pot4b.mtp"])
+def test_gram_of_wide_systems(ctx, name):
+    """Wider normal equations (p = 290 and 758: several tile groups and
+    shorter LDS row blocks) against the oracle's assembly and the textbook
+    sum of the device's own rows."""
+    rng = S.rng_for(91)
+    if name == "pot4b.mtp":
+        text = S.read_template(name)
+    else:
+        text = S.random_model(name, 2, 8, 1.9, 5.0, -0.1, 0.1, rng)
+    m = O.Model(text)
+    structs, nbs, labels = [], [], []
+    for k in range(2):
+        s = S.displace(S.lattice("bcc", (2, 2, 2 + k), 2.87), rng, 0.1)
+        s.types = (S.uniform(rng, s.n) * 2).astype(np.int32)
+        s.pos = O.wrap(s.cell, s.pbc, s.pos)
+        nb = O.Neighbors.build(s.cell, s.pbc, s.pos, s.types, m.cutoff)
+        E, F, St, _ = O.efs(m, nb)
+        e, f, st = S.noisy_labels(rng, s.n, E, F, St)
+        structs.append(s)
+        nbs.append(nb)
+        labels.append(O.Labels(s.n, energy=e, forces=f, stress=st))
+    st = SETTINGS["linear"]
+    _upload(ctx, text, structs, labels, st, cutoff=m.cutoff)
+    G, b = ctx.linear_system()
+    assert G.shape == (m.Z + m.S, m.Z + m.S)
+    A, y = ctx.linear_rows()
+    Gt, bt = O.gram(A, y)
+    assert rel_err(G, Gt) < 1e-12 and rel_err(b, bt) < 1e-12
+    Go, bo = O.linear_system_batch(m, nbs, labels, st, threads=8)
+    assert rel_err(G, Go) < 1e-10 and rel_err(b, bo) < 1e-10
+
+
+def test_fixed_species_coefficients(ctx, crystal_set):
+    """fix_species_coeffs: rows without the species columns and energy
+    targets less the species part, against the oracle; the rows follow a
+    change of the species coefficients; switching back restores p = Z + S."""
+    text, structs, nbs, labels = crystal_set
+    st = SETTINGS["per-atom"]
+    _upload(ctx, text, structs, labels, st)
+    m = O.Model(text)
+    try:
+        ctx.set_fix_species_coeffs(True)
+        A, y = ctx.linear_rows()
+        Ao = np.concatenate([O.linear_rows(m, nb, st, lb, fix_species=True)[0]
+                             for nb, lb in zip(nbs, labels)])
+        yo = np.concatenate([O.linear_rows(m, nb, st, lb, fix_species=True)[1]
+                             for nb, lb in zip(nbs, labels)])
+        assert A.shape == (Ao.shape[0], m.S)
+        assert rel_err(A, Ao) < 1e-10 and rel_err(y, yo) < 1e-10
+        G, b = ctx.linear_system()
+        Go, bo = O.linear_system_batch(m, nbs, labels, st, threads=8, fix_species=True)
+        assert rel_err(G, Go) < 1e-10 and rel_err(b, bo) < 1e-10
+        # new species coefficients: new energy targets, same matrix
+        c = ctx.get_coeffs()
+        c[m.nradial:m.nradial + m.Z] += np.array([0.3, -0.2])
+        ctx.set_coeffs(c)
+        m.coeffs = c
+        G2, b2 = ctx.linear_system()
+        Go2, bo2 = O.linear_system_batch(m, nbs, labels, st, threads=8, fix_species=True)
+        assert rel_err(b2, bo2) < 1e-10 and rel_err(G2, G) < 1e-12
+        assert rel_err(b2, b) > 1e-6
+    finally:
+        ctx.set_fix_species_coeffs(False)
+    G, b = ctx.linear_system()
+    assert G.shape == (m.Z + m.S, m.Z + m.S)
+
+
 def test_orthogonalize_matches_oracle(ctx):
     text, _ = S.training_models(4)
     m = O.Model(text)

@@ -280,6 +280,33 @@ def test_linear_rows_weights_and_gram():
     assert rel_err(lin @ G @ lin - 2 * lin @ b + y @ y, loss) < 1e-8
 
 
+def test_linear_rows_with_fixed_species_coefficients():
+    """fix_species_coeffs (train_mtp.cpp:1300-1302, 1381-1392): for any
+    moment coefficients theta, the reduced rows give the same residuals as
+    the full rows with the species coefficients held at the model's values,
+    and the loss at the model's own coefficients is unchanged."""
+    m, nb, lab = _config()
+    st = O.LossSettings.make(weight_eng=1.0, weight_force=0.01, weight_stress=1e-3)
+    A, y = O.linear_rows(m, nb, st, lab)
+    Af, yf = O.linear_rows(m, nb, st, lab, fix_species=True)
+    assert Af.shape == (A.shape[0], m.S)
+    csp = m.coeffs[m.nradial:m.nradial + m.Z]
+    assert np.abs(csp).max() > 0
+    rng = np.random.default_rng(5)
+    for theta in (m.coeffs[m.nradial + m.Z:], rng.standard_normal(m.S)):
+        full = A @ np.concatenate([csp, theta]) - y
+        red = Af @ theta - yf
+        assert rel_err(red, full) < 1e-12
+    # only the energy row's target moves, by sqrt(w) sum_s n_s c_s
+    n_s = np.bincount(nb.center_types, minlength=m.Z)
+    dy = y - yf
+    assert np.abs(dy[:-1]).max() == 0.0
+    assert rel_err(dy[-1], np.sqrt(1.0 / lab.n) * (n_s @ csp)) < 1e-13
+    G, b = O.linear_system_batch(m, [nb], [lab], st, threads=1, fix_species=True)
+    Gt, bt = O.gram(Af, yf)
+    assert rel_err(G, Gt) < 1e-15 and rel_err(b, bt) < 1e-15
+
+
 def test_orthogonalize_normalises_first_channel():
     """Orthogonalize (potential_mtp.cpp:3849-3930): channel 0 is divided by
     sqrt(sum c^2 + 1e-10 per term); later channels are projected with the norm
