@@ -103,6 +103,50 @@ def copy_probe(mib: int):
     print(json.dumps({"copy_probe_bytes": nbytes, "copies": 3}))
 
 
+def pmc_summary(dirs, delete_raw: bool):
+    """Per-kernel means of rocprofv3 csv output (counter collection and
+    kernel statistics) under each directory, as one JSON object keyed by the
+    directory name; with delete_raw the per-dispatch csv files are removed."""
+    import csv
+    import glob
+    import re
+    from collections import defaultdict
+
+    def short(name):
+        name = name.replace("(anonymous namespace)::", "").replace("mtpx::", "")
+        return re.sub(r"\(.*", "", name)[:160]
+
+    out = {}
+    for d in dirs:
+        res = {}
+        for f in glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True):
+            acc = defaultdict(lambda: defaultdict(float))
+            disp = defaultdict(set)
+            with open(f) as fh:
+                for row in csv.DictReader(fh):
+                    k = short(row["Kernel_Name"])
+                    acc[k][row["Counter_Name"]] += float(row["Counter_Value"])
+                    disp[k].add(row["Dispatch_Id"])
+            for k in acc:
+                n = len(disp[k])
+                res[k] = {"dispatches": n, **{c: v / n for c, v in acc[k].items()}}
+            if delete_raw:
+                os.remove(f)
+        for f in glob.glob(os.path.join(d, "**", "*kernel_stats.csv"), recursive=True):
+            with open(f) as fh:
+                res["_stats"] = [{"name": short(r["Name"]), "calls": int(r["Calls"]),
+                                  "avg_us": float(r["AverageNs"]) / 1e3,
+                                  "min_us": float(r["MinNs"]) / 1e3,
+                                  "max_us": float(r["MaxNs"]) / 1e3,
+                                  "percent": float(r["Percentage"])}
+                                 for r in csv.DictReader(fh)][:40]
+        if delete_raw:
+            for f in glob.glob(os.path.join(d, "**", "*kernel_trace.csv"), recursive=True):
+                os.remove(f)
+        out[os.path.basename(d.rstrip("/"))] = res
+    print(json.dumps(out, indent=1))
+
+
 def large_bench(ctx, steps: int, warmup: int):
     """The 256,000-atom level-20 four-species cell (40x40x40 FCC, a = 3.6 A,
     equiatomic, sigma 0.15 A, radial basis 10, cutoff 5.5 A): E/F/S with the
@@ -468,7 +512,14 @@ def main():
                          "byte counters against a plain copy of known size)")
     ap.add_argument("--no-large", action="store_true")
     ap.add_argument("--large-steps", type=int, default=20)
+    ap.add_argument("--pmc-summary", nargs="+", metavar="DIR",
+                    help="only print per-kernel means of rocprofv3 csv output in DIR...")
+    ap.add_argument("--delete-raw", action="store_true",
+                    help="with --pmc-summary: remove the per-dispatch csv files")
     args = ap.parse_args()
+    if args.pmc_summary:
+        pmc_summary(args.pmc_summary, args.delete_raw)
+        return
     if args.copy_probe:
         copy_probe(args.copy_probe)
         return
