@@ -124,8 +124,9 @@ int install_model(mtpx_context *ctx, Model &&m)
     if (dm.rb_general) {
         // per ordered pair: kind, min, max, scaling and the setup constants
         // of the basis (basis/basis.cpp setup(): mult, su, pu, pi / max,
-        // and b, 1 / su for Poly4 / Poly5)
-        std::vector<double> t((size_t)M.Z * M.Z * kRbStride);
+        // and b, 1 / su for Poly4 / Poly5; the configurable basis's cutoff
+        // and shift with their parameters and normalisations)
+        std::vector<double> t((size_t)M.Z * M.Z * kRbStride, 0.0);
         for (int q = 0; q < M.Z * M.Z; ++q) {
             const RadialBasis &b = M.pair_basis(q / M.Z, q % M.Z);
             double *r = &t[(size_t)q * kRbStride];
@@ -134,6 +135,20 @@ int install_model(mtpx_context *ctx, Model &&m)
             r[1] = b.rmin;
             r[2] = b.rmax;
             r[3] = b.scaling;
+            if (b.kind == kRBChebyshevConfigurable) {
+                r[4] = b.cut;
+                r[5] = b.shift;
+                r[6] = b.one_minus ? 1.0 : 0.0;
+                r[7] = b.cut_b;
+                r[8] = b.cut_r1;
+                r[9] = b.cut_r2;
+                r[10] = b.lambda;
+                r[11] = b.scale_lambda;
+                r[12] = 1.0 / su;
+                r[13] = std::expm1(b.lambda);
+                r[14] = std::tanh(b.scale_lambda);
+                continue;
+            }
             r[4] = 2.0 / (b.rmax - b.rmin);
             r[5] = su;
             r[6] = b.rmax + b.rmin;

@@ -77,6 +77,11 @@ class Cursor {
         p_ += (size_t)(e - b);
         return (int)v;
     }
+    char peek()
+    {
+        ws();
+        return p_ < s_.size() ? s_[p_] : 0;
+    }
     char ch()
     {
         ws();
@@ -239,6 +244,99 @@ void encode_tables(const RawTables &raw, int part0, int dummy, ML map_l, MR map_
 
 }  // namespace
 
+namespace {
+
+const char *const kCutNames[] = {"quadratic",      "normalized_quadratic", "cosine",
+                                 "cosine_left",    "cosine_unscaled",      "cosine_squared",
+                                 "sine_squared",   "poly3",                "poly4",
+                                 "poly5",          "smoothstep5",          "smoothstep7"};
+const char *const kShiftNames[] = {"linear", "exponential", "exponential_left", "i2",
+                                   "exponential_tanh"};
+
+// "key = value" and its number (cutoff.cpp / xtrans.cpp read_value,
+// read_double: the whole token must parse and be finite).
+bool key_value(Cursor &in, const char *key, std::string &v)
+{
+    if (in.word() != key || in.word() != "=")
+        return false;
+    v = in.word();
+    return in.ok();
+}
+bool key_double(Cursor &in, const char *key, double &x)
+{
+    std::string v;
+    if (!key_value(in, key, v))
+        return false;
+    char *e = nullptr;
+    x = std::strtod(v.c_str(), &e);
+    return e && *e == 0 && e != v.c_str() && std::isfinite(x);
+}
+
+}  // namespace
+
+// RBasis_ChebyshevConfigurable::LoadFromStream (basis/basis.cpp:893-911)
+// after the common lines: an optional basis_function_type, then
+// Cutoff::load_cutoff (cutoff.cpp:441-454) and XTransForm::load_shift
+// (xtrans.cpp:360-371), with the checks of their constructors (basis.cpp
+// :875-891, cutoff.cpp:187-206, xtrans.cpp FormulaShift / ExponentialShift).
+static bool read_configurable(Cursor &in, RadialBasis &b, std::string &err)
+{
+    const std::string bad = "Error loading configurable radial basis: ";
+    std::string v;
+    b.one_minus = false;
+    if (in.peek() == 'b') {
+        if (!key_value(in, "basis_function_type", v))
+            return fail(err, (bad + "expected basis_function_type = <value>").c_str());
+        if (v == "one_minus_chebyshev")
+            b.one_minus = true;
+        else if (v != "chebyshev")
+            return fail(err, ("Unknown configurable radial basis function type: " + v).c_str());
+    }
+    if (!key_value(in, "cutoff_type", v))
+        return fail(err, (bad + "expected cutoff_type = <value>").c_str());
+    b.cut = -1;
+    for (int k = 0; k < 12; ++k)
+        if (v == kCutNames[k])
+            b.cut = k;
+    if (b.cut < 0)
+        return fail(err, ("Unknown configurable radial cutoff type: " + v).c_str());
+    if (b.cut == kCutPoly3 || b.cut == kCutPoly4 || b.cut == kCutPoly5)
+        if (!key_double(in, "cutoff_b", b.cut_b))
+            return fail(err, (bad + "invalid cutoff_b").c_str());
+    if (b.cut == kCutSmoothstep7)
+        if (!key_double(in, "cutoff_r1", b.cut_r1) || !key_double(in, "cutoff_r2", b.cut_r2))
+            return fail(err, (bad + "invalid cutoff_r1 / cutoff_r2").c_str());
+    if (!key_value(in, "shift_type", v))
+        return fail(err, (bad + "expected shift_type = <value>").c_str());
+    b.shift = -1;
+    for (int k = 0; k < 5; ++k)
+        if (v == kShiftNames[k])
+            b.shift = k;
+    if (b.shift < 0)
+        return fail(err, ("Unknown configurable radial shift type: " + v).c_str());
+    const bool expo = b.shift == kShiftExponential || b.shift == kShiftExponentialLeft ||
+                      b.shift == kShiftExponentialTanh;
+    if (expo && !key_double(in, "shift_lambda", b.lambda))
+        return fail(err, (bad + "invalid shift_lambda").c_str());
+    if (b.shift == kShiftExponentialTanh && !key_double(in, "shift_scale_lambda", b.scale_lambda))
+        return fail(err, (bad + "invalid shift_scale_lambda").c_str());
+    if (b.cut == kCutCosineLeft && b.rmax == 0.0)
+        return fail(err, "cosine_left cutoff requires nonzero max_dist");
+    if (b.cut == kCutSmoothstep7 &&
+        !(b.rmin < b.cut_r1 && b.cut_r1 <= b.cut_r2 && b.cut_r2 < b.rmax))
+        return fail(err, "smoothstep7 cutoff requires min_dist < cutoff_r1 <= cutoff_r2 < max_dist");
+    if (b.shift == kShiftExponentialLeft && b.rmax == 0.0)
+        return fail(err, "exponential_left shift requires nonzero max_dist");
+    if (expo && b.lambda != 0.0) {
+        const double den = std::expm1(b.lambda);
+        if (!std::isfinite(den) || den == 0.0)
+            return fail(err, "shift_lambda produces a non-finite exponential normalization");
+    }
+    if (b.shift == kShiftExponentialTanh && b.scale_lambda != 0.0 && std::tanh(b.scale_lambda) == 0.0)
+        return fail(err, "shift_scale_lambda produces an invalid normalization");
+    return true;
+}
+
 bool parse_mtp(const std::string &text, Model &m, std::string &err)
 {
     m = Model();
@@ -297,6 +395,8 @@ bool parse_mtp(const std::string &text, Model &m, std::string &err)
             b.kind = kRBChebyshevPoly4;
         else if (name == "RBChebyshevPoly5")
             b.kind = kRBChebyshevPoly5;
+        else if (name == "RBChebyshevConfigurable")
+            b.kind = kRBChebyshevConfigurable;
         else
             return fail(err, ("unsupported radial basis type: " + name).c_str());
         b.scaling = m.scaling;
@@ -324,6 +424,8 @@ bool parse_mtp(const std::string &text, Model &m, std::string &err)
         }
         if (!std::isfinite(b.rmin) || !std::isfinite(b.rmax) || !(b.rmin < b.rmax))
             return fail(err, "Error in loading basis: min_dist < max_dist is required");
+        if (b.kind == kRBChebyshevConfigurable)
+            return read_configurable(in, b, err);
         return true;
     };
     if (m.split) {  // :206-265, one basis per ordered species pair
@@ -501,7 +603,7 @@ std::string save_mtp(const Model &m)
     };
     auto integer = [&](long v) { o += std::to_string(v); };
     static const char *kind_names[] = {"RBChebyshev", "RBChebyCos", "RBChebyshevPoly4",
-                                       "RBChebyshevPoly5"};
+                                       "RBChebyshevPoly5", "RBChebyshevConfigurable"};
     o += "MTP\nversion = 1.1.0\npotential_name = MTP1m\nscaling = ";
     num(m.bases.empty() ? m.scaling : m.bases[0].scaling);
     o += "\nspecies_count = ";
@@ -531,6 +633,28 @@ std::string save_mtp(const Model &m)
             o += "\trb_b = ";
             num(b.b);
             o += '\n';
+        }
+        if (b.kind == kRBChebyshevConfigurable) {  // basis.cpp:913-919
+            o += b.one_minus ? "\tbasis_function_type = one_minus_chebyshev\n"
+                             : "\tbasis_function_type = chebyshev\n";
+            o += std::string("\tcutoff_type = ") + kCutNames[b.cut] + "\n";
+            auto line = [&](const char *key, double v) {
+                o += std::string("\t") + key + " = ";
+                num(v);
+                o += '\n';
+            };
+            if (b.cut == kCutPoly3 || b.cut == kCutPoly4 || b.cut == kCutPoly5)
+                line("cutoff_b", b.cut_b);
+            if (b.cut == kCutSmoothstep7) {
+                line("cutoff_r1", b.cut_r1);
+                line("cutoff_r2", b.cut_r2);
+            }
+            o += std::string("\tshift_type = ") + kShiftNames[b.shift] + "\n";
+            if (b.shift == kShiftExponential || b.shift == kShiftExponentialLeft ||
+                b.shift == kShiftExponentialTanh)
+                line("shift_lambda", b.lambda);
+            if (b.shift == kShiftExponentialTanh)
+                line("shift_scale_lambda", b.scale_lambda);
         }
     }
     o += "radial_funcs_count = ";
@@ -612,7 +736,10 @@ bool validate_model(const Model &m, std::string &err)
     for (const RadialBasis &b : m.bases)
         if (!(b.rmax > b.rmin) || !std::isfinite(b.rmin) || !std::isfinite(b.rmax) ||
             !std::isfinite(b.scaling) || !std::isfinite(b.b) || b.kind < kRBChebyshev ||
-            b.kind > kRBChebyshevPoly5)
+            b.kind > kRBChebyshevConfigurable || b.cut < kCutQuadratic ||
+            b.cut > kCutSmoothstep7 || b.shift < kShiftLinear || b.shift > kShiftExponentialTanh ||
+            !std::isfinite(b.cut_b) || !std::isfinite(b.cut_r1) || !std::isfinite(b.cut_r2) ||
+            !std::isfinite(b.lambda) || !std::isfinite(b.scale_lambda))
             return fail(err, "invalid radial basis");
     if (!(m.rmax > m.rmin) || !std::isfinite(m.rmin) || !std::isfinite(m.rmax))
         return fail(err, "invalid radial basis interval");

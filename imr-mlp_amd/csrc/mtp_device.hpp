@@ -196,10 +196,200 @@ __device__ __forceinline__ void chebyshev(const DevModel &m, double d, double *Q
 //                     zero outside [min, max]                  (:585-619)
 //   RBChebyshevPoly5  (1 - x)^4 (1 + (4 + b) x), likewise      (:776-805)
 // t is the pair's row of the basis table (kRbStride doubles).
+//
+// RBChebyshevConfigurable (basis/basis.cpp:931-1011): zero outside
+// [min, max]; otherwise Q_k = s raw_k(x(r)) fc(r) with raw_k = T_k or, for
+// one_minus_chebyshev, 1 - T_(k+1), the Chebyshev polynomials of the shift
+// x(r) by T_k = 2 x T_(k-1) - T_(k-2).  The cutoff fc and the shift x with
+// their derivatives are the closed forms of Cutoff::* (basis/cutoff.cpp)
+// and XTransForm::* (basis/xtrans.cpp); table row {kind, min, max, s,
+// cutoff, shift, one_minus, cutoff_b, r1, r2, lambda, scale_lambda,
+// 1 / (max - min), expm1(lambda), tanh(scale_lambda)}.
+__device__ __forceinline__ void configurable_cutoff(const double *t, double r, double &fc,
+                                                    double &dfc)
+{
+    const double lo = t[1], hi = t[2], b = t[7], inv = t[12], pi = M_PI;
+    const double tt = (r - lo) * inv, q = 1.0 - tt, a = pi * tt;
+    switch ((int)t[4]) {
+    case kCutQuadratic: {
+        const double dl = r - hi;
+        fc = dl * dl;
+        dfc = 2.0 * dl;
+        break;
+    }
+    case kCutNormalizedQuadratic:
+        fc = q * q;
+        dfc = -2.0 * q * inv;
+        break;
+    case kCutCosine: {
+        const double freq = pi / (hi - lo), ph = (r - lo) * freq;
+        fc = 0.5 * (1.0 + cos(ph));
+        dfc = -0.5 * freq * sin(ph);
+        break;
+    }
+    case kCutCosineLeft: {
+        const double w = pi / hi, ph = w * r;
+        fc = 0.5 * (1.0 + cos(ph));
+        dfc = -0.5 * w * sin(ph);
+        break;
+    }
+    case kCutCosineUnscaled:
+        fc = 1.0 + cos(a);
+        dfc = -sin(a) * pi * inv;
+        break;
+    case kCutCosineSquared: {
+        const double g = 1.0 + cos(a), dg = -sin(a) * pi * inv;
+        fc = g * g;
+        dfc = 2.0 * g * dg;
+        break;
+    }
+    case kCutSineSquared: {
+        const double sn = sin(a);
+        fc = sn * sn;
+        dfc = 2.0 * sn * cos(a) * pi * inv;
+        break;
+    }
+    case kCutPoly3: {
+        const double p = 1.0 + (b + 2.0) * tt;
+        fc = q * q * p;
+        dfc = -2.0 * q * inv * p + q * q * (b + 2.0) * inv;
+        break;
+    }
+    case kCutPoly4: {
+        const double p = 1.0 + (b + 3.0) * tt;
+        fc = q * q * q * p;
+        dfc = -3.0 * q * q * inv * p + q * q * q * (b + 3.0) * inv;
+        break;
+    }
+    case kCutPoly5: {
+        const double sq = q * q;
+        fc = sq * sq * (1.0 + (4.0 + b) * tt);
+        dfc = -sq * q * (20.0 * tt + b * (5.0 * tt - 1.0)) * inv;
+        break;
+    }
+    case kCutSmoothstep5: {
+        const double q2 = q * q, q3 = q2 * q;
+        fc = 6.0 * q3 * q2 - 15.0 * q2 * q2 + 10.0 * q3;
+        dfc = -(30.0 * q2 * q2 - 60.0 * q3 + 30.0 * q2) * inv;
+        break;
+    }
+    default: {  // smoothstep7
+        const double r1 = t[8], r2 = t[9];
+        if (r <= r1 || r >= r2) {
+            const double dp = r <= r1 ? 1.0 / (r1 - lo) : 1.0 / (hi - r2);
+            const double p = r <= r1 ? (r - lo) * dp : (r - r2) * dp;
+            const double p2 = p * p, p3 = p2 * p, p4 = p2 * p2;
+            const double v = 35.0 * p4 - 84.0 * p4 * p + 70.0 * p3 * p3 - 20.0 * p3 * p4;
+            const double dv = (140.0 * p3 - 420.0 * p4 + 420.0 * p4 * p - 140.0 * p3 * p3) * dp;
+            fc = r <= r1 ? v : 1.0 - v;
+            dfc = r <= r1 ? dv : -dv;
+        } else {
+            fc = 1.0;
+            dfc = 0.0;
+        }
+        break;
+    }
+    }
+}
+
+__device__ __forceinline__ void configurable_shift(const double *t, double r, double &x,
+                                                   double &dx)
+{
+    const double lo = t[1], hi = t[2], lam = t[10], sl = t[11], inv = t[12], den = t[13];
+    const double tt = (r - lo) * inv;
+    switch ((int)t[5]) {
+    case kShiftLinear: {
+        const double slope = 2.0 / (hi - lo);
+        x = -1.0 + slope * (r - lo);
+        dx = slope;
+        break;
+    }
+    case kShiftExponential:
+        if (lam == 0.0) {
+            x = -1.0 + 2.0 * (r - lo) * inv;
+            dx = 2.0 * inv;
+        } else {
+            const double e = lam * (hi - r) * inv;
+            x = 1.0 - 2.0 * expm1(e) / den;
+            dx = 2.0 * lam * inv * exp(e) / den;
+        }
+        break;
+    case kShiftExponentialLeft:
+        if (lam == 0.0) {
+            x = 2.0 * (r / hi) - 1.0;
+            dx = 2.0 / hi;
+        } else {
+            const double e = exp(lam * (1.0 - r / hi));
+            x = 1.0 - (2.0 / den) * (e - 1.0);
+            dx = (2.0 / den) * e * lam / hi;
+        }
+        break;
+    case kShiftI2: {
+        const double k = (r - hi) * inv;
+        x = 2.0 * k * k - 1.0;
+        dx = 4.0 * k * inv;
+        break;
+    }
+    default: {  // exponential_tanh
+        double sh, dsh;
+        if (lam == 0.0) {
+            sh = 2.0 * tt - 1.0;
+            dsh = 2.0 * inv;
+        } else {
+            const double e = exp(lam * (1.0 - tt));
+            sh = 1.0 - (2.0 / den) * (e - 1.0);
+            dsh = (2.0 / den) * e * lam * inv;
+        }
+        if (sl == 0.0) {
+            x = sh;
+            dx = dsh;
+        } else {
+            const double th = tanh(sl * sh), tsl = t[14];
+            x = th / tsl;
+            dx = (1.0 - th * th) * sl * dsh / tsl;
+        }
+        break;
+    }
+    }
+}
+
+template <int RMAX>
+__device__ __forceinline__ void configurable_basis(const double *t, double d, double *Q,
+                                                   double *dQ)
+{
+    const bool inside = !(d < t[1] || d > t[2]);
+    double fc, dfc, x, dx;
+    configurable_cutoff(t, d, fc, dfc);
+    configurable_shift(t, d, x, dx);
+    const double s = t[3];
+    const bool om = t[6] != 0.0;
+    double T[RMAX + 1], dT[RMAX + 1];
+    T[0] = 1.0;
+    dT[0] = 0.0;
+    T[1] = x;
+    dT[1] = dx;
+#pragma unroll
+    for (int k = 2; k <= RMAX; ++k) {
+        T[k] = 2.0 * x * T[k - 1] - T[k - 2];
+        dT[k] = 2.0 * (dx * T[k - 1] + x * dT[k - 1]) - dT[k - 2];
+    }
+#pragma unroll
+    for (int k = 0; k < RMAX; ++k) {
+        const double raw = om ? 1.0 - T[k + 1] : T[k];
+        const double rawd = om ? -dT[k + 1] : dT[k];
+        Q[k] = inside ? s * raw * fc : 0.0;
+        dQ[k] = inside ? s * (rawd * fc + raw * dfc) : 0.0;
+    }
+}
+
 template <int RMAX>
 __device__ __forceinline__ void general_basis(const double *t, double d, double *Q, double *dQ)
 {
     const int kind = (int)t[0];
+    if (kind == kRBChebyshevConfigurable) {
+        configurable_basis<RMAX>(t, d, Q, dQ);
+        return;
+    }
     const double rmin = t[1], rmax = t[2], s = t[3], mult = t[4], su = t[5], pu = t[6];
     const double ksi = (2 * d - pu) / su;
     double rc, drc;

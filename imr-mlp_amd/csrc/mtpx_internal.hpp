@@ -100,16 +100,39 @@ bool tag_parse(const std::string &raw, int Z, MetaTag &tag, std::string &err);
 std::string tag_output(const MetaTag &tag);
 
 // Radial basis kinds (basis/basis.h:19-29): the Chebyshev polynomials of
-// xi = (2r - (min + max)) / (max - min) times an envelope.
-enum RadialKind { kRBChebyshev = 0, kRBChebyCos = 1, kRBChebyshevPoly4 = 2, kRBChebyshevPoly5 = 3 };
+// xi = (2r - (min + max)) / (max - min) times an envelope, and the
+// configurable basis (Chebyshev polynomials of a shift x(r) times a cutoff
+// function, basis/basis.cpp:866-1031, basis/cutoff.cpp, basis/xtrans.cpp).
+enum RadialKind {
+    kRBChebyshev = 0,
+    kRBChebyCos = 1,
+    kRBChebyshevPoly4 = 2,
+    kRBChebyshevPoly5 = 3,
+    kRBChebyshevConfigurable = 4
+};
+// Cutoff::CutoffType and XTransForm::ShiftType, in their enum order.
+enum CutoffKind {
+    kCutQuadratic, kCutNormalizedQuadratic, kCutCosine, kCutCosineLeft, kCutCosineUnscaled,
+    kCutCosineSquared, kCutSineSquared, kCutPoly3, kCutPoly4, kCutPoly5, kCutSmoothstep5,
+    kCutSmoothstep7
+};
+enum ShiftKind { kShiftLinear, kShiftExponential, kShiftExponentialLeft, kShiftI2, kShiftExponentialTanh };
 struct RadialBasis {
     int kind = kRBChebyshev;
     double rmin = 0, rmax = 0, scaling = 0.01;
     double b = 0;  // rb_b of the Poly4 / Poly5 envelopes
+    // RBChebyshevConfigurable: cutoff and shift kinds, one_minus_chebyshev,
+    // cutoff_b, cutoff_r1, cutoff_r2, shift_lambda, shift_scale_lambda
+    int cut = kCutQuadratic, shift = kShiftLinear;
+    bool one_minus = false;
+    double cut_b = 0, cut_r1 = 0, cut_r2 = 0, lambda = 0, scale_lambda = 0;
 };
 // Per-pair basis table on the device: kRbStride doubles per ordered species
-// pair {kind, min, max, scaling, mult, su, pu, pi / max, b, 1 / su}.
-constexpr int kRbStride = 10;
+// pair.  Envelope kinds: {kind, min, max, scaling, mult, su, pu, pi / max,
+// b, 1 / su}; the configurable kind: {kind, min, max, scaling, cutoff,
+// shift, one_minus, cutoff_b, r1, r2, lambda, scale_lambda, 1 / (max - min),
+// expm1(lambda), tanh(scale_lambda), 0}.
+constexpr int kRbStride = 16;
 
 // Host-side model: the linear MTP (potentials/potential_mtp.h:93) plus the
 // launch plan derived from its contraction graph.

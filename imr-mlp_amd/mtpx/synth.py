@@ -149,16 +149,47 @@ def fmt(x: float) -> str:
     return "%.17e" % x
 
 
-BASIS_TYPES = ("RBChebyshev", "RBChebyCos", "RBChebyshevPoly4", "RBChebyshevPoly5")
+BASIS_TYPES = ("RBChebyshev", "RBChebyCos", "RBChebyshevPoly4", "RBChebyshevPoly5",
+               "RBChebyshevConfigurable")
+CUTOFF_TYPES = ("quadratic", "normalized_quadratic", "cosine", "cosine_left", "cosine_unscaled",
+                "cosine_squared", "sine_squared", "poly3", "poly4", "poly5", "smoothstep5",
+                "smoothstep7")
+SHIFT_TYPES = ("linear", "exponential", "exponential_left", "i2", "exponential_tanh")
 
 
-def basis_lines(kind: str, rmin: float, rmax: float, R: int, b: float = -1.0 / 3.0):
+def configurable(cutoff="cosine", shift="linear", one_minus=False, cutoff_b=-0.25, r1=None,
+                 r2=None, lam=1.5, scale_lambda=0.8):
+    """An RBChebyshevConfigurable description for basis_lines / write_mtp."""
+    return dict(type="RBChebyshevConfigurable", cutoff=cutoff, shift=shift, one_minus=one_minus,
+                cutoff_b=cutoff_b, r1=r1, r2=r2, lam=lam, scale_lambda=scale_lambda)
+
+
+def basis_lines(kind, rmin: float, rmax: float, R: int, b: float = -1.0 / 3.0):
     """AnyBasis::SaveToStream (basis/basis.h:50-56), plus rb_b for the
-    Poly4 / Poly5 bases (basis/basis.cpp:560-564, :733-737)."""
-    out = ["radial_basis_type = " + kind, "\tmin_dist = " + fmt(rmin),
+    Poly4 / Poly5 bases (basis/basis.cpp:560-564, :733-737); kind may be a
+    configurable() description (RBasis_ChebyshevConfigurable::SaveToStream,
+    basis.cpp:913-919, with the cutoff and shift lines)."""
+    cfg = kind if isinstance(kind, dict) else None
+    name = cfg["type"] if cfg else kind
+    out = ["radial_basis_type = " + name, "\tmin_dist = " + fmt(rmin),
            "\tmax_dist = " + fmt(rmax), "\tradial_basis_size = %d" % R]
-    if kind in ("RBChebyshevPoly4", "RBChebyshevPoly5"):
+    if name in ("RBChebyshevPoly4", "RBChebyshevPoly5"):
         out.append("\trb_b = " + fmt(b))
+    if cfg:
+        out.append("\tbasis_function_type = " +
+                   ("one_minus_chebyshev" if cfg["one_minus"] else "chebyshev"))
+        out.append("\tcutoff_type = " + cfg["cutoff"])
+        if cfg["cutoff"] in ("poly3", "poly4", "poly5"):
+            out.append("\tcutoff_b = " + fmt(cfg["cutoff_b"]))
+        if cfg["cutoff"] == "smoothstep7":
+            r1 = cfg["r1"] if cfg["r1"] is not None else rmin + 0.25 * (rmax - rmin)
+            r2 = cfg["r2"] if cfg["r2"] is not None else rmin + 0.75 * (rmax - rmin)
+            out += ["\tcutoff_r1 = " + fmt(r1), "\tcutoff_r2 = " + fmt(r2)]
+        out.append("\tshift_type = " + cfg["shift"])
+        if cfg["shift"] in ("exponential", "exponential_left", "exponential_tanh"):
+            out.append("\tshift_lambda = " + fmt(cfg["lam"]))
+        if cfg["shift"] == "exponential_tanh":
+            out.append("\tshift_scale_lambda = " + fmt(cfg["scale_lambda"]))
     return out
 
 

@@ -72,8 +72,10 @@ const char *mtpx_version(void);
 int mtpx_load_model(mtpx_context *ctx, const mtpx_model_view *view);
 /* PotMTP::Load (potentials/potential_mtp.cpp:119-571): .mtp text with a
  * shared radial basis or one per ordered species pair (radial_basis_split),
- * of the kinds RBChebyshev, RBChebyCos, RBChebyshevPoly4 and
- * RBChebyshevPoly5 (basis/basis.h:19-29); scaling defaults to 0.01; the
+ * of the kinds RBChebyshev, RBChebyCos, RBChebyshevPoly4, RBChebyshevPoly5
+ * and RBChebyshevConfigurable with any of its cutoffs and shifts
+ * (basis/basis.h:19-29, basis/cutoff.h, basis/xtrans.h); scaling defaults
+ * to 0.01; the
  * potential_tag is read as the reference's metadata (a structured tag must
  * declare a linear MTP). */
 int mtpx_load_model_text(mtpx_context *ctx, const char *text);

@@ -164,13 +164,116 @@ static int basis_code(const char *name)
         return 2;
     if (strcmp(name, "RBChebyshevPoly5") == 0)
         return 3;
+    if (strcmp(name, "RBChebyshevConfigurable") == 0)
+        return 4;
     return -1;
 }
 static const char *basis_name(int code)
 {
     static const char *names[] = {"RBChebyshev", "RBChebyCos", "RBChebyshevPoly4",
-                                  "RBChebyshevPoly5"};
+                                  "RBChebyshevPoly5", "RBChebyshevConfigurable"};
     return names[code];
+}
+
+/* Cutoff::cutoff_type_name / XTransForm::shift_type_name (basis/cutoff.cpp,
+ * basis/xtrans.cpp), in the order of their enums. */
+static const char *cut_names[] = {"quadratic",    "normalized_quadratic", "cosine",
+                                  "cosine_left",  "cosine_unscaled",      "cosine_squared",
+                                  "sine_squared", "poly3",                "poly4",
+                                  "poly5",        "smoothstep5",          "smoothstep7"};
+static const char *shift_names[] = {"linear", "exponential", "exponential_left", "i2",
+                                    "exponential_tanh"};
+enum { CUT_QUAD, CUT_NQUAD, CUT_COS, CUT_COSL, CUT_COSU, CUT_COS2, CUT_SIN2, CUT_P3, CUT_P4,
+       CUT_P5, CUT_SS5, CUT_SS7 };
+enum { SH_LIN, SH_EXP, SH_EXPL, SH_I2, SH_EXPT };
+
+/* "key = value" (cutoff.cpp / xtrans.cpp read_value, read_double) */
+static int rd_keyval(rd_t *r, const char *key, char *val, int n)
+{
+    char tok[256];
+    rd_word(r, tok, sizeof tok);
+    if (strcmp(tok, key) != 0)
+        return 0;
+    rd_word(r, tok, sizeof tok);
+    if (strcmp(tok, "=") != 0)
+        return 0;
+    return rd_word(r, val, n) > 0;
+}
+static int rd_keydouble(rd_t *r, const char *key, double *v)
+{
+    char val[256], *end = NULL;
+    if (!rd_keyval(r, key, val, sizeof val))
+        return 0;
+    *v = strtod(val, &end);
+    return end && *end == 0 && end != val && isfinite(*v);
+}
+static int find_name(const char **names, int n, const char *s)
+{
+    for (int i = 0; i < n; ++i)
+        if (strcmp(names[i], s) == 0)
+            return i;
+    return -1;
+}
+
+/* RBasis_ChebyshevConfigurable::LoadFromStream (basis.cpp:893-911) after
+ * the common lines: an optional basis_function_type, then
+ * Cutoff::load_cutoff (cutoff.cpp:441-454) and XTransForm::load_shift
+ * (xtrans.cpp:360-371), with the constructors' checks (setup :875-891,
+ * FormulaCutoff :187-206, FormulaShift, ExponentialShift). */
+static const char *load_configurable(rd_t *r, orc_basis *b)
+{
+    char val[256];
+    b->one_minus = 0;
+    rd_skipws(r);
+    if (*r->p == 'b') {
+        if (!rd_keyval(r, "basis_function_type", val, sizeof val))
+            return "Error loading configurable radial basis: expected basis_function_type = <value>";
+        if (strcmp(val, "one_minus_chebyshev") == 0)
+            b->one_minus = 1;
+        else if (strcmp(val, "chebyshev") != 0)
+            return "Unknown configurable radial basis function type";
+    }
+    if (!rd_keyval(r, "cutoff_type", val, sizeof val))
+        return "Error loading configurable radial basis: expected cutoff_type = <value>";
+    b->cut = find_name(cut_names, 12, val);
+    if (b->cut < 0)
+        return "Unknown configurable radial cutoff type";
+    b->cut_b = b->cut_r1 = b->cut_r2 = 0;
+    if (b->cut == CUT_P3 || b->cut == CUT_P4 || b->cut == CUT_P5)
+        if (!rd_keydouble(r, "cutoff_b", &b->cut_b))
+            return "Error loading configurable radial basis: invalid cutoff_b";
+    if (b->cut == CUT_SS7)
+        if (!rd_keydouble(r, "cutoff_r1", &b->cut_r1) || !rd_keydouble(r, "cutoff_r2", &b->cut_r2))
+            return "Error loading configurable radial basis: invalid cutoff_r1/cutoff_r2";
+    if (!rd_keyval(r, "shift_type", val, sizeof val))
+        return "Error loading configurable radial basis: expected shift_type = <value>";
+    b->shift = find_name(shift_names, 5, val);
+    if (b->shift < 0)
+        return "Unknown configurable radial shift type";
+    b->lambda = b->scale_lambda = 0;
+    if (b->shift == SH_EXP || b->shift == SH_EXPL || b->shift == SH_EXPT)
+        if (!rd_keydouble(r, "shift_lambda", &b->lambda))
+            return "Error loading configurable radial basis: invalid shift_lambda";
+    if (b->shift == SH_EXPT)
+        if (!rd_keydouble(r, "shift_scale_lambda", &b->scale_lambda))
+            return "Error loading configurable radial basis: invalid shift_scale_lambda";
+    const double lo = b->rmin, hi = b->rmax;
+    if (!isfinite(lo) || !isfinite(hi) || !(lo < hi))
+        return "RBChebyshevConfigurable requires finite min_dist < max_dist";
+    if (b->cut == CUT_COSL && hi == 0.0)
+        return "cosine_left cutoff requires nonzero max_dist";
+    if (b->cut == CUT_SS7 && !(lo < b->cut_r1 && b->cut_r1 <= b->cut_r2 && b->cut_r2 < hi))
+        return "smoothstep7 cutoff requires min_dist < cutoff_r1 <= cutoff_r2 < max_dist";
+    if (b->shift == SH_EXPL && hi == 0.0)
+        return "exponential_left shift requires nonzero max_dist";
+    if ((b->shift == SH_EXP || b->shift == SH_EXPL || b->shift == SH_EXPT) && b->lambda != 0.0) {
+        const double den = expm1(b->lambda);
+        if (!isfinite(den) || den == 0.0)
+            return "shift_lambda produces a non-finite exponential normalization";
+    }
+    if (b->shift == SH_EXPT && b->scale_lambda != 0.0 && tanh(b->scale_lambda) == 0.0)
+        return "shift_scale_lambda produces an invalid normalization";
+    return 0;
 }
 
 /* AnyBasis::LoadFromStream (basis/basis.cpp:73-117) and, for Poly4/Poly5,
@@ -197,6 +300,8 @@ static const char *load_basis(rd_t *r, int code, double scaling, orc_basis *b)
 static const char *load_basis_tail(rd_t *r, orc_basis *b)
 {
     char tok[256];
+    if (b->type == 4)
+        return load_configurable(r, b);
     if (b->type == 2 || b->type == 3) {
         rd_word(r, tok, sizeof tok);
         if (strcmp(tok, "rb_b") != 0)
@@ -373,6 +478,9 @@ orc_model *orc_model_load_text(const char *text, char *err, int errlen)
             LOAD_FAIL(berr);
         m->cutoff = m->bases[0].rmax;
     }
+    for (int q = 0; q < (m->split ? m->Z * m->Z : 1); ++q)
+        if (m->bases[q].type == 4 && m->R > 62)
+            LOAD_FAIL("this restatement takes radial_basis_size <= 62 for RBChebyshevConfigurable");
     m->rmin = m->bases[0].rmin;
     m->rmax = m->cutoff;
     m->scaling = scaling;
@@ -694,6 +802,19 @@ int orc_model_save_text(const orc_model *m, char *buf, int buflen)
              bb->rmax, m->R);
         if (bb->type == 2 || bb->type == 3)
             EMIT("\trb_b = %.17e\n", bb->b);
+        if (bb->type == 4) {  /* RBasis_ChebyshevConfigurable::SaveToStream (basis.cpp:913-919) */
+            EMIT("\tbasis_function_type = %s\n", bb->one_minus ? "one_minus_chebyshev" : "chebyshev");
+            EMIT("\tcutoff_type = %s\n", cut_names[bb->cut]);
+            if (bb->cut == CUT_P3 || bb->cut == CUT_P4 || bb->cut == CUT_P5)
+                EMIT("\tcutoff_b = %.17e\n", bb->cut_b);
+            if (bb->cut == CUT_SS7)
+                EMIT("\tcutoff_r1 = %.17e\n\tcutoff_r2 = %.17e\n", bb->cut_r1, bb->cut_r2);
+            EMIT("\tshift_type = %s\n", shift_names[bb->shift]);
+            if (bb->shift == SH_EXP || bb->shift == SH_EXPL || bb->shift == SH_EXPT)
+                EMIT("\tshift_lambda = %.17e\n", bb->lambda);
+            if (bb->shift == SH_EXPT)
+                EMIT("\tshift_scale_lambda = %.17e\n", bb->scale_lambda);
+        }
     }
     EMIT("radial_funcs_count = %d\n", m->M);
     EMIT("radial_coeffs\n");
@@ -801,8 +922,175 @@ static double ksi_of(const orc_basis *bs, double value)
     return (2 * value - (bs->rmax + bs->rmin)) / (bs->rmax - bs->rmin);
 }
 
+/* Value and first derivative (the first two members of the reference's
+ * Jet2; the second derivative is not needed here). */
+typedef struct {
+    double v, d;
+} jet;
+static jet jc(double c) { jet r = {c, 0}; return r; }
+static jet jadd(jet a, jet b) { jet r = {a.v + b.v, a.d + b.d}; return r; }
+static jet jsub(jet a, jet b) { jet r = {a.v - b.v, a.d - b.d}; return r; }
+static jet jmul(jet a, jet b) { jet r = {a.v * b.v, a.d * b.v + a.v * b.d}; return r; }
+static jet jscale(double s, jet a) { jet r = {s * a.v, s * a.d}; return r; }
+static jet jsin(jet a) { jet r = {sin(a.v), cos(a.v) * a.d}; return r; }
+static jet jcos(jet a) { jet r = {cos(a.v), -sin(a.v) * a.d}; return r; }
+static jet jexp(jet a) { double e = exp(a.v); jet r = {e, e * a.d}; return r; }
+static jet jtanh(jet a) { double t = tanh(a.v); jet r = {t, (1.0 - t * t) * a.d}; return r; }
+static jet jpow2(jet a) { return jmul(a, a); }
+static jet jpow3(jet a) { return jmul(jmul(a, a), a); }
+static jet jpow4(jet a) { return jpow2(jpow2(a)); }
+static jet jpow5(jet a) { return jmul(jpow4(a), a); }
+static jet jpow6(jet a) { return jmul(jpow3(a), jpow3(a)); }
+static jet jpow7(jet a) { return jmul(jpow6(a), a); }
+
+/* Cutoff value and derivative: QuadraticCutoff, CosineCutoff, Poly5Cutoff
+ * (cutoff.cpp:325-421) and FormulaCutoff::evaluate (:147-185). */
+static void cutoff_der(const orc_basis *b, double r, double *fc, double *dfc)
+{
+    const double lo = b->rmin, hi = b->rmax, inv = 1.0 / (hi - lo), pi = M_PI;
+    if (b->cut == CUT_QUAD) {
+        const double delta = r - hi;
+        *fc = delta * delta;
+        *dfc = 2.0 * delta;
+        return;
+    }
+    if (b->cut == CUT_COS) {
+        const double freq = pi / (hi - lo), phase = (r - lo) * freq;
+        *fc = 0.5 * (1.0 + cos(phase));
+        *dfc = -0.5 * freq * sin(phase);
+        return;
+    }
+    if (b->cut == CUT_P5) {
+        const double x = (r - lo) * inv, omx = 1.0 - x, sq = omx * omx, cube = sq * omx;
+        *fc = sq * sq * (1.0 + (4.0 + b->cut_b) * x);
+        *dfc = -cube * (20.0 * x + b->cut_b * (5.0 * x - 1.0)) * inv;
+        return;
+    }
+    const jet radius = {r, 1.0}, one = jc(1.0);
+    const jet t = jmul(jsub(radius, jc(lo)), jc(inv));
+    const jet q = jsub(one, t);
+    jet res = one;
+    switch (b->cut) {
+    case CUT_NQUAD: res = jpow2(q); break;
+    case CUT_COSL: res = jscale(0.5, jadd(one, jcos(jscale(pi / hi, radius)))); break;
+    case CUT_COSU: res = jadd(one, jcos(jscale(pi, t))); break;
+    case CUT_COS2: res = jpow2(jadd(one, jcos(jscale(pi, t)))); break;
+    case CUT_SIN2: res = jpow2(jsin(jscale(pi, t))); break;
+    case CUT_P3: res = jmul(jpow2(q), jadd(one, jscale(b->cut_b + 2.0, t))); break;
+    case CUT_P4: res = jmul(jpow3(q), jadd(one, jscale(b->cut_b + 3.0, t))); break;
+    case CUT_SS5:
+        res = jadd(jsub(jscale(6.0, jpow5(q)), jscale(15.0, jpow4(q))), jscale(10.0, jpow3(q)));
+        break;
+    case CUT_SS7:
+        if (r <= b->cut_r1) {
+            const jet p = jscale(1.0 / (b->cut_r1 - lo), jsub(radius, jc(lo)));
+            res = jsub(jadd(jsub(jscale(35.0, jpow4(p)), jscale(84.0, jpow5(p))),
+                            jscale(70.0, jpow6(p))),
+                       jscale(20.0, jpow7(p)));
+        } else if (r >= b->cut_r2) {
+            const jet p = jscale(1.0 / (hi - b->cut_r2), jsub(radius, jc(b->cut_r2)));
+            res = jadd(jsub(jadd(jsub(one, jscale(35.0, jpow4(p))), jscale(84.0, jpow5(p))),
+                            jscale(70.0, jpow6(p))),
+                       jscale(20.0, jpow7(p)));
+        }
+        break;
+    }
+    *fc = res.v;
+    *dfc = res.d;
+}
+
+/* Shift value and derivative: LinearShift, ExponentialShift
+ * (xtrans.cpp:240-330) and FormulaShift::evaluate (:104-141). */
+static void shift_der(const orc_basis *b, double r, double *x, double *dx)
+{
+    const double lo = b->rmin, hi = b->rmax, inv = 1.0 / (hi - lo), lam = b->lambda;
+    if (b->shift == SH_LIN) {
+        const double slope = 2.0 / (hi - lo);
+        *x = -1.0 + slope * (r - lo);
+        *dx = slope;
+        return;
+    }
+    if (b->shift == SH_EXP) {
+        if (lam == 0.0) {
+            *x = -1.0 + 2.0 * (r - lo) * inv;
+            *dx = 2.0 * inv;
+            return;
+        }
+        const double den = expm1(lam), e = lam * (hi - r) * inv;
+        *x = 1.0 - 2.0 * expm1(e) / den;
+        *dx = 2.0 * lam * inv * exp(e) / den;
+        return;
+    }
+    const jet radius = {r, 1.0}, one = jc(1.0);
+    const jet t = jmul(jsub(radius, jc(lo)), jc(inv));
+    jet res = one;
+    if (b->shift == SH_I2) {
+        const jet k = jmul(jsub(radius, jc(hi)), jc(inv));
+        res = jsub(jscale(2.0, jmul(k, k)), one);
+    } else if (b->shift == SH_EXPL) {
+        if (lam == 0.0) {
+            res = jsub(jscale(2.0, jscale(1.0 / hi, radius)), one);
+        } else {
+            const double den = expm1(lam);
+            const jet ex = jscale(lam, jsub(one, jscale(1.0 / hi, radius)));
+            res = jsub(one, jscale(2.0 / den, jsub(jexp(ex), one)));
+        }
+    } else {  /* exponential_tanh */
+        jet sh;
+        if (lam == 0.0) {
+            sh = jsub(jscale(2.0, t), one);
+        } else {
+            const double den = expm1(lam);
+            sh = jsub(one, jscale(2.0 / den, jsub(jexp(jscale(lam, jsub(one, t))), one)));
+        }
+        res = b->scale_lambda == 0.0 ? sh
+                                     : jscale(1.0 / tanh(b->scale_lambda),
+                                              jtanh(jscale(b->scale_lambda, sh)));
+    }
+    *x = res.v;
+    *dx = res.d;
+}
+
+/* RBasis_ChebyshevConfigurable::calculate (basis.cpp:931-1011): zero
+ * outside [min, max]; otherwise the Chebyshev polynomials T_i of the shift
+ * x(r) (or 1 - T_{i+1} for one_minus_chebyshev) times the cutoff, scaled. */
+static void configurable_der(const orc_basis *b, int R, double value, double *val, double *der)
+{
+    if (value < b->rmin || value > b->rmax) {
+        for (int i = 0; i < R; ++i)
+            val[i] = der[i] = 0;
+        return;
+    }
+    double x, dx, fc, dfc;
+    shift_der(b, value, &x, &dx);
+    cutoff_der(b, value, &fc, &dfc);
+    const int np = R + (b->one_minus ? 1 : 0);
+    double T[64], dT[64];
+    T[0] = 1.0;
+    dT[0] = 0.0;
+    if (np > 1) {
+        T[1] = x;
+        dT[1] = dx;
+    }
+    for (int i = 2; i < np; ++i) {
+        T[i] = 2.0 * x * T[i - 1] - T[i - 2];
+        dT[i] = 2.0 * (dx * T[i - 1] + x * dT[i - 1]) - dT[i - 2];
+    }
+    for (int i = 0; i < R; ++i) {
+        const int k = i + (b->one_minus ? 1 : 0);
+        const double raw = b->one_minus ? 1.0 - T[k] : T[k];
+        const double rawd = b->one_minus ? -dT[k] : dT[k];
+        val[i] = b->scaling * raw * fc;
+        der[i] = b->scaling * (rawd * fc + raw * dfc);
+    }
+}
+
 static void basis_calc_der(const orc_basis *bs, int R, double value, double *val, double *der)
 {
+    if (bs->type == 4) {
+        configurable_der(bs, R, value, val, der);
+        return;
+    }
     const double min_val = bs->rmin, max_val = bs->rmax, scaling = bs->scaling;
     const double mult = 2.0 / (max_val - min_val);
     const double su = max_val - min_val;

@@ -19,11 +19,17 @@ extern "C" {
 #endif
 
 /* One radial basis (basis/basis.h:104-278): RBChebyshev (0), RBChebyCos (1),
- * RBChebyshevPoly4 (2), RBChebyshevPoly5 (3). */
+ * RBChebyshevPoly4 (2), RBChebyshevPoly5 (3), RBChebyshevConfigurable (4;
+ * basis/basis.cpp:866-1031 with basis/cutoff.cpp and basis/xtrans.cpp). */
 typedef struct orc_basis {
     int type;
     double rmin, rmax, scaling;   /* min_val, max_val, scaling */
     double b;                     /* rb_b of the Poly4/Poly5 bases */
+    /* RBChebyshevConfigurable: cutoff type (Cutoff::CutoffType order),
+     * shift type (XTransForm::ShiftType order), basis_function_type
+     * one_minus_chebyshev, and their parameters */
+    int cut, shift, one_minus;
+    double cut_b, cut_r1, cut_r2, lambda, scale_lambda;
 } orc_basis;
 
 /* Linear MTP (potentials/potential_mtp.h:93, coefficient layout

@@ -35,7 +35,7 @@ def test_efs_matches_oracle(ctx, kind):
     assert_efs_close(ctx.efs(), ref, 1e-10)
 
 
-@pytest.mark.parametrize("kind", ["split", "chebycos", "poly5"])
+@pytest.mark.parametrize("kind", ["split", "chebycos", "poly5", "configurable"])
 def test_level16_structure_with_general_bases(ctx, kind):
     """The level-16 moment graph on a general basis runs the run-time
     profile kernels (not the compile-time level-16 ones)."""
@@ -46,7 +46,7 @@ def test_level16_structure_with_general_bases(ctx, kind):
     assert_efs_close(ctx.efs(), ref, 1e-10)
 
 
-@pytest.mark.parametrize("kind", ["split", "chebycos", "poly4"])
+@pytest.mark.parametrize("kind", ["split", "chebycos", "poly4", "configurable", "split-configurable"])
 def test_loss_grad_matches_oracle(ctx, kind):
     text = model_text(kind, seed=733)
     ref_text = model_text(kind, seed=734)

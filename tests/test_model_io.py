@@ -19,7 +19,11 @@ SPLIT = [("RBChebyshev", 1.7, 4.6), ("RBChebyCos", 1.8, 4.9),
          ("RBChebyshevPoly5", 1.6, 5.2, -0.2), ("RBChebyshevPoly4", 1.9, 4.4, 0.5)]
 BASES = {"chebyshev": {}, "chebycos": dict(basis="RBChebyCos"),
          "poly4": dict(basis="RBChebyshevPoly4"), "poly5": dict(basis="RBChebyshevPoly5"),
-         "split": dict(pair_bases=SPLIT)}
+         "split": dict(pair_bases=SPLIT),
+         "configurable": dict(basis=S.configurable("smoothstep7", "exponential_tanh", True)),
+         "split-configurable": dict(pair_bases=[
+             (S.configurable("poly3", "i2"), 1.7, 4.6), (S.configurable("cosine_left", "exponential"), 1.8, 4.9),
+             (S.configurable("sine_squared", "exponential_left", True), 1.6, 5.2), ("RBChebyshevPoly5", 1.9, 4.4, 0.5)])}
 DEFAULT_TAG = '{"model":"linear","schema":"gpml.mtp.metadata","type":"MTP","version":1}'
 
 
@@ -171,8 +175,76 @@ def test_split_with_identical_pairs_equals_shared_basis():
         assert np.array_equal(np.asarray(x), np.asarray(y))
 
 
+# every cutoff once, the shifts in turn, both basis function types
+CONFIGS = [(c, S.SHIFT_TYPES[k % 5], k % 2 == 1) for k, c in enumerate(S.CUTOFF_TYPES)]
+
+
+def _cfg_model(cut, shift, om, R=6):
+    return O.Model(S.random_model("shapeev-06.mtp", 2, R, 1.8, 4.8, -0.5, 0.5, S.rng_for(723),
+                                  basis=S.configurable(cut, shift, om)))
+
+
+@pytest.mark.parametrize("cut,shift,om", CONFIGS)
+def test_configurable_structure(cut, shift, om):
+    """RBChebyshevConfigurable (basis.cpp:931-1011) is s raw_k(x(r)) fc(r):
+    Q_0 / s gives the cutoff and Q_1 / Q_0 the shift (chebyshev), and every
+    Q_k / Q_0 is T_k(x) = cos(k acos x) (or (1 - T_(k+1)) / (1 - x) for
+    one_minus); every cutoff vanishes at max_dist, each shift maps the
+    interval ends as its definition fixes, derivatives match central
+    differences, and the basis is zero outside [min, max]."""
+    m = _cfg_model(cut, shift, om)
+    s, lo, hi = 0.01, 1.8, 4.8
+    ends = {"linear": (-1, 1), "exponential": (-1, 1), "i2": (1, -1), "exponential_tanh": (-1, 1)}
+    for r in np.linspace(1.85, 4.75, 13):
+        v, d = m.rb_calc_der(r)
+        k = np.arange(6)
+        if abs(v[0]) > 1e-12:
+            if not om:
+                x = v[1] / v[0]
+                T = np.cos(k * np.arccos(np.clip(x, -1, 1)))
+                assert np.allclose(v / v[0], T, rtol=1e-9, atol=1e-9)
+            else:
+                # Q_k / Q_0 = (1 - T_(k+1)) / (1 - T_1), and Q_1 / Q_0 = 2 (1 + x)
+                x = v[1] / (2 * v[0]) - 1
+                T = np.cos((k + 1) * np.arccos(np.clip(x, -1, 1)))
+                assert np.allclose(v / v[0], (1 - T) / (1 - x), rtol=1e-8, atol=1e-8)
+            assert -1 - 1e-12 <= x <= 1 + 1e-12
+        h = 1e-6
+        fd = (m.rb_calc_der(r + h)[0] - m.rb_calc_der(r - h)[0]) / (2 * h)
+        assert np.allclose(d, fd, rtol=1e-6, atol=1e-10)
+    at_hi = m.rb_calc_der(hi)[0]
+    assert np.abs(at_hi).max() < 1e-13
+    assert not m.rb_calc_der(lo - 0.05)[0].any() and not m.rb_calc_der(hi + 0.05)[0].any()
+    if not om and shift in ends and cut in ("cosine", "smoothstep5", "poly3"):
+        # a cutoff that is positive at min_dist: the shift's value there
+        v = m.rb_calc_der(lo)[0]
+        assert abs(v[1] / v[0] - ends[shift][0]) < 1e-12
+
+
 needs_ref = pytest.mark.skipif(not O.ref_available("mlip_ref"),
                                reason="reference binaries not built (make -C oracle ref)")
+
+
+@needs_ref
+@pytest.mark.parametrize("cut,shift,om", CONFIGS)
+def test_configurable_matches_reference_core(workdir, cut, shift, om):
+    """Every cutoff, every shift and both basis function types against the
+    reference core's configurable basis (runtime/mtp/radial_basis.h) at
+    1e-12: E, site energies, forces, virial."""
+    text = S.random_model("shapeev-06.mtp", 2, 6, 1.8, 4.8, -0.5, 0.5, S.rng_for(724),
+                          basis=S.configurable(cut, shift, om))
+    m = O.Model(text)
+    rng = S.rng_for(725)
+    s = S.displace(S.strain(S.lattice("bcc", (3, 3, 3), 2.87), rng, 0.03), rng, 0.15)
+    s.types = (S.uniform(rng, s.n) * 2).astype(np.int32)
+    pos = O.wrap(s.cell, s.pbc, s.pos)
+    nb = O.Neighbors.build(s.cell, s.pbc, pos, s.types, m.cutoff)
+    E, F, St, se = O.efs(m, nb)
+    Er, ser, Fr, vr = O.ref_mlip_efs(text, nb, s.types, m.cutoff, workdir, m.Z)
+    sym = 0.5 * (St + St.T)
+    v6 = np.array([sym[0, 0], sym[1, 1], sym[2, 2], sym[0, 1], sym[0, 2], sym[1, 2]])
+    assert rel_err(E, Er) < 1e-12 and rel_err(se, ser) < 1e-12
+    assert rel_err(F, Fr) < 1e-12 and rel_err(v6, vr) < 1e-12
 
 
 @needs_ref
