@@ -11,20 +11,61 @@ namespace {
 
 // Upload coefficient-dependent arrays: radial, species, moment coefficients
 // and the adjoint seeds (sum of the moment coefficients mapped to a moment,
-// accumulated in scalar order as potential_mtp.cpp:2974-2977 does).
+// accumulated in scalar order as potential_mtp.cpp:2974-2977 does).  With an
+// MTP-M head the seeds depend on the atom: the head tables go up instead --
+// the distinct moments the scalars map to, in first-appearance order, the
+// moment coefficients of each descriptor summed per distinct moment in
+// scalar order (the projection of Cpu::Executor, runtime/mtp/cpu/
+// mtp_cpu.cpp:138-157), the descriptor species and the head coefficients.
 int upload_coeffs(mtpx_context *ctx)
 {
     const Model &m = ctx->model;
-    std::vector<double> radial(m.coef.begin(), m.coef.begin() + m.nradial());
-    std::vector<double> species(m.coef.begin() + m.nradial(), m.coef.begin() + m.nradial() + m.Z);
-    std::vector<double> moment(m.coef.begin() + m.nradial() + m.Z, m.coef.end());
+    const size_t sp = (size_t)m.nradial(), mo = sp + (size_t)m.nspecies();
+    std::vector<double> radial(m.coef.begin(), m.coef.begin() + sp);
+    std::vector<double> species(m.coef.begin() + sp, m.coef.begin() + sp + m.Z);
+    std::vector<double> moment(m.coef.begin() + mo, m.coef.begin() + mo + m.S);
     std::vector<double> seed((size_t)m.K, 0.0);
-    for (int s = 0; s < m.S; ++s)
-        seed[m.map[s]] += moment[s];
+    if (m.linear())
+        for (int s = 0; s < m.S; ++s)
+            seed[m.map[s]] += moment[s];
     HIP_TRY(upload(ctx->radial, radial, ctx->stream), "upload radial coefficients");
     HIP_TRY(upload(ctx->species, species, ctx->stream), "upload species coefficients");
     HIP_TRY(upload(ctx->moment, moment, ctx->stream), "upload moment coefficients");
     HIP_TRY(upload(ctx->seed, seed, ctx->stream), "upload adjoint seeds");
+    ctx->dm.hids = nullptr;
+    ctx->dm.hproj = ctx->dm.hdsp = ctx->dm.hc = nullptr;
+    if (!m.linear()) {
+        const int P = m.head.P;
+        std::vector<int> compact((size_t)m.K, -1), ids;
+        for (int s = 0; s < m.S; ++s)
+            if (compact[m.map[s]] < 0) {
+                compact[m.map[s]] = (int)ids.size();
+                ids.push_back(m.map[s]);
+            }
+        const size_t NS = ids.size();
+        std::vector<double> proj((size_t)P * NS, 0.0);
+        for (int p = 0; p < P; ++p)
+            for (int s = 0; s < m.S; ++s)
+                proj[p * NS + compact[m.map[s]]] += m.coef[mo + (size_t)p * m.S + s];
+        std::vector<double> dsp(m.coef.begin() + sp + m.Z, m.coef.begin() + mo);
+        std::vector<double> hc(m.coef.begin() + mo + m.nmoment(), m.coef.end());
+        // a head without coefficients (mtp_m_li) still gets a valid pointer
+        if (ids.empty())
+            ids.push_back(0);
+        if (proj.empty())
+            proj.push_back(0.0);
+        if (hc.empty())
+            hc.push_back(0.0);
+        HIP_TRY(upload(ctx->head_ids, ids, ctx->stream), "upload head tables");
+        HIP_TRY(upload(ctx->head_proj, proj, ctx->stream), "upload head tables");
+        HIP_TRY(upload(ctx->head_dsp, dsp, ctx->stream), "upload head tables");
+        HIP_TRY(upload(ctx->head_coef, hc, ctx->stream), "upload head tables");
+        ctx->dm.hNS = (int)NS;
+        ctx->dm.hids = ctx->head_ids.as<int>();
+        ctx->dm.hproj = ctx->head_proj.as<double>();
+        ctx->dm.hdsp = ctx->head_dsp.as<double>();
+        ctx->dm.hc = ctx->head_coef.as<double>();
+    }
     HIP_TRY(hipStreamSynchronize(ctx->stream), "upload coefficients");
     ctx->dm.radial = ctx->radial.as<double>();
     ctx->dm.species = ctx->species.as<double>();
@@ -67,6 +108,13 @@ void fill_model_sizes(const Model &M, const Plan &P, DevModel &dm)
     dm.efs_red = P.efs_red;
     dm.efs_stage = P.efs_stage;
     dm.efs_acc = P.efs_acc;
+    dm.efs_head = P.efs_head;
+    dm.head = M.head.kind;
+    dm.hP = M.head.P;
+    dm.h1 = M.head.h1;
+    dm.h2 = M.head.h2;
+    dm.hact = M.head.act;
+    dm.hNS = 0;
     dm.tr_red1 = P.tr_red1;
     dm.tr_red4 = P.tr_red4;
     dm.tr_stage = P.tr_stage;
@@ -594,6 +642,37 @@ int mtpx_model_info(const mtpx_context *ctx, int out8[8])
     const Model &m = ctx->model;
     const int v[8] = {m.Z, m.M, m.R, m.K, m.B, m.T, m.S, m.ncoef()};
     std::memcpy(out8, v, sizeof v);
+    return MTPX_OK;
+}
+
+int mtpx_model_head(const mtpx_context *ctx, int out6[6])
+{
+    if (!ctx || !out6)
+        return MTPX_E_INVALID;
+    if (!ctx->has_model)
+        return MTPX_E_NO_MODEL;
+    const Head &h = ctx->model.head;
+    const int v[6] = {h.kind, h.P, h.h1, h.h2, h.act, h.Mc};
+    std::memcpy(out6, v, sizeof v);
+    return MTPX_OK;
+}
+
+int mtpx_parse_model_head(const char *text, int out6[6], char *err, int errlen)
+{
+    if (!text || !out6)
+        return MTPX_E_INVALID;
+    Model m;
+    std::string e;
+    if (!parse_mtp(text, m, e)) {
+        if (err && errlen > 0) {
+            std::strncpy(err, e.c_str(), (size_t)errlen - 1);
+            err[errlen - 1] = 0;
+        }
+        return MTPX_E_MODEL;
+    }
+    const Head &h = m.head;
+    const int v[6] = {h.kind, h.P, h.h1, h.h2, h.act, h.Mc};
+    std::memcpy(out6, v, sizeof v);
     return MTPX_OK;
 }
 

@@ -23,6 +23,8 @@ struct mtpx_context {
     // model buffers
     DBuf radial, species, moment, map, seed, slot_basic, slot_abc, dup, fwd_level, fwd_steps,
         fwd_lcomb, fwd_comb, bwd_level, bwd_steps, bwd_lcomb, bwd_comb, rb_table;
+    // MTP-M head tables (DevModel::hids, hproj, hdsp, hc)
+    DBuf head_ids, head_proj, head_dsp, head_coef;
 
     // neighbour lists
     bool has_nbh = false;
@@ -113,7 +115,8 @@ struct mtpx_context {
     {
         for (DBuf *b : {&radial, &species, &moment, &map, &seed, &slot_basic, &slot_abc, &dup,
                         &fwd_level, &fwd_steps, &fwd_lcomb, &fwd_comb, &bwd_level, &bwd_steps,
-                        &bwd_lcomb, &bwd_comb, &rb_table, &offsets, &idx, &type, &x, &y, &z, &d,
+                        &bwd_lcomb, &bwd_comb, &rb_table, &head_ids, &head_proj, &head_dsp,
+                        &head_coef, &offsets, &idx, &type, &x, &y, &z, &d,
                         &center_type, &rev_offsets, &rev_pairs, &forces, &site_energy, &partial,
                         &pair_ders, &out10, &soff, &center_structure, &site_virial, &benergy,
                         &bstress, &active, &tE, &wE, &tF, &wF, &tS, &wS, &dLdE, &dLdF, &dLdS,
@@ -146,6 +149,18 @@ inline int set_error(mtpx_context *ctx, int code, const std::string &msg)
     if (ctx)
         ctx->err = msg;
     return code;
+}
+
+// The training, gradient and linear-fit paths restate the linear MTP's
+// trainer (train/train_mtp.cpp); a potential with an MTP-M head is evaluated
+// (E/F/S, energies, sites, batches, losses) but not trained here.
+inline int need_linear(mtpx_context *ctx, const char *what)
+{
+    if (ctx->has_model && !ctx->model.linear())
+        return set_error(ctx, MTPX_E_MODEL,
+                         std::string(what) + " supports the linear MTP only (the loaded "
+                                             "potential has an MTP-M head)");
+    return MTPX_OK;
 }
 
 inline int hip_fail(mtpx_context *ctx, hipError_t e, const char *what)

@@ -100,19 +100,28 @@ __global__ __launch_bounds__(kWave *kMaxWaves) void efs_kernel(DevModel m, DevNe
         run_rules<false, false>(fwd_tab, m.fwd_level_step, m.fwd_level_comb, m.fwd_comb, m.nfwd, ws, lane, 0);
 
         // ---- site energy (potential_mtp.cpp:2966-2970) and adjoint seed ----
+        // (an MTP-M head: the head of the descriptors, its seeds per atom)
         double e = 0.0;
-        for (int s = lane; s < m.S; s += kWave)
-            e += L.moment[s] * mom[L.map[s]];
-        e = wave_sum(e);
+        const bool energy_only = flags & kEfsEnergyOnly;
+        if (m.head) {
+            e = head_energy(m, ti, mom, ws + m.efs_head, lane, !energy_only);
+        } else {
+            for (int s = lane; s < m.S; s += kWave)
+                e += L.moment[s] * mom[L.map[s]];
+            e = wave_sum(e);
+        }
         const double site_energy = m.species[ti] + e;
         if (lane == 0) {
             out.site_energy[i] = site_energy;
             sums[0] += site_energy;
         }
-        if (flags & kEfsEnergyOnly)  // getE (potential_mtp.cpp:2604-2621): no gradient
+        if (energy_only)  // getE (potential_mtp.cpp:2604-2621): no gradient
             continue;
-        for (int k = lane; k < m.K; k += kWave)
-            A[k] = L.seed[k];
+        if (m.head)
+            head_seeds(m, ws + m.efs_head, A, lane);
+        else
+            for (int k = lane; k < m.K; k += kWave)
+                A[k] = L.seed[k];
         wave_sync();
 
         run_rules<false, true>(bwd_tab, m.bwd_level_step, m.bwd_level_comb, m.bwd_comb, m.nbwd, ws, lane, 0);

@@ -384,6 +384,8 @@ int mtpx_train_lbfgs(mtpx_context *ctx, const mtpx_lbfgs_params *params, const d
         return set_error(ctx, MTPX_E_INVALID, "null argument");
     if (!ctx->has_model)
         return set_error(ctx, MTPX_E_NO_MODEL, "no model loaded");
+    if (need_linear(ctx, "mtpx_train_lbfgs") != MTPX_OK)
+        return MTPX_E_MODEL;
     if (const char *bad = check_params(*params))
         return set_error(ctx, MTPX_E_INVALID, bad);
     const int n = ctx->model.ncoef();

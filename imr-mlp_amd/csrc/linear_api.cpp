@@ -212,6 +212,8 @@ int mtpx_efs_components(mtpx_context *ctx, double *energy_cmpts, double *force_c
 {
     if (!ctx)
         return MTPX_E_INVALID;
+    if (need_linear(ctx, "mtpx_efs_components") != MTPX_OK)
+        return MTPX_E_MODEL;
     (void)hipSetDevice(ctx->device);
     int rc = run_lin(ctx);
     if (rc != MTPX_OK)
@@ -242,6 +244,8 @@ int mtpx_linear_rows(mtpx_context *ctx, int64_t *nrows, double *A, double *y)
         return set_error(ctx, MTPX_E_NO_TOPOLOGY, "no structures");
     if (!ctx->has_model)
         return set_error(ctx, MTPX_E_NO_MODEL, "no model loaded");
+    if (need_linear(ctx, "mtpx_linear_rows") != MTPX_OK)
+        return MTPX_E_MODEL;
     (void)hipSetDevice(ctx->device);
     int64_t R = 0;
     int rc = build_rows(ctx, R);
@@ -284,6 +288,8 @@ int mtpx_linear_system(mtpx_context *ctx, double *G, double *b)
         return set_error(ctx, MTPX_E_NO_TOPOLOGY, "no structures");
     if (!ctx->has_model)
         return set_error(ctx, MTPX_E_NO_MODEL, "no model loaded");
+    if (need_linear(ctx, "mtpx_linear_system") != MTPX_OK)
+        return MTPX_E_MODEL;
     if (!gram_fits(row_width(ctx)))
         return set_error(ctx, MTPX_E_CAPACITY, "linear system of more than 1007 coefficients");
     (void)hipSetDevice(ctx->device);

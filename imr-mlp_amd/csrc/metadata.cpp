@@ -8,11 +8,17 @@
 // form the reference's vendored JSON library produces: object keys in byte
 // order, no blanks, integral numbers below 2^53 without a fraction and other
 // numbers with 17 significant digits, and its string escapes.  This file
-// reads and writes that form; only the linear-MTP subset of the schema is
-// accepted (type "MTP", model "linear"), which is what PotMTP::Load admits
-// (MTPMetadata::require_model, tools/mtp_metadata.h:520-529).
+// reads and writes that form for the short-range models: the linear MTP
+// (type "MTP", model "linear") and MTP-M potentials (type "MTP_M" with one
+// of the heads mtp_m_li / q2 / fs / n1 / n2), what the standalone runtime
+// reader admits (MTPMetadata::require_model with nonlinear models allowed,
+// tools/mtp_metadata.h:520-529; runtime/mtp/mlip.cpp:70-296).  Long-range
+// terms (type MTP_LES, "long_range") are refused.
 #include "mtpx_internal.hpp"
 
+#include <cctype>
+#include <cerrno>
+#include <climits>
 #include <cmath>
 #include <cstdio>
 #include <cstdlib>
@@ -338,8 +344,44 @@ bool fail(std::string &err, const std::string &msg)
 
 bool nonempty_text(const Json &v) { return v.kind == Json::Str && !v.str.empty(); }
 
-// Tag::validate for the linear MTP (tools/mtp_metadata.h:133-204, with
-// MTPMetadata::require_model, :520-529).
+// MTPMetadata::integer (tools/mtp_metadata.h:38-46): an integral number in
+// [minimum, INT_MAX].
+bool json_int(const Json &v, int minimum, int &out)
+{
+    if (v.kind != Json::Num || !std::isfinite(v.num) || v.num < minimum ||
+        v.num > 2147483647.0 || std::floor(v.num) != v.num)
+        return false;
+    out = (int)v.num;
+    return true;
+}
+
+std::string upper(std::string s)
+{
+    for (char &c : s)
+        c = (char)std::toupper((unsigned char)c);
+    return s;
+}
+
+// canonical_model (tools/mtp_metadata.h:66-71)
+std::string canonical_model(const std::string &name)
+{
+    return name == "mtp_m_nn2" ? std::string("mtp_m_n2") : name;
+}
+
+const char *const kHeadNames[] = {"linear", "mtp_m_li", "mtp_m_q2", "mtp_m_fs", "mtp_m_n1",
+                                  "mtp_m_n2"};
+const char *const kActNames[] = {"TANH", "RELU", "SIGMOID", "LINEAR"};
+
+int head_index(const std::string &model)
+{
+    for (int k = 0; k < 6; ++k)
+        if (model == kHeadNames[k])
+            return k;
+    return -1;
+}
+
+// Tag::validate (tools/mtp_metadata.h:133-204) with MTPMetadata::require_model
+// (:520-529) for the short-range models.
 bool validate(const std::map<std::string, Json> &f, int Z, std::string &err)
 {
     auto get = [&](const char *k) -> const Json * {
@@ -356,11 +398,14 @@ bool validate(const std::map<std::string, Json> &f, int Z, std::string &err)
         return fail(err, "type and model are required");
     if (!nonempty_text(*type) || !nonempty_text(*model))
         return fail(err, "type and model must be nonempty strings");
-    if (type->str != "MTP")
-        return fail(err, "model type '" + type->str + "' is not a linear MTP");
-    if (model->str != "linear")
-        return fail(err, "this potential does not support the model '" + model->str + "'");
-    if (get("q") || get("nn"))
+    if (type->str == "MTP_LES")
+        return fail(err, "long-range terms are not supported");
+    if (type->str != "MTP" && type->str != "MTP_M")
+        return fail(err, "unknown model type");
+    const std::string name = canonical_model(model->str);
+    if (head_index(name) < 0)
+        return fail(err, "unknown model");
+    if (type->str != "MTP_M" && name != "linear")
         return fail(err, "ordinary MTP cannot declare an external head");
     if (get("long_range"))
         return fail(err, "long-range terms are not supported");
@@ -377,12 +422,85 @@ bool validate(const std::map<std::string, Json> &f, int Z, std::string &err)
                 return fail(err, "duplicate element '" + x.str + "'");
         }
     }
-    if (const Json *c = get("model_coeffs_count")) {
-        double ip;
-        if (c->kind != Json::Num || c->num < 0 || c->num > 2147483647.0 ||
-            std::modf(c->num, &ip) != 0)
+    int v;
+    if (const Json *c = get("q"))
+        if (!json_int(*c, 1, v))
+            return fail(err, "q is outside the integer range");
+    if (const Json *c = get("model_coeffs_count"))
+        if (!json_int(*c, 0, v))
             return fail(err, "model_coeffs_count is outside the integer range");
+    if (type->str == "MTP_M") {
+        const Json *q = get("q");
+        if (!q)
+            return fail(err, "MTP_M requires q");
+        json_int(*q, 1, v);
+        if (name == "linear")
+            return fail(err, "MTP_M requires an external model");
+        if (name == "mtp_m_li" && v != 1)
+            return fail(err, "linear head requires q=1");
+        if ((name == "mtp_m_q2" || name == "mtp_m_fs") && v != 2)
+            return fail(err, "analytic head requires q=2");
+    } else if (get("q") || get("nn")) {
+        return fail(err, "ordinary MTP cannot declare an external head");
     }
+    if (const Json *nn = get("nn")) {
+        if (nn->kind != Json::Obj)
+            return fail(err, "nn must be an object");
+        auto a = nn->obj.find("activation");
+        auto h = nn->obj.find("hidden_layers");
+        if (a == nn->obj.end() || !nonempty_text(a->second))
+            return fail(err, "nn.activation must be a nonempty string");
+        if (h == nn->obj.end() || h->second.kind != Json::Arr)
+            return fail(err, "nn.hidden_layers must be an array");
+        const size_t expected = name == "mtp_m_n1" ? 1 : name == "mtp_m_n2" ? 2 : 0;
+        if (h->second.arr.size() != expected || expected == 0)
+            return fail(err, "nn.hidden_layers conflicts with model");
+        const std::string act = upper(a->second.str);
+        if (act != "TANH" && act != "RELU" && act != "SIGMOID" && act != "LINEAR")
+            return fail(err, "unknown activation");
+        for (const Json &layer : h->second.arr)
+            if (!json_int(layer, 1, v))
+                return fail(err, "nn.hidden_layers is outside the integer range");
+    }
+    return true;
+}
+
+// Head-field values of read_mtp_gpu_metadata (runtime/mtp/mlip.cpp:120-201):
+// "mtp_<key>" -> value text, merged from the tag and the file's lines.
+using Fields = std::map<std::string, std::string>;
+
+// MTPMetadata::merge_legacy with normalize_legacy (tools/mtp_metadata.h:
+// 400-421).
+bool merge_field(Fields &f, const std::string &key, std::string value, std::string &err)
+{
+    if (key == "mtp_model") {
+        value = canonical_model(value);
+        if (value == "mtp")
+            value = "linear";
+    }
+    if (key == "mtp_activation")
+        value = upper(value);
+    auto it = f.find(key);
+    if (it != f.end() && it->second != value) {
+        err = "Invalid MTP metadata: MTP metadata: conflicting JSON/footer metadata for " + key;
+        return false;
+    }
+    f[key] = value;
+    return true;
+}
+
+// std::stoi over the whole value (mlip.cpp:169-176)
+bool whole_int(const std::string &s, int &out)
+{
+    if (s.empty())
+        return false;
+    char *e = nullptr;
+    errno = 0;
+    const long v = std::strtol(s.c_str(), &e, 10);
+    if (e != s.c_str() + s.size() || errno || v < INT_MIN || v > INT_MAX ||
+        std::isspace((unsigned char)s[0]))
+        return false;
+    out = (int)v;
     return true;
 }
 
@@ -438,20 +556,204 @@ bool tag_parse(const std::string &raw, int Z, MetaTag &tag, std::string &err)
     if (lg != tag.fields.end() && !nonempty_text(lg->second))
         return fail(err, "legacy_tag must be a nonempty string");
     tag.legacy = lg != tag.fields.end() ? lg->second.str : "";
-    return validate(tag.fields, Z, err);
+    if (!validate(tag.fields, Z, err))
+        return false;
+    // Tag::parse's canonical forms (tools/mtp_metadata.h:319-329)
+    tag.fields["model"].str = canonical_model(tag.fields["model"].str);
+    auto nn = tag.fields.find("nn");
+    if (nn != tag.fields.end())
+        nn->second.obj["activation"].str = upper(nn->second.obj["activation"].str);
+    return true;
 }
 
-// Tag::output(model_metadata()) serialised (tools/mtp_metadata.h:353-370,
-// PotMTP::model_metadata potentials/potential_mtp.h:127-130).
-std::string tag_output(const MetaTag &tag)
+// read_mtp_gpu_metadata (runtime/mtp/mlip.cpp:70-296): the head fields of
+// the tag (MTPMetadata::legacy_model_fields, tools/mtp_metadata.h:374-398)
+// merged with the "mtp_<key> = value" lines of the text before any
+// "#MVS_v1.1" payload, then checked against the head's dimensions.
+bool head_parse(const std::string &text, const MetaTag &tag, Head &head, std::string &err)
+{
+    head = Head();
+    Fields f;
+    bool model_coeffs = false;
+    const std::string pre = "Invalid MTP metadata: ";
+    if (!tag.fields.empty()) {
+        f["mtp_model"] = canonical_model(tag.fields.at("model").str);
+        int v;
+        auto q = tag.fields.find("q");
+        if (q != tag.fields.end() && json_int(q->second, 0, v))
+            f["mtp_descriptor_count"] = std::to_string(v);
+        auto c = tag.fields.find("model_coeffs_count");
+        if (c != tag.fields.end() && json_int(c->second, 0, v))
+            f["mtp_model_coeffs_count"] = std::to_string(v);
+        auto nn = tag.fields.find("nn");
+        if (nn != tag.fields.end()) {
+            const Json &o = nn->second;
+            f["mtp_activation"] = upper(o.obj.at("activation").str);
+            const std::vector<Json> &layers = o.obj.at("hidden_layers").arr;
+            json_int(layers[0], 1, v);
+            f["mtp_hidden1"] = std::to_string(v);
+            if (layers.size() == 2)
+                json_int(layers[1], 1, v);
+            f["mtp_hidden2"] = layers.size() == 2 ? std::to_string(v) : "0";
+        }
+    }
+    size_t pos = 0;
+    while (pos <= text.size()) {
+        size_t eol = text.find('\n', pos);
+        if (eol == std::string::npos)
+            eol = text.size();
+        std::string line = trim(text.substr(pos, eol - pos));
+        pos = eol + 1;
+        if (line.rfind("#MVS_v1.1", 0) == 0)
+            break;
+        if (line.rfind("les_", 0) == 0 || line.rfind("sog_", 0) == 0 ||
+            line.rfind("lr_les", 0) == 0 || line.rfind("long_range", 0) == 0)
+            return fail(err, "long-range payload is unsupported by the short-range runtime");
+        if (line.rfind("model_coeffs", 0) == 0)
+            model_coeffs = true;
+        if (!line.empty() && line[0] == '#')
+            line = trim(line.substr(1));
+        if (line.rfind("mtp_", 0) != 0)
+            continue;
+        const size_t eq = line.find('=');
+        if (eq == std::string::npos)
+            continue;
+        if (!merge_field(f, trim(line.substr(0, eq)), trim(line.substr(eq + 1)), err))
+            return false;
+    }
+    // a value that does not parse reports "invalid value for <key>", the
+    // model and activation names included (mlip.cpp:196-200 catches their
+    // own errors)
+    int model = kHeadNone, q = 0, mcc = 0, h1 = 0, h2 = 0, act = kActTanh;
+    for (const auto &kv : f) {
+        const std::string &k = kv.first, &v = kv.second;
+        bool ok = true;
+        if (k == "mtp_model") {
+            model = head_index(v);
+            ok = model >= 0;
+        } else if (k == "mtp_descriptor_count") {
+            ok = whole_int(v, q);
+        } else if (k == "mtp_model_coeffs_count") {
+            ok = whole_int(v, mcc);
+        } else if (k == "mtp_hidden1") {
+            ok = whole_int(v, h1);
+        } else if (k == "mtp_hidden2") {
+            ok = whole_int(v, h2);
+        } else if (k == "mtp_activation") {
+            act = -1;
+            for (int a = 0; a < 4; ++a)
+                if (v == kActNames[a])
+                    act = a;
+            ok = act >= 0;
+        }
+        if (!ok) {
+            err = pre + "invalid value for " + k + ": '" + v + "'";
+            return false;
+        }
+    }
+    if (q < 0 || mcc < 0 || h1 < 0 || h2 < 0) {
+        err = pre + "model dimensions and coefficient counts must be nonnegative";
+        return false;
+    }
+    for (int d : {q, mcc, h1, h2})
+        if ((size_t)d > text.size()) {
+            err = pre + "model dimension exceeds the serialized model size";
+            return false;
+        }
+    auto bad = [&](const char *msg) {
+        err = pre + msg;
+        return false;
+    };
+    const bool neural = model == kHeadNn1 || model == kHeadNn2;
+    if (!neural && (h1 != 0 || h2 != 0))
+        return bad("non-neural models require zero hidden dimensions");
+    if (model == kHeadNn1 && h2 != 0)
+        return bad("NN1 requires zero hidden2");
+    if (model == kHeadNone) {
+        if (model_coeffs)
+            return bad("model_coeffs is present but mtp_model metadata is missing");
+        return true;
+    }
+    if (!model_coeffs)
+        return bad("nonlinear mtp_model requires a model_coeffs section");
+    if (model == kHeadLi) {
+        if (q == 0)
+            q = 1;
+        if (q != 1 || mcc != 0)
+            return bad("linear MTP-M requires one descriptor and no head coefficients");
+    } else if (model == kHeadQ2 || model == kHeadFs) {
+        if (q == 0)
+            q = 2;
+        else if (q != 2)
+            return bad("analytic q2/fs models require descriptor_count 2");
+        const int expected = model == kHeadQ2 ? 5 : 1;
+        if (mcc == 0)
+            mcc = expected;
+        else if (mcc != expected)
+            return bad("analytic model coefficient count does not match model type");
+    } else {
+        if (q <= 0 || h1 <= 0)
+            return bad("neural model requires positive descriptor_count and hidden1");
+        if (model == kHeadNn2 && h2 <= 0)
+            return bad("NN2 model requires positive hidden2");
+        const long long expected =
+            model == kHeadNn1 ? (long long)h1 * ((long long)q + 2)
+                              : (long long)q * h1 + h1 + (long long)h1 * h2 + 2LL * h2;
+        if (expected > INT_MAX)
+            return bad("neural coefficient count overflows the model index type");
+        if (model == kHeadNn2 && act == kActLinear)
+            return bad("NN2 does not support LINEAR activation");
+        if (mcc == 0)
+            mcc = (int)expected;
+        else if (mcc != expected)
+            return bad("neural model coefficient count does not match dimensions");
+    }
+    head.kind = model;
+    head.P = q;
+    head.h1 = neural ? h1 : 0;
+    head.h2 = model == kHeadNn2 ? h2 : 0;
+    head.act = act;
+    head.Mc = mcc;
+    return true;
+}
+
+// Tag::output(model_metadata()) serialised (tools/mtp_metadata.h:353-370;
+// PotMTP::model_metadata potentials/potential_mtp.h:127-130 for the linear
+// MTP, PotMTP_M::model_metadata potentials/potential_mtp_m.h:1564-1589 with a
+// head).
+std::string tag_output(const MetaTag &tag, const Head &head)
 {
     Json v;
     v.kind = Json::Obj;
     v.obj = tag.fields;
     for (const char *k : {"type", "model", "q", "nn", "model_coeffs_count", "long_range"})
         v.obj.erase(k);
-    v.obj["type"] = text_value("MTP");
-    v.obj["model"] = text_value("linear");
+    auto number = [](double x) {
+        Json n;
+        n.kind = Json::Num;
+        n.num = x;
+        return n;
+    };
+    if (head.kind != kHeadNone) {
+        v.obj["type"] = text_value("MTP_M");
+        v.obj["model"] = text_value(kHeadNames[head.kind]);
+        v.obj["q"] = number(head.P);
+        v.obj["model_coeffs_count"] = number(head.Mc);
+        if (head.kind == kHeadNn1 || head.kind == kHeadNn2) {
+            Json nn, layers;
+            nn.kind = Json::Obj;
+            layers.kind = Json::Arr;
+            layers.arr.push_back(number(head.h1));
+            if (head.kind == kHeadNn2)
+                layers.arr.push_back(number(head.h2));
+            nn.obj["activation"] = text_value(kActNames[head.act]);
+            nn.obj["hidden_layers"] = layers;
+            v.obj["nn"] = nn;
+        }
+    } else {
+        v.obj["type"] = text_value("MTP");
+        v.obj["model"] = text_value("linear");
+    }
     v.obj["schema"] = text_value("gpml.mtp.metadata");
     Json one;
     one.kind = Json::Num;

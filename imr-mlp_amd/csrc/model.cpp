@@ -557,6 +557,11 @@ bool parse_mtp(const std::string &text, Model &m, std::string &err)
     }
     in.skip_past('\n', 1000);
 
+    // the MTP-M head, if the potential declares one (its coefficient layout,
+    // PotMTP_M::Load, potentials/potential_mtp_m.h:2054-2063)
+    if (!head_parse(text, m.tag, m.head, err))
+        return false;
+    const int nsp = m.nspecies(), nmom = m.nmoment();
     m.coef.assign((size_t)m.ncoef(), 1e-3);
     std::copy(radial.begin(), radial.end(), m.coef.begin());
     double *lin = m.coef.data() + m.nradial();
@@ -564,7 +569,7 @@ bool parse_mtp(const std::string &text, Model &m, std::string &err)
     in.clear();
     if (key == "species_coeffs") {
         in.skip(4);
-        for (int i = 0; i < Z; ++i) {
+        for (int i = 0; i < nsp; ++i) {
             lin[i] = in.real();
             in.ch();
             if (!in.ok())
@@ -577,11 +582,24 @@ bool parse_mtp(const std::string &text, Model &m, std::string &err)
     if (key == "moment_coeffs") {
         in.skip(2);
         in.skip_past('{', 10);
-        for (int i = 0; i < m.S; ++i) {
-            lin[Z + i] = in.real();
+        for (int i = 0; i < nmom; ++i) {
+            lin[nsp + i] = in.real();
             in.ch();
             if (!in.ok())
                 return fail(err, "Error reading .mtp file, missing moment coefficient");
+        }
+        in.skip_past('\n', 1000);
+        key = in.word();
+        in.clear();
+    }
+    if (!m.linear() && key == "model_coeffs") {  // :2112-2124
+        in.skip(2);
+        in.skip_past('{', 10);
+        for (int i = 0; i < m.head.Mc; ++i) {
+            lin[nsp + nmom + i] = in.real();
+            in.ch();
+            if (!in.ok())
+                return fail(err, "Error reading .mtp file, missing model coefficient");
         }
     }
     return validate_model(m, err);
@@ -608,7 +626,7 @@ std::string save_mtp(const Model &m)
     num(m.bases.empty() ? m.scaling : m.bases[0].scaling);
     o += "\nspecies_count = ";
     integer(m.Z);
-    o += "\npotential_tag = " + tag_output(m.tag) + "\n";
+    o += "\npotential_tag = " + tag_output(m.tag, m.head) + "\n";
     if (m.split)
         o += "radial_basis_split = 1\n";
     for (size_t q = 0; q < m.bases.size(); ++q) {
@@ -705,19 +723,36 @@ std::string save_mtp(const Model &m)
             o += ", ";
         integer(m.map[i]);
     }
-    o += "}\nspecies_coeffs = {";
-    for (int i = 0; i < m.Z; ++i) {
-        if (i)
-            o += ", ";
-        num(m.coef[m.nradial() + i]);
-    }
-    o += "}\nmoment_coeffs = {";
-    for (int i = 0; i < m.S; ++i) {
-        if (i)
-            o += ", ";
-        num(m.coef[m.nradial() + m.Z + i]);
-    }
+    auto list = [&](const char *name, int first, int count) {
+        o += name;
+        o += " = {";
+        for (int i = 0; i < count; ++i) {
+            if (i)
+                o += ", ";
+            num(m.coef[first + i]);
+        }
+        o += "}\n";
+    };
     o += "}\n";
+    const int sp = m.nradial(), mo = sp + m.nspecies(), hc = mo + m.nmoment();
+    list("species_coeffs", sp, m.nspecies());
+    list("moment_coeffs", mo, m.nmoment());
+    if (!m.linear()) {
+        // PotMTP_M::Save (potentials/potential_mtp_m.h:2256-2336): the head's
+        // coefficients and the "# mtp_*" lines of a short-range potential
+        static const char *heads[] = {"linear", "mtp_m_li", "mtp_m_q2", "mtp_m_fs", "mtp_m_n1",
+                                      "mtp_m_n2"};
+        static const char *acts[] = {"TANH", "RELU", "SIGMOID", "LINEAR"};
+        list("model_coeffs", hc, m.head.Mc);
+        o += std::string("# mtp_model = ") + heads[m.head.kind] + "\n";
+        o += "# mtp_descriptor_count = " + std::to_string(m.head.P) + "\n";
+        o += "# mtp_model_coeffs_count = " + std::to_string(m.head.Mc) + "\n";
+        if (m.head.kind == kHeadNn1 || m.head.kind == kHeadNn2) {
+            o += std::string("# mtp_activation = ") + acts[m.head.act] + "\n";
+            o += "# mtp_hidden1 = " + std::to_string(m.head.h1) + "\n";
+            o += "# mtp_hidden2 = " + std::to_string(m.head.h2) + "\n";
+        }
+    }
     return o;
 }
 
@@ -743,6 +778,12 @@ bool validate_model(const Model &m, std::string &err)
             return fail(err, "invalid radial basis");
     if (!(m.rmax > m.rmin) || !std::isfinite(m.rmin) || !std::isfinite(m.rmax))
         return fail(err, "invalid radial basis interval");
+    const Head &h = m.head;
+    if (h.kind < kHeadNone || h.kind > kHeadNn2 || h.act < kActTanh || h.act > kActLinear ||
+        h.P < 1 || h.h1 < 0 || h.h2 < 0 || h.Mc < 0 || (h.kind == kHeadNone && (h.P != 1 || h.Mc)))
+        return fail(err, "invalid MTP-M head");
+    if ((long long)h.P * std::max(m.S, m.Z) > (1 << 24) || h.h1 > (1 << 16) || h.h2 > (1 << 16))
+        return fail(err, "MTP-M head exceeds the supported size");
     if ((int)m.basic.size() != 4 * m.B || (int)m.times.size() != 4 * m.T ||
         (int)m.map.size() != m.S || (int)m.coef.size() != m.ncoef())
         return fail(err, "inconsistent model array sizes");
@@ -917,6 +958,13 @@ bool build_plan(const Model &m, Plan &p, std::string &err)
     }
     p.efs_acc = (end + 3) & ~3;
     p.priv_doubles = p.efs_acc + 12;  // energy, virial[9], padding
+    if (!m.linear()) {
+        const long long hd = 2LL * m.head.P + 2LL * m.head.h1 + m.head.h2;
+        if (hd > 0xffff)
+            return fail(err, "MTP-M head too large: its work space exceeds 65535 doubles");
+        p.efs_head = p.priv_doubles;
+        p.priv_doubles += (int)((hd + 3) & ~3LL);
+    }
     if (p.priv_doubles > 0xffff)
         return fail(err, "model too large: per-atom work space exceeds 65535 doubles");
     for (int t = 0; t < m.T; ++t)

@@ -753,6 +753,141 @@ __device__ __forceinline__ void stage_shared(const DevModel &m, const Shared &L,
     }
 }
 
+// ---- MTP-M site heads -------------------------------------------------------
+// The activations of the neural heads and their derivatives (runtime/mtp/cpu/
+// mtp_cpu.cpp:21-45).
+__device__ __forceinline__ double head_activate(double x, int act, double &der)
+{
+    if (act == kActTanh) {
+        const double v = tanh(x);
+        der = 1.0 - v * v;
+        return v;
+    }
+    if (act == kActRelu) {
+        der = x > 0.0 ? 1.0 : 0.0;
+        return x > 0.0 ? x : 0.0;
+    }
+    if (act == kActSigmoid) {
+        const double v = 1.0 / (1.0 + exp(-x));
+        der = v * (1.0 - v);
+        return v;
+    }
+    der = 1.0;
+    return x;
+}
+
+// The site energy of an MTP-M potential less its species term, for the
+// centre species t, from the moments in LDS (mom), in every lane
+// (Executor::evaluate_site and Executor::head, mtp_cpu.cpp:291-368,
+// :418-427): the descriptors Q_p = dspecies[p Z + t] + sum_a proj[p][a]
+// m(ids[a]) are wave sums over the distinct scalar moments, the head's
+// hidden units run one per lane.  With grad, hs[P + p] = dE/dQ_p.  hs, the
+// wave's head work space: Q [P], dE/dQ [P], first-layer activations and
+// then responses [h1], their derivatives [h1], second-layer adjoints [h2].
+__device__ __forceinline__ double head_energy(const DevModel &m, int t, const double *mom,
+                                              double *hs, int lane, bool grad)
+{
+    const int P = m.hP, NS = m.hNS, h1 = m.h1, h2 = m.h2;
+    double *Q = hs, *dQ = hs + P, *a1 = dQ + P, *d1 = a1 + h1, *g2 = d1 + h1;
+    for (int p = 0; p < P; ++p) {
+        const double *w = m.hproj + (size_t)p * NS;
+        double v = 0.0;
+        for (int a = lane; a < NS; a += kWave)
+            v += w[a] * mom[m.hids[a]];
+        v = wave_sum(v);
+        if (lane == 0)
+            Q[p] = m.hdsp[p * m.Z + t] + v;
+    }
+    wave_sync();
+    const double *c = m.hc;
+    double e = 0.0;
+    if (m.head == kHeadLi) {
+        e = Q[0];
+        if (grad && lane == 0)
+            dQ[0] = 1.0;
+    } else if (m.head == kHeadQ2) {
+        const double x = Q[0], y = Q[1];
+        e = c[0] * x + c[1] * y + c[2] * x * x + c[3] * y * y + c[4] * x * y;
+        if (grad && lane == 0) {
+            dQ[0] = c[0] + 2.0 * c[2] * x + c[4] * y;
+            dQ[1] = c[1] + 2.0 * c[3] * y + c[4] * x;
+        }
+    } else if (m.head == kHeadFs) {
+        e = Q[0] + c[0] * asinh(Q[1]);
+        if (grad && lane == 0) {
+            dQ[0] = 1.0;
+            dQ[1] = c[0] / sqrt(1.0 + Q[1] * Q[1]);
+        }
+    } else {
+        // NN1: [W1 (h1 x P) | out (h1) | b1 (h1)]; NN2: [W1 | b1 | W2 (h2 x h1)
+        // | b2 (h2) | out (h2)] (the coefficient order of mtp_cpu.cpp:334-337)
+        const bool nn2 = m.head == kHeadNn2;
+        const double *b1 = c + P * h1 + (nn2 ? 0 : h1);
+        const double *w2 = b1 + h1, *b2 = w2 + (size_t)h1 * h2;
+        const double *out = nn2 ? b2 + h2 : c + P * h1;
+        double part = 0.0;
+        for (int h = lane; h < h1; h += kWave) {
+            double v = b1[h], d;
+            for (int p = 0; p < P; ++p)
+                v += c[h * P + p] * Q[p];
+            const double a = head_activate(v, m.hact, d);
+            a1[h] = a;
+            d1[h] = d;
+            if (!nn2)
+                part += out[h] * a;
+        }
+        wave_sync();
+        if (nn2) {
+            for (int k = lane; k < h2; k += kWave) {
+                double v = b2[k], d;
+                for (int h = 0; h < h1; ++h)
+                    v += w2[(size_t)k * h1 + h] * a1[h];
+                part += out[k] * head_activate(v, m.hact, d);
+                g2[k] = out[k] * d;
+            }
+            wave_sync();
+        }
+        e = wave_sum(part);
+        if (grad) {
+            // responses over the activations they replace (each lane its own)
+            for (int h = lane; h < h1; h += kWave) {
+                double r = nn2 ? 0.0 : out[h];
+                if (nn2)
+                    for (int k = 0; k < h2; ++k)
+                        r += w2[(size_t)k * h1 + h] * g2[k];
+                a1[h] = r * d1[h];
+            }
+            wave_sync();
+            for (int p = lane; p < P; p += kWave) {
+                double g = 0.0;
+                for (int h = 0; h < h1; ++h)
+                    g += c[h * P + p] * a1[h];
+                dQ[p] = g;
+            }
+        }
+    }
+    wave_sync();
+    return e;
+}
+
+// The adjoint seeds of an MTP-M site into A [K]: zero, then
+// A(ids[a]) = sum_p proj[p][a] dE/dQ_p (mtp_cpu.cpp:435-442).
+__device__ __forceinline__ void head_seeds(const DevModel &m, const double *hs, double *A,
+                                           int lane)
+{
+    const int P = m.hP, NS = m.hNS;
+    const double *dQ = hs + P;
+    for (int k = lane; k < m.K; k += kWave)
+        A[k] = 0.0;
+    wave_sync();
+    for (int a = lane; a < NS; a += kWave) {
+        double v = 0.0;
+        for (int p = 0; p < P; ++p)
+            v += m.hproj[(size_t)p * NS + a] * dQ[p];
+        A[m.hids[a]] = v;
+    }
+}
+
 // Launch shape for a kernel whose waves each own `priv_doubles` of LDS work
 // space next to the block-shared model tables: rule tables in LDS unless that
 // costs waves; false if a single wave does not fit.

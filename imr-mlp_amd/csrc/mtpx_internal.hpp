@@ -96,8 +96,23 @@ struct MetaTag {
     std::map<std::string, Json> fields;
     std::string legacy;
 };
+// MTP-M site-energy heads (potentials/potential_mtp_m.h; the kinds of
+// mlip::site_model_type, runtime/mtp/mlip.h:54) and the activations of the
+// neural ones (mlip::activation_type).
+enum HeadKind { kHeadNone = 0, kHeadLi, kHeadQ2, kHeadFs, kHeadNn1, kHeadNn2 };
+enum ActKind { kActTanh = 0, kActRelu, kActSigmoid, kActLinear };
+// The head of a potential: kind, descriptor count P (q), hidden layer sizes,
+// activation and head coefficient count.  kHeadNone is the linear MTP (P 1).
+struct Head {
+    int kind = kHeadNone, P = 1, h1 = 0, h2 = 0, act = kActTanh, Mc = 0;
+};
 bool tag_parse(const std::string &raw, int Z, MetaTag &tag, std::string &err);
-std::string tag_output(const MetaTag &tag);
+// The head a potential declares, from its structured tag and its
+// "mtp_<key> = value" lines (read_mtp_gpu_metadata, runtime/mtp/mlip.cpp:
+// 70-296), which also asks a head for a model_coeffs section and refuses one
+// without a head.
+bool head_parse(const std::string &text, const MetaTag &tag, Head &head, std::string &err);
+std::string tag_output(const MetaTag &tag, const Head &head);
 
 // Radial basis kinds (basis/basis.h:19-29): the Chebyshev polynomials of
 // xi = (2r - (min + max)) / (max - min) times an envelope, and the
@@ -134,8 +149,9 @@ struct RadialBasis {
 // expm1(lambda), tanh(scale_lambda), 0}.
 constexpr int kRbStride = 16;
 
-// Host-side model: the linear MTP (potentials/potential_mtp.h:93) plus the
-// launch plan derived from its contraction graph.
+// Host-side model: the linear MTP (potentials/potential_mtp.h:93) or an
+// MTP-M potential (potentials/potential_mtp_m.h) plus the launch plan derived
+// from its contraction graph.
 struct Model {
     int Z = 0, M = 0, R = 0, K = 0, B = 0, T = 0, S = 0;
     // rmin / scaling of the first basis, rmax the largest cutoff of any pair
@@ -149,9 +165,16 @@ struct Model {
     std::vector<int> basic;   // [B][4]
     std::vector<int> times;   // [T][4]
     std::vector<int> map;     // [S]
-    std::vector<double> coef; // [Z*Z*M*R | Z | S]
+    // linear MTP: [Z*Z*M*R | Z | S]; with a head (PotMTP_M::Load,
+    // potential_mtp_m.h:2057-2063): [Z*Z*M*R | Z | P*Z | P*S | Mc] -- species,
+    // descriptor species, moment coefficients per descriptor, head
+    std::vector<double> coef;
+    Head head;
+    bool linear() const { return head.kind == kHeadNone; }
     int nradial() const { return Z * Z * M * R; }
-    int ncoef() const { return nradial() + Z + S; }
+    int nspecies() const { return linear() ? Z : Z * (head.P + 1); }
+    int nmoment() const { return head.P * S; }
+    int ncoef() const { return nradial() + nspecies() + nmoment() + head.Mc; }
 };
 
 // Parses .mtp text (PotMTP::Load grammar).
@@ -184,9 +207,11 @@ struct Plan {
     // after the species where they do not fit there.
     int tr_delta = 0, tr_red1 = 0, tr_red4 = 0, tr_stage = 0, tr_grad = 0, tr_ctype = 0,
         tr_priv = 0;
-    // E/F/S kernel: transpose buffer, slot-ordered adjoints and the wave's
-    // energy/virial sums (offsets in doubles).
-    int efs_red = 0, efs_stage = 0, efs_acc = 0;
+    // E/F/S kernel: transpose buffer, slot-ordered adjoints, the wave's
+    // energy/virial sums and, with an MTP-M head, the head's work space
+    // (descriptors, their adjoints, hidden activations and derivatives, the
+    // second layer's adjoints) (offsets in doubles).
+    int efs_red = 0, efs_stage = 0, efs_acc = 0, efs_head = 0;
     // first slot of each (nu, mu) block, -1 where absent: [nu * kMaxMu + mu]
     int slot_base[(kMaxNu + 1) * kMaxMu];
     // Lane-major step tables, one per direction.  Level L owns steps
@@ -260,6 +285,14 @@ struct DevModel {
     int K4, dummy, part0, red0, priv_doubles;  // per-wave work space (Plan)
     int tr_delta, tr_red1, tr_red4, tr_stage, tr_grad, tr_ctype, tr_priv;
     int efs_red, efs_stage, efs_acc;
+    // MTP-M head (kHeadNone: the linear MTP of species, moment and seed):
+    // kind, descriptors P, distinct scalar moments NS, hidden sizes,
+    // activation and the per-wave head work space (offset in doubles)
+    int head, hP, hNS, h1, h2, hact, efs_head;
+    const int *hids;      // [NS] the distinct moments the scalars map to
+    const double *hproj;  // [P][NS] moment coefficients summed per distinct moment
+    const double *hdsp;   // [P][Z] descriptor species coefficients
+    const double *hc;     // [Mc] head coefficients
     int nradial, ncoef;
     int slot_base[(kMaxNu + 1) * kMaxMu];
     int fwd_nsteps, bwd_nsteps;                 // steps per lane, all levels

@@ -389,6 +389,8 @@ int mtpx_accumulate_gradient(mtpx_context *ctx, const double *dLdE, const double
     if (!ctx || !gradient)
         return set_error(ctx, MTPX_E_INVALID, "null argument");
     int rc = need_topology(ctx);
+    if (rc == MTPX_OK)
+        rc = need_linear(ctx, "mtpx_accumulate_gradient");
     if (rc != MTPX_OK)
         return rc;
     (void)hipSetDevice(ctx->device);
@@ -422,6 +424,8 @@ int mtpx_penalty(const mtpx_context *ctx, double weight, double reg_l2, double r
         return MTPX_E_INVALID;
     if (!ctx->has_model)
         return MTPX_E_NO_MODEL;
+    if (!ctx->model.linear())
+        return MTPX_E_MODEL;  // the trainer's penalty of the linear MTP
     penalty(ctx->model, weight, reg_l2, reg_l1, *loss, grad);
     return MTPX_OK;
 }
@@ -432,6 +436,8 @@ int mtpx_loss_grad(mtpx_context *ctx, int deterministic, double penalty_weight, 
     if (!ctx || !loss || !grad)
         return set_error(ctx, MTPX_E_INVALID, "null argument");
     int rc = need_topology(ctx);
+    if (rc == MTPX_OK)
+        rc = need_linear(ctx, "mtpx_loss_grad");
     if (rc != MTPX_OK)
         return rc;
     if (!ctx->has_labels)

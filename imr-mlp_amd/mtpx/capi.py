@@ -55,6 +55,8 @@ def lib():
         L.mtpx_load_model_text.argtypes = [C.c_void_p, C.c_char_p]
         L.mtpx_parse_model_text.argtypes = [C.c_char_p, _ip, _dp, C.c_char_p, C.c_int]
         L.mtpx_model_info.argtypes = [C.c_void_p, _ip]
+        L.mtpx_model_head.argtypes = [C.c_void_p, _ip]
+        L.mtpx_parse_model_head.argtypes = [C.c_char_p, _ip, C.c_char_p, C.c_int]
         L.mtpx_get_coeffs.argtypes = [C.c_void_p, _dp]
         L.mtpx_set_coeffs.argtypes = [C.c_void_p, _dp]
         L.mtpx_wrap.argtypes = [_dp, _ip, C.c_int, _dp]
@@ -259,6 +261,25 @@ def parse_model_text(text: str):
     return dict(zip(keys, [int(v) for v in info])), coef
 
 
+HEADS = ("linear", "mtp_m_li", "mtp_m_q2", "mtp_m_fs", "mtp_m_n1", "mtp_m_n2")
+ACTIVATIONS = ("TANH", "RELU", "SIGMOID", "LINEAR")
+
+
+def _head_dict(v):
+    return dict(head=HEADS[v[0]], q=int(v[1]), hidden1=int(v[2]), hidden2=int(v[3]),
+                activation=ACTIVATIONS[v[4]], model_coeffs_count=int(v[5]))
+
+
+def parse_model_head(text: str) -> dict:
+    """Host-only: the site-energy head .mtp text declares (mtpx_parse_model_head)."""
+    v = np.zeros(6, np.int32)
+    err = C.create_string_buffer(512)
+    rc = lib().mtpx_parse_model_head(text.encode(), _i(v), err, 512)
+    if rc != OK:
+        raise MtpxError(rc, err.value.decode())
+    return _head_dict(v)
+
+
 class Context:
     """One mtpx_context on one device."""
 
@@ -288,6 +309,12 @@ class Context:
         self._check(lib().mtpx_model_info(self.h, _i(info)), "model_info")
         self.info = dict(zip(["Z", "M", "R", "K", "B", "T", "S", "ncoef"], [int(v) for v in info]))
         return self.info
+
+    def model_head(self) -> dict:
+        """The loaded potential's head (mtpx_model_head)."""
+        v = np.zeros(6, np.int32)
+        self._check(lib().mtpx_model_head(self.h, _i(v)), "model_head")
+        return _head_dict(v)
 
     def save_model_text(self) -> str:
         n = C.c_size_t()

@@ -246,6 +246,57 @@ def random_model(template: str, Z: int, R: int, rmin: float, rmax: float, lo: fl
     return write_mtp(topo, Z, R, rmin, rmax, scaling, uniform(rng, n, lo, hi), **kw)
 
 
+MTPM_HEADS = ("mtp_m_li", "mtp_m_q2", "mtp_m_fs", "mtp_m_n1", "mtp_m_n2")
+ACTIVATIONS = ("TANH", "RELU", "SIGMOID", "LINEAR")
+
+
+def mtpm_coeff_count(head: str, q: int, h1: int = 0, h2: int = 0) -> int:
+    """Head coefficient count (runtime/mtp/mlip.cpp:244-296)."""
+    return {"mtp_m_li": 0, "mtp_m_q2": 5, "mtp_m_fs": 1, "mtp_m_n1": h1 * (q + 2),
+            "mtp_m_n2": q * h1 + h1 + h1 * h2 + 2 * h2}[head]
+
+
+def mtpm_model(linear_text: str, head: str, rng, q: int | None = None, h1: int = 0, h2: int = 0,
+               activation: str = "TANH", form: str = "both", lo: float = -0.1,
+               hi: float = 0.1, head_lo: float = -0.5, head_hi: float = 0.5) -> str:
+    """An MTP-M potential (PotMTP_M::Save, potentials/potential_mtp_m.h:
+    2256-2336) with the radial part and moment structure of a linear one:
+    Z (q + 1) species coefficients, q S moment coefficients and the head's
+    model_coeffs, all uniform random.  form says where the head is declared:
+    "tag" (a structured potential_tag), "footer" (the "# mtp_*" lines) or
+    "both", as Save writes it."""
+    if q is None:
+        q = {"mtp_m_li": 1, "mtp_m_q2": 2, "mtp_m_fs": 2}.get(head, 3)
+    lines = linear_text.rstrip("\n").split("\n")
+    Z = int(next(l for l in lines if l.startswith("species_count")).split("=")[1])
+    S = int(next(l for l in lines if l.startswith("alpha_scalar_moments")).split("=")[1])
+    body = [l for l in lines if not l.startswith(("species_coeffs", "moment_coeffs",
+                                                  "potential_tag"))]
+    mc = mtpm_coeff_count(head, q, h1, h2)
+    if form in ("tag", "both"):
+        nn = ""
+        if head in ("mtp_m_n1", "mtp_m_n2"):
+            layers = "[%d]" % h1 if head == "mtp_m_n1" else "[%d,%d]" % (h1, h2)
+            nn = ',"nn":{"activation":"%s","hidden_layers":%s}' % (activation, layers)
+        tag = ('{"model":"%s","model_coeffs_count":%d%s,"q":%d,'
+               '"schema":"gpml.mtp.metadata","type":"MTP_M","version":1}' % (head, mc, nn, q))
+        k = next(i for i, l in enumerate(body) if l.startswith("species_count"))
+        body.insert(k + 1, "potential_tag = " + tag)
+    body.append("species_coeffs = {" + ", ".join(fmt(c) for c in
+                                                 uniform(rng, Z * (q + 1), lo, hi)) + "}")
+    body.append("moment_coeffs = {" + ", ".join(fmt(c) for c in uniform(rng, q * S, lo, hi))
+                + "}")
+    body.append("model_coeffs = {" + ", ".join(fmt(c) for c in
+                                               uniform(rng, mc, head_lo, head_hi)) + "}")
+    if form in ("footer", "both"):
+        body += ["# mtp_model = " + head, "# mtp_descriptor_count = %d" % q,
+                 "# mtp_model_coeffs_count = %d" % mc]
+        if head in ("mtp_m_n1", "mtp_m_n2"):
+            body += ["# mtp_activation = " + activation, "# mtp_hidden1 = %d" % h1,
+                     "# mtp_hidden2 = %d" % (h2 if head == "mtp_m_n2" else 0)]
+    return "\n".join(body) + "\n"
+
+
 # ------------------------------------------------------------ workloads --
 
 def workload_inference(wid: int):

@@ -76,8 +76,14 @@ int mtpx_load_model(mtpx_context *ctx, const mtpx_model_view *view);
  * and RBChebyshevConfigurable with any of its cutoffs and shifts
  * (basis/basis.h:19-29, basis/cutoff.h, basis/xtrans.h); scaling defaults
  * to 0.01; the
- * potential_tag is read as the reference's metadata (a structured tag must
- * declare a linear MTP). */
+ * potential_tag is read as the reference's metadata (a structured tag
+ * declares a linear MTP or a short-range MTP-M potential).  An MTP-M
+ * potential (PotMTP_M::Load, potentials/potential_mtp_m.h:1950-2240, with
+ * the head metadata of read_mtp_gpu_metadata, runtime/mtp/mlip.cpp:70-296:
+ * a structured tag and / or "# mtp_*" lines) carries a site-energy head --
+ * mtp_m_li, mtp_m_q2, mtp_m_fs, mtp_m_n1 or mtp_m_n2 -- over q descriptors;
+ * its E/F/S, energies, sites and batch losses run on the device, its
+ * training and linear-fit entry points return MTPX_E_MODEL. */
 int mtpx_load_model_text(mtpx_context *ctx, const char *text);
 /* Host-only parse of .mtp text (no device needed): sizes Z M R K B T S ncoef
  * into out8, the flat coefficients into coeffs (may be NULL), the first
@@ -93,13 +99,25 @@ int mtpx_save_model_text(const mtpx_context *ctx, char *buf, size_t cap, size_t 
  * buf / cap / len as mtpx_save_model_text, the parse error into err. */
 int mtpx_format_model_text(const char *text, char *buf, size_t cap, size_t *len, char *err,
                            int errlen);
-/* Sizes: Z M R K B T S ncoef (ncoef = Z*Z*M*R + Z + S). */
+/* Sizes: Z M R K B T S ncoef (ncoef = Z*Z*M*R + Z + S for the linear MTP,
+ * Z*Z*M*R + Z*(q+1) + q*S + model_coeffs_count with an MTP-M head). */
 int mtpx_model_info(const mtpx_context *ctx, int out8[8]);
+/* The site-energy head of the loaded potential (PotMTP_M::model_metadata,
+ * potentials/potential_mtp_m.h:1564-1589; mlip::site_model_type,
+ * runtime/mtp/mlip.h:54): out6 = {head, q, hidden1, hidden2, activation,
+ * model_coeffs_count} with head 0 for the linear MTP (q 1), 1 mtp_m_li,
+ * 2 mtp_m_q2, 3 mtp_m_fs, 4 mtp_m_n1, 5 mtp_m_n2 and activation 0 TANH,
+ * 1 RELU, 2 SIGMOID, 3 LINEAR.  With a head the coefficients are ordered
+ * [radial | species Z | descriptor species q*Z | moment q*S | head]. */
+int mtpx_model_head(const mtpx_context *ctx, int out6[6]);
+/* Host-only: the head of .mtp text, as mtpx_model_head (no device needed). */
+int mtpx_parse_model_head(const char *text, int out6[6], char *err, int errlen);
 /* PotMTP::cutoff (potentials/potential_mtp.cpp:300-310): the largest
  * max_dist of the radial bases, the list cutoff of the model. */
 int mtpx_model_cutoff(const mtpx_context *ctx, double *cutoff);
 /* PotMTP::get_coeffs / set_coeffs (potential_mtp.cpp:4160-4245) in the flat
- * order [radial | species | moment]; MTPGpuDirect::update_coefficients
+ * order [radial | species | moment] (with a head, mtpx_model_head's order);
+ * MTPGpuDirect::update_coefficients
  * (mtp_gpu_direct.h:813-818). */
 int mtpx_get_coeffs(const mtpx_context *ctx, double *coeffs);
 int mtpx_set_coeffs(mtpx_context *ctx, const double *coeffs);

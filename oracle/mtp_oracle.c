@@ -314,6 +314,210 @@ static const char *load_basis_tail(rd_t *r, orc_basis *b)
     return 0;
 }
 
+/* ---- MTP-M metadata (runtime/mtp/mlip.cpp:70-296 read_mtp_gpu_metadata,
+ * tools/mtp_metadata.h:374-398 legacy_model_fields) ------------------------
+ * The fields come from a structured potential_tag (model, q,
+ * model_coeffs_count, nn.activation, nn.hidden_layers) and from
+ * "mtp_<key> = value" lines (a leading '#' allowed) before any "#MVS_v1.1"
+ * payload; a key given twice with different values is an error. */
+typedef struct {
+    char model[32], activation[32];
+    long q, mcc, h1, h2;  /* -1: absent */
+} mtpm_fields;
+
+/* A JSON string or integer member of the tag text (the tag is this
+ * library's own canonical JSON: "key":value with no spaces). */
+static int json_str(const char *js, const char *key, char *out, int n)
+{
+    char pat[64];
+    snprintf(pat, sizeof pat, "\"%s\":\"", key);
+    const char *p = strstr(js, pat);
+    if (!p)
+        return 0;
+    p += strlen(pat);
+    int k = 0;
+    while (*p && *p != '"' && k < n - 1)
+        out[k++] = *p++;
+    out[k] = 0;
+    return 1;
+}
+static long json_int(const char *js, const char *key)
+{
+    char pat[64];
+    snprintf(pat, sizeof pat, "\"%s\":", key);
+    const char *p = strstr(js, pat);
+    if (!p)
+        return -1;
+    return strtol(p + strlen(pat), NULL, 10);
+}
+static const char *set_field_l(long *f, long v)
+{
+    if (*f >= 0 && *f != v)
+        return "conflicting MTP-M metadata";
+    *f = v;
+    return 0;
+}
+static const char *set_field_s(char *f, int n, const char *v)
+{
+    if (f[0] && strcmp(f, v) != 0)
+        return "conflicting MTP-M metadata";
+    snprintf(f, (size_t)n, "%s", v);
+    return 0;
+}
+static const char *mtpm_read_fields(const char *text, const char *tag, mtpm_fields *F)
+{
+    memset(F, 0, sizeof *F);
+    F->q = F->mcc = F->h1 = F->h2 = -1;
+    const char *e;
+    if (tag[0] == '{') {
+        char v[32];
+        if (json_str(tag, "model", v, sizeof v) && (e = set_field_s(F->model, 32, v)))
+            return e;
+        if ((e = set_field_l(&F->q, json_int(tag, "q"))))
+            return e;
+        F->mcc = json_int(tag, "model_coeffs_count");
+        const char *nn = strstr(tag, "\"nn\":");
+        if (nn) {
+            if (json_str(nn, "activation", v, sizeof v))
+                snprintf(F->activation, sizeof F->activation, "%s", v);
+            const char *hl = strstr(nn, "\"hidden_layers\":[");
+            if (hl) {
+                char *end = NULL;
+                F->h1 = strtol(hl + 17, &end, 10);
+                F->h2 = (end && *end == ',') ? strtol(end + 1, NULL, 10) : 0;
+            }
+        }
+    }
+    if (strcmp(F->model, "mtp_m_nn2") == 0)
+        snprintf(F->model, sizeof F->model, "mtp_m_n2");
+    for (const char *line = text; line && *line;) {
+        const char *eol = strchr(line, '\n');
+        size_t len = eol ? (size_t)(eol - line) : strlen(line);
+        char buf[256];
+        if (len >= sizeof buf)
+            len = sizeof buf - 1;
+        memcpy(buf, line, len);
+        buf[len] = 0;
+        line = eol ? eol + 1 : NULL;
+        char *s = buf;
+        while (*s == ' ' || *s == '\t')
+            ++s;
+        if (strncmp(s, "#MVS_v1.1", 9) == 0)
+            break;
+        if (*s == '#')
+            ++s;
+        while (*s == ' ' || *s == '\t')
+            ++s;
+        if (strncmp(s, "mtp_", 4) != 0 || !strchr(s, '='))
+            continue;
+        char *eq = strchr(s, '=');
+        char *ke = eq;
+        while (ke > s && (ke[-1] == ' ' || ke[-1] == '\t'))
+            --ke;
+        *ke = 0;
+        char *v = eq + 1;
+        while (*v == ' ' || *v == '\t')
+            ++v;
+        char *ve = v + strlen(v);
+        while (ve > v && (ve[-1] == ' ' || ve[-1] == '\t' || ve[-1] == '\r'))
+            *--ve = 0;
+        if (strcmp(s, "mtp_model") == 0) {
+            const char *name = strcmp(v, "mtp_m_nn2") == 0 ? "mtp_m_n2"
+                               : strcmp(v, "mtp") == 0     ? "linear"
+                                                           : v;
+            if ((e = set_field_s(F->model, 32, name)))
+                return e;
+        } else if (strcmp(s, "mtp_descriptor_count") == 0) {
+            if ((e = set_field_l(&F->q, strtol(v, NULL, 10))))
+                return e;
+        } else if (strcmp(s, "mtp_model_coeffs_count") == 0) {
+            if ((e = set_field_l(&F->mcc, strtol(v, NULL, 10))))
+                return e;
+        } else if (strcmp(s, "mtp_hidden1") == 0) {
+            if ((e = set_field_l(&F->h1, strtol(v, NULL, 10))))
+                return e;
+        } else if (strcmp(s, "mtp_hidden2") == 0) {
+            if ((e = set_field_l(&F->h2, strtol(v, NULL, 10))))
+                return e;
+        } else if (strcmp(s, "mtp_activation") == 0) {
+            char up[32];
+            int k = 0;
+            for (; v[k] && k < 31; ++k)
+                up[k] = (char)toupper((unsigned char)v[k]);
+            up[k] = 0;
+            if ((e = set_field_s(F->activation, 32, up)))
+                return e;
+        }
+    }
+    for (char *c = F->activation; *c; ++c)
+        *c = (char)toupper((unsigned char)*c);
+    return 0;
+}
+
+/* the head, its dimensions and coefficient count (mlip.cpp:226-296) */
+static const char *mtpm_configure(orc_model *m, const mtpm_fields *F)
+{
+    static const char *names[] = {"linear", "mtp_m_li", "mtp_m_q2", "mtp_m_fs", "mtp_m_n1",
+                                  "mtp_m_n2"};
+    m->head = 0;
+    m->P = 1;
+    m->h1 = m->h2 = m->Mc = 0;
+    m->act = 0;
+    if (!F->model[0])
+        return 0;
+    int h = -1;
+    for (int k = 0; k < 6; ++k)
+        if (strcmp(F->model, names[k]) == 0)
+            h = k;
+    if (h < 0)
+        return "unknown mtp_model";
+    const long q = F->q < 0 ? 0 : F->q, mcc = F->mcc < 0 ? 0 : F->mcc;
+    const long h1 = F->h1 < 0 ? 0 : F->h1, h2 = F->h2 < 0 ? 0 : F->h2;
+    if (h != 4 && h != 5 && (h1 != 0 || h2 != 0))
+        return "non-neural models require zero hidden dimensions";
+    if (h == 4 && h2 != 0)
+        return "NN1 requires zero hidden2";
+    if (h == 0)
+        return 0;
+    m->head = h;
+    if (h == 1) {
+        m->P = q == 0 ? 1 : (int)q;
+        if (m->P != 1 || mcc != 0)
+            return "linear MTP-M requires one descriptor and no head coefficients";
+    } else if (h == 2 || h == 3) {
+        m->P = q == 0 ? 2 : (int)q;
+        if (m->P != 2)
+            return "analytic q2/fs models require descriptor_count 2";
+        const long want = h == 2 ? 5 : 1;
+        if (mcc != 0 && mcc != want)
+            return "analytic model coefficient count does not match model type";
+        m->Mc = (int)want;
+    } else {
+        if (q <= 0 || h1 <= 0)
+            return "neural model requires positive descriptor_count and hidden1";
+        if (h == 5 && h2 <= 0)
+            return "NN2 model requires positive hidden2";
+        m->P = (int)q;
+        m->h1 = (int)h1;
+        m->h2 = (int)h2;
+        const long want = h == 4 ? h1 * (q + 2) : q * h1 + h1 + h1 * h2 + 2 * h2;
+        if (mcc != 0 && mcc != want)
+            return "neural model coefficient count does not match dimensions";
+        m->Mc = (int)want;
+        const char *a = F->activation;
+        m->act = strcmp(a, "TANH") == 0      ? 0
+                 : strcmp(a, "RELU") == 0    ? 1
+                 : strcmp(a, "SIGMOID") == 0 ? 2
+                 : strcmp(a, "LINEAR") == 0  ? 3
+                                             : -1;
+        if (m->act < 0)
+            return "unknown mtp_activation";
+        if (h == 5 && m->act == 3)
+            return "NN2 does not support LINEAR activation";
+    }
+    return 0;
+}
+
 #define LOAD_FAIL(msg)                                                                     \
     do {                                                                                   \
         set_err(err, errlen, msg);                                                         \
@@ -628,19 +832,32 @@ orc_model *orc_model_load_text(const char *text, char *err, int errlen)
     }
     rd_ignore_until(&r, 1000, '\n');
 
-    m->ncoef = m->nradial + Z + m->S;
+    {
+        mtpm_fields F;
+        const char *herr = mtpm_read_fields(text, m->tag, &F);
+        if (!herr)
+            herr = mtpm_configure(m, &F);
+        if (herr) {
+            free(radial);
+            LOAD_FAIL(herr);
+        }
+    }
+    /* PotMTP_M::Load (potential_mtp_m.h:2018-2124): Z (P + 1) species
+     * coefficients, P S moment coefficients, then the head's */
+    const int nsp = m->head ? Z * (m->P + 1) : Z, nmom = m->P * m->S;
+    m->ncoef = m->nradial + nsp + nmom + m->Mc;
     m->coef = (double *)calloc((size_t)m->ncoef, sizeof(double));
     memcpy(m->coef, radial, sizeof(double) * (size_t)m->nradial);
     free(radial);
     double *lin = m->coef + m->nradial;
-    for (int i = 0; i < Z + m->S; ++i) /* :471-474 -- default linear coefficients */
+    for (int i = 0; i < nsp + nmom + m->Mc; ++i) /* :471-474 -- default linear coefficients */
         lin[i] = 1e-3;
     tok[0] = 0;
     rd_word(&r, tok, sizeof tok);
     r.fail = 0;
     if (strcmp(tok, "species_coeffs") == 0) { /* :479-489 */
         rd_ignore(&r, 4);
-        for (int i = 0; i < Z; ++i) {
+        for (int i = 0; i < nsp; ++i) {
             lin[i] = rd_double(&r);
             rd_char(&r);
             if (r.fail)
@@ -654,12 +871,30 @@ orc_model *orc_model_load_text(const char *text, char *err, int errlen)
     if (strcmp(tok, "moment_coeffs") == 0) { /* :490-502 */
         rd_ignore(&r, 2);
         rd_ignore_until(&r, 10, '{');
-        for (int i = 0; i < m->S; ++i) {
-            lin[Z + i] = rd_double(&r);
+        for (int i = 0; i < nmom; ++i) {
+            lin[nsp + i] = rd_double(&r);
             rd_char(&r);
             if (r.fail)
                 LOAD_FAIL("Error reading .mtp file, missing moment coefficient");
         }
+        rd_ignore_until(&r, 1000, '\n');
+        tok[0] = 0;
+        rd_word(&r, tok, sizeof tok);
+        r.fail = 0;
+    }
+    if (m->head) { /* potential_mtp_m.h:2112-2124; mlip.cpp:201-207 asks for the section */
+        if (strcmp(tok, "model_coeffs") != 0)
+            LOAD_FAIL("nonlinear mtp_model requires a model_coeffs section");
+        rd_ignore(&r, 2);
+        rd_ignore_until(&r, 10, '{');
+        for (int i = 0; i < m->Mc; ++i) {
+            lin[nsp + nmom + i] = rd_double(&r);
+            rd_char(&r);
+            if (r.fail)
+                LOAD_FAIL("Error reading .mtp file, missing model coefficient");
+        }
+    } else if (!m->head && strcmp(tok, "model_coeffs") == 0) {
+        LOAD_FAIL("model_coeffs is present but mtp_model metadata is missing");
     }
 
     /* PotMTP::init_basic, potential_mtp.cpp:576-604 */
@@ -674,6 +909,17 @@ orc_model *orc_model_load_text(const char *text, char *err, int errlen)
     m->max_nu1++;
     m->max_mu++;
     return m;
+}
+
+int orc_model_head(const orc_model *m, int *o)
+{
+    o[0] = m->head;
+    o[1] = m->P;
+    o[2] = m->h1;
+    o[3] = m->h2;
+    o[4] = m->act;
+    o[5] = m->Mc;
+    return m->head;
 }
 
 int orc_model_info(const orc_model *m, int *o)
@@ -760,10 +1006,10 @@ static size_t json_escape(const char *in, char *out)
  * MTPMetadata::Tag::output(model_metadata()) serialised
  * (tools/mtp_metadata.h:353-370): this restatement covers an absent tag and
  * a plain-text (legacy) tag, kept as "legacy_tag"; it returns -1 for a tag
- * in JSON form. */
+ * in JSON form and for a potential with an MTP-M head. */
 int orc_model_save_text(const orc_model *m, char *buf, int buflen)
 {
-    if (m->tag[0] == '{')
+    if (m->tag[0] == '{' || m->head)
         return -1;
     size_t cap = 1 << 16, len = 0;
     char *out = (char *)malloc(cap);
@@ -1780,21 +2026,128 @@ static void backpropagate(const orc_model *m, const double *mv, double *A)
     }
 }
 
+/* The activations of the neural heads (mtp_cpu.cpp:21-45). */
+static double activate(double x, int act, double *der)
+{
+    if (act == 0) {
+        const double v = tanh(x);
+        *der = 1.0 - v * v;
+        return v;
+    }
+    if (act == 1) {
+        *der = x > 0.0 ? 1.0 : 0.0;
+        return x > 0.0 ? x : 0.0;
+    }
+    if (act == 2) {
+        const double v = 1.0 / (1.0 + exp(-x));
+        *der = v * (1.0 - v);
+        return v;
+    }
+    *der = 1.0;
+    return x;
+}
+
+/* The MTP-M head (Executor::head, mtp_cpu.cpp:291-368; m_model_mtpq2,
+ * m_model_mtpfs, m_model_nn1, m_model_nn2 of potential_mtp_m.h): the
+ * energy of the descriptors Q [P] and, into dq, its gradient. */
+static double mtpm_head(const orc_model *m, const double *Q, double *dq)
+{
+    const double *c = m->coef + m->nradial + m->Z * (m->P + 1) + m->P * m->S;
+    const int q = m->P, h1 = m->h1, h2 = m->h2;
+    if (m->head == 1) {
+        dq[0] = 1.0;
+        return Q[0];
+    }
+    if (m->head == 2) {
+        const double x = Q[0], y = Q[1];
+        dq[0] = c[0] + 2.0 * c[2] * x + c[4] * y;
+        dq[1] = c[1] + 2.0 * c[3] * y + c[4] * x;
+        return c[0] * x + c[1] * y + c[2] * x * x + c[3] * y * y + c[4] * x * y;
+    }
+    if (m->head == 3) {
+        dq[0] = 1.0;
+        dq[1] = c[0] / sqrt(1.0 + Q[1] * Q[1]);
+        return Q[0] + c[0] * asinh(Q[1]);
+    }
+    const int nn2 = m->head == 5;
+    const double *b1 = c + q * h1 + (nn2 ? 0 : h1);
+    const double *w2 = nn2 ? b1 + h1 : NULL;
+    const double *b2 = nn2 ? w2 + h1 * h2 : NULL;
+    const double *out = nn2 ? b2 + h2 : c + q * h1;
+    double *a1 = (double *)calloc((size_t)(2 * h1 + h2 + 1), sizeof(double));
+    double *d1 = a1 + h1, *g2 = d1 + h1;
+    double e = 0.0;
+    for (int p = 0; p < q; ++p)
+        dq[p] = 0.0;
+    for (int h = 0; h < h1; ++h) {
+        double v = b1[h];
+        for (int p = 0; p < q; ++p)
+            v += c[h * q + p] * Q[p];
+        a1[h] = activate(v, m->act, &d1[h]);
+        if (!nn2)
+            e += out[h] * a1[h];
+    }
+    if (nn2)
+        for (int h = 0; h < h2; ++h) {
+            double v = b2[h], d = 0.0;
+            for (int k = 0; k < h1; ++k)
+                v += w2[h * h1 + k] * a1[k];
+            e += out[h] * activate(v, m->act, &d);
+            g2[h] = out[h] * d;
+        }
+    for (int h = 0; h < h1; ++h) {
+        double resp = nn2 ? 0.0 : out[h];
+        if (nn2)
+            for (int k = 0; k < h2; ++k)
+                resp += w2[k * h1 + h] * g2[k];
+        resp *= d1[h];
+        for (int p = 0; p < q; ++p)
+            dq[p] += c[h * q + p] * resp;
+    }
+    free(a1);
+    return e;
+}
+
+/* The site energy and the adjoint seeds dE/dm of the scalar moments: the
+ * linear MTP (potential_mtp.cpp:2959-2970) or the MTP-M head over the
+ * descriptors Q_p (potential_mtp_m.h:3403-3456). */
+static double site_energy_seeds(const orc_model *m, int t, const double *mv, double *A)
+{
+    const double *species = m->coef + m->nradial;
+    double e = species[t];
+    if (!m->head) {
+        const double *moment = species + m->Z;
+        for (int s = 0; s < m->S; ++s)
+            e += moment[s] * mv[m->map[s]];
+        if (A)
+            for (int s = 0; s < m->S; ++s)
+                A[m->map[s]] += moment[s];
+        return e;
+    }
+    const double *dsp = species + m->Z, *C = species + m->Z * (m->P + 1);
+    double *Q = (double *)calloc((size_t)(2 * m->P), sizeof(double)), *dq = Q + m->P;
+    for (int p = 0; p < m->P; ++p) {
+        Q[p] = dsp[p * m->Z + t];
+        for (int s = 0; s < m->S; ++s)
+            Q[p] += mv[m->map[s]] * C[p * m->S + s];
+    }
+    const double hv = mtpm_head(m, Q, dq);
+    if (A)
+        for (int s = 0; s < m->S; ++s)
+            for (int p = 0; p < m->P; ++p)
+                A[m->map[s]] += C[p * m->S + s] * dq[p];
+    free(Q);
+    return hv + e;
+}
+
 /* CalcSiteEFS (potential_mtp.cpp:2959-2984) with contract_site_forces
  * (:2938-2957). */
 static double site_efs(const orc_model *m, const orc_nbh *h, int i, ws_t *w)
 {
     const int n = h->offsets[i + 1] - h->offsets[i];
-    const double *species = m->coef + m->nradial;
-    const double *moment = species + m->Z;
     site_descriptors(m, h, i, w, 1);
-    double site_energy = 0;
-    site_energy += species[h->center_types[i]];
-    for (int s = 0; s < m->S; ++s)
-        site_energy += moment[s] * w->mv[m->map[s]];
     memset(w->A, 0, sizeof(double) * (size_t)m->K);
-    for (int s = 0; s < m->S; ++s)
-        w->A[m->map[s]] += moment[s];
+    const double site_energy = site_energy_seeds(m, h->center_types[i], w->mv, w->A);
     backpropagate(m, w->mv, w->A);
     memset(w->ders, 0, sizeof(double) * (size_t)n * 3);
     for (int b = 0; b < m->B; ++b) {
@@ -1928,14 +2281,10 @@ void orc_energy(const orc_model *m, const orc_nbh *h, double *energy, double *si
 {
     ws_t w;
     ws_init(&w, m, max_list(h), 0, 0);
-    const double *species = m->coef + m->nradial;
-    const double *moment = species + m->Z;
     *energy = 0;
     for (int i = 0; i < h->n; ++i) {
         site_descriptors(m, h, i, &w, 0);
-        double se = species[h->center_types[i]];
-        for (int s = 0; s < m->S; ++s)
-            se += moment[s] * w.mv[m->map[s]];
+        const double se = site_energy_seeds(m, h->center_types[i], w.mv, NULL);
         *energy += se;
         if (site_energies)
             site_energies[i] = se;

@@ -49,8 +49,16 @@ typedef struct orc_model {
     int *nu;                      /* [B] a+b+c (nu_arr_list) */
     int max_nu1;                  /* max_alpha_index_basic = max nu + 1 */
     int max_mu;                   /* max mu + 1 */
-    int nradial, ncoef;           /* Z*Z*M*R, nradial + Z + S */
+    int nradial, ncoef;           /* Z*Z*M*R, nradial + Z + S (linear MTP) */
     double *coef;                 /* [radial | species | moments] */
+    /* MTP-M site-energy head (potentials/potential_mtp_m.h:3383-3456; the
+     * heads of runtime/mtp/cpu/mtp_cpu.cpp:291-368): 0 linear MTP, 1
+     * mtp_m_li, 2 mtp_m_q2, 3 mtp_m_fs, 4 mtp_m_n1, 5 mtp_m_n2.  With a head
+     * the coefficients are [radial | species Z | descriptor species P*Z |
+     * moments P*S | head Mc] and E_i = species[t] + head(Q),
+     * Q_p = dspecies[p*Z + t] + sum_s moments[p*S + s] m_map(s). */
+    int head, P, h1, h2, act;     /* act: 0 tanh, 1 relu, 2 sigmoid, 3 linear */
+    int Mc;
 } orc_model;
 
 /* Directed neighbour lists in CSR form (base/anyneighborhoods.h:26-67). */
@@ -91,6 +99,7 @@ typedef struct orc_config {
 orc_model *orc_model_load_text(const char *text, char *err, int errlen);
 void orc_model_free(orc_model *m);
 int orc_model_info(const orc_model *m, int *out11);   /* Z M R K B T S max_nu1 max_mu nradial ncoef */
+int orc_model_head(const orc_model *m, int *out6);    /* head P h1 h2 act Mc; returns head */
 void orc_model_get_coeffs(const orc_model *m, double *x);
 void orc_model_set_coeffs(orc_model *m, const double *x);
 void orc_model_tables(const orc_model *m, int *basic, int *times, int *map, double *rb3);

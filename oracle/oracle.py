@@ -50,6 +50,7 @@ def lib():
         L.orc_model_load_text.argtypes = [C.c_char_p, C.c_char_p, C.c_int]
         L.orc_model_free.argtypes = [C.c_void_p]
         L.orc_model_info.argtypes = [C.c_void_p, _ip]
+        L.orc_model_head.argtypes = [C.c_void_p, _ip]
         L.orc_model_get_coeffs.argtypes = [C.c_void_p, _dp]
         L.orc_model_set_coeffs.argtypes = [C.c_void_p, _dp]
         L.orc_model_tables.argtypes = [C.c_void_p, _ip, _ip, _ip, _dp]
@@ -179,6 +180,17 @@ class Model:
         lib().orc_model_info(self.h, _i(info))
         (self.Z, self.M, self.R, self.K, self.B, self.T, self.S, self.max_nu1, self.max_mu,
          self.nradial, self.ncoef) = [int(v) for v in info]
+        hd = np.zeros(6, np.int32)
+        lib().orc_model_head(self.h, _i(hd))
+        # MTP-M head (runtime/mtp/mlip.cpp:70-296): 0 none, 1 li, 2 q2, 3 fs,
+        # 4 nn1, 5 nn2; descriptors P, hidden sizes, activation (0 tanh,
+        # 1 relu, 2 sigmoid, 3 linear), head coefficient count
+        self.head, self.P, self.h1, self.h2, self.act, self.Mc = [int(v) for v in hd]
+
+    def linear_only(self, what):
+        """The training and linear-fit restatements cover the linear MTP only."""
+        if self.head:
+            raise ValueError("%s: the oracle restates the linear MTP only" % what)
 
     @classmethod
     def from_file(cls, path):
@@ -343,6 +355,7 @@ def site_moments(model: Model, nb: Neighbors, i: int):
 
 
 def accumulate_fp_grad(model, nb, i, se_weight, f_weight=None, grad=None):
+    model.linear_only("accumulate_fp_grad")
     g = np.zeros(model.ncoef) if grad is None else grad
     fw = None if f_weight is None else _f64(f_weight, (-1,))
     lib().orc_accumulate_fp_grad(model.h, nb.h, i, float(se_weight),
@@ -351,6 +364,7 @@ def accumulate_fp_grad(model, nb, i, se_weight, f_weight=None, grad=None):
 
 
 def accumulate_efs_combination_grad(model, nb, dLdE, dLdF, dLdS, grad=None):
+    model.linear_only("accumulate_efs_combination_grad")
     g = np.zeros(model.ncoef) if grad is None else grad
     dLdF = _f64(dLdF, (-1,))
     dLdS = _f64(dLdS, (-1,))
@@ -362,6 +376,7 @@ def accumulate_efs_combination_grad(model, nb, dLdE, dLdF, dLdS, grad=None):
 def add_loss_grad(model, nb, settings: LossSettings, labels: Labels, grad=None):
     """Trainer_MTP::AddLossGard for one configuration.  Returns (loss, grad,
     metrics[loss_e, loss_f, loss_s, sq_e_at, sq_f, sq_s])."""
+    model.linear_only("add_loss_grad")
     g = np.zeros(model.ncoef) if grad is None else grad
     loss = C.c_double(0.0)
     met = np.zeros(6)
@@ -382,6 +397,7 @@ def penalty_grad(model, weight=1e-6, reg_l2=1e-10, reg_l1=0.0):
 def loss_grad_batch(model, nbs, labels, settings, penalty_weight=1e-6, reg_l2=1e-10,
                     reg_l1=0.0, threads=0):
     """Trainer_MTP::AccumulateGard: f, g over a batch of configurations."""
+    model.linear_only("loss_grad_batch")
     arr = (C.c_void_p * len(nbs))(*[nb.h for nb in nbs])
     cfgs = (_Config * len(labels))(*[lb.cstruct() for lb in labels])
     f = C.c_double()
@@ -395,6 +411,7 @@ def loss_grad_batch(model, nbs, labels, settings, penalty_weight=1e-6, reg_l2=1e
 def efs_components(model, nb):
     """CalcEFSCmpt_R (potential_mtp.cpp:2675-2707): energy[p], force[n,3,p],
     stress[3,3,p] with p = species + scalar moments."""
+    model.linear_only("efs_components")
     p = model.Z + model.S
     ec = np.zeros(p)
     fc = np.zeros((max(nb.n, 1), 3, p))
@@ -406,6 +423,7 @@ def efs_components(model, nb):
 def linear_rows(model, nb, settings, labels: Labels, fix_species=False):
     """AddLinearFast rows (train/train_mtp.cpp:1289-1395): F, S, E, scaled by
     sqrt(w); fix_species drops the species columns (fix_species_coeffs)."""
+    model.linear_only("linear_rows")
     cfg = labels.cstruct()
     rows = int(lib().orc_linear_row_count(C.byref(settings), C.byref(cfg)))
     p = model.S if fix_species else model.Z + model.S
@@ -428,6 +446,7 @@ def gram(A, y):
 
 
 def linear_system_batch(model, nbs, labels, settings, threads=0, fix_species=False):
+    model.linear_only("linear_system_batch")
     arr = (C.c_void_p * len(nbs))(*[nb.h for nb in nbs])
     cfgs = (_Config * len(labels))(*[lb.cstruct() for lb in labels])
     p = model.S if fix_species else model.Z + model.S
@@ -476,9 +495,11 @@ def ref_neighbors(cell, pbc, pos, types, cutoff, workdir):
     return dict(offsets=offsets, idx=idx, types=typ, vec=vec, dist=dist, center_types=ct)
 
 
-def ref_mlip_efs(model_text, nb: Neighbors, point_types, cutoff, workdir, Z):
-    """Run oracle/_ref/mlip_ref (runtime/mtp/mlip.cpp) over the oracle's periodic
-    images as ghost atoms.  Returns E, site E[n], F[n,3], virial6."""
+def ref_mlip_efs(model_text, nb: Neighbors, point_types, cutoff, workdir, Z, binary="mlip_ref"):
+    """Run oracle/_ref/mlip_ref (runtime/mtp/mlip.cpp) -- or, with binary
+    "mtpm_ref", the MTP-M site executor (runtime/mtp/cpu/mtp_cpu.cpp) -- over
+    the oracle's periodic images as ghost atoms.  Returns E, site E[n],
+    F[n,3], virial6."""
     pts, orig = nb.points()
     mpath = os.path.join(workdir, "model.mtp")
     with open(mpath, "w") as f:
@@ -493,7 +514,7 @@ def ref_mlip_efs(model_text, nb: Neighbors, point_types, cutoff, workdir, Z):
         f.write(_f64(pts).tobytes())
         f.write(_i32(np.asarray(point_types)[orig]).tobytes())
         f.write(_i32(orig).tobytes())
-    subprocess.run([os.path.join(REF_DIR, "mlip_ref"), mpath, fin, fout], check=True)
+    subprocess.run([os.path.join(REF_DIR, binary), mpath, fin, fout], check=True)
     raw = np.frombuffer(open(fout, "rb").read(), np.float64)
     n = nb.n
     return raw[0], raw[1:1 + n], raw[1 + n:1 + 4 * n].reshape(n, 3), raw[1 + 4 * n:7 + 4 * n]
