@@ -32,8 +32,7 @@ int upload_coeffs(mtpx_context *ctx)
     HIP_TRY(upload(ctx->species, species, ctx->stream), "upload species coefficients");
     HIP_TRY(upload(ctx->moment, moment, ctx->stream), "upload moment coefficients");
     HIP_TRY(upload(ctx->seed, seed, ctx->stream), "upload adjoint seeds");
-    ctx->dm.hids = nullptr;
-    ctx->dm.hproj = ctx->dm.hdsp = ctx->dm.hc = nullptr;
+    ctx->dm.hd = nullptr;
     if (!m.linear()) {
         const int P = m.head.P;
         std::vector<int> compact((size_t)m.K, -1), ids;
@@ -60,11 +59,24 @@ int upload_coeffs(mtpx_context *ctx)
         HIP_TRY(upload(ctx->head_proj, proj, ctx->stream), "upload head tables");
         HIP_TRY(upload(ctx->head_dsp, dsp, ctx->stream), "upload head tables");
         HIP_TRY(upload(ctx->head_coef, hc, ctx->stream), "upload head tables");
-        ctx->dm.hNS = (int)NS;
-        ctx->dm.hids = ctx->head_ids.as<int>();
-        ctx->dm.hproj = ctx->head_proj.as<double>();
-        ctx->dm.hdsp = ctx->head_dsp.as<double>();
-        ctx->dm.hc = ctx->head_coef.as<double>();
+        DevHead h{};
+        h.kind = m.head.kind;
+        h.P = P;
+        h.NS = (int)NS;
+        h.h1 = m.head.h1;
+        h.h2 = m.head.h2;
+        h.act = m.head.act;
+        h.Z = m.Z;
+        h.K = m.K;
+        h.ids = ctx->head_ids.as<int>();
+        h.proj = ctx->head_proj.as<double>();
+        h.dsp = ctx->head_dsp.as<double>();
+        h.c = ctx->head_coef.as<double>();
+        HIP_TRY(ctx->head_params.ensure(sizeof h), "upload head tables");
+        HIP_TRY(hipMemcpyAsync(ctx->head_params.p, &h, sizeof h, hipMemcpyHostToDevice,
+                               ctx->stream),
+                "upload head tables");
+        ctx->dm.hd = static_cast<const DevHead *>(ctx->head_params.p);
     }
     HIP_TRY(hipStreamSynchronize(ctx->stream), "upload coefficients");
     ctx->dm.radial = ctx->radial.as<double>();
@@ -110,11 +122,7 @@ void fill_model_sizes(const Model &M, const Plan &P, DevModel &dm)
     dm.efs_acc = P.efs_acc;
     dm.efs_head = P.efs_head;
     dm.head = M.head.kind;
-    dm.hP = M.head.P;
-    dm.h1 = M.head.h1;
-    dm.h2 = M.head.h2;
-    dm.hact = M.head.act;
-    dm.hNS = 0;
+    dm.hd = nullptr;
     dm.tr_red1 = P.tr_red1;
     dm.tr_red4 = P.tr_red4;
     dm.tr_stage = P.tr_stage;

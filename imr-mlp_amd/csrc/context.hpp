@@ -23,8 +23,8 @@ struct mtpx_context {
     // model buffers
     DBuf radial, species, moment, map, seed, slot_basic, slot_abc, dup, fwd_level, fwd_steps,
         fwd_lcomb, fwd_comb, bwd_level, bwd_steps, bwd_lcomb, bwd_comb, rb_table;
-    // MTP-M head tables (DevModel::hids, hproj, hdsp, hc)
-    DBuf head_ids, head_proj, head_dsp, head_coef;
+    // MTP-M head tables and the DevHead that points at them
+    DBuf head_ids, head_proj, head_dsp, head_coef, head_params;
 
     // neighbour lists
     bool has_nbh = false;
@@ -116,7 +116,7 @@ struct mtpx_context {
         for (DBuf *b : {&radial, &species, &moment, &map, &seed, &slot_basic, &slot_abc, &dup,
                         &fwd_level, &fwd_steps, &fwd_lcomb, &fwd_comb, &bwd_level, &bwd_steps,
                         &bwd_lcomb, &bwd_comb, &rb_table, &head_ids, &head_proj, &head_dsp,
-                        &head_coef, &offsets, &idx, &type, &x, &y, &z, &d,
+                        &head_coef, &head_params, &offsets, &idx, &type, &x, &y, &z, &d,
                         &center_type, &rev_offsets, &rev_pairs, &forces, &site_energy, &partial,
                         &pair_ders, &out10, &soff, &center_structure, &site_virial, &benergy,
                         &bstress, &active, &tE, &wE, &tF, &wF, &tS, &wS, &dLdE, &dLdF, &dLdS,

@@ -104,7 +104,8 @@ __global__ __launch_bounds__(kWave *kMaxWaves) void efs_kernel(DevModel m, DevNe
         double e = 0.0;
         const bool energy_only = flags & kEfsEnergyOnly;
         if (m.head) {
-            e = head_energy(m, ti, mom, ws + m.efs_head, lane, !energy_only);
+            const int w0 = (int)(ws - lds);
+            e = head_site(m.hd, ti, w0, w0 + m.efs_head, w0 + m.K4, lane, !energy_only);
         } else {
             for (int s = lane; s < m.S; s += kWave)
                 e += L.moment[s] * mom[L.map[s]];
@@ -117,9 +118,7 @@ __global__ __launch_bounds__(kWave *kMaxWaves) void efs_kernel(DevModel m, DevNe
         }
         if (energy_only)  // getE (potential_mtp.cpp:2604-2621): no gradient
             continue;
-        if (m.head)
-            head_seeds(m, ws + m.efs_head, A, lane);
-        else
+        if (!m.head)  // (a head has written its seeds)
             for (int k = lane; k < m.K; k += kWave)
                 A[k] = L.seed[k];
         wave_sync();

@@ -959,11 +959,20 @@ bool build_plan(const Model &m, Plan &p, std::string &err)
     p.efs_acc = (end + 3) & ~3;
     p.priv_doubles = p.efs_acc + 12;  // energy, virial[9], padding
     if (!m.linear()) {
+        // The head's work space lives from the end of the forward rules to
+        // the seeds.  Over that span the moment transpose buffer past the
+        // partial sums (and the slot-ordered adjoints, written only after
+        // the seeds) are dead: the head goes there where it fits, so the
+        // launch keeps its waves and its LDS step tables.
         const long long hd = 2LL * m.head.P + 2LL * m.head.h1 + m.head.h2;
         if (hd > 0xffff)
             return fail(err, "MTP-M head too large: its work space exceeds 65535 doubles");
-        p.efs_head = p.priv_doubles;
-        p.priv_doubles += (int)((hd + 3) & ~3LL);
+        if (hd <= p.efs_acc - p.red0) {
+            p.efs_head = p.red0;
+        } else {
+            p.efs_head = p.priv_doubles;
+            p.priv_doubles += (int)((hd + 3) & ~3LL);
+        }
     }
     if (p.priv_doubles > 0xffff)
         return fail(err, "model too large: per-atom work space exceeds 65535 doubles");

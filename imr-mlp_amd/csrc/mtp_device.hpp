@@ -776,43 +776,113 @@ __device__ __forceinline__ double head_activate(double x, int act, double &der)
     return x;
 }
 
-// The site energy of an MTP-M potential less its species term, for the
-// centre species t, from the moments in LDS (mom), in every lane
-// (Executor::evaluate_site and Executor::head, mtp_cpu.cpp:291-368,
-// :418-427): the descriptors Q_p = dspecies[p Z + t] + sum_a proj[p][a]
-// m(ids[a]) are wave sums over the distinct scalar moments, the head's
-// hidden units run one per lane.  With grad, hs[P + p] = dE/dQ_p.  hs, the
-// wave's head work space: Q [P], dE/dQ [P], first-layer activations and
-// then responses [h1], their derivatives [h1], second-layer adjoints [h2].
-__device__ __forceinline__ double head_energy(const DevModel &m, int t, const double *mom,
-                                              double *hs, int lane, bool grad)
+// Descriptor-indexed sums run in chunks of this many independent
+// accumulators per lane, so their loads overlap.
+constexpr int kHeadChunk = 8;
+
+// out[j] = sum over r in [0, n) of w[r * ld + j] * x[r] for j < nj
+// (nj <= kHeadChunk), every lane taking rows lane, lane + 64, ..., then
+// summed over the wave; the result is in every lane.
+__device__ __forceinline__ void wave_matvec_chunk(const double *w, int ld, int nj,
+                                                  const double *x, int n, int lane, double *out)
 {
-    const int P = m.hP, NS = m.hNS, h1 = m.h1, h2 = m.h2;
-    double *Q = hs, *dQ = hs + P, *a1 = dQ + P, *d1 = a1 + h1, *g2 = d1 + h1;
-    for (int p = 0; p < P; ++p) {
-        const double *w = m.hproj + (size_t)p * NS;
-        double v = 0.0;
-        for (int a = lane; a < NS; a += kWave)
-            v += w[a] * mom[m.hids[a]];
-        v = wave_sum(v);
+    double part[kHeadChunk];
+#pragma unroll
+    for (int j = 0; j < kHeadChunk; ++j)
+        part[j] = 0.0;
+    for (int r = lane; r < n; r += kWave) {
+        const double v = x[r];
+        const double *row = w + (size_t)r * ld;
+#pragma unroll
+        for (int j = 0; j < kHeadChunk; ++j)
+            if (j < nj)
+                part[j] += row[j] * v;
+    }
+#pragma unroll
+    for (int j = 0; j < kHeadChunk; ++j)
+        out[j] = j < nj ? wave_sum(part[j]) : 0.0;
+}
+
+// b + sum_k w[k * stride] x[k] for k < n, with four accumulators.
+__device__ __forceinline__ double dot4(double b, const double *w, size_t stride, const double *x,
+                                       int n)
+{
+    double a0 = b, a1 = 0.0, a2 = 0.0, a3 = 0.0;
+    int k = 0;
+    for (; k + 4 <= n; k += 4) {
+        a0 += w[k * stride] * x[k];
+        a1 += w[(k + 1) * stride] * x[k + 1];
+        a2 += w[(k + 2) * stride] * x[k + 2];
+        a3 += w[(k + 3) * stride] * x[k + 3];
+    }
+    for (; k < n; ++k)
+        a0 += w[k * stride] * x[k];
+    return (a0 + a1) + (a2 + a3);
+}
+
+// The dynamic LDS of a launch (the same storage as the kernels' own
+// extern __shared__ arrays), for device functions that are not inlined.
+extern __shared__ double mtpx_lds[];
+
+// The site energy of an MTP-M potential less its species term, for the
+// centre species t, in every lane (Executor::evaluate_site and
+// Executor::head, mtp_cpu.cpp:291-442).  The moments are at LDS offset
+// mom; the descriptors Q_p = dspecies[p Z + t] + sum_a proj[p][a] m(ids[a])
+// are wave sums over the distinct scalar moments, the hidden units run one
+// per lane and dE/dQ is a wave sum over them.  With grad the adjoint seeds
+// A(ids[a]) = sum_p proj[p][a] dE/dQ_p go to the block at LDS offset adj
+// (zero elsewhere).  hs (an LDS offset) is the wave's head work space:
+// Q [P], dE/dQ [P], first-layer activations and then responses [h1], their
+// derivatives [h1], second-layer adjoints [h2].  The sums are ordered
+// differently from the reference's loops (rounding only).  Out of line: the
+// E/F/S kernel's register allocation stays that of the linear model.
+__device__ __noinline__ double head_site(const DevHead *__restrict__ H, int t, int mom, int hs,
+                                         int adj, int lane, bool grad)
+{
+    const int P = H->P, NS = H->NS, h1 = H->h1, h2 = H->h2, act = H->act, kind = H->kind;
+    const int *ids = H->ids;
+    const double *proj = H->proj, *c = H->c;
+    const double *mv = mtpx_lds + mom;
+    double *Q = mtpx_lds + hs, *dQ = Q + P, *a1 = dQ + P, *d1 = a1 + h1, *g2 = d1 + h1;
+    double part[kHeadChunk];
+    // proj is [P][NS]: over the distinct moments a, column j at stride NS
+    for (int p0 = 0; p0 < P; p0 += kHeadChunk) {
+        const int np = min(kHeadChunk, P - p0);
+        double acc[kHeadChunk];
+#pragma unroll
+        for (int j = 0; j < kHeadChunk; ++j)
+            acc[j] = 0.0;
+        for (int a = lane; a < NS; a += kWave) {
+            const double v = mv[ids[a]];
+            const double *w = proj + (size_t)p0 * NS + a;
+#pragma unroll
+            for (int j = 0; j < kHeadChunk; ++j)
+                if (j < np)
+                    acc[j] += w[(size_t)j * NS] * v;
+        }
+#pragma unroll
+        for (int j = 0; j < kHeadChunk; ++j)
+            part[j] = j < np ? wave_sum(acc[j]) : 0.0;
         if (lane == 0)
-            Q[p] = m.hdsp[p * m.Z + t] + v;
+#pragma unroll
+            for (int j = 0; j < kHeadChunk; ++j)
+                if (j < np)
+                    Q[p0 + j] = H->dsp[(p0 + j) * H->Z + t] + part[j];
     }
     wave_sync();
-    const double *c = m.hc;
     double e = 0.0;
-    if (m.head == kHeadLi) {
+    if (kind == kHeadLi) {
         e = Q[0];
         if (grad && lane == 0)
             dQ[0] = 1.0;
-    } else if (m.head == kHeadQ2) {
+    } else if (kind == kHeadQ2) {
         const double x = Q[0], y = Q[1];
         e = c[0] * x + c[1] * y + c[2] * x * x + c[3] * y * y + c[4] * x * y;
         if (grad && lane == 0) {
             dQ[0] = c[0] + 2.0 * c[2] * x + c[4] * y;
             dQ[1] = c[1] + 2.0 * c[3] * y + c[4] * x;
         }
-    } else if (m.head == kHeadFs) {
+    } else if (kind == kHeadFs) {
         e = Q[0] + c[0] * asinh(Q[1]);
         if (grad && lane == 0) {
             dQ[0] = 1.0;
@@ -821,71 +891,58 @@ __device__ __forceinline__ double head_energy(const DevModel &m, int t, const do
     } else {
         // NN1: [W1 (h1 x P) | out (h1) | b1 (h1)]; NN2: [W1 | b1 | W2 (h2 x h1)
         // | b2 (h2) | out (h2)] (the coefficient order of mtp_cpu.cpp:334-337)
-        const bool nn2 = m.head == kHeadNn2;
+        const bool nn2 = kind == kHeadNn2;
         const double *b1 = c + P * h1 + (nn2 ? 0 : h1);
         const double *w2 = b1 + h1, *b2 = w2 + (size_t)h1 * h2;
         const double *out = nn2 ? b2 + h2 : c + P * h1;
-        double part = 0.0;
+        double sum = 0.0;
         for (int h = lane; h < h1; h += kWave) {
-            double v = b1[h], d;
-            for (int p = 0; p < P; ++p)
-                v += c[h * P + p] * Q[p];
-            const double a = head_activate(v, m.hact, d);
+            double d;
+            const double a = head_activate(dot4(b1[h], c + (size_t)h * P, 1, Q, P), act, d);
             a1[h] = a;
             d1[h] = d;
             if (!nn2)
-                part += out[h] * a;
+                sum += out[h] * a;
         }
         wave_sync();
         if (nn2) {
             for (int k = lane; k < h2; k += kWave) {
-                double v = b2[k], d;
-                for (int h = 0; h < h1; ++h)
-                    v += w2[(size_t)k * h1 + h] * a1[h];
-                part += out[k] * head_activate(v, m.hact, d);
+                double d;
+                sum += out[k] * head_activate(dot4(b2[k], w2 + (size_t)k * h1, 1, a1, h1), act, d);
                 g2[k] = out[k] * d;
             }
             wave_sync();
         }
-        e = wave_sum(part);
+        e = wave_sum(sum);
         if (grad) {
             // responses over the activations they replace (each lane its own)
             for (int h = lane; h < h1; h += kWave) {
-                double r = nn2 ? 0.0 : out[h];
-                if (nn2)
-                    for (int k = 0; k < h2; ++k)
-                        r += w2[(size_t)k * h1 + h] * g2[k];
+                const double r = nn2 ? dot4(0.0, w2 + h, (size_t)h1, g2, h2) : out[h];
                 a1[h] = r * d1[h];
             }
             wave_sync();
-            for (int p = lane; p < P; p += kWave) {
-                double g = 0.0;
-                for (int h = 0; h < h1; ++h)
-                    g += c[h * P + p] * a1[h];
-                dQ[p] = g;
+            // dE/dQ_p = sum_h W1[h][p] r_h: W1 read as rows h of P entries
+            for (int p0 = 0; p0 < P; p0 += kHeadChunk) {
+                const int np = min(kHeadChunk, P - p0);
+                wave_matvec_chunk(c + p0, P, np, a1, h1, lane, part);
+                if (lane == 0)
+#pragma unroll
+                    for (int j = 0; j < kHeadChunk; ++j)
+                        if (j < np)
+                            dQ[p0 + j] = part[j];
             }
         }
     }
     wave_sync();
-    return e;
-}
-
-// The adjoint seeds of an MTP-M site into A [K]: zero, then
-// A(ids[a]) = sum_p proj[p][a] dE/dQ_p (mtp_cpu.cpp:435-442).
-__device__ __forceinline__ void head_seeds(const DevModel &m, const double *hs, double *A,
-                                           int lane)
-{
-    const int P = m.hP, NS = m.hNS;
-    const double *dQ = hs + P;
-    for (int k = lane; k < m.K; k += kWave)
-        A[k] = 0.0;
-    wave_sync();
-    for (int a = lane; a < NS; a += kWave) {
-        double v = 0.0;
-        for (int p = 0; p < P; ++p)
-            v += m.hproj[(size_t)p * NS + a] * dQ[p];
-        A[m.hids[a]] = v;
+    if (grad) {
+        double *A = mtpx_lds + adj;
+        for (int k = lane; k < H->K; k += kWave)
+            A[k] = 0.0;
+        wave_sync();
+        for (int a = lane; a < NS; a += kWave)
+            A[ids[a]] = dot4(0.0, proj + a, (size_t)NS, dQ, P);
     }
+    return e;
 }
 
 // Launch shape for a kernel whose waves each own `priv_doubles` of LDS work

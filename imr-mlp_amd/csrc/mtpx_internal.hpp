@@ -210,7 +210,8 @@ struct Plan {
     // E/F/S kernel: transpose buffer, slot-ordered adjoints, the wave's
     // energy/virial sums and, with an MTP-M head, the head's work space
     // (descriptors, their adjoints, hidden activations and derivatives, the
-    // second layer's adjoints) (offsets in doubles).
+    // second layer's adjoints: over the dead transpose buffer where it fits)
+    // (offsets in doubles).
     int efs_red = 0, efs_stage = 0, efs_acc = 0, efs_head = 0;
     // first slot of each (nu, mu) block, -1 where absent: [nu * kMaxMu + mu]
     int slot_base[(kMaxNu + 1) * kMaxMu];
@@ -260,6 +261,18 @@ struct LinPlan {
 };
 bool build_lin_plan(const Model &m, const Plan &p, LinPlan &lp, std::string &err);
 
+// An MTP-M head on the device, one struct in device memory that the E/F/S
+// kernel's out-of-line head function reads: kind, descriptors P, distinct
+// scalar moments NS, hidden sizes, activation, species and moment counts
+// and the head tables.
+struct DevHead {
+    int kind, P, NS, h1, h2, act, Z, K;
+    const int *ids;      // [NS] the distinct moments the scalars map to
+    const double *proj;  // [P][NS] moment coefficients summed per distinct moment
+    const double *dsp;   // [P][Z] descriptor species coefficients
+    const double *c;     // [Mc] head coefficients
+};
+
 // Device view passed to the kernels by value.
 struct DevModel {
     int Z, M, R, K, B, T, S, nslots;
@@ -285,14 +298,10 @@ struct DevModel {
     int K4, dummy, part0, red0, priv_doubles;  // per-wave work space (Plan)
     int tr_delta, tr_red1, tr_red4, tr_stage, tr_grad, tr_ctype, tr_priv;
     int efs_red, efs_stage, efs_acc;
-    // MTP-M head (kHeadNone: the linear MTP of species, moment and seed):
-    // kind, descriptors P, distinct scalar moments NS, hidden sizes,
-    // activation and the per-wave head work space (offset in doubles)
-    int head, hP, hNS, h1, h2, hact, efs_head;
-    const int *hids;      // [NS] the distinct moments the scalars map to
-    const double *hproj;  // [P][NS] moment coefficients summed per distinct moment
-    const double *hdsp;   // [P][Z] descriptor species coefficients
-    const double *hc;     // [Mc] head coefficients
+    // MTP-M head (kHeadNone: the linear MTP of species, moment and seed),
+    // the per-wave head work space (offset in doubles) and the head itself
+    int head, efs_head;
+    const DevHead *hd;
     int nradial, ncoef;
     int slot_base[(kMaxNu + 1) * kMaxMu];
     int fwd_nsteps, bwd_nsteps;                 // steps per lane, all levels
