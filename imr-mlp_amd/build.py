@@ -43,6 +43,7 @@ SOURCES = [
     ("sites.cpp", ["-ffp-contract=off"]),
     ("metadata.cpp", ["-ffp-contract=off"]),
     ("lbfgs.cpp", ["-ffp-contract=off"]),
+    ("gpm.cpp", ["-ffp-contract=off"]),
 ]
 
 

@@ -6,7 +6,7 @@
 // --energy-only), and writes the configurations back
 // (GPIO::write_next_mlpcfg, io/gpio_write.cpp:224-380).
 //
-//   mtpx_calc_efs --pot potential.mtp --in input.cfg --out output-efs.cfg
+//   mtpx_calc_efs --pot potential.mtp|.gpm --in input.cfg --out output-efs.cfg
 //       [--energy-only] [--no-site-energy] [--lossless] [--show-progress]
 //       [--gpu-id K] [--gpu-batch-atoms N] [--gpu-batch-structures N]
 //       [--deterministic]
@@ -311,7 +311,7 @@ int main(int argc, char **argv)
     if (gpu < 0)
         gpu = 0;
 
-    std::ifstream pf(pot);
+    std::ifstream pf(pot, std::ios::binary);
     if (!pf)
         die("cannot read " + pot);
     const std::string text((std::istreambuf_iterator<char>(pf)), {});
@@ -328,7 +328,11 @@ int main(int argc, char **argv)
 
     mtpx_context *ctx = nullptr;
     check(nullptr, mtpx_create(gpu, &ctx), "mtpx_create");
-    check(ctx, mtpx_load_model_text(ctx, text.c_str()), "load potential");
+    // a GPM bundle (by its magic, as GPM::is_file) or .mtp text
+    if (text.size() >= 8 && text.compare(0, 8, "GPMLMODL") == 0)
+        check(ctx, mtpx_load_model_gpm(ctx, text.data(), text.size()), "load potential");
+    else
+        check(ctx, mtpx_load_model_text(ctx, text.c_str()), "load potential");
     int info[8];
     check(ctx, mtpx_model_info(ctx, info), "model info");
     double cutoff = 0;

@@ -614,6 +614,119 @@ int mtpx_save_model_text(const mtpx_context *ctx, char *buf, size_t cap, size_t 
     return copy_text(save_mtp(ctx->model), buf, cap, len);
 }
 
+namespace {
+void copy_err(const std::string &e, char *err, int errlen)
+{
+    if (err && errlen > 0) {
+        std::strncpy(err, e.c_str(), (size_t)errlen - 1);
+        err[errlen - 1] = 0;
+    }
+}
+
+int copy_bytes(const std::string &b, void *buf, size_t cap, size_t *len)
+{
+    if (len)
+        *len = b.size();
+    if (!buf)
+        return MTPX_OK;
+    if (cap < b.size())
+        return MTPX_E_CAPACITY;
+    std::memcpy(buf, b.data(), b.size());
+    return MTPX_OK;
+}
+
+// A bundle's model: its .mtp text parsed, each radial basis given its own
+// scaling (read_mtp, potentials/gpm_codec.cpp:370-382).
+bool model_from_gpm(const void *bytes, size_t n, Model &m, std::string &e)
+{
+    std::string text;
+    std::vector<double> scalings;
+    if (!gpm_read(bytes, n, text, scalings, e) || !parse_mtp(text, m, e))
+        return false;
+    if (scalings.size() != m.bases.size()) {
+        e = "GPM: radial bases do not match the model";
+        return false;
+    }
+    for (size_t i = 0; i < scalings.size(); ++i)
+        m.bases[i].scaling = scalings[i];
+    m.scaling = scalings[0];
+    return validate_model(m, e);
+}
+}  // namespace
+
+int mtpx_load_model_gpm(mtpx_context *ctx, const void *bytes, size_t n)
+{
+    if (!ctx || !bytes)
+        return set_error(ctx, MTPX_E_INVALID, "null argument");
+    Model m;
+    std::string err;
+    if (!model_from_gpm(bytes, n, m, err))
+        return set_error(ctx, MTPX_E_MODEL, err);
+    (void)hipSetDevice(ctx->device);
+    return install_model(ctx, std::move(m));
+}
+
+int mtpx_save_model_gpm(const mtpx_context *ctx, int zstd_level, void *buf, size_t cap,
+                        size_t *len)
+{
+    if (!ctx)
+        return MTPX_E_INVALID;
+    if (!ctx->has_model)
+        return MTPX_E_NO_MODEL;
+    std::string out, err;
+    if (!gpm_write(ctx->model, zstd_level, out, err))
+        return MTPX_E_MODEL;
+    return copy_bytes(out, buf, cap, len);
+}
+
+int mtpx_gpm_to_text(const void *bytes, size_t n, char *buf, size_t cap, size_t *len, char *err,
+                     int errlen)
+{
+    if (!bytes)
+        return MTPX_E_INVALID;
+    std::string text, e;
+    std::vector<double> scalings;
+    if (!gpm_read(bytes, n, text, scalings, e)) {
+        copy_err(e, err, errlen);
+        return MTPX_E_MODEL;
+    }
+    return copy_text(text, buf, cap, len);
+}
+
+int mtpx_gpm_from_text(const char *text, int zstd_level, void *buf, size_t cap, size_t *len,
+                       char *err, int errlen)
+{
+    if (!text)
+        return MTPX_E_INVALID;
+    Model m;
+    std::string out, e;
+    if (!parse_mtp(text, m, e) || !gpm_write(m, zstd_level, out, e)) {
+        copy_err(e, err, errlen);
+        return MTPX_E_MODEL;
+    }
+    return copy_bytes(out, buf, cap, len);
+}
+
+int mtpx_parse_model_gpm(const void *bytes, size_t n, int out8[8], double *coeffs, char *err,
+                         int errlen)
+{
+    if (!bytes)
+        return MTPX_E_INVALID;
+    Model m;
+    std::string e;
+    if (!model_from_gpm(bytes, n, m, e)) {
+        copy_err(e, err, errlen);
+        return MTPX_E_MODEL;
+    }
+    if (out8) {
+        const int v[8] = {m.Z, m.M, m.R, m.K, m.B, m.T, m.S, m.ncoef()};
+        std::memcpy(out8, v, sizeof v);
+    }
+    if (coeffs)
+        std::memcpy(coeffs, m.coef.data(), sizeof(double) * m.coef.size());
+    return MTPX_OK;
+}
+
 int mtpx_format_model_text(const char *text, char *buf, size_t cap, size_t *len, char *err,
                            int errlen)
 {

@@ -605,6 +605,44 @@ bool parse_mtp(const std::string &text, Model &m, std::string &err)
     return validate_model(m, err);
 }
 
+// The "key = value" lines of AnyBasis::SaveToStream (basis/basis.h:50-56,
+// the rb_b line of Poly4 / Poly5, basis.cpp:560-564, and the configurable
+// basis's basis.cpp:913-919) with numbers as a stream set to 17 significant
+// digits writes them (printf "%.17g"), in their order.
+std::vector<std::pair<std::string, std::string>> basis_settings(const RadialBasis &b, int R)
+{
+    static const char *kind_names[] = {"RBChebyshev", "RBChebyCos", "RBChebyshevPoly4",
+                                       "RBChebyshevPoly5", "RBChebyshevConfigurable"};
+    auto g = [](double v) {
+        char buf[64];
+        std::snprintf(buf, sizeof buf, "%.17g", v);
+        return std::string(buf);
+    };
+    std::vector<std::pair<std::string, std::string>> o = {{"radial_basis_type", kind_names[b.kind]},
+                                                          {"min_dist", g(b.rmin)},
+                                                          {"max_dist", g(b.rmax)},
+                                                          {"radial_basis_size", std::to_string(R)}};
+    if (b.kind == kRBChebyshevPoly4 || b.kind == kRBChebyshevPoly5)
+        o.push_back({"rb_b", g(b.b)});
+    if (b.kind == kRBChebyshevConfigurable) {
+        o.push_back({"basis_function_type", b.one_minus ? "one_minus_chebyshev" : "chebyshev"});
+        o.push_back({"cutoff_type", kCutNames[b.cut]});
+        if (b.cut == kCutPoly3 || b.cut == kCutPoly4 || b.cut == kCutPoly5)
+            o.push_back({"cutoff_b", g(b.cut_b)});
+        if (b.cut == kCutSmoothstep7) {
+            o.push_back({"cutoff_r1", g(b.cut_r1)});
+            o.push_back({"cutoff_r2", g(b.cut_r2)});
+        }
+        o.push_back({"shift_type", kShiftNames[b.shift]});
+        if (b.shift == kShiftExponential || b.shift == kShiftExponentialLeft ||
+            b.shift == kShiftExponentialTanh)
+            o.push_back({"shift_lambda", g(b.lambda)});
+        if (b.shift == kShiftExponentialTanh)
+            o.push_back({"shift_scale_lambda", g(b.scale_lambda)});
+    }
+    return o;
+}
+
 // PotMTP::Save (potentials/potential_mtp.cpp:1052-1061): write_header
 // (:656-671), write_radial_info (:673-690; AnyBasis::SaveToStream,
 // basis/basis.h:50-56, and the rb_b line of Poly4 / Poly5, basis.cpp:560-564,

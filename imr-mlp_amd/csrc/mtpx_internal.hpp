@@ -184,6 +184,18 @@ bool parse_mtp(const std::string &text, Model &m, std::string &err);
 std::string save_mtp(const Model &m);
 // Validates sizes and index ranges of a model view.
 bool validate_model(const Model &m, std::string &err);
+// The named settings of a radial basis as AnyBasis::SaveToStream writes
+// them on a stream of 17 significant digits, in order.
+std::vector<std::pair<std::string, std::string>> basis_settings(const RadialBasis &b, int R);
+// GPM v2 model bundles (gpm.cpp): the .mtp text of a bundle's root MTP or
+// MTP-M model (GPM::mtp_text, tools/gpm_mtp.h:160-289) with each radial
+// basis's own scaling, and the bundle of a model (encode_mtp,
+// potentials/gpm_codec.cpp:190-312, in ModelBundle::save_potential's
+// manifest); zstd_level > 0 compresses the blocks.
+bool gpm_is_bundle(const void *bytes, size_t n);
+bool gpm_read(const void *bytes, size_t n, std::string &text, std::vector<double> &scalings,
+              std::string &err);
+bool gpm_write(const Model &m, int zstd_level, std::string &out, std::string &err);
 
 // Launch plan: basic moments in canonical order, the product rules grouped by
 // dependency level and output (forward) or destination (reverse).

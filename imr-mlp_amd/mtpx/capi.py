@@ -56,6 +56,14 @@ def lib():
         L.mtpx_parse_model_text.argtypes = [C.c_char_p, _ip, _dp, C.c_char_p, C.c_int]
         L.mtpx_model_info.argtypes = [C.c_void_p, _ip]
         L.mtpx_model_head.argtypes = [C.c_void_p, _ip]
+        L.mtpx_load_model_gpm.argtypes = [C.c_void_p, C.c_char_p, C.c_size_t]
+        L.mtpx_save_model_gpm.argtypes = [C.c_void_p, C.c_int, C.c_void_p, C.c_size_t,
+                                          C.POINTER(C.c_size_t)]
+        L.mtpx_gpm_to_text.argtypes = [C.c_char_p, C.c_size_t, C.c_char_p, C.c_size_t,
+                                       C.POINTER(C.c_size_t), C.c_char_p, C.c_int]
+        L.mtpx_gpm_from_text.argtypes = [C.c_char_p, C.c_int, C.c_void_p, C.c_size_t,
+                                         C.POINTER(C.c_size_t), C.c_char_p, C.c_int]
+        L.mtpx_parse_model_gpm.argtypes = [C.c_char_p, C.c_size_t, _ip, _dp, C.c_char_p, C.c_int]
         L.mtpx_parse_model_head.argtypes = [C.c_char_p, _ip, C.c_char_p, C.c_int]
         L.mtpx_get_coeffs.argtypes = [C.c_void_p, _dp]
         L.mtpx_set_coeffs.argtypes = [C.c_void_p, _dp]
@@ -200,6 +208,48 @@ def i32(a):
     return np.ascontiguousarray(a, dtype=np.int32)
 
 
+def gpm_to_text(data: bytes) -> str:
+    """The .mtp text of a GPM bundle's root model (mtpx_gpm_to_text)."""
+    n = C.c_size_t()
+    err = C.create_string_buffer(512)
+    rc = lib().mtpx_gpm_to_text(data, len(data), None, 0, C.byref(n), err, 512)
+    if rc != OK:
+        raise MtpxError(rc, err.value.decode())
+    buf = C.create_string_buffer(n.value + 1)
+    rc = lib().mtpx_gpm_to_text(data, len(data), buf, n.value + 1, C.byref(n), err, 512)
+    if rc != OK:
+        raise MtpxError(rc, err.value.decode())
+    return buf.value.decode()
+
+
+def gpm_from_text(text: str, zstd_level: int = 0) -> bytes:
+    """The GPM bundle of .mtp text (mtpx_gpm_from_text)."""
+    n = C.c_size_t()
+    err = C.create_string_buffer(512)
+    rc = lib().mtpx_gpm_from_text(text.encode(), int(zstd_level), None, 0, C.byref(n), err, 512)
+    if rc != OK:
+        raise MtpxError(rc, err.value.decode())
+    buf = C.create_string_buffer(max(n.value, 1))
+    rc = lib().mtpx_gpm_from_text(text.encode(), int(zstd_level), buf, n.value, C.byref(n), err,
+                                  512)
+    if rc != OK:
+        raise MtpxError(rc, err.value.decode())
+    return buf.raw[:n.value]
+
+
+def parse_model_gpm(data: bytes):
+    """Host-only parse of a GPM bundle: (sizes dict, coefficients)."""
+    info = np.zeros(8, np.int32)
+    err = C.create_string_buffer(512)
+    rc = lib().mtpx_parse_model_gpm(data, len(data), _i(info), None, err, 512)
+    if rc != OK:
+        raise MtpxError(rc, err.value.decode())
+    coef = np.zeros(int(info[7]))
+    lib().mtpx_parse_model_gpm(data, len(data), _i(info), _d(coef), err, 512)
+    keys = ["Z", "M", "R", "K", "B", "T", "S", "ncoef"]
+    return dict(zip(keys, [int(v) for v in info])), coef
+
+
 def format_model_text(text: str) -> str:
     """PotMTP::Load then PotMTP::Save on the host (mtpx_format_model_text)."""
     n = C.c_size_t()
@@ -309,6 +359,22 @@ class Context:
         self._check(lib().mtpx_model_info(self.h, _i(info)), "model_info")
         self.info = dict(zip(["Z", "M", "R", "K", "B", "T", "S", "ncoef"], [int(v) for v in info]))
         return self.info
+
+    def load_model_gpm(self, data: bytes):
+        self._check(lib().mtpx_load_model_gpm(self.h, data, len(data)), "load_model_gpm")
+        info = np.zeros(8, np.int32)
+        self._check(lib().mtpx_model_info(self.h, _i(info)), "model_info")
+        self.info = dict(zip(["Z", "M", "R", "K", "B", "T", "S", "ncoef"], [int(v) for v in info]))
+        return self.info
+
+    def save_model_gpm(self, zstd_level: int = 0) -> bytes:
+        n = C.c_size_t()
+        self._check(lib().mtpx_save_model_gpm(self.h, int(zstd_level), None, 0, C.byref(n)),
+                    "save_model_gpm")
+        buf = C.create_string_buffer(max(n.value, 1))
+        self._check(lib().mtpx_save_model_gpm(self.h, int(zstd_level), buf, n.value, C.byref(n)),
+                    "save_model_gpm")
+        return buf.raw[:n.value]
 
     def model_head(self) -> dict:
         """The loaded potential's head (mtpx_model_head)."""

@@ -99,6 +99,27 @@ int mtpx_save_model_text(const mtpx_context *ctx, char *buf, size_t cap, size_t 
  * buf / cap / len as mtpx_save_model_text, the parse error into err. */
 int mtpx_format_model_text(const char *text, char *buf, size_t cap, size_t *len, char *err,
                            int errlen);
+/* GPM v2 model bundles (tools/gpm_container.h; the MTP node of
+ * potentials/gpm_codec.cpp:190-382).  Loading: ModelBundle::load /
+ * MLIPCore::read_model_text's GPM branch (runtime/mtp/mlip.cpp:354-383) for
+ * a root model of type "mtp" or "mtp_m", blocks stored raw or zstd (the
+ * system's libzstd.so.1, opened at run time); each radial basis keeps its
+ * own scaling.  Saving: ModelBundle::save_potential (inference profile,
+ * potentials/model_bundle.cpp:131-155) with blocks raw, or zstd at
+ * zstd_level > 0; buf / cap / len as mtpx_save_model_text, without a
+ * terminating 0 (cap must be at least *len).  The host-only forms need no
+ * device: mtpx_gpm_to_text is GPM::mtp_text (tools/gpm_mtp.h:160-289),
+ * mtpx_gpm_from_text the bundle of .mtp text, mtpx_parse_model_gpm the
+ * sizes and coefficients of a bundle as mtpx_parse_model_text. */
+int mtpx_load_model_gpm(mtpx_context *ctx, const void *bytes, size_t n);
+int mtpx_save_model_gpm(const mtpx_context *ctx, int zstd_level, void *buf, size_t cap,
+                        size_t *len);
+int mtpx_gpm_to_text(const void *bytes, size_t n, char *buf, size_t cap, size_t *len, char *err,
+                     int errlen);
+int mtpx_gpm_from_text(const char *text, int zstd_level, void *buf, size_t cap, size_t *len,
+                       char *err, int errlen);
+int mtpx_parse_model_gpm(const void *bytes, size_t n, int out8[8], double *coeffs, char *err,
+                         int errlen);
 /* Sizes: Z M R K B T S ncoef (ncoef = Z*Z*M*R + Z + S for the linear MTP,
  * Z*Z*M*R + Z*(q+1) + q*S + model_coeffs_count with an MTP-M head). */
 int mtpx_model_info(const mtpx_context *ctx, int out8[8]);

@@ -501,9 +501,14 @@ def ref_mlip_efs(model_text, nb: Neighbors, point_types, cutoff, workdir, Z, bin
     the oracle's periodic images as ghost atoms.  Returns E, site E[n],
     F[n,3], virial6."""
     pts, orig = nb.points()
-    mpath = os.path.join(workdir, "model.mtp")
-    with open(mpath, "w") as f:
-        f.write(model_text)
+    if isinstance(model_text, bytes):  # a GPM bundle, read by the same core
+        mpath = os.path.join(workdir, "model.gpm")
+        with open(mpath, "wb") as f:
+            f.write(model_text)
+    else:
+        mpath = os.path.join(workdir, "model.mtp")
+        with open(mpath, "w") as f:
+            f.write(model_text)
     fin = os.path.join(workdir, "mlip_in.bin")
     fout = os.path.join(workdir, "mlip_out.bin")
     with open(fin, "wb") as f:
