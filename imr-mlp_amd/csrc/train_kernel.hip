@@ -263,18 +263,47 @@ struct DualCtx {
     int lane, row, delta;
 };
 
+// Powers u_x^k, u_y^k, u_z^k for k = 0 .. N: every monomial of every shell
+// is a product of three of them, so the passes below hold 3 (N + 1) values
+// per lane instead of two whole shells (at level 20, 27 doubles against 81),
+// which lets the kernel run two waves per SIMD.
+template <int N, int MMAX>
+__device__ __forceinline__ void unit_powers(const Nbr<MMAX> &q, double *px, double *py, double *pz)
+{
+    px[0] = py[0] = pz[0] = 1.0;
+#pragma unroll
+    for (int k = 1; k <= N; ++k) {
+        px[k] = px[k - 1] * q.ux;
+        py[k] = py[k - 1] * q.uy;
+        pz[k] = pz[k - 1] * q.uz;
+    }
+}
+
+// W . grad_u Y_abc = a W_x Y_(a-1)bc + b W_y Y_a(b-1)c + c W_z Y_ab(c-1),
+// with the weights (wx, wy, wz) as given
+template <int NU>
+__device__ __forceinline__ double grad_u_dot(int a, int b, const double *px, const double *py,
+                                             const double *pz, double wx, double wy, double wz)
+{
+    const int c = NU - a - b;
+    double gy = 0.0;
+    if (a > 0)
+        gy = fma(a * wx, px[a - 1] * (py[b] * pz[c]), gy);
+    if (b > 0)
+        gy = fma(b * wy, px[a] * (py[b - 1] * pz[c]), gy);
+    if (c > 0)
+        gy = fma(c * wz, px[a] * (py[b] * pz[c - 1]), gy);
+    return gy;
+}
+
 // Step 1: per (nu, mu) block, rows m = f Y and q = W . grad_r(f Y)
 //   = Y (f' - nu f/d) w_u + (f/d) W . grad_u Y.
 template <int NU, class P>
 __device__ __forceinline__ void fwd_dual_shells(const DevModel &m, DualCtx &cx,
                                                 const Nbr<P::M> &q, const GradNbr &g,
-                                                const double *prev)
+                                                const double *px, const double *py,
+                                                const double *pz)
 {
-    double cur[shell_size(NU)];
-    if constexpr (NU == 0)
-        cur[0] = 1.0;
-    else
-        next_shell<NU, P::M>(prev, cur, q);
     auto flush = [&]() {
         reduce_rows(cx.red, kChunk, cx.row - kChunk, cx.lane, [&](int r, double acc) {
             const int b = cx.slot_basic[r >> 1];
@@ -292,19 +321,11 @@ __device__ __forceinline__ void fwd_dual_shells(const DevModel &m, DualCtx &cx,
             for (int a = NU; a >= 0; --a)
 #pragma unroll
                 for (int b = NU - a; b >= 0; --b) {
-                    const int i = shell_index(NU, a, b);
-                    double gy = 0.0;
-                    if constexpr (NU > 0) {
-                        if (a > 0)
-                            gy += (a * g.wx) * prev[shell_index(NU - 1, a - 1, b)];
-                        if (b > 0)
-                            gy += (b * g.wy) * prev[shell_index(NU - 1, a, b - 1)];
-                        if (NU - a - b > 0)
-                            gy += ((NU - a - b) * g.wz) * prev[shell_index(NU - 1, a, b)];
-                    }
-                    cx.red[(cx.row % kChunk) * kRedStride + cx.lane] = q.f[mu] * cur[i];
+                    const double y = px[a] * (py[b] * pz[NU - a - b]);
+                    const double gy = grad_u_dot<NU>(a, b, px, py, pz, g.wx, g.wy, g.wz);
+                    cx.red[(cx.row % kChunk) * kRedStride + cx.lane] = q.f[mu] * y;
                     ++cx.row;
-                    cx.red[(cx.row % kChunk) * kRedStride + cx.lane] = hw * cur[i] + fd * gy;
+                    cx.red[(cx.row % kChunk) * kRedStride + cx.lane] = hw * y + fd * gy;
                     ++cx.row;
                     if (cx.row % kChunk == 0)
                         flush();
@@ -313,56 +334,40 @@ __device__ __forceinline__ void fwd_dual_shells(const DevModel &m, DualCtx &cx,
     }
     if constexpr (NU < P::NUMAX) {
         if (P::deeper(m, NU))
-            fwd_dual_shells<NU + 1, P>(m, cx, q, g, cur);
+            fwd_dual_shells<NU + 1, P>(m, cx, q, g, px, py, pz);
     }
 }
 
-// Step 4, all radial functions at once (nu outer, like the E/F/S backward
-// pass): per mu, alpha_mu (without its beta-like term) and U_mu.
-//   alpha += Gb Y - nu (w_u/d) A Y + (W/d) . (aA Y_a-1, bA Y_b-1, cA Y_c-1)
+// Step 4, all radial functions at once, monomial by monomial with the
+// radial functions innermost: per mu, alpha_mu (without its beta-like
+// term) and U_mu,
+//   alpha += G Y + A (W/d . grad_u Y - nu (w_u/d) Y),  U += A Y.
 template <int NU, class P>
 __device__ __forceinline__ void rad_shells(const DevModel &m, const double2 *AG,
-                                           const Nbr<P::M> &q, const GradNbr &g,
-                                           const double *prev, double *alpha, double *U)
+                                           const double *px, const double *py, const double *pz,
+                                           const GradNbr &g, double invd, double *alpha,
+                                           double *U)
 {
-    double cur[shell_size(NU)];
-    if constexpr (NU == 0)
-        cur[0] = 1.0;
-    else
-        next_shell<NU, P::M>(prev, cur, q);
-    const double ncw = -NU * g.wu * q.invd;
-    const double wxd = g.wx * q.invd, wyd = g.wy * q.invd, wzd = g.wz * q.invd;
+    const double ncw = -NU * g.wu * invd;
+    const double wxd = g.wx * invd, wyd = g.wy * invd, wzd = g.wz * invd;
 #pragma unroll
-    for (int mu = 0; mu < P::M; ++mu) {
-        if (P::active(m, mu, NU)) {
-            __builtin_amdgcn_sched_barrier(0);
-            const int base = slot_base<P>(m, NU, mu);
-            double uu = 0.0, al = 0.0;
+    for (int a = NU; a >= 0; --a)
 #pragma unroll
-            for (int a = NU; a >= 0; --a)
+        for (int b = NU - a; b >= 0; --b) {
+            const int i = shell_index(NU, a, b);
+            const double y = px[a] * (py[b] * pz[NU - a - b]);
+            const double t = fma(ncw, y, grad_u_dot<NU>(a, b, px, py, pz, wxd, wyd, wzd));
 #pragma unroll
-                for (int b = NU - a; b >= 0; --b) {
-                    const int i = shell_index(NU, a, b);
-                    const double2 w = AG[base + i];  // {A, G}, LDS broadcast
-                    uu = fma(w.x, cur[i], uu);
-                    al = fma(w.y, cur[i], al);
-                    if constexpr (NU > 0) {
-                        if (a > 0)
-                            al = fma(w.x * (a * wxd), prev[shell_index(NU - 1, a - 1, b)], al);
-                        if (b > 0)
-                            al = fma(w.x * (b * wyd), prev[shell_index(NU - 1, a, b - 1)], al);
-                        if (NU - a - b > 0)
-                            al = fma(w.x * ((NU - a - b) * wzd), prev[shell_index(NU - 1, a, b)],
-                                     al);
-                    }
+            for (int mu = 0; mu < P::M; ++mu)
+                if (P::active(m, mu, NU)) {
+                    const double2 w = AG[slot_base<P>(m, NU, mu) + i];  // {A, G}, LDS broadcast
+                    U[mu] = fma(w.x, y, U[mu]);
+                    alpha[mu] = fma(w.y, y, fma(w.x, t, alpha[mu]));
                 }
-            alpha[mu] += fma(uu, ncw, al);
-            U[mu] += uu;
         }
-    }
     if constexpr (NU < P::NUMAX) {
         if (P::deeper(m, NU))
-            rad_shells<NU + 1, P>(m, AG, q, g, cur, alpha, U);
+            rad_shells<NU + 1, P>(m, AG, px, py, pz, g, invd, alpha, U);
     }
 }
 
@@ -425,7 +430,9 @@ __global__ __launch_bounds__(kWave *kMaxWaves) void grad_kernel(DevModel m, DevN
             const int64_t p = beg + base + lane;
             load_neighbor<P>(m, nb, L.coef, ti, p, valid, q);
             const GradNbr g = pair_weight<P>(nb, t, fi, S, p, valid, q);
-            fwd_dual_shells<0, P>(m, cx, q, g, nullptr);
+            double px[P::NUMAX + 1], py[P::NUMAX + 1], pz[P::NUMAX + 1];
+            unit_powers<P::NUMAX>(q, px, py, pz);
+            fwd_dual_shells<0, P>(m, cx, q, g, px, py, pz);
             const int rest = cx.row % kChunk;
             if (rest)
                 reduce_rows(red1, rest, cx.row - rest, lane, [&](int r, double acc) {
@@ -493,7 +500,9 @@ __global__ __launch_bounds__(kWave *kMaxWaves) void grad_kernel(DevModel m, DevN
 #pragma unroll
             for (int mu = 0; mu < P::M; ++mu)
                 alpha[mu] = U[mu] = 0.0;
-            rad_shells<0, P>(m, AG, q, g, nullptr, alpha, U);
+            double px[P::NUMAX + 1], py[P::NUMAX + 1], pz[P::NUMAX + 1];
+            unit_powers<P::NUMAX>(q, px, py, pz);
+            rad_shells<0, P>(m, AG, px, py, pz, g, q.invd, alpha, U);
             double Q[P::RMAX], dQ[P::RMAX];
             radial_basis<P>(m, ti, tj, q.d, Q, dQ);
             int row = 0;
