@@ -29,6 +29,7 @@
 
 #include <algorithm>
 #include <climits>
+#include <thread>
 #include <cmath>
 
 namespace mtpx {
@@ -902,12 +903,16 @@ hipError_t launch_site_prepare(int nrows, const int *offsets, const int *center_
     return hipGetLastError();
 }
 
-int build_neighbors_batch_gpu(int nconf, const int *atom_offsets, const double *cells,
-                              const int *pbc, const double *pos, const int *types, double cutoff,
-                              hipStream_t s, NeighborStore &out, NeighborStore &tmp,
-                              NeighborScratch &w, std::string &err)
+namespace {
+
+// The structures [0, nconf) one after the other on stream s, concatenated
+// into `out` (atom and entry indices relative to the block's first atom).
+int build_block(int nconf, const int *atom_offsets, const double *cells, const int *pbc,
+                const double *pos, const int *types, double cutoff, hipStream_t s,
+                NeighborStore &out, NeighborStore &tmp, NeighborScratch &w, int first,
+                std::string &err)
 {
-    const int ntot = atom_offsets[nconf];
+    const int ntot = atom_offsets[nconf] - atom_offsets[0];
     out.n = ntot;
     out.P = 0;
     DTRY(out.offsets.ensure(sizeof(int) * ((size_t)ntot + 1)));
@@ -915,11 +920,11 @@ int build_neighbors_batch_gpu(int nconf, const int *atom_offsets, const double *
     DTRY(hipMemsetAsync(out.offsets.p, 0, sizeof(int) * ((size_t)ntot + 1), s));
     int64_t P = 0;
     for (int c = 0; c < nconf; ++c) {
-        const int a0 = atom_offsets[c], nc = atom_offsets[c + 1] - a0;
+        const int a0 = atom_offsets[c] - atom_offsets[0], nc = atom_offsets[c + 1] - atom_offsets[c];
         int rc = build_neighbors_gpu(cells + 9 * (size_t)c, pbc + 3 * (size_t)c, nc,
                                      pos + 3 * (size_t)a0, types + a0, cutoff, s, tmp, w, err);
         if (rc != MTPX_OK) {
-            err = "structure " + std::to_string(c) + ": " + err;
+            err = "structure " + std::to_string(first + c) + ": " + err;
             return rc;
         }
         const int64_t Pc = tmp.P, Pn = P + Pc;
@@ -959,6 +964,160 @@ int build_neighbors_batch_gpu(int nconf, const int *atom_offsets, const double *
     DTRY(hipStreamSynchronize(s));
     out.P = P;
     return MTPX_OK;
+}
+
+void release_store(NeighborStore &st)
+{
+    for (DBuf *b : {&st.offsets, &st.idx, &st.type, &st.x, &st.y, &st.z, &st.d, &st.center_type})
+        b->release();
+}
+
+}  // namespace
+
+// Every structure's build is a short chain of small launches with a few
+// host synchronisations, so a large batch is split into contiguous blocks
+// of structures (balanced by atom count) built by host threads, each on a
+// stream, scratch and lists of its own; the blocks are then appended in
+// order on the caller's stream.  The lists are those of the one-by-one
+// build, entry for entry.
+int build_neighbors_batch_gpu(int nconf, const int *atom_offsets, const double *cells,
+                              const int *pbc, const double *pos, const int *types, double cutoff,
+                              hipStream_t s, NeighborStore &out, NeighborStore &tmp,
+                              NeighborScratch &w, std::string &err)
+{
+    const int ntot = atom_offsets[nconf];
+    constexpr int kWorkers = 4;  // the hardware queues a process gets (8 measured 6-8 % faster)
+    if (nconf < 4 * kWorkers)
+        return build_block(nconf, atom_offsets, cells, pbc, pos, types, cutoff, s, out, tmp, w, 0,
+                           err);
+    // contiguous blocks of about equal atom counts (at least one structure each)
+    int cut[kWorkers + 1];
+    cut[0] = 0;
+    for (int k = 1; k < kWorkers; ++k) {
+        const int64_t want = (int64_t)ntot * k / kWorkers;
+        int c = cut[k - 1] + 1;
+        while (c < nconf - (kWorkers - k) && atom_offsets[c] < want)
+            ++c;
+        cut[k] = c;
+    }
+    cut[kWorkers] = nconf;
+    int device = 0;
+    DTRY(hipGetDevice(&device));
+    struct Part {
+        hipStream_t s = nullptr;
+        NeighborStore lists, one;
+        NeighborScratch w;
+        std::string err;
+        int rc = MTPX_OK;
+    };
+    std::vector<Part> parts(kWorkers);
+    for (Part &q : parts)
+        if (hipStreamCreate(&q.s) != hipSuccess) {
+            for (Part &r : parts)
+                if (r.s)
+                    (void)hipStreamDestroy(r.s);
+            err = "neighbour build: cannot create a stream";
+            return MTPX_E_DEVICE;
+        }
+    std::vector<std::thread> threads;
+    bool spawned = true;
+    for (int k = 0; k < kWorkers && spawned; ++k)
+        try {
+            threads.emplace_back([&, k] {
+            Part &q = parts[k];
+            if (hipSetDevice(device) != hipSuccess) {
+                q.rc = MTPX_E_DEVICE;
+                q.err = "neighbour build: cannot select the device";
+                return;
+            }
+            const int c0 = cut[k], a0 = atom_offsets[c0];
+            q.rc = build_block(cut[k + 1] - c0, atom_offsets + c0, cells + 9 * (size_t)c0,
+                               pbc + 3 * (size_t)c0, pos + 3 * (size_t)a0, types + a0, cutoff, q.s,
+                               q.lists, q.one, q.w, c0, q.err);
+            });
+        } catch (...) {  // no thread: the remaining blocks run on this one
+            spawned = false;
+        }
+    for (std::thread &t : threads)
+        t.join();
+    for (int k = (int)threads.size(); k < kWorkers; ++k) {
+        Part &q = parts[k];
+        const int c0 = cut[k], a0 = atom_offsets[c0];
+        q.rc = build_block(cut[k + 1] - c0, atom_offsets + c0, cells + 9 * (size_t)c0,
+                           pbc + 3 * (size_t)c0, pos + 3 * (size_t)a0, types + a0, cutoff, q.s,
+                           q.lists, q.one, q.w, c0, q.err);
+    }
+    int rc = MTPX_OK;
+    int64_t P = 0;
+    for (Part &q : parts) {
+        if (rc == MTPX_OK && q.rc != MTPX_OK) {
+            rc = q.rc;
+            err = q.err;
+        }
+        P += q.lists.P;
+    }
+    if (rc == MTPX_OK && P > INT32_MAX) {
+        rc = MTPX_E_CAPACITY;
+        err = "batch has more than 2^31 - 1 neighbour entries";
+    }
+    hipError_t e = hipSuccess;
+    if (rc == MTPX_OK) {
+        const size_t Pz = (size_t)std::max<int64_t>(P, 1);
+        out.n = ntot;
+        out.P = P;
+        for (DBuf *b : {&out.idx, &out.type})
+            if (e == hipSuccess)
+                e = b->ensure(sizeof(int) * Pz);
+        for (DBuf *b : {&out.x, &out.y, &out.z, &out.d})
+            if (e == hipSuccess)
+                e = b->ensure(sizeof(double) * Pz);
+        if (e == hipSuccess)
+            e = out.offsets.ensure(sizeof(int) * ((size_t)ntot + 1));
+        if (e == hipSuccess)
+            e = out.center_type.ensure(sizeof(int) * std::max(ntot, 1));
+        int64_t p0 = 0;
+        for (int k = 0; k < kWorkers && e == hipSuccess; ++k) {
+            const Part &q = parts[k];
+            const int a0 = atom_offsets[cut[k]], nk = atom_offsets[cut[k + 1]] - a0;
+            const int64_t Pk = q.lists.P;
+            auto copy = [&](const DBuf &from, const DBuf &to, size_t at, size_t bytes) {
+                if (e == hipSuccess && bytes)
+                    e = hipMemcpyAsync(static_cast<char *>(to.p) + at, from.p, bytes,
+                                       hipMemcpyDeviceToDevice, s);
+            };
+            if (e == hipSuccess)
+                e = hipStreamSynchronize(q.s);
+            copy(q.lists.center_type, out.center_type, sizeof(int) * a0, sizeof(int) * nk);
+            copy(q.lists.type, out.type, sizeof(int) * p0, sizeof(int) * Pk);
+            copy(q.lists.x, out.x, sizeof(double) * p0, sizeof(double) * Pk);
+            copy(q.lists.y, out.y, sizeof(double) * p0, sizeof(double) * Pk);
+            copy(q.lists.z, out.z, sizeof(double) * p0, sizeof(double) * Pk);
+            copy(q.lists.d, out.d, sizeof(double) * p0, sizeof(double) * Pk);
+            if (e == hipSuccess) {
+                const int64_t work = std::max<int64_t>(Pk, (int64_t)nk + 1);
+                hipLaunchKernelGGL(append_lists_kernel, dim3((unsigned)((work + 255) / 256)),
+                                   dim3(256), 0, s, q.lists.offsets.as<int>(),
+                                   q.lists.idx.as<int>(), nk, Pk, a0, p0, out.offsets.as<int>(),
+                                   out.idx.as<int>());
+                e = hipGetLastError();
+            }
+            p0 += Pk;
+        }
+        if (e == hipSuccess)
+            e = hipStreamSynchronize(s);
+        if (e != hipSuccess) {
+            rc = e == hipErrorOutOfMemory ? MTPX_E_ALLOC : MTPX_E_DEVICE;
+            err = std::string("neighbour build: ") + hipGetErrorString(e);
+        }
+    }
+    for (Part &q : parts) {
+        (void)hipStreamSynchronize(q.s);
+        (void)hipStreamDestroy(q.s);
+        release_store(q.lists);
+        release_store(q.one);
+        q.w.release_all();
+    }
+    return rc;
 }
 
 }  // namespace mtpx
