@@ -59,11 +59,16 @@ struct NeighborStore {
 struct NeighborScratch {
     DBuf pos, types, pts, orig, cand, flags, scan, tmp, minmax, box, box_start, box_cur,
         box_items, rank, cnt, cursor, key, st_idx, st_type, st_vec, st_d, scalars;
+    // per-structure tables of a batch: atom offsets and wrap flags, cells,
+    // candidate/box/interior-box offsets, flag offsets, geometry, image
+    // counts, point offsets; and the wrapped positions
+    DBuf seg_atoms, seg_cells, seg_tabs, seg_flags, seg_geo, seg_imgs, seg_pts, wrapped;
     void release_all()
     {
         for (DBuf *b : {&pos, &types, &pts, &orig, &cand, &flags, &scan, &tmp, &minmax, &box,
                         &box_start, &box_cur, &box_items, &rank, &cnt, &cursor, &key, &st_idx,
-                        &st_type, &st_vec, &st_d, &scalars})
+                        &st_type, &st_vec, &st_d, &scalars, &seg_atoms, &seg_cells, &seg_tabs,
+                        &seg_flags, &seg_geo, &seg_imgs, &seg_pts, &wrapped})
             b->release();
     }
 };
@@ -72,8 +77,8 @@ int build_neighbors_gpu(const double cell[9], const int pbc[3], int n, const dou
                         const int *types, double cutoff, hipStream_t s, NeighborStore &out,
                         NeighborScratch &w, std::string &err);
 
-// Builds the lists of nconf structures (atoms atom_offsets[c] .. [c+1]) one
-// after the other and concatenates them: atom and entry indices are global.
+// Builds the lists of nconf structures (atoms atom_offsets[c] .. [c+1]) in
+// the same launches and concatenates them: atom and entry indices are global.
 int build_neighbors_batch_gpu(int nconf, const int *atom_offsets, const double *cells,
                               const int *pbc, const double *pos, const int *types, double cutoff,
                               hipStream_t s, NeighborStore &out, NeighborStore &tmp,

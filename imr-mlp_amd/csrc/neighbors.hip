@@ -4,7 +4,8 @@
 // keeps the reference's operation order, and fp64 division and sqrt are
 // IEEE correctly rounded on gfx950.
 //
-// Pipeline (all on one stream):
+// Pipeline (all on one stream, every structure of a chunk in the same
+// launches):
 //   1. wrap (load_positions, only for fully periodic cells) and AABB min/max;
 //   2. periodic images: the host walks the integer image triples in the
 //      reference's lexicographic order (outermost = longest periodic axis),
@@ -29,8 +30,8 @@
 
 #include <algorithm>
 #include <climits>
-#include <thread>
 #include <cmath>
+#include <cstdlib>
 
 namespace mtpx {
 
@@ -52,137 +53,6 @@ __device__ __forceinline__ void dev_row_times(const double *p, const double *M, 
     out[0] = r[0];
     out[1] = r[1];
     out[2] = r[2];
-}
-
-// load_positions (neighborhoods_base.h:113-127)
-__global__ void wrap_kernel(const double *pos, int n, Cell c, int wrap, double *pts)
-{
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= n)
-        return;
-    double p[3] = {pos[3 * i], pos[3 * i + 1], pos[3 * i + 2]};
-    if (wrap) {
-        double f[3];
-        dev_row_times(p, c.inv, f);
-        f[0] -= floor(f[0]);
-        f[1] -= floor(f[1]);
-        f[2] -= floor(f[2]);
-        dev_row_times(f, c.m, p);
-    }
-    pts[3 * i] = p[0];
-    pts[3 * i + 1] = p[1];
-    pts[3 * i + 2] = p[2];
-}
-
-// Component-wise min/max over the originals; one workgroup, ordered.
-__global__ __launch_bounds__(256) void minmax_kernel(const double *pts, int n, double *out6)
-{
-    __shared__ double lo[256][3], hi[256][3];
-    const int t = threadIdx.x;
-    double l[3] = {pts[0], pts[1], pts[2]}, h[3] = {pts[0], pts[1], pts[2]};
-    for (int i = t; i < n; i += 256)
-#pragma unroll
-        for (int d = 0; d < 3; ++d) {
-            const double v = pts[3 * i + d];
-            l[d] = v < l[d] ? v : l[d];
-            h[d] = v > h[d] ? v : h[d];
-        }
-#pragma unroll
-    for (int d = 0; d < 3; ++d) {
-        lo[t][d] = l[d];
-        hi[t][d] = h[d];
-    }
-    __syncthreads();
-    for (int w = 128; w >= 1; w >>= 1) {
-        if (t < w)
-#pragma unroll
-            for (int d = 0; d < 3; ++d) {
-                lo[t][d] = lo[t + w][d] < lo[t][d] ? lo[t + w][d] : lo[t][d];
-                hi[t][d] = hi[t + w][d] > hi[t][d] ? hi[t + w][d] : hi[t][d];
-            }
-        __syncthreads();
-    }
-    if (t < 3) {
-        out6[t] = lo[0][t];
-        out6[3 + t] = hi[0][t];
-    }
-}
-
-struct Bounds {
-    double lo[3], hi[3], cutoff;
-};
-
-// flag[c*n + i] = image c of atom i lies in [lo - rc, hi + rc] (append_images, :72-80)
-__global__ void image_flag_kernel(const double *pts, int n, const double *cand, int ncand,
-                                  Bounds b, int *flags)
-{
-    const int64_t k = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (k >= (int64_t)n * ncand)
-        return;
-    const int c = (int)(k / n), i = (int)(k % n);
-    const double p0 = pts[3 * i] + cand[3 * c], p1 = pts[3 * i + 1] + cand[3 * c + 1],
-                 p2 = pts[3 * i + 2] + cand[3 * c + 2];
-    const bool out = p0 < b.lo[0] - b.cutoff || p1 < b.lo[1] - b.cutoff ||
-                     p2 < b.lo[2] - b.cutoff || p0 > b.hi[0] + b.cutoff ||
-                     p1 > b.hi[1] + b.cutoff || p2 > b.hi[2] + b.cutoff;
-    flags[k] = out ? 0 : 1;
-}
-
-__global__ void image_write_kernel(const double *cand, int n, int64_t total, const int *flags,
-                                   const int *scan, double *pts, int *orig)
-{
-    const int64_t k = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (k >= total || !flags[k])
-        return;
-    const int c = (int)(k / n), i = (int)(k % n);
-    const int64_t q = n + scan[k];
-    pts[3 * q] = pts[3 * i] + cand[3 * c];
-    pts[3 * q + 1] = pts[3 * i + 1] + cand[3 * c + 1];
-    pts[3 * q + 2] = pts[3 * i + 2] + cand[3 * c + 2];
-    orig[q] = i;
-}
-
-__global__ void orig_identity_kernel(int *orig, int n)
-{
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < n)
-        orig[i] = i;
-}
-
-struct BoxGeom {
-    double lo[3], xd[3];
-    int bl[3];
-};
-
-// Box index (neighborhoods_base.h:179-224): ceil(tp * (bl - 2) / xd), originals
-// clamped into [1, bl-2], images into [0, bl-1].
-__global__ void box_index_kernel(const double *pts, int n, int npts, BoxGeom g, int *box,
-                                 int *box_count)
-{
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= npts)
-        return;
-    int ix[3];
-#pragma unroll
-    for (int d = 0; d < 3; ++d) {
-        const double tp = pts[3 * i + d] - g.lo[d];
-        int v = (int)ceil(tp * (g.bl[d] - 2) / g.xd[d]);
-        if (i < n) {
-            if (v == 0)
-                v = 1;
-            if (v == g.bl[d] - 1)
-                --v;
-        } else {
-            if (v < 0)
-                v = 0;
-            if (v >= g.bl[d])
-                v = g.bl[d] - 1;
-        }
-        ix[d] = v;
-    }
-    const int b = (ix[0] * g.bl[1] + ix[1]) * g.bl[2] + ix[2];
-    box[i] = b;
-    atomicAdd(&box_count[b], 1);
 }
 
 // Place each point at box_start[b] + (number of points of box b with a smaller
@@ -210,128 +80,6 @@ __global__ void box_rank_kernel(const int *box, const int *box_start, int npts,
     for (int u = s; u < e; ++u)
         r += unsorted[u] < i;
     items[s + r] = i;
-}
-
-// Originals per interior box, in the lexicographic walk order of construct().
-__global__ void interior_count_kernel(const int *box_start, const int *items, BoxGeom g, int n,
-                                      int *count)
-{
-    const int w = blockIdx.x * blockDim.x + threadIdx.x;
-    const int ni = (g.bl[0] - 2), nj = (g.bl[1] - 2), nk = (g.bl[2] - 2);
-    if (w >= ni * nj * nk)
-        return;
-    const int i = w / (nj * nk) + 1, j = (w / nk) % nj + 1, k = w % nk + 1;
-    const int b = (i * g.bl[1] + j) * g.bl[2] + k;
-    int c = 0;
-    for (int q = box_start[b]; q < box_start[b + 1]; ++q)
-        c += items[q] < n;
-    count[w] = c;
-}
-
-// Processing rank of every original: prefix over interior boxes + slot.
-__global__ void centre_rank_kernel(const int *box_start, const int *items, const int *prefix,
-                                   BoxGeom g, int n, int *rank, int *centre_box)
-{
-    const int w = blockIdx.x * blockDim.x + threadIdx.x;
-    const int ni = (g.bl[0] - 2), nj = (g.bl[1] - 2), nk = (g.bl[2] - 2);
-    if (w >= ni * nj * nk)
-        return;
-    const int i = w / (nj * nk) + 1, j = (w / nk) % nj + 1, k = w % nk + 1;
-    const int b = (i * g.bl[1] + j) * g.bl[2] + k;
-    int r = prefix[w];
-    for (int q = box_start[b]; q < box_start[b + 1]; ++q) {
-        const int p = items[q];
-        if (p < n) {
-            rank[p] = r++;
-            centre_box[p] = b;
-        }
-    }
-}
-
-struct Construct {
-    const double *pts;
-    const int *orig, *box_start, *items, *types, *rank, *centre_box;
-    int n;
-    int bl1, bl2;
-    double cutoffsq;
-};
-
-// construct() (neighborhood.cpp:89-141) for one centre per wave.  MODE 0
-// counts the entries of every list, MODE 1 writes them with their keys.
-// The lanes test 64 candidates of a box at a time; an accepted candidate's
-// event number (its rank among the centre's accepted candidates in the
-// reference's traversal order) is the count so far plus the accepted lanes
-// below it, so the keys, and the lists they order, are those of the serial
-// traversal.
-template <int MODE>
-__global__ __launch_bounds__(256) void construct_kernel(Construct c, int *cnt, int *cursor,
-                                                        uint64_t *key, int *st_idx, int *st_type,
-                                                        double *st_vec, double *st_d)
-{
-    const int lane = threadIdx.x & 63;
-    const int indi = blockIdx.x * (blockDim.x / 64) + threadIdx.x / 64;
-    if (indi >= c.n)
-        return;  // uniform over the wave
-    const int b = c.centre_box[indi];
-    const int bi = b / (c.bl1 * c.bl2), bj = (b / c.bl2) % c.bl1, bk = b % c.bl2;
-    const double pi0 = c.pts[3 * indi], pi1 = c.pts[3 * indi + 1], pi2 = c.pts[3 * indi + 2];
-    const uint64_t krank = (uint64_t)(unsigned)c.rank[indi] << 32;
-    const uint64_t below = (1ull << lane) - 1;
-    unsigned ev = 0;
-    int own = 0;
-    for (int l1 = -1; l1 <= 1; l1++)
-        for (int l2 = -1; l2 <= 1; l2++)
-            for (int l3 = -1; l3 <= 1; l3++) {
-                const int nb = ((bi + l1) * c.bl1 + (bj + l2)) * c.bl2 + (bk + l3);
-                const int t0 = c.box_start[nb], t1 = c.box_start[nb + 1];
-                for (int tb = t0; tb < t1; tb += 64) {
-                    const int t = tb + lane;
-                    bool ok = false;
-                    double r0 = 0.0, r1 = 0.0, r2 = 0.0, dijsq = 0.0;
-                    int oj = 0;
-                    if (t < t1) {
-                        const int indj = c.items[t];
-                        r0 = c.pts[3 * indj] - pi0;
-                        r1 = c.pts[3 * indj + 1] - pi1;
-                        r2 = c.pts[3 * indj + 2] - pi2;
-                        dijsq = r0 * r0 + r1 * r1 + r2 * r2;
-                        oj = c.orig[indj];
-                        ok = dijsq < c.cutoffsq && indi != indj && indi <= oj;
-                    }
-                    const uint64_t acc = __ballot(ok);
-                    if (ok) {
-                        if (MODE == 0) {
-                            if (indi != oj)
-                                atomicAdd(&cnt[oj], 1);
-                        } else {
-                            const double dij = sqrt(dijsq);
-                            const uint64_t k = krank | (ev + (unsigned)__popcll(acc & below));
-                            int q = atomicAdd(&cursor[indi], 1);
-                            key[q] = k;
-                            st_idx[q] = oj;
-                            st_type[q] = c.types[oj];
-                            st_vec[3 * (int64_t)q] = r0;
-                            st_vec[3 * (int64_t)q + 1] = r1;
-                            st_vec[3 * (int64_t)q + 2] = r2;
-                            st_d[q] = dij;
-                            if (indi != oj) {
-                                q = atomicAdd(&cursor[oj], 1);
-                                key[q] = k;
-                                st_idx[q] = indi;
-                                st_type[q] = c.types[indi];
-                                st_vec[3 * (int64_t)q] = -r0;
-                                st_vec[3 * (int64_t)q + 1] = -r1;
-                                st_vec[3 * (int64_t)q + 2] = -r2;
-                                st_d[q] = dij;
-                            }
-                        }
-                    }
-                    ev += (unsigned)__popcll(acc);
-                    own += __popcll(acc);
-                }
-            }
-    if (MODE == 0 && lane == 0)
-        atomicAdd(&cnt[indi], own);
 }
 
 // Rank every staged entry within its list by key and write it to its final
@@ -601,210 +349,6 @@ int image_candidates(const double cell[9], const int pbc[3], const double lo[3],
 
 }  // namespace
 
-int build_neighbors_gpu(const double cell[9], const int pbc[3], int n, const double *pos,
-                        const int *types, double cutoff, hipStream_t s, NeighborStore &out,
-                        NeighborScratch &w, std::string &err)
-{
-    out.n = n;
-    out.P = 0;
-    DTRY(out.offsets.ensure(sizeof(int) * ((size_t)n + 1)));
-    DTRY(hipMemsetAsync(out.offsets.p, 0, sizeof(int) * ((size_t)n + 1), s));
-    DTRY(out.center_type.ensure(sizeof(int) * std::max(n, 1)));
-    if (n == 0) {
-        DTRY(hipStreamSynchronize(s));
-        return MTPX_OK;
-    }
-    const bool fully = pbc[0] && pbc[1] && pbc[2];
-    Cell c;
-    std::copy(cell, cell + 9, c.m);
-    if (fully && !cell_inverse(cell, c.inv)) {
-        err = "singular cell";
-        return MTPX_E_INVALID;
-    }
-    DTRY(w.pos.ensure(sizeof(double) * 3 * n));
-    DTRY(w.types.ensure(sizeof(int) * n));
-    DTRY(w.minmax.ensure(sizeof(double) * 8));
-    DTRY(w.scalars.ensure(sizeof(int) * 16));
-    DTRY(hipMemcpyAsync(w.pos.p, pos, sizeof(double) * 3 * n, hipMemcpyHostToDevice, s));
-    DTRY(hipMemcpyAsync(w.types.p, types, sizeof(int) * n, hipMemcpyHostToDevice, s));
-    hipLaunchKernelGGL(gather_types_kernel, dim3(blocks(n, 256)), dim3(256), 0, s,
-                       w.types.as<int>(), n, out.center_type.as<int>());
-    // the points buffer is sized after the image count is known; wrap into scratch first
-    DTRY(w.tmp.ensure(sizeof(double) * 3 * n));
-    double *wrapped = w.tmp.as<double>();
-    hipLaunchKernelGGL(wrap_kernel, dim3(blocks(n, 256)), dim3(256), 0, s, w.pos.as<double>(), n,
-                       c, fully ? 1 : 0, wrapped);
-    hipLaunchKernelGGL(minmax_kernel, dim3(1), dim3(256), 0, s, wrapped, n, w.minmax.as<double>());
-    double mm[6];
-    DTRY(hipMemcpyAsync(mm, w.minmax.p, sizeof mm, hipMemcpyDeviceToHost, s));
-    DTRY(hipStreamSynchronize(s));
-    Bounds bd;
-    for (int d = 0; d < 3; ++d) {
-        bd.lo[d] = mm[d];
-        bd.hi[d] = mm[3 + d];
-        if (bd.hi[d] - bd.lo[d] < cutoff)  // extent_impl, :140-143
-            bd.hi[d] = bd.lo[d] + cutoff;
-    }
-    bd.cutoff = cutoff;
-
-    std::vector<double> cand;
-    int rc = image_candidates(cell, pbc, bd.lo, bd.hi, cutoff, cand, err);
-    if (rc != MTPX_OK)
-        return rc;
-    const int ncand = (int)cand.size() / 3;
-    int nimg = 0;
-    const int64_t total = (int64_t)ncand * n;
-    if (total > INT_MAX) {
-        err = "too many periodic image candidates";
-        return MTPX_E_CAPACITY;
-    }
-    if (ncand > 0) {
-        DTRY(w.cand.ensure(sizeof(double) * cand.size()));
-        DTRY(hipMemcpyAsync(w.cand.p, cand.data(), sizeof(double) * cand.size(),
-                            hipMemcpyHostToDevice, s));
-        DTRY(w.flags.ensure(sizeof(int) * total));
-        DTRY(w.scan.ensure(sizeof(int) * total));
-        hipLaunchKernelGGL(image_flag_kernel, dim3(blocks(total, 256)), dim3(256), 0, s, wrapped,
-                           n, w.cand.as<double>(), ncand, bd, w.flags.as<int>());
-        DTRY(scan_exclusive(w.flags.as<int>(), total, w.scan.as<int>(), w.box_cur,
-                            w.scalars.as<int>(), s));
-        DTRY(hipMemcpyAsync(&nimg, w.scalars.p, sizeof(int), hipMemcpyDeviceToHost, s));
-        DTRY(hipStreamSynchronize(s));
-    }
-    const int npts = n + nimg;
-    DTRY(w.pts.ensure(sizeof(double) * 3 * npts));
-    DTRY(w.orig.ensure(sizeof(int) * npts));
-    DTRY(hipMemcpyAsync(w.pts.p, wrapped, sizeof(double) * 3 * n, hipMemcpyDeviceToDevice, s));
-    hipLaunchKernelGGL(orig_identity_kernel, dim3(blocks(n, 256)), dim3(256), 0, s,
-                       w.orig.as<int>(), n);
-    if (nimg > 0)
-        hipLaunchKernelGGL(image_write_kernel, dim3(blocks(total, 256)), dim3(256), 0, s,
-                           w.cand.as<double>(), n, total, w.flags.as<int>(), w.scan.as<int>(),
-                           w.pts.as<double>(), w.orig.as<int>());
-
-    // boxes (extent_impl, :145-225)
-    BoxGeom g;
-    for (int d = 0; d < 3; ++d) {
-        g.lo[d] = bd.lo[d];
-        g.xd[d] = bd.hi[d] - bd.lo[d];
-        const double count = std::floor((bd.hi[d] - bd.lo[d]) / cutoff) + 2;
-        if (!std::isfinite(count) || count >= 2e9) {
-            err = "Neighbor spatial box count exceeds integer range";
-            return MTPX_E_RANGE;
-        }
-        g.bl[d] = (int)count;
-        if (g.bl[d] == 2)
-            g.bl[d] = 3;
-    }
-    const int64_t nbox = (int64_t)g.bl[0] * g.bl[1] * g.bl[2];
-    if (nbox > INT_MAX / 2) {
-        err = "Neighbor spatial box count exceeds integer range";
-        return MTPX_E_RANGE;
-    }
-    DTRY(w.box.ensure(sizeof(int) * npts));
-    DTRY(w.box_start.ensure(sizeof(int) * (nbox + 1)));
-    DTRY(w.box_cur.ensure(sizeof(int) * (nbox + 1)));
-    DTRY(w.box_items.ensure(sizeof(int) * npts));
-    DTRY(w.flags.ensure(sizeof(int) * std::max<int64_t>(npts, nbox + 1)));
-    int *box_count = w.cnt.ensure(sizeof(int) * (nbox + 1)) == hipSuccess ? w.cnt.as<int>() : nullptr;
-    if (!box_count) {
-        err = "neighbour build: out of memory";
-        return MTPX_E_ALLOC;
-    }
-    DTRY(hipMemsetAsync(box_count, 0, sizeof(int) * (nbox + 1), s));
-    hipLaunchKernelGGL(box_index_kernel, dim3(blocks(npts, 256)), dim3(256), 0, s,
-                       w.pts.as<double>(), n, npts, g, w.box.as<int>(), box_count);
-    DTRY(scan_exclusive(box_count, nbox + 1, w.box_start.as<int>(), w.tmp, w.scalars.as<int>(), s));
-    DTRY(hipMemcpyAsync(w.box_cur.p, w.box_start.p, sizeof(int) * (nbox + 1),
-                        hipMemcpyDeviceToDevice, s));
-    int *unsorted = w.flags.as<int>();
-    hipLaunchKernelGGL(box_place_kernel, dim3(blocks(npts, 256)), dim3(256), 0, s,
-                       w.box.as<int>(), npts, w.box_cur.as<int>(), unsorted);
-    hipLaunchKernelGGL(box_rank_kernel, dim3(blocks(npts, 256)), dim3(256), 0, s,
-                       w.box.as<int>(), w.box_start.as<int>(), (int)npts, unsorted,
-                       w.box_items.as<int>());
-
-    // processing ranks of the centres
-    const int64_t ninterior = (int64_t)(g.bl[0] - 2) * (g.bl[1] - 2) * (g.bl[2] - 2);
-    DTRY(w.rank.ensure(sizeof(int) * (2 * (size_t)n + 2 * (ninterior + 1))));
-    int *rank = w.rank.as<int>();
-    int *centre_box = rank + n;
-    int *icount = centre_box + n;
-    int *iprefix = icount + (ninterior + 1);
-    hipLaunchKernelGGL(interior_count_kernel, dim3(blocks(ninterior, 256)), dim3(256), 0, s,
-                       w.box_start.as<int>(), w.box_items.as<int>(), g, n, icount);
-    DTRY(scan_exclusive(icount, ninterior, iprefix, w.tmp, w.scalars.as<int>(), s));
-    hipLaunchKernelGGL(centre_rank_kernel, dim3(blocks(ninterior, 256)), dim3(256), 0, s,
-                       w.box_start.as<int>(), w.box_items.as<int>(), iprefix, g, n, rank,
-                       centre_box);
-
-    // construct: count, offsets, fill, rank within lists
-    Construct cs;
-    cs.pts = w.pts.as<double>();
-    cs.orig = w.orig.as<int>();
-    cs.box_start = w.box_start.as<int>();
-    cs.items = w.box_items.as<int>();
-    cs.types = w.types.as<int>();
-    cs.rank = rank;
-    cs.centre_box = centre_box;
-    cs.n = n;
-    cs.bl1 = g.bl[1];
-    cs.bl2 = g.bl[2];
-    cs.cutoffsq = cutoff * cutoff;
-    DTRY(w.cursor.ensure(sizeof(int) * ((size_t)n + 1)));
-    int *cnt = w.cursor.as<int>();
-    DTRY(hipMemsetAsync(cnt, 0, sizeof(int) * ((size_t)n + 1), s));
-    // one wave per centre, four per workgroup
-    hipLaunchKernelGGL(construct_kernel<0>, dim3((n + 3) / 4), dim3(256), 0, s, cs, cnt,
-                       nullptr, nullptr, nullptr, nullptr, nullptr, nullptr);
-    // the entry total in 64 bits: offsets and entry indices are int32
-    unsigned long long *total64 = reinterpret_cast<unsigned long long *>(w.scalars.as<int>() + 8);
-    DTRY(hipMemsetAsync(total64, 0, sizeof *total64, s));
-    hipLaunchKernelGGL(sum64_kernel, dim3(std::min<unsigned>(blocks(n, 256), 1024)), dim3(256), 0,
-                       s, cnt, (int64_t)n, total64);
-    DTRY(scan_exclusive(cnt, (int64_t)n + 1, out.offsets.as<int>(), w.tmp, w.scalars.as<int>(), s));
-    unsigned long long P64 = 0;
-    DTRY(hipMemcpyAsync(&P64, total64, sizeof P64, hipMemcpyDeviceToHost, s));
-    DTRY(hipStreamSynchronize(s));
-    if (P64 > (unsigned long long)INT32_MAX) {
-        err = "structure has more than 2^31 - 1 neighbour entries";
-        return MTPX_E_CAPACITY;
-    }
-    const int64_t P = (int64_t)P64;
-    out.P = P;
-    const size_t Pz = (size_t)std::max<int64_t>(P, 1);
-    DTRY(out.idx.ensure(sizeof(int) * Pz));
-    DTRY(out.type.ensure(sizeof(int) * Pz));
-    DTRY(out.x.ensure(sizeof(double) * Pz));
-    DTRY(out.y.ensure(sizeof(double) * Pz));
-    DTRY(out.z.ensure(sizeof(double) * Pz));
-    DTRY(out.d.ensure(sizeof(double) * Pz));
-    if (P == 0)
-        return MTPX_OK;
-    DTRY(w.key.ensure(sizeof(uint64_t) * Pz));
-    DTRY(w.st_idx.ensure(sizeof(int) * Pz));
-    DTRY(w.st_type.ensure(sizeof(int) * Pz));
-    DTRY(w.st_vec.ensure(sizeof(double) * 3 * Pz));
-    DTRY(w.st_d.ensure(sizeof(double) * Pz));
-    DTRY(hipMemcpyAsync(cnt, out.offsets.p, sizeof(int) * n, hipMemcpyDeviceToDevice, s));
-    hipLaunchKernelGGL(construct_kernel<1>, dim3((n + 3) / 4), dim3(256), 0, s, cs, nullptr, cnt,
-                       w.key.as<uint64_t>(), w.st_idx.as<int>(), w.st_type.as<int>(),
-                       w.st_vec.as<double>(), w.st_d.as<double>());
-    DTRY(w.flags.ensure(sizeof(int) * Pz));
-    int *entry_list = w.flags.as<int>();
-    hipLaunchKernelGGL(entry_list_kernel, dim3(n), dim3(64), 0, s, out.offsets.as<int>(), n,
-                       entry_list);
-    hipLaunchKernelGGL(list_rank_kernel, dim3(blocks(P, 256)), dim3(256), 0, s,
-                       out.offsets.as<int>(), entry_list, P, w.key.as<uint64_t>(),
-                       w.st_idx.as<int>(), w.st_type.as<int>(), w.st_vec.as<double>(),
-                       w.st_d.as<double>(), out.idx.as<int>(), out.type.as<int>(),
-                       out.x.as<double>(), out.y.as<double>(), out.z.as<double>(),
-                       out.d.as<double>());
-    DTRY(hipGetLastError());
-    DTRY(hipStreamSynchronize(s));
-    return MTPX_OK;
-}
-
 namespace {
 
 // Entry geometry of a site request, one wave per centre row: r = x[j] - x[i]
@@ -903,221 +447,763 @@ hipError_t launch_site_prepare(int nrows, const int *offsets, const int *center_
     return hipGetLastError();
 }
 
+// ---- the pipeline over a chunk of structures ----------------------------
+//
+// Every kernel runs over the concatenation of a chunk's structures with a
+// table of per-structure offsets (atoms, points, image flags, image
+// candidates, box counters with one closing counter each, interior boxes)
+// and geometry; a thread finds its structure by binary search over the
+// offsets.  Points are numbered structure by structure (originals, then
+// images), atoms and list entries over the chunk, so the lists come out as
+// the structures' own lists concatenated with chunk-wide atom indices.  A
+// single structure is a chunk of one.  Three host synchronisations per
+// chunk: the AABBs, the image counts and the entry total.
 namespace {
 
-// The structures [0, nconf) one after the other on stream s, concatenated
-// into `out` (atom and entry indices relative to the block's first atom).
-int build_block(int nconf, const int *atom_offsets, const double *cells, const int *pbc,
-                const double *pos, const int *types, double cutoff, hipStream_t s,
-                NeighborStore &out, NeighborStore &tmp, NeighborScratch &w, int first,
-                std::string &err)
+struct SegGeom {      // per structure, after the AABB
+    double lo[3], hi[3], xd[3], cutoff;
+    int bl[3];
+};
+
+struct Seg {
+    int nconf;
+    const int *atom_off, *pt_off, *cand_off, *box_off, *int_off;  // [nconf + 1]
+    const long long *flag_off;                                    // [nconf + 1]
+    const Cell *cell;                                             // [nconf]
+    const int *wrap;                                              // [nconf]
+    const SegGeom *geo;                                           // [nconf]
+    const double *cand;                                           // [3 * candidates]
+};
+
+// The segment holding k: off[c] <= k < off[c + 1] (the last such c when
+// segments are empty).
+template <class T>
+__device__ __forceinline__ int seg_of(const T *off, int n, T k)
 {
-    const int ntot = atom_offsets[nconf] - atom_offsets[0];
-    out.n = ntot;
-    out.P = 0;
-    DTRY(out.offsets.ensure(sizeof(int) * ((size_t)ntot + 1)));
-    DTRY(out.center_type.ensure(sizeof(int) * std::max(ntot, 1)));
-    DTRY(hipMemsetAsync(out.offsets.p, 0, sizeof(int) * ((size_t)ntot + 1), s));
-    int64_t P = 0;
-    for (int c = 0; c < nconf; ++c) {
-        const int a0 = atom_offsets[c] - atom_offsets[0], nc = atom_offsets[c + 1] - atom_offsets[c];
-        int rc = build_neighbors_gpu(cells + 9 * (size_t)c, pbc + 3 * (size_t)c, nc,
-                                     pos + 3 * (size_t)a0, types + a0, cutoff, s, tmp, w, err);
-        if (rc != MTPX_OK) {
-            err = "structure " + std::to_string(first + c) + ": " + err;
-            return rc;
-        }
-        const int64_t Pc = tmp.P, Pn = P + Pc;
-        if (Pn > INT32_MAX) {
-            err = "batch has more than 2^31 - 1 neighbour entries";
-            return MTPX_E_CAPACITY;
-        }
-        const size_t keep = (size_t)P, need = (size_t)std::max<int64_t>(Pn, 1);
-        DTRY(grow_keep(out.idx, sizeof(int) * need, sizeof(int) * keep, s));
-        DTRY(grow_keep(out.type, sizeof(int) * need, sizeof(int) * keep, s));
-        DTRY(grow_keep(out.x, sizeof(double) * need, sizeof(double) * keep, s));
-        DTRY(grow_keep(out.y, sizeof(double) * need, sizeof(double) * keep, s));
-        DTRY(grow_keep(out.z, sizeof(double) * need, sizeof(double) * keep, s));
-        DTRY(grow_keep(out.d, sizeof(double) * need, sizeof(double) * keep, s));
-        if (nc > 0)
-            DTRY(hipMemcpyAsync(out.center_type.as<int>() + a0, tmp.center_type.p,
-                                sizeof(int) * nc, hipMemcpyDeviceToDevice, s));
-        if (Pc > 0) {
-            DTRY(hipMemcpyAsync(out.type.as<int>() + P, tmp.type.p, sizeof(int) * Pc,
-                                hipMemcpyDeviceToDevice, s));
-            DTRY(hipMemcpyAsync(out.x.as<double>() + P, tmp.x.p, sizeof(double) * Pc,
-                                hipMemcpyDeviceToDevice, s));
-            DTRY(hipMemcpyAsync(out.y.as<double>() + P, tmp.y.p, sizeof(double) * Pc,
-                                hipMemcpyDeviceToDevice, s));
-            DTRY(hipMemcpyAsync(out.z.as<double>() + P, tmp.z.p, sizeof(double) * Pc,
-                                hipMemcpyDeviceToDevice, s));
-            DTRY(hipMemcpyAsync(out.d.as<double>() + P, tmp.d.p, sizeof(double) * Pc,
-                                hipMemcpyDeviceToDevice, s));
-        }
-        const int64_t work = std::max<int64_t>(Pc, (int64_t)nc + 1);
-        hipLaunchKernelGGL(append_lists_kernel, dim3((unsigned)((work + 255) / 256)), dim3(256),
-                           0, s, tmp.offsets.as<int>(), tmp.idx.as<int>(), nc, Pc, a0, P,
-                           out.offsets.as<int>(), out.idx.as<int>());
-        DTRY(hipGetLastError());
-        P = Pn;
+    int lo = 0, hi = n;  // off[lo] <= k < off[hi]
+    while (hi - lo > 1) {
+        const int mid = (lo + hi) >> 1;
+        if (off[mid] <= k)
+            lo = mid;
+        else
+            hi = mid;
     }
+    return lo;
+}
+
+// load_positions (neighborhoods_base.h:113-127): fractional wrap into the
+// cell of a fully periodic structure.
+__global__ void wrap_kernel(Seg g, const double *pos, int ntot, double *wr)
+{
+    const int a = blockIdx.x * blockDim.x + threadIdx.x;
+    if (a >= ntot)
+        return;
+    const int c = seg_of(g.atom_off, g.nconf, a);
+    double p[3] = {pos[3 * a], pos[3 * a + 1], pos[3 * a + 2]};
+    if (g.wrap[c]) {
+        const Cell &cl = g.cell[c];
+        double f[3];
+        dev_row_times(p, cl.inv, f);
+        f[0] -= floor(f[0]);
+        f[1] -= floor(f[1]);
+        f[2] -= floor(f[2]);
+        dev_row_times(f, cl.m, p);
+    }
+    wr[3 * a] = p[0];
+    wr[3 * a + 1] = p[1];
+    wr[3 * a + 2] = p[2];
+}
+
+// One workgroup per structure: min/max of its wrapped atoms (exact).
+__global__ __launch_bounds__(256) void minmax_kernel(Seg g, const double *wr, double *out6)
+{
+    __shared__ double lo[256][3], hi[256][3];
+    const int c = blockIdx.x, t = threadIdx.x;
+    const int a0 = g.atom_off[c], n = g.atom_off[c + 1] - a0;
+    if (n == 0)
+        return;
+    const double *pts = wr + 3 * (size_t)a0;
+    double l[3] = {pts[0], pts[1], pts[2]}, h[3] = {pts[0], pts[1], pts[2]};
+    for (int i = t; i < n; i += 256)
+#pragma unroll
+        for (int d = 0; d < 3; ++d) {
+            const double v = pts[3 * i + d];
+            l[d] = v < l[d] ? v : l[d];
+            h[d] = v > h[d] ? v : h[d];
+        }
+#pragma unroll
+    for (int d = 0; d < 3; ++d) {
+        lo[t][d] = l[d];
+        hi[t][d] = h[d];
+    }
+    __syncthreads();
+    for (int w = 128; w >= 1; w >>= 1) {
+        if (t < w)
+#pragma unroll
+            for (int d = 0; d < 3; ++d) {
+                lo[t][d] = lo[t + w][d] < lo[t][d] ? lo[t + w][d] : lo[t][d];
+                hi[t][d] = hi[t + w][d] > hi[t][d] ? hi[t + w][d] : hi[t][d];
+            }
+        __syncthreads();
+    }
+    if (t < 3) {
+        out6[6 * (size_t)c + t] = lo[0][t];
+        out6[6 * (size_t)c + 3 + t] = hi[0][t];
+    }
+}
+
+// flag[k] = image q of atom i of structure c lies in [lo - rc, hi + rc]
+// (append_images, neighborhoods_base.h:72-80); k - flag_off[c] = q n_c + i.
+__global__ void image_flag_kernel(Seg g, const double *wr, long long total, int *flags)
+{
+    const long long k = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (k >= total)
+        return;
+    const int c = seg_of(g.flag_off, g.nconf, k);
+    const int a0 = g.atom_off[c], n = g.atom_off[c + 1] - a0;
+    const long long kk = k - g.flag_off[c];
+    const int q = (int)(kk / n), i = (int)(kk % n);
+    const double *t = g.cand + 3 * (size_t)(g.cand_off[c] + q);
+    const double *w = wr + 3 * (size_t)(a0 + i);
+    const SegGeom &b = g.geo[c];
+    const double p0 = w[0] + t[0], p1 = w[1] + t[1], p2 = w[2] + t[2];
+    const bool out = p0 < b.lo[0] - b.cutoff || p1 < b.lo[1] - b.cutoff ||
+                     p2 < b.lo[2] - b.cutoff || p0 > b.hi[0] + b.cutoff ||
+                     p1 > b.hi[1] + b.cutoff || p2 > b.hi[2] + b.cutoff;
+    flags[k] = out ? 0 : 1;
+}
+
+// images of each structure: the flags' exclusive scan at its end less at its start
+__global__ void image_count_kernel(Seg g, const int *flags, const int *scan, int *nimg)
+{
+    const int c = blockIdx.x * blockDim.x + threadIdx.x;
+    if (c >= g.nconf)
+        return;
+    const long long f0 = g.flag_off[c], f1 = g.flag_off[c + 1];
+    nimg[c] = f1 == f0 ? 0 : scan[f1 - 1] + flags[f1 - 1] - scan[f0];
+}
+
+// originals: point pt_off[c] + i is atom a0 + i
+__global__ void points_kernel(Seg g, const double *wr, int ntot, double *pts, int *orig)
+{
+    const int a = blockIdx.x * blockDim.x + threadIdx.x;
+    if (a >= ntot)
+        return;
+    const int c = seg_of(g.atom_off, g.nconf, a);
+    const int q = g.pt_off[c] + (a - g.atom_off[c]);
+    pts[3 * (size_t)q] = wr[3 * (size_t)a];
+    pts[3 * (size_t)q + 1] = wr[3 * (size_t)a + 1];
+    pts[3 * (size_t)q + 2] = wr[3 * (size_t)a + 2];
+    orig[q] = a;
+}
+
+__global__ void image_write_kernel(Seg g, const double *wr, long long total,
+                                         const int *flags, const int *scan, double *pts,
+                                         int *orig)
+{
+    const long long k = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (k >= total || !flags[k])
+        return;
+    const int c = seg_of(g.flag_off, g.nconf, k);
+    const int a0 = g.atom_off[c], n = g.atom_off[c + 1] - a0;
+    const long long kk = k - g.flag_off[c];
+    const int q = (int)(kk / n), i = (int)(kk % n);
+    const double *t = g.cand + 3 * (size_t)(g.cand_off[c] + q);
+    const double *w = wr + 3 * (size_t)(a0 + i);
+    const size_t o = (size_t)g.pt_off[c] + n + (scan[k] - scan[g.flag_off[c]]);
+    pts[3 * o] = w[0] + t[0];
+    pts[3 * o + 1] = w[1] + t[1];
+    pts[3 * o + 2] = w[2] + t[2];
+    orig[o] = a0 + i;
+}
+
+// Box index (neighborhoods_base.h:179-224): ceil(tp * (bl - 2) / xd), originals
+// clamped into [1, bl-2], images into [0, bl-1]; boxes numbered globally.
+__global__ void box_index_kernel(Seg g, const double *pts, int npts, int *box,
+                                       int *box_count)
+{
+    const int p = blockIdx.x * blockDim.x + threadIdx.x;
+    if (p >= npts)
+        return;
+    const int c = seg_of(g.pt_off, g.nconf, p);
+    const int n = g.atom_off[c + 1] - g.atom_off[c];
+    const bool original = p - g.pt_off[c] < n;
+    const SegGeom &b = g.geo[c];
+    int ix[3];
+#pragma unroll
+    for (int d = 0; d < 3; ++d) {
+        const double tp = pts[3 * (size_t)p + d] - b.lo[d];
+        int v = (int)ceil(tp * (b.bl[d] - 2) / b.xd[d]);
+        if (original) {
+            if (v == 0)
+                v = 1;
+            if (v == b.bl[d] - 1)
+                --v;
+        } else {
+            if (v < 0)
+                v = 0;
+            if (v >= b.bl[d])
+                v = b.bl[d] - 1;
+        }
+        ix[d] = v;
+    }
+    const int gb = g.box_off[c] + (ix[0] * b.bl[1] + ix[1]) * b.bl[2] + ix[2];
+    box[p] = gb;
+    atomicAdd(&box_count[gb], 1);
+}
+
+// interior box w of structure c (walk order i, j, k from 1)
+__device__ __forceinline__ int interior_box(const SegGeom &b, int w)
+{
+    const int nj = b.bl[1] - 2, nk = b.bl[2] - 2;
+    const int i = w / (nj * nk) + 1, j = (w / nk) % nj + 1, k = w % nk + 1;
+    return (i * b.bl[1] + j) * b.bl[2] + k;
+}
+
+// Originals per interior box, in the lexicographic walk order of construct().
+__global__ void interior_count_kernel(Seg g, const int *box_start, const int *items,
+                                            int nint, int *count)
+{
+    const int w = blockIdx.x * blockDim.x + threadIdx.x;
+    if (w >= nint)
+        return;
+    const int c = seg_of(g.int_off, g.nconf, w);
+    const int gb = g.box_off[c] + interior_box(g.geo[c], w - g.int_off[c]);
+    const int lim = g.pt_off[c] + (g.atom_off[c + 1] - g.atom_off[c]);
+    int k = 0;
+    for (int q = box_start[gb]; q < box_start[gb + 1]; ++q)
+        k += items[q] < lim;
+    count[w] = k;
+}
+
+// Processing rank of every original: prefix over interior boxes + slot.
+__global__ void centre_rank_kernel(Seg g, const int *box_start, const int *items,
+                                         const int *prefix, int nint, int *rank, int *centre_box)
+{
+    const int w = blockIdx.x * blockDim.x + threadIdx.x;
+    if (w >= nint)
+        return;
+    const int c = seg_of(g.int_off, g.nconf, w);
+    const int bl = interior_box(g.geo[c], w - g.int_off[c]);
+    const int gb = g.box_off[c] + bl;
+    const int p0 = g.pt_off[c], lim = p0 + (g.atom_off[c + 1] - g.atom_off[c]);
+    int r = prefix[w];
+    for (int q = box_start[gb]; q < box_start[gb + 1]; ++q) {
+        const int p = items[q];
+        if (p < lim) {
+            const int a = g.atom_off[c] + (p - p0);
+            rank[a] = r++;
+            centre_box[a] = bl;
+        }
+    }
+}
+
+struct Construct {
+    const double *pts;
+    const int *orig, *box_start, *items, *types, *rank, *centre_box;
+    int ntot;
+    double cutoffsq;
+};
+
+// construct() (neighborhood.cpp:89-141) for one centre per wave.  MODE 0
+// counts the entries of every list, MODE 1 writes them with their keys.
+// The lanes test 64 candidates of a box at a time; an accepted candidate's
+// event number (its rank among the centre's accepted candidates in the
+// reference's traversal order) is the count so far plus the accepted lanes
+// below it, so the keys, and the lists they order, are those of the serial
+// traversal.  Ranks are global over a chunk, which keeps each structure's
+// order.
+template <int MODE>
+__global__ __launch_bounds__(256) void construct_kernel(Seg g, Construct cb, int *cnt,
+                                                              int *cursor, uint64_t *key,
+                                                              int *st_idx, int *st_type,
+                                                              double *st_vec, double *st_d)
+{
+    const int lane = threadIdx.x & 63;
+    const int a = blockIdx.x * (blockDim.x / 64) + threadIdx.x / 64;
+    if (a >= cb.ntot)
+        return;  // uniform over the wave
+    const int c = seg_of(g.atom_off, g.nconf, a);
+    const SegGeom &geo = g.geo[c];
+    const int bl1 = geo.bl[1], bl2 = geo.bl[2], box0 = g.box_off[c];
+    const int indi = g.pt_off[c] + (a - g.atom_off[c]);  // the centre's point
+    const int b = cb.centre_box[a];
+    const int bi = b / (bl1 * bl2), bj = (b / bl2) % bl1, bk = b % bl2;
+    const double pi0 = cb.pts[3 * (size_t)indi], pi1 = cb.pts[3 * (size_t)indi + 1],
+                 pi2 = cb.pts[3 * (size_t)indi + 2];
+    const uint64_t krank = (uint64_t)(unsigned)cb.rank[a] << 32;
+    const uint64_t below = (1ull << lane) - 1;
+    unsigned ev = 0;
+    int own = 0;
+    for (int l1 = -1; l1 <= 1; l1++)
+        for (int l2 = -1; l2 <= 1; l2++)
+            for (int l3 = -1; l3 <= 1; l3++) {
+                const int nb = box0 + ((bi + l1) * bl1 + (bj + l2)) * bl2 + (bk + l3);
+                const int t0 = cb.box_start[nb], t1 = cb.box_start[nb + 1];
+                for (int tb = t0; tb < t1; tb += 64) {
+                    const int t = tb + lane;
+                    bool ok = false;
+                    double r0 = 0.0, r1 = 0.0, r2 = 0.0, dijsq = 0.0;
+                    int oj = 0;
+                    if (t < t1) {
+                        const int indj = cb.items[t];
+                        r0 = cb.pts[3 * (size_t)indj] - pi0;
+                        r1 = cb.pts[3 * (size_t)indj + 1] - pi1;
+                        r2 = cb.pts[3 * (size_t)indj + 2] - pi2;
+                        dijsq = r0 * r0 + r1 * r1 + r2 * r2;
+                        oj = cb.orig[indj];
+                        ok = dijsq < cb.cutoffsq && indi != indj && a <= oj;
+                    }
+                    const uint64_t acc = __ballot(ok);
+                    if (ok) {
+                        if (MODE == 0) {
+                            if (a != oj)
+                                atomicAdd(&cnt[oj], 1);
+                        } else {
+                            const double dij = sqrt(dijsq);
+                            const uint64_t k = krank | (ev + (unsigned)__popcll(acc & below));
+                            int q = atomicAdd(&cursor[a], 1);
+                            key[q] = k;
+                            st_idx[q] = oj;
+                            st_type[q] = cb.types[oj];
+                            st_vec[3 * (int64_t)q] = r0;
+                            st_vec[3 * (int64_t)q + 1] = r1;
+                            st_vec[3 * (int64_t)q + 2] = r2;
+                            st_d[q] = dij;
+                            if (a != oj) {
+                                q = atomicAdd(&cursor[oj], 1);
+                                key[q] = k;
+                                st_idx[q] = a;
+                                st_type[q] = cb.types[a];
+                                st_vec[3 * (int64_t)q] = -r0;
+                                st_vec[3 * (int64_t)q + 1] = -r1;
+                                st_vec[3 * (int64_t)q + 2] = -r2;
+                                st_d[q] = dij;
+                            }
+                        }
+                    }
+                    ev += (unsigned)__popcll(acc);
+                    own += __popcll(acc);
+                }
+            }
+    if (MODE == 0 && lane == 0)
+        atomicAdd(&cnt[a], own);
+}
+
+
+// Budgets of one chunk: its atoms (set before the build), its image flags,
+// boxes and interior boxes (the chunk ends early at the structure that would
+// pass them), so every point, box and flag index fits in int32.
+constexpr int kChunkAtoms = 1 << 21;
+constexpr long long kChunkFlags = INT_MAX / 4;
+constexpr long long kChunkBoxes = INT_MAX / 4;
+
+template <class T>
+hipError_t to_device(DBuf &b, const std::vector<T> &v, hipStream_t s)
+{
+    hipError_t e = b.ensure(sizeof(T) * std::max<size_t>(v.size(), 1));
+    if (e == hipSuccess && !v.empty())
+        e = hipMemcpyAsync(b.p, v.data(), sizeof(T) * v.size(), hipMemcpyHostToDevice, s);
+    return e;
+}
+
+hipError_t init_store(NeighborStore &st, int n, hipStream_t s)
+{
+    st.n = n;
+    st.P = 0;
+    hipError_t e = st.offsets.ensure(sizeof(int) * ((size_t)n + 1));
+    if (e == hipSuccess)
+        e = st.center_type.ensure(sizeof(int) * std::max(n, 1));
+    if (e == hipSuccess)
+        e = hipMemsetAsync(st.offsets.p, 0, sizeof(int) * ((size_t)n + 1), s);
+    return e;
+}
+
+// Atoms per chunk: kChunkAtoms, or less when MTPX_NEIGHBOR_CHUNK_ATOMS asks
+// for it (a smaller peak of builder scratch for very large batches).
+int chunk_atoms()
+{
+    const char *v = std::getenv("MTPX_NEIGHBOR_CHUNK_ATOMS");
+    const long k = v ? std::strtol(v, nullptr, 10) : 0;
+    return k > 0 && k < kChunkAtoms ? (int)k : kChunkAtoms;
+}
+
+// Structures [c0, c1) -- fewer when a budget ends the chunk; *done says how
+// many -- into `out`, atoms numbered from the chunk's first atom.  Errors
+// name the structure when `named`.
+int build_chunk(int c0, int c1, const int *atom_offsets, const double *cells, const int *pbc,
+                const double *pos, const int *types, double cutoff, hipStream_t s,
+                NeighborStore &out, NeighborScratch &w, int *done, bool named, std::string &err)
+{
+    int nconf = c1 - c0;
+    const int base = atom_offsets[c0];
+    int ntot = atom_offsets[c1] - base;
+    *done = nconf;
+    DTRY(init_store(out, ntot, s));
+    if (ntot == 0) {
+        DTRY(hipStreamSynchronize(s));
+        return MTPX_OK;
+    }
+    auto fail_at = [&](int c, const std::string &what, int code) {
+        err = named ? "structure " + std::to_string(c0 + c) + ": " + what : what;
+        return code;
+    };
+    cells += 9 * (size_t)c0;
+    pbc += 3 * (size_t)c0;
+    pos += 3 * (size_t)base;
+    types += base;
+    // host tables: offsets, cells
+    std::vector<int> atom_off((size_t)nconf + 1), wrapf((size_t)nconf);
+    for (int c = 0; c <= nconf; ++c)
+        atom_off[c] = atom_offsets[c0 + c] - base;
+    std::vector<Cell> cl((size_t)nconf);
+    for (int c = 0; c < nconf; ++c) {
+        const int *pb = pbc + 3 * (size_t)c;
+        wrapf[c] = pb[0] && pb[1] && pb[2];
+        std::copy(cells + 9 * (size_t)c, cells + 9 * (size_t)c + 9, cl[c].m);
+        if (wrapf[c] && atom_off[c + 1] > atom_off[c] && !cell_inverse(cl[c].m, cl[c].inv))
+            return fail_at(c, "singular cell", MTPX_E_INVALID);
+    }
+    DTRY(w.scalars.ensure(sizeof(int) * 16));
+    std::vector<int> head(atom_off);
+    head.insert(head.end(), wrapf.begin(), wrapf.end());
+    DTRY(to_device(w.seg_atoms, head, s));
+    DTRY(w.seg_cells.ensure(sizeof(Cell) * nconf));
+    DTRY(hipMemcpyAsync(w.seg_cells.p, cl.data(), sizeof(Cell) * nconf, hipMemcpyHostToDevice, s));
+    DTRY(w.pos.ensure(sizeof(double) * 3 * (size_t)ntot));
+    DTRY(w.types.ensure(sizeof(int) * (size_t)ntot));
+    DTRY(hipMemcpyAsync(w.pos.p, pos, sizeof(double) * 3 * (size_t)ntot, hipMemcpyHostToDevice, s));
+    DTRY(hipMemcpyAsync(w.types.p, types, sizeof(int) * (size_t)ntot, hipMemcpyHostToDevice, s));
+    hipLaunchKernelGGL(gather_types_kernel, dim3(blocks(ntot, 256)), dim3(256), 0, s,
+                       w.types.as<int>(), ntot, out.center_type.as<int>());
+    Seg g{};
+    g.nconf = nconf;
+    g.atom_off = w.seg_atoms.as<int>();
+    g.wrap = w.seg_atoms.as<int>() + nconf + 1;
+    g.cell = static_cast<const Cell *>(w.seg_cells.p);
+    DTRY(w.wrapped.ensure(sizeof(double) * 3 * (size_t)ntot));
+    DTRY(w.minmax.ensure(sizeof(double) * 6 * (size_t)nconf));
+    double *wr = w.wrapped.as<double>();
+    hipLaunchKernelGGL(wrap_kernel, dim3(blocks(ntot, 256)), dim3(256), 0, s, g,
+                       w.pos.as<double>(), ntot, wr);
+    hipLaunchKernelGGL(minmax_kernel, dim3(nconf), dim3(256), 0, s, g, wr,
+                       w.minmax.as<double>());
+    std::vector<double> mm(6 * (size_t)nconf);
+    DTRY(hipMemcpyAsync(mm.data(), w.minmax.p, sizeof(double) * mm.size(), hipMemcpyDeviceToHost, s));
     DTRY(hipStreamSynchronize(s));
+
+    // per structure: AABB with the extent fix, image candidates, boxes
+    std::vector<SegGeom> geo((size_t)nconf);
+    std::vector<double> cand, cc;
+    std::vector<int> cand_off(1, 0), box_off(1, 0), int_off(1, 0);
+    std::vector<long long> flag_off(1, 0);
+    for (int c = 0; c < nconf; ++c) {
+        const int n = atom_off[c + 1] - atom_off[c];
+        SegGeom &gc = geo[c];
+        gc = SegGeom{};
+        gc.cutoff = cutoff;
+        long long nflag = 0;
+        long long nbox = 0, nint = 0;
+        if (n > 0) {
+            for (int d = 0; d < 3; ++d) {
+                gc.lo[d] = mm[6 * (size_t)c + d];
+                gc.hi[d] = mm[6 * (size_t)c + 3 + d];
+                if (gc.hi[d] - gc.lo[d] < cutoff)  // extent_impl, :140-143
+                    gc.hi[d] = gc.lo[d] + cutoff;
+            }
+            int rc = image_candidates(cells + 9 * (size_t)c, pbc + 3 * (size_t)c, gc.lo, gc.hi,
+                                      cutoff, cc, err);
+            if (rc != MTPX_OK)
+                return fail_at(c, err, rc);
+            const long long ncand = (long long)cc.size() / 3;
+            if (ncand * n > INT_MAX)
+                return fail_at(c, "too many periodic image candidates", MTPX_E_CAPACITY);
+            nflag = ncand * n;
+            for (int d = 0; d < 3; ++d) {
+                gc.xd[d] = gc.hi[d] - gc.lo[d];
+                const double count = std::floor((gc.hi[d] - gc.lo[d]) / cutoff) + 2;
+                if (!std::isfinite(count) || count >= 2e9)
+                    return fail_at(c, "Neighbor spatial box count exceeds integer range",
+                                   MTPX_E_RANGE);
+                gc.bl[d] = (int)count;
+                if (gc.bl[d] == 2)
+                    gc.bl[d] = 3;
+            }
+            nbox = (long long)gc.bl[0] * gc.bl[1] * gc.bl[2];
+            if (nbox > INT_MAX / 2)
+                return fail_at(c, "Neighbor spatial box count exceeds integer range",
+                               MTPX_E_RANGE);
+            nint = (long long)(gc.bl[0] - 2) * (gc.bl[1] - 2) * (gc.bl[2] - 2);
+            nbox += 1;  // the structure's closing counter
+        }
+        if (flag_off.back() + nflag > kChunkFlags || box_off.back() + nbox > kChunkBoxes ||
+            int_off.back() + nint > kChunkBoxes) {
+            if (c == 0)
+                return fail_at(c, "too many periodic images or boxes for the neighbour builder",
+                               MTPX_E_CAPACITY);
+            nconf = c;  // the chunk ends before this structure
+            break;
+        }
+        if (n > 0)
+            cand.insert(cand.end(), cc.begin(), cc.end());
+        cand_off.push_back((int)(cand.size() / 3));
+        flag_off.push_back(flag_off.back() + nflag);
+        box_off.push_back(box_off.back() + (int)nbox);
+        int_off.push_back(int_off.back() + (int)nint);
+    }
+    if (nconf < c1 - c0) {
+        *done = nconf;
+        ntot = atom_off[nconf];
+        out.n = ntot;
+        g.nconf = nconf;
+    }
+    const long long nflags = flag_off.back();
+    const int nboxes = box_off.back(), nint = int_off.back();
+    std::vector<int> tabs(cand_off);
+    tabs.insert(tabs.end(), box_off.begin(), box_off.end());
+    tabs.insert(tabs.end(), int_off.begin(), int_off.end());
+    DTRY(to_device(w.seg_tabs, tabs, s));
+    DTRY(to_device(w.seg_flags, flag_off, s));
+    DTRY(w.seg_geo.ensure(sizeof(SegGeom) * nconf));
+    DTRY(hipMemcpyAsync(w.seg_geo.p, geo.data(), sizeof(SegGeom) * nconf, hipMemcpyHostToDevice,
+                        s));
+    DTRY(to_device(w.cand, cand, s));
+    g.cand_off = w.seg_tabs.as<int>();
+    g.box_off = g.cand_off + (nconf + 1);
+    g.int_off = g.box_off + (nconf + 1);
+    g.flag_off = w.seg_flags.as<long long>();
+    g.geo = static_cast<const SegGeom *>(w.seg_geo.p);
+    g.cand = w.cand.as<double>();
+
+    // image flags, their scan and the image count of every structure
+    std::vector<int> nimg((size_t)nconf, 0);
+    DTRY(w.seg_imgs.ensure(sizeof(int) * nconf));
+    if (nflags > 0) {
+        DTRY(w.flags.ensure(sizeof(int) * (size_t)nflags));
+        DTRY(w.scan.ensure(sizeof(int) * (size_t)nflags));
+        hipLaunchKernelGGL(image_flag_kernel, dim3(blocks(nflags, 256)), dim3(256), 0, s, g,
+                           wr, nflags, w.flags.as<int>());
+        DTRY(scan_exclusive(w.flags.as<int>(), nflags, w.scan.as<int>(), w.box_cur,
+                            w.scalars.as<int>() ? w.scalars.as<int>() : nullptr, s));
+        hipLaunchKernelGGL(image_count_kernel, dim3(blocks(nconf, 256)), dim3(256), 0, s, g,
+                           w.flags.as<int>(), w.scan.as<int>(), w.seg_imgs.as<int>());
+        DTRY(hipMemcpyAsync(nimg.data(), w.seg_imgs.p, sizeof(int) * nconf, hipMemcpyDeviceToHost, s));
+        DTRY(hipStreamSynchronize(s));
+    }
+    std::vector<int> pt_off(1, 0);
+    for (int c = 0; c < nconf; ++c) {
+        const long long next = (long long)pt_off.back() + (atom_off[c + 1] - atom_off[c]) + nimg[c];
+        if (next > INT_MAX / 2)
+            return fail_at(c, "batch has too many points", MTPX_E_CAPACITY);
+        pt_off.push_back((int)next);
+    }
+    const int npts = pt_off.back();
+    DTRY(to_device(w.seg_pts, pt_off, s));
+    g.pt_off = w.seg_pts.as<int>();
+    DTRY(w.pts.ensure(sizeof(double) * 3 * (size_t)npts));
+    DTRY(w.orig.ensure(sizeof(int) * (size_t)npts));
+    hipLaunchKernelGGL(points_kernel, dim3(blocks(ntot, 256)), dim3(256), 0, s, g,
+                       wr, ntot, w.pts.as<double>(), w.orig.as<int>());
+    if (nflags > 0)
+        hipLaunchKernelGGL(image_write_kernel, dim3(blocks(nflags, 256)), dim3(256), 0, s,
+                           g, wr, nflags, w.flags.as<int>(), w.scan.as<int>(),
+                           w.pts.as<double>(), w.orig.as<int>());
+
+    // boxes: counts, starts, stable placement
+    DTRY(w.box.ensure(sizeof(int) * (size_t)npts));
+    DTRY(w.box_start.ensure(sizeof(int) * ((size_t)nboxes + 1)));
+    DTRY(w.box_cur.ensure(sizeof(int) * ((size_t)nboxes + 1)));
+    DTRY(w.box_items.ensure(sizeof(int) * (size_t)npts));
+    DTRY(w.cnt.ensure(sizeof(int) * ((size_t)nboxes + 1)));
+    DTRY(w.flags.ensure(sizeof(int) * std::max<size_t>((size_t)npts, 1)));
+    int *box_count = w.cnt.as<int>();
+    DTRY(hipMemsetAsync(box_count, 0, sizeof(int) * ((size_t)nboxes + 1), s));
+    hipLaunchKernelGGL(box_index_kernel, dim3(blocks(npts, 256)), dim3(256), 0, s, g,
+                       w.pts.as<double>(), npts, w.box.as<int>(), box_count);
+    DTRY(scan_exclusive(box_count, (int64_t)nboxes + 1, w.box_start.as<int>(), w.tmp,
+                        w.scalars.as<int>(), s));
+    DTRY(hipMemcpyAsync(w.box_cur.p, w.box_start.p, sizeof(int) * ((size_t)nboxes + 1),
+                        hipMemcpyDeviceToDevice, s));
+    int *unsorted = w.flags.as<int>();
+    hipLaunchKernelGGL(box_place_kernel, dim3(blocks(npts, 256)), dim3(256), 0, s,
+                       w.box.as<int>(), npts, w.box_cur.as<int>(), unsorted);
+    hipLaunchKernelGGL(box_rank_kernel, dim3(blocks(npts, 256)), dim3(256), 0, s,
+                       w.box.as<int>(), w.box_start.as<int>(), npts, unsorted,
+                       w.box_items.as<int>());
+
+    // processing ranks of the centres
+    DTRY(w.rank.ensure(sizeof(int) * (2 * (size_t)ntot + 2 * ((size_t)nint + 1))));
+    int *rank = w.rank.as<int>();
+    int *centre_box = rank + ntot;
+    int *icount = centre_box + ntot;
+    int *iprefix = icount + (nint + 1);
+    if (nint > 0) {
+        hipLaunchKernelGGL(interior_count_kernel, dim3(blocks(nint, 256)), dim3(256), 0, s,
+                           g, w.box_start.as<int>(), w.box_items.as<int>(), nint, icount);
+        DTRY(scan_exclusive(icount, nint, iprefix, w.tmp, w.scalars.as<int>(), s));
+        hipLaunchKernelGGL(centre_rank_kernel, dim3(blocks(nint, 256)), dim3(256), 0, s, g,
+                           w.box_start.as<int>(), w.box_items.as<int>(), iprefix, nint, rank,
+                           centre_box);
+    }
+
+    // construct: count, offsets, fill, rank within lists
+    Construct cb;
+    cb.pts = w.pts.as<double>();
+    cb.orig = w.orig.as<int>();
+    cb.box_start = w.box_start.as<int>();
+    cb.items = w.box_items.as<int>();
+    cb.types = w.types.as<int>();
+    cb.rank = rank;
+    cb.centre_box = centre_box;
+    cb.ntot = ntot;
+    cb.cutoffsq = cutoff * cutoff;
+    DTRY(w.cursor.ensure(sizeof(int) * ((size_t)ntot + 1)));
+    int *cnt = w.cursor.as<int>();
+    DTRY(hipMemsetAsync(cnt, 0, sizeof(int) * ((size_t)ntot + 1), s));
+    hipLaunchKernelGGL(construct_kernel<0>, dim3((ntot + 3) / 4), dim3(256), 0, s, g, cb,
+                       cnt, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr);
+    unsigned long long *total64 = reinterpret_cast<unsigned long long *>(w.scalars.as<int>() + 8);
+    DTRY(hipMemsetAsync(total64, 0, sizeof *total64, s));
+    hipLaunchKernelGGL(sum64_kernel, dim3(std::min<unsigned>(blocks(ntot, 256), 1024)), dim3(256),
+                       0, s, cnt, (int64_t)ntot, total64);
+    DTRY(scan_exclusive(cnt, (int64_t)ntot + 1, out.offsets.as<int>(), w.tmp, w.scalars.as<int>(),
+                        s));
+    unsigned long long P64 = 0;
+    DTRY(hipMemcpyAsync(&P64, total64, sizeof P64, hipMemcpyDeviceToHost, s));
+    DTRY(hipStreamSynchronize(s));
+    if (P64 > (unsigned long long)INT32_MAX) {
+        err = named ? "batch has more than 2^31 - 1 neighbour entries"
+                    : "structure has more than 2^31 - 1 neighbour entries";
+        return MTPX_E_CAPACITY;
+    }
+    const int64_t P = (int64_t)P64;
     out.P = P;
+    const size_t Pz = (size_t)std::max<int64_t>(P, 1);
+    DTRY(out.idx.ensure(sizeof(int) * Pz));
+    DTRY(out.type.ensure(sizeof(int) * Pz));
+    DTRY(out.x.ensure(sizeof(double) * Pz));
+    DTRY(out.y.ensure(sizeof(double) * Pz));
+    DTRY(out.z.ensure(sizeof(double) * Pz));
+    DTRY(out.d.ensure(sizeof(double) * Pz));
+    if (P == 0)
+        return MTPX_OK;
+    DTRY(w.key.ensure(sizeof(uint64_t) * Pz));
+    DTRY(w.st_idx.ensure(sizeof(int) * Pz));
+    DTRY(w.st_type.ensure(sizeof(int) * Pz));
+    DTRY(w.st_vec.ensure(sizeof(double) * 3 * Pz));
+    DTRY(w.st_d.ensure(sizeof(double) * Pz));
+    DTRY(hipMemcpyAsync(cnt, out.offsets.p, sizeof(int) * (size_t)ntot, hipMemcpyDeviceToDevice, s));
+    hipLaunchKernelGGL(construct_kernel<1>, dim3((ntot + 3) / 4), dim3(256), 0, s, g, cb,
+                       nullptr, cnt, w.key.as<uint64_t>(), w.st_idx.as<int>(),
+                       w.st_type.as<int>(), w.st_vec.as<double>(), w.st_d.as<double>());
+    DTRY(w.flags.ensure(sizeof(int) * Pz));
+    int *entry_list = w.flags.as<int>();
+    hipLaunchKernelGGL(entry_list_kernel, dim3(ntot), dim3(64), 0, s, out.offsets.as<int>(), ntot,
+                       entry_list);
+    hipLaunchKernelGGL(list_rank_kernel, dim3(blocks(P, 256)), dim3(256), 0, s,
+                       out.offsets.as<int>(), entry_list, P, w.key.as<uint64_t>(),
+                       w.st_idx.as<int>(), w.st_type.as<int>(), w.st_vec.as<double>(),
+                       w.st_d.as<double>(), out.idx.as<int>(), out.type.as<int>(),
+                       out.x.as<double>(), out.y.as<double>(), out.z.as<double>(),
+                       out.d.as<double>());
+    DTRY(hipGetLastError());
+    DTRY(hipStreamSynchronize(s));
     return MTPX_OK;
 }
 
-void release_store(NeighborStore &st)
+// Appends a chunk's lists (atoms from a0, entries from p0) to `out`.
+int append_store(NeighborStore &out, const NeighborStore &ch, int a0, int64_t p0, hipStream_t s,
+                 std::string &err)
 {
-    for (DBuf *b : {&st.offsets, &st.idx, &st.type, &st.x, &st.y, &st.z, &st.d, &st.center_type})
-        b->release();
+    const int nc = ch.n;
+    const int64_t Pc = ch.P;
+    const size_t keep = (size_t)p0, need = (size_t)std::max<int64_t>(p0 + Pc, 1);
+    DTRY(grow_keep(out.idx, sizeof(int) * need, sizeof(int) * keep, s));
+    DTRY(grow_keep(out.type, sizeof(int) * need, sizeof(int) * keep, s));
+    DTRY(grow_keep(out.x, sizeof(double) * need, sizeof(double) * keep, s));
+    DTRY(grow_keep(out.y, sizeof(double) * need, sizeof(double) * keep, s));
+    DTRY(grow_keep(out.z, sizeof(double) * need, sizeof(double) * keep, s));
+    DTRY(grow_keep(out.d, sizeof(double) * need, sizeof(double) * keep, s));
+    if (nc > 0)
+        DTRY(hipMemcpyAsync(out.center_type.as<int>() + a0, ch.center_type.p, sizeof(int) * nc,
+                            hipMemcpyDeviceToDevice, s));
+    if (Pc > 0) {
+        DTRY(hipMemcpyAsync(out.type.as<int>() + p0, ch.type.p, sizeof(int) * Pc,
+                            hipMemcpyDeviceToDevice, s));
+        DTRY(hipMemcpyAsync(out.x.as<double>() + p0, ch.x.p, sizeof(double) * Pc,
+                            hipMemcpyDeviceToDevice, s));
+        DTRY(hipMemcpyAsync(out.y.as<double>() + p0, ch.y.p, sizeof(double) * Pc,
+                            hipMemcpyDeviceToDevice, s));
+        DTRY(hipMemcpyAsync(out.z.as<double>() + p0, ch.z.p, sizeof(double) * Pc,
+                            hipMemcpyDeviceToDevice, s));
+        DTRY(hipMemcpyAsync(out.d.as<double>() + p0, ch.d.p, sizeof(double) * Pc,
+                            hipMemcpyDeviceToDevice, s));
+    }
+    const int64_t work = std::max<int64_t>(Pc, (int64_t)nc + 1);
+    hipLaunchKernelGGL(append_lists_kernel, dim3(blocks(work, 256)), dim3(256), 0, s,
+                       ch.offsets.as<int>(), ch.idx.as<int>(), nc, Pc, a0, p0,
+                       out.offsets.as<int>(), out.idx.as<int>());
+    DTRY(hipGetLastError());
+    DTRY(hipStreamSynchronize(s));
+    return MTPX_OK;
 }
 
 }  // namespace
 
-// Every structure's build is a short chain of small launches with a few
-// host synchronisations, so a large batch is split into contiguous blocks
-// of structures (balanced by atom count) built by host threads, each on a
-// stream, scratch and lists of its own; the blocks are then appended in
-// order on the caller's stream.  The lists are those of the one-by-one
-// build, entry for entry.
+int build_neighbors_gpu(const double cell[9], const int pbc[3], int n, const double *pos,
+                        const int *types, double cutoff, hipStream_t s, NeighborStore &out,
+                        NeighborScratch &w, std::string &err)
+{
+    const int off[2] = {0, n};
+    int done = 0;
+    return build_chunk(0, 1, off, cell, pbc, pos, types, cutoff, s, out, w, &done, false, err);
+}
+
+// A batch goes through build_chunk in one piece when it fits the budgets
+// (the usual case: then the chunk is the batch's store), else chunk by chunk
+// into `tmp`, appended in order.
 int build_neighbors_batch_gpu(int nconf, const int *atom_offsets, const double *cells,
                               const int *pbc, const double *pos, const int *types, double cutoff,
                               hipStream_t s, NeighborStore &out, NeighborStore &tmp,
                               NeighborScratch &w, std::string &err)
 {
     const int ntot = atom_offsets[nconf];
-    constexpr int kWorkers = 4;  // the hardware queues a process gets (8 measured 6-8 % faster)
-    if (nconf < 4 * kWorkers)
-        return build_block(nconf, atom_offsets, cells, pbc, pos, types, cutoff, s, out, tmp, w, 0,
-                           err);
-    // contiguous blocks of about equal atom counts (at least one structure each)
-    int cut[kWorkers + 1];
-    cut[0] = 0;
-    for (int k = 1; k < kWorkers; ++k) {
-        const int64_t want = (int64_t)ntot * k / kWorkers;
-        int c = cut[k - 1] + 1;
-        while (c < nconf - (kWorkers - k) && atom_offsets[c] < want)
-            ++c;
-        cut[k] = c;
-    }
-    cut[kWorkers] = nconf;
-    int device = 0;
-    DTRY(hipGetDevice(&device));
-    struct Part {
-        hipStream_t s = nullptr;
-        NeighborStore lists, one;
-        NeighborScratch w;
-        std::string err;
-        int rc = MTPX_OK;
-    };
-    std::vector<Part> parts(kWorkers);
-    for (Part &q : parts)
-        if (hipStreamCreate(&q.s) != hipSuccess) {
-            for (Part &r : parts)
-                if (r.s)
-                    (void)hipStreamDestroy(r.s);
-            err = "neighbour build: cannot create a stream";
-            return MTPX_E_DEVICE;
-        }
-    std::vector<std::thread> threads;
-    bool spawned = true;
-    for (int k = 0; k < kWorkers && spawned; ++k)
-        try {
-            threads.emplace_back([&, k] {
-            Part &q = parts[k];
-            if (hipSetDevice(device) != hipSuccess) {
-                q.rc = MTPX_E_DEVICE;
-                q.err = "neighbour build: cannot select the device";
-                return;
-            }
-            const int c0 = cut[k], a0 = atom_offsets[c0];
-            q.rc = build_block(cut[k + 1] - c0, atom_offsets + c0, cells + 9 * (size_t)c0,
-                               pbc + 3 * (size_t)c0, pos + 3 * (size_t)a0, types + a0, cutoff, q.s,
-                               q.lists, q.one, q.w, c0, q.err);
-            });
-        } catch (...) {  // no thread: the remaining blocks run on this one
-            spawned = false;
-        }
-    for (std::thread &t : threads)
-        t.join();
-    for (int k = (int)threads.size(); k < kWorkers; ++k) {
-        Part &q = parts[k];
-        const int c0 = cut[k], a0 = atom_offsets[c0];
-        q.rc = build_block(cut[k + 1] - c0, atom_offsets + c0, cells + 9 * (size_t)c0,
-                           pbc + 3 * (size_t)c0, pos + 3 * (size_t)a0, types + a0, cutoff, q.s,
-                           q.lists, q.one, q.w, c0, q.err);
-    }
-    int rc = MTPX_OK;
     int64_t P = 0;
-    for (Part &q : parts) {
-        if (rc == MTPX_OK && q.rc != MTPX_OK) {
-            rc = q.rc;
-            err = q.err;
+    bool in_out = false;  // out holds the first chunk itself
+    const int limit = chunk_atoms();
+    for (int c0 = 0; c0 < nconf || (nconf == 0 && c0 == 0);) {
+        int c1 = std::min(c0 + 1, nconf);
+        while (c1 < nconf && atom_offsets[c1 + 1] - atom_offsets[c0] <= limit)
+            ++c1;
+        const bool whole = c0 == 0 && c1 == nconf;
+        NeighborStore &dst = whole ? out : tmp;
+        int done = 0;
+        int rc = build_chunk(c0, c1, atom_offsets, cells, pbc, pos, types, cutoff, s, dst, w,
+                             &done, true, err);
+        if (rc != MTPX_OK)
+            return rc;
+        if (whole && done == c1 - c0)
+            return MTPX_OK;
+        if (whole) {  // a budget ended the first chunk: it moves to tmp
+            std::swap(out, tmp);
+            in_out = false;
         }
-        P += q.lists.P;
-    }
-    if (rc == MTPX_OK && P > INT32_MAX) {
-        rc = MTPX_E_CAPACITY;
-        err = "batch has more than 2^31 - 1 neighbour entries";
-    }
-    hipError_t e = hipSuccess;
-    if (rc == MTPX_OK) {
-        const size_t Pz = (size_t)std::max<int64_t>(P, 1);
-        out.n = ntot;
+        if (c0 == 0 && !in_out) {
+            DTRY(init_store(out, ntot, s));
+            in_out = true;
+        }
+        if ((int64_t)P + tmp.P > INT32_MAX) {
+            err = "batch has more than 2^31 - 1 neighbour entries";
+            return MTPX_E_CAPACITY;
+        }
+        rc = append_store(out, tmp, atom_offsets[c0], P, s, err);
+        if (rc != MTPX_OK)
+            return rc;
+        P += tmp.P;
         out.P = P;
-        for (DBuf *b : {&out.idx, &out.type})
-            if (e == hipSuccess)
-                e = b->ensure(sizeof(int) * Pz);
-        for (DBuf *b : {&out.x, &out.y, &out.z, &out.d})
-            if (e == hipSuccess)
-                e = b->ensure(sizeof(double) * Pz);
-        if (e == hipSuccess)
-            e = out.offsets.ensure(sizeof(int) * ((size_t)ntot + 1));
-        if (e == hipSuccess)
-            e = out.center_type.ensure(sizeof(int) * std::max(ntot, 1));
-        int64_t p0 = 0;
-        for (int k = 0; k < kWorkers && e == hipSuccess; ++k) {
-            const Part &q = parts[k];
-            const int a0 = atom_offsets[cut[k]], nk = atom_offsets[cut[k + 1]] - a0;
-            const int64_t Pk = q.lists.P;
-            auto copy = [&](const DBuf &from, const DBuf &to, size_t at, size_t bytes) {
-                if (e == hipSuccess && bytes)
-                    e = hipMemcpyAsync(static_cast<char *>(to.p) + at, from.p, bytes,
-                                       hipMemcpyDeviceToDevice, s);
-            };
-            if (e == hipSuccess)
-                e = hipStreamSynchronize(q.s);
-            copy(q.lists.center_type, out.center_type, sizeof(int) * a0, sizeof(int) * nk);
-            copy(q.lists.type, out.type, sizeof(int) * p0, sizeof(int) * Pk);
-            copy(q.lists.x, out.x, sizeof(double) * p0, sizeof(double) * Pk);
-            copy(q.lists.y, out.y, sizeof(double) * p0, sizeof(double) * Pk);
-            copy(q.lists.z, out.z, sizeof(double) * p0, sizeof(double) * Pk);
-            copy(q.lists.d, out.d, sizeof(double) * p0, sizeof(double) * Pk);
-            if (e == hipSuccess) {
-                const int64_t work = std::max<int64_t>(Pk, (int64_t)nk + 1);
-                hipLaunchKernelGGL(append_lists_kernel, dim3((unsigned)((work + 255) / 256)),
-                                   dim3(256), 0, s, q.lists.offsets.as<int>(),
-                                   q.lists.idx.as<int>(), nk, Pk, a0, p0, out.offsets.as<int>(),
-                                   out.idx.as<int>());
-                e = hipGetLastError();
-            }
-            p0 += Pk;
-        }
-        if (e == hipSuccess)
-            e = hipStreamSynchronize(s);
-        if (e != hipSuccess) {
-            rc = e == hipErrorOutOfMemory ? MTPX_E_ALLOC : MTPX_E_DEVICE;
-            err = std::string("neighbour build: ") + hipGetErrorString(e);
-        }
+        c0 += done;
     }
-    for (Part &q : parts) {
-        (void)hipStreamSynchronize(q.s);
-        (void)hipStreamDestroy(q.s);
-        release_store(q.lists);
-        release_store(q.one);
-        q.w.release_all();
-    }
-    return rc;
+    return MTPX_OK;
 }
 
 }  // namespace mtpx

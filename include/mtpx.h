@@ -271,8 +271,11 @@ int mtpx_compute_sites(mtpx_context *ctx, const mtpx_site_request *req);
  * mtpx_build_neighbors and concatenated into one CSR with global atom
  * indices: the flattened topology of MTPGpuBatchRequest
  * (mtp_gpu_direct.h:452-517) and MTPGpuBatch::build
- * (potentials/mtp_gpu_adapter.cpp:1011-1200).  Replaces the resident lists;
- * mtpx_build_neighbors / mtpx_set_neighbors make a batch of one. */
+ * (potentials/mtp_gpu_adapter.cpp:1011-1200).  All structures are built in
+ * the same kernel launches; batches above 2^21 atoms (or the environment
+ * variable MTPX_NEIGHBOR_CHUNK_ATOMS, when smaller) are built in chunks of
+ * whole structures.  Replaces the resident lists; mtpx_build_neighbors /
+ * mtpx_set_neighbors make a batch of one. */
 int mtpx_set_structures(mtpx_context *ctx, int nconf, const int *atom_offsets,
                         const double *cells, const int *pbc, const double *pos, const int *types,
                         double cutoff);

@@ -104,3 +104,47 @@ def test_device_lists_drive_efs(ctx):
     assert abs(Eg - E) < 1e-10 * abs(E)
     assert np.abs(Fg - F).max() < 1e-10 * np.abs(F).max()
     assert np.abs(Sg - St).max() < 1e-10 * np.abs(St).max()
+
+
+def _concat(lists):
+    """The lists of several structures as one batch: offsets and neighbour
+    indices shifted by the atoms and entries before each structure."""
+    off, idx, types, ct, vec, dist = [np.zeros(1, np.int64)], [], [], [], [], []
+    a0 = p0 = 0
+    for nb in lists:
+        off.append(nb.offsets[1:].astype(np.int64) + p0)
+        idx.append(nb.idx.astype(np.int64) + a0)
+        types.append(nb.types)
+        ct.append(nb.center_types)
+        vec.append(nb.vec.reshape(-1, 3))
+        dist.append(nb.dist)
+        a0 += len(nb.offsets) - 1
+        p0 += int(nb.offsets[-1])
+    return dict(offsets=np.concatenate(off), idx=np.concatenate(idx),
+                types=np.concatenate(types), center_types=np.concatenate(ct),
+                vec=np.concatenate(vec), dist=np.concatenate(dist))
+
+
+@pytest.mark.parametrize("chunk", [None, "1", "150"], ids=["one-chunk", "chunk1", "chunk150"])
+def test_batch_lists_bit_exact(nctx, monkeypatch, chunk):
+    """Every structure above in one batch (cutoff 5, an empty structure in the
+    middle), built in the same launches, and in chunks of at most 1 and 150
+    atoms appended in order: the concatenation of the oracle's lists."""
+    if chunk is not None:
+        monkeypatch.setenv("MTPX_NEIGHBOR_CHUNK_ATOMS", chunk)
+    rc = 5.0
+    structs = []
+    for _, s, _ in CASES:
+        pos = O.wrap(s.cell, s.pbc, s.pos) if np.any(s.pbc) else s.pos
+        structs.append(S.Structure(s.cell, pos, s.types, s.pbc))
+    structs.insert(3, S.Structure(np.eye(3) * 5, np.zeros((0, 3)), np.zeros(0, np.int32),
+                                  np.ones(3, np.int32)))
+    nctx.set_structures(structs, rc)
+    got = nctx.get_neighbors()
+    exp = _concat([O.Neighbors.build(s.cell, s.pbc, s.pos, s.types, rc) for s in structs])
+    assert np.array_equal(got["offsets"], exp["offsets"])
+    assert np.array_equal(got["idx"], exp["idx"])
+    assert np.array_equal(got["types"], exp["types"])
+    assert np.array_equal(got["center_types"], exp["center_types"])
+    assert np.array_equal(got["vec"].view(np.uint64), exp["vec"].view(np.uint64))
+    assert np.array_equal(got["dist"].view(np.uint64), exp["dist"].view(np.uint64))
