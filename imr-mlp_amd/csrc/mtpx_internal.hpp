@@ -57,18 +57,18 @@ struct NeighborStore {
     DBuf offsets, idx, type, x, y, z, d, center_type;
 };
 struct NeighborScratch {
-    DBuf pos, types, pts, orig, cand, flags, scan, tmp, minmax, box, box_start, box_cur,
+    DBuf pos, types, pts, orig, flags, scan, tmp, minmax, box, box_start, box_cur,
         box_items, rank, cnt, cursor, key, st_idx, st_type, st_vec, st_d, scalars;
-    // per-structure tables of a batch: atom offsets and wrap flags, cells,
-    // candidate/box/interior-box offsets, flag offsets, geometry, image
-    // counts, point offsets; and the wrapped positions
-    DBuf seg_atoms, seg_cells, seg_tabs, seg_flags, seg_geo, seg_imgs, seg_pts, wrapped;
+    // per-structure tables of a batch (atom offsets, wrap flags and cells;
+    // candidate, box, interior-box and flag offsets, geometry and image
+    // candidates; image counts; point offsets) and the wrapped positions
+    DBuf seg_head, seg_tabs, seg_imgs, seg_pts, wrapped;
     void release_all()
     {
-        for (DBuf *b : {&pos, &types, &pts, &orig, &cand, &flags, &scan, &tmp, &minmax, &box,
+        for (DBuf *b : {&pos, &types, &pts, &orig, &flags, &scan, &tmp, &minmax, &box,
                         &box_start, &box_cur, &box_items, &rank, &cnt, &cursor, &key, &st_idx,
-                        &st_type, &st_vec, &st_d, &scalars, &seg_atoms, &seg_cells, &seg_tabs,
-                        &seg_flags, &seg_geo, &seg_imgs, &seg_pts, &wrapped})
+                        &st_type, &st_vec, &st_d, &scalars, &seg_head, &seg_tabs, &seg_imgs,
+                        &seg_pts, &wrapped})
             b->release();
     }
 };

@@ -32,6 +32,7 @@
 #include <climits>
 #include <cmath>
 #include <cstdlib>
+#include <cstring>
 
 namespace mtpx {
 
@@ -83,35 +84,47 @@ __global__ void box_rank_kernel(const int *box, const int *box_start, int npts,
 }
 
 // Rank every staged entry within its list by key and write it to its final
-// slot (SoA).  One thread per entry.
-__global__ void list_rank_kernel(const int *offsets, const int *entry_list, int64_t P,
-                                 const uint64_t *key, const int *st_idx, const int *st_type,
-                                 const double *st_vec, const double *st_d, int *idx, int *type,
-                                 double *x, double *y, double *z, double *d)
+// slot (SoA).  One wave per list: lanes take 64 entries at a time and count
+// the list's smaller keys, read 64 at a time and broadcast lane by lane
+// (keys within a list are distinct).
+__device__ __forceinline__ uint64_t readlane_u64(uint64_t v, int l)
 {
-    const int64_t q = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (q >= P)
-        return;
-    const int l = entry_list[q];
-    const int s = offsets[l], e = offsets[l + 1];
-    const uint64_t k = key[q];
-    int r = 0;
-    for (int u = s; u < e; ++u)
-        r += key[u] < k;
-    const int64_t o = s + r;
-    idx[o] = st_idx[q];
-    type[o] = st_type[q];
-    x[o] = st_vec[3 * q];
-    y[o] = st_vec[3 * q + 1];
-    z[o] = st_vec[3 * q + 2];
-    d[o] = st_d[q];
+    const unsigned lo = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)v, l);
+    const unsigned hi = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)(v >> 32), l);
+    return ((uint64_t)hi << 32) | lo;
 }
 
-__global__ void entry_list_kernel(const int *offsets, int n, int *entry_list)
+__global__ __launch_bounds__(256) void list_rank_kernel(const int *offsets, int n,
+                                                        const uint64_t *key, const int *st_idx,
+                                                        const int *st_type, const double *st_vec,
+                                                        const double *st_d, int *idx, int *type,
+                                                        double *x, double *y, double *z, double *d)
 {
-    const int i = blockIdx.x;
-    for (int q = offsets[i] + threadIdx.x; q < offsets[i + 1]; q += blockDim.x)
-        entry_list[q] = i;
+    const int lane = threadIdx.x & 63;
+    const int l = blockIdx.x * (blockDim.x / 64) + threadIdx.x / 64;
+    if (l >= n)
+        return;  // uniform over the wave
+    const int s = offsets[l], e = offsets[l + 1];
+    for (int q0 = s; q0 < e; q0 += 64) {
+        const int q = q0 + lane;
+        const uint64_t k = q < e ? key[q] : 0;
+        int r = 0;
+        for (int u0 = s; u0 < e; u0 += 64) {
+            const uint64_t ku = u0 + lane < e ? key[u0 + lane] : 0;
+            const int m = e - u0 < 64 ? e - u0 : 64;
+            for (int j = 0; j < m; ++j)
+                r += readlane_u64(ku, j) < k;
+        }
+        if (q < e) {
+            const int64_t o = s + r;
+            idx[o] = st_idx[q];
+            type[o] = st_type[q];
+            x[o] = st_vec[3 * (int64_t)q];
+            y[o] = st_vec[3 * (int64_t)q + 1];
+            z[o] = st_vec[3 * (int64_t)q + 2];
+            d[o] = st_d[q];
+        }
+    }
 }
 
 __global__ void gather_types_kernel(const int *types, int n, int *center_type)
@@ -222,10 +235,62 @@ __global__ __launch_bounds__(256) void sum64_kernel(const int *in, int64_t n,
         atomicAdd(total, buf[0]);
 }
 
+// Exclusive scan of up to kScan1Max values in one workgroup of 16 waves:
+// wave w owns values [w 64 m, (w+1) 64 m) and reads them 64 at a time
+// (coalesced); a first pass sums each wave's values, a second scans them
+// 64 at a time after the sums of the waves before.  One launch instead of
+// three.
+constexpr int kScan1Waves = 16, kScan1Max = kScan1Waves * 64 * 64;
+
+__global__ __launch_bounds__(kScan1Waves * 64) void scan_one_block(const int *in, int n, int m,
+                                                                   int *out, int *total)
+{
+    __shared__ int wsum[kScan1Waves];
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int base = wv * 64 * m;
+    int s = 0;
+    for (int k = 0; k < m; ++k) {
+        const int i = base + k * 64 + lane;
+        if (i < n)
+            s += in[i];
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1)
+        s += __shfl_xor(s, o);
+    if (lane == 0)
+        wsum[wv] = s;
+    __syncthreads();
+    int carry = 0;
+    for (int k = 0; k < wv; ++k)
+        carry += wsum[k];
+    for (int k = 0; k < m; ++k) {
+        const int i = base + k * 64 + lane;
+        const int v = i < n ? in[i] : 0;
+        int x = v;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const int u = __shfl_up(x, o);
+            if (lane >= o)
+                x += u;
+        }
+        if (i < n)
+            out[i] = carry + x - v;
+        carry += __shfl(x, 63);
+    }
+    if (threadIdx.x == kScan1Waves * 64 - 1)
+        *total = carry;
+}
+
 // Exclusive scan; *total receives the sum (device), returns the error.
 hipError_t scan_exclusive(const int *in, int64_t n, int *out, DBuf &tmp, int *total,
                           hipStream_t s)
 {
+    if (n <= kScan1Max) {
+        const int m = (int)std::max<int64_t>(1, (n + kScan1Waves * 64 - 1) / (kScan1Waves * 64));
+        hipLaunchKernelGGL(scan_one_block, dim3(1), dim3(kScan1Waves * 64), 0, s, in, (int)n, m,
+                           out, total);
+        return hipGetLastError();
+    }
     const int64_t ntiles = std::max<int64_t>(1, (n + kScanTile - 1) / kScanTile);
     hipError_t e = tmp.ensure(sizeof(int) * (size_t)ntiles);
     if (e != hipSuccess)
@@ -491,46 +556,41 @@ __device__ __forceinline__ int seg_of(const T *off, int n, T k)
     return lo;
 }
 
-// load_positions (neighborhoods_base.h:113-127): fractional wrap into the
-// cell of a fully periodic structure.
-__global__ void wrap_kernel(Seg g, const double *pos, int ntot, double *wr)
-{
-    const int a = blockIdx.x * blockDim.x + threadIdx.x;
-    if (a >= ntot)
-        return;
-    const int c = seg_of(g.atom_off, g.nconf, a);
-    double p[3] = {pos[3 * a], pos[3 * a + 1], pos[3 * a + 2]};
-    if (g.wrap[c]) {
-        const Cell &cl = g.cell[c];
-        double f[3];
-        dev_row_times(p, cl.inv, f);
-        f[0] -= floor(f[0]);
-        f[1] -= floor(f[1]);
-        f[2] -= floor(f[2]);
-        dev_row_times(f, cl.m, p);
-    }
-    wr[3 * a] = p[0];
-    wr[3 * a + 1] = p[1];
-    wr[3 * a + 2] = p[2];
-}
-
-// One workgroup per structure: min/max of its wrapped atoms (exact).
-__global__ __launch_bounds__(256) void minmax_kernel(Seg g, const double *wr, double *out6)
+// load_positions (neighborhoods_base.h:113-127) and the AABB.  Workgroup k
+// of structure c (B per structure) wraps the atoms [k m, (k+1) m) of it,
+// m = ceil(n_c / B), into the cell if the structure is fully periodic, and
+// writes their component-wise min and max (+inf / -inf for an empty range);
+// the host takes the min / max of the B partials.  Min and max are exact.
+__global__ __launch_bounds__(256) void wrap_minmax_kernel(Seg g, const double *pos, int B,
+                                                          double *wr, double *part)
 {
     __shared__ double lo[256][3], hi[256][3];
-    const int c = blockIdx.x, t = threadIdx.x;
+    const int c = blockIdx.x / B, k = blockIdx.x % B, t = threadIdx.x;
     const int a0 = g.atom_off[c], n = g.atom_off[c + 1] - a0;
-    if (n == 0)
-        return;
-    const double *pts = wr + 3 * (size_t)a0;
-    double l[3] = {pts[0], pts[1], pts[2]}, h[3] = {pts[0], pts[1], pts[2]};
-    for (int i = t; i < n; i += 256)
+    const int m = (n + B - 1) / B;
+    const int i0 = min(n, k * m), i1 = min(n, i0 + m);
+    const bool wrap = g.wrap[c] != 0;
+    const Cell &cl = g.cell[c];
+    double l[3] = {__builtin_inf(), __builtin_inf(), __builtin_inf()};
+    double h[3] = {-__builtin_inf(), -__builtin_inf(), -__builtin_inf()};
+    for (int i = i0 + t; i < i1; i += 256) {
+        const size_t q = 3 * (size_t)(a0 + i);
+        double p[3] = {pos[q], pos[q + 1], pos[q + 2]};
+        if (wrap) {
+            double f[3];
+            dev_row_times(p, cl.inv, f);
+            f[0] -= floor(f[0]);
+            f[1] -= floor(f[1]);
+            f[2] -= floor(f[2]);
+            dev_row_times(f, cl.m, p);
+        }
 #pragma unroll
         for (int d = 0; d < 3; ++d) {
-            const double v = pts[3 * i + d];
-            l[d] = v < l[d] ? v : l[d];
-            h[d] = v > h[d] ? v : h[d];
+            wr[q + d] = p[d];
+            l[d] = p[d] < l[d] ? p[d] : l[d];
+            h[d] = p[d] > h[d] ? p[d] : h[d];
         }
+    }
 #pragma unroll
     for (int d = 0; d < 3; ++d) {
         lo[t][d] = l[d];
@@ -547,8 +607,8 @@ __global__ __launch_bounds__(256) void minmax_kernel(Seg g, const double *wr, do
         __syncthreads();
     }
     if (t < 3) {
-        out6[6 * (size_t)c + t] = lo[0][t];
-        out6[6 * (size_t)c + 3 + t] = hi[0][t];
+        part[6 * (size_t)blockIdx.x + t] = lo[0][t];
+        part[6 * (size_t)blockIdx.x + 3 + t] = hi[0][t];
     }
 }
 
@@ -707,17 +767,20 @@ struct Construct {
 
 // construct() (neighborhood.cpp:89-141) for one centre per wave.  MODE 0
 // counts the entries of every list, MODE 1 writes them with their keys.
-// The lanes test 64 candidates of a box at a time; an accepted candidate's
-// event number (its rank among the centre's accepted candidates in the
-// reference's traversal order) is the count so far plus the accepted lanes
-// below it, so the keys, and the lists they order, are those of the serial
-// traversal.  Ranks are global over a chunk, which keeps each structure's
-// order.
+// The candidates of the 27 neighbour boxes, taken in the reference's
+// traversal order (l1, l2, l3 from -1, then each box's points in order),
+// are numbered 0 .. total-1 and the lanes test 64 consecutive numbers at a
+// time; a lane finds its box by a branch-free binary search over the
+// boxes' running sizes (held by lanes 0..26).  An accepted candidate's
+// event number (its rank among the centre's accepted candidates in that
+// order) is the count so far plus the accepted lanes below it, so the
+// keys, and the lists they order, are those of the serial traversal.
+// Ranks are global over a chunk, which keeps each structure's order.
 template <int MODE>
 __global__ __launch_bounds__(256) void construct_kernel(Seg g, Construct cb, int *cnt,
-                                                              int *cursor, uint64_t *key,
-                                                              int *st_idx, int *st_type,
-                                                              double *st_vec, double *st_d)
+                                                        int *cursor, uint64_t *key, int *st_idx,
+                                                        int *st_type, double *st_vec,
+                                                        double *st_d)
 {
     const int lane = threadIdx.x & 63;
     const int a = blockIdx.x * (blockDim.x / 64) + threadIdx.x / 64;
@@ -733,59 +796,92 @@ __global__ __launch_bounds__(256) void construct_kernel(Seg g, Construct cb, int
                  pi2 = cb.pts[3 * (size_t)indi + 2];
     const uint64_t krank = (uint64_t)(unsigned)cb.rank[a] << 32;
     const uint64_t below = (1ull << lane) - 1;
+
+    // lane k < 27: the first point of box k and the running size of boxes 0..k
+    int first = 0, size = 0;
+    if (lane < 27) {
+        const int nb = box0 + ((bi + lane / 9 - 1) * bl1 + (bj + (lane / 3) % 3 - 1)) * bl2 +
+                       (bk + lane % 3 - 1);
+        first = cb.box_start[nb];
+        size = cb.box_start[nb + 1] - first;
+    }
+    int incl = size;
+#pragma unroll
+    for (int o = 1; o < 32; o <<= 1) {
+        const int v = __shfl_up(incl, o);
+        if (lane >= o)
+            incl += v;
+    }
+    const int excl = incl - size;
+    const int total = __shfl(incl, 26);
+
     unsigned ev = 0;
     int own = 0;
-    for (int l1 = -1; l1 <= 1; l1++)
-        for (int l2 = -1; l2 <= 1; l2++)
-            for (int l3 = -1; l3 <= 1; l3++) {
-                const int nb = box0 + ((bi + l1) * bl1 + (bj + l2)) * bl2 + (bk + l3);
-                const int t0 = cb.box_start[nb], t1 = cb.box_start[nb + 1];
-                for (int tb = t0; tb < t1; tb += 64) {
-                    const int t = tb + lane;
-                    bool ok = false;
-                    double r0 = 0.0, r1 = 0.0, r2 = 0.0, dijsq = 0.0;
-                    int oj = 0;
-                    if (t < t1) {
-                        const int indj = cb.items[t];
-                        r0 = cb.pts[3 * (size_t)indj] - pi0;
-                        r1 = cb.pts[3 * (size_t)indj + 1] - pi1;
-                        r2 = cb.pts[3 * (size_t)indj + 2] - pi2;
-                        dijsq = r0 * r0 + r1 * r1 + r2 * r2;
-                        oj = cb.orig[indj];
-                        ok = dijsq < cb.cutoffsq && indi != indj && a <= oj;
-                    }
-                    const uint64_t acc = __ballot(ok);
-                    if (ok) {
-                        if (MODE == 0) {
-                            if (a != oj)
-                                atomicAdd(&cnt[oj], 1);
-                        } else {
-                            const double dij = sqrt(dijsq);
-                            const uint64_t k = krank | (ev + (unsigned)__popcll(acc & below));
-                            int q = atomicAdd(&cursor[a], 1);
-                            key[q] = k;
-                            st_idx[q] = oj;
-                            st_type[q] = cb.types[oj];
-                            st_vec[3 * (int64_t)q] = r0;
-                            st_vec[3 * (int64_t)q + 1] = r1;
-                            st_vec[3 * (int64_t)q + 2] = r2;
-                            st_d[q] = dij;
-                            if (a != oj) {
-                                q = atomicAdd(&cursor[oj], 1);
-                                key[q] = k;
-                                st_idx[q] = a;
-                                st_type[q] = cb.types[a];
-                                st_vec[3 * (int64_t)q] = -r0;
-                                st_vec[3 * (int64_t)q + 1] = -r1;
-                                st_vec[3 * (int64_t)q + 2] = -r2;
-                                st_d[q] = dij;
-                            }
-                        }
-                    }
-                    ev += (unsigned)__popcll(acc);
-                    own += __popcll(acc);
+    for (int tb = 0; tb < total; tb += 64) {
+        const int f = tb + lane;
+        // box of candidate number f: the number of boxes whose running size is <= f
+        int k = 0;
+#pragma unroll
+        for (int step = 16; step >= 1; step >>= 1) {
+            const int probe = k + step - 1;
+            const int v = __shfl(incl, probe < 27 ? probe : 26);
+            if (probe < 27 && v <= f)
+                k += step;
+        }
+        const int kk = k < 27 ? k : 26;
+        const int t = __shfl(first, kk) + (f - __shfl(excl, kk));
+        bool ok = false;
+        double r0 = 0.0, r1 = 0.0, r2 = 0.0, dijsq = 0.0;
+        int oj = 0;
+        if (f < total) {
+            const int indj = cb.items[t];
+            r0 = cb.pts[3 * (size_t)indj] - pi0;
+            r1 = cb.pts[3 * (size_t)indj + 1] - pi1;
+            r2 = cb.pts[3 * (size_t)indj + 2] - pi2;
+            dijsq = r0 * r0 + r1 * r1 + r2 * r2;
+            oj = cb.orig[indj];
+            ok = dijsq < cb.cutoffsq && indi != indj && a <= oj;
+        }
+        const uint64_t acc = __ballot(ok);
+        // MODE 1: the accepted lanes' own entries take consecutive slots
+        // (one atomic per wave)
+        int own0 = 0;
+        if (MODE == 1 && acc) {
+            if (lane == 0)
+                own0 = atomicAdd(&cursor[a], __popcll(acc));
+            own0 = __shfl(own0, 0);
+        }
+        if (ok) {
+            if (MODE == 0) {
+                if (a != oj)
+                    atomicAdd(&cnt[oj], 1);
+            } else {
+                const double dij = sqrt(dijsq);
+                const int slot = __popcll(acc & below);
+                const uint64_t kv = krank | (ev + (unsigned)slot);
+                int q = own0 + slot;
+                key[q] = kv;
+                st_idx[q] = oj;
+                st_type[q] = cb.types[oj];
+                st_vec[3 * (int64_t)q] = r0;
+                st_vec[3 * (int64_t)q + 1] = r1;
+                st_vec[3 * (int64_t)q + 2] = r2;
+                st_d[q] = dij;
+                if (a != oj) {
+                    q = atomicAdd(&cursor[oj], 1);
+                    key[q] = kv;
+                    st_idx[q] = a;
+                    st_type[q] = cb.types[a];
+                    st_vec[3 * (int64_t)q] = -r0;
+                    st_vec[3 * (int64_t)q + 1] = -r1;
+                    st_vec[3 * (int64_t)q + 2] = -r2;
+                    st_d[q] = dij;
                 }
             }
+        }
+        ev += (unsigned)__popcll(acc);
+        own += __popcll(acc);
+    }
     if (MODE == 0 && lane == 0)
         atomicAdd(&cnt[a], own);
 }
@@ -805,6 +901,30 @@ hipError_t to_device(DBuf &b, const std::vector<T> &v, hipStream_t s)
     if (e == hipSuccess && !v.empty())
         e = hipMemcpyAsync(b.p, v.data(), sizeof(T) * v.size(), hipMemcpyHostToDevice, s);
     return e;
+}
+
+// Host tables packed into one upload: each table at a 16-byte aligned
+// offset of one buffer.
+struct Pack {
+    std::vector<unsigned char> bytes;
+    template <class T>
+    size_t add(const T *v, size_t n)
+    {
+        const size_t off = (bytes.size() + 15) & ~size_t(15);
+        bytes.resize(off + sizeof(T) * n);
+        if (n)
+            std::memcpy(bytes.data() + off, v, sizeof(T) * n);
+        return off;
+    }
+    template <class T>
+    size_t add(const std::vector<T> &v) { return add(v.data(), v.size()); }
+    hipError_t upload(DBuf &b, hipStream_t s) const { return to_device(b, bytes, s); }
+};
+
+template <class T>
+const T *at(const DBuf &b, size_t off)
+{
+    return reinterpret_cast<const T *>(static_cast<const unsigned char *>(b.p) + off);
 }
 
 hipError_t init_store(NeighborStore &st, int n, hipStream_t s)
@@ -865,11 +985,9 @@ int build_chunk(int c0, int c1, const int *atom_offsets, const double *cells, co
             return fail_at(c, "singular cell", MTPX_E_INVALID);
     }
     DTRY(w.scalars.ensure(sizeof(int) * 16));
-    std::vector<int> head(atom_off);
-    head.insert(head.end(), wrapf.begin(), wrapf.end());
-    DTRY(to_device(w.seg_atoms, head, s));
-    DTRY(w.seg_cells.ensure(sizeof(Cell) * nconf));
-    DTRY(hipMemcpyAsync(w.seg_cells.p, cl.data(), sizeof(Cell) * nconf, hipMemcpyHostToDevice, s));
+    Pack head;
+    const size_t o_atoms = head.add(atom_off), o_wrap = head.add(wrapf), o_cell = head.add(cl);
+    DTRY(head.upload(w.seg_head, s));
     DTRY(w.pos.ensure(sizeof(double) * 3 * (size_t)ntot));
     DTRY(w.types.ensure(sizeof(int) * (size_t)ntot));
     DTRY(hipMemcpyAsync(w.pos.p, pos, sizeof(double) * 3 * (size_t)ntot, hipMemcpyHostToDevice, s));
@@ -878,19 +996,35 @@ int build_chunk(int c0, int c1, const int *atom_offsets, const double *cells, co
                        w.types.as<int>(), ntot, out.center_type.as<int>());
     Seg g{};
     g.nconf = nconf;
-    g.atom_off = w.seg_atoms.as<int>();
-    g.wrap = w.seg_atoms.as<int>() + nconf + 1;
-    g.cell = static_cast<const Cell *>(w.seg_cells.p);
+    g.atom_off = at<int>(w.seg_head, o_atoms);
+    g.wrap = at<int>(w.seg_head, o_wrap);
+    g.cell = at<Cell>(w.seg_head, o_cell);
     DTRY(w.wrapped.ensure(sizeof(double) * 3 * (size_t)ntot));
-    DTRY(w.minmax.ensure(sizeof(double) * 6 * (size_t)nconf));
     double *wr = w.wrapped.as<double>();
-    hipLaunchKernelGGL(wrap_kernel, dim3(blocks(ntot, 256)), dim3(256), 0, s, g,
-                       w.pos.as<double>(), ntot, wr);
-    hipLaunchKernelGGL(minmax_kernel, dim3(nconf), dim3(256), 0, s, g, wr,
-                       w.minmax.as<double>());
-    std::vector<double> mm(6 * (size_t)nconf);
-    DTRY(hipMemcpyAsync(mm.data(), w.minmax.p, sizeof(double) * mm.size(), hipMemcpyDeviceToHost, s));
+    // workgroups per structure: about 2048 atoms each, at most 64
+    int nmax = 0;
+    for (int c = 0; c < nconf; ++c)
+        nmax = std::max(nmax, atom_off[c + 1] - atom_off[c]);
+    const int B = std::min(64, std::max(1, (nmax + 2047) / 2048));
+    DTRY(w.minmax.ensure(sizeof(double) * 6 * (size_t)nconf * B));
+    hipLaunchKernelGGL(wrap_minmax_kernel, dim3((unsigned)((size_t)nconf * B)), dim3(256), 0, s, g,
+                       w.pos.as<double>(), B, wr, w.minmax.as<double>());
+    std::vector<double> part(6 * (size_t)nconf * B), mm(6 * (size_t)nconf);
+    DTRY(hipMemcpyAsync(part.data(), w.minmax.p, sizeof(double) * part.size(),
+                        hipMemcpyDeviceToHost, s));
     DTRY(hipStreamSynchronize(s));
+    for (int c = 0; c < nconf; ++c)
+        for (int d = 0; d < 3; ++d) {
+            double l = part[6 * (size_t)c * B + d], h = part[6 * (size_t)c * B + 3 + d];
+            for (int k = 1; k < B; ++k) {
+                const double pl = part[6 * ((size_t)c * B + k) + d];
+                const double ph = part[6 * ((size_t)c * B + k) + 3 + d];
+                l = pl < l ? pl : l;
+                h = ph > h ? ph : h;
+            }
+            mm[6 * (size_t)c + d] = l;
+            mm[6 * (size_t)c + 3 + d] = h;
+        }
 
     // per structure: AABB with the extent fix, image candidates, boxes
     std::vector<SegGeom> geo((size_t)nconf);
@@ -959,21 +1093,17 @@ int build_chunk(int c0, int c1, const int *atom_offsets, const double *cells, co
     }
     const long long nflags = flag_off.back();
     const int nboxes = box_off.back(), nint = int_off.back();
-    std::vector<int> tabs(cand_off);
-    tabs.insert(tabs.end(), box_off.begin(), box_off.end());
-    tabs.insert(tabs.end(), int_off.begin(), int_off.end());
-    DTRY(to_device(w.seg_tabs, tabs, s));
-    DTRY(to_device(w.seg_flags, flag_off, s));
-    DTRY(w.seg_geo.ensure(sizeof(SegGeom) * nconf));
-    DTRY(hipMemcpyAsync(w.seg_geo.p, geo.data(), sizeof(SegGeom) * nconf, hipMemcpyHostToDevice,
-                        s));
-    DTRY(to_device(w.cand, cand, s));
-    g.cand_off = w.seg_tabs.as<int>();
-    g.box_off = g.cand_off + (nconf + 1);
-    g.int_off = g.box_off + (nconf + 1);
-    g.flag_off = w.seg_flags.as<long long>();
-    g.geo = static_cast<const SegGeom *>(w.seg_geo.p);
-    g.cand = w.cand.as<double>();
+    Pack tabs;
+    const size_t o_cand_off = tabs.add(cand_off), o_box_off = tabs.add(box_off),
+                 o_int_off = tabs.add(int_off), o_flag_off = tabs.add(flag_off),
+                 o_geo = tabs.add(geo.data(), (size_t)nconf), o_cand = tabs.add(cand);
+    DTRY(tabs.upload(w.seg_tabs, s));
+    g.cand_off = at<int>(w.seg_tabs, o_cand_off);
+    g.box_off = at<int>(w.seg_tabs, o_box_off);
+    g.int_off = at<int>(w.seg_tabs, o_int_off);
+    g.flag_off = at<long long>(w.seg_tabs, o_flag_off);
+    g.geo = at<SegGeom>(w.seg_tabs, o_geo);
+    g.cand = at<double>(w.seg_tabs, o_cand);
 
     // image flags, their scan and the image count of every structure
     std::vector<int> nimg((size_t)nconf, 0);
@@ -1096,16 +1226,11 @@ int build_chunk(int c0, int c1, const int *atom_offsets, const double *cells, co
     hipLaunchKernelGGL(construct_kernel<1>, dim3((ntot + 3) / 4), dim3(256), 0, s, g, cb,
                        nullptr, cnt, w.key.as<uint64_t>(), w.st_idx.as<int>(),
                        w.st_type.as<int>(), w.st_vec.as<double>(), w.st_d.as<double>());
-    DTRY(w.flags.ensure(sizeof(int) * Pz));
-    int *entry_list = w.flags.as<int>();
-    hipLaunchKernelGGL(entry_list_kernel, dim3(ntot), dim3(64), 0, s, out.offsets.as<int>(), ntot,
-                       entry_list);
-    hipLaunchKernelGGL(list_rank_kernel, dim3(blocks(P, 256)), dim3(256), 0, s,
-                       out.offsets.as<int>(), entry_list, P, w.key.as<uint64_t>(),
-                       w.st_idx.as<int>(), w.st_type.as<int>(), w.st_vec.as<double>(),
-                       w.st_d.as<double>(), out.idx.as<int>(), out.type.as<int>(),
-                       out.x.as<double>(), out.y.as<double>(), out.z.as<double>(),
-                       out.d.as<double>());
+    hipLaunchKernelGGL(list_rank_kernel, dim3((ntot + 3) / 4), dim3(256), 0, s,
+                       out.offsets.as<int>(), ntot, w.key.as<uint64_t>(), w.st_idx.as<int>(),
+                       w.st_type.as<int>(), w.st_vec.as<double>(), w.st_d.as<double>(),
+                       out.idx.as<int>(), out.type.as<int>(), out.x.as<double>(),
+                       out.y.as<double>(), out.z.as<double>(), out.d.as<double>());
     DTRY(hipGetLastError());
     DTRY(hipStreamSynchronize(s));
     return MTPX_OK;
