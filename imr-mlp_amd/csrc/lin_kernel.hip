@@ -2,7 +2,7 @@
 //
 //   lin_site_kernel   per site: the scalar moments (energy components) and,
 //                     for every neighbour entry, dm_s/dr_j of every scalar s
-//                     into a pair buffer (PotMTP::CalcEFSCmpt_R,
+//                     into a pair buffer, chunk-major (PotMTP::CalcEFSCmpt_R,
 //                     potentials/potential_mtp.cpp:2675-2707, over
 //                     CalcSiteBasisDers, :3163-3280)
 //   lin_gather_kernel force rows sum_j dm/dr_j - sum_{i: j of i} dm_i/dr_j
@@ -326,6 +326,19 @@ __device__ __forceinline__ void opaque(Nbr<MMAX> &q)
         asm volatile("" : "+v"(q.f[mu]), "+v"(q.fd[mu]));
 }
 
+// One entry's derivatives of a chunk as a block [3][kLinChunk] (component
+// a of scalar s0 + k at a kLinChunk + k; values past the chunk's scalars are
+// zero): 16-byte stores of consecutive addresses.
+__device__ __forceinline__ void store_block(double *blk, const double (&acc)[3 * kLinChunk])
+{
+#pragma unroll
+    for (int a = 0; a < 3; ++a)
+#pragma unroll
+        for (int k = 0; k < kLinChunk; k += 2)
+            *reinterpret_cast<double2 *>(blk + a * kLinChunk + k) =
+                make_double2(acc[3 * k + a], acc[3 * (k + 1) + a]);
+}
+
 template <class P, int kMaxWaves, class CP = void>
 __global__ __launch_bounds__(kWave *kMaxWaves) void lin_site_kernel(DevModel m, DevLin L,
                                                                     DevNeighbors nb, LinGroup g)
@@ -380,37 +393,30 @@ __global__ __launch_bounds__(kWave *kMaxWaves) void lin_site_kernel(DevModel m, 
         run_rules<false, false>(L.steps, L.level_step, L.level_comb, L.comb, L.nlev, ws, lane, 0);
 
         // ---- dm_s/dr_j of every entry, a chunk of scalars at a time, into
-        // the pair buffer [entry][3][Sp] (the lane's entry)
+        // the pair buffer [chunk][entry][3][kLinChunk] (the lane's entry:
+        // 24 contiguous values per chunk)
         for (int base = 0; base < n; base += kWave) {
             const bool valid = lane < n - base;
             const int64_t pe = beg + base + lane;
             Nbr<P::M> q;
             load_neighbor<P>(m, nb, Ls.coef, ti, pe, valid, q);
-            double *dst = g.pair + (size_t)(pe - g.e0) * 3 * g.Sp;
+            double *dst = g.pair + (size_t)(pe - g.e0) * kLinBlock;
             if constexpr (!std::is_void_v<CP>) {
                 // a run-time loop over the chunks (each chunk's walk is its
                 // own block: registers are allocated chunk by chunk)
                 for (int ch = 0; ch < CP::nchunks; ++ch) {
-                    const int s0 = L.chunk_s0[ch], nch = L.chunk_s0[ch + 1] - s0;
                     double acc[3 * kLinChunk];
 #pragma unroll
                     for (int r = 0; r < 3 * kLinChunk; ++r)
                         acc[r] = 0.0;
                     opaque(q);
                     lin_chunk_cp<CP, 0, P>(ch, q, ws, acc);
-                    if (valid) {
-#pragma unroll
-                        for (int a = 0; a < 3; ++a)
-#pragma unroll
-                            for (int k = 0; k < kLinChunk; ++k)
-                                if (k < nch)
-                                    dst[a * g.Sp + s0 + k] = acc[3 * k + a];
-                    }
+                    if (valid)
+                        store_block(dst + (size_t)ch * g.cstride, acc);
                 }
                 continue;
             }
             for (int ch = 0; ch < L.nchunks; ++ch) {
-                const int s0 = L.chunk_s0[ch], nch = L.chunk_s0[ch + 1] - s0;
                 LinWalk w;
                 w.pos = 0;
                 if constexpr (P::exact) {
@@ -429,14 +435,8 @@ __global__ __launch_bounds__(kWave *kMaxWaves) void lin_site_kernel(DevModel m, 
                 opaque(q);
                 int slot = 0;
                 lin_shells<0, P>(m, q, nullptr, slot, w, ws, acc);
-                if (valid) {
-#pragma unroll
-                    for (int a = 0; a < 3; ++a)
-#pragma unroll
-                        for (int k = 0; k < kLinChunk; ++k)
-                            if (k < nch)
-                                dst[a * g.Sp + s0 + k] = acc[3 * k + a];
-                }
+                if (valid)
+                    store_block(dst + (size_t)ch * g.cstride, acc);
             }
         }
         wave_sync();
@@ -444,55 +444,46 @@ __global__ __launch_bounds__(kWave *kMaxWaves) void lin_site_kernel(DevModel m, 
 }
 
 // Force rows and per-atom stress partials of a group from the pair buffer,
-// one thread per (atom, scalar), in a fixed order:
+// in a fixed order:
 //   fc[i][a][Z+s] = sum_{e in list(i)} D_e[a][s] - sum_{e: idx[e] = i} D_e[a][s]
 //   site[i][3a+b][s] = -sum_{e in list(i)} D_e[a][s] r_e[b]
+// One thread per atom and value v of the chunk blocks (v = 24 chunk + 8 a +
+// k, scalar chunk_s0[chunk] + k; gather_per threads per atom, whole
+// waves): consecutive lanes read consecutive doubles of an entry's blocks.
 __global__ __launch_bounds__(256) void lin_gather_kernel(int S, int Z, int p, DevNeighbors nb,
-                                                         const int *rev_off, const int *rev_pairs,
-                                                         LinGroup g, double *fc)
+                                                         const int *rev_off,
+                                                         const int *rev_pairs, LinGroup g,
+                                                         double *fc)
 {
     const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (t >= (int64_t)(g.a1 - g.a0) * S)
+    const int il = (int)(t / g.gather_per), v = (int)(t % g.gather_per);
+    if (il >= g.a1 - g.a0)
         return;
-    const int il = (int)(t / S), s = (int)(t % S);
+    const int ch = v / kLinBlock, rem = v % kLinBlock;
+    if (ch >= g.nchunks)
+        return;
+    const int a = rem / kLinChunk, s = g.chunk_s0[ch] + rem % kLinChunk;
+    if (s >= g.chunk_s0[ch + 1])
+        return;
     const int i = g.a0 + il;
-    const size_t st = 3 * (size_t)g.Sp;
-    const double *D = g.pair - (size_t)g.e0 * st + s;
-    double f0 = 0.0, f1 = 0.0, f2 = 0.0;
-    double sv[9];
-#pragma unroll
-    for (int q = 0; q < 9; ++q)
-        sv[q] = 0.0;
+    const double *D = g.pair - (size_t)g.e0 * kLinBlock + (size_t)ch * g.cstride + rem;
+    double f = 0.0, sv0 = 0.0, sv1 = 0.0, sv2 = 0.0;
 #pragma unroll 4
     for (int e = nb.offsets[i], e1 = nb.offsets[i + 1]; e < e1; ++e) {
-        const double *d = D + (size_t)e * st;
-        const double dx = d[0], dy = d[g.Sp], dz = d[2 * g.Sp];
-        const double r[3] = {nb.x[e], nb.y[e], nb.z[e]};
-        f0 += dx;
-        f1 += dy;
-        f2 += dz;
-#pragma unroll
-        for (int b = 0; b < 3; ++b) {
-            sv[b] -= dx * r[b];
-            sv[3 + b] -= dy * r[b];
-            sv[6 + b] -= dz * r[b];
-        }
+        const double d = D[(size_t)e * kLinBlock];
+        f += d;
+        sv0 -= d * nb.x[e];
+        sv1 -= d * nb.y[e];
+        sv2 -= d * nb.z[e];
     }
 #pragma unroll 4
-    for (int k = rev_off[i], k1 = rev_off[i + 1]; k < k1; ++k) {
-        const double *d = D + (size_t)rev_pairs[k] * st;
-        f0 -= d[0];
-        f1 -= d[g.Sp];
-        f2 -= d[2 * g.Sp];
-    }
-    double *f = fc + (size_t)i * 3 * p + Z + s;
-    f[0] = f0;
-    f[p] = f1;
-    f[2 * p] = f2;
+    for (int k = rev_off[i], k1 = rev_off[i + 1]; k < k1; ++k)
+        f -= D[(size_t)rev_pairs[k] * kLinBlock];
+    fc[(size_t)i * 3 * p + (size_t)a * p + Z + s] = f;
     double *srow = g.site + (size_t)il * 10 * S + s;
-#pragma unroll
-    for (int q = 0; q < 9; ++q)
-        srow[q * S] = sv[q];
+    srow[(size_t)(3 * a) * S] = sv0;
+    srow[(size_t)(3 * a + 1) * S] = sv1;
+    srow[(size_t)(3 * a + 2) * S] = sv2;
 }
 
 // Energy and stress components of a group's structures: ordered sums of the
@@ -647,7 +638,7 @@ hipError_t launch_lin_site(const DevModel &m, const DevLin &L, const DevNeighbor
 hipError_t launch_lin_gather(const DevModel &m, const DevNeighbors &nb, const int *rev_off,
                              const int *rev_pairs, const LinGroup &g, double *fc, hipStream_t s)
 {
-    const int64_t work = (int64_t)(g.a1 - g.a0) * m.S;
+    const int64_t work = (int64_t)(g.a1 - g.a0) * g.gather_per;
     if (work > 0)
         hipLaunchKernelGGL(lin_gather_kernel, dim3((unsigned)((work + 255) / 256)), dim3(256), 0,
                            s, m.S, m.Z, m.Z + m.S, nb, rev_off, rev_pairs, g, fc);

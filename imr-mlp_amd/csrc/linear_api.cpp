@@ -62,8 +62,7 @@ int run_lin(mtpx_context *ctx)
         return rc;
     const DevModel &m = ctx->dm;
     const int S = m.S;
-    const int Sp = (S + kLinChunk - 1) / kLinChunk * kLinChunk;
-    const size_t per_entry = sizeof(double) * 3 * (size_t)Sp;
+    const size_t per_entry = sizeof(double) * kLinBlock * (size_t)ctx->dl.nchunks;
     const std::vector<int> &off = ctx->offsets_host;
     const size_t budget = pair_budget();
 
@@ -98,7 +97,10 @@ int run_lin(mtpx_context *ctx)
         g.a0 = ctx->soff_host[r.c0];
         g.a1 = ctx->soff_host[r.c1];
         g.e0 = off[g.a0];
-        g.Sp = Sp;
+        g.cstride = (int64_t)kLinBlock * (int64_t)max_entries;
+        g.nchunks = ctx->dl.nchunks;
+        g.gather_per = (kLinBlock * g.nchunks + kWave - 1) / kWave * kWave;
+        g.chunk_s0 = ctx->dl.chunk_s0;
         g.pair = ctx->lin_pair.as<double>();
         g.site = ctx->lin_site.as<double>();
         if (g.a1 > g.a0) {

@@ -393,12 +393,17 @@ struct DevLin {
 };
 // One group of whole structures for the linear-fit kernels: atoms
 // [a0, a1), structures [c0, c1), entries from e0; pair buffer
-// [entries][3][Sp] (Sp = S rounded up to the chunk), site rows
+// [nchunks][entries][3][kLinChunk] (a plane of cstride doubles per chunk of
+// scalars, chunk c holding scalars chunk_s0[c] ..), site rows
 // [a1 - a0][10][S] (9 stress partials, then the scalar moments).
+constexpr int kLinBlock = 3 * kLinChunk;  // doubles per entry and chunk
 struct LinGroup {
     int a0, a1, c0, c1;
     int64_t e0;
-    int Sp;
+    int64_t cstride;
+    int nchunks;
+    int gather_per;       // gather threads per atom: 24 nchunks rounded up to a wave
+    const int *chunk_s0;  // [nchunks + 1]
     double *pair;
     double *site;
 };
