@@ -326,17 +326,26 @@ __device__ __forceinline__ void opaque(Nbr<MMAX> &q)
         asm volatile("" : "+v"(q.f[mu]), "+v"(q.fd[mu]));
 }
 
-// One entry's derivatives of a chunk as a block [3][kLinChunk] (component
-// a of scalar s0 + k at a kLinChunk + k; values past the chunk's scalars are
-// zero): 16-byte stores of consecutive addresses.
-__device__ __forceinline__ void store_block(double *blk, const double (&acc)[3 * kLinChunk])
+// Width of chunk c's rows in the pair buffer: its scalar count rounded up
+// to even (16-byte stores).
+__device__ __forceinline__ int chunk_width(const int *chunk_s0, int c)
+{
+    return (chunk_s0[c + 1] - chunk_s0[c] + 1) & ~1;
+}
+
+// One entry's derivatives of a chunk as a block [3][w] (component a of
+// scalar s0 + k at a w + k; w even, a padding value is zero): 16-byte stores
+// of consecutive addresses.
+__device__ __forceinline__ void store_block(double *blk, int w,
+                                            const double (&acc)[3 * kLinChunk])
 {
 #pragma unroll
     for (int a = 0; a < 3; ++a)
 #pragma unroll
         for (int k = 0; k < kLinChunk; k += 2)
-            *reinterpret_cast<double2 *>(blk + a * kLinChunk + k) =
-                make_double2(acc[3 * k + a], acc[3 * (k + 1) + a]);
+            if (k < w)
+                *reinterpret_cast<double2 *>(blk + a * w + k) =
+                    make_double2(acc[3 * k + a], acc[3 * (k + 1) + a]);
 }
 
 template <class P, int kMaxWaves, class CP = void>
@@ -393,18 +402,19 @@ __global__ __launch_bounds__(kWave *kMaxWaves) void lin_site_kernel(DevModel m, 
         run_rules<false, false>(L.steps, L.level_step, L.level_comb, L.comb, L.nlev, ws, lane, 0);
 
         // ---- dm_s/dr_j of every entry, a chunk of scalars at a time, into
-        // the pair buffer [chunk][entry][3][kLinChunk] (the lane's entry:
-        // 24 contiguous values per chunk)
+        // the pair buffer [chunk][entry][3][w] (the lane's entry: 3 w
+        // contiguous values per chunk)
         for (int base = 0; base < n; base += kWave) {
             const bool valid = lane < n - base;
             const int64_t pe = beg + base + lane;
             Nbr<P::M> q;
             load_neighbor<P>(m, nb, Ls.coef, ti, pe, valid, q);
-            double *dst = g.pair + (size_t)(pe - g.e0) * kLinBlock;
+            const size_t el = (size_t)(pe - g.e0);
             if constexpr (!std::is_void_v<CP>) {
                 // a run-time loop over the chunks (each chunk's walk is its
                 // own block: registers are allocated chunk by chunk)
-                for (int ch = 0; ch < CP::nchunks; ++ch) {
+                for (int ch = 0, boff = 0; ch < CP::nchunks; ++ch) {
+                    const int w = chunk_width(L.chunk_s0, ch);
                     double acc[3 * kLinChunk];
 #pragma unroll
                     for (int r = 0; r < 3 * kLinChunk; ++r)
@@ -412,11 +422,13 @@ __global__ __launch_bounds__(kWave *kMaxWaves) void lin_site_kernel(DevModel m, 
                     opaque(q);
                     lin_chunk_cp<CP, 0, P>(ch, q, ws, acc);
                     if (valid)
-                        store_block(dst + (size_t)ch * g.cstride, acc);
+                        store_block(g.pair + (size_t)boff * g.pg + el * 3 * w, w, acc);
+                    boff += 3 * w;
                 }
                 continue;
             }
-            for (int ch = 0; ch < L.nchunks; ++ch) {
+            for (int ch = 0, boff = 0; ch < L.nchunks; ++ch) {
+                const int cw = chunk_width(L.chunk_s0, ch);
                 LinWalk w;
                 w.pos = 0;
                 if constexpr (P::exact) {
@@ -436,7 +448,8 @@ __global__ __launch_bounds__(kWave *kMaxWaves) void lin_site_kernel(DevModel m, 
                 int slot = 0;
                 lin_shells<0, P>(m, q, nullptr, slot, w, ws, acc);
                 if (valid)
-                    store_block(dst + (size_t)ch * g.cstride, acc);
+                    store_block(g.pair + (size_t)boff * g.pg + el * 3 * cw, cw, acc);
+                boff += 3 * cw;
             }
         }
         wave_sync();
@@ -447,9 +460,10 @@ __global__ __launch_bounds__(kWave *kMaxWaves) void lin_site_kernel(DevModel m, 
 // in a fixed order:
 //   fc[i][a][Z+s] = sum_{e in list(i)} D_e[a][s] - sum_{e: idx[e] = i} D_e[a][s]
 //   site[i][3a+b][s] = -sum_{e in list(i)} D_e[a][s] r_e[b]
-// One thread per atom and value v of the chunk blocks (v = 24 chunk + 8 a +
-// k, scalar chunk_s0[chunk] + k; gather_per threads per atom, whole
-// waves): consecutive lanes read consecutive doubles of an entry's blocks.
+// One thread per atom and value v of an entry's chunk blocks (v runs over
+// the blocks [3][w] of the chunks in order; gather_per threads per atom,
+// whole waves): consecutive lanes read consecutive doubles of an entry's
+// blocks.
 __global__ __launch_bounds__(256) void lin_gather_kernel(int S, int Z, int p, DevNeighbors nb,
                                                          const int *rev_off,
                                                          const int *rev_pairs, LinGroup g,
@@ -459,18 +473,26 @@ __global__ __launch_bounds__(256) void lin_gather_kernel(int S, int Z, int p, De
     const int il = (int)(t / g.gather_per), v = (int)(t % g.gather_per);
     if (il >= g.a1 - g.a0)
         return;
-    const int ch = v / kLinBlock, rem = v % kLinBlock;
-    if (ch >= g.nchunks)
-        return;
-    const int a = rem / kLinChunk, s = g.chunk_s0[ch] + rem % kLinChunk;
+    // the chunk of value v, its row width and the plane offset (doubles
+    // per entry of the chunks before it)
+    int ch = 0, rem = v, boff = 0, w = chunk_width(g.chunk_s0, 0);
+    while (rem >= 3 * w) {
+        rem -= 3 * w;
+        boff += 3 * w;
+        if (++ch >= g.nchunks)
+            return;
+        w = chunk_width(g.chunk_s0, ch);
+    }
+    const int a = rem / w, s = g.chunk_s0[ch] + rem % w;
     if (s >= g.chunk_s0[ch + 1])
         return;
+    const int bw = 3 * w;
     const int i = g.a0 + il;
-    const double *D = g.pair - (size_t)g.e0 * kLinBlock + (size_t)ch * g.cstride + rem;
+    const double *D = g.pair + (size_t)boff * g.pg - (size_t)g.e0 * bw + rem;
     double f = 0.0, sv0 = 0.0, sv1 = 0.0, sv2 = 0.0;
 #pragma unroll 4
     for (int e = nb.offsets[i], e1 = nb.offsets[i + 1]; e < e1; ++e) {
-        const double d = D[(size_t)e * kLinBlock];
+        const double d = D[(size_t)e * bw];
         f += d;
         sv0 -= d * nb.x[e];
         sv1 -= d * nb.y[e];
@@ -478,7 +500,7 @@ __global__ __launch_bounds__(256) void lin_gather_kernel(int S, int Z, int p, De
     }
 #pragma unroll 4
     for (int k = rev_off[i], k1 = rev_off[i + 1]; k < k1; ++k)
-        f -= D[(size_t)rev_pairs[k] * kLinBlock];
+        f -= D[(size_t)rev_pairs[k] * bw];
     fc[(size_t)i * 3 * p + (size_t)a * p + Z + s] = f;
     double *srow = g.site + (size_t)il * 10 * S + s;
     srow[(size_t)(3 * a) * S] = sv0;

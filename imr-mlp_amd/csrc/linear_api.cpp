@@ -62,7 +62,13 @@ int run_lin(mtpx_context *ctx)
         return rc;
     const DevModel &m = ctx->dm;
     const int S = m.S;
-    const size_t per_entry = sizeof(double) * kLinBlock * (size_t)ctx->dl.nchunks;
+    // doubles per entry of the pair buffer: 3 w_c per chunk (linear_api and
+    // lin_kernel agree on w_c = scalar count rounded up to even)
+    const std::vector<int> &cs0 = ctx->lin.chunk_s0;
+    size_t row = 0;
+    for (size_t c = 0; c + 1 < cs0.size(); ++c)
+        row += 3 * (size_t)((cs0[c + 1] - cs0[c] + 1) & ~1);
+    const size_t per_entry = sizeof(double) * row;
     const std::vector<int> &off = ctx->offsets_host;
     const size_t budget = pair_budget();
 
@@ -97,9 +103,9 @@ int run_lin(mtpx_context *ctx)
         g.a0 = ctx->soff_host[r.c0];
         g.a1 = ctx->soff_host[r.c1];
         g.e0 = off[g.a0];
-        g.cstride = (int64_t)kLinBlock * (int64_t)max_entries;
+        g.pg = (int64_t)max_entries;
         g.nchunks = ctx->dl.nchunks;
-        g.gather_per = (kLinBlock * g.nchunks + kWave - 1) / kWave * kWave;
+        g.gather_per = (int)((row + kWave - 1) / kWave * kWave);
         g.chunk_s0 = ctx->dl.chunk_s0;
         g.pair = ctx->lin_pair.as<double>();
         g.site = ctx->lin_site.as<double>();

@@ -393,14 +393,14 @@ struct DevLin {
 };
 // One group of whole structures for the linear-fit kernels: atoms
 // [a0, a1), structures [c0, c1), entries from e0; pair buffer
-// [nchunks][entries][3][kLinChunk] (a plane of cstride doubles per chunk of
-// scalars, chunk c holding scalars chunk_s0[c] ..), site rows
+// [nchunks][entries][3][w_c] (chunk c holds scalars chunk_s0[c] .. and rows
+// of w_c = its scalar count rounded up to even; the plane of chunk c starts
+// at pg 3 sum_{c' < c} w_c', pg entries per plane), site rows
 // [a1 - a0][10][S] (9 stress partials, then the scalar moments).
-constexpr int kLinBlock = 3 * kLinChunk;  // doubles per entry and chunk
 struct LinGroup {
     int a0, a1, c0, c1;
     int64_t e0;
-    int64_t cstride;
+    int64_t pg;
     int nchunks;
     int gather_per;       // gather threads per atom: 24 nchunks rounded up to a wave
     const int *chunk_s0;  // [nchunks + 1]
