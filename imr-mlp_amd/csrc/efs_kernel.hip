@@ -42,7 +42,7 @@ namespace mtpx {
 
 namespace {
 
-template <class P, bool kTabLds, int kMaxWaves>
+template <class P, bool kTabLds, int kMaxWaves, bool kHead>
 __global__ __launch_bounds__(kWave *kMaxWaves) void efs_kernel(DevModel m, DevNeighbors nb,
                                                                EfsOut out, int flags)
 {
@@ -103,7 +103,7 @@ __global__ __launch_bounds__(kWave *kMaxWaves) void efs_kernel(DevModel m, DevNe
         // (an MTP-M head: the head of the descriptors, its seeds per atom)
         double e = 0.0;
         const bool energy_only = flags & kEfsEnergyOnly;
-        if (m.head) {
+        if constexpr (kHead) {
             const int w0 = (int)(ws - lds);
             e = head_site(m.hd, ti, w0, w0 + m.efs_head, w0 + m.K4, lane, !energy_only);
         } else {
@@ -118,7 +118,7 @@ __global__ __launch_bounds__(kWave *kMaxWaves) void efs_kernel(DevModel m, DevNe
         }
         if (energy_only)  // getE (potential_mtp.cpp:2604-2621): no gradient
             continue;
-        if (!m.head)  // (a head has written its seeds)
+        if constexpr (!kHead)  // (a head has written its seeds)
             for (int k = lane; k < m.K; k += kWave)
                 A[k] = L.seed[k];
         wave_sync();
@@ -362,13 +362,24 @@ template <class P>
 void launch_variant(const DevModel &m, const DevNeighbors &nb, const EfsOut &out,
                     const EfsLaunch &cfg, int det, hipStream_t s)
 {
+    // MTP-M heads get kernels of their own: a linear model's kernel holds no
+    // call of the out-of-line head (a call site costs registers and a stack)
     constexpr int W = VariantWaves<P>::value;
-    if (cfg.lds_tables)
-        hipLaunchKernelGGL((efs_kernel<P, true, W>), dim3(cfg.grid), dim3(kWave * cfg.waves),
-                           cfg.lds_bytes, s, m, nb, out, det);
-    else
-        hipLaunchKernelGGL((efs_kernel<P, false, W>), dim3(cfg.grid), dim3(kWave * cfg.waves),
-                           cfg.lds_bytes, s, m, nb, out, det);
+    const dim3 grid(cfg.grid), block(kWave * cfg.waves);
+    if (m.head) {
+        if (cfg.lds_tables)
+            hipLaunchKernelGGL((efs_kernel<P, true, W, true>), grid, block, cfg.lds_bytes, s, m,
+                               nb, out, det);
+        else
+            hipLaunchKernelGGL((efs_kernel<P, false, W, true>), grid, block, cfg.lds_bytes, s, m,
+                               nb, out, det);
+    } else if (cfg.lds_tables) {
+        hipLaunchKernelGGL((efs_kernel<P, true, W, false>), grid, block, cfg.lds_bytes, s, m, nb,
+                           out, det);
+    } else {
+        hipLaunchKernelGGL((efs_kernel<P, false, W, false>), grid, block, cfg.lds_bytes, s, m, nb,
+                           out, det);
+    }
 }
 
 int variant_max_waves(int v)
