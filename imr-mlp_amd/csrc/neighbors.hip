@@ -58,10 +58,10 @@ __device__ __forceinline__ void dev_row_times(const double *p, const double *M, 
 
 // Place each point at box_start[b] + (number of points of box b with a smaller
 // index): the first pass drops points in any order, the second ranks them.
-__global__ void box_place_kernel(const int *box, int npts, int *box_cur, int *items)
+__global__ void box_place_kernel(const int *box, const int *npts, int *box_cur, int *items)
 {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= npts)
+    if (i >= *npts)
         return;
     const int q = atomicAdd(&box_cur[box[i]], 1);
     items[q] = i;
@@ -69,11 +69,11 @@ __global__ void box_place_kernel(const int *box, int npts, int *box_cur, int *it
 
 // One thread per point: its slot in its box is the number of the box's
 // points with a smaller index (a box of a small cell can hold every point).
-__global__ void box_rank_kernel(const int *box, const int *box_start, int npts,
+__global__ void box_rank_kernel(const int *box, const int *box_start, const int *npts,
                                 const int *unsorted, int *items)
 {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= npts)
+    if (i >= *npts)
         return;
     const int b = box[i];
     const int s = box_start[b], e = box_start[b + 1];
@@ -188,7 +188,7 @@ __global__ __launch_bounds__(1024) void scan_sums(int *sums, int ntiles, int *to
 }
 
 __global__ __launch_bounds__(kScanBlock) void scan_tiles(const int *in, int64_t n,
-                                                          const int *sums, int *out)
+                                                          const int *sums, int *out, int *out2)
 {
     __shared__ int buf[kScanBlock];
     const int64_t base = (int64_t)blockIdx.x * kScanTile + (int64_t)threadIdx.x * kScanItems;
@@ -208,8 +208,11 @@ __global__ __launch_bounds__(kScanBlock) void scan_tiles(const int *in, int64_t 
     }
     int run = sums[blockIdx.x] + buf[threadIdx.x] - s;
     for (int k = 0; k < kScanItems; ++k) {
-        if (base + k < n)
+        if (base + k < n) {
             out[base + k] = run;
+            if (out2)
+                out2[base + k] = run;
+        }
         run += v[k];
     }
 }
@@ -243,7 +246,8 @@ __global__ __launch_bounds__(256) void sum64_kernel(const int *in, int64_t n,
 constexpr int kScan1Waves = 16, kScan1Max = kScan1Waves * 64 * 64;
 
 __global__ __launch_bounds__(kScan1Waves * 64) void scan_one_block(const int *in, int n, int m,
-                                                                   int *out, int *total)
+                                                                   int *out, int *out2,
+                                                                   int *total)
 {
     __shared__ int wsum[kScan1Waves];
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
@@ -273,22 +277,27 @@ __global__ __launch_bounds__(kScan1Waves * 64) void scan_one_block(const int *in
             if (lane >= o)
                 x += u;
         }
-        if (i < n)
+        if (i < n) {
             out[i] = carry + x - v;
+            if (out2)
+                out2[i] = carry + x - v;
+        }
         carry += __shfl(x, 63);
     }
     if (threadIdx.x == kScan1Waves * 64 - 1)
         *total = carry;
 }
 
-// Exclusive scan; *total receives the sum (device), returns the error.
+// Exclusive scan into out (and out2 when given, which may be in: every
+// value is read before its slot is written); *total receives the sum
+// (device); returns the error.
 hipError_t scan_exclusive(const int *in, int64_t n, int *out, DBuf &tmp, int *total,
-                          hipStream_t s)
+                          hipStream_t s, int *out2 = nullptr)
 {
     if (n <= kScan1Max) {
         const int m = (int)std::max<int64_t>(1, (n + kScan1Waves * 64 - 1) / (kScan1Waves * 64));
         hipLaunchKernelGGL(scan_one_block, dim3(1), dim3(kScan1Waves * 64), 0, s, in, (int)n, m,
-                           out, total);
+                           out, out2, total);
         return hipGetLastError();
     }
     const int64_t ntiles = std::max<int64_t>(1, (n + kScanTile - 1) / kScanTile);
@@ -299,7 +308,7 @@ hipError_t scan_exclusive(const int *in, int64_t n, int *out, DBuf &tmp, int *to
                        tmp.as<int>());
     hipLaunchKernelGGL(scan_sums, dim3(1), dim3(1024), 0, s, tmp.as<int>(), (int)ntiles, total);
     hipLaunchKernelGGL(scan_tiles, dim3((unsigned)ntiles), dim3(kScanBlock), 0, s, in, n,
-                       tmp.as<int>(), out);
+                       tmp.as<int>(), out, out2);
     return hipGetLastError();
 }
 
@@ -521,8 +530,10 @@ hipError_t launch_site_prepare(int nrows, const int *offsets, const int *center_
 // offsets.  Points are numbered structure by structure (originals, then
 // images), atoms and list entries over the chunk, so the lists come out as
 // the structures' own lists concatenated with chunk-wide atom indices.  A
-// single structure is a chunk of one.  Three host synchronisations per
-// chunk: the AABBs, the image counts and the entry total.
+// single structure is a chunk of one.  Two host synchronisations per chunk,
+// the AABBs and the entry total (point counts and offsets stay on the
+// device), and a third for the point total where the bound on the points
+// would need large new buffers.
 namespace {
 
 struct SegGeom {      // per structure, after the AABB
@@ -633,20 +644,37 @@ __global__ void image_flag_kernel(Seg g, const double *wr, long long total, int 
     flags[k] = out ? 0 : 1;
 }
 
-// images of each structure: the flags' exclusive scan at its end less at its start
-__global__ void image_count_kernel(Seg g, const int *flags, const int *scan, int *nimg)
+// points of each structure: its atoms and its images (the flags' exclusive
+// scan at its end less at its start); entry nconf is 0, so an exclusive scan
+// gives the point offsets and the point total
+__global__ void point_count_kernel(Seg g, const int *flags, const int *scan, int *count)
 {
     const int c = blockIdx.x * blockDim.x + threadIdx.x;
-    if (c >= g.nconf)
+    if (c > g.nconf)
         return;
+    if (c == g.nconf) {
+        count[c] = 0;
+        return;
+    }
     const long long f0 = g.flag_off[c], f1 = g.flag_off[c + 1];
-    nimg[c] = f1 == f0 ? 0 : scan[f1 - 1] + flags[f1 - 1] - scan[f0];
+    const int nimg = f1 == f0 ? 0 : scan[f1 - 1] + flags[f1 - 1] - scan[f0];
+    count[c] = g.atom_off[c + 1] - g.atom_off[c] + nimg;
 }
 
-// originals: point pt_off[c] + i is atom a0 + i
-__global__ void points_kernel(Seg g, const double *wr, int ntot, double *pts, int *orig)
+// originals: point pt_off[c] + i is atom a0 + i; the grid also clears the
+// box counters [nz1] and the list counters [nz2] and *z64 for the launches
+// after it (fewer launches than separate fills)
+__global__ void points_kernel(Seg g, const double *wr, int ntot, double *pts, int *orig, int *z1,
+                              int nz1, int *z2, int nz2, unsigned long long *z64)
 {
     const int a = blockIdx.x * blockDim.x + threadIdx.x;
+    const int stride = gridDim.x * blockDim.x;
+    for (int k = a; k < nz1; k += stride)
+        z1[k] = 0;
+    for (int k = a; k < nz2; k += stride)
+        z2[k] = 0;
+    if (a == 0)
+        *z64 = 0;
     if (a >= ntot)
         return;
     const int c = seg_of(g.atom_off, g.nconf, a);
@@ -679,11 +707,10 @@ __global__ void image_write_kernel(Seg g, const double *wr, long long total,
 
 // Box index (neighborhoods_base.h:179-224): ceil(tp * (bl - 2) / xd), originals
 // clamped into [1, bl-2], images into [0, bl-1]; boxes numbered globally.
-__global__ void box_index_kernel(Seg g, const double *pts, int npts, int *box,
-                                       int *box_count)
+__global__ void box_index_kernel(Seg g, const double *pts, int *box, int *box_count)
 {
     const int p = blockIdx.x * blockDim.x + threadIdx.x;
-    if (p >= npts)
+    if (p >= g.pt_off[g.nconf])
         return;
     const int c = seg_of(g.pt_off, g.nconf, p);
     const int n = g.atom_off[c + 1] - g.atom_off[c];
@@ -891,6 +918,9 @@ __global__ __launch_bounds__(256) void construct_kernel(Seg g, Construct cb, int
 // boxes and interior boxes (the chunk ends early at the structure that would
 // pass them), so every point, box and flag index fits in int32.
 constexpr int kChunkAtoms = 1 << 21;
+// Point buffers sized by the bound ntot + nflags up to this many points
+// (24 MB of positions) without reading the image total back.
+constexpr long long kPointBound = 1 << 20;
 constexpr long long kChunkFlags = INT_MAX / 4;
 constexpr long long kChunkBoxes = INT_MAX / 4;
 
@@ -1105,59 +1135,65 @@ int build_chunk(int c0, int c1, const int *atom_offsets, const double *cells, co
     g.geo = at<SegGeom>(w.seg_tabs, o_geo);
     g.cand = at<double>(w.seg_tabs, o_cand);
 
-    // image flags, their scan and the image count of every structure
-    std::vector<int> nimg((size_t)nconf, 0);
-    DTRY(w.seg_imgs.ensure(sizeof(int) * nconf));
+    // image flags, their scan, and the point offsets on the device.  The
+    // point buffers and grids take the bound ntot + nflags when it is small
+    // or already allocated (no host synchronisation for the image counts;
+    // threads past the device total exit), else the total read back.
+    long long npts_max = (long long)ntot + nflags;  // < 2^30 by the chunk budgets
+    const bool bound = npts_max <= kPointBound || w.pts.bytes >= sizeof(double) * 3 * npts_max;
+    DTRY(w.flags.ensure(sizeof(int) * (size_t)std::max<long long>(nflags, 1)));
     if (nflags > 0) {
-        DTRY(w.flags.ensure(sizeof(int) * (size_t)nflags));
         DTRY(w.scan.ensure(sizeof(int) * (size_t)nflags));
         hipLaunchKernelGGL(image_flag_kernel, dim3(blocks(nflags, 256)), dim3(256), 0, s, g,
                            wr, nflags, w.flags.as<int>());
         DTRY(scan_exclusive(w.flags.as<int>(), nflags, w.scan.as<int>(), w.box_cur,
-                            w.scalars.as<int>() ? w.scalars.as<int>() : nullptr, s));
-        hipLaunchKernelGGL(image_count_kernel, dim3(blocks(nconf, 256)), dim3(256), 0, s, g,
-                           w.flags.as<int>(), w.scan.as<int>(), w.seg_imgs.as<int>());
-        DTRY(hipMemcpyAsync(nimg.data(), w.seg_imgs.p, sizeof(int) * nconf, hipMemcpyDeviceToHost, s));
-        DTRY(hipStreamSynchronize(s));
+                            w.scalars.as<int>(), s));
     }
-    std::vector<int> pt_off(1, 0);
-    for (int c = 0; c < nconf; ++c) {
-        const long long next = (long long)pt_off.back() + (atom_off[c + 1] - atom_off[c]) + nimg[c];
-        if (next > INT_MAX / 2)
-            return fail_at(c, "batch has too many points", MTPX_E_CAPACITY);
-        pt_off.push_back((int)next);
-    }
-    const int npts = pt_off.back();
-    DTRY(to_device(w.seg_pts, pt_off, s));
+    DTRY(w.seg_imgs.ensure(sizeof(int) * ((size_t)nconf + 1)));
+    DTRY(w.seg_pts.ensure(sizeof(int) * ((size_t)nconf + 1)));
+    hipLaunchKernelGGL(point_count_kernel, dim3(blocks(nconf + 1, 256)), dim3(256), 0, s, g,
+                       w.flags.as<int>(), w.scan.as<int>(), w.seg_imgs.as<int>());
+    DTRY(scan_exclusive(w.seg_imgs.as<int>(), (int64_t)nconf + 1, w.seg_pts.as<int>(), w.tmp,
+                        w.scalars.as<int>(), s));
     g.pt_off = w.seg_pts.as<int>();
-    DTRY(w.pts.ensure(sizeof(double) * 3 * (size_t)npts));
-    DTRY(w.orig.ensure(sizeof(int) * (size_t)npts));
-    hipLaunchKernelGGL(points_kernel, dim3(blocks(ntot, 256)), dim3(256), 0, s, g,
-                       wr, ntot, w.pts.as<double>(), w.orig.as<int>());
+    const int *npts = g.pt_off + nconf;  // device
+    if (!bound) {
+        int np = 0;
+        DTRY(hipMemcpyAsync(&np, npts, sizeof(int), hipMemcpyDeviceToHost, s));
+        DTRY(hipStreamSynchronize(s));
+        npts_max = np;
+    }
+    DTRY(w.pts.ensure(sizeof(double) * 3 * (size_t)npts_max));
+    DTRY(w.orig.ensure(sizeof(int) * (size_t)npts_max));
+    DTRY(w.cnt.ensure(sizeof(int) * ((size_t)nboxes + 1)));
+    DTRY(w.cursor.ensure(sizeof(int) * ((size_t)ntot + 1)));
+    int *box_count = w.cnt.as<int>();
+    int *cnt = w.cursor.as<int>();
+    unsigned long long *total64 = reinterpret_cast<unsigned long long *>(w.scalars.as<int>() + 8);
+    hipLaunchKernelGGL(points_kernel, dim3(blocks(ntot, 256)), dim3(256), 0, s, g, wr, ntot,
+                       w.pts.as<double>(), w.orig.as<int>(), box_count, nboxes + 1, cnt, ntot + 1,
+                       total64);
     if (nflags > 0)
         hipLaunchKernelGGL(image_write_kernel, dim3(blocks(nflags, 256)), dim3(256), 0, s,
                            g, wr, nflags, w.flags.as<int>(), w.scan.as<int>(),
                            w.pts.as<double>(), w.orig.as<int>());
 
     // boxes: counts, starts, stable placement
-    DTRY(w.box.ensure(sizeof(int) * (size_t)npts));
+    DTRY(w.box.ensure(sizeof(int) * (size_t)npts_max));
     DTRY(w.box_start.ensure(sizeof(int) * ((size_t)nboxes + 1)));
     DTRY(w.box_cur.ensure(sizeof(int) * ((size_t)nboxes + 1)));
-    DTRY(w.box_items.ensure(sizeof(int) * (size_t)npts));
-    DTRY(w.cnt.ensure(sizeof(int) * ((size_t)nboxes + 1)));
-    DTRY(w.flags.ensure(sizeof(int) * std::max<size_t>((size_t)npts, 1)));
-    int *box_count = w.cnt.as<int>();
-    DTRY(hipMemsetAsync(box_count, 0, sizeof(int) * ((size_t)nboxes + 1), s));
-    hipLaunchKernelGGL(box_index_kernel, dim3(blocks(npts, 256)), dim3(256), 0, s, g,
-                       w.pts.as<double>(), npts, w.box.as<int>(), box_count);
+    DTRY(w.box_items.ensure(sizeof(int) * (size_t)npts_max));
+    hipLaunchKernelGGL(box_index_kernel, dim3(blocks(npts_max, 256)), dim3(256), 0, s, g,
+                       w.pts.as<double>(), w.box.as<int>(), box_count);
     DTRY(scan_exclusive(box_count, (int64_t)nboxes + 1, w.box_start.as<int>(), w.tmp,
-                        w.scalars.as<int>(), s));
-    DTRY(hipMemcpyAsync(w.box_cur.p, w.box_start.p, sizeof(int) * ((size_t)nboxes + 1),
-                        hipMemcpyDeviceToDevice, s));
+                        w.scalars.as<int>(), s, w.box_cur.as<int>()));
+    // the image flags are dead after image_write_kernel: their buffer takes
+    // the unsorted placement (growing it waits for the queued work)
+    DTRY(w.flags.ensure(sizeof(int) * (size_t)std::max<long long>(npts_max, 1)));
     int *unsorted = w.flags.as<int>();
-    hipLaunchKernelGGL(box_place_kernel, dim3(blocks(npts, 256)), dim3(256), 0, s,
+    hipLaunchKernelGGL(box_place_kernel, dim3(blocks(npts_max, 256)), dim3(256), 0, s,
                        w.box.as<int>(), npts, w.box_cur.as<int>(), unsorted);
-    hipLaunchKernelGGL(box_rank_kernel, dim3(blocks(npts, 256)), dim3(256), 0, s,
+    hipLaunchKernelGGL(box_rank_kernel, dim3(blocks(npts_max, 256)), dim3(256), 0, s,
                        w.box.as<int>(), w.box_start.as<int>(), npts, unsorted,
                        w.box_items.as<int>());
 
@@ -1187,17 +1223,13 @@ int build_chunk(int c0, int c1, const int *atom_offsets, const double *cells, co
     cb.centre_box = centre_box;
     cb.ntot = ntot;
     cb.cutoffsq = cutoff * cutoff;
-    DTRY(w.cursor.ensure(sizeof(int) * ((size_t)ntot + 1)));
-    int *cnt = w.cursor.as<int>();
-    DTRY(hipMemsetAsync(cnt, 0, sizeof(int) * ((size_t)ntot + 1), s));
     hipLaunchKernelGGL(construct_kernel<0>, dim3((ntot + 3) / 4), dim3(256), 0, s, g, cb,
                        cnt, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr);
-    unsigned long long *total64 = reinterpret_cast<unsigned long long *>(w.scalars.as<int>() + 8);
-    DTRY(hipMemsetAsync(total64, 0, sizeof *total64, s));
     hipLaunchKernelGGL(sum64_kernel, dim3(std::min<unsigned>(blocks(ntot, 256), 1024)), dim3(256),
                        0, s, cnt, (int64_t)ntot, total64);
+    // the offsets, and the same values over the counts as the fill cursors
     DTRY(scan_exclusive(cnt, (int64_t)ntot + 1, out.offsets.as<int>(), w.tmp, w.scalars.as<int>(),
-                        s));
+                        s, cnt));
     unsigned long long P64 = 0;
     DTRY(hipMemcpyAsync(&P64, total64, sizeof P64, hipMemcpyDeviceToHost, s));
     DTRY(hipStreamSynchronize(s));
@@ -1222,7 +1254,6 @@ int build_chunk(int c0, int c1, const int *atom_offsets, const double *cells, co
     DTRY(w.st_type.ensure(sizeof(int) * Pz));
     DTRY(w.st_vec.ensure(sizeof(double) * 3 * Pz));
     DTRY(w.st_d.ensure(sizeof(double) * Pz));
-    DTRY(hipMemcpyAsync(cnt, out.offsets.p, sizeof(int) * (size_t)ntot, hipMemcpyDeviceToDevice, s));
     hipLaunchKernelGGL(construct_kernel<1>, dim3((ntot + 3) / 4), dim3(256), 0, s, g, cb,
                        nullptr, cnt, w.key.as<uint64_t>(), w.st_idx.as<int>(),
                        w.st_type.as<int>(), w.st_vec.as<double>(), w.st_d.as<double>());
