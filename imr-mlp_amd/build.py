@@ -33,6 +33,7 @@ SOURCES = [
     ("efs_kernel.hip", ["-ffp-contract=fast"]),
     ("train_kernel.hip", ["-ffp-contract=fast"]),
     ("lin_kernel.hip", ["-ffp-contract=fast"]),
+    ("lin_kernel.hip", ["-ffp-contract=fast", "-DMTPX_LIN_PART=2"], "lin_kernel_part2"),
     ("gram_kernel.hip", ["-ffp-contract=fast"]),
     ("neighbors.hip", ["-ffp-contract=off"]),
     ("geometry.cpp", ["-ffp-contract=off"]),
@@ -48,7 +49,15 @@ SOURCES = [
 
 
 def sources():
-    return [(s, f) for s, f in SOURCES if os.path.exists(os.path.join(CSRC, s))]
+    """(source, flags, object name) of every translation unit; a source may
+    be compiled more than once under different names."""
+    out = []
+    for e in SOURCES:
+        src, flags = e[0], e[1]
+        name = e[2] if len(e) > 2 else src
+        if os.path.exists(os.path.join(CSRC, src)):
+            out.append((src, flags, name))
+    return out
 
 
 def _newest_header() -> float:
@@ -65,8 +74,8 @@ def build(verbose: bool = False, changed_only: bool = False) -> str:
     objs, cmds = [], []
     t0 = time.time()
     newest_h = _newest_header()
-    for src, flags in sources():
-        obj = os.path.join(OBJ_DIR, src + ".o")
+    for src, flags, name in sources():
+        obj = os.path.join(OBJ_DIR, name + ".o")
         objs.append(obj)
         if changed_only and os.path.exists(obj):
             t_obj = os.path.getmtime(obj)

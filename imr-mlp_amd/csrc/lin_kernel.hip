@@ -21,9 +21,18 @@
 // form dm_s/dr_j = sum_b L[s][b] grad_r(f_b Y_b)(r_j) for a chunk of
 // scalars at a time.  Structures are processed in groups whose pair buffer
 // fits a fixed budget.
+//
+// The file is compiled twice (two objects, so the two halves of the longest
+// compile run in parallel): MTPX_LIN_PART 2 holds the site kernels of the
+// compiled level-16 walk and of level 20 (launch_lin_site_part2); the
+// default part holds everything else.
 #include "mtp_device.hpp"
 
 #include <type_traits>
+
+#ifndef MTPX_LIN_PART
+#define MTPX_LIN_PART 1
+#endif
 
 namespace mtpx {
 namespace {
@@ -456,6 +465,7 @@ __global__ __launch_bounds__(kWave *kMaxWaves) void lin_site_kernel(DevModel m, 
     }
 }
 
+#if MTPX_LIN_PART == 1
 // Force rows and per-atom stress partials of a group from the pair buffer,
 // in a fixed order:
 //   fc[i][a][Z+s] = sum_{e in list(i)} D_e[a][s] - sum_{e: idx[e] = i} D_e[a][s]
@@ -568,20 +578,19 @@ __global__ __launch_bounds__(256) void rows_kernel(const double *comp, const int
 
 // Waves per workgroup: the level-10 kernel fits 256 registers (eight waves);
 // the others use up to 512 (one wave per SIMD).
+#endif  // MTPX_LIN_PART == 1
+
 template <class P>
-struct LinWaves {
-    static constexpr int value = 4;
-};
-template <>
-struct LinWaves<ProfLevel10> {
-    static constexpr int value = 8;
-};
+constexpr int lin_waves()
+{
+    return std::is_same_v<P, ProfLevel10> ? 8 : 4;
+}
 
 template <class P, class CP = void>
 void launch_lin_variant(const DevModel &m, const DevLin &L, const DevNeighbors &nb,
                         const LinGroup &g, const EfsLaunch &cfg, hipStream_t s)
 {
-    constexpr int W = LinWaves<P>::value;
+    constexpr int W = lin_waves<P>();
     hipLaunchKernelGGL((lin_site_kernel<P, W, CP>), dim3(cfg.grid), dim3(kWave * cfg.waves),
                        cfg.lds_bytes, s, m, L, nb, g);
 }
@@ -590,6 +599,23 @@ static_assert(exact_slot_count<ProfLevel16>() == LinPlanLevel16::nslots,
               "the compiled level-16 walk must cover the level-16 profile's slots");
 
 }  // namespace
+
+#if MTPX_LIN_PART == 2
+// variant 5 (level 16, compiled walk) and 1 (level 20)
+void launch_lin_site_part2(int variant, const DevModel &m, const DevLin &L,
+                           const DevNeighbors &nb, const LinGroup &g, const EfsLaunch &cfg,
+                           hipStream_t s)
+{
+    if (variant == 5)
+        launch_lin_variant<ProfLevel16, LinPlanLevel16>(m, L, nb, g, cfg, s);
+    else
+        launch_lin_variant<ProfLevel20>(m, L, nb, g, cfg, s);
+}
+#else
+// in the other object of this file
+void launch_lin_site_part2(int variant, const DevModel &m, const DevLin &L,
+                           const DevNeighbors &nb, const LinGroup &g, const EfsLaunch &cfg,
+                           hipStream_t s);
 
 // The E/F/S variant, or the generic one where the compile-time walk's
 // tables do not hold the plan; 5: the level-16 profile with the compiled
@@ -646,10 +672,10 @@ hipError_t launch_lin_site(const DevModel &m, const DevLin &L, const DevNeighbor
 {
     if (g.a1 <= g.a0)
         return hipSuccess;
-    switch (lin_variant(m, L)) {
+    switch (const int v = lin_variant(m, L)) {
     case 0: launch_lin_variant<ProfLevel16>(m, L, nb, g, cfg, s); break;
-    case 5: launch_lin_variant<ProfLevel16, LinPlanLevel16>(m, L, nb, g, cfg, s); break;
-    case 1: launch_lin_variant<ProfLevel20>(m, L, nb, g, cfg, s); break;
+    case 1:
+    case 5: launch_lin_site_part2(v, m, L, nb, g, cfg, s); break;
     case 2: launch_lin_variant<ProfLevel10>(m, L, nb, g, cfg, s); break;
     case 3: launch_lin_variant<ProfSmall>(m, L, nb, g, cfg, s); break;
     default: launch_lin_variant<ProfGeneric>(m, L, nb, g, cfg, s); break;
@@ -687,4 +713,5 @@ hipError_t launch_lin_rows(const double *comp, const int64_t *src, const double 
     return hipGetLastError();
 }
 
+#endif  // MTPX_LIN_PART
 }  // namespace mtpx
