@@ -242,9 +242,11 @@ def test_linear_after_orthogonalize(ctx, crystal_set):
 
 
 def test_level10_and_runtime_profile_models(ctx):
-    """Level-10 (compile-time profile) and a model on the runtime profile."""
+    """Level-10 and level-20 (compile-time profiles; the level-20 site kernel
+    lives in the second object of lin_kernel.hip) and a model on the runtime
+    profile."""
     rng = S.rng_for(77)
-    for name, R in [("shapeev-10.mtp", 8), ("shapeev-16.mtp", 6)]:
+    for name, R in [("shapeev-10.mtp", 8), ("shapeev-20.mtp", 10), ("shapeev-16.mtp", 6)]:
         text = S.random_model(name, 2, R, 1.9, 5.0, -0.1, 0.1, rng)
         m = O.Model(text)
         s = S.displace(S.lattice("fcc", (3, 3, 3), 3.56), rng, 0.1)
