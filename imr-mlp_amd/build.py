@@ -39,6 +39,7 @@ SOURCES = [
     ("geometry.cpp", ["-ffp-contract=off"]),
     ("model.cpp", ["-ffp-contract=off"]),
     ("capi.cpp", ["-ffp-contract=off"]),
+    ("model_view.cpp", ["-ffp-contract=off"]),
     ("train_api.cpp", ["-ffp-contract=off"]),
     ("linear_api.cpp", ["-ffp-contract=off"]),
     ("sites.cpp", ["-ffp-contract=off"]),

@@ -25,6 +25,7 @@
 #include "mtpx.h"
 
 #include <algorithm>
+#include <climits>
 #include <cmath>
 #include <cstdio>
 #include <cstdlib>
@@ -93,7 +94,7 @@ bool read_config(std::istream &is, Config &c, int index)
         die(where + "missing Size");
     {
         auto t = split(line);
-        if (t.empty() || !number(t[0], v) || v < 0 || v != std::floor(v))
+        if (t.empty() || !number(t[0], v) || v < 0 || v != std::floor(v) || v > INT_MAX)
             die(where + "invalid Size");
         c.n = (int)v;
     }

@@ -282,6 +282,12 @@ int install_model(mtpx_context *ctx, Model &&m)
     int rc = upload_coeffs(ctx);
     if (rc != MTPX_OK)
         return rc;
+    // a new model starts with the identity species map over [0, Z)
+    ctx->spmap.resize((size_t)M.Z);
+    for (int t = 0; t < M.Z; ++t)
+        ctx->spmap[t] = t;
+    ctx->max_type = M.Z;
+    ctx->spmap_set = false;
     ctx->has_lin = lin_ok;
     ctx->has_model = true;
     return MTPX_OK;
@@ -290,6 +296,29 @@ int install_model(mtpx_context *ctx, Model &&m)
 }  // namespace
 
 namespace mtpx {
+
+int map_species(mtpx_context *ctx, const int *types, size_t n, bool allow_unmapped,
+                std::vector<int> &buf, const int *&out)
+{
+    out = types;
+    if (!ctx->has_model || !ctx->spmap_set || n == 0)
+        return MTPX_OK;
+    buf.resize(n);
+    for (size_t i = 0; i < n; ++i) {
+        const int t = types[i];
+        // the requests' type checks (mtp_gpu_direct.cu:9454, 9510)
+        if (t < 0 || t >= ctx->max_type)
+            return set_error(ctx, MTPX_E_INVALID, "atom type is outside the species-map range");
+        const int sp = ctx->spmap[t];
+        if (sp < 0 && !allow_unmapped)
+            return set_error(ctx, MTPX_E_INVALID,
+                             "atom type " + std::to_string(t) +
+                                 " maps to species -1; only site requests skip such atoms");
+        buf[i] = sp;
+    }
+    out = buf.data();
+    return MTPX_OK;
+}
 
 DevNeighbors dev_neighbors(const mtpx_context *ctx)
 {
@@ -524,37 +553,45 @@ int mtpx_load_model(mtpx_context *ctx, const mtpx_model_view *v)
 {
     if (!ctx || !v)
         return set_error(ctx, MTPX_E_INVALID, "null argument");
-    if (v->species_count <= 0 || v->radial_func_count <= 0 || v->rb_size <= 0 ||
-        v->alpha_index_basic_count <= 0 || v->alpha_moments_count <= 0 ||
-        v->alpha_index_times_count < 0 || v->alpha_scalar_moments < 0 || !v->alpha_index_basic ||
-        (v->alpha_index_times_count > 0 && !v->alpha_index_times) ||
-        (v->alpha_scalar_moments > 0 && (!v->alpha_moment_mapping || !v->moment_coeffs)) ||
-        !v->radial_coeffs || !v->species_coeffs)
-        return set_error(ctx, MTPX_E_INVALID, "incomplete model view");
     Model m;
-    m.Z = v->species_count;
-    m.M = v->radial_func_count;
-    m.R = v->rb_size;
-    m.rmin = v->min_dist;
-    m.rmax = v->max_dist;
-    m.scaling = v->scaling;
-    RadialBasis rb;
-    rb.rmin = v->min_dist;
-    rb.rmax = v->max_dist;
-    rb.scaling = v->scaling;
-    m.bases.assign(1, rb);
-    m.K = v->alpha_moments_count;
-    m.B = v->alpha_index_basic_count;
-    m.T = v->alpha_index_times_count;
-    m.S = v->alpha_scalar_moments;
-    m.basic.assign(v->alpha_index_basic, v->alpha_index_basic + 4 * m.B);
-    m.times.assign(v->alpha_index_times, v->alpha_index_times + 4 * m.T);
-    m.map.assign(v->alpha_moment_mapping, v->alpha_moment_mapping + m.S);
-    m.coef.assign(v->radial_coeffs, v->radial_coeffs + m.nradial());
-    m.coef.insert(m.coef.end(), v->species_coeffs, v->species_coeffs + m.Z);
-    m.coef.insert(m.coef.end(), v->moment_coeffs, v->moment_coeffs + m.S);
+    std::vector<int> spmap;
+    int code = MTPX_OK;
+    std::string err;
+    if (!model_from_view(*v, m, spmap, code, err))
+        return set_error(ctx, code, err);
     (void)hipSetDevice(ctx->device);
-    return install_model(ctx, std::move(m));
+    if (int rc = install_model(ctx, std::move(m)))
+        return rc;
+    ctx->spmap = std::move(spmap);
+    ctx->max_type = v->max_type;
+    ctx->spmap_set = true;
+    return MTPX_OK;
+}
+
+int mtpx_set_species_map(mtpx_context *ctx, int max_type, const int *spmap)
+{
+    if (!ctx)
+        return MTPX_E_INVALID;
+    if (!ctx->has_model)
+        return set_error(ctx, MTPX_E_NO_MODEL, "no model loaded");
+    const int Z = ctx->model.Z;
+    if (!spmap) {
+        ctx->spmap.resize((size_t)Z);
+        for (int t = 0; t < Z; ++t)
+            ctx->spmap[t] = t;
+        ctx->max_type = Z;
+        ctx->spmap_set = false;
+        return MTPX_OK;
+    }
+    if (max_type <= 0)
+        return set_error(ctx, MTPX_E_INVALID, "invalid max_type/spmap");
+    for (int t = 0; t < max_type; ++t)
+        if (spmap[t] < -1 || spmap[t] >= Z)
+            return set_error(ctx, MTPX_E_INVALID, "species mapping is outside [-1, species_count)");
+    ctx->spmap.assign(spmap, spmap + max_type);
+    ctx->max_type = max_type;
+    ctx->spmap_set = true;
+    return MTPX_OK;
 }
 
 int mtpx_load_model_text(mtpx_context *ctx, const char *text)
@@ -836,6 +873,11 @@ int mtpx_set_neighbors(mtpx_context *ctx, int n, const int *offsets, const int *
     const int64_t P = offsets[n];
     if (P > 0 && (!indices || !types || !vecs || !dists))
         return set_error(ctx, MTPX_E_INVALID, "invalid neighbour arrays");
+    std::vector<int> tbuf, cbuf;
+    if (int rc = map_species(ctx, types, (size_t)P, false, tbuf, types))
+        return rc;
+    if (int rc = map_species(ctx, center_types, (size_t)n, false, cbuf, center_types))
+        return rc;
     int Z = ctx->has_model ? ctx->model.Z : 1 << 30;
     for (int64_t p = 0; p < P; ++p) {
         if (indices[p] < 0 || indices[p] >= n)
@@ -892,6 +934,9 @@ int mtpx_build_neighbors(mtpx_context *ctx, const double cell[9], const int pbc[
     for (int i = 0; i < 3 * n; ++i)
         if (!std::isfinite(pos[i]))
             return set_error(ctx, MTPX_E_INVALID, "non-finite position");
+    std::vector<int> tbuf;
+    if (int rc = map_species(ctx, types, (size_t)n, false, tbuf, types))
+        return rc;
     const int Z = ctx->has_model ? ctx->model.Z : 1 << 30;
     int maxs = -1;
     for (int i = 0; i < n; ++i) {

@@ -18,6 +18,12 @@ struct mtpx_context {
 
     bool has_model = false;
     Model model;
+    // MTPGpuPotentialView::spmap: caller types [0, max_type) -> species
+    // [-1, Z); the identity over [0, Z) unless a view or mtpx_set_species_map
+    // set one (spmap_set)
+    std::vector<int> spmap;
+    int max_type = 0;
+    bool spmap_set = false;
     Plan plan;
     DevModel dm{};
     // model buffers
@@ -162,6 +168,20 @@ inline int need_linear(mtpx_context *ctx, const char *what)
                                              "potential has an MTP-M head)");
     return MTPX_OK;
 }
+
+// MTPGpuPotentialView -> host model and species map (model_view.cpp), with
+// validate_potential_view's checks; on failure code and err are set.
+bool model_from_view(const mtpx_model_view &v, Model &m, std::vector<int> &spmap, int &code,
+                     std::string &err);
+
+// Caller atom types -> species through the loaded model's species map.
+// Without an explicit map (text or GPM loads) `out` is `types` itself and
+// nothing is checked here.  With one, every type must lie in [0, max_type)
+// ("atom type is outside the species-map range", as the reference's
+// requests); allow_unmapped keeps species -1 (site requests skip such
+// atoms), otherwise a type mapped to -1 is refused.
+int map_species(mtpx_context *ctx, const int *types, size_t n, bool allow_unmapped,
+                std::vector<int> &buf, const int *&out);
 
 inline int hip_fail(mtpx_context *ctx, hipError_t e, const char *what)
 {

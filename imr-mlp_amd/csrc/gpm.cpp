@@ -27,6 +27,7 @@
 #include <cstring>
 #include <map>
 #include <set>
+#include <stdexcept>
 #include <string>
 #include <vector>
 
@@ -279,9 +280,14 @@ struct Reader {
         return it->second;
     }
 
+    // Reader::read's default limit (tools/gpm_container.h:512-515): neither
+    // size of a block may pass 8 GiB, checked before anything is allocated.
+    static constexpr uint64_t kReadLimit = uint64_t(8) << 30;
+
     Bytes read(const std::string &id) const
     {
         const Block &b = info(id);
+        require(b.raw <= kReadLimit && b.stored <= kReadLimit, "block exceeds read limit: " + id);
         require(b.codec == "none" || b.codec == "zstd", "unsupported codec " + b.codec);
         const unsigned char *s = p + data + b.offset;
         if (b.codec == "none")
@@ -606,6 +612,9 @@ bool gpm_read(const void *bytes, size_t n, std::string &out, std::vector<double>
     } catch (const GpmError &e) {
         err = e.msg;
         return false;
+    } catch (const std::exception &e) {
+        err = std::string("GPM: ") + e.what();
+        return false;
     }
 }
 
@@ -722,6 +731,9 @@ bool gpm_write(const Model &m, int zstd_level, std::string &out, std::string &er
         return true;
     } catch (const GpmError &e) {
         err = e.msg;
+        return false;
+    } catch (const std::exception &e) {
+        err = std::string("GPM: ") + e.what();
         return false;
     }
 }

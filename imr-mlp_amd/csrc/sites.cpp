@@ -148,7 +148,13 @@ int mtpx_compute_sites(mtpx_context *ctx, const mtpx_site_request *req)
         return set_error(ctx, MTPX_E_INVALID, "null argument");
     if (!ctx->has_model)
         return set_error(ctx, MTPX_E_NO_MODEL, "no model loaded");
-    const mtpx_site_request &r = *req;
+    // atom types through the species map; species -1 is skipped below
+    mtpx_site_request mapped = *req;
+    std::vector<int> tbuf;
+    if (req->ntotal > 0 && req->type)
+        if (int rc = map_species(ctx, req->type, (size_t)req->ntotal, true, tbuf, mapped.type))
+            return rc;
+    const mtpx_site_request &r = mapped;
     auto &S = ctx->sites;
     const int64_t P_in = r.center_count > 0 && r.offsets ? r.offsets[r.center_count] : 0;
     // reuse_topology: the same counts (the reference rebuilds when atom or
@@ -158,6 +164,11 @@ int mtpx_compute_sites(mtpx_context *ctx, const mtpx_site_request *req)
     std::vector<int> rows;
     if (int rc = check_request(ctx, r, !reuse, rows))
         return rc;
+    // the kept centres changed: the topology is packed again from the
+    // caller's offsets and neighbours, which are then checked in full
+    if (reuse && rows != S.row_src)
+        if (int rc = check_request(ctx, r, true, rows))
+            return rc;
     (void)hipSetDevice(ctx->device);
     if (!reuse || rows != S.row_src)
         if (int rc = upload_topology(ctx, r, rows))

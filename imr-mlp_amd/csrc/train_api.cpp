@@ -201,6 +201,9 @@ int mtpx_set_structures(mtpx_context *ctx, int nconf, const int *atom_offsets,
         return set_error(ctx, MTPX_E_INVALID, "non-finite cell");
     if (!finite_all(pos, 3 * (size_t)N))
         return set_error(ctx, MTPX_E_INVALID, "non-finite position");
+    std::vector<int> tbuf;
+    if (int rc = map_species(ctx, types, (size_t)N, false, tbuf, types))
+        return rc;
     const int Z = ctx->has_model ? ctx->model.Z : 1 << 30;
     int maxs = -1;
     for (int i = 0; i < N; ++i) {

@@ -109,8 +109,106 @@ def lib():
                                              C.POINTER(C.c_size_t), C.c_char_p, C.c_int]
         L.mtpx_efs_noalloc.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p]
         L.mtpx_compute_sites.argtypes = [C.c_void_p, C.POINTER(SiteRequest)]
+        L.mtpx_load_model.argtypes = [C.c_void_p, C.POINTER(ModelView)]
+        L.mtpx_format_model_view.argtypes = [C.POINTER(ModelView), C.c_char_p, C.c_size_t,
+                                             C.POINTER(C.c_size_t), C.c_char_p, C.c_int]
+        L.mtpx_set_species_map.argtypes = [C.c_void_p, C.c_int, _ip]
         _lib = L
     return _lib
+
+
+# Enum values of a model view: RadialBasis, RadialCutoff, RadialTransform,
+# MTPGpuModel and MTPGpuActivation of the reference's GPU runtime
+# (runtime/mtp/gpu-direct/mtp_gpu_direct.h:152-213).
+RB_KINDS = {"RBChebyshev": 0, "RBChebyCos": 1, "RBChebyshevPoly5": 2,
+            "RBChebyshevConfigurable": 3, "RBChebyshevPoly4": 4, "RBPolyB": 5, "RBPolyBCos": 6}
+CUTOFFS = {"quadratic": 0, "cosine": 1, "poly5": 2, "normalized_quadratic": 3,
+           "cosine_left": 4, "cosine_unscaled": 5, "cosine_squared": 6, "sine_squared": 7,
+           "poly3": 8, "poly4": 9, "smoothstep5": 10, "smoothstep7": 11}
+SHIFTS = {"linear": 0, "exponential": 1, "exponential_left": 2, "i2": 3, "exponential_tanh": 4}
+VIEW_MODELS = {"linear": 0, "mtp_m_q2": 1, "mtp_m_fs": 2, "mtp_m_n1": 3, "mtp_m_n2": 4,
+               "mtp_m_li": 5}
+VIEW_ACTIVATIONS = {"TANH": 0, "RELU": 1, "SIGMOID": 2, "LINEAR": 3}
+
+
+class RadialBasisView(C.Structure):
+    """mtpx_radial_basis_view (MTPGpuRadialBasisView)."""
+    _fields_ = [("radial_basis", C.c_int), ("min_dist", C.c_double), ("max_dist", C.c_double),
+                ("scaling", C.c_double), ("cutoff", C.c_int), ("transform", C.c_int),
+                ("cutoff_parameter", C.c_double), ("transform_parameter", C.c_double),
+                ("one_minus_chebyshev", C.c_int), ("cutoff_r1", C.c_double),
+                ("cutoff_r2", C.c_double), ("transform_scale_parameter", C.c_double),
+                ("polynomial_matrix", _dp), ("polynomial_normalizations", _dp)]
+
+
+class ModelView(C.Structure):
+    """mtpx_model_view (MTPGpuPotentialView), field for field."""
+    _fields_ = [("species_count", C.c_int), ("max_type", C.c_int), ("spmap", _ip),
+                ("alpha_moments_count", C.c_int), ("alpha_index_basic_count", C.c_int),
+                ("alpha_index_times_count", C.c_int), ("alpha_scalar_moments", C.c_int),
+                ("radial_func_count", C.c_int), ("rb_size", C.c_int), ("max_mu", C.c_int),
+                ("max_alpha_index_basic", C.c_int), ("min_dist", C.c_double),
+                ("max_dist", C.c_double), ("cutoff", C.c_double), ("scaling", C.c_double),
+                ("radial_basis", C.c_int),
+                ("pair_radial_bases", C.POINTER(RadialBasisView)),
+                ("pair_radial_basis_count", C.c_int), ("radial_coeffs", _dp),
+                ("radial_coeffs_count", C.c_int), ("species_coeffs", _dp),
+                ("moment_coeffs", _dp), ("model", C.c_int), ("descriptor_count", C.c_int),
+                ("scalar_gather", C.c_int), ("input_mean", _dp), ("input_inverse_std", _dp),
+                ("input_species", _dp), ("descriptor_species_coeffs", _dp),
+                ("descriptor_moment_coeffs", _dp), ("model_coeffs", _dp),
+                ("model_coeffs_count", C.c_int), ("model_activation", C.c_int),
+                ("model_hidden1", C.c_int), ("model_hidden2", C.c_int),
+                ("alpha_index_basic", _ip), ("alpha_index_times", _ip),
+                ("alpha_moment_mapping", _ip), ("nu_arr_list", _ip)]
+
+
+def make_view(fields: dict, pair_bases=None):
+    """A ModelView from plain values and numpy arrays (kept alive on the
+    returned object as `_keep`).  Array fields are converted to contiguous
+    int32 / float64; pair_bases is a list of dicts of RadialBasisView
+    fields (or None)."""
+    keep = []
+    v = ModelView()
+    for name, ctype in ModelView._fields_:
+        if name not in fields or fields[name] is None or name == "pair_radial_bases":
+            continue
+        val = fields[name]
+        if ctype is _ip:
+            a = np.ascontiguousarray(val, np.int32)
+            keep.append(a)
+            setattr(v, name, a.ctypes.data_as(_ip))
+        elif ctype is _dp:
+            a = np.ascontiguousarray(val, np.float64)
+            keep.append(a)
+            setattr(v, name, a.ctypes.data_as(_dp))
+        else:
+            setattr(v, name, val)
+    if pair_bases:
+        arr = (RadialBasisView * len(pair_bases))()
+        for k, b in enumerate(pair_bases):
+            for name, val in b.items():
+                setattr(arr[k], name, val)
+        keep.append(arr)
+        v.pair_radial_bases = C.cast(arr, C.POINTER(RadialBasisView))
+        v.pair_radial_basis_count = len(pair_bases)
+    v._keep = keep
+    return v
+
+
+def format_model_view(view: ModelView) -> str:
+    """mtpx_format_model_view: the .mtp text of the model a view describes
+    (host only)."""
+    n = C.c_size_t()
+    err = C.create_string_buffer(512)
+    rc = lib().mtpx_format_model_view(C.byref(view), None, 0, C.byref(n), err, 512)
+    if rc != OK:
+        raise MtpxError(rc, err.value.decode())
+    buf = C.create_string_buffer(n.value + 1)
+    rc = lib().mtpx_format_model_view(C.byref(view), buf, n.value + 1, C.byref(n), err, 512)
+    if rc != OK:
+        raise MtpxError(rc, err.value.decode())
+    return buf.value.decode()
 
 
 class SiteRequest(C.Structure):
@@ -359,6 +457,22 @@ class Context:
         self._check(lib().mtpx_model_info(self.h, _i(info)), "model_info")
         self.info = dict(zip(["Z", "M", "R", "K", "B", "T", "S", "ncoef"], [int(v) for v in info]))
         return self.info
+
+    def load_model_view(self, view: ModelView):
+        """mtpx_load_model (MTPGpuDirect::initialize over a view)."""
+        self._check(lib().mtpx_load_model(self.h, C.byref(view)), "load_model")
+        info = np.zeros(8, np.int32)
+        self._check(lib().mtpx_model_info(self.h, _i(info)), "model_info")
+        self.info = dict(zip(["Z", "M", "R", "K", "B", "T", "S", "ncoef"], [int(v) for v in info]))
+        return self.info
+
+    def set_species_map(self, spmap=None):
+        """mtpx_set_species_map: caller types -> species (None: identity)."""
+        if spmap is None:
+            self._check(lib().mtpx_set_species_map(self.h, 0, None), "set_species_map")
+            return
+        a = np.ascontiguousarray(spmap, np.int32)
+        self._check(lib().mtpx_set_species_map(self.h, a.size, _i(a)), "set_species_map")
 
     def load_model_gpm(self, data: bytes):
         self._check(lib().mtpx_load_model_gpm(self.h, data, len(data)), "load_model_gpm")

@@ -35,25 +35,138 @@ extern "C" {
 
 typedef struct mtpx_context mtpx_context;
 
-/* Flat model view: the linear-MTP / RBChebyshev subset of
- * MTPGpuPotentialView (runtime/mtp/gpu-direct/mtp_gpu_direct.h:239-289).
- * Arrays are borrowed for the call and copied. */
+/* Radial basis kinds, cutoffs and coordinate transforms of a model view, with
+ * the values of the reference's RadialBasis, RadialCutoff and RadialTransform
+ * (runtime/mtp/gpu-direct/mtp_gpu_direct.h:152-190). */
+#define MTPX_RB_CHEBYSHEV 0
+#define MTPX_RB_CHEBYCOS 1
+#define MTPX_RB_CHEBYSHEV_POLY5 2
+#define MTPX_RB_CHEBYSHEV_CONFIGURABLE 3
+#define MTPX_RB_CHEBYSHEV_POLY4 4
+#define MTPX_RB_POLYB 5          /* refused: MTPX_E_MODEL */
+#define MTPX_RB_POLYBCOS 6       /* refused: MTPX_E_MODEL */
+#define MTPX_CUT_QUADRATIC 0
+#define MTPX_CUT_COSINE 1
+#define MTPX_CUT_POLY5 2
+#define MTPX_CUT_NORMALIZED_QUADRATIC 3
+#define MTPX_CUT_COSINE_LEFT 4
+#define MTPX_CUT_COSINE_UNSCALED 5
+#define MTPX_CUT_COSINE_SQUARED 6
+#define MTPX_CUT_SINE_SQUARED 7
+#define MTPX_CUT_POLY3 8
+#define MTPX_CUT_POLY4 9
+#define MTPX_CUT_SMOOTHSTEP5 10
+#define MTPX_CUT_SMOOTHSTEP7 11
+#define MTPX_SHIFT_LINEAR 0
+#define MTPX_SHIFT_EXPONENTIAL 1
+#define MTPX_SHIFT_EXPONENTIAL_LEFT 2
+#define MTPX_SHIFT_I2 3
+#define MTPX_SHIFT_EXPONENTIAL_TANH 4
+/* Site-energy models and activations, the values of MTPGpuModel and
+ * MTPGpuActivation (mtp_gpu_direct.h:196-213): the linear MTP and the MTP-M
+ * heads mtp_m_q2, mtp_m_fs, mtp_m_n1, mtp_m_n2 and mtp_m_li. */
+#define MTPX_MODEL_LINEAR 0
+#define MTPX_MODEL_MTPM_QUADRATIC 1
+#define MTPX_MODEL_MTPM_ASINH 2
+#define MTPX_MODEL_MTPM_NN1 3
+#define MTPX_MODEL_MTPM_NN2 4
+#define MTPX_MODEL_MTPM_LINEAR 5
+#define MTPX_ACT_TANH 0
+#define MTPX_ACT_RELU 1
+#define MTPX_ACT_SIGMOID 2
+#define MTPX_ACT_LINEAR 3
+
+/* One radial basis: MTPGpuRadialBasisView (mtp_gpu_direct.h:215-236), as
+ * MTPGpuEvaluator's radial_basis_for fills it
+ * (potentials/mtp_gpu_adapter.cpp:110-212). */
+typedef struct mtpx_radial_basis_view {
+    int radial_basis;            /* MTPX_RB_* */
+    double min_dist, max_dist, scaling;
+    /* RBChebyshevConfigurable: */
+    int cutoff;                  /* MTPX_CUT_* */
+    int transform;               /* MTPX_SHIFT_* */
+    double cutoff_parameter;     /* RBChebyshevPoly4/5 rb_b, or the configurable cutoff_b */
+    double transform_parameter;  /* shift_lambda */
+    int one_minus_chebyshev;     /* basis_function_type one_minus_chebyshev */
+    double cutoff_r1, cutoff_r2; /* smoothstep7 interval */
+    double transform_scale_parameter; /* shift_scale_lambda */
+    /* PolyB / PolyBCos orthogonalisation tables (those kinds are refused) */
+    const double *polynomial_matrix;
+    const double *polynomial_normalizations;
+} mtpx_radial_basis_view;
+
+/* Flat model view: MTPGpuPotentialView (mtp_gpu_direct.h:239-289), field for
+ * field, as MTPGpuEvaluator::initialize fills it
+ * (potentials/mtp_gpu_adapter.cpp:427-441) and make_lammps_pair_view does
+ * for the LAMMPS pair styles.  Arrays are borrowed for the call and copied.
+ *
+ * - spmap [max_type] maps the caller's atom types to species in
+ *   [-1, species_count); -1 drops the atom from site requests.  Every type
+ *   the context is later given (neighbour builds, batches, CSR lists, site
+ *   requests) goes through it and must lie in [0, max_type).
+ * - With pair_radial_basis_count == 0 the one basis is {radial_basis,
+ *   min_dist, max_dist, scaling}, of kind MTPX_RB_CHEBYSHEV or
+ *   MTPX_RB_CHEBYCOS.  Otherwise pair_radial_bases holds species_count^2
+ *   bases in (centre, neighbour) species order: a split model, or one basis
+ *   repeated (a non-split Poly4/Poly5/configurable model, as the adapter
+ *   passes it).
+ * - cutoff is the list cutoff, PotMTP::cutoff: the largest max_dist of the
+ *   bases (0 takes that value).
+ * - model selects the site-energy head.  MTPX_MODEL_LINEAR reads
+ *   species_coeffs [species_count] and moment_coeffs [alpha_scalar_moments];
+ *   an MTP-M head reads species_coeffs [species_count],
+ *   descriptor_species_coeffs [descriptor_count][species_count],
+ *   descriptor_moment_coeffs [descriptor_count][alpha_scalar_moments] and
+ *   model_coeffs [model_coeffs_count], with moment_coeffs NULL.
+ * - max_mu, max_alpha_index_basic and nu_arr_list are recomputed from
+ *   alpha_index_basic and not read.
+ * Refused with MTPX_E_MODEL: PolyB / PolyBCos bases, a RBChebyshevPoly5 or
+ * configurable basis without pair descriptors, and the legacy NN scalar
+ * gather (scalar_gather != 0). */
 typedef struct mtpx_model_view {
     int species_count;          /* Z */
-    int radial_func_count;      /* M */
-    int rb_size;                /* R */
-    double min_dist, max_dist;  /* RBChebyshev interval; max_dist is the cutoff */
-    double scaling;             /* radial basis scaling */
+    int max_type;               /* entries of spmap */
+    const int *spmap;           /* [max_type] */
+
     int alpha_moments_count;    /* K */
     int alpha_index_basic_count;/* B */
     int alpha_index_times_count;/* T */
     int alpha_scalar_moments;   /* S */
+
+    int radial_func_count;      /* M */
+    int rb_size;                /* R */
+    int max_mu;
+    int max_alpha_index_basic;
+
+    double min_dist, max_dist;  /* the shared basis's interval */
+    double cutoff;              /* list cutoff (0: the largest max_dist) */
+    double scaling;             /* the shared basis's scaling */
+    int radial_basis;           /* MTPX_RB_* of the shared basis */
+
+    const mtpx_radial_basis_view *pair_radial_bases; /* [Z*Z] or NULL */
+    int pair_radial_basis_count;                     /* 0 or Z*Z */
+
+    const double *radial_coeffs;    /* [Z][Z][M][R] */
+    int radial_coeffs_count;        /* Z*Z*M*R, or 0 for that */
+    const double *species_coeffs;   /* [Z] */
+    const double *moment_coeffs;    /* [S] (linear MTP only) */
+
+    int model;                      /* MTPX_MODEL_* */
+    int descriptor_count;           /* q (0 for the linear MTP) */
+    int scalar_gather;              /* legacy NN inference: refused */
+    const double *input_mean, *input_inverse_std, *input_species;
+    const double *descriptor_species_coeffs; /* [q][Z] */
+    const double *descriptor_moment_coeffs;  /* [q][S] */
+    const double *model_coeffs;              /* [model_coeffs_count] */
+    int model_coeffs_count;
+    int model_activation;           /* MTPX_ACT_* */
+    int model_hidden1;
+    int model_hidden2;
+
     const int *alpha_index_basic;   /* [B][4] {mu, a, b, c} */
     const int *alpha_index_times;   /* [T][4] {l, r, c, out} */
     const int *alpha_moment_mapping;/* [S] */
-    const double *radial_coeffs;    /* [Z][Z][M][R] */
-    const double *species_coeffs;   /* [Z] */
-    const double *moment_coeffs;    /* [S] */
+    const int *nu_arr_list;         /* not read */
 } mtpx_model_view;
 
 /* ---- context ---------------------------------------------------------
@@ -68,8 +181,21 @@ const char *mtpx_version(void);
 
 /* ---- model -----------------------------------------------------------
  * MTPGpuDirect::initialize(const MTPGpuPotentialView&)
- * (mtp_gpu_direct.h:800-806). */
+ * (mtp_gpu_direct.h:800-806), with the checks of validate_potential_view
+ * (runtime/mtp/gpu-direct/mtp_gpu_direct.cu:419-660): MTPX_E_INVALID for an
+ * inconsistent view (the reference's texts), MTPX_E_MODEL for a kind this
+ * library does not evaluate.  The species map stays with the model. */
 int mtpx_load_model(mtpx_context *ctx, const mtpx_model_view *view);
+/* Host-only: the .mtp text (PotMTP::Save layout, as mtpx_save_model_text) of
+ * the model a view describes, after the same checks; buf / cap / len as
+ * mtpx_save_model_text, the first error into err.  No device needed. */
+int mtpx_format_model_view(const mtpx_model_view *view, char *buf, size_t cap, size_t *len,
+                           char *err, int errlen);
+/* The species map of the LAMMPS pair styles (make_lammps_pair_view,
+ * mtp_gpu_direct.h:291-330) for the loaded model: spmap [max_type] in
+ * [-1, Z), applied as mtpx_load_model's; NULL restores the identity map
+ * over [0, Z) that a text or GPM load sets. */
+int mtpx_set_species_map(mtpx_context *ctx, int max_type, const int *spmap);
 /* PotMTP::Load (potentials/potential_mtp.cpp:119-571): .mtp text with a
  * shared radial basis or one per ordered species pair (radial_basis_split),
  * of the kinds RBChebyshev, RBChebyCos, RBChebyshevPoly4, RBChebyshevPoly5
@@ -190,8 +316,10 @@ int mtpx_efs_device(mtpx_context *ctx, int deterministic);
 int mtpx_last_timings(const mtpx_context *ctx, double out_ms[4]);
 
 /* No counterpart in the reference: an allocation-free mtpx_efs for callers
- * that cannot allocate device memory (HIP graph capture, serving loops,
- * harnesses that forbid hipMalloc).  The fast (non-deterministic) E/F/S of
+ * that cannot allocate device memory (serving loops, harnesses that
+ * forbid hipMalloc).  It launches on the context's own stream and
+ * synchronises it before returning, so it cannot be recorded into a HIP
+ * graph.  The fast (non-deterministic) E/F/S of
  * the resident model and lists, written to the caller's device buffers on
  * the context's device: forces [n][3] (overwritten), site_energies [n],
  * energy_stress [10] (energy, then the 3x3 stress row-major).  The per-wave
@@ -221,8 +349,9 @@ int mtpx_set_add_efs(mtpx_context *ctx, int add_efs);
  * (< nlocal) with neighbours neighbors[offsets[c] .. offsets[c+1]-1] & mask,
  * atom indices < ntotal (ghosts allowed).  Per entry r = x[j] - x[i] (or the
  * given neighbor_vectors); entries with r.r == 0, r.r >= cutoff^2 or a
- * neighbour of negative type are skipped, and so are centres of negative
- * type (the reference's species map returning -1).
+ * neighbour of species -1 are skipped, and so are centres of species -1
+ * (the reference's species map returning -1; under the identity map, any
+ * negative type).
  *
  * Outputs (each may be NULL):
  *   force [ntotal][3]: f_i += sum_j D_j, f_j -= D_j; added onto the array
@@ -238,7 +367,8 @@ int mtpx_set_add_efs(mtpx_context *ctx, int add_efs);
  *     overwritten.
  * reuse_topology keeps the centres, offsets and neighbour indices of the
  * previous request (the counts must match) and refreshes types and
- * positions.  deterministic orders every sum (no floating-point atomics).
+ * positions; when the kept centres change (a centre's species turns -1 or
+ * back) the caller's offsets and neighbours are read and checked again.  deterministic orders every sum (no floating-point atomics).
  * Independent of the resident lists of mtpx_build_neighbors /
  * mtpx_set_structures, which stay as they are. */
 typedef struct mtpx_site_request {
@@ -250,7 +380,11 @@ typedef struct mtpx_site_request {
     const int *neighbors;          /* [offsets[center_count]] atom indices (before the mask) */
     int neighbor_index_mask;       /* LAMMPS NEIGHMASK; -1 keeps every bit */
     const double *neighbor_vectors;/* [P][3] r_j - r_i, or NULL to take x[j] - x[i] */
-    const int *type;               /* [ntotal] species 0 .. Z-1, negative: skipped */
+    const int *type;               /* [ntotal] atom types through the species map
+                                      (identity over 0 .. Z-1 unless a view or
+                                      mtpx_set_species_map gave one); an atom
+                                      whose species is -1 is skipped, and so is
+                                      a negative type under the identity map */
     const double *x;               /* [ntotal][3]; may be NULL with neighbor_vectors */
     double *force;                 /* [ntotal][3] */
     double *total_energy;

@@ -142,6 +142,21 @@ def test_zstd_blocks():
     assert capi.gpm_to_text(data) == capi.gpm_to_text(capi.gpm_from_text(text))
 
 
+@pytest.mark.skipif(_zstd() is None, reason="libzstd.so.1 not present")
+def test_zstd_block_beyond_the_read_limit_is_refused():
+    """A few-hundred-byte bundle whose zstd block declares 16 GiB of raw
+    data is refused before anything is allocated (Reader::read's 8 GiB
+    limit, tools/gpm_container.h:512-515)."""
+    data = capi.gpm_from_text(MODELS["mtp_m_n2"](), zstd_level=3)
+    man, payload = _unpack(data)
+    rad = next(b for b in man["blocks"] if b["id"] == "root/radial")
+    rad["shape"] = [str(1 << 31)]
+    rad["raw_size"] = str(8 << 31)
+    with pytest.raises(capi.MtpxError) as e:
+        capi.parse_model_gpm(_pack(man, payload))
+    assert "block exceeds read limit: root/radial" in str(e.value)
+
+
 # ------------------------------------------------------ reference container --
 
 @needs_gpm_ref
