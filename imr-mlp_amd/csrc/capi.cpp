@@ -240,6 +240,8 @@ int install_model(mtpx_context *ctx, Model &&m)
         HIP_TRY(upload(ctx->lin_chunk, lp.chunk_s0, s), "upload model");
         HIP_TRY(upload(ctx->lin_maskw, lp.maskw, s), "upload model");
         HIP_TRY(upload(ctx->lin_clist, lp.clist, s), "upload model");
+        HIP_TRY(upload(ctx->lin_walk, lp.walk, s), "upload model");
+        HIP_TRY(upload(ctx->lin_walk_off, lp.walk_off, s), "upload model");
         HIP_TRY(upload(ctx->lin_flevel, lp.fwd_level_step, s), "upload model");
         HIP_TRY(upload(ctx->lin_fsteps, lp.fwd_steps, s), "upload model");
         HIP_TRY(upload(ctx->lin_flcomb, lp.fwd_level_comb, s), "upload model");
@@ -270,6 +272,12 @@ int install_model(mtpx_context *ctx, Model &&m)
         L.chunk_s0 = ctx->lin_chunk.as<int>();
         L.maskw = ctx->lin_maskw.as<int>();
         L.clist = ctx->lin_clist.as<int>();
+        L.walk = ctx->lin_walk.as<int>();
+        L.walk_off = ctx->lin_walk_off.as<int>();
+        L.nwalk = lp.walk_off.back();
+        L.max_walk = 0;
+        for (int c = 0; c < lp.nchunks; ++c)
+            L.max_walk = std::max(L.max_walk, lp.walk_off[c + 1] - lp.walk_off[c]);
         L.lane_walk = lp.lane_walk ? 1 : 0;
         // MTPX_LIN_WALK=runtime (tuning): keep the run-time walk
         static const bool runtime_walk = [] {

@@ -72,8 +72,10 @@ struct mtpx_context {
     LinPlan lin;
     DevLin dl{};
     DBuf lin_level, lin_steps, lin_lcomb, lin_comb, lin_ent, lin_estart, lin_chunk, lin_maskw,
-        lin_clist, lin_flevel, lin_fsteps, lin_flcomb, lin_fcomb;
+        lin_clist, lin_flevel, lin_fsteps, lin_flcomb, lin_fcomb, lin_walk, lin_walk_off;
     DBuf comp, row_src, row_sw, row_y, rowsA, rowsY, gram_part, gram_out, lin_pair, lin_site;
+    // tile path: walk-order Jacobian values per site, structure lists per size class
+    DBuf lin_lw, lin_tiles;
     long rows_gen = -1;  // label_gen and p of the uploaded row descriptors
     int rows_p = -1;
     int64_t rows_R = 0;
@@ -130,9 +132,10 @@ struct mtpx_context {
                         &nbh_tmp.idx, &nbh_tmp.type, &nbh_tmp.x, &nbh_tmp.y, &nbh_tmp.z,
                         &nbh_tmp.d, &nbh_tmp.center_type, &lin_level, &lin_steps, &lin_lcomb,
                         &lin_comb, &lin_ent, &lin_estart, &lin_chunk, &lin_maskw, &lin_clist,
+                        &lin_walk, &lin_walk_off,
                         &comp, &row_src, &row_sw, &row_y, &rowsA, &rowsY, &gram_part, &gram_out,
                         &lin_pair, &lin_site, &lin_flevel, &lin_fsteps, &lin_flcomb,
-                        &lin_fcomb})
+                        &lin_fcomb, &lin_lw, &lin_tiles})
             b->release();
         scratch.release_all();
         sites.release();

@@ -181,37 +181,34 @@ __global__ __launch_bounds__(kWave *kMaxWaves) void efs_kernel(DevModel m, DevNe
                 }
             }
         }
-        if (!deterministic) {
-            fi0 = wave_sum(fi0);
-            fi1 = wave_sum(fi1);
-            fi2 = wave_sum(fi2);
-            if (lane == 0) {
-                atomicAdd(&out.forces[3 * ai + 0], fi0);
-                atomicAdd(&out.forces[3 * ai + 1], fi1);
-                atomicAdd(&out.forces[3 * ai + 2], fi2);
-            }
-        }
-        // this atom's virial: summed over the lanes, added to the wave's sums
-#pragma unroll
-        for (int k = 0; k < 9; ++k)
-            vs[k] = wave_sum(vs[k]);
-        if (lane == 0) {
-#pragma unroll
-            for (int k = 0; k < 9; ++k)
-                sums[1 + k] += vs[k];
+        // this atom's force (its own entries) and virial, summed over the
+        // lanes in one pass: lane 16 r + k (k < 3) ends with one total
+        double fv[12] = {fi0, fi1, fi2, vs[0], vs[1], vs[2], vs[3], vs[4], vs[5], vs[6], vs[7],
+                         vs[8]};
+        int vi;
+        const double tot = wave_reduce_scatter<12>(fv, lane, vi);
+        if (vi >= 0 && vi < 3) {
+            if (!deterministic)
+                atomicAdd(&out.forces[3 * ai + vi], tot);
+        } else if (vi >= 3) {
+            sums[vi - 2] += tot;  // the wave's virial sums, sums[1 .. 9]
             if (out.site_virial)
-#pragma unroll
-                for (int k = 0; k < 9; ++k)
-                    out.site_virial[9 * (size_t)i + k] = vs[k];
-            if (out.site_virial6 && !deterministic) {
-                // the centre's half of its entries (mlip.cpp:1164-1180)
+                out.site_virial[9 * (size_t)i + vi - 3] = tot;
+        }
+        if (out.site_virial6 && !deterministic) {
+            // the centre's half of its entries (mlip.cpp:1164-1180), from the
+            // nine totals gathered through the (idle) transpose buffer
+            if (vi >= 3)
+                red[vi - 3] = tot;
+            wave_sync();
+            if (lane == 0) {
                 double *v = out.site_virial6 + 6 * (size_t)ai;
-                atomicAdd(v + 0, 0.5 * vs[0]);
-                atomicAdd(v + 1, 0.5 * vs[4]);
-                atomicAdd(v + 2, 0.5 * vs[8]);
-                atomicAdd(v + 3, 0.25 * (vs[3] + vs[1]));
-                atomicAdd(v + 4, 0.25 * (vs[6] + vs[2]));
-                atomicAdd(v + 5, 0.25 * (vs[7] + vs[5]));
+                atomicAdd(v + 0, 0.5 * red[0]);
+                atomicAdd(v + 1, 0.5 * red[4]);
+                atomicAdd(v + 2, 0.5 * red[8]);
+                atomicAdd(v + 3, 0.25 * (red[3] + red[1]));
+                atomicAdd(v + 4, 0.25 * (red[6] + red[2]));
+                atomicAdd(v + 5, 0.25 * (red[7] + red[5]));
             }
         }
         wave_sync();

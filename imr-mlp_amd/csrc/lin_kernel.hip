@@ -59,6 +59,7 @@ struct LinWalk {
     const const_int *mw;  // [kLinMaskWords] slot masks of the chunk, 4 per word
     double lc0, lc1;      // lane l: L values of entries l and 64 + l
     int pos;              // next entry (uniform)
+    const double *lch;    // runtime walks of the tile kernel: L values in walk order
 };
 
 __device__ __forceinline__ double readlane_d(double v, int l)
@@ -124,7 +125,7 @@ __device__ __forceinline__ void lin_apply(int mk, int sl, double gx, double gy, 
                 const int e = w.pos++;
                 lv = readlane_d(e < 64 ? w.lc0 : w.lc1, e & 63);
             } else {
-                lv = ws[w.lidx[(size_t)sl * kLinChunk + k]];
+                lv = w.lch ? w.lch[w.pos++] : ws[w.lidx[(size_t)sl * kLinChunk + k]];
             }
             acc[3 * k] += lv * gx;
             acc[3 * k + 1] += lv * gy;
@@ -263,9 +264,13 @@ constexpr int walk_pos(int c, int sl)
     return e;
 }
 
-template <class CP, int C, int NU, class P>
+// kStaged: the L values come in walk order, in two lane registers (lane l
+// holds entries l and 64 + l of the chunk's walk), read with readlane at
+// constant lanes; otherwise from the site's work space in LDS.
+template <class CP, int C, int NU, class P, bool kStaged = false>
 __device__ __forceinline__ void lin_shells_cp(const Nbr<P::M> &q, const double *prev,
-                                              const double *ws, double (&acc)[3 * kLinChunk])
+                                              const double *ws, double (&acc)[3 * kLinChunk],
+                                              double lc0 = 0.0, double lc1 = 0.0)
 {
     double cur[shell_size(NU)];
     if constexpr (NU == 0)
@@ -296,7 +301,11 @@ __device__ __forceinline__ void lin_shells_cp(const Nbr<P::M> &q, const double *
                         constexpr int k = decltype(K)::value;
                         if constexpr ((mk >> k) & 1) {
                             constexpr int e = e0 + popc(mk & ((1 << k) - 1));
-                            const double lv = ws[CP::clist[C][e]];  // LDS broadcast
+                            double lv;
+                            if constexpr (kStaged)
+                                lv = readlane_d(e < kWave ? lc0 : lc1, e % kWave);
+                            else
+                                lv = ws[CP::clist[C][e]];  // LDS broadcast
                             acc[3 * k] += lv * gx;
                             acc[3 * k + 1] += lv * gy;
                             acc[3 * k + 2] += lv * gz;
@@ -307,59 +316,30 @@ __device__ __forceinline__ void lin_shells_cp(const Nbr<P::M> &q, const double *
         }
     });
     if constexpr (NU < P::NUMAX)
-        lin_shells_cp<CP, C, NU + 1, P>(q, cur, ws, acc);
+        lin_shells_cp<CP, C, NU + 1, P, kStaged>(q, cur, ws, acc, lc0, lc1);
 }
 
 // The compiled walk of chunk `ch` (a chain of uniform compares).
-template <class CP, int C, class P>
+template <class CP, int C, class P, bool kStaged = false>
 __device__ __forceinline__ void lin_chunk_cp(int ch, const Nbr<P::M> &q, const double *ws,
-                                             double (&acc)[3 * kLinChunk])
+                                             double (&acc)[3 * kLinChunk], double lc0 = 0.0,
+                                             double lc1 = 0.0)
 {
     if (ch == C) {
-        lin_shells_cp<CP, C, 0, P>(q, nullptr, ws, acc);
+        lin_shells_cp<CP, C, 0, P, kStaged>(q, nullptr, ws, acc, lc0, lc1);
         return;
     }
     if constexpr (C + 1 < CP::nchunks)
-        lin_chunk_cp<CP, C + 1, P>(ch, q, ws, acc);
+        lin_chunk_cp<CP, C + 1, P, kStaged>(ch, q, ws, acc, lc0, lc1);
 }
 
-// Makes the neighbour's values opaque to the optimiser (no instruction):
-// the shell values of a chunk walk are then recomputed per chunk instead of
-// being hoisted out of the chunk loop, which would keep all of them live.
-template <int MMAX>
-__device__ __forceinline__ void opaque(Nbr<MMAX> &q)
-{
-    asm volatile("" : "+v"(q.d), "+v"(q.invd), "+v"(q.ux), "+v"(q.uy), "+v"(q.uz));
-#pragma unroll
-    for (int mu = 0; mu < MMAX; ++mu)
-        asm volatile("" : "+v"(q.f[mu]), "+v"(q.fd[mu]));
-}
-
-// Width of chunk c's rows in the pair buffer: its scalar count rounded up
-// to even (16-byte stores).
-__device__ __forceinline__ int chunk_width(const int *chunk_s0, int c)
-{
-    return (chunk_s0[c + 1] - chunk_s0[c] + 1) & ~1;
-}
-
-// One entry's derivatives of a chunk as a block [3][w] (component a of
-// scalar s0 + k at a w + k; w even, a padding value is zero): 16-byte stores
-// of consecutive addresses.
-__device__ __forceinline__ void store_block(double *blk, int w,
-                                            const double (&acc)[3 * kLinChunk])
-{
-#pragma unroll
-    for (int a = 0; a < 3; ++a)
-#pragma unroll
-        for (int k = 0; k < kLinChunk; k += 2)
-            if (k < w)
-                *reinterpret_cast<double2 *>(blk + a * w + k) =
-                    make_double2(acc[3 * k + a], acc[3 * (k + 1) + a]);
-}
-
-template <class P, int kMaxWaves, class CP = void>
-__global__ __launch_bounds__(kWave *kMaxWaves) void lin_site_kernel(DevModel m, DevLin L,
-                                                                    DevNeighbors nb, LinGroup g)
+// ---- tile path --------------------------------------------------------------
+// lin_jac_kernel, one wave per site: the scalar moments (energy components)
+// and the site Jacobian L, whose values the walks read, exported in walk
+// order (chunk after chunk) to lw[site][nwalk].
+template <class P, int kMaxWaves>
+__global__ __launch_bounds__(kWave *kMaxWaves) void lin_jac_kernel(DevModel m, DevLin L,
+                                                                   DevNeighbors nb, LinGroup g)
 {
     extern __shared__ double lds[];
     const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
@@ -380,8 +360,6 @@ __global__ __launch_bounds__(kWave *kMaxWaves) void lin_site_kernel(DevModel m, 
         for (int k = lane; k < m.K; k += kWave)
             mom[k] = 0.0;
         wave_sync();
-
-        // ---- moments (as the E/F/S kernel) --------------------------------
         for (int base = 0; base < n; base += kWave) {
             FwdCtx cx{red, mom, Ls.slot_basic, lane, 0};
             Nbr<P::M> q;
@@ -397,144 +375,247 @@ __global__ __launch_bounds__(kWave *kMaxWaves) void lin_site_kernel(DevModel m, 
         wave_sync();
         run_rules<false, false>(L.fwd_steps, L.fwd_level_step, L.fwd_level_comb, L.fwd_comb,
                                 L.nfwd, ws, lane, 0);
-
-        // ---- the site's scalar moments (energy components) ---------------
-        double *srow = g.site + (size_t)(i - g.a0) * 10 * m.S + 9 * m.S;
+        double *srow = g.site + (size_t)(i - g.a0) * m.S;
         for (int s = lane; s < m.S; s += kWave)
             srow[s] = mom[Ls.map[s]];
-
-        // ---- site Jacobian of the scalars w.r.t. the basics (its space lies
-        // over the transpose buffer of the moments) ------------------------
         for (int k = L.one + lane; k < L.L0 + L.nL; k += kWave)
             ws[k] = k == L.one ? 1.0 : 0.0;
         wave_sync();
         run_rules<false, false>(L.steps, L.level_step, L.level_comb, L.comb, L.nlev, ws, lane, 0);
-
-        // ---- dm_s/dr_j of every entry, a chunk of scalars at a time, into
-        // the pair buffer [chunk][entry][3][w] (the lane's entry: 3 w
-        // contiguous values per chunk)
-        for (int base = 0; base < n; base += kWave) {
-            const bool valid = lane < n - base;
-            const int64_t pe = beg + base + lane;
-            Nbr<P::M> q;
-            load_neighbor<P>(m, nb, Ls.coef, ti, pe, valid, q);
-            const size_t el = (size_t)(pe - g.e0);
-            if constexpr (!std::is_void_v<CP>) {
-                // a run-time loop over the chunks (each chunk's walk is its
-                // own block: registers are allocated chunk by chunk)
-                for (int ch = 0, boff = 0; ch < CP::nchunks; ++ch) {
-                    const int w = chunk_width(L.chunk_s0, ch);
-                    double acc[3 * kLinChunk];
-#pragma unroll
-                    for (int r = 0; r < 3 * kLinChunk; ++r)
-                        acc[r] = 0.0;
-                    opaque(q);
-                    lin_chunk_cp<CP, 0, P>(ch, q, ws, acc);
-                    if (valid)
-                        store_block(g.pair + (size_t)boff * g.pg + el * 3 * w, w, acc);
-                    boff += 3 * w;
-                }
-                continue;
-            }
-            for (int ch = 0, boff = 0; ch < L.nchunks; ++ch) {
-                const int cw = chunk_width(L.chunk_s0, ch);
-                LinWalk w;
-                w.pos = 0;
-                if constexpr (P::exact) {
-                    w.mw = (const const_int *)(L.maskw + (size_t)ch * kLinMaskWords);
-                    const int *clp = L.clist + (size_t)ch * kLinEntries;
-                    w.lc0 = ws[clp[lane]];
-                    w.lc1 = ws[clp[kWave + lane]];
-                } else {
-                    w.mask = L.slot_mask + (size_t)ch * m.nslots;
-                    w.lidx = L.slot_L + (size_t)ch * m.nslots * kLinChunk;
-                }
-                double acc[3 * kLinChunk];
-#pragma unroll
-                for (int r = 0; r < 3 * kLinChunk; ++r)
-                    acc[r] = 0.0;
-                opaque(q);
-                int slot = 0;
-                lin_shells<0, P>(m, q, nullptr, slot, w, ws, acc);
-                if (valid)
-                    store_block(g.pair + (size_t)boff * g.pg + el * 3 * cw, cw, acc);
-                boff += 3 * cw;
-            }
-        }
+        double *lw = g.lw + (size_t)(i - g.a0) * L.nwalk;
+        for (int e = lane; e < L.nwalk; e += kWave)
+            lw[e] = ws[L.walk[e]];
         wave_sync();
     }
 }
 
-#if MTPX_LIN_PART == 1
-// Force rows and per-atom stress partials of a group from the pair buffer,
-// in a fixed order:
-//   fc[i][a][Z+s] = sum_{e in list(i)} D_e[a][s] - sum_{e: idx[e] = i} D_e[a][s]
-//   site[i][3a+b][s] = -sum_{e in list(i)} D_e[a][s] r_e[b]
-// One thread per atom and value v of an entry's chunk blocks (v runs over
-// the blocks [3][w] of the chunks in order; gather_per threads per atom,
-// whole waves): consecutive lanes read consecutive doubles of an entry's
-// blocks.
-__global__ __launch_bounds__(256) void lin_gather_kernel(int S, int Z, int p, DevNeighbors nb,
-                                                         const int *rev_off,
-                                                         const int *rev_pairs, LinGroup g,
-                                                         double *fc)
+// One (structure, chunk) per wave: the force rows of the structure's atoms
+// for the chunk's scalars,
+//   fc[i][a][Z+s] = sum_{e in list(i)} D_e[a][s] - sum_{e: idx[e] = i} D_e[a][s],
+// accumulated over the structure's sites in the wave's own tile (in LDS, or
+// for a structure larger than a tile in the rows of fc itself), in site
+// order: one wave is the only writer of its rows, so the sums are
+// repeatable.  The structure's stress
+// components -sum_e D_e[a][s] r_e[b] are summed per lane in registers and
+// over the wave at the end.  The site's walk-order L values are staged in
+// LDS; the walk is the site kernel's.
+template <class P, class CP>
+__global__ __launch_bounds__(kWave) void lin_tile_kernel(DevModel m, DevLin L, DevNeighbors nb,
+                                                         LinTile t)
 {
-    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    const int il = (int)(t / g.gather_per), v = (int)(t % g.gather_per);
-    if (il >= g.a1 - g.a0)
+    const bool lds_tile = t.rows_cap > 0;
+    extern __shared__ double lds[];
+    const int lane = threadIdx.x;
+    // chunk-major: the waves that run at the same time mostly walk the same
+    // chunk, whose code then stays in the instruction cache
+    const int item = blockIdx.x;
+    if (item >= t.count * t.nchunks)
         return;
-    // the chunk of value v, its row width and the plane offset (doubles
-    // per entry of the chunks before it)
-    int ch = 0, rem = v, boff = 0, w = chunk_width(g.chunk_s0, 0);
-    while (rem >= 3 * w) {
-        rem -= 3 * w;
-        boff += 3 * w;
-        if (++ch >= g.nchunks)
-            return;
-        w = chunk_width(g.chunk_s0, ch);
+    const int c = t.structs[item % t.count], ch = item / t.count;
+    const int i0 = t.soff[c], i1 = t.soff[c + 1], N = i1 - i0;
+    const int s0 = L.chunk_s0[ch], w = L.chunk_s0[ch + 1] - s0;
+    const int wb = L.walk_off[ch], ne = L.walk_off[ch + 1] - wb;
+    // tile row: [3][kLinChunk] and one pad double, so that rows are an odd
+    // number of doubles apart and the lanes' atomics on different rows fall
+    // in different banks
+    constexpr int kRow = 3 * kLinChunk + 1;
+
+    double *coef = lds;
+    const int ncr = m.Z * m.Z * m.M * m.R;
+    double *lch = lds + ((ncr + 3) & ~3);
+    double *tile = lch + ((L.max_walk + 3) & ~3);
+    for (int k = lane; k < ncr; k += kWave)
+        coef[k] = m.radial[k];
+    if (lds_tile)
+        for (int k = lane; k < N * kRow; k += kWave)
+            tile[k] = 0.0;
+    double st[9 * kLinChunk];
+#pragma unroll
+    for (int k = 0; k < 9 * kLinChunk; ++k)
+        st[k] = 0.0;
+    // fc rows of this chunk: fc[(i0 + j) 3p + a p + Z + s0 + k]
+    double *frow = t.fc + (size_t)i0 * 3 * t.p + t.Z + s0;
+    wave_sync();
+
+    // The next site's first 128 L values and first batch of entries are
+    // fetched one site ahead (a wave per SIMD: their latency would otherwise
+    // stall it); the rest of a long walk and further batches load in place.
+    auto fetch_l = [&](int i, double &l0, double &l1) {
+        const double *src = t.lw + (size_t)(i - t.a0) * L.nwalk + wb;
+        l0 = lane < ne ? src[lane] : 0.0;
+        l1 = kWave + lane < ne ? src[kWave + lane] : 0.0;
+    };
+    // List bounds and species are read two sites ahead with vector loads
+    // (lane-dependent addresses; lanes 0 and 1 hold begin and end) and taken
+    // into scalars one site ahead, so that the next site's entries can be
+    // fetched a whole site ahead: scalar loads would share the LDS wait
+    // counter and make every LDS wait of the walk wait for them too.
+    int zero = 0;
+    asm volatile("" : "+v"(zero));  // a lane value the compiler cannot fold
+    int vb = 0, vt = 0;
+    auto fetch_bounds = [&](int i) {
+        vb = nb.offsets[i + (lane & 1)];
+        vt = nb.center_type[i + zero];
+    };
+    int nbeg = 0, nend = 0, nti = 0;  // the next site's bounds and species
+    auto take_bounds = [&]() {
+        nbeg = __builtin_amdgcn_readlane(vb, 0);
+        nend = __builtin_amdgcn_readlane(vb, 1);
+        nti = __builtin_amdgcn_readfirstlane(vt);
+    };
+    double nl0 = 0.0, nl1 = 0.0;
+    EntryRaw nx{0.0, 0.0, 0.0, 0.0, 0, -1};
+    int cbeg = 0, cend = 0, cti = 0;  // this site's
+    if (i0 < i1) {
+        fetch_bounds(i0);
+        take_bounds();
+        cbeg = nbeg;
+        cend = nend;
+        cti = nti;
+        fetch_l(i0, nl0, nl1);
+        nx = fetch_entry(nb, cbeg + lane, lane < cend - cbeg);
+        if (i0 + 1 < i1) {
+            fetch_bounds(i0 + 1);
+            take_bounds();
+        }
     }
-    const int a = rem / w, s = g.chunk_s0[ch] + rem % w;
-    if (s >= g.chunk_s0[ch + 1])
-        return;
-    const int bw = 3 * w;
-    const int i = g.a0 + il;
-    const double *D = g.pair + (size_t)boff * g.pg - (size_t)g.e0 * bw + rem;
-    double f = 0.0, sv0 = 0.0, sv1 = 0.0, sv2 = 0.0;
-#pragma unroll 4
-    for (int e = nb.offsets[i], e1 = nb.offsets[i + 1]; e < e1; ++e) {
-        const double d = D[(size_t)e * bw];
-        f += d;
-        sv0 -= d * nb.x[e];
-        sv1 -= d * nb.y[e];
-        sv2 -= d * nb.z[e];
+    // compiled and exact walks read this site's L values from lane registers;
+    // the run-time walks from the LDS stage
+    constexpr bool kLaneL = !std::is_void_v<CP> || P::exact;
+    for (int i = i0; i < i1; ++i) {
+        const double cl0 = nl0, cl1 = nl1;
+        if constexpr (!kLaneL) {
+            if (lane < ne)
+                lch[lane] = nl0;
+            if (kWave + lane < ne)
+                lch[kWave + lane] = nl1;
+            if (ne > 2 * kWave) {
+                const double *src = t.lw + (size_t)(i - t.a0) * L.nwalk + wb;
+                for (int e = 2 * kWave + lane; e < ne; e += kWave)
+                    lch[e] = src[e];
+            }
+        }
+        const EntryRaw first = nx;
+        const int ti = cti, beg = cbeg, n = cend - cbeg;
+        if (i + 1 < i1) {
+            fetch_l(i + 1, nl0, nl1);
+            nx = fetch_entry(nb, nbeg + lane, lane < nend - nbeg);
+            cbeg = nbeg;
+            cend = nend;
+            cti = nti;
+            if (i + 2 < i1)
+                fetch_bounds(i + 2);
+        }
+        if constexpr (!kLaneL)
+            wave_sync();
+        for (int base = 0; base < n; base += kWave) {
+            const bool valid = lane < n - base;
+            const int64_t pe = beg + base + lane;
+            const EntryRaw en = base == 0 ? first : fetch_entry(nb, pe, valid);
+            Nbr<P::M> q;
+            neighbor_from<P>(m, coef, ti, en, valid, q);
+            double acc[3 * kLinChunk];
+#pragma unroll
+            for (int r = 0; r < 3 * kLinChunk; ++r)
+                acc[r] = 0.0;
+            if constexpr (!std::is_void_v<CP>) {
+                lin_chunk_cp<CP, 0, P, true>(ch, q, lch, acc, cl0, cl1);
+            } else {
+                LinWalk wk;
+                wk.pos = 0;
+                wk.lch = nullptr;
+                if constexpr (P::exact) {
+                    wk.mw = (const const_int *)(L.maskw + (size_t)ch * kLinMaskWords);
+                    wk.lc0 = cl0;
+                    wk.lc1 = cl1;
+                } else {
+                    wk.mask = L.slot_mask + (size_t)ch * m.nslots;
+                    wk.lch = lch;
+                }
+                int slot = 0;
+                lin_shells<0, P>(m, q, nullptr, slot, wk, lch, acc);
+            }
+            // the neighbour's row: minus this entry's derivatives
+            const int jl = valid ? en.j - i0 : -1;
+            if ((unsigned)jl < (unsigned)N) {
+                if (lds_tile) {
+                    double *row = tile + (size_t)jl * kRow;
+#pragma unroll
+                    for (int k = 0; k < kLinChunk; ++k)
+                        if (k < w)
+#pragma unroll
+                            for (int a = 0; a < 3; ++a)
+                                atomicAdd(row + a * kLinChunk + k, -acc[3 * k + a]);
+                } else {
+                    double *row = frow + (size_t)jl * 3 * t.p;
+#pragma unroll
+                    for (int k = 0; k < kLinChunk; ++k)
+                        if (k < w)
+#pragma unroll
+                            for (int a = 0; a < 3; ++a)
+                                atomicAdd(row + (size_t)a * t.p + k, -acc[3 * k + a]);
+                }
+            }
+            // stress: -D_a r_b
+            const double r3[3] = {q.x, q.y, q.z};
+#pragma unroll
+            for (int k = 0; k < kLinChunk; ++k)
+#pragma unroll
+                for (int a = 0; a < 3; ++a)
+#pragma unroll
+                    for (int bq = 0; bq < 3; ++bq)
+                        st[(3 * a + bq) * kLinChunk + k] -= acc[3 * k + a] * r3[bq];
+            // the centre's row: the sum of this batch's derivatives
+            int vi;
+            const double v = wave_reduce_scatter<3 * kLinChunk>(acc, lane, vi);
+            if (vi >= 0 && vi / 3 < w) {
+                const int k = vi / 3, a = vi % 3;
+                if (lds_tile)
+                    atomicAdd(tile + (size_t)(i - i0) * kRow + a * kLinChunk + k, v);
+                else
+                    atomicAdd(frow + (size_t)(i - i0) * 3 * t.p + (size_t)a * t.p + k, v);
+            }
+        }
+        if (i + 2 < i1)
+            take_bounds();
+        if constexpr (!kLaneL)
+            wave_sync();  // the next site's values overwrite the stage
     }
-#pragma unroll 4
-    for (int k = rev_off[i], k1 = rev_off[i + 1]; k < k1; ++k)
-        f -= D[(size_t)rev_pairs[k] * bw];
-    fc[(size_t)i * 3 * p + (size_t)a * p + Z + s] = f;
-    double *srow = g.site + (size_t)il * 10 * S + s;
-    srow[(size_t)(3 * a) * S] = sv0;
-    srow[(size_t)(3 * a + 1) * S] = sv1;
-    srow[(size_t)(3 * a + 2) * S] = sv2;
+    if (lds_tile) {
+        wave_sync();
+        for (int k = lane; k < N * 3 * w; k += kWave) {
+            const int j = k / (3 * w), r = k % (3 * w), a = r / w, kk = r % w;
+            frow[(size_t)j * 3 * t.p + (size_t)a * t.p + kk] = tile[(size_t)j * kRow + a * kLinChunk + kk];
+        }
+    }
+#pragma unroll
+    for (int qq = 0; qq < 9; ++qq)
+#pragma unroll
+        for (int k = 0; k < kLinChunk; ++k)
+            if (k < w) {
+                const double v = wave_sum(st[qq * kLinChunk + k]);
+                if (lane == 0)
+                    t.sc[((size_t)c * 9 + qq) * t.p + t.Z + s0 + k] = v;
+            }
 }
 
-// Energy and stress components of a group's structures: ordered sums of the
-// site rows over each structure's atoms, and the species counts.
+#if MTPX_LIN_PART == 1
+// Energy components of a group's structures: ordered sums of the sites'
+// scalar moments over each structure's atoms, and the species counts.
 __global__ __launch_bounds__(256) void lin_reduce_kernel(int S, int Z, int p, const int *soff,
                                                          const int *center_type, LinGroup g,
-                                                         double *ec, double *sc)
+                                                         double *ec)
 {
-    const int w = 10 * S + Z;
+    const int w = S + Z;
     const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (t >= (int64_t)(g.c1 - g.c0) * w)
         return;
     const int c = g.c0 + (int)(t / w), r = (int)(t % w);
     const int i0 = soff[c], i1 = soff[c + 1];
-    if (r < 10 * S) {
-        const int q = r / S, s = r % S;
+    if (r < S) {
         // loads of several atoms in flight; the sum stays in atom order
-        const double *src = g.site + (size_t)(i0 - g.a0) * 10 * S + r;
-        const size_t st = 10 * (size_t)S;
+        const double *src = g.site + (size_t)(i0 - g.a0) * S + r;
+        const size_t st = (size_t)S;
         double acc = 0.0;
         int i = i0;
         for (; i + 8 <= i1; i += 8, src += 8 * st) {
@@ -548,12 +629,9 @@ __global__ __launch_bounds__(256) void lin_reduce_kernel(int S, int Z, int p, co
         }
         for (; i < i1; ++i, src += st)
             acc += *src;
-        if (q < 9)
-            sc[((size_t)c * 9 + q) * p + Z + s] = acc;
-        else
-            ec[(size_t)c * p + Z + s] = acc;
+        ec[(size_t)c * p + Z + r] = acc;
     } else {
-        const int sp = r - 10 * S;
+        const int sp = r - S;
         int cnt = 0;
         for (int i = i0; i < i1; ++i)
             cnt += center_type[i] == sp;
@@ -586,13 +664,23 @@ constexpr int lin_waves()
     return std::is_same_v<P, ProfLevel10> ? 8 : 4;
 }
 
-template <class P, class CP = void>
-void launch_lin_variant(const DevModel &m, const DevLin &L, const DevNeighbors &nb,
+template <class P>
+void launch_jac_variant(const DevModel &m, const DevLin &L, const DevNeighbors &nb,
                         const LinGroup &g, const EfsLaunch &cfg, hipStream_t s)
 {
     constexpr int W = lin_waves<P>();
-    hipLaunchKernelGGL((lin_site_kernel<P, W, CP>), dim3(cfg.grid), dim3(kWave * cfg.waves),
+    hipLaunchKernelGGL((lin_jac_kernel<P, W>), dim3(cfg.grid), dim3(kWave * cfg.waves),
                        cfg.lds_bytes, s, m, L, nb, g);
+}
+
+template <class P, class CP = void>
+void launch_tile_variant(const DevModel &m, const DevLin &L, const DevNeighbors &nb,
+                         const LinTile &t, size_t lds_bytes, hipStream_t s)
+{
+    const int items = t.count * t.nchunks;
+    const unsigned grid = (unsigned)((items + 7) / 8 * 8);
+    hipLaunchKernelGGL((lin_tile_kernel<P, CP>), dim3(grid), dim3(kWave), lds_bytes, s, m, L, nb,
+                       t);
 }
 
 static_assert(exact_slot_count<ProfLevel16>() == LinPlanLevel16::nslots,
@@ -601,20 +689,20 @@ static_assert(exact_slot_count<ProfLevel16>() == LinPlanLevel16::nslots,
 }  // namespace
 
 #if MTPX_LIN_PART == 2
-// variant 5 (level 16, compiled walk) and 1 (level 20)
-void launch_lin_site_part2(int variant, const DevModel &m, const DevLin &L,
-                           const DevNeighbors &nb, const LinGroup &g, const EfsLaunch &cfg,
+// tile kernels of variant 5 (level 16, compiled walk) and 1 (level 20)
+void launch_lin_tile_part2(int variant, const DevModel &m, const DevLin &L,
+                           const DevNeighbors &nb, const LinTile &t, size_t lds_bytes,
                            hipStream_t s)
 {
     if (variant == 5)
-        launch_lin_variant<ProfLevel16, LinPlanLevel16>(m, L, nb, g, cfg, s);
+        launch_tile_variant<ProfLevel16, LinPlanLevel16>(m, L, nb, t, lds_bytes, s);
     else
-        launch_lin_variant<ProfLevel20>(m, L, nb, g, cfg, s);
+        launch_tile_variant<ProfLevel20>(m, L, nb, t, lds_bytes, s);
 }
 #else
 // in the other object of this file
-void launch_lin_site_part2(int variant, const DevModel &m, const DevLin &L,
-                           const DevNeighbors &nb, const LinGroup &g, const EfsLaunch &cfg,
+void launch_lin_tile_part2(int variant, const DevModel &m, const DevLin &L,
+                           const DevNeighbors &nb, const LinTile &t, size_t lds_bytes,
                            hipStream_t s);
 
 // The E/F/S variant, or the generic one where the compile-time walk's
@@ -667,39 +755,53 @@ bool lin_configure(const DevModel &m, const DevLin &L, int n, int num_cus, size_
     return true;
 }
 
-hipError_t launch_lin_site(const DevModel &m, const DevLin &L, const DevNeighbors &nb,
-                           const LinGroup &g, const EfsLaunch &cfg, hipStream_t s)
+size_t lin_tile_lds(const DevModel &m, const DevLin &L, int rows)
+{
+    const size_t ncr = ((size_t)m.Z * m.Z * m.M * m.R + 3) & ~size_t(3);
+    const size_t stage = ((size_t)L.max_walk + 3) & ~size_t(3);
+    return sizeof(double) * (ncr + stage + (size_t)rows * (3 * kLinChunk + 1));
+}
+
+hipError_t launch_lin_jac(const DevModel &m, const DevLin &L, const DevNeighbors &nb,
+                          const LinGroup &g, const EfsLaunch &cfg, hipStream_t s)
 {
     if (g.a1 <= g.a0)
         return hipSuccess;
-    switch (const int v = lin_variant(m, L)) {
-    case 0: launch_lin_variant<ProfLevel16>(m, L, nb, g, cfg, s); break;
-    case 1:
-    case 5: launch_lin_site_part2(v, m, L, nb, g, cfg, s); break;
-    case 2: launch_lin_variant<ProfLevel10>(m, L, nb, g, cfg, s); break;
-    case 3: launch_lin_variant<ProfSmall>(m, L, nb, g, cfg, s); break;
-    default: launch_lin_variant<ProfGeneric>(m, L, nb, g, cfg, s); break;
+    switch (lin_variant(m, L)) {
+    case 0:
+    case 5: launch_jac_variant<ProfLevel16>(m, L, nb, g, cfg, s); break;
+    case 1: launch_jac_variant<ProfLevel20>(m, L, nb, g, cfg, s); break;
+    case 2: launch_jac_variant<ProfLevel10>(m, L, nb, g, cfg, s); break;
+    case 3: launch_jac_variant<ProfSmall>(m, L, nb, g, cfg, s); break;
+    default: launch_jac_variant<ProfGeneric>(m, L, nb, g, cfg, s); break;
     }
     return hipGetLastError();
 }
 
-hipError_t launch_lin_gather(const DevModel &m, const DevNeighbors &nb, const int *rev_off,
-                             const int *rev_pairs, const LinGroup &g, double *fc, hipStream_t s)
+hipError_t launch_lin_tile(const DevModel &m, const DevLin &L, const DevNeighbors &nb,
+                           const LinTile &t, hipStream_t s)
 {
-    const int64_t work = (int64_t)(g.a1 - g.a0) * g.gather_per;
-    if (work > 0)
-        hipLaunchKernelGGL(lin_gather_kernel, dim3((unsigned)((work + 255) / 256)), dim3(256), 0,
-                           s, m.S, m.Z, m.Z + m.S, nb, rev_off, rev_pairs, g, fc);
+    if (t.count <= 0 || t.nchunks <= 0)
+        return hipSuccess;
+    const size_t lds = lin_tile_lds(m, L, t.rows_cap);
+    switch (const int v = lin_variant(m, L)) {
+    case 0: launch_tile_variant<ProfLevel16>(m, L, nb, t, lds, s); break;
+    case 1:
+    case 5: launch_lin_tile_part2(v, m, L, nb, t, lds, s); break;
+    case 2: launch_tile_variant<ProfLevel10>(m, L, nb, t, lds, s); break;
+    case 3: launch_tile_variant<ProfSmall>(m, L, nb, t, lds, s); break;
+    default: launch_tile_variant<ProfGeneric>(m, L, nb, t, lds, s); break;
+    }
     return hipGetLastError();
 }
 
 hipError_t launch_lin_reduce(const DevModel &m, const int *soff, const int *center_type,
-                             const LinGroup &g, double *ec, double *sc, hipStream_t s)
+                             const LinGroup &g, double *ec, hipStream_t s)
 {
-    const int64_t work = (int64_t)(g.c1 - g.c0) * (10 * m.S + m.Z);
+    const int64_t work = (int64_t)(g.c1 - g.c0) * (m.S + m.Z);
     if (work > 0)
         hipLaunchKernelGGL(lin_reduce_kernel, dim3((unsigned)((work + 255) / 256)), dim3(256), 0,
-                           s, m.S, m.Z, m.Z + m.S, soff, center_type, g, ec, sc);
+                           s, m.S, m.Z, m.Z + m.S, soff, center_type, g, ec);
     return hipGetLastError();
 }
 

@@ -27,19 +27,27 @@ CompLayout comp_layout(const mtpx_context *ctx)
     return l;
 }
 
-// Pair-buffer budget of one group of structures (MTPX_LIN_PAIR_MB, tuning;
-// 8 GiB by default: fewer, larger groups keep the site kernel's launches
-// full); a structure larger than the budget forms a group of its own.
-size_t pair_budget()
+// Budget of one group's per-site Jacobian values (MTPX_LIN_GROUP_MB, tuning;
+// 8 GiB by default); a structure larger than the budget forms a group of
+// its own.
+size_t group_budget()
 {
-    const char *e = getenv("MTPX_LIN_PAIR_MB");
+    const char *e = getenv("MTPX_LIN_GROUP_MB");
     const long v = e ? atol(e) : 0;
     return (v > 0 ? (size_t)v : (size_t)8192) << 20;
 }
 
 // Components of every structure of the resident topology into ctx->comp,
-// group by group: site kernel (pair buffer and scalar moments), gather
-// (force rows, per-atom stress partials), ordered per-structure reduction.
+// group by group:
+//   lin_jac_kernel    per site: the scalar moments and the walk-order values
+//                     of the site Jacobian;
+//   lin_reduce_kernel energy components and species counts per structure;
+//   lin_tile_kernel   one wave per (structure, chunk of scalars): force and
+//                     stress components, each row written once.
+// The tile kernel's launches go by structure size: the LDS tile of a launch
+// holds the force rows of its largest structure, so structures of similar
+// size share a launch; larger structures than one LDS tile holds accumulate
+// in their rows of the output instead.  Every sum has a fixed order.
 int run_lin(mtpx_context *ctx)
 {
     if (!ctx->has_model)
@@ -55,73 +63,114 @@ int run_lin(mtpx_context *ctx)
     HIP_TRY(ctx->comp.ensure(sizeof(double) * std::max<size_t>(cl.total, 1)),
             "allocate components");
     if (cl.total)
-        HIP_TRY(hipMemsetAsync(ctx->comp.p, 0, sizeof(double) * cl.total, s), "clear components");
+        HIP_TRY(launch_fill_zero(ctx->comp.as<double>(), cl.total, s), "clear components");
     if (ctx->n == 0)
         return MTPX_OK;
-    if (int rc = ensure_reverse_index(ctx))
-        return rc;
     const DevModel &m = ctx->dm;
-    const int S = m.S;
-    // doubles per entry of the pair buffer: 3 w_c per chunk (linear_api and
-    // lin_kernel agree on w_c = scalar count rounded up to even)
-    const std::vector<int> &cs0 = ctx->lin.chunk_s0;
-    size_t row = 0;
-    for (size_t c = 0; c + 1 < cs0.size(); ++c)
-        row += 3 * (size_t)((cs0[c + 1] - cs0[c] + 1) & ~1);
-    const size_t per_entry = sizeof(double) * row;
-    const std::vector<int> &off = ctx->offsets_host;
-    const size_t budget = pair_budget();
+    const DevLin &L = ctx->dl;
+    const size_t per_atom = sizeof(double) * ((size_t)L.nwalk + m.S);
+    const size_t budget = group_budget();
+    const std::vector<int> &so = ctx->soff_host;
 
     // groups of whole structures
     struct Range {
         int c0, c1;
     };
     std::vector<Range> groups;
-    size_t max_entries = 1, max_atoms = 1;
+    size_t max_atoms = 1;
     for (int c0 = 0; c0 < ctx->nconf;) {
         int c1 = c0 + 1;
-        auto entries = [&](int cb, int ce) {
-            return (size_t)(off[ctx->soff_host[ce]] - off[ctx->soff_host[cb]]);
-        };
-        while (c1 < ctx->nconf && entries(c0, c1 + 1) * per_entry <= budget)
+        while (c1 < ctx->nconf && (size_t)(so[c1 + 1] - so[c0]) * per_atom <= budget)
             ++c1;
         groups.push_back({c0, c1});
-        max_entries = std::max(max_entries, entries(c0, c1));
-        max_atoms = std::max(max_atoms, (size_t)(ctx->soff_host[c1] - ctx->soff_host[c0]));
+        max_atoms = std::max(max_atoms, (size_t)(so[c1] - so[c0]));
         c0 = c1;
     }
-    HIP_TRY(ctx->lin_pair.ensure(per_entry * max_entries), "allocate pair buffer");
-    HIP_TRY(ctx->lin_site.ensure(sizeof(double) * 10 * (size_t)S * max_atoms),
+    HIP_TRY(ctx->lin_lw.ensure(sizeof(double) * (size_t)L.nwalk * max_atoms),
+            "allocate site Jacobians");
+    HIP_TRY(ctx->lin_site.ensure(sizeof(double) * (size_t)m.S * max_atoms),
             "allocate site rows");
+
+    // Size classes of the tile launches: a class holds the structures of at
+    // most `cap` atoms not held by a smaller class; the last class (cap 0)
+    // takes the structures too large for an LDS tile.
+    const size_t row_bytes = sizeof(double) * (3 * kLinChunk + 1);  // the tile's row stride
+    const size_t base = lin_tile_lds(m, L, 0);
+    int max_rows = ctx->lds_limit > base ? (int)((ctx->lds_limit - base) / row_bytes) : 0;
+    // MTPX_LIN_TILE_ROWS (tests, tuning): a smaller LDS tile; 0 takes every
+    // structure through its output rows
+    if (const char *e = getenv("MTPX_LIN_TILE_ROWS"))
+        max_rows = std::min(max_rows, std::max(0, atoi(e)));
+    std::vector<int> caps;
+    for (int c : {64, 128, 192, 256, 384, 512, 768})
+        if (c < max_rows)
+            caps.push_back(c);
+    if (max_rows > 0)
+        caps.push_back(max_rows);
+    const int ncls = (int)caps.size() + 1;
+    // structure lists of every (group, class), one upload
+    std::vector<int> lists;
+    std::vector<std::vector<int>> cls_off(groups.size(), std::vector<int>(ncls + 1, 0));
+    for (size_t gi = 0; gi < groups.size(); ++gi) {
+        std::vector<std::vector<int>> by((size_t)ncls);
+        for (int c = groups[gi].c0; c < groups[gi].c1; ++c) {
+            const int N = so[c + 1] - so[c];
+            if (N == 0)
+                continue;
+            int k = 0;
+            while (k < (int)caps.size() && N > caps[k])
+                ++k;
+            by[k].push_back(c);
+        }
+        for (int k = 0; k < ncls; ++k) {
+            // largest structures first: the longest waves start first
+            std::stable_sort(by[k].begin(), by[k].end(), [&](int x, int y) {
+                return so[x + 1] - so[x] > so[y + 1] - so[y];
+            });
+            cls_off[gi][k] = (int)lists.size();
+            lists.insert(lists.end(), by[k].begin(), by[k].end());
+        }
+        cls_off[gi][ncls] = (int)lists.size();
+    }
+    HIP_TRY(upload(ctx->lin_tiles, lists, s), "upload structure lists");
 
     double *comp = ctx->comp.as<double>();
     const DevNeighbors nb = dev_neighbors(ctx);
-    for (const Range &r : groups) {
+    for (size_t gi = 0; gi < groups.size(); ++gi) {
+        const Range &r = groups[gi];
         LinGroup g;
         g.c0 = r.c0;
         g.c1 = r.c1;
-        g.a0 = ctx->soff_host[r.c0];
-        g.a1 = ctx->soff_host[r.c1];
-        g.e0 = off[g.a0];
-        g.pg = (int64_t)max_entries;
-        g.nchunks = ctx->dl.nchunks;
-        g.gather_per = (int)((row + kWave - 1) / kWave * kWave);
-        g.chunk_s0 = ctx->dl.chunk_s0;
-        g.pair = ctx->lin_pair.as<double>();
+        g.a0 = so[r.c0];
+        g.a1 = so[r.c1];
         g.site = ctx->lin_site.as<double>();
+        g.lw = ctx->lin_lw.as<double>();
         if (g.a1 > g.a0) {
             EfsLaunch cfg;
-            if (!lin_configure(m, ctx->dl, g.a1 - g.a0, ctx->num_cus, ctx->lds_limit, cfg))
+            if (!lin_configure(m, L, g.a1 - g.a0, ctx->num_cus, ctx->lds_limit, cfg))
                 return set_error(ctx, MTPX_E_CAPACITY,
                                  "model needs more LDS than a CU provides for the linear fit");
-            HIP_TRY(launch_lin_site(m, ctx->dl, nb, g, cfg, s), "launch linear-fit site kernel");
-            HIP_TRY(launch_lin_gather(m, nb, ctx->rev_offsets.as<int>(),
-                                      ctx->rev_pairs.as<int>(), g, comp + cl.fc, s),
-                    "launch linear-fit gather");
+            HIP_TRY(launch_lin_jac(m, L, nb, g, cfg, s), "launch linear-fit site kernel");
         }
         HIP_TRY(launch_lin_reduce(m, ctx->soff.as<int>(), ctx->center_type.as<int>(), g,
-                                  comp + cl.ec, comp + cl.sc, s),
+                                  comp + cl.ec, s),
                 "launch linear-fit reduction");
+        for (int k = ncls - 1; k >= 0; --k) {  // the classes of larger structures first
+            LinTile t;
+            t.structs = ctx->lin_tiles.as<int>() + cls_off[gi][k];
+            t.count = cls_off[gi][k + 1] - cls_off[gi][k];
+            t.nchunks = L.nchunks;
+            const bool lds_tile = k < (int)caps.size();
+            t.rows_cap = lds_tile ? caps[k] : 0;
+            t.soff = ctx->soff.as<int>();
+            t.lw = g.lw;
+            t.a0 = g.a0;
+            t.p = cl.p;
+            t.Z = m.Z;
+            t.fc = comp + cl.fc;
+            t.sc = comp + cl.sc;
+            HIP_TRY(launch_lin_tile(m, L, nb, t, s), "launch linear-fit tile kernel");
+        }
     }
     return MTPX_OK;
 }

@@ -1204,6 +1204,19 @@ bool build_lin_plan(const Model &m, const Plan &p, LinPlan &lp, std::string &err
                 lp.slot_L[at * kLinChunk + k] = li;
             }
         }
+    // every walk's L indices in walk order (slot ascending, then scalar),
+    // chunk after chunk: the values the tile kernel reads per site
+    lp.walk_off.assign(1, 0);
+    lp.walk.clear();
+    for (int c = 0; c < lp.nchunks; ++c) {
+        for (int sl = 0; sl < p.nslots; ++sl) {
+            const size_t at = (size_t)c * p.nslots + sl;
+            for (int k = 0; k < kLinChunk; ++k)
+                if (lp.slot_mask[at] & (1 << k))
+                    lp.walk.push_back(lp.slot_L[at * kLinChunk + k]);
+        }
+        lp.walk_off.push_back((int)lp.walk.size());
+    }
     lp.lane_walk = p.nslots <= 4 * kLinMaskWords && lp.max_chunk_entries <= kLinEntries;
     lp.maskw.assign((size_t)lp.nchunks * kLinMaskWords, 0);
     lp.clist.assign((size_t)lp.nchunks * kLinEntries, lp.one);

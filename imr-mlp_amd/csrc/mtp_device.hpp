@@ -112,6 +112,52 @@ __device__ __forceinline__ double wave_sum(double v)
     return v;
 }
 
+// Sums over the wave of NV values per lane (NV a multiple of 4) in one pass:
+// the wave halves, then the rows, exchange half of their values (lane swaps;
+// a lane keeps the half its position selects and adds its partner's), and
+// each row of 16 sums its NV/4 values over its lanes (DPP).  Lane 16 r + k
+// (k < NV/4) returns the total of value k + (NV/4) (r & 1) + (NV/2) (r >> 1)
+// and sets idx to that index; the other lanes return 0 with idx = -1.
+// About (NV/2 + NV/4) * 3 + (NV/4) * 12 instructions instead of NV * 18 for
+// NV separate wave_sum calls.
+template <int NV>
+__device__ __forceinline__ double wave_reduce_scatter(const double (&v)[NV], int lane, int &idx)
+{
+    static_assert(NV % 4 == 0, "NV must be a multiple of 4");
+    constexpr int H = NV / 2, Q = NV / 4;
+    double u[H], w[Q];
+#pragma unroll
+    for (int k = 0; k < H; ++k) {
+        // lanes < 32 keep value k, lanes >= 32 value k + H
+        const unsigned alo = __double2loint(v[k]), ahi = __double2hiint(v[k]);
+        const unsigned blo = __double2loint(v[k + H]), bhi = __double2hiint(v[k + H]);
+        const auto lo = __builtin_amdgcn_permlane32_swap(alo, blo, false, false);
+        const auto hi = __builtin_amdgcn_permlane32_swap(ahi, bhi, false, false);
+        u[k] = __hiloint2double(hi[0], lo[0]) + __hiloint2double(hi[1], lo[1]);
+    }
+#pragma unroll
+    for (int k = 0; k < Q; ++k) {
+        // even rows keep value k, odd rows value k + Q
+        const unsigned alo = __double2loint(u[k]), ahi = __double2hiint(u[k]);
+        const unsigned blo = __double2loint(u[k + Q]), bhi = __double2hiint(u[k + Q]);
+        const auto lo = __builtin_amdgcn_permlane16_swap(alo, blo, false, false);
+        const auto hi = __builtin_amdgcn_permlane16_swap(ahi, bhi, false, false);
+        double x = __hiloint2double(hi[0], lo[0]) + __hiloint2double(hi[1], lo[1]);
+        x = dpp_add<0xB1>(x);   // quad_perm [1,0,3,2]
+        x = dpp_add<0x4E>(x);   // quad_perm [2,3,0,1]
+        x = dpp_add<0x141>(x);  // row_half_mirror
+        x = dpp_add<0x140>(x);  // row_mirror
+        w[k] = x;
+    }
+    const int r = lane >> 4, k = lane & 15;
+    double out = 0.0;
+#pragma unroll
+    for (int j = 0; j < Q; ++j)
+        out = k == j ? w[j] : out;
+    idx = k < Q ? k + Q * (r & 1) + H * (r >> 1) : -1;
+    return out;
+}
+
 // Orders the LDS accesses of one wave: a wave's LDS operations complete in
 // issue order, so a compiler-level fence at wavefront scope is all that is
 // needed between a lane's store and another lane's load.
@@ -443,8 +489,70 @@ __device__ __forceinline__ void radial_basis(const DevModel &m, int ti, int tj, 
     chebyshev<P::RMAX>(m, d, Q, dQ);
 }
 
-// Geometry plus the radial functions f_mu = sum_k c[ti,tj,mu,k] Q_k and
-// their derivatives (coefficients staged in LDS), zero beyond the cutoff.
+// The fields of list entry p that load_neighbor reads (zeros and type 0 for
+// a lane without an entry), so that a kernel can fetch the next batch's
+// entries ahead of their use; j is the neighbour's atom (-1 without entry).
+struct EntryRaw {
+    double x, y, z, d;
+    int tj, j;
+};
+__device__ __forceinline__ EntryRaw fetch_entry(const DevNeighbors &nb, int64_t p, bool valid)
+{
+    EntryRaw e;
+    e.x = valid ? nb.x[p] : 0.0;
+    e.y = valid ? nb.y[p] : 0.0;
+    e.z = valid ? nb.z[p] : 0.0;
+    e.d = valid ? nb.d[p] : 0.0;
+    e.tj = valid ? nb.type[p] : 0;
+    e.j = valid ? nb.idx[p] : -1;
+    return e;
+}
+
+// Geometry (as load_geometry) plus the radial functions
+// f_mu = sum_k c[ti,tj,mu,k] Q_k and their derivatives (coefficients staged
+// in LDS) of a fetched entry, zero beyond the cutoff.
+template <class P>
+__device__ __forceinline__ void neighbor_from(const DevModel &m, const double *coef_lds, int ti,
+                                              const EntryRaw &e, bool valid, Nbr<P::M> &q)
+{
+    constexpr int RMAX = P::RMAX;
+    const int tj = e.tj;
+    q.x = e.x;
+    q.y = e.y;
+    q.z = e.z;
+    const double rc = pair_cutoff<!P::exact>(m, ti, tj);
+    const double dd = valid ? e.d : rc;
+    const bool in_cutoff = valid && !(dd > rc);
+    const double d = in_cutoff ? dd : rc;
+    q.d = d;
+    q.invd = 1.0 / d;
+    q.ux = q.x * q.invd;
+    q.uy = q.y * q.invd;
+    q.uz = q.z * q.invd;
+    const double w = in_cutoff ? 1.0 : 0.0;
+    double Q[RMAX], dQ[RMAX];
+    radial_basis<P>(m, ti, tj, q.d, Q, dQ);
+    // exact profiles fix M and R at compile time
+    const int R = P::exact ? RMAX : m.R;
+    const double *c = coef_lds + (ti * m.Z + tj) * (P::exact ? P::M : m.M) * R;
+#pragma unroll
+    for (int mu = 0; mu < P::M; ++mu) {
+        double f = 0, fd = 0;
+        if (P::exact || mu < m.M) {
+            const double *cm = c + mu * R;
+#pragma unroll
+            for (int k = 0; k < RMAX; ++k)
+                if (P::exact || k < m.R) {
+                    f += cm[k] * Q[k];
+                    fd += cm[k] * dQ[k];
+                }
+        }
+        q.f[mu] = f * w;
+        q.fd[mu] = fd * w;
+    }
+}
+
+// Geometry plus the radial functions of list entry p.
 template <class P>
 __device__ __forceinline__ void load_neighbor(const DevModel &m, const DevNeighbors &nb,
                                               const double *coef_lds, int ti, int64_t p,

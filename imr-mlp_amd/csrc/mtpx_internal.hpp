@@ -275,6 +275,9 @@ struct LinPlan {
     std::vector<int> slot_L;     // [nchunks][nslots][kLinChunk] L index of each bit
     std::vector<int> maskw;      // [nchunks][kLinMaskWords] slot masks, 4 per word
     std::vector<int> clist;      // [nchunks][kLinEntries] L indices in walk order
+    // the L indices of every chunk's walk in walk order, chunk c at
+    // [walk_off[c], walk_off[c+1]) (any plan; clist holds the same per chunk)
+    std::vector<int> walk, walk_off;
 };
 bool build_lin_plan(const Model &m, const Plan &p, LinPlan &lp, std::string &err);
 
@@ -390,32 +393,41 @@ struct DevLin {
     const int *slot_L;      // [nchunks][nslots][kLinChunk]
     const int *maskw;       // [nchunks][kLinMaskWords]
     const int *clist;       // [nchunks][kLinEntries]
+    const int *walk;        // [nwalk] L work-space indices in walk order, chunk after chunk
+    const int *walk_off;    // [nchunks + 1]
+    int nwalk, max_walk;    // entries of all walks; of the longest chunk's walk
 };
 // One group of whole structures for the linear-fit kernels: atoms
-// [a0, a1), structures [c0, c1), entries from e0; pair buffer
-// [nchunks][entries][3][w_c] (chunk c holds scalars chunk_s0[c] .. and rows
-// of w_c = its scalar count rounded up to even; the plane of chunk c starts
-// at pg 3 sum_{c' < c} w_c', pg entries per plane), site rows
-// [a1 - a0][10][S] (9 stress partials, then the scalar moments).
+// [a0, a1), structures [c0, c1); per site the scalar moments site
+// [a1 - a0][S] and the walk-order Jacobian values lw [a1 - a0][nwalk].
 struct LinGroup {
     int a0, a1, c0, c1;
-    int64_t e0;
-    int64_t pg;
-    int nchunks;
-    int gather_per;       // gather threads per atom: 24 nchunks rounded up to a wave
-    const int *chunk_s0;  // [nchunks + 1]
-    double *pair;
     double *site;
+    double *lw;
+};
+// One launch of the tile kernel: `count` structures of a group, every chunk
+// of each (one wave per structure and chunk), force rows accumulated in LDS
+// tiles of rows_cap atoms (rows_cap 0: in the rows of fc, for structures
+// larger than a tile).
+struct LinTile {
+    const int *structs;   // [count] structures of this launch
+    int count, nchunks, rows_cap;
+    const int *soff;      // [nconf+1] first atom of each structure
+    const double *lw;     // [atoms of the group][nwalk]
+    int a0;               // first atom of the group
+    int p, Z;
+    double *fc, *sc;      // force [N][3][p] and stress [nconf][9][p] components
 };
 bool lin_configure(const DevModel &m, const DevLin &L, int n, int num_cus, size_t lds_limit,
                    EfsLaunch &cfg);
 bool lin_walk_compiled(const LinPlan &lp, int nslots);
-hipError_t launch_lin_site(const DevModel &m, const DevLin &L, const DevNeighbors &nb,
-                           const LinGroup &g, const EfsLaunch &cfg, hipStream_t s);
-hipError_t launch_lin_gather(const DevModel &m, const DevNeighbors &nb, const int *rev_off,
-                             const int *rev_pairs, const LinGroup &g, double *fc, hipStream_t s);
+size_t lin_tile_lds(const DevModel &m, const DevLin &L, int rows);
+hipError_t launch_lin_jac(const DevModel &m, const DevLin &L, const DevNeighbors &nb,
+                          const LinGroup &g, const EfsLaunch &cfg, hipStream_t s);
+hipError_t launch_lin_tile(const DevModel &m, const DevLin &L, const DevNeighbors &nb,
+                           const LinTile &t, hipStream_t s);
 hipError_t launch_lin_reduce(const DevModel &m, const int *soff, const int *center_type,
-                             const LinGroup &g, double *ec, double *sc, hipStream_t s);
+                             const LinGroup &g, double *ec, hipStream_t s);
 hipError_t launch_lin_rows(const double *comp, const int64_t *src, const double *sw,
                            const double *yw, int64_t R, int p, double *A, double *y, hipStream_t s);
 // Gram columns padded to a multiple of 16 (p coefficients plus the target).

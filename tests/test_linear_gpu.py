@@ -126,19 +126,56 @@ def test_linear_system_matches_oracle(ctx, crystal_set, name):
 
 
 def test_components_independent_of_grouping(ctx, crystal_set, monkeypatch):
-    """Structures are processed in groups bounded by a pair-buffer budget
-    (MTPX_LIN_PAIR_MB): a 1 MB budget puts every structure in a group of
-    its own; the components are bitwise those of one group (fixed-order
-    sums, no atomics)."""
+    """Structures are processed in groups bounded by a budget for the sites'
+    Jacobian values (MTPX_LIN_GROUP_MB): a 1 MB budget puts every structure
+    in a group of its own; the components are bitwise those of one group
+    (each row has one writer, which sums in site order)."""
     text, structs, nbs, labels = crystal_set
     _upload(ctx, text, structs, labels, SETTINGS["linear"])
-    monkeypatch.setenv("MTPX_LIN_PAIR_MB", "1")
+    monkeypatch.setenv("MTPX_LIN_GROUP_MB", "1")
     small = ctx.efs_components()
-    monkeypatch.setenv("MTPX_LIN_PAIR_MB", "4096")
+    monkeypatch.setenv("MTPX_LIN_GROUP_MB", "4096")
     big = ctx.efs_components()
     again = ctx.efs_components()
     for a, b, c in zip(small, big, again):
         assert np.array_equal(a, b) and np.array_equal(b, c)
+
+
+def test_components_of_large_structures(ctx, monkeypatch):
+    """Structures of every tile size class, up to 1,372 atoms (beyond what
+    one LDS tile holds, so their rows accumulate in the output itself):
+    components 1e-10 against the oracle; every structure through the
+    output-row path (MTPX_LIN_TILE_ROWS=0) gives the same components to
+    rounding (the two atomic units order the adds of one instruction to the
+    same row, periodic images of one atom, differently) and is repeatable
+    bit for bit, as the default path is."""
+    ref_text, text = S.training_models(4)
+    m = O.Model(text)
+    rng = S.rng_for(91)
+    structs, nbs = [], []
+    for kind, reps in [("fcc", (2, 2, 2)), ("bcc", (4, 4, 5)), ("fcc", (4, 4, 5)),
+                       ("fcc", (5, 5, 5)), ("bcc", (7, 7, 7)), ("fcc", (7, 7, 7))]:
+        s = S.displace(S.lattice(kind, reps, 3.56 if kind == "fcc" else 2.86), rng, 0.1)
+        s.types = (S.uniform(rng, s.n) * 2).astype(np.int32)
+        s.pos = O.wrap(s.cell, s.pbc, s.pos)
+        structs.append(s)
+        nbs.append(O.Neighbors.build(s.cell, s.pbc, s.pos, s.types, 5.0))
+    assert max(s.n for s in structs) > 1000
+    ctx.load_model_text(text)
+    off = ctx.set_structures(structs, 5.0)
+    ec, fc, sc = ctx.efs_components()
+    for c, nb in enumerate(nbs):
+        eo, fo, so = O.efs_components(m, nb)
+        assert rel_err(ec[c], eo) < 1e-10
+        assert rel_err(fc[off[c]:off[c + 1]], fo) < 1e-10
+        assert rel_err(sc[c], so) < 1e-10
+    again = ctx.efs_components()
+    monkeypatch.setenv("MTPX_LIN_TILE_ROWS", "0")
+    rows = ctx.efs_components()
+    rows2 = ctx.efs_components()
+    for a, b, c, d in zip((ec, fc, sc), again, rows, rows2):
+        assert np.array_equal(a, b) and np.array_equal(c, d)
+        assert np.abs(a - c).max() <= 1e-13 * np.abs(a).max()
 
 
 def test_gram_of_the_device_rows(ctx, crystal_set):
