@@ -60,24 +60,39 @@ def efs_flops(model_text: str, n: int, P: int) -> float:
     return float(P) * per_pair + float(n) * per_site
 
 
-def traffic_of(key: str):
-    """HBM bytes per launch of a kernel on a workload, from the calibrated
-    FETCH_SIZE / WRITE_SIZE summaries under profiles/ (None if absent)."""
-    path = os.path.join(ROOT, "profiles", key + "_traffic.json")
-    if os.path.exists(path):
-        return json.load(open(path)).get("hbm_bytes_per_launch")
-    return None
+def traffic_of(*keys: str):
+    """HBM bytes of one launch of a kernel (or, for several keys, of one step
+    that launches each of those kernels as often as its summary's
+    dispatches_per_step says), from the calibrated FETCH_SIZE / WRITE_SIZE
+    summaries under profiles/ (None if one is absent)."""
+    total = 0.0
+    for key in keys:
+        path = os.path.join(ROOT, "profiles", key + "_traffic.json")
+        if not os.path.exists(path):
+            return None
+        js = json.load(open(path))
+        total += js["hbm_bytes_per_launch"] * (js.get("dispatches_per_step", 1) if len(keys) > 1
+                                               else 1)
+    return total
 
 
-def compute_roofline(flops: float, ms: float, kernel: str, traffic_key: str, pipe="fp64 VALU",
+def compute_roofline(flops: float, ms: float, kernel: str, traffic_keys, pipe="fp64 VALU",
                      **extra):
-    """Roofline of an fp64 compute-bound kernel: algorithmic flops per launch
-    over its mean duration against the MI355X fp64 peak (78.6 TFLOP/s for
-    the vector and the matrix pipe alike; "mfma" names the compute roof)."""
+    """Roofline of an fp64 compute-bound kernel (or step): algorithmic flops
+    per launch over its mean duration against the MI355X fp64 peak
+    (78.6 TFLOP/s for the vector and the matrix pipe alike; `bound` names the
+    pipe whose roof applies), and its HBM bytes over the same duration
+    against the 8 TB/s HBM peak."""
     achieved = flops / (ms * 1e-3) / 1e12
-    r = {"bound": "mfma", "achieved": achieved, "peak": FP64_PEAK_TFLOPS, "unit": "TFLOP/s",
-         "frac": achieved / FP64_PEAK_TFLOPS, "traffic": traffic_of(traffic_key),
-         "kernel": kernel, "pipe": pipe, "kernel_ms": ms, "algorithmic_flops_per_launch": flops}
+    keys = (traffic_keys,) if isinstance(traffic_keys, str) else tuple(traffic_keys)
+    traffic = traffic_of(*keys)
+    hbm = None if traffic is None else traffic / (ms * 1e-3) / 1e9
+    r = {"bound": "mfma" if pipe == "fp64 MFMA" else "fp64 VALU", "achieved": achieved,
+         "peak": FP64_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": achieved / FP64_PEAK_TFLOPS,
+         "traffic": traffic, "hbm_gbs": hbm, "hbm_peak_gbs": HBM_PEAK_GBS,
+         "hbm_frac": None if hbm is None else hbm / HBM_PEAK_GBS,
+         "kernel": kernel, "pipe": pipe, "kernel_ms": ms, "algorithmic_flops_per_launch": flops,
+         "traffic_keys": list(keys)}
     r.update(extra)
     return r
 
@@ -251,9 +266,10 @@ def train_bench(ctx, steps: int, warmup: int, nconf: int):
                    "atoms": n, "neighbor_entries": P},
         "roofline": compute_roofline(
             flops, dev_ms, "loss+grad step (efs_kernel, loss_kernel, grad_kernel)",
-            "grad_lvl20_1000", efs_ms=float(np.mean(tims[:, 1])),
+            ("efs_lvl20_1000", "grad_lvl20_1000"), efs_ms=float(np.mean(tims[:, 1])),
             loss_ms=float(np.mean(tims[:, 2])), grad_ms=grad_ms,
-            traffic_kernel="grad_kernel (the step's largest kernel)"),
+            traffic_scope="one step: the E/F/S and gradient kernels (loss and reductions "
+                          "move under 0.1 % of it)"),
         "loss": f,
         "list_build_ms": build_ms,
     }, (start_text, structs, off, tE, tF, tS, cutoff)
@@ -323,10 +339,11 @@ def linear_bench(ctx, steps: int, nconf: int):
                                "configs of 64-256 atoms, weights 1/0.01/0.001" % nconf,
                    "atoms": n, "neighbor_entries": P, "rows": rows, "p": int(G.shape[0])},
         "roofline": compute_roofline(
-            flops, dev_ms, "linear-fit step (lin_site_kernel, lin_gather_kernel, gram_kernel)",
-            "lin_site_lvl16_2000", pipe="fp64 VALU (design rows) + fp64 MFMA (Gram)",
+            flops, dev_ms, "linear-fit step (lin_jac_kernel, lin_tile_kernel, gram_kernel)",
+            ("lin_jac_lvl16_2000", "lin_tile_lvl16_2000", "gram_lvl16_2000"),
+            pipe="fp64 VALU (design rows) + fp64 MFMA (Gram)",
             components_ms=float(np.mean(tims[:, 1])), gram_ms=float(np.mean(tims[:, 2])),
-            traffic_kernel="lin_site_kernel (the step's largest kernel)"),
+            traffic_scope="one step: every kernel of the assembly"),
         "list_build_ms": build_ms,
     }, (start_text, structs, off, tE, tF, tS)
 
@@ -358,14 +375,26 @@ def oracle_module():
 
 
 def host_info():
+    """Host of the CPU baseline: the CPU model as lscpu names it (else
+    /proc/cpuinfo's model name), core counts, OMP_NUM_THREADS."""
+    import subprocess
     model = "unknown"
     try:
-        for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
+        r = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10)
+        for line in r.stdout.splitlines():
+            if line.strip().startswith("Model name:"):
                 model = line.split(":", 1)[1].strip()
                 break
-    except OSError:
+    except (OSError, subprocess.SubprocessError):
         pass
+    if model == "unknown":
+        try:
+            for line in open("/proc/cpuinfo"):
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+        except OSError:
+            pass
     try:
         affinity = len(os.sched_getaffinity(0))
     except AttributeError:
