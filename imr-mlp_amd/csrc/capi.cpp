@@ -305,6 +305,32 @@ int install_model(mtpx_context *ctx, Model &&m)
 
 namespace mtpx {
 
+// Every value finite (no exponent of all ones); branch-free, so the
+// compiler vectorises the pass over the positions.
+bool all_finite(const double *v, size_t n)
+{
+    uint64_t bad = 0;
+    for (size_t i = 0; i < n; ++i) {
+        uint64_t b;
+        std::memcpy(&b, v + i, sizeof b);
+        bad |= (uint64_t)((b & 0x7ff0000000000000ull) == 0x7ff0000000000000ull);
+    }
+    return bad == 0;
+}
+
+// Every species in [0, Z); *maxs receives the largest (-1 for none).
+bool species_in_range(const int *t, size_t n, int Z, int &maxs)
+{
+    unsigned bad = 0;
+    int m = -1;
+    for (size_t i = 0; i < n; ++i) {
+        bad |= (unsigned)((unsigned)t[i] >= (unsigned)Z);
+        m = t[i] > m ? t[i] : m;
+    }
+    maxs = m;
+    return bad == 0;
+}
+
 int map_species(mtpx_context *ctx, const int *types, size_t n, bool allow_unmapped,
                 std::vector<int> &buf, const int *&out)
 {
@@ -379,11 +405,15 @@ int ensure_reverse_index(mtpx_context *ctx)
 
 int set_single_structure(mtpx_context *ctx)
 {
-    ctx->nconf = 1;
-    ctx->soff_host = {0, ctx->n};
     ctx->has_batch_out = false;
     ctx->has_adjoints = false;
     ctx->has_labels = false;
+    // the device tables of one structure of n atoms are still in place
+    if (ctx->single_n == ctx->n && ctx->nconf == 1)
+        return MTPX_OK;
+    ctx->single_n = -1;
+    ctx->nconf = 1;
+    ctx->soff_host = {0, ctx->n};
     HIP_TRY(upload(ctx->soff, ctx->soff_host, ctx->stream), "upload structure offsets");
     HIP_TRY(ctx->center_structure.ensure(sizeof(int) * std::max(ctx->n, 1)),
             "allocate structure index");
@@ -391,6 +421,7 @@ int set_single_structure(mtpx_context *ctx)
                            ctx->stream),
             "clear structure index");
     HIP_TRY(hipStreamSynchronize(ctx->stream), "upload structure offsets");
+    ctx->single_n = ctx->n;
     return MTPX_OK;
 }
 
@@ -469,7 +500,7 @@ int run_efs(mtpx_context *ctx, bool deterministic, bool site_virial, bool energy
     }
     DevNeighbors nb = dev_neighbors(ctx);
     if (!deterministic && !energy_only && n > 0)
-        HIP_TRY(hipMemsetAsync(out.forces, 0, sizeof(double) * 3 * n, s), "clear forces");
+        HIP_TRY(launch_fill_zero(out.forces, 3 * (size_t)n, s), "clear forces");
     HIP_TRY(hipEventRecord(ctx->ev[0], s), "record event");
     if (n > 0)
         HIP_TRY(launch_efs(ctx->dm, nb, out, cfg,
@@ -939,19 +970,15 @@ int mtpx_build_neighbors(mtpx_context *ctx, const double cell[9], const int pbc[
     for (int i = 0; i < 9; ++i)
         if (!std::isfinite(cell[i]))
             return set_error(ctx, MTPX_E_INVALID, "non-finite cell");
-    for (int i = 0; i < 3 * n; ++i)
-        if (!std::isfinite(pos[i]))
-            return set_error(ctx, MTPX_E_INVALID, "non-finite position");
+    if (!all_finite(pos, 3 * (size_t)n))
+        return set_error(ctx, MTPX_E_INVALID, "non-finite position");
     std::vector<int> tbuf;
     if (int rc = map_species(ctx, types, (size_t)n, false, tbuf, types))
         return rc;
     const int Z = ctx->has_model ? ctx->model.Z : 1 << 30;
     int maxs = -1;
-    for (int i = 0; i < n; ++i) {
-        if (types[i] < 0 || types[i] >= Z)
-            return set_error(ctx, MTPX_E_INVALID, "species out of range");
-        maxs = std::max(maxs, types[i]);
-    }
+    if (!species_in_range(types, (size_t)n, Z, maxs))
+        return set_error(ctx, MTPX_E_INVALID, "species out of range");
     (void)hipSetDevice(ctx->device);
     ctx->has_nbh = false;
     ctx->rev_ready = false;

@@ -49,6 +49,7 @@ struct mtpx_context {
     int nconf = 0;
     std::vector<int> soff_host;          // [nconf+1] first atom of each structure
     DBuf soff, center_structure;         // device copies; [N] structure of each atom
+    int single_n = -1;  // soff and center_structure describe one structure of this many atoms
 
     // outputs
     DBuf forces, site_energy, partial, pair_ders, out10;
@@ -176,6 +177,11 @@ inline int need_linear(mtpx_context *ctx, const char *what)
 // validate_potential_view's checks; on failure code and err are set.
 bool model_from_view(const mtpx_model_view &v, Model &m, std::vector<int> &spmap, int &code,
                      std::string &err);
+
+// Every value finite (branch-free, vectorised).
+bool all_finite(const double *v, size_t n);
+// Every species in [0, Z); maxs receives the largest (-1 for none).
+bool species_in_range(const int *t, size_t n, int Z, int &maxs);
 
 // Caller atom types -> species through the loaded model's species map.
 // Without an explicit map (text or GPM loads) `out` is `types` itself and

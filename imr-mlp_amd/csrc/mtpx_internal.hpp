@@ -50,6 +50,35 @@ struct DBuf {
     }
 };
 
+// Pinned host memory (hipHostMalloc) for uploads and read-backs that the
+// stream runs asynchronously; growing it assumes that no copy from or into
+// it is still queued.
+struct HBuf {
+    void *p = nullptr;
+    size_t bytes = 0;
+    hipError_t ensure(size_t need)
+    {
+        if (need <= bytes && p)
+            return hipSuccess;
+        release();
+        const size_t want = need < 4096 ? 4096 : need;
+        hipError_t e = hipHostMalloc(&p, want, 0);
+        if (e == hipSuccess)
+            bytes = want;
+        else
+            p = nullptr;
+        return e;
+    }
+    template <class T> T *as() const { return static_cast<T *>(p); }
+    void release()
+    {
+        if (p)
+            (void)hipHostFree(p);
+        p = nullptr;
+        bytes = 0;
+    }
+};
+
 // Resident neighbour lists (SoA) and the builder's scratch.
 struct NeighborStore {
     int n = 0;
@@ -57,19 +86,27 @@ struct NeighborStore {
     DBuf offsets, idx, type, x, y, z, d, center_type;
 };
 struct NeighborScratch {
-    DBuf pos, types, pts, orig, flags, scan, tmp, minmax, box, box_start, box_cur,
-        box_items, rank, cnt, cursor, key, st_idx, st_type, st_vec, st_d, scalars;
-    // per-structure tables of a batch (atom offsets, wrap flags and cells;
-    // candidate, box, interior-box and flag offsets, geometry and image
-    // candidates; image counts; point offsets) and the wrapped positions
+    DBuf pts, orig, flags, scan, tmp, minmax, box, box_start, box_cur, box_items, rank, cnt,
+        cursor, key, st_idx, st_type, st_vec, st_d, scalars;
+    // per-structure tables of a batch with the positions and species (atom
+    // offsets, wrap flags and cells; candidate, box, interior-box and flag
+    // offsets, geometry and image candidates; image counts; point offsets)
+    // and the wrapped positions
     DBuf seg_head, seg_tabs, seg_imgs, seg_pts, wrapped;
+    // pinned staging of the two uploads and of the read-backs
+    HBuf up_head, up_tabs, down;
+    // entries per atom that the staging of a one-pass build reserves (0: none
+    // known yet); set from the longest list of the last counted build
+    long long bin_cap = 0;
     void release_all()
     {
-        for (DBuf *b : {&pos, &types, &pts, &orig, &flags, &scan, &tmp, &minmax, &box,
-                        &box_start, &box_cur, &box_items, &rank, &cnt, &cursor, &key, &st_idx,
-                        &st_type, &st_vec, &st_d, &scalars, &seg_head, &seg_tabs, &seg_imgs,
-                        &seg_pts, &wrapped})
+        for (DBuf *b : {&pts, &orig, &flags, &scan, &tmp, &minmax, &box, &box_start, &box_cur,
+                        &box_items, &rank, &cnt, &cursor, &key, &st_idx, &st_type, &st_vec,
+                        &st_d, &scalars, &seg_head, &seg_tabs, &seg_imgs, &seg_pts, &wrapped})
             b->release();
+        for (HBuf *b : {&up_head, &up_tabs, &down})
+            b->release();
+        bin_cap = 0;
     }
 };
 // Builds the lists on the device (neighbors.hip); returns an MTPX_* code.

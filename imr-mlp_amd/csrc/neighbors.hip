@@ -86,7 +86,9 @@ __global__ void box_rank_kernel(const int *box, const int *box_start, const int 
 // Rank every staged entry within its list by key and write it to its final
 // slot (SoA).  One wave per list: lanes take 64 entries at a time and count
 // the list's smaller keys, read 64 at a time and broadcast lane by lane
-// (keys within a list are distinct).
+// (keys within a list are distinct).  The staged entries of list l lie at
+// its final offsets (cap == 0) or in its bin from l cap; with bins, a set
+// overflow flag means the staging is incomplete and nothing is written.
 __device__ __forceinline__ uint64_t readlane_u64(uint64_t v, int l)
 {
     const unsigned lo = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)v, l);
@@ -94,50 +96,50 @@ __device__ __forceinline__ uint64_t readlane_u64(uint64_t v, int l)
     return ((uint64_t)hi << 32) | lo;
 }
 
-__global__ __launch_bounds__(256) void list_rank_kernel(const int *offsets, int n,
-                                                        const uint64_t *key, const int *st_idx,
-                                                        const int *st_type, const double *st_vec,
-                                                        const double *st_d, int *idx, int *type,
-                                                        double *x, double *y, double *z, double *d)
+__global__ __launch_bounds__(256) void list_rank_kernel(const int *offsets, int n, int cap,
+                                                        const int *overflow, const uint64_t *key,
+                                                        const int *st_idx, const int *st_type,
+                                                        const double *st_vec, const double *st_d,
+                                                        int *idx, int *type, double *x, double *y,
+                                                        double *z, double *d)
 {
     const int lane = threadIdx.x & 63;
     const int l = blockIdx.x * (blockDim.x / 64) + threadIdx.x / 64;
-    if (l >= n)
+    if (l >= n || (overflow && *overflow))
         return;  // uniform over the wave
-    const int s = offsets[l], e = offsets[l + 1];
-    for (int q0 = s; q0 < e; q0 += 64) {
-        const int q = q0 + lane;
-        const uint64_t k = q < e ? key[q] : 0;
+    const int s = offsets[l], cnt = offsets[l + 1] - s;
+    const int64_t sb = cap ? (int64_t)l * cap : s;  // the list's first staged entry
+    for (int j0 = 0; j0 < cnt; j0 += 64) {
+        const int j = j0 + lane;
+        const int64_t q = sb + j;
+        const uint64_t k = j < cnt ? key[q] : 0;
         int r = 0;
-        for (int u0 = s; u0 < e; u0 += 64) {
-            const uint64_t ku = u0 + lane < e ? key[u0 + lane] : 0;
-            const int m = e - u0 < 64 ? e - u0 : 64;
-            for (int j = 0; j < m; ++j)
-                r += readlane_u64(ku, j) < k;
+        for (int u0 = 0; u0 < cnt; u0 += 64) {
+            const uint64_t ku = u0 + lane < cnt ? key[sb + u0 + lane] : 0;
+            const int m = cnt - u0 < 64 ? cnt - u0 : 64;
+            for (int u = 0; u < m; ++u)
+                r += readlane_u64(ku, u) < k;
         }
-        if (q < e) {
+        if (j < cnt) {
             const int64_t o = s + r;
             idx[o] = st_idx[q];
             type[o] = st_type[q];
-            x[o] = st_vec[3 * (int64_t)q];
-            y[o] = st_vec[3 * (int64_t)q + 1];
-            z[o] = st_vec[3 * (int64_t)q + 2];
+            x[o] = st_vec[3 * q];
+            y[o] = st_vec[3 * q + 1];
+            z[o] = st_vec[3 * q + 2];
             d[o] = st_d[q];
         }
     }
 }
 
-__global__ void gather_types_kernel(const int *types, int n, int *center_type)
-{
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < n)
-        center_type[i] = types[i];
-}
-
 // ---- exclusive scan of int32 (three passes) ---------------------------
 constexpr int kScanBlock = 256, kScanItems = 8, kScanTile = kScanBlock * kScanItems;
 
-__global__ __launch_bounds__(kScanBlock) void scan_tile_sums(const int *in, int64_t n, int *sums)
+// Every scan reads min(in[i], clamp): the per-list counts of a one-pass
+// build are taken up to their bin size, which keeps the sums in int32 when
+// a list has outgrown its bin (that build is then discarded).
+__global__ __launch_bounds__(kScanBlock) void scan_tile_sums(const int *in, int64_t n, int clamp,
+                                                             int *sums)
 {
     __shared__ int buf[kScanBlock];
     const int64_t base = (int64_t)blockIdx.x * kScanTile;
@@ -145,7 +147,7 @@ __global__ __launch_bounds__(kScanBlock) void scan_tile_sums(const int *in, int6
     for (int k = 0; k < kScanItems; ++k) {
         const int64_t i = base + (int64_t)k * kScanBlock + threadIdx.x;
         if (i < n)
-            s += in[i];
+            s += min(in[i], clamp);
     }
     buf[threadIdx.x] = s;
     __syncthreads();
@@ -187,7 +189,7 @@ __global__ __launch_bounds__(1024) void scan_sums(int *sums, int ntiles, int *to
         *total = carry;
 }
 
-__global__ __launch_bounds__(kScanBlock) void scan_tiles(const int *in, int64_t n,
+__global__ __launch_bounds__(kScanBlock) void scan_tiles(const int *in, int64_t n, int clamp,
                                                           const int *sums, int *out, int *out2)
 {
     __shared__ int buf[kScanBlock];
@@ -195,7 +197,7 @@ __global__ __launch_bounds__(kScanBlock) void scan_tiles(const int *in, int64_t 
     int v[kScanItems];
     int s = 0;
     for (int k = 0; k < kScanItems; ++k) {
-        v[k] = base + k < n ? in[base + k] : 0;
+        v[k] = base + k < n ? min(in[base + k], clamp) : 0;
         s += v[k];
     }
     buf[threadIdx.x] = s;
@@ -217,87 +219,131 @@ __global__ __launch_bounds__(kScanBlock) void scan_tiles(const int *in, int64_t 
     }
 }
 
-// 64-bit sum of n non-negative ints into *total (zeroed by the caller): the
-// list-length total, checked against the int32 entry indices before any
-// offset is trusted.
+// 64-bit sum of n non-negative ints into *total and their maximum into
+// *largest (both zeroed by the caller): the list-length total, checked
+// against the int32 entry indices before any offset is trusted, and the
+// longest list, which sizes the bins of the next build.
 __global__ __launch_bounds__(256) void sum64_kernel(const int *in, int64_t n,
-                                                    unsigned long long *total)
+                                                    unsigned long long *total, int *largest)
 {
     __shared__ unsigned long long buf[256];
+    __shared__ int big[256];
     unsigned long long s = 0;
-    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256)
+    int mx = 0;
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n;
+         i += (int64_t)gridDim.x * 256) {
         s += (unsigned)in[i];
+        mx = max(mx, in[i]);
+    }
     buf[threadIdx.x] = s;
+    big[threadIdx.x] = mx;
     __syncthreads();
     for (int w = 128; w >= 1; w >>= 1) {
-        if ((int)threadIdx.x < w)
+        if ((int)threadIdx.x < w) {
             buf[threadIdx.x] += buf[threadIdx.x + w];
+            big[threadIdx.x] = max(big[threadIdx.x], big[threadIdx.x + w]);
+        }
         __syncthreads();
     }
-    if (threadIdx.x == 0)
+    if (threadIdx.x == 0) {
         atomicAdd(total, buf[0]);
+        atomicMax(largest, big[0]);
+    }
 }
 
-// Exclusive scan of up to kScan1Max values in one workgroup of 16 waves:
-// wave w owns values [w 64 m, (w+1) 64 m) and reads them 64 at a time
-// (coalesced); a first pass sums each wave's values, a second scans them
-// 64 at a time after the sums of the waves before.  One launch instead of
-// three.
-constexpr int kScan1Waves = 16, kScan1Max = kScan1Waves * 64 * 64;
-
-__global__ __launch_bounds__(kScan1Waves * 64) void scan_one_block(const int *in, int n, int m,
-                                                                   int *out, int *out2,
-                                                                   int *total)
+// Inclusive prefix sum over the 64 lanes of a wave: rows of 16 by DPP row
+// shifts (lanes without a source add 0), then each row adds the totals of
+// the rows before it (lane reads).
+__device__ __forceinline__ int wave_incl_scan(int x, int lane)
 {
-    __shared__ int wsum[kScan1Waves];
+    x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xf, 0xf, false);  // row_shr:1
+    x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xf, 0xf, false);  // row_shr:2
+    x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xf, 0xf, false);  // row_shr:4
+    x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xf, 0xf, false);  // row_shr:8
+    const int t0 = __builtin_amdgcn_readlane(x, 15), t1 = __builtin_amdgcn_readlane(x, 31),
+              t2 = __builtin_amdgcn_readlane(x, 47);
+    const int r = lane >> 4;
+    return x + (r >= 1 ? t0 : 0) + (r >= 2 ? t1 : 0) + (r >= 3 ? t2 : 0);
+}
+
+// One-workgroup scans use 1,024 threads (16 waves).
+constexpr int kScan1Threads = 1024, kScan1Waves = kScan1Threads / 64;
+
+// Exclusive prefix of one value per thread over such a workgroup (thread
+// order); tot receives the workgroup's total.
+__device__ __forceinline__ int block_excl_scan(int v, int *wsum, int &tot)
+{
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-    const int base = wv * 64 * m;
-    int s = 0;
-    for (int k = 0; k < m; ++k) {
-        const int i = base + k * 64 + lane;
-        if (i < n)
-            s += in[i];
-    }
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1)
-        s += __shfl_xor(s, o);
-    if (lane == 0)
-        wsum[wv] = s;
+    const int x = wave_incl_scan(v, lane);
+    if (lane == 63)
+        wsum[wv] = x;
     __syncthreads();
     int carry = 0;
-    for (int k = 0; k < wv; ++k)
-        carry += wsum[k];
-    for (int k = 0; k < m; ++k) {
-        const int i = base + k * 64 + lane;
-        const int v = i < n ? in[i] : 0;
-        int x = v;
-#pragma unroll
-        for (int o = 1; o < 64; o <<= 1) {
-            const int u = __shfl_up(x, o);
-            if (lane >= o)
-                x += u;
-        }
-        if (i < n) {
-            out[i] = carry + x - v;
-            if (out2)
-                out2[i] = carry + x - v;
-        }
-        carry += __shfl(x, 63);
+    tot = 0;
+    for (int k = 0; k < kScan1Waves; ++k) {
+        const int w = wsum[k];
+        carry += k < wv ? w : 0;
+        tot += w;
     }
-    if (threadIdx.x == kScan1Waves * 64 - 1)
-        *total = carry;
+    return carry + x - v;
+}
+
+// Exclusive scan of up to kScanLdsMax values in one workgroup through LDS:
+// the values go in with coalesced loads (slot i + i / 32, so that threads
+// reading consecutive runs hit distinct banks), thread t scans the run
+// [t m, (t+1) m) after the prefix of the runs before it, and the prefixes
+// go out with coalesced stores.  Every value is read before any is written,
+// so out and out2 may be in.  One launch instead of three.
+constexpr int kScanLdsMax = 36864;
+
+__host__ __device__ constexpr size_t scan_lds_bytes(int n)
+{
+    return sizeof(int) * ((size_t)n + (size_t)n / 32 + 1);
+}
+
+__global__ __launch_bounds__(kScan1Threads) void scan_one_block(const int *in, int n, int clamp,
+                                                                int *out, int *out2, int *total)
+{
+    extern __shared__ int buf[];
+    __shared__ int wsum[kScan1Waves];
+    const int t = threadIdx.x;
+#pragma unroll 8
+    for (int i = t; i < n; i += kScan1Threads)
+        buf[i + (i >> 5)] = min(in[i], clamp);
+    __syncthreads();
+    const int m = (n + kScan1Threads - 1) / kScan1Threads;
+    const int b0 = min(n, t * m), b1 = min(n, b0 + m);
+    int sum = 0;
+    for (int i = b0; i < b1; ++i)
+        sum += buf[i + (i >> 5)];
+    int tot;
+    int run = block_excl_scan(sum, wsum, tot);
+    for (int i = b0; i < b1; ++i) {
+        const int v = buf[i + (i >> 5)];
+        buf[i + (i >> 5)] = run;
+        run += v;
+    }
+    __syncthreads();
+#pragma unroll 8
+    for (int i = t; i < n; i += kScan1Threads) {
+        const int v = buf[i + (i >> 5)];
+        out[i] = v;
+        if (out2)
+            out2[i] = v;
+    }
+    if (t == 0)
+        *total = tot;
 }
 
 // Exclusive scan into out (and out2 when given, which may be in: every
 // value is read before its slot is written); *total receives the sum
 // (device); returns the error.
 hipError_t scan_exclusive(const int *in, int64_t n, int *out, DBuf &tmp, int *total,
-                          hipStream_t s, int *out2 = nullptr)
+                          hipStream_t s, int *out2 = nullptr, int clamp = INT_MAX)
 {
-    if (n <= kScan1Max) {
-        const int m = (int)std::max<int64_t>(1, (n + kScan1Waves * 64 - 1) / (kScan1Waves * 64));
-        hipLaunchKernelGGL(scan_one_block, dim3(1), dim3(kScan1Waves * 64), 0, s, in, (int)n, m,
-                           out, out2, total);
+    if (n <= kScanLdsMax) {
+        hipLaunchKernelGGL(scan_one_block, dim3(1), dim3(kScan1Threads), scan_lds_bytes((int)n), s,
+                           in, (int)n, clamp, out, out2, total);
         return hipGetLastError();
     }
     const int64_t ntiles = std::max<int64_t>(1, (n + kScanTile - 1) / kScanTile);
@@ -305,9 +351,9 @@ hipError_t scan_exclusive(const int *in, int64_t n, int *out, DBuf &tmp, int *to
     if (e != hipSuccess)
         return e;
     hipLaunchKernelGGL(scan_tile_sums, dim3((unsigned)ntiles), dim3(kScanBlock), 0, s, in, n,
-                       tmp.as<int>());
+                       clamp, tmp.as<int>());
     hipLaunchKernelGGL(scan_sums, dim3(1), dim3(1024), 0, s, tmp.as<int>(), (int)ntiles, total);
-    hipLaunchKernelGGL(scan_tiles, dim3((unsigned)ntiles), dim3(kScanBlock), 0, s, in, n,
+    hipLaunchKernelGGL(scan_tiles, dim3((unsigned)ntiles), dim3(kScanBlock), 0, s, in, n, clamp,
                        tmp.as<int>(), out, out2);
     return hipGetLastError();
 }
@@ -567,13 +613,15 @@ __device__ __forceinline__ int seg_of(const T *off, int n, T k)
     return lo;
 }
 
-// load_positions (neighborhoods_base.h:113-127) and the AABB.  Workgroup k
+// load_positions (neighborhoods_base.h:113-127) and the AABB; the centres'
+// species are copied on the way.  Workgroup k
 // of structure c (B per structure) wraps the atoms [k m, (k+1) m) of it,
 // m = ceil(n_c / B), into the cell if the structure is fully periodic, and
 // writes their component-wise min and max (+inf / -inf for an empty range);
 // the host takes the min / max of the B partials.  Min and max are exact.
-__global__ __launch_bounds__(256) void wrap_minmax_kernel(Seg g, const double *pos, int B,
-                                                          double *wr, double *part)
+__global__ __launch_bounds__(256) void wrap_minmax_kernel(Seg g, const double *pos,
+                                                          const int *types, int B, double *wr,
+                                                          double *part, int *center_type)
 {
     __shared__ double lo[256][3], hi[256][3];
     const int c = blockIdx.x / B, k = blockIdx.x % B, t = threadIdx.x;
@@ -585,6 +633,7 @@ __global__ __launch_bounds__(256) void wrap_minmax_kernel(Seg g, const double *p
     double l[3] = {__builtin_inf(), __builtin_inf(), __builtin_inf()};
     double h[3] = {-__builtin_inf(), -__builtin_inf(), -__builtin_inf()};
     for (int i = i0 + t; i < i1; i += 256) {
+        center_type[a0 + i] = types[a0 + i];
         const size_t q = 3 * (size_t)(a0 + i);
         double p[3] = {pos[q], pos[q + 1], pos[q + 2]};
         if (wrap) {
@@ -623,13 +672,10 @@ __global__ __launch_bounds__(256) void wrap_minmax_kernel(Seg g, const double *p
     }
 }
 
-// flag[k] = image q of atom i of structure c lies in [lo - rc, hi + rc]
+// flag k = image q of atom i of structure c lies in [lo - rc, hi + rc]
 // (append_images, neighborhoods_base.h:72-80); k - flag_off[c] = q n_c + i.
-__global__ void image_flag_kernel(Seg g, const double *wr, long long total, int *flags)
+__device__ __forceinline__ int image_flag_at(const Seg &g, const double *wr, long long k)
 {
-    const long long k = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-    if (k >= total)
-        return;
     const int c = seg_of(g.flag_off, g.nconf, k);
     const int a0 = g.atom_off[c], n = g.atom_off[c + 1] - a0;
     const long long kk = k - g.flag_off[c];
@@ -641,68 +687,132 @@ __global__ void image_flag_kernel(Seg g, const double *wr, long long total, int 
     const bool out = p0 < b.lo[0] - b.cutoff || p1 < b.lo[1] - b.cutoff ||
                      p2 < b.lo[2] - b.cutoff || p0 > b.hi[0] + b.cutoff ||
                      p1 > b.hi[1] + b.cutoff || p2 > b.hi[2] + b.cutoff;
-    flags[k] = out ? 0 : 1;
+    return out ? 0 : 1;
+}
+
+__global__ void image_flag_kernel(Seg g, const double *wr, long long total, int *flags)
+{
+    const long long k = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (k < total)
+        flags[k] = image_flag_at(g, wr, k);
+}
+
+// The flags of one scan tile per workgroup (the tiles of scan_tile_sums)
+// and the tile's sum, so the scan needs two more launches, not three.
+__global__ __launch_bounds__(kScanBlock) void image_flag_tiles_kernel(Seg g, const double *wr,
+                                                                      long long total,
+                                                                      int *flags, int *sums)
+{
+    __shared__ int buf[kScanBlock];
+    const long long base = (long long)blockIdx.x * kScanTile;
+    int s = 0;
+    for (int k = 0; k < kScanItems; ++k) {
+        const long long i = base + (long long)k * kScanBlock + threadIdx.x;
+        if (i < total) {
+            const int f = image_flag_at(g, wr, i);
+            flags[i] = f;
+            s += f;
+        }
+    }
+    buf[threadIdx.x] = s;
+    __syncthreads();
+    for (int w = kScanBlock / 2; w >= 1; w >>= 1) {
+        if ((int)threadIdx.x < w)
+            buf[threadIdx.x] += buf[threadIdx.x + w];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0)
+        sums[blockIdx.x] = buf[0];
 }
 
 // points of each structure: its atoms and its images (the flags' exclusive
 // scan at its end less at its start); entry nconf is 0, so an exclusive scan
 // gives the point offsets and the point total
+__device__ __forceinline__ int point_count_of(const Seg &g, const int *flags, const int *scan,
+                                              int c)
+{
+    if (c >= g.nconf)
+        return 0;
+    const long long f0 = g.flag_off[c], f1 = g.flag_off[c + 1];
+    const int nimg = f1 == f0 ? 0 : scan[f1 - 1] + flags[f1 - 1] - scan[f0];
+    return g.atom_off[c + 1] - g.atom_off[c] + nimg;
+}
+
 __global__ void point_count_kernel(Seg g, const int *flags, const int *scan, int *count)
 {
     const int c = blockIdx.x * blockDim.x + threadIdx.x;
-    if (c > g.nconf)
-        return;
-    if (c == g.nconf) {
-        count[c] = 0;
-        return;
-    }
-    const long long f0 = g.flag_off[c], f1 = g.flag_off[c + 1];
-    const int nimg = f1 == f0 ? 0 : scan[f1 - 1] + flags[f1 - 1] - scan[f0];
-    count[c] = g.atom_off[c + 1] - g.atom_off[c] + nimg;
+    if (c <= g.nconf)
+        count[c] = point_count_of(g, flags, scan, c);
 }
 
-// originals: point pt_off[c] + i is atom a0 + i; the grid also clears the
-// box counters [nz1] and the list counters [nz2] and *z64 for the launches
-// after it (fewer launches than separate fills)
-__global__ void points_kernel(Seg g, const double *wr, int ntot, double *pts, int *orig, int *z1,
-                              int nz1, int *z2, int nz2, unsigned long long *z64)
+// The point offsets [nconf + 1] in one workgroup (nconf + 1 <= 8 x 1,024):
+// thread t counts the structures [t m, (t+1) m) and the counts are scanned.
+constexpr int kOffsetsPerThread = 8;
+
+__global__ __launch_bounds__(kScan1Threads) void point_offsets_kernel(Seg g, const int *flags,
+                                                                     const int *scan,
+                                                                     int *pt_off)
 {
-    const int a = blockIdx.x * blockDim.x + threadIdx.x;
-    const int stride = gridDim.x * blockDim.x;
-    for (int k = a; k < nz1; k += stride)
-        z1[k] = 0;
-    for (int k = a; k < nz2; k += stride)
-        z2[k] = 0;
-    if (a == 0)
-        *z64 = 0;
-    if (a >= ntot)
-        return;
-    const int c = seg_of(g.atom_off, g.nconf, a);
-    const int q = g.pt_off[c] + (a - g.atom_off[c]);
-    pts[3 * (size_t)q] = wr[3 * (size_t)a];
-    pts[3 * (size_t)q + 1] = wr[3 * (size_t)a + 1];
-    pts[3 * (size_t)q + 2] = wr[3 * (size_t)a + 2];
-    orig[q] = a;
+    __shared__ int wsum[kScan1Waves];
+    const int n = g.nconf + 1;
+    const int m = (n + kScan1Threads - 1) / kScan1Threads;
+    const int c0 = threadIdx.x * m;
+    int v[kOffsetsPerThread], sum = 0;
+#pragma unroll
+    for (int j = 0; j < kOffsetsPerThread; ++j) {
+        v[j] = j < m && c0 + j < n ? point_count_of(g, flags, scan, c0 + j) : 0;
+        sum += v[j];
+    }
+    int tot;
+    int run = block_excl_scan(sum, wsum, tot);
+#pragma unroll
+    for (int j = 0; j < kOffsetsPerThread; ++j)
+        if (j < m && c0 + j < n) {
+            pt_off[c0 + j] = run;
+            run += v[j];
+        }
 }
 
-__global__ void image_write_kernel(Seg g, const double *wr, long long total,
-                                         const int *flags, const int *scan, double *pts,
-                                         int *orig)
+// Thread k: the original point pt_off[c] + i = atom a0 + i (k < ntot) and
+// the image of flag k when it is set (k < nflags); the grid also clears the
+// box counters [nz1], the list counters [nz2], *z64 and z3[0 .. 3] for the
+// launches after it (fewer launches than separate fills).
+__global__ void points_kernel(Seg g, const double *wr, int ntot, long long nflags,
+                              const int *flags, const int *scan, double *pts, int *orig, int *z1,
+                              int nz1, int *z2, int nz2, unsigned long long *z64, int *z3)
 {
     const long long k = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-    if (k >= total || !flags[k])
-        return;
-    const int c = seg_of(g.flag_off, g.nconf, k);
-    const int a0 = g.atom_off[c], n = g.atom_off[c + 1] - a0;
-    const long long kk = k - g.flag_off[c];
-    const int q = (int)(kk / n), i = (int)(kk % n);
-    const double *t = g.cand + 3 * (size_t)(g.cand_off[c] + q);
-    const double *w = wr + 3 * (size_t)(a0 + i);
-    const size_t o = (size_t)g.pt_off[c] + n + (scan[k] - scan[g.flag_off[c]]);
-    pts[3 * o] = w[0] + t[0];
-    pts[3 * o + 1] = w[1] + t[1];
-    pts[3 * o + 2] = w[2] + t[2];
-    orig[o] = a0 + i;
+    const long long stride = (long long)gridDim.x * blockDim.x;
+    for (long long j = k; j < nz1; j += stride)
+        z1[j] = 0;
+    for (long long j = k; j < nz2; j += stride)
+        z2[j] = 0;
+    if (k == 0)
+        *z64 = 0;
+    if (k < 4)
+        z3[k] = 0;
+    if (k < ntot) {
+        const int a = (int)k;
+        const int c = seg_of(g.atom_off, g.nconf, a);
+        const int q = g.pt_off[c] + (a - g.atom_off[c]);
+        pts[3 * (size_t)q] = wr[3 * (size_t)a];
+        pts[3 * (size_t)q + 1] = wr[3 * (size_t)a + 1];
+        pts[3 * (size_t)q + 2] = wr[3 * (size_t)a + 2];
+        orig[q] = a;
+    }
+    if (k < nflags && flags[k]) {
+        const int c = seg_of(g.flag_off, g.nconf, k);
+        const int a0 = g.atom_off[c], n = g.atom_off[c + 1] - a0;
+        const long long kk = k - g.flag_off[c];
+        const int q = (int)(kk / n), i = (int)(kk % n);
+        const double *t = g.cand + 3 * (size_t)(g.cand_off[c] + q);
+        const double *w = wr + 3 * (size_t)(a0 + i);
+        const size_t o = (size_t)g.pt_off[c] + n + (scan[k] - scan[g.flag_off[c]]);
+        pts[3 * o] = w[0] + t[0];
+        pts[3 * o + 1] = w[1] + t[1];
+        pts[3 * o + 2] = w[2] + t[2];
+        orig[o] = a0 + i;
+    }
 }
 
 // Box index (neighborhoods_base.h:179-224): ceil(tp * (bl - 2) / xd), originals
@@ -747,34 +857,29 @@ __device__ __forceinline__ int interior_box(const SegGeom &b, int w)
     return (i * b.bl[1] + j) * b.bl[2] + k;
 }
 
-// Originals per interior box, in the lexicographic walk order of construct().
-__global__ void interior_count_kernel(Seg g, const int *box_start, const int *items,
-                                            int nint, int *count)
+// Originals in interior box w (walk order over the chunk), and its box
+// within the structure (bl) and over the chunk (gb).
+__device__ __forceinline__ int interior_originals(const Seg &g, const int *box_start,
+                                                  const int *items, int w, int &c, int &bl,
+                                                  int &gb)
 {
-    const int w = blockIdx.x * blockDim.x + threadIdx.x;
-    if (w >= nint)
-        return;
-    const int c = seg_of(g.int_off, g.nconf, w);
-    const int gb = g.box_off[c] + interior_box(g.geo[c], w - g.int_off[c]);
+    c = seg_of(g.int_off, g.nconf, w);
+    bl = interior_box(g.geo[c], w - g.int_off[c]);
+    gb = g.box_off[c] + bl;
     const int lim = g.pt_off[c] + (g.atom_off[c + 1] - g.atom_off[c]);
     int k = 0;
     for (int q = box_start[gb]; q < box_start[gb + 1]; ++q)
         k += items[q] < lim;
-    count[w] = k;
+    return k;
 }
 
-// Processing rank of every original: prefix over interior boxes + slot.
-__global__ void centre_rank_kernel(Seg g, const int *box_start, const int *items,
-                                         const int *prefix, int nint, int *rank, int *centre_box)
+// The originals of interior box w take the processing ranks prefix,
+// prefix + 1, ... in box order.
+__device__ __forceinline__ void rank_interior(const Seg &g, const int *box_start,
+                                              const int *items, int c, int bl, int gb, int r,
+                                              int *rank, int *centre_box)
 {
-    const int w = blockIdx.x * blockDim.x + threadIdx.x;
-    if (w >= nint)
-        return;
-    const int c = seg_of(g.int_off, g.nconf, w);
-    const int bl = interior_box(g.geo[c], w - g.int_off[c]);
-    const int gb = g.box_off[c] + bl;
     const int p0 = g.pt_off[c], lim = p0 + (g.atom_off[c + 1] - g.atom_off[c]);
-    int r = prefix[w];
     for (int q = box_start[gb]; q < box_start[gb + 1]; ++q) {
         const int p = items[q];
         if (p < lim) {
@@ -785,15 +890,44 @@ __global__ void centre_rank_kernel(Seg g, const int *box_start, const int *items
     }
 }
 
+// Originals per interior box, in the lexicographic walk order of construct().
+__global__ void interior_count_kernel(Seg g, const int *box_start, const int *items,
+                                            int nint, int *count)
+{
+    const int w = blockIdx.x * blockDim.x + threadIdx.x;
+    if (w >= nint)
+        return;
+    int c, bl, gb;
+    count[w] = interior_originals(g, box_start, items, w, c, bl, gb);
+}
+
+// Processing rank of every original: prefix over interior boxes + slot.
+__global__ void centre_rank_kernel(Seg g, const int *box_start, const int *items,
+                                         const int *prefix, int nint, int *rank, int *centre_box)
+{
+    const int w = blockIdx.x * blockDim.x + threadIdx.x;
+    if (w >= nint)
+        return;
+    int c, bl, gb;
+    (void)interior_originals(g, box_start, items, w, c, bl, gb);
+    rank_interior(g, box_start, items, c, bl, gb, prefix[w], rank, centre_box);
+}
+
 struct Construct {
     const double *pts;
     const int *orig, *box_start, *items, *types, *rank, *centre_box;
     int ntot;
     double cutoffsq;
+    int cap;        // MODE 2: staged entries per list (list a at a cap)
+    int *overflow;  // MODE 2: set when a list outgrows its bin
 };
 
 // construct() (neighborhood.cpp:89-141) for one centre per wave.  MODE 0
-// counts the entries of every list, MODE 1 writes them with their keys.
+// counts the entries of every list, MODE 1 writes them with their keys at
+// the cursors (the counts' exclusive scan), MODE 2 counts and writes them in
+// one pass into bins of cb.cap entries per list (cursors from zero; an entry
+// past its bin is dropped and sets *cb.overflow, and the build is redone
+// with MODE 0 and 1).
 // The candidates of the 27 neighbour boxes, taken in the reference's
 // traversal order (l1, l2, l3 from -1, then each box's points in order),
 // are numbered 0 .. total-1 and the lanes test 64 consecutive numbers at a
@@ -803,6 +937,17 @@ struct Construct {
 // order) is the count so far plus the accepted lanes below it, so the
 // keys, and the lists they order, are those of the serial traversal.
 // Ranks are global over a chunk, which keeps each structure's order.
+// Wave-scope order of LDS accesses (a wave's LDS operations complete in
+// issue order; this keeps the compiler from moving them across).
+__device__ __forceinline__ void wave_barrier()
+{
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+constexpr int kAcceptBuf = 256;  // accepted candidates a wave buffers
+
 template <int MODE>
 __global__ __launch_bounds__(256) void construct_kernel(Seg g, Construct cb, int *cnt,
                                                         int *cursor, uint64_t *key, int *st_idx,
@@ -842,7 +987,68 @@ __global__ __launch_bounds__(256) void construct_kernel(Seg g, Construct cb, int
     const int excl = incl - size;
     const int total = __shfl(incl, 26);
 
-    unsigned ev = 0;
+    // MODE 1, 2: the accepted candidates (their points) wait in the wave's
+    // LDS buffer and are written together, one lane per entry, so the
+    // writes of a centre take about one pass instead of one per batch
+    __shared__ int accepted[4][kAcceptBuf];
+    int *abuf = accepted[threadIdx.x / 64];
+    int nacc = 0;     // buffered (uniform)
+    unsigned ev = 0;  // events before the buffer's first (uniform)
+    auto flush = [&]() {
+        wave_barrier();
+        int own0 = 0;
+        if (lane == 0)
+            own0 = atomicAdd(&cursor[a], nacc);
+        own0 = __shfl(own0, 0);
+        for (int e = lane; e < nacc; e += 64) {
+            const int indj = abuf[e];
+            // the same operations as the test below, so the same bits
+            const double r0 = cb.pts[3 * (size_t)indj] - pi0;
+            const double r1 = cb.pts[3 * (size_t)indj + 1] - pi1;
+            const double r2 = cb.pts[3 * (size_t)indj + 2] - pi2;
+            const double dij = sqrt(r0 * r0 + r1 * r1 + r2 * r2);
+            const int oj = cb.orig[indj];
+            const uint64_t kv = krank | (ev + (unsigned)e);
+            int64_t q = own0 + e;
+            bool put = true;
+            if (MODE == 2) {
+                put = q < cb.cap;
+                q += (int64_t)a * cb.cap;
+            }
+            if (put) {
+                key[q] = kv;
+                st_idx[q] = oj;
+                st_type[q] = cb.types[oj];
+                st_vec[3 * q] = r0;
+                st_vec[3 * q + 1] = r1;
+                st_vec[3 * q + 2] = r2;
+                st_d[q] = dij;
+            } else {
+                *cb.overflow = 1;
+            }
+            if (a != oj) {
+                q = atomicAdd(&cursor[oj], 1);
+                if (MODE == 2) {
+                    put = q < cb.cap;
+                    q += (int64_t)oj * cb.cap;
+                }
+                if (put) {
+                    key[q] = kv;
+                    st_idx[q] = a;
+                    st_type[q] = cb.types[a];
+                    st_vec[3 * q] = -r0;
+                    st_vec[3 * q + 1] = -r1;
+                    st_vec[3 * q + 2] = -r2;
+                    st_d[q] = dij;
+                } else {
+                    *cb.overflow = 1;
+                }
+            }
+        }
+        ev += (unsigned)nacc;
+        nacc = 0;
+        wave_barrier();
+    };
     int own = 0;
     for (int tb = 0; tb < total; tb += 64) {
         const int f = tb + lane;
@@ -858,61 +1064,49 @@ __global__ __launch_bounds__(256) void construct_kernel(Seg g, Construct cb, int
         const int kk = k < 27 ? k : 26;
         const int t = __shfl(first, kk) + (f - __shfl(excl, kk));
         bool ok = false;
-        double r0 = 0.0, r1 = 0.0, r2 = 0.0, dijsq = 0.0;
-        int oj = 0;
+        int oj = 0, indj = 0;
         if (f < total) {
-            const int indj = cb.items[t];
-            r0 = cb.pts[3 * (size_t)indj] - pi0;
-            r1 = cb.pts[3 * (size_t)indj + 1] - pi1;
-            r2 = cb.pts[3 * (size_t)indj + 2] - pi2;
-            dijsq = r0 * r0 + r1 * r1 + r2 * r2;
+            indj = cb.items[t];
+            const double r0 = cb.pts[3 * (size_t)indj] - pi0;
+            const double r1 = cb.pts[3 * (size_t)indj + 1] - pi1;
+            const double r2 = cb.pts[3 * (size_t)indj + 2] - pi2;
+            const double dijsq = r0 * r0 + r1 * r1 + r2 * r2;
             oj = cb.orig[indj];
             ok = dijsq < cb.cutoffsq && indi != indj && a <= oj;
         }
         const uint64_t acc = __ballot(ok);
-        // MODE 1: the accepted lanes' own entries take consecutive slots
-        // (one atomic per wave)
-        int own0 = 0;
-        if (MODE == 1 && acc) {
-            if (lane == 0)
-                own0 = atomicAdd(&cursor[a], __popcll(acc));
-            own0 = __shfl(own0, 0);
+        const int nok = __popcll(acc);
+        if (MODE == 0) {
+            if (ok && a != oj)
+                atomicAdd(&cnt[oj], 1);
+            own += nok;
+        } else if (nok) {
+            if (nacc + nok > kAcceptBuf)
+                flush();
+            if (ok)
+                abuf[nacc + __popcll(acc & below)] = indj;
+            nacc += nok;
         }
-        if (ok) {
-            if (MODE == 0) {
-                if (a != oj)
-                    atomicAdd(&cnt[oj], 1);
-            } else {
-                const double dij = sqrt(dijsq);
-                const int slot = __popcll(acc & below);
-                const uint64_t kv = krank | (ev + (unsigned)slot);
-                int q = own0 + slot;
-                key[q] = kv;
-                st_idx[q] = oj;
-                st_type[q] = cb.types[oj];
-                st_vec[3 * (int64_t)q] = r0;
-                st_vec[3 * (int64_t)q + 1] = r1;
-                st_vec[3 * (int64_t)q + 2] = r2;
-                st_d[q] = dij;
-                if (a != oj) {
-                    q = atomicAdd(&cursor[oj], 1);
-                    key[q] = kv;
-                    st_idx[q] = a;
-                    st_type[q] = cb.types[a];
-                    st_vec[3 * (int64_t)q] = -r0;
-                    st_vec[3 * (int64_t)q + 1] = -r1;
-                    st_vec[3 * (int64_t)q + 2] = -r2;
-                    st_d[q] = dij;
-                }
-            }
-        }
-        ev += (unsigned)__popcll(acc);
-        own += __popcll(acc);
     }
     if (MODE == 0 && lane == 0)
         atomicAdd(&cnt[a], own);
+    if (MODE != 0 && nacc)
+        flush();
 }
 
+
+// Clears the list counters [n], the 64-bit entry total and the longest
+// list before a counted build that follows a one-pass build.
+__global__ void zero_counts_kernel(int *cnt, int n, unsigned long long *z64, int *largest)
+{
+    const int stride = gridDim.x * blockDim.x;
+    for (int k = blockIdx.x * blockDim.x + threadIdx.x; k < n; k += stride)
+        cnt[k] = 0;
+    if (blockIdx.x == 0 && threadIdx.x == 0) {
+        *z64 = 0;
+        *largest = 0;
+    }
+}
 
 // Budgets of one chunk: its atoms (set before the build), its image flags,
 // boxes and interior boxes (the chunk ends early at the structure that would
@@ -925,49 +1119,62 @@ constexpr long long kChunkFlags = INT_MAX / 4;
 constexpr long long kChunkBoxes = INT_MAX / 4;
 
 template <class T>
-hipError_t to_device(DBuf &b, const std::vector<T> &v, hipStream_t s)
-{
-    hipError_t e = b.ensure(sizeof(T) * std::max<size_t>(v.size(), 1));
-    if (e == hipSuccess && !v.empty())
-        e = hipMemcpyAsync(b.p, v.data(), sizeof(T) * v.size(), hipMemcpyHostToDevice, s);
-    return e;
-}
-
-// Host tables packed into one upload: each table at a 16-byte aligned
-// offset of one buffer.
-struct Pack {
-    std::vector<unsigned char> bytes;
-    template <class T>
-    size_t add(const T *v, size_t n)
-    {
-        const size_t off = (bytes.size() + 15) & ~size_t(15);
-        bytes.resize(off + sizeof(T) * n);
-        if (n)
-            std::memcpy(bytes.data() + off, v, sizeof(T) * n);
-        return off;
-    }
-    template <class T>
-    size_t add(const std::vector<T> &v) { return add(v.data(), v.size()); }
-    hipError_t upload(DBuf &b, hipStream_t s) const { return to_device(b, bytes, s); }
-};
-
-template <class T>
 const T *at(const DBuf &b, size_t off)
 {
     return reinterpret_cast<const T *>(static_cast<const unsigned char *>(b.p) + off);
 }
 
-hipError_t init_store(NeighborStore &st, int n, hipStream_t s)
+// Sizes the store for n atoms; clear zeroes the offsets (a builder that
+// writes every offset passes false).
+hipError_t init_store(NeighborStore &st, int n, hipStream_t s, bool clear = true)
 {
     st.n = n;
     st.P = 0;
     hipError_t e = st.offsets.ensure(sizeof(int) * ((size_t)n + 1));
     if (e == hipSuccess)
         e = st.center_type.ensure(sizeof(int) * std::max(n, 1));
-    if (e == hipSuccess)
+    if (e == hipSuccess && clear)
         e = hipMemsetAsync(st.offsets.p, 0, sizeof(int) * ((size_t)n + 1), s);
     return e;
 }
+
+// Host tables and arrays sent up in one copy through pinned memory: each
+// part at a 16-byte aligned offset.  The parts are copied into the pinned
+// buffer when sent, so the caller's arrays may change afterwards.
+struct Upload {
+    struct Part {
+        const void *src;
+        size_t off, bytes;
+    };
+    std::vector<Part> parts;
+    size_t size = 0;
+    template <class T>
+    size_t add(const T *v, size_t n)
+    {
+        const size_t off = (size + 15) & ~size_t(15);
+        parts.push_back({v, off, sizeof(T) * n});
+        size = off + sizeof(T) * n;
+        return off;
+    }
+    template <class T>
+    size_t add(const std::vector<T> &v) { return add(v.data(), v.size()); }
+    hipError_t send(HBuf &h, DBuf &d, hipStream_t s) const
+    {
+        const size_t n = std::max<size_t>(size, 16);
+        hipError_t e = h.ensure(n);
+        if (e == hipSuccess)
+            e = d.ensure(n);
+        if (e != hipSuccess)
+            return e;
+        for (const Part &q : parts)
+            if (q.bytes)
+                std::memcpy(h.as<unsigned char>() + q.off, q.src, q.bytes);
+        return hipMemcpyAsync(d.p, h.p, n, hipMemcpyHostToDevice, s);
+    }
+};
+
+// Entries that the bins of a one-pass build may hold (6.4 GB of staging).
+constexpr long long kBinEntries = 1LL << 27;
 
 // Atoms per chunk: kChunkAtoms, or less when MTPX_NEIGHBOR_CHUNK_ATOMS asks
 // for it (a smaller peak of builder scratch for very large batches).
@@ -989,7 +1196,7 @@ int build_chunk(int c0, int c1, const int *atom_offsets, const double *cells, co
     const int base = atom_offsets[c0];
     int ntot = atom_offsets[c1] - base;
     *done = nconf;
-    DTRY(init_store(out, ntot, s));
+    DTRY(init_store(out, ntot, s, ntot == 0));
     if (ntot == 0) {
         DTRY(hipStreamSynchronize(s));
         return MTPX_OK;
@@ -1014,16 +1221,17 @@ int build_chunk(int c0, int c1, const int *atom_offsets, const double *cells, co
         if (wrapf[c] && atom_off[c + 1] > atom_off[c] && !cell_inverse(cl[c].m, cl[c].inv))
             return fail_at(c, "singular cell", MTPX_E_INVALID);
     }
+    // scalars: [0] scan totals, [8..9] the 64-bit entry total, [10] bin
+    // overflow, [11] longest list, [12] entry total of a one-pass build
     DTRY(w.scalars.ensure(sizeof(int) * 16));
-    Pack head;
-    const size_t o_atoms = head.add(atom_off), o_wrap = head.add(wrapf), o_cell = head.add(cl);
-    DTRY(head.upload(w.seg_head, s));
-    DTRY(w.pos.ensure(sizeof(double) * 3 * (size_t)ntot));
-    DTRY(w.types.ensure(sizeof(int) * (size_t)ntot));
-    DTRY(hipMemcpyAsync(w.pos.p, pos, sizeof(double) * 3 * (size_t)ntot, hipMemcpyHostToDevice, s));
-    DTRY(hipMemcpyAsync(w.types.p, types, sizeof(int) * (size_t)ntot, hipMemcpyHostToDevice, s));
-    hipLaunchKernelGGL(gather_types_kernel, dim3(blocks(ntot, 256)), dim3(256), 0, s,
-                       w.types.as<int>(), ntot, out.center_type.as<int>());
+    int *scal = w.scalars.as<int>();
+    // the structure tables, positions and species: one copy
+    Upload head;
+    const size_t o_atoms = head.add(atom_off), o_wrap = head.add(wrapf), o_cell = head.add(cl),
+                 o_pos = head.add(pos, 3 * (size_t)ntot), o_types = head.add(types, (size_t)ntot);
+    DTRY(head.send(w.up_head, w.seg_head, s));
+    const double *dpos = at<double>(w.seg_head, o_pos);
+    const int *dtypes = at<int>(w.seg_head, o_types);
     Seg g{};
     g.nconf = nconf;
     g.atom_off = at<int>(w.seg_head, o_atoms);
@@ -1036,13 +1244,15 @@ int build_chunk(int c0, int c1, const int *atom_offsets, const double *cells, co
     for (int c = 0; c < nconf; ++c)
         nmax = std::max(nmax, atom_off[c + 1] - atom_off[c]);
     const int B = std::min(64, std::max(1, (nmax + 2047) / 2048));
-    DTRY(w.minmax.ensure(sizeof(double) * 6 * (size_t)nconf * B));
+    const size_t npart = 6 * (size_t)nconf * B;
+    DTRY(w.minmax.ensure(sizeof(double) * npart));
+    DTRY(w.down.ensure(sizeof(double) * npart));
     hipLaunchKernelGGL(wrap_minmax_kernel, dim3((unsigned)((size_t)nconf * B)), dim3(256), 0, s, g,
-                       w.pos.as<double>(), B, wr, w.minmax.as<double>());
-    std::vector<double> part(6 * (size_t)nconf * B), mm(6 * (size_t)nconf);
-    DTRY(hipMemcpyAsync(part.data(), w.minmax.p, sizeof(double) * part.size(),
-                        hipMemcpyDeviceToHost, s));
+                       dpos, dtypes, B, wr, w.minmax.as<double>(), out.center_type.as<int>());
+    DTRY(hipMemcpyAsync(w.down.p, w.minmax.p, sizeof(double) * npart, hipMemcpyDeviceToHost, s));
     DTRY(hipStreamSynchronize(s));
+    const double *part = w.down.as<double>();
+    std::vector<double> mm(6 * (size_t)nconf);
     for (int c = 0; c < nconf; ++c)
         for (int d = 0; d < 3; ++d) {
             double l = part[6 * (size_t)c * B + d], h = part[6 * (size_t)c * B + 3 + d];
@@ -1123,11 +1333,11 @@ int build_chunk(int c0, int c1, const int *atom_offsets, const double *cells, co
     }
     const long long nflags = flag_off.back();
     const int nboxes = box_off.back(), nint = int_off.back();
-    Pack tabs;
+    Upload tabs;
     const size_t o_cand_off = tabs.add(cand_off), o_box_off = tabs.add(box_off),
                  o_int_off = tabs.add(int_off), o_flag_off = tabs.add(flag_off),
                  o_geo = tabs.add(geo.data(), (size_t)nconf), o_cand = tabs.add(cand);
-    DTRY(tabs.upload(w.seg_tabs, s));
+    DTRY(tabs.send(w.up_tabs, w.seg_tabs, s));
     g.cand_off = at<int>(w.seg_tabs, o_cand_off);
     g.box_off = at<int>(w.seg_tabs, o_box_off);
     g.int_off = at<int>(w.seg_tabs, o_int_off);
@@ -1142,26 +1352,41 @@ int build_chunk(int c0, int c1, const int *atom_offsets, const double *cells, co
     long long npts_max = (long long)ntot + nflags;  // < 2^30 by the chunk budgets
     const bool bound = npts_max <= kPointBound || w.pts.bytes >= sizeof(double) * 3 * npts_max;
     DTRY(w.flags.ensure(sizeof(int) * (size_t)std::max<long long>(nflags, 1)));
-    if (nflags > 0) {
+    if (nflags > kScanLdsMax) {
+        // flags with the scan's tile sums, then the two scan passes
+        const long long ntiles = (nflags + kScanTile - 1) / kScanTile;
+        DTRY(w.scan.ensure(sizeof(int) * (size_t)nflags));
+        DTRY(w.box_cur.ensure(sizeof(int) * (size_t)ntiles));
+        int *sums = w.box_cur.as<int>();
+        hipLaunchKernelGGL(image_flag_tiles_kernel, dim3((unsigned)ntiles), dim3(kScanBlock), 0,
+                           s, g, wr, nflags, w.flags.as<int>(), sums);
+        hipLaunchKernelGGL(scan_sums, dim3(1), dim3(1024), 0, s, sums, (int)ntiles, scal);
+        hipLaunchKernelGGL(scan_tiles, dim3((unsigned)ntiles), dim3(kScanBlock), 0, s,
+                           w.flags.as<int>(), (int64_t)nflags, INT_MAX, sums, w.scan.as<int>(),
+                           nullptr);
+    } else if (nflags > 0) {
         DTRY(w.scan.ensure(sizeof(int) * (size_t)nflags));
         hipLaunchKernelGGL(image_flag_kernel, dim3(blocks(nflags, 256)), dim3(256), 0, s, g,
                            wr, nflags, w.flags.as<int>());
-        DTRY(scan_exclusive(w.flags.as<int>(), nflags, w.scan.as<int>(), w.box_cur,
-                            w.scalars.as<int>(), s));
+        DTRY(scan_exclusive(w.flags.as<int>(), nflags, w.scan.as<int>(), w.box_cur, scal, s));
     }
     DTRY(w.seg_imgs.ensure(sizeof(int) * ((size_t)nconf + 1)));
     DTRY(w.seg_pts.ensure(sizeof(int) * ((size_t)nconf + 1)));
-    hipLaunchKernelGGL(point_count_kernel, dim3(blocks(nconf + 1, 256)), dim3(256), 0, s, g,
-                       w.flags.as<int>(), w.scan.as<int>(), w.seg_imgs.as<int>());
-    DTRY(scan_exclusive(w.seg_imgs.as<int>(), (int64_t)nconf + 1, w.seg_pts.as<int>(), w.tmp,
-                        w.scalars.as<int>(), s));
+    if (nconf + 1 <= kScan1Threads * kOffsetsPerThread) {
+        hipLaunchKernelGGL(point_offsets_kernel, dim3(1), dim3(kScan1Threads), 0, s, g,
+                           w.flags.as<int>(), w.scan.as<int>(), w.seg_pts.as<int>());
+    } else {
+        hipLaunchKernelGGL(point_count_kernel, dim3(blocks(nconf + 1, 256)), dim3(256), 0, s, g,
+                           w.flags.as<int>(), w.scan.as<int>(), w.seg_imgs.as<int>());
+        DTRY(scan_exclusive(w.seg_imgs.as<int>(), (int64_t)nconf + 1, w.seg_pts.as<int>(),
+                            w.tmp, scal, s));
+    }
     g.pt_off = w.seg_pts.as<int>();
     const int *npts = g.pt_off + nconf;  // device
     if (!bound) {
-        int np = 0;
-        DTRY(hipMemcpyAsync(&np, npts, sizeof(int), hipMemcpyDeviceToHost, s));
+        DTRY(hipMemcpyAsync(w.down.p, npts, sizeof(int), hipMemcpyDeviceToHost, s));
         DTRY(hipStreamSynchronize(s));
-        npts_max = np;
+        npts_max = *w.down.as<int>();
     }
     DTRY(w.pts.ensure(sizeof(double) * 3 * (size_t)npts_max));
     DTRY(w.orig.ensure(sizeof(int) * (size_t)npts_max));
@@ -1169,14 +1394,11 @@ int build_chunk(int c0, int c1, const int *atom_offsets, const double *cells, co
     DTRY(w.cursor.ensure(sizeof(int) * ((size_t)ntot + 1)));
     int *box_count = w.cnt.as<int>();
     int *cnt = w.cursor.as<int>();
-    unsigned long long *total64 = reinterpret_cast<unsigned long long *>(w.scalars.as<int>() + 8);
-    hipLaunchKernelGGL(points_kernel, dim3(blocks(ntot, 256)), dim3(256), 0, s, g, wr, ntot,
+    unsigned long long *total64 = reinterpret_cast<unsigned long long *>(scal + 8);
+    hipLaunchKernelGGL(points_kernel, dim3(blocks(std::max<long long>(ntot, nflags), 256)),
+                       dim3(256), 0, s, g, wr, ntot, nflags, w.flags.as<int>(), w.scan.as<int>(),
                        w.pts.as<double>(), w.orig.as<int>(), box_count, nboxes + 1, cnt, ntot + 1,
-                       total64);
-    if (nflags > 0)
-        hipLaunchKernelGGL(image_write_kernel, dim3(blocks(nflags, 256)), dim3(256), 0, s,
-                           g, wr, nflags, w.flags.as<int>(), w.scan.as<int>(),
-                           w.pts.as<double>(), w.orig.as<int>());
+                       total64, scal + 10);
 
     // boxes: counts, starts, stable placement
     DTRY(w.box.ensure(sizeof(int) * (size_t)npts_max));
@@ -1187,7 +1409,7 @@ int build_chunk(int c0, int c1, const int *atom_offsets, const double *cells, co
                        w.pts.as<double>(), w.box.as<int>(), box_count);
     DTRY(scan_exclusive(box_count, (int64_t)nboxes + 1, w.box_start.as<int>(), w.tmp,
                         w.scalars.as<int>(), s, w.box_cur.as<int>()));
-    // the image flags are dead after image_write_kernel: their buffer takes
+    // the image flags are dead after points_kernel: their buffer takes
     // the unsorted placement (growing it waits for the queued work)
     DTRY(w.flags.ensure(sizeof(int) * (size_t)std::max<long long>(npts_max, 1)));
     int *unsorted = w.flags.as<int>();
@@ -1206,7 +1428,7 @@ int build_chunk(int c0, int c1, const int *atom_offsets, const double *cells, co
     if (nint > 0) {
         hipLaunchKernelGGL(interior_count_kernel, dim3(blocks(nint, 256)), dim3(256), 0, s,
                            g, w.box_start.as<int>(), w.box_items.as<int>(), nint, icount);
-        DTRY(scan_exclusive(icount, nint, iprefix, w.tmp, w.scalars.as<int>(), s));
+        DTRY(scan_exclusive(icount, nint, iprefix, w.tmp, scal, s));
         hipLaunchKernelGGL(centre_rank_kernel, dim3(blocks(nint, 256)), dim3(256), 0, s, g,
                            w.box_start.as<int>(), w.box_items.as<int>(), iprefix, nint, rank,
                            centre_box);
@@ -1218,50 +1440,89 @@ int build_chunk(int c0, int c1, const int *atom_offsets, const double *cells, co
     cb.orig = w.orig.as<int>();
     cb.box_start = w.box_start.as<int>();
     cb.items = w.box_items.as<int>();
-    cb.types = w.types.as<int>();
+    cb.types = dtypes;
     cb.rank = rank;
     cb.centre_box = centre_box;
     cb.ntot = ntot;
     cb.cutoffsq = cutoff * cutoff;
+    cb.cap = 0;
+    cb.overflow = scal + 10;
+    DTRY(w.down.ensure(sizeof(int) * 16));
+    int *down = w.down.as<int>();
+    auto ensure_entries = [&](size_t n) -> hipError_t {
+        const size_t nz = std::max<size_t>(n, 1);
+        for (DBuf *b : {&out.idx, &out.type, &w.st_idx, &w.st_type})
+            if (hipError_t e = b->ensure(sizeof(int) * nz))
+                return e;
+        for (DBuf *b : {&out.x, &out.y, &out.z, &out.d, &w.st_d})
+            if (hipError_t e = b->ensure(sizeof(double) * nz))
+                return e;
+        if (hipError_t e = w.key.ensure(sizeof(uint64_t) * nz))
+            return e;
+        return w.st_vec.ensure(sizeof(double) * 3 * nz);
+    };
+    auto rank_lists = [&](int cap, const int *overflow) {
+        hipLaunchKernelGGL(list_rank_kernel, dim3((ntot + 3) / 4), dim3(256), 0, s,
+                           out.offsets.as<int>(), ntot, cap, overflow, w.key.as<uint64_t>(),
+                           w.st_idx.as<int>(), w.st_type.as<int>(), w.st_vec.as<double>(),
+                           w.st_d.as<double>(), out.idx.as<int>(), out.type.as<int>(),
+                           out.x.as<double>(), out.y.as<double>(), out.z.as<double>(),
+                           out.d.as<double>());
+    };
+
+    // One pass into bins sized from the previous counted build: the entry
+    // total comes back with the final synchronisation.  A list that outgrows
+    // its bin sends the chunk through the counted build below.
+    const long long cap = w.bin_cap;
+    if (cap > 0 && (long long)ntot * cap <= kBinEntries) {
+        cb.cap = (int)cap;
+        DTRY(ensure_entries((size_t)ntot * cap));
+        hipLaunchKernelGGL(construct_kernel<2>, dim3((ntot + 3) / 4), dim3(256), 0, s, g, cb,
+                           nullptr, cnt, w.key.as<uint64_t>(), w.st_idx.as<int>(),
+                           w.st_type.as<int>(), w.st_vec.as<double>(), w.st_d.as<double>());
+        DTRY(scan_exclusive(cnt, (int64_t)ntot + 1, out.offsets.as<int>(), w.tmp, scal + 12, s,
+                            nullptr, (int)cap));
+        rank_lists((int)cap, scal + 10);
+        DTRY(hipMemcpyAsync(down, scal + 10, sizeof(int) * 3, hipMemcpyDeviceToHost, s));
+        DTRY(hipGetLastError());
+        DTRY(hipStreamSynchronize(s));
+        if (down[0] == 0) {
+            out.P = down[2];
+            return MTPX_OK;
+        }
+        cb.cap = 0;
+        hipLaunchKernelGGL(zero_counts_kernel, dim3(blocks(ntot + 1, 256)), dim3(256), 0, s, cnt,
+                           ntot + 1, total64, scal + 11);
+    }
+
+    // counted build: count, offsets, fill at the cursors, rank within lists
     hipLaunchKernelGGL(construct_kernel<0>, dim3((ntot + 3) / 4), dim3(256), 0, s, g, cb,
                        cnt, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr);
     hipLaunchKernelGGL(sum64_kernel, dim3(std::min<unsigned>(blocks(ntot, 256), 1024)), dim3(256),
-                       0, s, cnt, (int64_t)ntot, total64);
+                       0, s, cnt, (int64_t)ntot, total64, scal + 11);
     // the offsets, and the same values over the counts as the fill cursors
-    DTRY(scan_exclusive(cnt, (int64_t)ntot + 1, out.offsets.as<int>(), w.tmp, w.scalars.as<int>(),
-                        s, cnt));
-    unsigned long long P64 = 0;
-    DTRY(hipMemcpyAsync(&P64, total64, sizeof P64, hipMemcpyDeviceToHost, s));
+    DTRY(scan_exclusive(cnt, (int64_t)ntot + 1, out.offsets.as<int>(), w.tmp, scal, s, cnt));
+    DTRY(hipMemcpyAsync(down, scal + 8, sizeof(int) * 4, hipMemcpyDeviceToHost, s));
     DTRY(hipStreamSynchronize(s));
+    unsigned long long P64 = 0;
+    std::memcpy(&P64, down, sizeof P64);
+    const int longest = down[3];
     if (P64 > (unsigned long long)INT32_MAX) {
         err = named ? "batch has more than 2^31 - 1 neighbour entries"
                     : "structure has more than 2^31 - 1 neighbour entries";
         return MTPX_E_CAPACITY;
     }
+    // bins for the next build of this size: the longest list and a margin
+    w.bin_cap = (long long)longest + longest / 4 + 8;
     const int64_t P = (int64_t)P64;
     out.P = P;
-    const size_t Pz = (size_t)std::max<int64_t>(P, 1);
-    DTRY(out.idx.ensure(sizeof(int) * Pz));
-    DTRY(out.type.ensure(sizeof(int) * Pz));
-    DTRY(out.x.ensure(sizeof(double) * Pz));
-    DTRY(out.y.ensure(sizeof(double) * Pz));
-    DTRY(out.z.ensure(sizeof(double) * Pz));
-    DTRY(out.d.ensure(sizeof(double) * Pz));
+    DTRY(ensure_entries((size_t)P));
     if (P == 0)
         return MTPX_OK;
-    DTRY(w.key.ensure(sizeof(uint64_t) * Pz));
-    DTRY(w.st_idx.ensure(sizeof(int) * Pz));
-    DTRY(w.st_type.ensure(sizeof(int) * Pz));
-    DTRY(w.st_vec.ensure(sizeof(double) * 3 * Pz));
-    DTRY(w.st_d.ensure(sizeof(double) * Pz));
     hipLaunchKernelGGL(construct_kernel<1>, dim3((ntot + 3) / 4), dim3(256), 0, s, g, cb,
                        nullptr, cnt, w.key.as<uint64_t>(), w.st_idx.as<int>(),
                        w.st_type.as<int>(), w.st_vec.as<double>(), w.st_d.as<double>());
-    hipLaunchKernelGGL(list_rank_kernel, dim3((ntot + 3) / 4), dim3(256), 0, s,
-                       out.offsets.as<int>(), ntot, w.key.as<uint64_t>(), w.st_idx.as<int>(),
-                       w.st_type.as<int>(), w.st_vec.as<double>(), w.st_d.as<double>(),
-                       out.idx.as<int>(), out.type.as<int>(), out.x.as<double>(),
-                       out.y.as<double>(), out.z.as<double>(), out.d.as<double>());
+    rank_lists(0, nullptr);
     DTRY(hipGetLastError());
     DTRY(hipStreamSynchronize(s));
     return MTPX_OK;

@@ -19,14 +19,6 @@
 
 namespace {
 
-bool finite_all(const double *v, size_t n)
-{
-    for (size_t i = 0; i < n; ++i)
-        if (!std::isfinite(v[i]))
-            return false;
-    return true;
-}
-
 // Packs and uploads the request's topology into ctx->sites.
 int upload_topology(mtpx_context *ctx, const mtpx_site_request &r, const std::vector<int> &rows)
 {
@@ -131,9 +123,9 @@ int check_request(mtpx_context *ctx, const mtpx_site_request &r, bool check_topo
     }
     if (P > 0 && !r.neighbor_vectors && !r.x)
         return set_error(ctx, MTPX_E_INVALID, "site request needs positions or vectors");
-    if (r.x && !finite_all(r.x, 3 * (size_t)r.ntotal))
+    if (r.x && !all_finite(r.x, 3 * (size_t)r.ntotal))
         return set_error(ctx, MTPX_E_INVALID, "non-finite position");
-    if (r.neighbor_vectors && !finite_all(r.neighbor_vectors, 3 * (size_t)P))
+    if (r.neighbor_vectors && !all_finite(r.neighbor_vectors, 3 * (size_t)P))
         return set_error(ctx, MTPX_E_INVALID, "non-finite neighbour vector");
     return MTPX_OK;
 }

@@ -9,14 +9,6 @@
 
 namespace {
 
-bool finite_all(const double *v, size_t n)
-{
-    for (size_t i = 0; i < n; ++i)
-        if (!std::isfinite(v[i]))
-            return false;
-    return true;
-}
-
 // Uploads n values, or zeros when the host array is absent.
 template <class T>
 hipError_t upload_or_zero(DBuf &b, const T *host, size_t n, hipStream_t s)
@@ -197,20 +189,17 @@ int mtpx_set_structures(mtpx_context *ctx, int nconf, const int *atom_offsets,
     const int N = atom_offsets[nconf];
     if (N > 0 && (!pos || !types))
         return set_error(ctx, MTPX_E_INVALID, "invalid batch arguments");
-    if (!finite_all(cells, 9 * (size_t)nconf))
+    if (!all_finite(cells, 9 * (size_t)nconf))
         return set_error(ctx, MTPX_E_INVALID, "non-finite cell");
-    if (!finite_all(pos, 3 * (size_t)N))
+    if (!all_finite(pos, 3 * (size_t)N))
         return set_error(ctx, MTPX_E_INVALID, "non-finite position");
     std::vector<int> tbuf;
     if (int rc = map_species(ctx, types, (size_t)N, false, tbuf, types))
         return rc;
     const int Z = ctx->has_model ? ctx->model.Z : 1 << 30;
     int maxs = -1;
-    for (int i = 0; i < N; ++i) {
-        if (types[i] < 0 || types[i] >= Z)
-            return set_error(ctx, MTPX_E_INVALID, "species out of range");
-        maxs = std::max(maxs, types[i]);
-    }
+    if (!species_in_range(types, (size_t)N, Z, maxs))
+        return set_error(ctx, MTPX_E_INVALID, "species out of range");
     (void)hipSetDevice(ctx->device);
     ctx->has_nbh = false;
     ctx->rev_ready = false;
@@ -221,6 +210,7 @@ int mtpx_set_structures(mtpx_context *ctx, int nconf, const int *atom_offsets,
     if (rc != MTPX_OK)
         return set_error(ctx, rc, err);
     ctx->nconf = nconf;
+    ctx->single_n = -1;
     ctx->max_species = maxs;
     ctx->soff_host.assign(atom_offsets, atom_offsets + nconf + 1);
     std::vector<int> cs((size_t)N);

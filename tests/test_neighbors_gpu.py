@@ -91,6 +91,30 @@ def test_full_size_workload2_lists_bit_exact(nctx):
     assert 40 <= counts.mean() <= 55
 
 
+def test_one_pass_and_counted_builds_agree():
+    """The builder counts the lists on a context's first build and, on the
+    next builds, writes them in one pass into bins sized from the longest
+    list seen (plus a quarter and 8); a list that outgrows its bin sends the
+    build back through the counting pass.  A fresh context walks every path:
+    counted (first build), one pass (same cell), overflow then counted (a
+    cutoff of 7 gives lists about 2.7 times longer), one pass at the longer
+    cutoff, one pass back at the shorter one.  Every result is the oracle's
+    lists bit for bit."""
+    from mtpx import capi
+    _, s = S.workload_inference(1)
+    pos = O.wrap(s.cell, s.pbc, s.pos)
+    ref = {rc: O.Neighbors.build(s.cell, s.pbc, pos, s.types, rc) for rc in (5.0, 7.0)}
+    longest = int(np.diff(ref[5.0].offsets).max())
+    assert int(np.diff(ref[7.0].offsets).max()) > longest + longest // 4 + 8
+    c = capi.Context(0)
+    try:
+        for rc in (5.0, 5.0, 7.0, 7.0, 5.0):
+            c.build_neighbors(s.cell, s.pbc, pos, s.types, rc)
+            _compare(c.get_neighbors(), ref[rc])
+    finally:
+        c.close()
+
+
 def test_device_lists_drive_efs(ctx):
     """Build on the device, evaluate on the device, compare with the oracle."""
     model_text, s = S.scaled_inference(2, (4, 4, 4))
