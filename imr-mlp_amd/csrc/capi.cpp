@@ -368,6 +368,7 @@ DevNeighbors dev_neighbors(const mtpx_context *ctx)
     nb.d = ctx->d.as<double>();
     nb.center_type = ctx->center_type.as<int>();
     nb.center = nullptr;
+    nb.mirror = ctx->nbh.has_mirror ? ctx->nbh.mirror.as<int>() : nullptr;
     return nb;
 }
 
@@ -460,7 +461,15 @@ int run_efs(mtpx_context *ctx, bool deterministic, bool site_virial, bool energy
         return set_error(ctx, MTPX_E_NO_TOPOLOGY, "no neighbour lists");
     if (int rc = check_species(ctx))
         return rc;
-    if (deterministic)
+    // Lists built here carry each entry's mirror: the forces are then
+    // assembled without atomics (per-entry derivatives, each atom's own force
+    // stored, the reactions gathered by the mirrors), which is also the
+    // ordered assembly.  Lists handed over take the reaction atomics, or the
+    // reverse index when an ordered assembly is asked for.
+    const bool mirror = ctx->nbh.has_mirror && !energy_only;
+    if (mirror)
+        deterministic = true;
+    else if (deterministic)
         if (int rc = ensure_reverse_index(ctx))
             return rc;
     const int n = ctx->n;
@@ -505,7 +514,7 @@ int run_efs(mtpx_context *ctx, bool deterministic, bool site_virial, bool energy
     if (n > 0)
         HIP_TRY(launch_efs(ctx->dm, nb, out, cfg,
                            (deterministic ? kEfsDeterministic : 0) |
-                               (energy_only ? kEfsEnergyOnly : 0),
+                               (energy_only ? kEfsEnergyOnly : 0) | (mirror ? kEfsOwnForce : 0),
                            s),
                 "launch efs kernel");
     HIP_TRY(hipEventRecord(ctx->ev[1], s), "record event");
@@ -935,6 +944,7 @@ int mtpx_set_neighbors(mtpx_context *ctx, int n, const int *offsets, const int *
     (void)hipSetDevice(ctx->device);
     ctx->has_nbh = false;
     ctx->rev_ready = false;
+    ctx->nbh.has_mirror = false;  // lists handed over carry no mirror entries
     std::vector<double> xs((size_t)P), ys((size_t)P), zs((size_t)P);
     for (int64_t p = 0; p < P; ++p) {
         xs[p] = vecs[3 * p];

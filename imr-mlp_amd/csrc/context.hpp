@@ -131,7 +131,8 @@ struct mtpx_context {
                         &bstress, &active, &tE, &wE, &tF, &wF, &tS, &wS, &dLdE, &dLdF, &dLdS,
                         &metric_rows, &metrics, &grad_rows, &grad, &nbh_tmp.offsets,
                         &nbh_tmp.idx, &nbh_tmp.type, &nbh_tmp.x, &nbh_tmp.y, &nbh_tmp.z,
-                        &nbh_tmp.d, &nbh_tmp.center_type, &lin_level, &lin_steps, &lin_lcomb,
+                        &nbh_tmp.d, &nbh_tmp.center_type, &nbh.mirror, &nbh_tmp.mirror,
+                        &lin_level, &lin_steps, &lin_lcomb,
                         &lin_comb, &lin_ent, &lin_estart, &lin_chunk, &lin_maskw, &lin_clist,
                         &lin_walk, &lin_walk_off,
                         &comp, &row_src, &row_sw, &row_y, &rowsA, &rowsY, &gram_part, &gram_out,

@@ -160,9 +160,13 @@ __global__ __launch_bounds__(kWave *kMaxWaves) void efs_kernel(DevModel m, DevNe
             fi2 += D2;
             if (valid) {
                 if (deterministic) {
-                    out.pair_ders[3 * p + 0] = D0;
-                    out.pair_ders[3 * p + 1] = D1;
-                    out.pair_ders[3 * p + 2] = D2;
+                    // with the mirror assembly D goes to the slot of the
+                    // entry's mirror, so the gather reads each list's
+                    // reactions in order
+                    const int64_t w = (flags & kEfsOwnForce) ? (int64_t)nb.mirror[p] : p;
+                    out.pair_ders[3 * w + 0] = D0;
+                    out.pair_ders[3 * w + 1] = D1;
+                    out.pair_ders[3 * w + 2] = D2;
                 } else {
                     const int j = nb.idx[p];
                     atomicAdd(&out.forces[3 * j + 0], -D0);
@@ -190,6 +194,8 @@ __global__ __launch_bounds__(kWave *kMaxWaves) void efs_kernel(DevModel m, DevNe
         if (vi >= 0 && vi < 3) {
             if (!deterministic)
                 atomicAdd(&out.forces[3 * ai + vi], tot);
+            else if (flags & kEfsOwnForce)
+                out.forces[3 * ai + vi] = tot;
         } else if (vi >= 3) {
             sums[vi - 2] += tot;  // the wave's virial sums, sums[1 .. 9]
             if (out.site_virial)
@@ -219,9 +225,8 @@ __global__ __launch_bounds__(kWave *kMaxWaves) void efs_kernel(DevModel m, DevNe
         out.partial[10 * row + lane] = sums[lane];
 }
 
-// Ordered reduction of the per-wave partials (one workgroup).
-__global__ __launch_bounds__(256) void partial_reduce_kernel(const double *partial, int nrows,
-                                                             double *out10)
+// Ordered reduction of the per-wave partials (one workgroup of 256).
+__device__ __forceinline__ void partial_reduce(const double *partial, int nrows, double *out10)
 {
     __shared__ double buf[256][10];
     const int t = threadIdx.x;
@@ -243,6 +248,12 @@ __global__ __launch_bounds__(256) void partial_reduce_kernel(const double *parti
     }
     if (t < 10)
         out10[t] = buf[0][t];
+}
+
+__global__ __launch_bounds__(256) void partial_reduce_kernel(const double *partial, int nrows,
+                                                             double *out10)
+{
+    partial_reduce(partial, nrows, out10);
 }
 
 // Deterministic force assembly: F_k = sum_{p in list(k)} D_p - sum_{p : idx_p = k} D_p,
@@ -269,6 +280,39 @@ __global__ __launch_bounds__(256) void force_gather_kernel(DevNeighbors nb, cons
     forces[3 * k] = f0;
     forces[3 * k + 1] = f1;
     forces[3 * k + 2] = f2;
+}
+
+// The reactions: F_a -= sum over a's entries q of Dm[q], the derivative of
+// q's mirror entry (the E/F/S kernel stored each entry's derivative at its
+// mirror's slot), onto the own force the kernel stored.  Sixteen lanes per
+// atom stride over its entries (contiguous reads) and sum over their row
+// (DPP), so the order is fixed and the result repeatable.
+// The last workgroup reduces the per-wave partials instead (one launch for
+// both).
+__global__ __launch_bounds__(256) void mirror_gather_kernel(DevNeighbors nb, const double *Dm,
+                                                            double *forces, const double *partial,
+                                                            int nrows, double *out10)
+{
+    if (blockIdx.x == gridDim.x - 1) {
+        partial_reduce(partial, nrows, out10);
+        return;
+    }
+    const int t = blockIdx.x * blockDim.x + threadIdx.x;
+    const int a = t >> 4, l = t & 15;
+    double f0 = 0.0, f1 = 0.0, f2 = 0.0;
+    if (a < nb.n) {
+        const int e = nb.offsets[a + 1];
+        for (int64_t q = nb.offsets[a] + l; q < e; q += 16) {
+            f0 += Dm[3 * q];
+            f1 += Dm[3 * q + 1];
+            f2 += Dm[3 * q + 2];
+        }
+    }
+    f0 = row16_sum(f0);
+    f1 = row16_sum(f1);
+    f2 = row16_sum(f2);
+    if (a < nb.n && l < 3)
+        forces[3 * (int64_t)a + l] -= l == 0 ? f0 : l == 1 ? f1 : f2;
 }
 
 // -1/2 D r^T, symmetrised off the diagonal, as (xx, yy, zz, xy, xz, yz): one
@@ -462,6 +506,12 @@ hipError_t launch_efs_finish(const DevNeighbors &nb, const EfsOut &out, int rows
                              bool deterministic, const int *rev_offsets, const int *rev_pairs,
                              double *energy_stress10, hipStream_t s)
 {
+    if (deterministic && nb.n > 0 && nb.mirror) {
+        const unsigned gather = (unsigned)(((int64_t)nb.n * 16 + 255) / 256);
+        hipLaunchKernelGGL(mirror_gather_kernel, dim3(gather + 1), dim3(256), 0, s, nb,
+                           out.pair_ders, out.forces, out.partial, rows, energy_stress10);
+        return hipGetLastError();
+    }
     hipLaunchKernelGGL(partial_reduce_kernel, dim3(1), dim3(256), 0, s, out.partial, rows,
                        energy_stress10);
     if (deterministic && nb.n > 0)

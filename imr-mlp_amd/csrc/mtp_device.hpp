@@ -97,6 +97,17 @@ __device__ __forceinline__ double dpp_add(double v)
     return v + __hiloint2double(hi, lo);
 }
 
+// Sum over the lane's row of 16, in every lane of the row (the last four
+// steps of wave_sum below).
+__device__ __forceinline__ double row16_sum(double v)
+{
+    v = dpp_add<0xB1>(v);   // quad_perm [1,0,3,2]
+    v = dpp_add<0x4E>(v);   // quad_perm [2,3,0,1]
+    v = dpp_add<0x141>(v);  // row_half_mirror
+    v = dpp_add<0x140>(v);  // row_mirror
+    return v;
+}
+
 // Sum over the whole wave, in every lane: the two lane swaps, then within
 // each row of 16 the quad permutations [1,0,3,2] and [2,3,0,1], the
 // half-row mirror and the row mirror (each pairs lanes holding disjoint

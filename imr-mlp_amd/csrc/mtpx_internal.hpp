@@ -84,10 +84,16 @@ struct NeighborStore {
     int n = 0;
     int64_t P = 0;
     DBuf offsets, idx, type, x, y, z, d, center_type;
+    // mirror[p]: the entry of list idx[p] that is entry p seen from the other
+    // end (an image of the centre at the opposite offset; p itself for the
+    // images of the centre): lists built here have it, lists handed over do
+    // not
+    DBuf mirror;
+    bool has_mirror = false;
 };
 struct NeighborScratch {
     DBuf pts, orig, flags, scan, tmp, minmax, box, box_start, box_cur, box_items, rank, cnt,
-        cursor, key, st_idx, st_type, st_vec, st_d, scalars;
+        cursor, key, st_idx, st_type, st_vec, st_d, st_mate, st_final, scalars;
     // per-structure tables of a batch with the positions and species (atom
     // offsets, wrap flags and cells; candidate, box, interior-box and flag
     // offsets, geometry and image candidates; image counts; point offsets)
@@ -102,7 +108,8 @@ struct NeighborScratch {
     {
         for (DBuf *b : {&pts, &orig, &flags, &scan, &tmp, &minmax, &box, &box_start, &box_cur,
                         &box_items, &rank, &cnt, &cursor, &key, &st_idx, &st_type, &st_vec,
-                        &st_d, &scalars, &seg_head, &seg_tabs, &seg_imgs, &seg_pts, &wrapped})
+                        &st_d, &st_mate, &st_final, &scalars, &seg_head, &seg_tabs, &seg_imgs,
+                        &seg_pts, &wrapped})
             b->release();
         for (HBuf *b : {&up_head, &up_tabs, &down})
             b->release();
@@ -382,6 +389,7 @@ struct DevNeighbors {
     const double *x, *y, *z, *d;  // [P]
     const int *center_type; // [n]
     const int *center;      // [n] atom of each centre row; nullptr: row i is atom i
+    const int *mirror = nullptr;  // [P] the opposite entry of each entry, or nullptr
 };
 
 struct EfsOut {
@@ -408,9 +416,13 @@ struct EfsLaunch {
 bool efs_configure(const DevModel &m, int n, int num_cus, int max_waves, size_t lds_limit,
                    EfsLaunch &cfg, int table_pref = -1);
 int efs_variant(const DevModel &m, int R);
-// launch_efs flags: ordered force assembly; site energies and energy only.
+// launch_efs flags: ordered force assembly (per-entry derivatives, no
+// atomics); site energies and energy only; with the ordered assembly, each
+// atom's own force stored by the kernel (the gather over the mirror entries
+// subtracts the reactions).
 constexpr int kEfsDeterministic = 1;
 constexpr int kEfsEnergyOnly = 2;
+constexpr int kEfsOwnForce = 4;
 hipError_t launch_efs(const DevModel &m, const DevNeighbors &nb, const EfsOut &out,
                       const EfsLaunch &cfg, int flags, hipStream_t s);
 // Linear fit (lin_kernel.hip).
@@ -530,6 +542,9 @@ hipError_t noalloc_scratch_address(double **ptr);
 // Zero-fill kernel (used where a caller may capture the launches).
 hipError_t launch_fill_zero(double *p, size_t count, hipStream_t s);
 
+// The per-wave partials reduced in order; with deterministic, the forces
+// assembled from the per-entry derivatives: by the mirror entries when nb has
+// them (the kernel ran with kEfsOwnForce), else by the reverse index.
 hipError_t launch_efs_finish(const DevNeighbors &nb, const EfsOut &out, int rows,
                              bool deterministic, const int *rev_offsets, const int *rev_pairs,
                              double *energy_stress10, hipStream_t s);

@@ -101,7 +101,7 @@ __global__ __launch_bounds__(256) void list_rank_kernel(const int *offsets, int 
                                                         const int *st_idx, const int *st_type,
                                                         const double *st_vec, const double *st_d,
                                                         int *idx, int *type, double *x, double *y,
-                                                        double *z, double *d)
+                                                        double *z, double *d, int *st_final)
 {
     const int lane = threadIdx.x & 63;
     const int l = blockIdx.x * (blockDim.x / 64) + threadIdx.x / 64;
@@ -128,7 +128,26 @@ __global__ __launch_bounds__(256) void list_rank_kernel(const int *offsets, int 
             y[o] = st_vec[3 * q + 1];
             z[o] = st_vec[3 * q + 2];
             d[o] = st_d[q];
+            st_final[q] = (int)o;
         }
+    }
+}
+
+// mirror[final(q)] = final(mate(q)) for every staged entry q (the staging
+// as list_rank_kernel reads it; nothing when a bin overflowed).
+__global__ __launch_bounds__(256) void mirror_kernel(const int *offsets, int n, int cap,
+                                                     const int *overflow, const int *mate,
+                                                     const int *st_final, int *mirror)
+{
+    const int lane = threadIdx.x & 63;
+    const int l = blockIdx.x * (blockDim.x / 64) + threadIdx.x / 64;
+    if (l >= n || (overflow && *overflow))
+        return;  // uniform over the wave
+    const int s = offsets[l], cnt = offsets[l + 1] - s;
+    const int64_t sb = cap ? (int64_t)l * cap : s;
+    for (int j = lane; j < cnt; j += 64) {
+        const int64_t q = sb + j;
+        mirror[st_final[q]] = st_final[mate[q]];
     }
 }
 
@@ -518,14 +537,17 @@ __global__ __launch_bounds__(256) void site_prepare_kernel(
 }
 
 // Append one structure's lists (atoms from a0, entries from p0) to a batch.
-__global__ void append_lists_kernel(const int *offsets, const int *idx, int n, int64_t P, int a0,
-                                    int64_t p0, int *out_offsets, int *out_idx)
+__global__ void append_lists_kernel(const int *offsets, const int *idx, const int *mirror, int n,
+                                    int64_t P, int a0, int64_t p0, int *out_offsets, int *out_idx,
+                                    int *out_mirror)
 {
     const int64_t k = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (k <= n)
         out_offsets[a0 + k] = (int)(p0 + offsets[k]);
-    if (k < P)
+    if (k < P) {
         out_idx[p0 + k] = a0 + idx[k];
+        out_mirror[p0 + k] = (int)(p0 + mirror[k]);
+    }
 }
 
 // Grows a device buffer to `need` bytes, keeping its first `keep` bytes.
@@ -920,6 +942,7 @@ struct Construct {
     double cutoffsq;
     int cap;        // MODE 2: staged entries per list (list a at a cap)
     int *overflow;  // MODE 2: set when a list outgrows its bin
+    int *mate;      // MODE 1, 2: staged index of each staged entry's mirror
 };
 
 // construct() (neighborhood.cpp:89-141) for one centre per wave.  MODE 0
@@ -1015,6 +1038,8 @@ __global__ __launch_bounds__(256) void construct_kernel(Seg g, Construct cb, int
                 put = q < cb.cap;
                 q += (int64_t)a * cb.cap;
             }
+            const int64_t q1 = q;
+            const bool put1 = put;
             if (put) {
                 key[q] = kv;
                 st_idx[q] = oj;
@@ -1040,9 +1065,16 @@ __global__ __launch_bounds__(256) void construct_kernel(Seg g, Construct cb, int
                     st_vec[3 * q + 1] = -r1;
                     st_vec[3 * q + 2] = -r2;
                     st_d[q] = dij;
+                    cb.mate[q] = (int)q1;
                 } else {
                     *cb.overflow = 1;
                 }
+                if (put1)
+                    cb.mate[q1] = (int)q;
+            } else if (put1) {
+                // an image of the centre: the opposite image is an entry of
+                // its own, and the pair of them cancels either way round
+                cb.mate[q1] = (int)q1;
             }
         }
         ev += (unsigned)nacc;
@@ -1130,6 +1162,7 @@ hipError_t init_store(NeighborStore &st, int n, hipStream_t s, bool clear = true
 {
     st.n = n;
     st.P = 0;
+    st.has_mirror = false;
     hipError_t e = st.offsets.ensure(sizeof(int) * ((size_t)n + 1));
     if (e == hipSuccess)
         e = st.center_type.ensure(sizeof(int) * std::max(n, 1));
@@ -1447,11 +1480,13 @@ int build_chunk(int c0, int c1, const int *atom_offsets, const double *cells, co
     cb.cutoffsq = cutoff * cutoff;
     cb.cap = 0;
     cb.overflow = scal + 10;
+    cb.mate = nullptr;  // set once the staging is sized
     DTRY(w.down.ensure(sizeof(int) * 16));
     int *down = w.down.as<int>();
     auto ensure_entries = [&](size_t n) -> hipError_t {
         const size_t nz = std::max<size_t>(n, 1);
-        for (DBuf *b : {&out.idx, &out.type, &w.st_idx, &w.st_type})
+        for (DBuf *b : {&out.idx, &out.type, &out.mirror, &w.st_idx, &w.st_type, &w.st_mate,
+                        &w.st_final})
             if (hipError_t e = b->ensure(sizeof(int) * nz))
                 return e;
         for (DBuf *b : {&out.x, &out.y, &out.z, &out.d, &w.st_d})
@@ -1467,7 +1502,10 @@ int build_chunk(int c0, int c1, const int *atom_offsets, const double *cells, co
                            w.st_idx.as<int>(), w.st_type.as<int>(), w.st_vec.as<double>(),
                            w.st_d.as<double>(), out.idx.as<int>(), out.type.as<int>(),
                            out.x.as<double>(), out.y.as<double>(), out.z.as<double>(),
-                           out.d.as<double>());
+                           out.d.as<double>(), w.st_final.as<int>());
+        hipLaunchKernelGGL(mirror_kernel, dim3((ntot + 3) / 4), dim3(256), 0, s,
+                           out.offsets.as<int>(), ntot, cap, overflow, w.st_mate.as<int>(),
+                           w.st_final.as<int>(), out.mirror.as<int>());
     };
 
     // One pass into bins sized from the previous counted build: the entry
@@ -1477,6 +1515,7 @@ int build_chunk(int c0, int c1, const int *atom_offsets, const double *cells, co
     if (cap > 0 && (long long)ntot * cap <= kBinEntries) {
         cb.cap = (int)cap;
         DTRY(ensure_entries((size_t)ntot * cap));
+        cb.mate = w.st_mate.as<int>();
         hipLaunchKernelGGL(construct_kernel<2>, dim3((ntot + 3) / 4), dim3(256), 0, s, g, cb,
                            nullptr, cnt, w.key.as<uint64_t>(), w.st_idx.as<int>(),
                            w.st_type.as<int>(), w.st_vec.as<double>(), w.st_d.as<double>());
@@ -1488,6 +1527,7 @@ int build_chunk(int c0, int c1, const int *atom_offsets, const double *cells, co
         DTRY(hipStreamSynchronize(s));
         if (down[0] == 0) {
             out.P = down[2];
+            out.has_mirror = true;
             return MTPX_OK;
         }
         cb.cap = 0;
@@ -1517,8 +1557,10 @@ int build_chunk(int c0, int c1, const int *atom_offsets, const double *cells, co
     const int64_t P = (int64_t)P64;
     out.P = P;
     DTRY(ensure_entries((size_t)P));
+    out.has_mirror = true;
     if (P == 0)
         return MTPX_OK;
+    cb.mate = w.st_mate.as<int>();
     hipLaunchKernelGGL(construct_kernel<1>, dim3((ntot + 3) / 4), dim3(256), 0, s, g, cb,
                        nullptr, cnt, w.key.as<uint64_t>(), w.st_idx.as<int>(),
                        w.st_type.as<int>(), w.st_vec.as<double>(), w.st_d.as<double>());
@@ -1541,6 +1583,7 @@ int append_store(NeighborStore &out, const NeighborStore &ch, int a0, int64_t p0
     DTRY(grow_keep(out.y, sizeof(double) * need, sizeof(double) * keep, s));
     DTRY(grow_keep(out.z, sizeof(double) * need, sizeof(double) * keep, s));
     DTRY(grow_keep(out.d, sizeof(double) * need, sizeof(double) * keep, s));
+    DTRY(grow_keep(out.mirror, sizeof(int) * need, sizeof(int) * keep, s));
     if (nc > 0)
         DTRY(hipMemcpyAsync(out.center_type.as<int>() + a0, ch.center_type.p, sizeof(int) * nc,
                             hipMemcpyDeviceToDevice, s));
@@ -1558,8 +1601,8 @@ int append_store(NeighborStore &out, const NeighborStore &ch, int a0, int64_t p0
     }
     const int64_t work = std::max<int64_t>(Pc, (int64_t)nc + 1);
     hipLaunchKernelGGL(append_lists_kernel, dim3(blocks(work, 256)), dim3(256), 0, s,
-                       ch.offsets.as<int>(), ch.idx.as<int>(), nc, Pc, a0, p0,
-                       out.offsets.as<int>(), out.idx.as<int>());
+                       ch.offsets.as<int>(), ch.idx.as<int>(), ch.mirror.as<int>(), nc, Pc, a0,
+                       p0, out.offsets.as<int>(), out.idx.as<int>(), out.mirror.as<int>());
     DTRY(hipGetLastError());
     DTRY(hipStreamSynchronize(s));
     return MTPX_OK;
@@ -1620,6 +1663,7 @@ int build_neighbors_batch_gpu(int nconf, const int *atom_offsets, const double *
         out.P = P;
         c0 += done;
     }
+    out.has_mirror = true;  // every chunk's entries came with their mirrors
     return MTPX_OK;
 }
 

@@ -115,6 +115,66 @@ def test_one_pass_and_counted_builds_agree():
         c.close()
 
 
+def _rel(a, b):
+    a, b = np.asarray(a, float), np.asarray(b, float)
+    return np.abs(a - b).max() / max(np.abs(b).max(), 1e-300)
+
+
+@pytest.mark.parametrize("name,s,rc", CASES, ids=[c[0] for c in CASES])
+def test_mirror_assembly_matches_reaction_atomics(ctx, name, s, rc):
+    """Lists built on the device carry each entry's mirror (the entry of the
+    neighbour's list that points back, or for an image of the centre the
+    opposite image), and E/F/S then assembles the forces from per-entry
+    derivatives without atomics: the own force stored, the reactions gathered
+    through the mirrors.  The same lists handed over (no mirrors) take the
+    reaction atomics and, when ordered, the reverse index.  All three agree
+    (1e-13), on every structure above: skewed cells, a cell smaller than the
+    cutoff (many images of the centre in its own list), a slab, a cluster and
+    a single atom.  The mirror assembly is bitwise repeatable."""
+    text, _ = S.scaled_inference(2, (2, 2, 2))  # two species
+    cut = O.Model(text).cutoff
+    pos = O.wrap(s.cell, s.pbc, s.pos) if np.any(s.pbc) else s.pos
+    ctx.load_model_text(text)
+    ctx.build_neighbors(s.cell, s.pbc, pos, s.types % 2, cut)
+    got = ctx.efs()
+    again = ctx.efs(deterministic=True)
+    for x, y in zip(got, again):
+        assert np.array_equal(np.asarray(x).view(np.uint64), np.asarray(y).view(np.uint64))
+    nb = ctx.get_neighbors()
+    ctx.set_neighbors(nb["offsets"], nb["idx"], nb["types"], nb["vec"], nb["dist"],
+                      nb["center_types"])
+    for det in (False, True):
+        ref = ctx.efs(deterministic=det)
+        assert abs(got[0] - ref[0]) <= 1e-13 * max(abs(ref[0]), 1.0)
+        if np.abs(ref[1]).max() > 0:
+            assert _rel(got[1], ref[1]) < 1e-13
+        else:
+            assert np.abs(got[1]).max() < 1e-14
+        assert _rel(got[2], ref[2]) < 1e-13
+        assert _rel(got[3], ref[3]) < 1e-13
+
+
+@pytest.mark.parametrize("chunk", ["1", "150"], ids=["chunk1", "chunk150"])
+def test_mirror_assembly_of_chunked_batches(ctx, monkeypatch, chunk):
+    """A batch built in chunks appends each chunk's mirrors shifted to the
+    batch's entries: compute_batch on it equals compute_batch on the batch
+    built in one piece (1e-13)."""
+    text, _ = S.scaled_inference(2, (2, 2, 2))
+    cut = O.Model(text).cutoff
+    structs = []
+    for _, s, _ in CASES:
+        pos = O.wrap(s.cell, s.pbc, s.pos) if np.any(s.pbc) else s.pos
+        structs.append(S.Structure(s.cell, pos, (s.types % 2).astype(np.int32), s.pbc))
+    ctx.load_model_text(text)
+    ctx.set_structures(structs, cut)
+    ref = ctx.compute_batch()
+    monkeypatch.setenv("MTPX_NEIGHBOR_CHUNK_ATOMS", chunk)
+    ctx.set_structures(structs, cut)
+    got = ctx.compute_batch()
+    for x, y in zip(got, ref):
+        assert _rel(x, y) < 1e-13
+
+
 def test_device_lists_drive_efs(ctx):
     """Build on the device, evaluate on the device, compare with the oracle."""
     model_text, s = S.scaled_inference(2, (4, 4, 4))
