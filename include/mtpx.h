@@ -300,7 +300,11 @@ int mtpx_set_neighbors(mtpx_context *ctx, int n, const int *offsets, const int *
  * MTPGpuDirect::compute_batch (mtp_gpu_direct.h:892).  Outputs: total energy,
  * forces [n][3], stress [3][3] (extensive virial, eV, S_ab = -sum D_a r_b),
  * site energies [n].  Any output pointer may be NULL.  deterministic != 0
- * orders every reduction (no floating-point atomics): byte-repeatable. */
+ * orders every reduction (no floating-point atomics): byte-repeatable.
+ * Lists built by mtpx_build_neighbors or mtpx_set_structures are always
+ * assembled that way (each entry's reaction is gathered through the entry
+ * of the other list that points back); lists from mtpx_set_neighbors use
+ * floating-point atomics unless deterministic is set. */
 int mtpx_efs(mtpx_context *ctx, int deterministic, double *energy, double *forces,
              double *stress, double *site_energies);
 /* PotMTP::getE (potentials/potential_mtp.cpp:2604-2621, over
