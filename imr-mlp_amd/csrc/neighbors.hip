@@ -992,13 +992,28 @@ __global__ __launch_bounds__(256) void construct_kernel(Seg g, Construct cb, int
     const uint64_t krank = (uint64_t)(unsigned)cb.rank[a] << 32;
     const uint64_t below = (1ull << lane) - 1;
 
-    // lane k < 27: the first point of box k and the running size of boxes 0..k
+    // lane k < 27: the first point of box k and the running size of boxes 0..k.
+    // A box holds its points in ascending index: originals by atom, then
+    // images.  The points up to the centre's own are originals of atoms up to
+    // the centre, which never pass a <= oj (or indi != indj), so the box is
+    // taken from the first point past the centre's; the accepted candidates,
+    // their order and their event numbers are unchanged.
     int first = 0, size = 0;
     if (lane < 27) {
         const int nb = box0 + ((bi + lane / 9 - 1) * bl1 + (bj + (lane / 3) % 3 - 1)) * bl2 +
                        (bk + lane % 3 - 1);
         first = cb.box_start[nb];
         size = cb.box_start[nb + 1] - first;
+        int lo = 0, hi = size;  // first item > indi
+        while (lo < hi) {
+            const int mid = (lo + hi) >> 1;
+            if (cb.items[first + mid] <= indi)
+                lo = mid + 1;
+            else
+                hi = mid;
+        }
+        first += lo;
+        size -= lo;
     }
     int incl = size;
 #pragma unroll
