@@ -93,25 +93,25 @@ struct NeighborStore {
 };
 struct NeighborScratch {
     DBuf pts, orig, flags, scan, tmp, minmax, box, box_start, box_cur, box_items, rank, cnt,
-        cursor, key, st_idx, st_type, st_vec, st_d, st_mate, st_final, scalars;
+        cursor, key, st_nbr, st_ctr, st_mate, st_final, scalars;
     // per-structure tables of a batch with the positions and species (atom
     // offsets, wrap flags and cells; candidate, box, interior-box and flag
     // offsets, geometry and image candidates; image counts; point offsets)
     // and the wrapped positions
     DBuf seg_head, seg_tabs, seg_imgs, seg_pts, wrapped;
-    // pinned staging of the two uploads and of the read-backs
-    HBuf up_head, up_tabs, down;
+    // pinned staging of the two table uploads and of the read-backs, and
+    // the positions and species, which the wrap kernel reads in place
+    HBuf up_head, up_tabs, down, up_pos;
     // entries per atom that the staging of a one-pass build reserves (0: none
     // known yet); set from the longest list of the last counted build
     long long bin_cap = 0;
     void release_all()
     {
         for (DBuf *b : {&pts, &orig, &flags, &scan, &tmp, &minmax, &box, &box_start, &box_cur,
-                        &box_items, &rank, &cnt, &cursor, &key, &st_idx, &st_type, &st_vec,
-                        &st_d, &st_mate, &st_final, &scalars, &seg_head, &seg_tabs, &seg_imgs,
-                        &seg_pts, &wrapped})
+                        &box_items, &rank, &cnt, &cursor, &key, &st_nbr, &st_ctr, &st_mate,
+                        &st_final, &scalars, &seg_head, &seg_tabs, &seg_imgs, &seg_pts, &wrapped})
             b->release();
-        for (HBuf *b : {&up_head, &up_tabs, &down})
+        for (HBuf *b : {&up_head, &up_tabs, &down, &up_pos})
             b->release();
         bin_cap = 0;
     }

@@ -84,7 +84,8 @@ __global__ void box_rank_kernel(const int *box, const int *box_start, const int 
 }
 
 // Rank every staged entry within its list by key and write it to its final
-// slot (SoA).  One wave per list: lanes take 64 entries at a time and count
+// slot (SoA); a staged entry is its key and its two points (neighbour,
+// centre), from which the displacement and distance are formed again.  One wave per list: lanes take 64 entries at a time and count
 // the list's smaller keys, read 64 at a time and broadcast lane by lane
 // (keys within a list are distinct).  The staged entries of list l lie at
 // its final offsets (cap == 0) or in its bin from l cap; with bins, a set
@@ -98,10 +99,11 @@ __device__ __forceinline__ uint64_t readlane_u64(uint64_t v, int l)
 
 __global__ __launch_bounds__(256) void list_rank_kernel(const int *offsets, int n, int cap,
                                                         const int *overflow, const uint64_t *key,
-                                                        const int *st_idx, const int *st_type,
-                                                        const double *st_vec, const double *st_d,
-                                                        int *idx, int *type, double *x, double *y,
-                                                        double *z, double *d, int *st_final)
+                                                        const int *st_nbr, const int *st_ctr,
+                                                        const double *pts, const int *orig,
+                                                        const int *types, int *idx, int *type,
+                                                        double *x, double *y, double *z,
+                                                        double *d, int *st_final)
 {
     const int lane = threadIdx.x & 63;
     const int l = blockIdx.x * (blockDim.x / 64) + threadIdx.x / 64;
@@ -122,12 +124,20 @@ __global__ __launch_bounds__(256) void list_rank_kernel(const int *offsets, int 
         }
         if (j < cnt) {
             const int64_t o = s + r;
-            idx[o] = st_idx[q];
-            type[o] = st_type[q];
-            x[o] = st_vec[3 * q];
-            y[o] = st_vec[3 * q + 1];
-            z[o] = st_vec[3 * q + 2];
-            d[o] = st_d[q];
+            // the entry from its two points, by the operations construct
+            // tested it with (the mirrored entry's vector is the exact
+            // negation, its distance the same)
+            const int pn = st_nbr[q], pc = st_ctr[q];
+            const double r0 = pts[3 * (size_t)pn] - pts[3 * (size_t)pc];
+            const double r1 = pts[3 * (size_t)pn + 1] - pts[3 * (size_t)pc + 1];
+            const double r2 = pts[3 * (size_t)pn + 2] - pts[3 * (size_t)pc + 2];
+            const int aj = orig[pn];
+            idx[o] = aj;
+            type[o] = types[aj];
+            x[o] = r0;
+            y[o] = r1;
+            z[o] = r2;
+            d[o] = sqrt(r0 * r0 + r1 * r1 + r2 * r2);
             st_final[q] = (int)o;
         }
     }
@@ -973,9 +983,8 @@ constexpr int kAcceptBuf = 256;  // accepted candidates a wave buffers
 
 template <int MODE>
 __global__ __launch_bounds__(256) void construct_kernel(Seg g, Construct cb, int *cnt,
-                                                        int *cursor, uint64_t *key, int *st_idx,
-                                                        int *st_type, double *st_vec,
-                                                        double *st_d)
+                                                        int *cursor, uint64_t *key, int *st_nbr,
+                                                        int *st_ctr)
 {
     const int lane = threadIdx.x & 63;
     const int a = blockIdx.x * (blockDim.x / 64) + threadIdx.x / 64;
@@ -1040,11 +1049,6 @@ __global__ __launch_bounds__(256) void construct_kernel(Seg g, Construct cb, int
         own0 = __shfl(own0, 0);
         for (int e = lane; e < nacc; e += 64) {
             const int indj = abuf[e];
-            // the same operations as the test below, so the same bits
-            const double r0 = cb.pts[3 * (size_t)indj] - pi0;
-            const double r1 = cb.pts[3 * (size_t)indj + 1] - pi1;
-            const double r2 = cb.pts[3 * (size_t)indj + 2] - pi2;
-            const double dij = sqrt(r0 * r0 + r1 * r1 + r2 * r2);
             const int oj = cb.orig[indj];
             const uint64_t kv = krank | (ev + (unsigned)e);
             int64_t q = own0 + e;
@@ -1057,12 +1061,8 @@ __global__ __launch_bounds__(256) void construct_kernel(Seg g, Construct cb, int
             const bool put1 = put;
             if (put) {
                 key[q] = kv;
-                st_idx[q] = oj;
-                st_type[q] = cb.types[oj];
-                st_vec[3 * q] = r0;
-                st_vec[3 * q + 1] = r1;
-                st_vec[3 * q + 2] = r2;
-                st_d[q] = dij;
+                st_nbr[q] = indj;
+                st_ctr[q] = indi;
             } else {
                 *cb.overflow = 1;
             }
@@ -1074,12 +1074,8 @@ __global__ __launch_bounds__(256) void construct_kernel(Seg g, Construct cb, int
                 }
                 if (put) {
                     key[q] = kv;
-                    st_idx[q] = a;
-                    st_type[q] = cb.types[a];
-                    st_vec[3 * q] = -r0;
-                    st_vec[3 * q + 1] = -r1;
-                    st_vec[3 * q + 2] = -r2;
-                    st_d[q] = dij;
+                    st_nbr[q] = indi;
+                    st_ctr[q] = indj;
                     cb.mate[q] = (int)q1;
                 } else {
                     *cb.overflow = 1;
@@ -1273,13 +1269,22 @@ int build_chunk(int c0, int c1, const int *atom_offsets, const double *cells, co
     // overflow, [11] longest list, [12] entry total of a one-pass build
     DTRY(w.scalars.ensure(sizeof(int) * 16));
     int *scal = w.scalars.as<int>();
-    // the structure tables, positions and species: one copy
+    // the structure tables: one copy; the positions and species are staged
+    // in pinned memory, which the wrap kernel reads in place (it copies the
+    // species to the centre types, which the later kernels read)
     Upload head;
-    const size_t o_atoms = head.add(atom_off), o_wrap = head.add(wrapf), o_cell = head.add(cl),
-                 o_pos = head.add(pos, 3 * (size_t)ntot), o_types = head.add(types, (size_t)ntot);
+    const size_t o_atoms = head.add(atom_off), o_wrap = head.add(wrapf), o_cell = head.add(cl);
     DTRY(head.send(w.up_head, w.seg_head, s));
-    const double *dpos = at<double>(w.seg_head, o_pos);
-    const int *dtypes = at<int>(w.seg_head, o_types);
+    const size_t pos_bytes = sizeof(double) * 3 * (size_t)ntot;
+    DTRY(w.up_pos.ensure(pos_bytes + sizeof(int) * (size_t)ntot));
+    std::memcpy(w.up_pos.p, pos, pos_bytes);
+    std::memcpy(w.up_pos.as<unsigned char>() + pos_bytes, types, sizeof(int) * (size_t)ntot);
+    void *hpos = nullptr;
+    DTRY(hipHostGetDevicePointer(&hpos, w.up_pos.p, 0));
+    const double *dpos = static_cast<const double *>(hpos);
+    const int *dtypes_host = reinterpret_cast<const int *>(static_cast<unsigned char *>(hpos) +
+                                                           pos_bytes);
+    const int *dtypes = out.center_type.as<int>();  // device copy, written by the wrap kernel
     Seg g{};
     g.nconf = nconf;
     g.atom_off = at<int>(w.seg_head, o_atoms);
@@ -1296,7 +1301,7 @@ int build_chunk(int c0, int c1, const int *atom_offsets, const double *cells, co
     DTRY(w.minmax.ensure(sizeof(double) * npart));
     DTRY(w.down.ensure(sizeof(double) * npart));
     hipLaunchKernelGGL(wrap_minmax_kernel, dim3((unsigned)((size_t)nconf * B)), dim3(256), 0, s, g,
-                       dpos, dtypes, B, wr, w.minmax.as<double>(), out.center_type.as<int>());
+                       dpos, dtypes_host, B, wr, w.minmax.as<double>(), out.center_type.as<int>());
     DTRY(hipMemcpyAsync(w.down.p, w.minmax.p, sizeof(double) * npart, hipMemcpyDeviceToHost, s));
     DTRY(hipStreamSynchronize(s));
     const double *part = w.down.as<double>();
@@ -1500,22 +1505,20 @@ int build_chunk(int c0, int c1, const int *atom_offsets, const double *cells, co
     int *down = w.down.as<int>();
     auto ensure_entries = [&](size_t n) -> hipError_t {
         const size_t nz = std::max<size_t>(n, 1);
-        for (DBuf *b : {&out.idx, &out.type, &out.mirror, &w.st_idx, &w.st_type, &w.st_mate,
+        for (DBuf *b : {&out.idx, &out.type, &out.mirror, &w.st_nbr, &w.st_ctr, &w.st_mate,
                         &w.st_final})
             if (hipError_t e = b->ensure(sizeof(int) * nz))
                 return e;
-        for (DBuf *b : {&out.x, &out.y, &out.z, &out.d, &w.st_d})
+        for (DBuf *b : {&out.x, &out.y, &out.z, &out.d})
             if (hipError_t e = b->ensure(sizeof(double) * nz))
                 return e;
-        if (hipError_t e = w.key.ensure(sizeof(uint64_t) * nz))
-            return e;
-        return w.st_vec.ensure(sizeof(double) * 3 * nz);
+        return w.key.ensure(sizeof(uint64_t) * nz);
     };
     auto rank_lists = [&](int cap, const int *overflow) {
         hipLaunchKernelGGL(list_rank_kernel, dim3((ntot + 3) / 4), dim3(256), 0, s,
                            out.offsets.as<int>(), ntot, cap, overflow, w.key.as<uint64_t>(),
-                           w.st_idx.as<int>(), w.st_type.as<int>(), w.st_vec.as<double>(),
-                           w.st_d.as<double>(), out.idx.as<int>(), out.type.as<int>(),
+                           w.st_nbr.as<int>(), w.st_ctr.as<int>(), w.pts.as<double>(),
+                           w.orig.as<int>(), dtypes, out.idx.as<int>(), out.type.as<int>(),
                            out.x.as<double>(), out.y.as<double>(), out.z.as<double>(),
                            out.d.as<double>(), w.st_final.as<int>());
         hipLaunchKernelGGL(mirror_kernel, dim3((ntot + 3) / 4), dim3(256), 0, s,
@@ -1532,8 +1535,8 @@ int build_chunk(int c0, int c1, const int *atom_offsets, const double *cells, co
         DTRY(ensure_entries((size_t)ntot * cap));
         cb.mate = w.st_mate.as<int>();
         hipLaunchKernelGGL(construct_kernel<2>, dim3((ntot + 3) / 4), dim3(256), 0, s, g, cb,
-                           nullptr, cnt, w.key.as<uint64_t>(), w.st_idx.as<int>(),
-                           w.st_type.as<int>(), w.st_vec.as<double>(), w.st_d.as<double>());
+                           nullptr, cnt, w.key.as<uint64_t>(), w.st_nbr.as<int>(),
+                           w.st_ctr.as<int>());
         DTRY(scan_exclusive(cnt, (int64_t)ntot + 1, out.offsets.as<int>(), w.tmp, scal + 12, s,
                             nullptr, (int)cap));
         rank_lists((int)cap, scal + 10);
@@ -1552,7 +1555,7 @@ int build_chunk(int c0, int c1, const int *atom_offsets, const double *cells, co
 
     // counted build: count, offsets, fill at the cursors, rank within lists
     hipLaunchKernelGGL(construct_kernel<0>, dim3((ntot + 3) / 4), dim3(256), 0, s, g, cb,
-                       cnt, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr);
+                       cnt, nullptr, nullptr, nullptr, nullptr);
     hipLaunchKernelGGL(sum64_kernel, dim3(std::min<unsigned>(blocks(ntot, 256), 1024)), dim3(256),
                        0, s, cnt, (int64_t)ntot, total64, scal + 11);
     // the offsets, and the same values over the counts as the fill cursors
@@ -1577,8 +1580,8 @@ int build_chunk(int c0, int c1, const int *atom_offsets, const double *cells, co
         return MTPX_OK;
     cb.mate = w.st_mate.as<int>();
     hipLaunchKernelGGL(construct_kernel<1>, dim3((ntot + 3) / 4), dim3(256), 0, s, g, cb,
-                       nullptr, cnt, w.key.as<uint64_t>(), w.st_idx.as<int>(),
-                       w.st_type.as<int>(), w.st_vec.as<double>(), w.st_d.as<double>());
+                       nullptr, cnt, w.key.as<uint64_t>(), w.st_nbr.as<int>(),
+                       w.st_ctr.as<int>());
     rank_lists(0, nullptr);
     DTRY(hipGetLastError());
     DTRY(hipStreamSynchronize(s));
