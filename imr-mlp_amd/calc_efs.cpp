@@ -1,15 +1,26 @@
 // mtpx_calc_efs: the calc_efs front end (apps/calc_efs.cpp:179-389, the
 // --device=hip branch) over the C ABI.  Reads structures in the text MLIP
-// configuration format (io/gpio_read_cfg.cpp:319-615), evaluates energy,
-// forces, stress and site energies on the device in structure-preserving
-// chunks (mtpx_set_structures + mtpx_compute_batch, or mtpx_energy with
-// --energy-only), and writes the configurations back
+// configuration format (io/gpio_read_cfg.cpp:319-615) or a VASP POSCAR
+// (GPIO::read_vasp_poscar, io/gpio_read_vasp.cpp:1108-1234), evaluates
+// energy, forces, stress and site energies on the device in
+// structure-preserving chunks (mtpx_set_structures + mtpx_compute_batch, or
+// mtpx_energy with --energy-only), and writes the configurations back
 // (GPIO::write_next_mlpcfg, io/gpio_write.cpp:224-380).
 //
-//   mtpx_calc_efs --pot potential.mtp|.gpm --in input.cfg --out output-efs.cfg
+//   mtpx_calc_efs --pot potential.mtp|.gpm --in input.cfg|POSCAR --out output-efs.cfg
+//       [--input-format cfg|POSCAR] [--index index.map]
 //       [--energy-only] [--no-site-energy] [--lossless] [--show-progress]
 //       [--gpu-id K] [--gpu-batch-atoms N] [--gpu-batch-structures N]
 //       [--deterministic]
+//
+// The input format is the one named, else cfg when the file holds
+// BEGIN_CFG, else POSCAR.  POSCAR element names become species through the
+// reference's species map (GPIO::install_species_map, io/gpio.cpp:103-200):
+// the index file (one element per line, in species order; index.map by
+// default) when it exists, else the element order the potential declares
+// (its potential_tag "elements"), else the periodic table (an element's
+// species is its atomic number); a named index file that is missing is an
+// error unless the potential declares its elements.
 //
 // Read: BEGIN_CFG, Size, an optional Supercell of three rows (periodic in
 // all three directions; without it the structure is a cluster), AtomData
@@ -26,6 +37,7 @@
 
 #include <algorithm>
 #include <climits>
+#include <cctype>
 #include <cmath>
 #include <cstdio>
 #include <cstdlib>
@@ -193,6 +205,197 @@ bool read_config(std::istream &is, Config &c, int index)
     die(where + "missing END_CFG");
 }
 
+// ---- POSCAR --------------------------------------------------------------
+
+// Element symbols by atomic number ("X" for 0), the periodic-table map.
+const char *const kElements[] = {
+    "X",  "H",  "He", "Li", "Be", "B",  "C",  "N",  "O",  "F",  "Ne", "Na", "Mg", "Al", "Si",
+    "P",  "S",  "Cl", "Ar", "K",  "Ca", "Sc", "Ti", "V",  "Cr", "Mn", "Fe", "Co", "Ni", "Cu",
+    "Zn", "Ga", "Ge", "As", "Se", "Br", "Kr", "Rb", "Sr", "Y",  "Zr", "Nb", "Mo", "Tc", "Ru",
+    "Rh", "Pd", "Ag", "Cd", "In", "Sn", "Sb", "Te", "I",  "Xe", "Cs", "Ba", "La", "Ce", "Pr",
+    "Nd", "Pm", "Sm", "Eu", "Gd", "Tb", "Dy", "Ho", "Er", "Tm", "Yb", "Lu", "Hf", "Ta", "W",
+    "Re", "Os", "Ir", "Pt", "Au", "Hg", "Tl", "Pb", "Bi", "Po", "At", "Rn", "Fr", "Ra", "Ac",
+    "Th", "Pa", "U",  "Np", "Pu", "Am", "Cm", "Bk", "Cf", "Es", "Fm", "Md", "No", "Lr", "Rf",
+    "Db", "Sg", "Bh", "Hs", "Mt", "Ds", "Rg", "Cn", "Nh", "Fl", "Mc", "Lv", "Ts", "Og"};
+
+// The element list of a potential_tag's "elements" array in .mtp text
+// (empty when there is none).
+std::vector<std::string> model_elements(const std::string &mtp_text)
+{
+    std::vector<std::string> out;
+    const size_t tag = mtp_text.find("potential_tag");
+    if (tag == std::string::npos)
+        return out;
+    const size_t eol = mtp_text.find('\n', tag);
+    const std::string line = mtp_text.substr(tag, eol == std::string::npos ? std::string::npos
+                                                                             : eol - tag);
+    const size_t key = line.find("\"elements\"");
+    if (key == std::string::npos)
+        return out;
+    const size_t open = line.find('[', key), close = line.find(']', key);
+    if (open == std::string::npos || close == std::string::npos || close < open)
+        return out;
+    const std::string body = line.substr(open + 1, close - open - 1);
+    for (size_t q = body.find('"'); q != std::string::npos;) {
+        const size_t e = body.find('"', q + 1);
+        if (e == std::string::npos)
+            break;
+        out.push_back(body.substr(q + 1, e - q - 1));
+        q = body.find('"', e + 1);
+    }
+    return out;
+}
+
+// install_species_map: element name -> species.
+std::vector<std::string> species_names(const std::string &index, bool index_named,
+                                       const std::vector<std::string> &declared)
+{
+    std::ifstream f(index);
+    if (f) {
+        // GPIO::readmap: the first word of each line, species in line order
+        std::vector<std::string> names;
+        std::string line;
+        while (std::getline(f, line)) {
+            auto t = split(line);
+            if (t.empty())
+                break;
+            names.push_back(t[0]);
+        }
+        if (names.empty())
+            die("cannot read species map: " + index);
+        return names;
+    }
+    bool valid = !declared.empty();
+    for (size_t k = 0; k < declared.size() && valid; ++k) {
+        valid = std::find(std::begin(kElements) + 1, std::end(kElements), declared[k]) !=
+                std::end(kElements);
+        for (size_t q = 0; q < k && valid; ++q)
+            valid = declared[q] != declared[k];
+    }
+    if (valid) {
+        if (index_named)
+            std::fprintf(stderr,
+                         "mtpx_calc_efs: index file \"%s\" not found; using the element order "
+                         "declared by the model\n",
+                         index.c_str());
+        return declared;
+    }
+    if (index_named)
+        die("index file \"" + index +
+            "\" not found and the model does not declare an element order");
+    std::fprintf(stderr,
+                 "mtpx_calc_efs: index file \"%s\" not found; using the periodic table\n",
+                 index.c_str());
+    return std::vector<std::string>(std::begin(kElements), std::end(kElements));
+}
+
+// GPIO::read_vasp_poscar: one periodic structure.  The scale multiplies the
+// cell, or, negative, sets its volume; an optional "Selective dynamics" line
+// (its per-atom flags are read and dropped) precedes Cartesian (C, K) or
+// Direct (D, F) coordinates; direct coordinates are turned into Cartesian
+// ones (row vector times the cell, rows the lattice vectors).
+Config read_poscar(std::istream &is, const std::vector<std::string> &names)
+{
+    Config c;
+    c.periodic = true;
+    std::string line;
+    auto need = [&](const char *what) {
+        if (!std::getline(is, line))
+            die(std::string("POSCAR: missing ") + what);
+    };
+    need("comment line");
+    need("scale");
+    double scale = 0;
+    {
+        bool found = false;
+        for (const auto &t : split(line))
+            if (number(t, scale)) {
+                found = true;
+                break;
+            }
+        if (!found)
+            die("POSCAR: invalid scale");
+    }
+    for (int a = 0; a < 3; ++a) {
+        need("lattice vector");
+        auto t = split(line);
+        if (t.size() < 3)
+            die("POSCAR: invalid lattice vector");
+        for (int b = 0; b < 3; ++b)
+            if (!number(t[b], c.cell[3 * a + b]))
+                die("POSCAR: invalid lattice vector");
+    }
+    double f = scale;
+    if (scale <= 0) {
+        const double *m = c.cell;
+        const double det = m[0] * (m[4] * m[8] - m[5] * m[7]) -
+                           m[1] * (m[3] * m[8] - m[5] * m[6]) +
+                           m[2] * (m[3] * m[7] - m[4] * m[6]);
+        f = std::pow(-scale / std::fabs(det), 1.0 / 3.0);
+    }
+    for (double &v : c.cell)
+        v *= f;
+    need("element names");
+    std::vector<int> chem;
+    for (const auto &t : split(line)) {
+        const auto it = std::find(names.begin(), names.end(), t);
+        if (it == names.end())
+            die("POSCAR: element " + t + " is not in the species map");
+        chem.push_back((int)(it - names.begin()));
+    }
+    need("element counts");
+    {
+        auto t = split(line);
+        if (t.size() < chem.size())
+            die("POSCAR: missing element counts");
+        for (size_t k = 0; k < chem.size(); ++k) {
+            double v = 0;
+            if (!number(t[k], v) || v < 0 || v != std::floor(v) || c.n + v > INT_MAX)
+                die("POSCAR: invalid element count");
+            c.type.insert(c.type.end(), (size_t)v, chem[k]);
+            c.n += (int)v;
+        }
+    }
+    need("coordinate mode");
+    auto mode = [&]() {
+        auto t = split(line);
+        return t.empty() ? '?' : (char)std::toupper((unsigned char)t[0][0]);
+    };
+    char flag = mode();
+    const bool selective = flag == 'S';
+    if (selective) {
+        need("coordinate mode");
+        flag = mode();
+    }
+    bool direct;
+    if (flag == 'C' || flag == 'K')
+        direct = false;
+    else if (flag == 'D' || flag == 'F')
+        direct = true;
+    else
+        die("POSCAR: unknown POSCAR format");
+    c.pos.assign(3 * (size_t)c.n, 0.0);
+    for (int i = 0; i < c.n; ++i) {
+        need("position");
+        auto t = split(line);
+        if (t.size() < (selective ? 6u : 3u))
+            die(selective ? "POSCAR: no selective dynamics info given" : "POSCAR: short position");
+        double p[3];
+        for (int a = 0; a < 3; ++a)
+            if (!number(t[a], p[a]))
+                die("POSCAR: invalid position");
+        for (int a = 3; selective && a < 6; ++a) {
+            const char q = (char)std::toupper((unsigned char)t[a][0]);
+            if (q != 'T' && q != 'F')
+                die("POSCAR: unknown selective dynamics info " + t[a]);
+        }
+        for (int b = 0; b < 3; ++b)
+            c.pos[3 * (size_t)i + b] =
+                direct ? (p[0] * c.cell[b] + p[1] * c.cell[3 + b]) + p[2] * c.cell[6 + b] : p[b];
+    }
+    return c;
+}
+
 void write_num(std::ostream &os, double v, bool lossless, bool lead_space = true)
 {
     char buf[64];
@@ -266,6 +469,8 @@ void check(mtpx_context *ctx, int rc, const char *what)
 int main(int argc, char **argv)
 {
     std::string pot = "potential.mtp", in = "POSCAR", out = "output-efs.cfg";
+    std::string informat, index = "index.map";
+    bool index_named = false;
     bool energy_only = false, site_energy = true, lossless = false, progress = false;
     bool deterministic = false;
     int gpu = 0;
@@ -283,6 +488,12 @@ int main(int argc, char **argv)
             in = value();
         else if (a == "--out" || a == "--output")
             out = value();
+        else if (a == "--input-format" || a == "--if")
+            informat = value();
+        else if (a == "--index" || a == "--id") {
+            index = value();
+            index_named = true;
+        }
         else if (a == "--energy-only")
             energy_only = true;
         else if (a == "--no-site-energy")
@@ -300,7 +511,8 @@ int main(int argc, char **argv)
         else if (a == "--gpu-batch-structures")
             batch_structures = std::atol(value().c_str());
         else if (a == "-h" || a == "--help") {
-            std::puts("mtpx_calc_efs --pot F.mtp --in F.cfg --out F.cfg [--energy-only] "
+            std::puts("mtpx_calc_efs --pot F.mtp --in F.cfg|POSCAR --out F.cfg "
+                      "[--input-format cfg|POSCAR] [--index index.map] [--energy-only] "
                       "[--no-site-energy] [--lossless] [--show-progress] [--deterministic] "
                       "[--gpu-id K] [--gpu-batch-atoms N] [--gpu-batch-structures N]");
             return 0;
@@ -319,21 +531,48 @@ int main(int argc, char **argv)
     std::ifstream inf(in);
     if (!inf)
         die("cannot read " + in);
-    std::vector<Config> cfgs;
-    for (;;) {
-        Config c;
-        if (!read_config(inf, c, (int)cfgs.size()))
-            break;
-        cfgs.push_back(std::move(c));
+    std::string fmt = informat;
+    for (char &ch : fmt)
+        ch = (char)std::tolower((unsigned char)ch);
+    if (fmt.empty()) {
+        // the format by content: a configuration file holds BEGIN_CFG
+        std::string head(4096, '\0');
+        inf.read(&head[0], (std::streamsize)head.size());
+        head.resize((size_t)inf.gcount());
+        fmt = head.find("BEGIN_CFG") != std::string::npos ? "cfg" : "poscar";
+        inf.clear();
+        inf.seekg(0);
     }
+    const bool poscar = fmt == "poscar" || fmt == "vasp" || fmt == "contcar";
+    if (!poscar && fmt != "cfg" && fmt != "mlip" && fmt != "mlp")
+        die("unknown input format " + informat);
 
     mtpx_context *ctx = nullptr;
     check(nullptr, mtpx_create(gpu, &ctx), "mtpx_create");
     // a GPM bundle (by its magic, as GPM::is_file) or .mtp text
-    if (text.size() >= 8 && text.compare(0, 8, "GPMLMODL") == 0)
+    const bool gpm = text.size() >= 8 && text.compare(0, 8, "GPMLMODL") == 0;
+    if (gpm)
         check(ctx, mtpx_load_model_gpm(ctx, text.data(), text.size()), "load potential");
     else
         check(ctx, mtpx_load_model_text(ctx, text.c_str()), "load potential");
+
+    std::vector<Config> cfgs;
+    if (poscar) {
+        // the element order the model declares, from its saved text
+        size_t len = 0;
+        check(ctx, mtpx_save_model_text(ctx, nullptr, 0, &len), "model text");
+        std::string saved(len + 1, '\0');
+        check(ctx, mtpx_save_model_text(ctx, &saved[0], saved.size(), &len), "model text");
+        saved.resize(len);
+        cfgs.push_back(read_poscar(inf, species_names(index, index_named, model_elements(saved))));
+    } else {
+        for (;;) {
+            Config c;
+            if (!read_config(inf, c, (int)cfgs.size()))
+                break;
+            cfgs.push_back(std::move(c));
+        }
+    }
     int info[8];
     check(ctx, mtpx_model_info(ctx, info), "model info");
     double cutoff = 0;

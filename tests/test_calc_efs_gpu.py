@@ -1,7 +1,11 @@
 """mtpx_calc_efs, the calc_efs front end (apps/calc_efs.cpp:179-389) over
-the C ABI: configurations in the text MLIP format in, the same
+the C ABI: configurations in the text MLIP format or a VASP POSCAR
+(GPIO::read_vasp_poscar, io/gpio_read_vasp.cpp:1108-1234) in, the
 configurations with the device's energy, forces, stress and site energies
-out, against the oracle's getEFS of each structure.
+out, against the oracle's getEFS of each structure.  POSCAR element names
+become species through an index file, the element order the potential
+declares, or the periodic table (GPIO::install_species_map,
+io/gpio.cpp:103-200).
 
 Tolerances: 1e-10 relative with --lossless (numbers that read back to the
 same doubles); the fixed-width form carries 8 significant digits, so 1e-7
@@ -153,3 +157,138 @@ def test_fixed_width_and_energy_only(run_case):
         assert "fx" not in g["cols"] and "site_en" not in g["cols"] and "stress" not in g
     got, _ = run("--no-site-energy", "--lossless", "--deterministic")
     assert "site_en" not in got[0]["cols"] and "fx" in got[0]["cols"]
+
+
+# ---- POSCAR ----------------------------------------------------------------
+
+def _poscar(path, s, names, direct=True, scale=1.0, selective=False, cell_scale=1.0):
+    """POSCAR of structure s (atoms grouped by species, as POSCAR keeps
+    them), the cell written divided by cell_scale.  Returns the structure
+    in that order."""
+    order = np.argsort(s.types, kind="stable")
+    pos, types = s.pos[order], s.types[order]
+    cell = s.cell / cell_scale
+    with open(path, "w") as f:
+        f.write("synthetic test structure\n%.17g\n" % float(scale))
+        for r in cell:
+            f.write("  %.17g %.17g %.17g\n" % tuple(r))
+        present = sorted(set(types.tolist()))
+        f.write("  " + " ".join(names[t] for t in present) + "\n")
+        f.write("  " + " ".join(str(int((types == t).sum())) for t in present) + "\n")
+        if selective:
+            f.write("Selective dynamics\n")
+        f.write("Direct\n" if direct else "Cartesian\n")
+        frac = pos @ np.linalg.inv(s.cell)
+        for i in range(s.n):
+            v = frac[i] if direct else pos[i]
+            f.write("  %.17g %.17g %.17g%s\n" % (tuple(v) + (" T T F" if selective else "",)))
+    st = S.Structure(s.cell.copy(), pos.copy(), types.astype(np.int32), s.pbc.copy())
+    if direct:
+        # the reader's Cartesian positions: row vector times the cell, summed
+        # left to right
+        c = s.cell
+        st.pos = np.stack([(frac[:, 0] * c[0, b] + frac[:, 1] * c[1, b]) + frac[:, 2] * c[2, b]
+                           for b in range(3)], 1)
+    return st
+
+
+def _poscar_case(tmp_path, text, s, names, flags=(), **kw):
+    mtp = tmp_path / "pot.mtp"
+    mtp.write_text(text)
+    st = _poscar(tmp_path / "POSCAR", s, names, **kw)
+    out = tmp_path / "out.cfg"
+    r = subprocess.run([EXE, "--pot", str(mtp), "--in", str(tmp_path / "POSCAR"), "--out",
+                        str(out), "--lossless"] + list(flags), capture_output=True, text=True,
+                       timeout=120, cwd=str(tmp_path))
+    return st, r, out
+
+
+def _check_against_oracle(model, st, out, tol=1e-10):
+    got = _read_cfg(out)
+    assert len(got) == 1
+    g = got[0]
+    pos, E, F, St, se = _oracle(model, st)
+    c = g["cols"]
+    assert np.array_equal(c["type"], st.types)
+    assert np.allclose(np.stack([c["cartes_x"], c["cartes_y"], c["cartes_z"]], 1), pos,
+                       rtol=0, atol=1e-12)
+    assert rel_err(g["energy"], E) < tol
+    assert rel_err(np.stack([c["fx"], c["fy"], c["fz"]], 1), F) < tol
+    voigt = np.array([St[0, 0], St[1, 1], St[2, 2], St[1, 2], St[0, 2], St[0, 1]])
+    assert rel_err(g["stress"], voigt) < tol
+
+
+def _two_species_structure(seed):
+    rng = S.rng_for(seed)
+    s = S.displace(S.strain(S.lattice("fcc", (2, 2, 2), 3.6), rng, 0.03), rng, 0.1)
+    s.types = (S.uniform(rng, s.n) * 2).astype(np.int32)
+    return s
+
+
+def test_poscar_direct_with_index_map(tmp_path):
+    """Direct coordinates, element names mapped by index.map (found in the
+    working directory, as the reference's default): species = line order."""
+    text = S.random_model("shapeev-16.mtp", 2, 8, 1.9, 5.0, -0.05, 0.05, S.rng_for(1203))
+    (tmp_path / "index.map").write_text("Al 1.43\nNi 1.24\n")
+    s = _two_species_structure(1204)
+    st, r, out = _poscar_case(tmp_path, text, s, ["Al", "Ni"])
+    assert r.returncode == 0, r.stderr
+    _check_against_oracle(O.Model(text), st, out)
+
+
+def test_poscar_cartesian_selective_volume_scale(tmp_path):
+    """Cartesian coordinates after a Selective dynamics line (its flags are
+    read and dropped) and a negative scale, which sets the cell volume; an
+    index file named on the command line."""
+    text = S.random_model("shapeev-16.mtp", 2, 8, 1.9, 5.0, -0.05, 0.05, S.rng_for(1205))
+    (tmp_path / "elements.txt").write_text("Ni\nAl\n")
+    s = _two_species_structure(1206)
+    vol = abs(np.linalg.det(s.cell))
+    st, r, out = _poscar_case(tmp_path, text, s, ["Ni", "Al"],
+                              flags=("--index", "elements.txt", "--input-format", "POSCAR"),
+                              direct=False, selective=True, scale=-vol, cell_scale=1.25)
+    assert r.returncode == 0, r.stderr
+    # the cell comes back scaled to the volume: (vol / (vol / 1.25^3))^(1/3) = 1.25
+    g = _read_cfg(out)[0]
+    assert np.allclose(g["cell"], s.cell, rtol=1e-13, atol=1e-13)
+    st.cell = g["cell"]
+    _check_against_oracle(O.Model(text), st, out)
+
+
+def test_poscar_species_from_model_elements(tmp_path):
+    """Without an index file the element order the potential declares (its
+    potential_tag "elements") maps the names; an element outside it is
+    refused."""
+    tag = ('{"elements":["Ta","W"],"model":"linear","schema":"gpml.mtp.metadata",'
+           '"type":"MTP","version":1}')
+    text = S.random_model("shapeev-16.mtp", 2, 8, 1.9, 5.0, -0.05, 0.05, S.rng_for(1207),
+                          tag=tag)
+    s = _two_species_structure(1208)
+    st, r, out = _poscar_case(tmp_path, text, s, ["Ta", "W"])
+    assert r.returncode == 0, r.stderr
+    _check_against_oracle(O.Model(text), st, out)
+    st, r, _ = _poscar_case(tmp_path, text, s, ["Ta", "Mo"])
+    assert r.returncode != 0 and "element Mo is not in the species map" in r.stderr
+    # a named index file that is missing: the declared order is used, with a warning
+    st, r, out = _poscar_case(tmp_path, text, s, ["Ta", "W"], flags=("--index", "none.map"))
+    assert r.returncode == 0 and "using the element order declared by the model" in r.stderr
+
+
+def test_poscar_periodic_table_and_errors(tmp_path):
+    """No index file and no declared elements: species are atomic numbers
+    (X = 0, H = 1), so a two-species model takes X and H; a named index file
+    that is missing is then an error; a bad coordinate mode is refused."""
+    text = S.random_model("shapeev-16.mtp", 2, 8, 1.9, 5.0, -0.05, 0.05, S.rng_for(1209))
+    s = _two_species_structure(1210)
+    s.types[:] = 1
+    st, r, out = _poscar_case(tmp_path, text, s, ["X", "H"])
+    assert r.returncode == 0, r.stderr
+    assert "using the periodic table" in r.stderr
+    _check_against_oracle(O.Model(text), st, out)
+    _, r, _ = _poscar_case(tmp_path, text, s, ["X", "H"], flags=("--index", "missing.map"))
+    assert r.returncode != 0 and "does not declare an element order" in r.stderr
+    (tmp_path / "POSCAR").write_text("x\n1.0\n5 0 0\n0 5 0\n0 0 5\nH\n1\nQ\n0 0 0\n")
+    r = subprocess.run([EXE, "--pot", str(tmp_path / "pot.mtp"), "--in",
+                        str(tmp_path / "POSCAR"), "--out", str(tmp_path / "o.cfg")],
+                       capture_output=True, text=True, timeout=120, cwd=str(tmp_path))
+    assert r.returncode != 0 and "unknown POSCAR format" in r.stderr
