@@ -8,13 +8,15 @@
 // (GPIO::write_next_mlpcfg, io/gpio_write.cpp:224-380).
 //
 //   mtpx_calc_efs --pot potential.mtp|.gpm --in input.cfg|POSCAR --out output-efs.cfg
-//       [--input-format cfg|POSCAR] [--index index.map]
+//       [--input-format cfg|POSCAR|bin] [--index index.map]
 //       [--energy-only] [--no-site-energy] [--lossless] [--show-progress]
 //       [--gpu-id K] [--gpu-batch-atoms N] [--gpu-batch-structures N]
 //       [--deterministic]
 //
-// The input format is the one named, else cfg when the file holds
-// BEGIN_CFG, else POSCAR.  POSCAR element names become species through the
+// Binary configurations (io/gpio_binary.h, GPIO::load_next_from_mlpcfg_binary,
+// io/gpio_read_cfg.cpp:38-316) are read too.  The input format is the one
+// named (cfg, POSCAR, bin), else bin when the file starts with GPMLBIN2, cfg
+// when it holds BEGIN_CFG, else POSCAR.  POSCAR element names become species through the
 // reference's species map (GPIO::install_species_map, io/gpio.cpp:103-200):
 // the index file (one element per line, in species order; index.map by
 // default) when it exists, else the element order the potential declares
@@ -41,6 +43,7 @@
 #include <cmath>
 #include <cstdio>
 #include <cstdlib>
+#include <cstdint>
 #include <cstring>
 #include <fstream>
 #include <iostream>
@@ -52,7 +55,8 @@ namespace {
 
 struct Config {
     int n = 0;
-    bool periodic = false;
+    bool periodic = false;  // all three axes (text cfg with a Supercell, POSCAR)
+    int pbc[3] = {0, 0, 0};
     double cell[9] = {0, 0, 0, 0, 0, 0, 0, 0, 0};
     std::vector<int> type;
     std::vector<double> pos;              // [n][3]
@@ -114,6 +118,7 @@ bool read_config(std::istream &is, Config &c, int index)
         die(where + "truncated");
     if (line.find("Supercell") != std::string::npos) {
         c.periodic = true;
+        c.pbc[0] = c.pbc[1] = c.pbc[2] = 1;
         for (int a = 0; a < 3; ++a) {
             if (!std::getline(is, line))
                 die(where + "truncated Supercell");
@@ -298,6 +303,7 @@ Config read_poscar(std::istream &is, const std::vector<std::string> &names)
 {
     Config c;
     c.periodic = true;
+    c.pbc[0] = c.pbc[1] = c.pbc[2] = 1;
     std::string line;
     auto need = [&](const char *what) {
         if (!std::getline(is, line))
@@ -394,6 +400,130 @@ Config read_poscar(std::istream &is, const std::vector<std::string> &names)
                 direct ? (p[0] * c.cell[b] + p[1] * c.cell[3 + b]) + p[2] * c.cell[6 + b] : p[b];
     }
     return c;
+}
+
+// ---- binary configurations ---------------------------------------------
+//
+// GPIO::load_next_from_mlpcfg_binary (io/gpio_read_cfg.cpp:38-316) over the
+// frame layout of io/gpio_binary.h: "GPMLBIN2", a uint32 version (2 or 3)
+// and an int32 atom count, then tagged records up to '#'.  The cell is
+// written as Eigen stores a 3 x 3 matrix (column-major, the rows of the
+// reference's cell being lattice vectors); positions are 3 doubles per atom,
+// types an int32 per atom, the periodicity three bytes (version 2 has none
+// and is periodic).  The other records (forces, energies, stresses, per-atom
+// and global attributes) are read past; Feature records are kept.
+template <class T>
+bool get(std::istream &is, T &v)
+{
+    return (bool)is.read(reinterpret_cast<char *>(&v), sizeof v);
+}
+
+bool skip(std::istream &is, long long bytes)
+{
+    if (bytes < 0)
+        return false;
+    is.ignore(bytes);
+    return is.gcount() == bytes;
+}
+
+bool get_string(std::istream &is, std::string &v)
+{
+    int32_t n = 0;
+    if (!get(is, n) || n < 0 || n > (1 << 20))
+        return false;
+    v.resize((size_t)n);
+    return n == 0 || (bool)is.read(&v[0], n);
+}
+
+// false at a clean end of input; dies on a malformed frame.
+bool read_binary(std::istream &is, Config &c, int index)
+{
+    if (is.peek() == std::char_traits<char>::eof())
+        return false;
+    const std::string where = "binary configuration " + std::to_string(index) + ": ";
+    char magic[8];
+    uint32_t version = 0;
+    int32_t natoms = 0;
+    if (!is.read(magic, 8) || std::memcmp(magic, "GPMLBIN2", 8) != 0 || !get(is, version) ||
+        !get(is, natoms) || version < 2 || version > 3 || natoms < 0 || natoms > (1 << 28) / 3)
+        die(where + "invalid binary mlpcfg header");
+    c.n = natoms;
+    c.type.assign((size_t)natoms, 0);
+    c.pos.assign(3 * (size_t)natoms, 0.0);
+    bool has_cell = false, has_pos = false, has_pbc = false;
+    const long long n = natoms;
+    for (;;) {
+        char tag = 0;
+        if (!get(is, tag))
+            die(where + "truncated");
+        bool ok = true;
+        std::string name, value;
+        int32_t rows = 0;
+        switch (tag) {
+        case 'l': {
+            double m[9];
+            ok = (bool)is.read(reinterpret_cast<char *>(m), sizeof m);
+            for (int i = 0; i < 3; ++i)
+                for (int j = 0; j < 3; ++j)
+                    c.cell[3 * i + j] = m[i + 3 * j];
+            has_cell = true;
+            break;
+        }
+        case 'p':
+            ok = n == 0 || (bool)is.read(reinterpret_cast<char *>(c.pos.data()),
+                                         (std::streamsize)(sizeof(double) * 3 * n));
+            has_pos = true;
+            break;
+        case 't':
+            ok = n == 0 || (bool)is.read(reinterpret_cast<char *>(c.type.data()),
+                                         (std::streamsize)(sizeof(int32_t) * n));
+            break;
+        case 'b': {
+            uint8_t f[3];
+            ok = (bool)is.read(reinterpret_cast<char *>(f), 3);
+            for (int d = 0; d < 3 && ok; ++d) {
+                ok = f[d] <= 1;
+                c.pbc[d] = f[d];
+            }
+            has_pbc = true;
+            break;
+        }
+        case 'f': case 'm': case 'u': ok = skip(is, 24 * n); break;      // 3 doubles per atom
+        case 'v': case 'M': case 'c': ok = skip(is, 8 * n); break;       // a double per atom
+        case 'i': ok = skip(is, 4 * n); break;                           // an int per atom
+        case 'h': case 'e': ok = skip(is, 8); break;
+        case 's': ok = skip(is, 72); break;
+        case 'F':
+            ok = get_string(is, name) && get_string(is, value);
+            if (ok)
+                c.features.push_back("Feature   " + name + "\t" + value);
+            break;
+        case 'A': ok = get_string(is, name) && skip(is, 8 * n); break;
+        case 'H': ok = get_string(is, name) && skip(is, 4 * n); break;
+        case 'B': case 'I':
+            ok = get_string(is, name) && get(is, rows) && rows >= 0 && rows <= (1 << 28) &&
+                 (n == 0 || rows <= (1 << 28) / n) &&
+                 skip(is, (tag == 'B' ? 8LL : 4LL) * rows * n);
+            break;
+        case 'C': ok = get_string(is, name) && skip(is, 8); break;
+        case 'E': ok = get_string(is, name) && skip(is, 4); break;
+        case 'D': case 'G':
+            ok = get_string(is, name) && get(is, rows) && rows >= 0 && rows <= (1 << 28) &&
+                 skip(is, (tag == 'D' ? 8LL : 4LL) * rows);
+            break;
+        case '#':
+            if (!has_cell || !has_pos)
+                die(where + "no cell or positions");
+            if (!has_pbc)  // version 2: periodic
+                c.pbc[0] = c.pbc[1] = c.pbc[2] = 1;
+            c.periodic = c.pbc[0] && c.pbc[1] && c.pbc[2];
+            return true;
+        default:
+            die(where + "unsupported binary mlpcfg tag " + std::string(1, tag));
+        }
+        if (!ok)
+            die(where + "truncated or invalid record '" + std::string(1, tag) + "'");
+    }
 }
 
 void write_num(std::ostream &os, double v, bool lossless, bool lead_space = true)
@@ -512,7 +642,7 @@ int main(int argc, char **argv)
             batch_structures = std::atol(value().c_str());
         else if (a == "-h" || a == "--help") {
             std::puts("mtpx_calc_efs --pot F.mtp --in F.cfg|POSCAR --out F.cfg "
-                      "[--input-format cfg|POSCAR] [--index index.map] [--energy-only] "
+                      "[--input-format cfg|POSCAR|bin] [--index index.map] [--energy-only] "
                       "[--no-site-energy] [--lossless] [--show-progress] [--deterministic] "
                       "[--gpu-id K] [--gpu-batch-atoms N] [--gpu-batch-structures N]");
             return 0;
@@ -535,16 +665,20 @@ int main(int argc, char **argv)
     for (char &ch : fmt)
         ch = (char)std::tolower((unsigned char)ch);
     if (fmt.empty()) {
-        // the format by content: a configuration file holds BEGIN_CFG
+        // the format by content: a binary configuration starts with its
+        // magic, a text one holds BEGIN_CFG, anything else is a POSCAR
         std::string head(4096, '\0');
         inf.read(&head[0], (std::streamsize)head.size());
         head.resize((size_t)inf.gcount());
-        fmt = head.find("BEGIN_CFG") != std::string::npos ? "cfg" : "poscar";
+        fmt = head.compare(0, 8, "GPMLBIN2") == 0        ? "bin"
+              : head.find("BEGIN_CFG") != std::string::npos ? "cfg"
+                                                           : "poscar";
         inf.clear();
         inf.seekg(0);
     }
     const bool poscar = fmt == "poscar" || fmt == "vasp" || fmt == "contcar";
-    if (!poscar && fmt != "cfg" && fmt != "mlip" && fmt != "mlp")
+    const bool binary = fmt == "bin" || fmt == "binary" || fmt == "cfgbin";
+    if (!poscar && !binary && fmt != "cfg" && fmt != "mlip" && fmt != "mlp")
         die("unknown input format " + informat);
 
     mtpx_context *ctx = nullptr;
@@ -568,7 +702,8 @@ int main(int argc, char **argv)
     } else {
         for (;;) {
             Config c;
-            if (!read_config(inf, c, (int)cfgs.size()))
+            if (!(binary ? read_binary(inf, c, (int)cfgs.size())
+                         : read_config(inf, c, (int)cfgs.size())))
                 break;
             cfgs.push_back(std::move(c));
         }
@@ -602,10 +737,10 @@ int main(int argc, char **argv)
             for (int q = 0; q < 9; ++q)
                 cells[9 * (size_t)k + q] = c.cell[q];
             for (int a = 0; a < 3; ++a)
-                pbc[3 * (size_t)k + a] = c.periodic ? 1 : 0;
-            // Atoms::wrap before the lists (calc_efs.cpp:195), as the
-            // reference writes the wrapped positions back
-            if (c.periodic)
+                pbc[3 * (size_t)k + a] = c.pbc[a] ? 1 : 0;
+            // Atoms::wrap before the lists (calc_efs.cpp:195), along the
+            // periodic axes, as the reference writes the wrapped positions back
+            if (c.pbc[0] || c.pbc[1] || c.pbc[2])
                 check(ctx, mtpx_wrap(c.cell, &pbc[3 * (size_t)k], c.n, c.pos.data()), "wrap");
             pos.insert(pos.end(), c.pos.begin(), c.pos.end());
             types.insert(types.end(), c.type.begin(), c.type.end());

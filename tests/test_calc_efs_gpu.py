@@ -292,3 +292,67 @@ def test_poscar_periodic_table_and_errors(tmp_path):
                         str(tmp_path / "POSCAR"), "--out", str(tmp_path / "o.cfg")],
                        capture_output=True, text=True, timeout=120, cwd=str(tmp_path))
     assert r.returncode != 0 and "unknown POSCAR format" in r.stderr
+
+
+# ---- binary configurations ----------------------------------------------------
+
+def _bin_frame(s, version=3, extras=True):
+    """One frame of the binary configuration format (io/gpio_binary.h): the
+    cell as Eigen stores it (column-major), positions, types, periodicity
+    (version 3) and, with extras, records the reader passes over."""
+    import struct
+    out = [b"GPMLBIN2", struct.pack("<Ii", version, s.n)]
+    out += [b"l", np.asarray(s.cell, "<f8").T.tobytes()]
+    out += [b"p", np.asarray(s.pos, "<f8").tobytes(), b"t", np.asarray(s.types, "<i4").tobytes()]
+    if version >= 3:
+        out += [b"b", bytes(int(v) for v in s.pbc)]
+    if extras:
+        name = b"tag"
+        out += [b"e", struct.pack("<d", -1.5), b"s", np.zeros(9).tobytes(),
+                b"f", np.ones((s.n, 3)).tobytes(), b"c", np.arange(s.n, dtype="<f8").tobytes(),
+                b"A", struct.pack("<i", len(name)) + name + np.zeros(s.n).tobytes(),
+                b"I", struct.pack("<i", len(name)) + name + struct.pack("<i", 2)
+                + np.zeros((2, s.n), "<i4").tobytes(),
+                b"D", struct.pack("<i", 1) + b"g" + struct.pack("<i", 3) + np.zeros(3).tobytes(),
+                b"F", struct.pack("<i", 6) + b"EFS_by" + struct.pack("<i", 3) + b"dft"]
+    out.append(b"#")
+    return b"".join(out)
+
+
+def test_binary_configurations(run_case, tmp_path):
+    """Binary frames (found by their magic): a periodic cell with every kind
+    of record the reader passes over, a slab periodic along x and y, and a
+    version-2 frame without periodicity flags (periodic)."""
+    model, structs, _ = run_case
+    rng = S.rng_for(1211)
+    slab = S.displace(S.lattice("fcc", (3, 3, 2), 3.6), rng, 0.1)
+    slab.types = (S.uniform(rng, slab.n) * 2).astype(np.int32)
+    slab.pbc = np.array([1, 1, 0], np.int32)
+    frames = [(structs[0], 3, True), (slab, 3, False), (structs[1], 2, False)]
+    path = tmp_path / "in.bin"
+    path.write_bytes(b"".join(_bin_frame(s, v, x) for s, v, x in frames))
+    mtp = tmp_path / "pot.mtp"
+    mtp.write_text(model.save_text())
+    out = tmp_path / "out.cfg"
+    r = subprocess.run([EXE, "--pot", str(mtp), "--in", str(path), "--out", str(out),
+                        "--lossless"], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stderr
+    got = _read_cfg(out)
+    assert len(got) == 3
+    for (s, _, x), g in zip(frames, got):
+        pos, E, F, St, se = _oracle(model, s)
+        c = g["cols"]
+        assert np.array_equal(c["type"], s.types)
+        assert np.array_equal(np.stack([c["cartes_x"], c["cartes_y"], c["cartes_z"]], 1), pos)
+        assert rel_err(g["energy"], E) < 1e-10
+        assert rel_err(np.stack([c["fx"], c["fy"], c["fz"]], 1), F) < 1e-10
+        voigt = np.array([St[0, 0], St[1, 1], St[2, 2], St[1, 2], St[0, 2], St[0, 1]])
+        assert rel_err(g["stress"], voigt) < 1e-10
+        assert np.array_equal(g["cell"], s.cell)
+        assert len(g["features"]) == (1 if x else 0)
+    # a frame with an unknown record is refused
+    bad = _bin_frame(structs[0], 3, False)[:-1] + b"Z#"
+    path.write_bytes(bad)
+    r = subprocess.run([EXE, "--pot", str(mtp), "--in", str(path), "--out", str(out)],
+                       capture_output=True, text=True, timeout=120)
+    assert r.returncode != 0 and "unsupported binary mlpcfg tag Z" in r.stderr
