@@ -85,11 +85,12 @@ __global__ void box_rank_kernel(const int *box, const int *box_start, const int 
 
 // Rank every staged entry within its list by key and write it to its final
 // slot (SoA); a staged entry is its key and its two points (neighbour,
-// centre), from which the displacement and distance are formed again.  One wave per list: lanes take 64 entries at a time and count
-// the list's smaller keys, read 64 at a time and broadcast lane by lane
-// (keys within a list are distinct).  The staged entries of list l lie at
-// its final offsets (cap == 0) or in its bin from l cap; with bins, a set
-// overflow flag means the staging is incomplete and nothing is written.
+// centre), from which the displacement and distance are formed again.  One
+// wave per list: lanes take 64 entries at a time and count the list's
+// smaller keys, read 64 at a time and broadcast lane by lane (keys within a
+// list are distinct).  The staged entries of list l lie at its final offsets
+// (cap == 0) or in its bin from l cap; with bins, a set overflow flag means
+// the staging is incomplete and nothing is written.
 __device__ __forceinline__ uint64_t readlane_u64(uint64_t v, int l)
 {
     const unsigned lo = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)v, l);
@@ -1083,8 +1084,9 @@ __global__ __launch_bounds__(256) void construct_kernel(Seg g, Construct cb, int
                 if (put1)
                     cb.mate[q1] = (int)q;
             } else if (put1) {
-                // an image of the centre: the opposite image is an entry of
-                // its own, and the pair of them cancels either way round
+                // an image of the centre is its own mirror: the reaction it
+                // takes back from its own atom cancels the force it gave
+                // (the opposite image is another entry of the same list)
                 cb.mate[q1] = (int)q1;
             }
         }
