@@ -238,6 +238,7 @@ int install_model(mtpx_context *ctx, Model &&m)
         HIP_TRY(upload(ctx->lin_ent, lp.slot_L, s), "upload model");
         HIP_TRY(upload(ctx->lin_estart, lp.slot_mask, s), "upload model");
         HIP_TRY(upload(ctx->lin_chunk, lp.chunk_s0, s), "upload model");
+        HIP_TRY(upload(ctx->lin_cscal, lp.chunk_scalar, s), "upload model");
         HIP_TRY(upload(ctx->lin_maskw, lp.maskw, s), "upload model");
         HIP_TRY(upload(ctx->lin_clist, lp.clist, s), "upload model");
         HIP_TRY(upload(ctx->lin_walk, lp.walk, s), "upload model");
@@ -270,6 +271,7 @@ int install_model(mtpx_context *ctx, Model &&m)
         L.slot_L = ctx->lin_ent.as<int>();
         L.slot_mask = ctx->lin_estart.as<int>();
         L.chunk_s0 = ctx->lin_chunk.as<int>();
+        L.chunk_scalar = ctx->lin_cscal.as<int>();
         L.maskw = ctx->lin_maskw.as<int>();
         L.clist = ctx->lin_clist.as<int>();
         L.walk = ctx->lin_walk.as<int>();

@@ -73,7 +73,7 @@ struct mtpx_context {
     LinPlan lin;
     DevLin dl{};
     DBuf lin_level, lin_steps, lin_lcomb, lin_comb, lin_ent, lin_estart, lin_chunk, lin_maskw,
-        lin_clist, lin_flevel, lin_fsteps, lin_flcomb, lin_fcomb, lin_walk, lin_walk_off;
+        lin_clist, lin_flevel, lin_fsteps, lin_flcomb, lin_fcomb, lin_walk, lin_walk_off, lin_cscal;
     DBuf comp, row_src, row_sw, row_y, rowsA, rowsY, gram_part, gram_out, lin_pair, lin_site;
     // tile path: walk-order Jacobian values per site, structure lists per size class
     DBuf lin_lw, lin_tiles;
@@ -134,7 +134,7 @@ struct mtpx_context {
                         &nbh_tmp.d, &nbh_tmp.center_type, &nbh.mirror, &nbh_tmp.mirror,
                         &lin_level, &lin_steps, &lin_lcomb,
                         &lin_comb, &lin_ent, &lin_estart, &lin_chunk, &lin_maskw, &lin_clist,
-                        &lin_walk, &lin_walk_off,
+                        &lin_walk, &lin_walk_off, &lin_cscal,
                         &comp, &row_src, &row_sw, &row_y, &rowsA, &rowsY, &gram_part, &gram_out,
                         &lin_pair, &lin_site, &lin_flevel, &lin_fsteps, &lin_flcomb,
                         &lin_fcomb, &lin_lw, &lin_tiles})

@@ -1,30 +1,30 @@
 // Linear-fit kernels for gfx950 (fp64).
 //
-//   lin_site_kernel   per site: the scalar moments (energy components) and,
-//                     for every neighbour entry, dm_s/dr_j of every scalar s
-//                     into a pair buffer, chunk-major (PotMTP::CalcEFSCmpt_R,
-//                     potentials/potential_mtp.cpp:2675-2707, over
-//                     CalcSiteBasisDers, :3163-3280)
-//   lin_gather_kernel force rows sum_j dm/dr_j - sum_{i: j of i} dm_i/dr_j
-//                     and per-atom stress partials -sum_j dm/dr_j r_j, read
-//                     from the pair buffer through the lists and the
-//                     reverse index (fixed order, no atomics)
-//   lin_reduce_kernel energy and stress components per structure, ordered
+//   lin_jac_kernel    one wave per site: the scalar moments (the site's
+//                     energy components) and the sparse site Jacobian
+//                     L[s][b] = dm_s/dm_b, exported in walk order
+//                     (PotMTP::CalcEFSCmpt_R, potentials/potential_mtp.cpp:
+//                     2675-2707, over CalcSiteBasisDers, :3163-3280)
+//   lin_tile_kernel   one wave per (structure, chunk of scalars): force rows
+//                     sum_{e in list(i)} D_e - sum_{e: idx[e] = i} D_e with
+//                     D_e = dm_s/dr_e = sum_b L[s][b] grad_r(f_b Y_b)(r_e),
+//                     accumulated in an LDS tile in site order, and the
+//                     stress components -sum_e D_e r_e
+//   lin_reduce_kernel energy components and species counts per structure,
+//                     ordered
 //   rows_kernel       AddLinearFast rows (train/train_mtp.cpp:1289-1395):
 //                     component rows scaled by sqrt(w), targets sqrt(w) y
 //
-// lin_site_kernel runs one wave per site.  The reference propagates the
-// Jacobian of every moment w.r.t. all 3 n_i coordinates through the rules.
-// Here the scalar moments are differentiated through the sparse site
-// Jacobian L[s][b] = dm_map(s)/dm_b instead: L is computed once per site by
-// a step table (the rule-table machinery), then lanes take neighbours and
-// form dm_s/dr_j = sum_b L[s][b] grad_r(f_b Y_b)(r_j) for a chunk of
-// scalars at a time.  Structures are processed in groups whose pair buffer
-// fits a fixed budget.
+// The reference propagates the Jacobian of every moment w.r.t. all 3 n_i
+// coordinates through the rules.  Here the scalar moments are
+// differentiated through L instead: L comes from a step table (the
+// rule-table machinery) once per site, then lanes take neighbour entries and
+// form D_e for a chunk of scalars at a time.  The chunks group scalars that
+// share basic moments (build_lin_plan).
 //
 // The file is compiled twice (two objects, so the two halves of the longest
-// compile run in parallel): MTPX_LIN_PART 2 holds the site kernels of the
-// compiled level-16 walk and of level 20 (launch_lin_site_part2); the
+// compile run in parallel): MTPX_LIN_PART 2 holds the tile kernels of the
+// compiled level-16 walk and of level 20 (launch_lin_tile_part2); the
 // default part holds everything else.
 #include "mtp_device.hpp"
 
@@ -115,7 +115,7 @@ static_assert(shell_inverse_ok(), "shell_a/shell_b must invert shell_index");
 template <class P>
 __device__ __forceinline__ void lin_apply(int mk, int sl, double gx, double gy, double gz,
                                           LinWalk &w, const double *ws,
-                                          double (&acc)[3 * kLinChunk])
+                                          double (&acc)[kLinAcc])
 {
     static_for<0, kLinChunk>([&](auto K) __attribute__((always_inline)) {
         constexpr int k = decltype(K)::value;
@@ -143,7 +143,7 @@ __device__ __forceinline__ void lin_apply(int mk, int sl, double gx, double gy, 
 template <int NU, class P>
 __device__ __forceinline__ void lin_shells(const DevModel &m, const Nbr<P::M> &q,
                                            const double *prev, int &slot, LinWalk &w,
-                                           const double *ws, double (&acc)[3 * kLinChunk])
+                                           const double *ws, double (&acc)[kLinAcc])
 {
     double cur[shell_size(NU)];
     if constexpr (NU == 0)
@@ -269,7 +269,7 @@ constexpr int walk_pos(int c, int sl)
 // constant lanes; otherwise from the site's work space in LDS.
 template <class CP, int C, int NU, class P, bool kStaged = false>
 __device__ __forceinline__ void lin_shells_cp(const Nbr<P::M> &q, const double *prev,
-                                              const double *ws, double (&acc)[3 * kLinChunk],
+                                              const double *ws, double (&acc)[kLinAcc],
                                               double lc0 = 0.0, double lc1 = 0.0)
 {
     double cur[shell_size(NU)];
@@ -322,7 +322,7 @@ __device__ __forceinline__ void lin_shells_cp(const Nbr<P::M> &q, const double *
 // The compiled walk of chunk `ch` (a chain of uniform compares).
 template <class CP, int C, class P, bool kStaged = false>
 __device__ __forceinline__ void lin_chunk_cp(int ch, const Nbr<P::M> &q, const double *ws,
-                                             double (&acc)[3 * kLinChunk], double lc0 = 0.0,
+                                             double (&acc)[kLinAcc], double lc0 = 0.0,
                                              double lc1 = 0.0)
 {
     if (ch == C) {
@@ -397,8 +397,9 @@ __global__ __launch_bounds__(kWave *kMaxWaves) void lin_jac_kernel(DevModel m, D
 // order: one wave is the only writer of its rows, so the sums are
 // repeatable.  The structure's stress
 // components -sum_e D_e[a][s] r_e[b] are summed per lane in registers and
-// over the wave at the end.  The site's walk-order L values are staged in
-// LDS; the walk is the site kernel's.
+// over the wave at the end.  The site's walk-order L values come in lane
+// registers (compiled and exact walks) or through a stage in LDS (run-time
+// walks).
 template <class P, class CP>
 __global__ __launch_bounds__(kWave) void lin_tile_kernel(DevModel m, DevLin L, DevNeighbors nb,
                                                          LinTile t)
@@ -413,17 +414,22 @@ __global__ __launch_bounds__(kWave) void lin_tile_kernel(DevModel m, DevLin L, D
         return;
     const int c = t.structs[item % t.count], ch = item / t.count;
     const int i0 = t.soff[c], i1 = t.soff[c + 1], N = i1 - i0;
-    const int s0 = L.chunk_s0[ch], w = L.chunk_s0[ch + 1] - s0;
+    // the chunk's scalars: its output columns are Z + cols[k]
+    const int q0 = L.chunk_s0[ch], w = L.chunk_s0[ch + 1] - q0;
+    const int *cols = L.chunk_scalar + q0;
     const int wb = L.walk_off[ch], ne = L.walk_off[ch + 1] - wb;
     // tile row: [3][kLinChunk] and one pad double, so that rows are an odd
     // number of doubles apart and the lanes' atomics on different rows fall
     // in different banks
     constexpr int kRow = 3 * kLinChunk + 1;
 
+    // compiled and exact walks read a site's L values from lane registers;
+    // the run-time walks from a stage in LDS
+    constexpr bool kLaneL = !std::is_void_v<CP> || P::exact;
     double *coef = lds;
     const int ncr = m.Z * m.Z * m.M * m.R;
     double *lch = lds + ((ncr + 3) & ~3);
-    double *tile = lch + ((L.max_walk + 3) & ~3);
+    double *tile = lch + (kLaneL ? 0 : ((L.max_walk + 3) & ~3));
     for (int k = lane; k < ncr; k += kWave)
         coef[k] = m.radial[k];
     if (lds_tile)
@@ -433,8 +439,12 @@ __global__ __launch_bounds__(kWave) void lin_tile_kernel(DevModel m, DevLin L, D
 #pragma unroll
     for (int k = 0; k < 9 * kLinChunk; ++k)
         st[k] = 0.0;
-    // fc rows of this chunk: fc[(i0 + j) 3p + a p + Z + s0 + k]
-    double *frow = t.fc + (size_t)i0 * 3 * t.p + t.Z + s0;
+    // fc rows of the structure: fc[(i0 + j) 3p + a p + Z + cols[k]]
+    double *frow = t.fc + (size_t)i0 * 3 * t.p + t.Z;
+    int col[kLinChunk];  // uniform
+#pragma unroll
+    for (int k = 0; k < kLinChunk; ++k)
+        col[k] = k < w ? cols[k] : 0;
     wave_sync();
 
     // The next site's first 128 L values and first batch of entries are
@@ -479,9 +489,6 @@ __global__ __launch_bounds__(kWave) void lin_tile_kernel(DevModel m, DevLin L, D
             take_bounds();
         }
     }
-    // compiled and exact walks read this site's L values from lane registers;
-    // the run-time walks from the LDS stage
-    constexpr bool kLaneL = !std::is_void_v<CP> || P::exact;
     for (int i = i0; i < i1; ++i) {
         const double cl0 = nl0, cl1 = nl1;
         if constexpr (!kLaneL) {
@@ -514,9 +521,9 @@ __global__ __launch_bounds__(kWave) void lin_tile_kernel(DevModel m, DevLin L, D
             const EntryRaw en = base == 0 ? first : fetch_entry(nb, pe, valid);
             Nbr<P::M> q;
             neighbor_from<P>(m, coef, ti, en, valid, q);
-            double acc[3 * kLinChunk];
+            double acc[kLinAcc];
 #pragma unroll
-            for (int r = 0; r < 3 * kLinChunk; ++r)
+            for (int r = 0; r < kLinAcc; ++r)
                 acc[r] = 0.0;
             if constexpr (!std::is_void_v<CP>) {
                 lin_chunk_cp<CP, 0, P, true>(ch, q, lch, acc, cl0, cl1);
@@ -553,7 +560,7 @@ __global__ __launch_bounds__(kWave) void lin_tile_kernel(DevModel m, DevLin L, D
                         if (k < w)
 #pragma unroll
                             for (int a = 0; a < 3; ++a)
-                                atomicAdd(row + (size_t)a * t.p + k, -acc[3 * k + a]);
+                                atomicAdd(row + (size_t)a * t.p + col[k], -acc[3 * k + a]);
                 }
             }
             // stress: -D_a r_b
@@ -567,13 +574,13 @@ __global__ __launch_bounds__(kWave) void lin_tile_kernel(DevModel m, DevLin L, D
                         st[(3 * a + bq) * kLinChunk + k] -= acc[3 * k + a] * r3[bq];
             // the centre's row: the sum of this batch's derivatives
             int vi;
-            const double v = wave_reduce_scatter<3 * kLinChunk>(acc, lane, vi);
+            const double v = wave_reduce_scatter<kLinAcc>(acc, lane, vi);
             if (vi >= 0 && vi / 3 < w) {
                 const int k = vi / 3, a = vi % 3;
                 if (lds_tile)
                     atomicAdd(tile + (size_t)(i - i0) * kRow + a * kLinChunk + k, v);
                 else
-                    atomicAdd(frow + (size_t)(i - i0) * 3 * t.p + (size_t)a * t.p + k, v);
+                    atomicAdd(frow + (size_t)(i - i0) * 3 * t.p + (size_t)a * t.p + cols[k], v);
             }
         }
         if (i + 2 < i1)
@@ -585,7 +592,8 @@ __global__ __launch_bounds__(kWave) void lin_tile_kernel(DevModel m, DevLin L, D
         wave_sync();
         for (int k = lane; k < N * 3 * w; k += kWave) {
             const int j = k / (3 * w), r = k % (3 * w), a = r / w, kk = r % w;
-            frow[(size_t)j * 3 * t.p + (size_t)a * t.p + kk] = tile[(size_t)j * kRow + a * kLinChunk + kk];
+            frow[(size_t)j * 3 * t.p + (size_t)a * t.p + cols[kk]] =
+                tile[(size_t)j * kRow + a * kLinChunk + kk];
         }
     }
 #pragma unroll
@@ -595,7 +603,7 @@ __global__ __launch_bounds__(kWave) void lin_tile_kernel(DevModel m, DevLin L, D
             if (k < w) {
                 const double v = wave_sum(st[qq * kLinChunk + k]);
                 if (lane == 0)
-                    t.sc[((size_t)c * 9 + qq) * t.p + t.Z + s0 + k] = v;
+                    t.sc[((size_t)c * 9 + qq) * t.p + t.Z + col[k]] = v;
             }
 }
 
@@ -716,8 +724,8 @@ int lin_variant(const DevModel &m, const DevLin &L)
     return v <= 2 && !L.lane_walk ? 4 : v;
 }
 
-// True when the plan equals the compiled level-16 walk (same chunks, masks
-// and L indices), so that walk computes exactly what the run-time walk would.
+// True when the plan equals the compiled level-16 walk (same chunks and
+// scalars, masks and L indices), so that walk computes exactly what the run-time walk would.
 bool lin_walk_compiled(const LinPlan &lp, int nslots)
 {
     using CP = LinPlanLevel16;
@@ -725,6 +733,9 @@ bool lin_walk_compiled(const LinPlan &lp, int nslots)
         return false;
     for (int c = 0; c <= CP::nchunks; ++c)
         if (lp.chunk_s0[c] != CP::chunk_s0[c])
+            return false;
+    for (int q = 0; q < CP::S; ++q)
+        if ((int)lp.chunk_scalar.size() != CP::S || lp.chunk_scalar[q] != CP::scalar[q])
             return false;
     for (int c = 0; c < CP::nchunks; ++c) {
         for (int s = 0; s < CP::nslots; ++s)
@@ -758,7 +769,9 @@ bool lin_configure(const DevModel &m, const DevLin &L, int n, int num_cus, size_
 size_t lin_tile_lds(const DevModel &m, const DevLin &L, int rows)
 {
     const size_t ncr = ((size_t)m.Z * m.Z * m.M * m.R + 3) & ~size_t(3);
-    const size_t stage = ((size_t)L.max_walk + 3) & ~size_t(3);
+    // the L-value stage of the run-time walks (the small and generic profiles)
+    const int v = lin_variant(m, L);
+    const size_t stage = v == 3 || v == 4 ? ((size_t)L.max_walk + 3) & ~size_t(3) : 0;
     return sizeof(double) * (ncr + stage + (size_t)rows * (3 * kLinChunk + 1));
 }
 

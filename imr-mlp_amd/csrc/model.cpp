@@ -1058,6 +1058,140 @@ bool build_plan(const Model &m, Plan &p, std::string &err)
     return true;
 }
 
+namespace {
+
+// Groups the scalar moments into the linear-fit walks' chunks: at most W
+// scalars and at most E (slot, scalar) entries each (a scalar with more
+// entries is a chunk of its own).  A chunk's walk forms grad(f Y) once per
+// slot that any of its scalars uses and the monomial shells up to the
+// highest degree among them, so scalars that share slots belong together.
+// The grouping minimises an instruction estimate of one walk,
+//   7 per slot formed + 6 per (slot, scalar) entry + 2 per monomial of the
+//   shells formed + 12 per scalar + 420 per chunk (radial functions,
+//   centre-row reduction, stress and row updates),
+// by simulated annealing (moves and swaps of scalars between chunks,
+// geometric cooling, a fixed-seed generator) from the chunks of
+// consecutive scalars.  Deterministic: the same moment structure gives the
+// same chunks on every host.  Returns the chunks, each in ascending
+// scalar order, costliest first.
+std::vector<std::vector<int>> group_scalars(const std::vector<std::vector<int>> &slots,
+                                            const std::vector<int> &slot_nu, int W, int E)
+{
+    const int S = (int)slots.size();
+    const int nslots = (int)slot_nu.size(), words = (nslots + 63) / 64;
+    std::vector<uint64_t> bits((size_t)S * words, 0);
+    std::vector<int> nnz((size_t)S), top((size_t)S, 0);
+    for (int s = 0; s < S; ++s) {
+        for (int sl : slots[s]) {
+            bits[(size_t)s * words + sl / 64] |= uint64_t(1) << (sl % 64);
+            top[s] = std::max(top[s], slot_nu[sl]);
+        }
+        nnz[s] = (int)slots[s].size();
+    }
+    auto shell_cost = [](int nu) {
+        int c = 0;
+        for (int n = 1; n <= nu; ++n)
+            c += (n + 1) * (n + 2) / 2;
+        return c;
+    };
+    std::vector<uint64_t> u((size_t)words);
+    auto cost = [&](const std::vector<int> &g) -> long {
+        if (g.empty())
+            return 0;
+        std::fill(u.begin(), u.end(), 0);
+        long ent = 0;
+        int nu = 0;
+        for (int s : g) {
+            for (int w = 0; w < words; ++w)
+                u[w] |= bits[(size_t)s * words + w];
+            ent += nnz[s];
+            nu = std::max(nu, top[s]);
+        }
+        long used = 0;
+        for (uint64_t x : u)
+            used += __builtin_popcountll(x);
+        return 7 * used + 6 * ent + 2 * shell_cost(nu) + 12 * (long)g.size() + 420;
+    };
+    auto fits = [&](const std::vector<int> &g) {
+        if ((int)g.size() > W)
+            return false;
+        long ent = 0;
+        for (int s : g)
+            ent += nnz[s];
+        return ent <= E || g.size() == 1;
+    };
+    // start: consecutive scalars, then three empty chunks to move into
+    std::vector<std::vector<int>> gs;
+    for (int s = 0; s < S; ++s) {
+        if (gs.empty() || !fits([&] {
+                auto t = gs.back();
+                t.push_back(s);
+                return t;
+            }()))
+            gs.emplace_back();
+        gs.back().push_back(s);
+    }
+    for (int k = 0; k < 3; ++k)
+        gs.emplace_back();
+    std::vector<long> c((size_t)gs.size());
+    for (size_t k = 0; k < gs.size(); ++k)
+        c[k] = cost(gs[k]);
+    uint64_t state = 0x2545F4914F6CDD1DULL;
+    auto next = [&](uint64_t n) {
+        state = state * 6364136223846793005ULL + 1442695040888963407ULL;
+        return (state >> 33) % n;
+    };
+    auto uniform = [&] {
+        state = state * 6364136223846793005ULL + 1442695040888963407ULL;
+        return (double)(state >> 11) * 0x1.0p-53;
+    };
+    const int G = (int)gs.size();
+    double T = 200.0;
+    const int iters = S > 1 ? 200000 : 0;
+    std::vector<int> na, nb;
+    for (int it = 0; it < iters; ++it, T = std::max(1.0, T * 0.99997)) {
+        const int a = (int)next(G), b = (int)next(G);
+        if (a == b || gs[a].empty())
+            continue;
+        const int i = (int)next(gs[a].size());
+        na = gs[a];
+        na.erase(na.begin() + i);
+        nb = gs[b];
+        if (next(2) == 0 || gs[b].empty()) {
+            nb.push_back(gs[a][i]);
+        } else {
+            const int j = (int)next(gs[b].size());
+            na.push_back(gs[b][j]);
+            nb.erase(nb.begin() + j);
+            nb.push_back(gs[a][i]);
+        }
+        if (!fits(na) || !fits(nb))
+            continue;
+        const long ca = cost(na), cb = cost(nb), d = ca + cb - c[a] - c[b];
+        if (d <= 0 || uniform() < std::exp(-(double)d / T)) {
+            gs[a].swap(na);
+            gs[b].swap(nb);
+            c[a] = ca;
+            c[b] = cb;
+        }
+    }
+    std::vector<std::pair<long, std::vector<int>>> out;
+    for (int k = 0; k < G; ++k)
+        if (!gs[k].empty()) {
+            std::sort(gs[k].begin(), gs[k].end());
+            out.push_back({c[k], gs[k]});
+        }
+    std::sort(out.begin(), out.end(), [](const auto &x, const auto &y) {
+        return x.first != y.first ? x.first > y.first : x.second[0] < y.second[0];
+    });
+    std::vector<std::vector<int>> res;
+    for (auto &o : out)
+        res.push_back(std::move(o.second));
+    return res;
+}
+
+}  // namespace
+
 // Linear-fit plan.  The scalar moments are polynomials in the basic moments,
 // so dm_s/dr_j = sum_b L[s][b] grad_r(f_b Y_b)(r_j) with the sparse site
 // Jacobian L[x][b] = dm_x/dm_b.  Its support follows the rules:
@@ -1170,31 +1304,42 @@ bool build_lin_plan(const Model &m, const Plan &p, LinPlan &lp, std::string &err
                   lp.fwd_comb, lp.fwd_level_comb);
     encode_tables(raw, lp.part0, lp.dummy, same, same, same, lp.steps, lp.level_step, lp.comb,
                   lp.level_comb);
-    // Chunks of consecutive scalars: at most kLinChunk scalars and at most
-    // kLinEntries (slot, scalar) entries each (a scalar with more entries
-    // makes a chunk of its own).  Per chunk and slot: a mask of the chunk's
-    // scalars whose support holds the slot's basic, and their L indices
-    // (`one` where the bit is clear); for the compile-time walks also the
-    // masks packed four per word and the L indices in walk order (slot
-    // ascending, then scalar).
-    lp.chunk_s0.assign(1, 0);
-    for (int s = 0, cnt = 0, ent = 0; s < m.S; ++s) {
-        const int e = (int)supp[m.map[s]].size();
-        if (cnt > 0 && (cnt == kLinChunk || ent + e > kLinEntries)) {
-            lp.chunk_s0.push_back(s);
-            cnt = ent = 0;
+    // Chunks of scalars (group_scalars): at most kLinChunk scalars and at
+    // most kLinEntries (slot, scalar) entries each.  Per chunk and slot: a
+    // mask of the chunk's scalars whose support holds the slot's basic, and
+    // their L indices (`one` where the bit is clear); for the compile-time
+    // walks also the masks packed four per word and the L indices in walk
+    // order (slot ascending, then scalar).
+    std::vector<int> slot_nu((size_t)p.nslots);
+    for (int s = 0; s < p.nslots; ++s) {
+        const int abc = p.slot_abc[s];
+        slot_nu[s] = (abc & 0xff) + ((abc >> 8) & 0xff) + ((abc >> 16) & 0xff);
+    }
+    std::vector<std::vector<int>> scalar_slots((size_t)m.S);
+    for (int s = 0; s < m.S; ++s)
+        for (int b : supp[m.map[s]]) {
+            if (slot_of[b] < 0)
+                return fail(err, "internal error: linear-fit support outside the slots");
+            scalar_slots[s].push_back(slot_of[b]);
         }
-        ++cnt;
-        ent += e;
+    const auto chunks = group_scalars(scalar_slots, slot_nu, kLinChunk, kLinEntries);
+    lp.chunk_s0.assign(1, 0);
+    lp.chunk_scalar.clear();
+    for (const auto &g : chunks) {
+        int ent = 0;
+        for (int s : g) {
+            lp.chunk_scalar.push_back(s);
+            ent += (int)scalar_slots[s].size();
+        }
+        lp.chunk_s0.push_back((int)lp.chunk_scalar.size());
         lp.max_chunk_entries = std::max(lp.max_chunk_entries, ent);
     }
-    lp.chunk_s0.push_back(m.S);
     lp.nchunks = (int)lp.chunk_s0.size() - 1;
     lp.slot_mask.assign((size_t)lp.nchunks * p.nslots, 0);
     lp.slot_L.assign((size_t)lp.nchunks * p.nslots * kLinChunk, lp.one);
     for (int c = 0; c < lp.nchunks; ++c)
-        for (int s = lp.chunk_s0[c]; s < lp.chunk_s0[c + 1]; ++s) {
-            const int k = s - lp.chunk_s0[c], x = m.map[s];
+        for (int q = lp.chunk_s0[c]; q < lp.chunk_s0[c + 1]; ++q) {
+            const int s = lp.chunk_scalar[q], k = q - lp.chunk_s0[c], x = m.map[s];
             for (int b : supp[x]) {
                 const int sl = slot_of[b], li = lws(x, b);
                 if (sl < 0 || li < 0)

@@ -304,7 +304,11 @@ bool build_plan(const Model &m, Plan &p, std::string &err);
 // moments, see build_lin_plan).  Work space per wave (doubles): the E/F/S
 // block [0, red0), the transpose buffer, `one` (1.0), the Jacobian values
 // [L0, L0 + nL), the step partials [part0, acc); priv = acc.
-constexpr int kLinChunk = 8;  // scalars per pass (their derivatives live in registers)
+// Scalars per pass: their derivatives live in registers, and a tile row of
+// 3 kLinChunk + 1 doubles keeps a 256-atom structure's tile (with the
+// radial coefficients) within a quarter of the 160 KB LDS, one wave per SIMD.
+constexpr int kLinChunk = 6;
+constexpr int kLinAcc = (3 * kLinChunk + 3) & ~3;  // derivative registers, a multiple of 4
 constexpr int kLinEntries = 128;   // (slot, scalar) entries per pass: two lane registers
 constexpr int kLinMaskWords = 128; // slot masks of a pass, 4 per word: two lane registers
 struct LinPlan {
@@ -314,7 +318,8 @@ struct LinPlan {
     bool lane_walk = false;  // maskw/clist valid (nslots <= 4 kLinMaskWords)
     std::vector<int> level_step, steps, level_comb, comb;  // L rules, as Plan's rule tables
     std::vector<int> fwd_level_step, fwd_steps, fwd_level_comb, fwd_comb;  // forward rules
-    std::vector<int> chunk_s0;   // [nchunks+1] first scalar of each chunk
+    std::vector<int> chunk_s0;   // [nchunks+1] first position of each chunk in chunk_scalar
+    std::vector<int> chunk_scalar;  // [S] the scalars of chunk after chunk
     std::vector<int> slot_mask;  // [nchunks][nslots] bit k: scalar k of the chunk uses the slot
     std::vector<int> slot_L;     // [nchunks][nslots][kLinChunk] L index of each bit
     std::vector<int> maskw;      // [nchunks][kLinMaskWords] slot masks, 4 per word
@@ -437,7 +442,8 @@ struct DevLin {
     const int *level_step, *level_comb;  // [nlev + 1]
     const int2 *steps;
     const int4 *comb;
-    const int *chunk_s0;    // [nchunks + 1]
+    const int *chunk_s0;    // [nchunks + 1] into chunk_scalar
+    const int *chunk_scalar;  // [S] the scalars of chunk after chunk
     const int *slot_mask;   // [nchunks][nslots]
     const int *slot_L;      // [nchunks][nslots][kLinChunk]
     const int *maskw;       // [nchunks][kLinMaskWords]
