@@ -30,6 +30,9 @@
 
 #include <type_traits>
 
+#ifndef MTPX_LIN_LDSL
+#define MTPX_LIN_LDSL 0
+#endif
 #ifndef MTPX_LIN_PART
 #define MTPX_LIN_PART 1
 #endif
@@ -43,6 +46,10 @@ namespace {
 namespace mtpx {
 
 namespace {
+
+// The compiled walk's L values from an LDS stage (broadcast reads) instead
+// of lane registers (readlane).
+constexpr bool kLinLdsL = MTPX_LIN_LDSL != 0;
 
 // Read-only model table in the constant address space: wave-uniform
 // indices compile to scalar loads (SGPRs, no VALU work).
@@ -264,12 +271,13 @@ constexpr int walk_pos(int c, int sl)
     return e;
 }
 
-// kStaged: the L values come in walk order, in two lane registers (lane l
-// holds entries l and 64 + l of the chunk's walk), read with readlane at
-// constant lanes; otherwise from the site's work space in LDS.
-template <class CP, int C, int NU, class P, bool kStaged = false>
+// The L values of the chunk's walk come in walk order: with kLds false in
+// two lane registers (lane l holds entries l and 64 + l), read with
+// readlane at constant lanes; with kLds true in an LDS stage `ls`, read as
+// broadcasts at constant offsets.
+template <class CP, int C, int NU, class P, bool kLds>
 __device__ __forceinline__ void lin_shells_cp(const Nbr<P::M> &q, const double *prev,
-                                              const double *ws, double (&acc)[kLinAcc],
+                                              const double *ls, double (&acc)[kLinAcc],
                                               double lc0 = 0.0, double lc1 = 0.0)
 {
     double cur[shell_size(NU)];
@@ -302,10 +310,10 @@ __device__ __forceinline__ void lin_shells_cp(const Nbr<P::M> &q, const double *
                         if constexpr ((mk >> k) & 1) {
                             constexpr int e = e0 + popc(mk & ((1 << k) - 1));
                             double lv;
-                            if constexpr (kStaged)
-                                lv = readlane_d(e < kWave ? lc0 : lc1, e % kWave);
+                            if constexpr (kLds)
+                                lv = ls[e];  // LDS broadcast
                             else
-                                lv = ws[CP::clist[C][e]];  // LDS broadcast
+                                lv = readlane_d(e < kWave ? lc0 : lc1, e % kWave);
                             acc[3 * k] += lv * gx;
                             acc[3 * k + 1] += lv * gy;
                             acc[3 * k + 2] += lv * gz;
@@ -316,21 +324,21 @@ __device__ __forceinline__ void lin_shells_cp(const Nbr<P::M> &q, const double *
         }
     });
     if constexpr (NU < P::NUMAX)
-        lin_shells_cp<CP, C, NU + 1, P, kStaged>(q, cur, ws, acc, lc0, lc1);
+        lin_shells_cp<CP, C, NU + 1, P, kLds>(q, cur, ls, acc, lc0, lc1);
 }
 
 // The compiled walk of chunk `ch` (a chain of uniform compares).
-template <class CP, int C, class P, bool kStaged = false>
-__device__ __forceinline__ void lin_chunk_cp(int ch, const Nbr<P::M> &q, const double *ws,
+template <class CP, int C, class P, bool kLds>
+__device__ __forceinline__ void lin_chunk_cp(int ch, const Nbr<P::M> &q, const double *ls,
                                              double (&acc)[kLinAcc], double lc0 = 0.0,
                                              double lc1 = 0.0)
 {
     if (ch == C) {
-        lin_shells_cp<CP, C, 0, P, kStaged>(q, nullptr, ws, acc, lc0, lc1);
+        lin_shells_cp<CP, C, 0, P, kLds>(q, nullptr, ls, acc, lc0, lc1);
         return;
     }
     if constexpr (C + 1 < CP::nchunks)
-        lin_chunk_cp<CP, C + 1, P, kStaged>(ch, q, ws, acc, lc0, lc1);
+        lin_chunk_cp<CP, C + 1, P, kLds>(ch, q, ls, acc, lc0, lc1);
 }
 
 // ---- tile path --------------------------------------------------------------
@@ -396,8 +404,8 @@ __global__ __launch_bounds__(kWave *kMaxWaves) void lin_jac_kernel(DevModel m, D
 // for a structure larger than a tile in the rows of fc itself), in site
 // order: one wave is the only writer of its rows, so the sums are
 // repeatable.  The structure's stress
-// components -sum_e D_e[a][s] r_e[b] are summed per lane in registers and
-// over the wave at the end.  The site's walk-order L values come in lane
+// components -sum_e D_e[a][s] r_e[b] (a <= b; the tensor is symmetric) are
+// summed per lane in registers and over the wave at the end.  The site's walk-order L values come in lane
 // registers (compiled and exact walks) or through a stage in LDS (run-time
 // walks).
 template <class P, class CP>
@@ -423,9 +431,11 @@ __global__ __launch_bounds__(kWave) void lin_tile_kernel(DevModel m, DevLin L, D
     // in different banks
     constexpr int kRow = 3 * kLinChunk + 1;
 
-    // compiled and exact walks read a site's L values from lane registers;
-    // the run-time walks from a stage in LDS
-    constexpr bool kLaneL = !std::is_void_v<CP> || P::exact;
+    // compiled and exact walks read a site's L values from lane registers
+    // (the compiled walk from an LDS stage where kLinLdsL is set); the
+    // run-time walks from the stage
+    constexpr bool kCompiled = !std::is_void_v<CP>;
+    constexpr bool kLaneL = kCompiled ? !kLinLdsL : P::exact;
     double *coef = lds;
     const int ncr = m.Z * m.Z * m.M * m.R;
     double *lch = lds + ((ncr + 3) & ~3);
@@ -435,9 +445,14 @@ __global__ __launch_bounds__(kWave) void lin_tile_kernel(DevModel m, DevLin L, D
     if (lds_tile)
         for (int k = lane; k < N * kRow; k += kWave)
             tile[k] = 0.0;
-    double st[9 * kLinChunk];
+    // The stress of a scalar, sum over sites of the site virial of a
+    // rotation-invariant function of the site's neighbour vectors, is
+    // symmetric: the upper triangle is summed (component u is (kSymA[u],
+    // kSymB[u])) and mirrored.
+    constexpr int kSymA[6] = {0, 0, 0, 1, 1, 2}, kSymB[6] = {0, 1, 2, 1, 2, 2};
+    double st[6 * kLinChunk];
 #pragma unroll
-    for (int k = 0; k < 9 * kLinChunk; ++k)
+    for (int k = 0; k < 6 * kLinChunk; ++k)
         st[k] = 0.0;
     // fc rows of the structure: fc[(i0 + j) 3p + a p + Z + cols[k]]
     double *frow = t.fc + (size_t)i0 * 3 * t.p + t.Z;
@@ -504,15 +519,6 @@ __global__ __launch_bounds__(kWave) void lin_tile_kernel(DevModel m, DevLin L, D
         }
         const EntryRaw first = nx;
         const int ti = cti, beg = cbeg, n = cend - cbeg;
-        if (i + 1 < i1) {
-            fetch_l(i + 1, nl0, nl1);
-            nx = fetch_entry(nb, nbeg + lane, lane < nend - nbeg);
-            cbeg = nbeg;
-            cend = nend;
-            cti = nti;
-            if (i + 2 < i1)
-                fetch_bounds(i + 2);
-        }
         if constexpr (!kLaneL)
             wave_sync();
         for (int base = 0; base < n; base += kWave) {
@@ -521,12 +527,24 @@ __global__ __launch_bounds__(kWave) void lin_tile_kernel(DevModel m, DevLin L, D
             const EntryRaw en = base == 0 ? first : fetch_entry(nb, pe, valid);
             Nbr<P::M> q;
             neighbor_from<P>(m, coef, ti, en, valid, q);
+            // The next site's loads are issued once this batch's entry is in
+            // registers: loads still in flight at the top of this loop would
+            // make its wait for the entry wait for them too.
+            if (base == 0 && i + 1 < i1) {
+                fetch_l(i + 1, nl0, nl1);
+                nx = fetch_entry(nb, nbeg + lane, lane < nend - nbeg);
+                cbeg = nbeg;
+                cend = nend;
+                cti = nti;
+                if (i + 2 < i1)
+                    fetch_bounds(i + 2);
+            }
             double acc[kLinAcc];
 #pragma unroll
             for (int r = 0; r < kLinAcc; ++r)
                 acc[r] = 0.0;
             if constexpr (!std::is_void_v<CP>) {
-                lin_chunk_cp<CP, 0, P, true>(ch, q, lch, acc, cl0, cl1);
+                lin_chunk_cp<CP, 0, P, kLinLdsL>(ch, q, lch, acc, cl0, cl1);
             } else {
                 LinWalk wk;
                 wk.pos = 0;
@@ -563,15 +581,13 @@ __global__ __launch_bounds__(kWave) void lin_tile_kernel(DevModel m, DevLin L, D
                                 atomicAdd(row + (size_t)a * t.p + col[k], -acc[3 * k + a]);
                 }
             }
-            // stress: -D_a r_b
+            // stress: -D_a r_b for a <= b
             const double r3[3] = {q.x, q.y, q.z};
 #pragma unroll
             for (int k = 0; k < kLinChunk; ++k)
 #pragma unroll
-                for (int a = 0; a < 3; ++a)
-#pragma unroll
-                    for (int bq = 0; bq < 3; ++bq)
-                        st[(3 * a + bq) * kLinChunk + k] -= acc[3 * k + a] * r3[bq];
+                for (int u = 0; u < 6; ++u)
+                    st[u * kLinChunk + k] -= acc[3 * k + kSymA[u]] * r3[kSymB[u]];
             // the centre's row: the sum of this batch's derivatives
             int vi;
             const double v = wave_reduce_scatter<kLinAcc>(acc, lane, vi);
@@ -597,13 +613,17 @@ __global__ __launch_bounds__(kWave) void lin_tile_kernel(DevModel m, DevLin L, D
         }
     }
 #pragma unroll
-    for (int qq = 0; qq < 9; ++qq)
+    for (int u = 0; u < 6; ++u)
 #pragma unroll
         for (int k = 0; k < kLinChunk; ++k)
             if (k < w) {
-                const double v = wave_sum(st[qq * kLinChunk + k]);
-                if (lane == 0)
-                    t.sc[((size_t)c * 9 + qq) * t.p + t.Z + col[k]] = v;
+                const double v = wave_sum(st[u * kLinChunk + k]);
+                if (lane == 0) {
+                    const int a = kSymA[u], b = kSymB[u];
+                    t.sc[((size_t)c * 9 + 3 * a + b) * t.p + t.Z + col[k]] = v;
+                    if (a != b)
+                        t.sc[((size_t)c * 9 + 3 * b + a) * t.p + t.Z + col[k]] = v;
+                }
             }
 }
 
@@ -771,7 +791,8 @@ size_t lin_tile_lds(const DevModel &m, const DevLin &L, int rows)
     const size_t ncr = ((size_t)m.Z * m.Z * m.M * m.R + 3) & ~size_t(3);
     // the L-value stage of the run-time walks (the small and generic profiles)
     const int v = lin_variant(m, L);
-    const size_t stage = v == 3 || v == 4 ? ((size_t)L.max_walk + 3) & ~size_t(3) : 0;
+    const bool staged = v == 3 || v == 4 || (v == 5 && kLinLdsL);
+    const size_t stage = staged ? ((size_t)L.max_walk + 3) & ~size_t(3) : 0;
     return sizeof(double) * (ncr + stage + (size_t)rows * (3 * kLinChunk + 1));
 }
 
