@@ -30,9 +30,6 @@
 
 #include <type_traits>
 
-#ifndef MTPX_LIN_LDSL
-#define MTPX_LIN_LDSL 0
-#endif
 #ifndef MTPX_LIN_PART
 #define MTPX_LIN_PART 1
 #endif
@@ -46,10 +43,6 @@ namespace {
 namespace mtpx {
 
 namespace {
-
-// The compiled walk's L values from an LDS stage (broadcast reads) instead
-// of lane registers (readlane).
-constexpr bool kLinLdsL = MTPX_LIN_LDSL != 0;
 
 // Read-only model table in the constant address space: wave-uniform
 // indices compile to scalar loads (SGPRs, no VALU work).
@@ -271,14 +264,12 @@ constexpr int walk_pos(int c, int sl)
     return e;
 }
 
-// The L values of the chunk's walk come in walk order: with kLds false in
-// two lane registers (lane l holds entries l and 64 + l), read with
-// readlane at constant lanes; with kLds true in an LDS stage `ls`, read as
-// broadcasts at constant offsets.
-template <class CP, int C, int NU, class P, bool kLds>
+// The L values of the chunk's walk come in walk order in two lane
+// registers (lane l holds entries l and 64 + l), read with readlane at
+// constant lanes.
+template <class CP, int C, int NU, class P>
 __device__ __forceinline__ void lin_shells_cp(const Nbr<P::M> &q, const double *prev,
-                                              const double *ls, double (&acc)[kLinAcc],
-                                              double lc0 = 0.0, double lc1 = 0.0)
+                                              double (&acc)[kLinAcc], double lc0, double lc1)
 {
     double cur[shell_size(NU)];
     if constexpr (NU == 0)
@@ -309,11 +300,7 @@ __device__ __forceinline__ void lin_shells_cp(const Nbr<P::M> &q, const double *
                         constexpr int k = decltype(K)::value;
                         if constexpr ((mk >> k) & 1) {
                             constexpr int e = e0 + popc(mk & ((1 << k) - 1));
-                            double lv;
-                            if constexpr (kLds)
-                                lv = ls[e];  // LDS broadcast
-                            else
-                                lv = readlane_d(e < kWave ? lc0 : lc1, e % kWave);
+                            const double lv = readlane_d(e < kWave ? lc0 : lc1, e % kWave);
                             acc[3 * k] += lv * gx;
                             acc[3 * k + 1] += lv * gy;
                             acc[3 * k + 2] += lv * gz;
@@ -324,21 +311,20 @@ __device__ __forceinline__ void lin_shells_cp(const Nbr<P::M> &q, const double *
         }
     });
     if constexpr (NU < P::NUMAX)
-        lin_shells_cp<CP, C, NU + 1, P, kLds>(q, cur, ls, acc, lc0, lc1);
+        lin_shells_cp<CP, C, NU + 1, P>(q, cur, acc, lc0, lc1);
 }
 
 // The compiled walk of chunk `ch` (a chain of uniform compares).
-template <class CP, int C, class P, bool kLds>
-__device__ __forceinline__ void lin_chunk_cp(int ch, const Nbr<P::M> &q, const double *ls,
-                                             double (&acc)[kLinAcc], double lc0 = 0.0,
-                                             double lc1 = 0.0)
+template <class CP, int C, class P>
+__device__ __forceinline__ void lin_chunk_cp(int ch, const Nbr<P::M> &q, double (&acc)[kLinAcc],
+                                             double lc0, double lc1)
 {
     if (ch == C) {
-        lin_shells_cp<CP, C, 0, P, kLds>(q, nullptr, ls, acc, lc0, lc1);
+        lin_shells_cp<CP, C, 0, P>(q, nullptr, acc, lc0, lc1);
         return;
     }
     if constexpr (C + 1 < CP::nchunks)
-        lin_chunk_cp<CP, C + 1, P, kLds>(ch, q, ls, acc, lc0, lc1);
+        lin_chunk_cp<CP, C + 1, P>(ch, q, acc, lc0, lc1);
 }
 
 // ---- tile path --------------------------------------------------------------
@@ -431,11 +417,9 @@ __global__ __launch_bounds__(kWave) void lin_tile_kernel(DevModel m, DevLin L, D
     // in different banks
     constexpr int kRow = 3 * kLinChunk + 1;
 
-    // compiled and exact walks read a site's L values from lane registers
-    // (the compiled walk from an LDS stage where kLinLdsL is set); the
-    // run-time walks from the stage
-    constexpr bool kCompiled = !std::is_void_v<CP>;
-    constexpr bool kLaneL = kCompiled ? !kLinLdsL : P::exact;
+    // compiled and exact walks read a site's L values from lane registers;
+    // the run-time walks from a stage in LDS
+    constexpr bool kLaneL = !std::is_void_v<CP> || P::exact;
     double *coef = lds;
     const int ncr = m.Z * m.Z * m.M * m.R;
     double *lch = lds + ((ncr + 3) & ~3);
@@ -544,7 +528,7 @@ __global__ __launch_bounds__(kWave) void lin_tile_kernel(DevModel m, DevLin L, D
             for (int r = 0; r < kLinAcc; ++r)
                 acc[r] = 0.0;
             if constexpr (!std::is_void_v<CP>) {
-                lin_chunk_cp<CP, 0, P, kLinLdsL>(ch, q, lch, acc, cl0, cl1);
+                lin_chunk_cp<CP, 0, P>(ch, q, acc, cl0, cl1);
             } else {
                 LinWalk wk;
                 wk.pos = 0;
@@ -791,8 +775,7 @@ size_t lin_tile_lds(const DevModel &m, const DevLin &L, int rows)
     const size_t ncr = ((size_t)m.Z * m.Z * m.M * m.R + 3) & ~size_t(3);
     // the L-value stage of the run-time walks (the small and generic profiles)
     const int v = lin_variant(m, L);
-    const bool staged = v == 3 || v == 4 || (v == 5 && kLinLdsL);
-    const size_t stage = staged ? ((size_t)L.max_walk + 3) & ~size_t(3) : 0;
+    const size_t stage = v == 3 || v == 4 ? ((size_t)L.max_walk + 3) & ~size_t(3) : 0;
     return sizeof(double) * (ncr + stage + (size_t)rows * (3 * kLinChunk + 1));
 }
 
