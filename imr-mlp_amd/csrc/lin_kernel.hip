@@ -456,9 +456,9 @@ __global__ __launch_bounds__(kWave) void lin_tile_kernel(DevModel m, DevLin L, D
     };
     // List bounds and species are read two sites ahead with vector loads
     // (lane-dependent addresses; lanes 0 and 1 hold begin and end) and taken
-    // into scalars one site ahead, so that the next site's entries can be
-    // fetched a whole site ahead: scalar loads would share the LDS wait
-    // counter and make every LDS wait of the walk wait for them too.
+    // into scalars at the top of the next site, so that the next site's
+    // entries can be fetched a whole site ahead: scalar loads would share
+    // the LDS wait counter and make every LDS wait wait for them too.
     int zero = 0;
     asm volatile("" : "+v"(zero));  // a lane value the compiler cannot fold
     int vb = 0, vt = 0;
@@ -483,13 +483,13 @@ __global__ __launch_bounds__(kWave) void lin_tile_kernel(DevModel m, DevLin L, D
         cti = nti;
         fetch_l(i0, nl0, nl1);
         nx = fetch_entry(nb, cbeg + lane, lane < cend - cbeg);
-        if (i0 + 1 < i1) {
+        if (i0 + 1 < i1)
             fetch_bounds(i0 + 1);
-            take_bounds();
-        }
     }
     for (int i = i0; i < i1; ++i) {
         const double cl0 = nl0, cl1 = nl1;
+        if (i + 1 < i1)
+            take_bounds();  // the next site's, loaded at the end of the last walk
         if constexpr (!kLaneL) {
             if (lane < ne)
                 lch[lane] = nl0;
@@ -520,8 +520,6 @@ __global__ __launch_bounds__(kWave) void lin_tile_kernel(DevModel m, DevLin L, D
                 cbeg = nbeg;
                 cend = nend;
                 cti = nti;
-                if (i + 2 < i1)
-                    fetch_bounds(i + 2);
             }
             double acc[kLinAcc];
 #pragma unroll
@@ -544,6 +542,12 @@ __global__ __launch_bounds__(kWave) void lin_tile_kernel(DevModel m, DevLin L, D
                 int slot = 0;
                 lin_shells<0, P>(m, q, nullptr, slot, wk, lch, acc);
             }
+            // the bounds of the site after next: loaded after the walk (a
+            // value loaded before it could be moved between registers inside
+            // the walk, which then waits for every load in flight), taken at
+            // the top of the next site
+            if (base == 0 && i + 2 < i1)
+                fetch_bounds(i + 2);
             // the neighbour's row: minus this entry's derivatives
             const int jl = valid ? en.j - i0 : -1;
             if ((unsigned)jl < (unsigned)N) {
@@ -583,8 +587,6 @@ __global__ __launch_bounds__(kWave) void lin_tile_kernel(DevModel m, DevLin L, D
                     atomicAdd(frow + (size_t)(i - i0) * 3 * t.p + (size_t)a * t.p + cols[k], v);
             }
         }
-        if (i + 2 < i1)
-            take_bounds();
         if constexpr (!kLaneL)
             wave_sync();  // the next site's values overwrite the stage
     }
