@@ -345,6 +345,16 @@ __global__ __launch_bounds__(kWave *kMaxWaves) void lin_jac_kernel(DevModel m, D
     stage_shared(m, Ls, false, tid, blockDim.x);
     for (int k = L.dummy + lane; k < L.red0; k += kWave)
         ws[k] = 0.0;
+    // the walk order's work-space indices, the same for every site: held in
+    // lane registers where they fit (entry lane + 64 k in register k)
+    constexpr int kWalkRegs = 16;
+    const bool walk_regs = L.nwalk <= kWalkRegs * kWave;
+    int widx[kWalkRegs];
+#pragma unroll
+    for (int k = 0; k < kWalkRegs; ++k) {
+        const int e = lane + kWave * k;
+        widx[k] = walk_regs && e < L.nwalk ? L.walk[e] : 0;
+    }
     __syncthreads();
 
     for (int i = g.a0 + blockIdx.x * nwaves + wave; i < g.a1; i += gridDim.x * nwaves) {
@@ -377,8 +387,15 @@ __global__ __launch_bounds__(kWave *kMaxWaves) void lin_jac_kernel(DevModel m, D
         wave_sync();
         run_rules<false, false>(L.steps, L.level_step, L.level_comb, L.comb, L.nlev, ws, lane, 0);
         double *lw = g.lw + (size_t)(i - g.a0) * L.nwalk;
-        for (int e = lane; e < L.nwalk; e += kWave)
-            lw[e] = ws[L.walk[e]];
+        if (walk_regs) {
+#pragma unroll
+            for (int k = 0; k < kWalkRegs; ++k)
+                if (lane + kWave * k < L.nwalk)
+                    lw[lane + kWave * k] = ws[widx[k]];
+        } else {
+            for (int e = lane; e < L.nwalk; e += kWave)
+                lw[e] = ws[L.walk[e]];
+        }
         wave_sync();
     }
 }
