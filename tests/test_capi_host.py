@@ -214,3 +214,33 @@ def test_compiled_linear_walk_is_current(tmp_path):
     other = subprocess.run([exe, "tests/golden/templates/shapeev-20.mtp", "LinPlanLevel16"],
                            cwd=root, check=True, capture_output=True, text=True).stdout
     assert other.split("struct", 1)[1] != out.split("struct", 1)[1]
+    for text in (out, other):
+        _check_lin_chunks(text)
+
+
+def _check_lin_chunks(text):
+    """The chunks of a generated plan partition the scalars into groups of at
+    most 6 scalars and 128 (slot, scalar) entries, and share slots: they form
+    fewer slots per site than chunks of consecutive scalars would."""
+    import re
+    S = int(re.search(r"nslots = (\d+), nchunks = (\d+), S = (\d+)", text).group(3))
+    nch = int(re.search(r"nchunks = (\d+)", text).group(1))
+    s0 = [int(v) for v in re.search(r"chunk_s0\[\d+\] = \{([^}]*)\}", text).group(1).split(",")]
+    scal = [int(v) for v in re.search(r"scalar\[\d+\] = \{([^}]*)\}", text).group(1).split(",")]
+    body = re.search(r"mask\[\d+\]\[\d+\] = \{(.*?)\};", text, re.S).group(1)
+    masks = [[int(v) for v in row.split(",")] for row in re.findall(r"\{([^{}]*)\}", body)]
+    assert sorted(scal) == list(range(S)) and len(s0) == nch + 1 and s0[-1] == S
+    slots_of = {}
+    for c in range(nch):
+        w = s0[c + 1] - s0[c]
+        assert 1 <= w <= 6
+        ent = sum(bin(v).count("1") for v in masks[c])
+        assert ent <= 128 or w == 1
+        assert all(v >> w == 0 for v in masks[c])
+        for k in range(w):
+            slots_of[scal[s0[c] + k]] = {sl for sl, v in enumerate(masks[c]) if v >> k & 1}
+    formed = sum(len(set().union(*(slots_of[scal[q]] for q in range(s0[c], s0[c + 1]))))
+                 for c in range(nch))
+    consecutive = sum(len(set().union(*(slots_of[q] for q in range(a, min(a + 6, S)))))
+                      for a in range(0, S, 6))
+    assert formed < consecutive
