@@ -298,6 +298,36 @@ def test_level10_and_runtime_profile_models(ctx):
         assert rel_err(sc[0], so) < 1e-10
 
 
+def test_components_with_repeated_atoms(ctx):
+    """Cells narrower than twice the cutoff put several images of one atom in
+    a list, so lanes of one batch add to the same tile row.  Small and large
+    cells in one batch, the level-16 model (the compiled walk), against the
+    oracle."""
+    text, _ = S.training_models(4)
+    m = O.Model(text)
+    rng = S.rng_for(91)
+    structs = []
+    for reps, a in [((2, 2, 2), 3.56), ((1, 1, 2), 3.56), ((3, 3, 3), 3.6), ((1, 1, 1), 3.5)]:
+        s = S.displace(S.lattice("fcc", reps, a), rng, 0.1)
+        s.types = (S.uniform(rng, s.n) * 2).astype(np.int32)
+        s.pos = O.wrap(s.cell, s.pbc, s.pos)
+        structs.append(s)
+    ctx.load_model_text(text)
+    off = ctx.set_structures(structs, 5.0)
+    ec, fc, sc = ctx.efs_components()
+    repeats = 0
+    for c, s in enumerate(structs):
+        nb = O.Neighbors.build(s.cell, s.pbc, s.pos, s.types, m.cutoff)
+        for i in range(nb.n):
+            row = nb.idx[nb.offsets[i]:nb.offsets[i + 1]]
+            repeats += len(row) - len(set(row.tolist()))
+        eo, fo, so = O.efs_components(m, nb)
+        assert rel_err(ec[c], eo) < 1e-10
+        assert rel_err(fc[off[c]:off[c + 1]], fo) < 1e-10
+        assert rel_err(sc[c], so) < 1e-10
+    assert repeats > 0  # the small cells do repeat atoms within a list
+
+
 def test_empty_batch_linear_system(ctx):
     text, _ = S.training_models(4)
     ctx.load_model_text(text)
