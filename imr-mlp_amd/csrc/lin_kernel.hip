@@ -670,6 +670,21 @@ __global__ __launch_bounds__(256) void lin_reduce_kernel(int S, int Z, int p, co
     }
 }
 
+// Clears what the linear-fit kernels leave unwritten: the species columns
+// of the force rows and the stress rows (whole).
+__global__ __launch_bounds__(256) void lin_clear_kernel(double *comp, int64_t frows, int64_t srows,
+                                                        int p, int Z)
+{
+    const int64_t nf = frows * Z, total = nf + srows * p;
+    for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < total;
+         t += (int64_t)gridDim.x * blockDim.x) {
+        if (t < nf)
+            comp[(t / Z) * p + t % Z] = 0.0;
+        else
+            comp[frows * p + (t - nf)] = 0.0;
+    }
+}
+
 // AddLinearFast rows: A[r][q] = sw_r comp[src_r + q], y[r] = y_r.
 __global__ __launch_bounds__(256) void rows_kernel(const double *comp, const int64_t *src,
                                                    const double *sw, const double *yw, int64_t R,
@@ -828,6 +843,17 @@ hipError_t launch_lin_tile(const DevModel &m, const DevLin &L, const DevNeighbor
     case 3: launch_tile_variant<ProfSmall>(m, L, nb, t, lds, s); break;
     default: launch_tile_variant<ProfGeneric>(m, L, nb, t, lds, s); break;
     }
+    return hipGetLastError();
+}
+
+hipError_t launch_lin_clear(double *comp, int64_t frows, int64_t srows, int p, int Z,
+                            hipStream_t s)
+{
+    const int64_t total = frows * Z + srows * p;
+    if (total > 0)
+        hipLaunchKernelGGL(lin_clear_kernel,
+                           dim3((unsigned)std::min<int64_t>((total + 255) / 256, 4096)), dim3(256),
+                           0, s, comp, frows, srows, p, Z);
     return hipGetLastError();
 }
 

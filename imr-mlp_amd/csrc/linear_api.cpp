@@ -62,10 +62,11 @@ int run_lin(mtpx_context *ctx)
     hipStream_t s = ctx->stream;
     HIP_TRY(ctx->comp.ensure(sizeof(double) * std::max<size_t>(cl.total, 1)),
             "allocate components");
-    if (cl.total)
-        HIP_TRY(launch_fill_zero(ctx->comp.as<double>(), cl.total, s), "clear components");
-    if (ctx->n == 0)
+    if (ctx->n == 0) {
+        if (cl.total)
+            HIP_TRY(launch_fill_zero(ctx->comp.as<double>(), cl.total, s), "clear components");
         return MTPX_OK;
+    }
     const DevModel &m = ctx->dm;
     const DevLin &L = ctx->dl;
     const size_t per_atom = sizeof(double) * ((size_t)L.nwalk + m.S);
@@ -133,6 +134,19 @@ int run_lin(mtpx_context *ctx)
         cls_off[gi][ncls] = (int)lists.size();
     }
     HIP_TRY(upload(ctx->lin_tiles, lists, s), "upload structure lists");
+    // The kernels write every component but the species columns of the
+    // force and stress rows (and the stress rows of empty structures), so
+    // only those are cleared, unless a structure adds into its force rows
+    // directly (the class past the largest LDS tile): then all are.
+    bool direct = false;
+    for (size_t gi = 0; gi < groups.size(); ++gi)
+        direct = direct || cls_off[gi][ncls] > cls_off[gi][ncls - 1];
+    if (direct)
+        HIP_TRY(launch_fill_zero(ctx->comp.as<double>(), cl.total, s), "clear components");
+    else
+        HIP_TRY(launch_lin_clear(ctx->comp.as<double>(), (int64_t)ctx->n * 3,
+                                 (int64_t)ctx->nconf * 9, cl.p, m.Z, s),
+                "clear components");
 
     double *comp = ctx->comp.as<double>();
     const DevNeighbors nb = dev_neighbors(ctx);

@@ -481,6 +481,11 @@ hipError_t launch_lin_jac(const DevModel &m, const DevLin &L, const DevNeighbors
                           const LinGroup &g, const EfsLaunch &cfg, hipStream_t s);
 hipError_t launch_lin_tile(const DevModel &m, const DevLin &L, const DevNeighbors &nb,
                            const LinTile &t, hipStream_t s);
+// Zeroes the species columns [0, Z) of the first frows rows (the force
+// rows) of comp (rows of p doubles) and the next srows rows (the stress
+// rows) whole.
+hipError_t launch_lin_clear(double *comp, int64_t frows, int64_t srows, int p, int Z,
+                            hipStream_t s);
 hipError_t launch_lin_reduce(const DevModel &m, const int *soff, const int *center_type,
                              const LinGroup &g, double *ec, hipStream_t s);
 hipError_t launch_lin_rows(const double *comp, const int64_t *src, const double *sw,
