@@ -522,7 +522,9 @@ __global__ __launch_bounds__(kWave) void lin_tile_kernel(DevModel m, DevLin L, D
         const int ti = cti, beg = cbeg, n = cend - cbeg;
         if constexpr (!kLaneL)
             wave_sync();
-        for (int base = 0; base < n; base += kWave) {
+        // at least one pass, for the next site's loads below, also for a
+        // site without neighbours (its pass adds zeros)
+        for (int base = 0; base < max(n, 1); base += kWave) {
             const bool valid = lane < n - base;
             const int64_t pe = beg + base + lane;
             const EntryRaw en = base == 0 ? first : fetch_entry(nb, pe, valid);

@@ -328,6 +328,39 @@ def test_components_with_repeated_atoms(ctx):
     assert repeats > 0  # the small cells do repeat atoms within a list
 
 
+def test_components_with_isolated_atoms(ctx):
+    """Atoms with empty neighbour lists in the middle of a structure (a slab
+    with atoms out in its vacuum): the sites after them keep their own
+    entries.  Level-16 model (the compiled walk), against the oracle."""
+    text, _ = S.training_models(4)
+    m = O.Model(text)
+    rng = S.rng_for(93)
+    slab = S.displace(S.lattice("fcc", (2, 2, 2), 3.56), rng, 0.05)
+    cell = slab.cell.copy()
+    cell[2, 2] = 30.0
+    far = np.array([[1.0, 2.0, 15.0], [3.0, 1.0, 22.5]])
+    pos = np.concatenate([slab.pos[:10], far[:1], slab.pos[10:21], far[1:], slab.pos[21:]])
+    s = S.Structure(cell, pos, (S.uniform(rng, len(pos)) * 2).astype(np.int32),
+                    np.ones(3, np.int32))
+    s.pos = O.wrap(s.cell, s.pbc, s.pos)
+    big = S.displace(S.lattice("fcc", (3, 3, 3), 3.6), rng, 0.1)
+    big.types = (S.uniform(rng, big.n) * 2).astype(np.int32)
+    big.pos = O.wrap(big.cell, big.pbc, big.pos)
+    structs = [s, big]
+    ctx.load_model_text(text)
+    off = ctx.set_structures(structs, 5.0)
+    ec, fc, sc = ctx.efs_components()
+    empty = 0
+    for c, st in enumerate(structs):
+        nb = O.Neighbors.build(st.cell, st.pbc, st.pos, st.types, m.cutoff)
+        empty += int(np.sum(np.diff(nb.offsets) == 0))
+        eo, fo, so = O.efs_components(m, nb)
+        assert rel_err(ec[c], eo) < 1e-10
+        assert rel_err(fc[off[c]:off[c + 1]], fo) < 1e-10
+        assert rel_err(sc[c], so) < 1e-10
+    assert empty == 2
+
+
 def test_empty_batch_linear_system(ctx):
     text, _ = S.training_models(4)
     ctx.load_model_text(text)
