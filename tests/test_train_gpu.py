@@ -132,6 +132,48 @@ def test_loss_grad_matches_oracle_lvl20_liquid(ctx, lvl20_set):
         assert np.abs(blk).max() > 0
 
 
+def test_isolated_atoms_in_a_batch(ctx):
+    """A slab with two atoms out in its vacuum (empty neighbour lists in the
+    middle of a structure) beside a crystal: E/F/S and the loss gradient
+    against the oracle."""
+    ref_text, start_text = S.training_models(4)
+    mref = O.Model(ref_text)
+    rng = S.rng_for(95)
+    slab = S.displace(S.lattice("fcc", (2, 2, 2), 3.56), rng, 0.05)
+    cell = slab.cell.copy()
+    cell[2, 2] = 30.0
+    far = np.array([[1.0, 2.0, 15.0], [3.0, 1.0, 22.5]])
+    pos = np.concatenate([slab.pos[:10], far[:1], slab.pos[10:21], far[1:], slab.pos[21:]])
+    s = S.Structure(cell, pos, (S.uniform(rng, len(pos)) * 2).astype(np.int32),
+                    np.ones(3, np.int32))
+    big = S.displace(S.lattice("fcc", (3, 3, 3), 3.6), rng, 0.1)
+    big.types = (S.uniform(rng, big.n) * 2).astype(np.int32)
+    structs, nbs, labels = [], [], []
+    for st in (s, big):
+        st.pos = O.wrap(st.cell, st.pbc, st.pos)
+        nb = O.Neighbors.build(st.cell, st.pbc, st.pos, st.types, 5.0)
+        E, F, St, _ = O.efs(mref, nb)
+        e, f, sv = S.noisy_labels(rng, st.n, E, F, St)
+        structs.append(st)
+        nbs.append(nb)
+        labels.append(O.Labels(st.n, energy=e, forces=f, stress=sv))
+    assert sum(int(np.sum(np.diff(nb.offsets) == 0)) for nb in nbs) == 2
+    settings = SETTINGS["default"]
+    off = _upload(ctx, start_text, 5.0, structs, labels, settings)
+    m = O.Model(start_text)
+    E, F, St, se = ctx.compute_batch()
+    for c, nb in enumerate(nbs):
+        Eo, Fo, So, seo = O.efs(m, nb)
+        assert rel_err(E[c], Eo) < 1e-10
+        assert rel_err(F[off[c]:off[c + 1]], Fo) < 1e-10
+        assert rel_err(St[c], So) < 1e-10
+    f_o, g_o = O.loss_grad_batch(m, nbs, labels, settings, penalty_weight=1e-3, reg_l2=1e-4,
+                                 threads=8)
+    f, g, _ = ctx.loss_grad(penalty_weight=1e-3, reg_l2=1e-4)
+    assert rel_err(f, f_o) < 1e-9
+    assert rel_err(g, g_o) < 1e-9
+
+
 def test_gradient_of_explicit_adjoints(ctx, lvl16_set):
     """AccumulateEFSCombinationGard with arbitrary adjoints, summed over
     structures, accumulating into a given vector."""
