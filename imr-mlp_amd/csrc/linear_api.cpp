@@ -102,9 +102,17 @@ int run_lin(mtpx_context *ctx)
     // structure through its output rows
     if (const char *e = getenv("MTPX_LIN_TILE_ROWS"))
         max_rows = std::min(max_rows, std::max(0, atoi(e)));
+    // The tile kernel runs one wave per SIMD (its registers allow no more),
+    // so every structure whose tile fits a quarter of the LDS shares the
+    // first class: one launch, largest structures first, the small ones
+    // filling its tail.
     std::vector<int> caps;
-    for (int c : {64, 128, 192, 256, 384, 512, 768})
-        if (c < max_rows)
+    const size_t quarter_bytes = ctx->lds_limit / 4;
+    const int quarter = quarter_bytes > base ? (int)((quarter_bytes - base) / row_bytes) : 0;
+    if (quarter > 0 && quarter < max_rows)
+        caps.push_back(quarter);
+    for (int c : {384, 512, 768})
+        if (c > quarter && c < max_rows)
             caps.push_back(c);
     if (max_rows > 0)
         caps.push_back(max_rows);
