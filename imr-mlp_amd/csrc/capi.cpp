@@ -512,26 +512,33 @@ int run_efs(mtpx_context *ctx, bool deterministic, bool site_virial, bool energy
     DevNeighbors nb = dev_neighbors(ctx);
     if (!deterministic && !energy_only && n > 0)
         HIP_TRY(launch_fill_zero(out.forces, 3 * (size_t)n, s), "clear forces");
-    HIP_TRY(hipEventRecord(ctx->ev[0], s), "record event");
+    const bool timed = ctx->timings_on;
+    if (timed)
+        HIP_TRY(hipEventRecord(ctx->ev[0], s), "record event");
     if (n > 0)
         HIP_TRY(launch_efs(ctx->dm, nb, out, cfg,
                            (deterministic ? kEfsDeterministic : 0) |
                                (energy_only ? kEfsEnergyOnly : 0) | (mirror ? kEfsOwnForce : 0),
                            s),
                 "launch efs kernel");
-    HIP_TRY(hipEventRecord(ctx->ev[1], s), "record event");
+    if (timed)
+        HIP_TRY(hipEventRecord(ctx->ev[1], s), "record event");
     if (n > 0)
         HIP_TRY(launch_efs_finish(nb, out, cfg.rows, deterministic, ctx->rev_offsets.as<int>(),
                                   ctx->rev_pairs.as<int>(), ctx->out10.as<double>(), s),
                 "launch efs reductions");
     else
         HIP_TRY(hipMemsetAsync(ctx->out10.p, 0, sizeof(double) * 10, s), "clear outputs");
-    HIP_TRY(hipEventRecord(ctx->ev[2], s), "record event");
-    HIP_TRY(hipEventSynchronize(ctx->ev[2]), "efs");
     float t01 = 0, t12 = 0, t02 = 0;
-    (void)hipEventElapsedTime(&t01, ctx->ev[0], ctx->ev[1]);
-    (void)hipEventElapsedTime(&t12, ctx->ev[1], ctx->ev[2]);
-    (void)hipEventElapsedTime(&t02, ctx->ev[0], ctx->ev[2]);
+    if (timed) {
+        HIP_TRY(hipEventRecord(ctx->ev[2], s), "record event");
+        HIP_TRY(hipEventSynchronize(ctx->ev[2]), "efs");
+        (void)hipEventElapsedTime(&t01, ctx->ev[0], ctx->ev[1]);
+        (void)hipEventElapsedTime(&t12, ctx->ev[1], ctx->ev[2]);
+        (void)hipEventElapsedTime(&t02, ctx->ev[0], ctx->ev[2]);
+    } else {
+        HIP_TRY(hipStreamSynchronize(s), "efs");
+    }
     ctx->timings[0] = t02;
     ctx->timings[1] = t01;
     ctx->timings[2] = t12;
@@ -1181,6 +1188,14 @@ int mtpx_last_timings(const mtpx_context *ctx, double out_ms[4])
     if (!ctx || !out_ms)
         return MTPX_E_INVALID;
     std::memcpy(out_ms, ctx->timings, sizeof ctx->timings);
+    return MTPX_OK;
+}
+
+int mtpx_set_timings(mtpx_context *ctx, int enabled)
+{
+    if (!ctx)
+        return MTPX_E_INVALID;
+    ctx->timings_on = enabled != 0;
     return MTPX_OK;
 }
 

@@ -91,6 +91,7 @@ struct mtpx_context {
 
     hipEvent_t ev[3] = {nullptr, nullptr, nullptr};
     double timings[4] = {0, 0, 0, 0};
+    bool timings_on = true;  // mtpx_set_timings
 
     // PotMTP::add_efs: E/F/S outputs are added onto the caller's arrays
     bool add_efs = false;

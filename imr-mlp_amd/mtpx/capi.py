@@ -76,6 +76,7 @@ def lib():
         L.mtpx_efs_device.argtypes = [C.c_void_p, C.c_int]
         L.mtpx_energy.argtypes = [C.c_void_p, _dp, _dp]
         L.mtpx_last_timings.argtypes = [C.c_void_p, _dp]
+        L.mtpx_set_timings.argtypes = [C.c_void_p, C.c_int]
         L.mtpx_set_structures.argtypes = [C.c_void_p, C.c_int, _ip, _dp, _ip, _dp, _ip,
                                           C.c_double]
         L.mtpx_structure_count.argtypes = [C.c_void_p, _ip]
@@ -626,6 +627,9 @@ class Context:
         t = np.zeros(4)
         self._check(lib().mtpx_last_timings(self.h, _d(t)), "last_timings")
         return t
+
+    def set_timings(self, enabled: bool):
+        self._check(lib().mtpx_set_timings(self.h, int(bool(enabled))), "set_timings")
 
     # ---- training batches ----
     def set_structures(self, structures, cutoff):

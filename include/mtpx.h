@@ -318,6 +318,11 @@ int mtpx_efs_device(mtpx_context *ctx, int deterministic);
  * with HIP events on the library's stream, in milliseconds:
  * {E/F/S kernel + reductions, E/F/S kernel alone, reductions, 0}. */
 int mtpx_last_timings(const mtpx_context *ctx, double out_ms[4]);
+/* No counterpart in the reference (its evaluations have no device timers):
+ * enabled != 0 (the default) records those HIP events on every E/F/S call;
+ * 0 skips them (about 7 us per call on a 32,000-atom cell: three event
+ * records and their read-back), and mtpx_last_timings then reports zeros. */
+int mtpx_set_timings(mtpx_context *ctx, int enabled);
 
 /* No counterpart in the reference: an allocation-free mtpx_efs for callers
  * that cannot allocate device memory (serving loops, harnesses that

@@ -76,6 +76,28 @@ def test_deterministic_mode_is_bitwise_repeatable(ctx):
         assert np.array_equal(np.asarray(x).view(np.uint64), np.asarray(y).view(np.uint64))
 
 
+def test_timings_switch(ctx):
+    """mtpx_set_timings: with the HIP events off a call reports zero timings
+    and the same results, bit for bit; back on, the kernel time is positive."""
+    model_text, s = S.scaled_inference(2, (3, 3, 3))
+    pos = O.wrap(s.cell, s.pbc, s.pos)
+    ctx.load_model_text(model_text)
+    ctx.build_neighbors(s.cell, s.pbc, pos, s.types, 5.0)
+    ctx.efs_device(False)
+    assert ctx.last_timings()[1] > 0
+    on = ctx.efs()
+    ctx.set_timings(False)
+    ctx.efs_device(False)
+    assert not ctx.last_timings().any()
+    off = ctx.efs()
+    assert not ctx.last_timings().any()
+    for x, y in zip(on, off):
+        assert np.array_equal(np.asarray(x).view(np.uint64), np.asarray(y).view(np.uint64))
+    ctx.set_timings(True)
+    ctx.efs_device(False)
+    assert ctx.last_timings()[1] > 0
+
+
 def test_isolated_atom_energy_is_species_coefficient(ctx):
     model_text, _ = S.scaled_inference(2, (2, 2, 2))
     ctx.load_model_text(model_text)
