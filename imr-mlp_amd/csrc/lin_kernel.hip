@@ -406,9 +406,9 @@ __global__ __launch_bounds__(kWave *kMaxWaves) void lin_jac_kernel(DevModel m, D
 // accumulated over the structure's sites in the wave's own tile (in LDS, or
 // for a structure larger than a tile in the rows of fc itself), in site
 // order: one wave is the only writer of its rows, so the sums are
-// repeatable.  The structure's stress
-// components -sum_e D_e[a][s] r_e[b] (a <= b; the tensor is symmetric) are
-// summed per lane in registers and over the wave at the end.  The site's walk-order L values come in lane
+// repeatable.  The structure's stress components -sum_e D_e[a][s] r_e[b]
+// (a <= b; the tensor is symmetric) are summed per lane in registers and
+// over the wave at the end.  The site's walk-order L values come in lane
 // registers (compiled and exact walks) or through a stage in LDS (run-time
 // walks).
 template <class P, class CP>
