@@ -326,6 +326,10 @@ def test_components_with_repeated_atoms(ctx):
         assert rel_err(fc[off[c]:off[c + 1]], fo) < 1e-10
         assert rel_err(sc[c], so) < 1e-10
     assert repeats > 0  # the small cells do repeat atoms within a list
+    # lanes adding to one row in one instruction are applied in a fixed order
+    again = ctx.efs_components()
+    for x, y in zip((ec, fc, sc), again):
+        assert np.array_equal(x.view(np.uint64), y.view(np.uint64))
 
 
 def test_components_with_isolated_atoms(ctx):
