@@ -134,8 +134,8 @@ void fill_model_sizes(const Model &M, const Plan &P, DevModel &dm)
     dm.rb_general = M.general_basis() ? 1 : 0;
     dm.rb_table = nullptr;
     std::memcpy(dm.slot_base, P.slot_base, sizeof dm.slot_base);
-    dm.fwd_nsteps = P.fwd_level_step.back();
-    dm.bwd_nsteps = P.bwd_level_step.back();
+    dm.fwd_nsteps = (int)(P.fwd_steps.size() / (2 * kWave));
+    dm.bwd_nsteps = (int)(P.bwd_steps.size() / (2 * kWave));
 }
 
 int install_model(mtpx_context *ctx, Model &&m)

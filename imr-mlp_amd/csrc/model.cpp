@@ -125,10 +125,11 @@ struct RawTables {
 
 // One dependency level: tasks longer than a cap are split into pieces
 // ending in partial sums, the pieces are spread over the 64 lanes by
-// longest-processing-time, and the level is padded to a multiple of 4 steps.
-// The cap is the one, from the fair share (entries / 64) up to the longest
-// task, that gives the fewest steps and then the fewest partial sums: a
-// split that does not shorten the padded level only adds combine work.
+// longest-processing-time, and the level takes as many steps as its
+// longest lane.  The cap is the one, from the fair share (entries / 64, at
+// least kMinPiece) up to the longest task, that gives the fewest steps and
+// then the fewest partial sums: a split that does not shorten the level
+// only adds combine work.
 void emit_level(std::vector<Task> &tasks, RawTables &raw)
 {
     size_t total = 0, longest = 0;
@@ -175,10 +176,10 @@ void emit_level(std::vector<Task> &tasks, RawTables &raw)
             L.lane[q].insert(L.lane[q].end(), L.pieces[t].begin(), L.pieces[t].end());
             load[q] += L.pieces[t].size();
         }
-        L.nst = (*std::max_element(load.begin(), load.end()) + 3) & ~size_t(3);
+        L.nst = *std::max_element(load.begin(), load.end());
         return L;
     };
-    const size_t cap0 = std::max<size_t>(4, (total + kWave - 1) / kWave);
+    const size_t cap0 = std::max<size_t>(kMinPiece, (total + kWave - 1) / kWave);
     Layout best = layout(cap0);
     for (size_t cap = cap0 + 1; cap <= longest; ++cap) {
         Layout L = layout(cap);
@@ -201,17 +202,19 @@ void emit_level(std::vector<Task> &tasks, RawTables &raw)
 // Encodes raw entries into int2 work-space steps: x = l | r << 16,
 // y = w | first << 16 | last << 17 | c << 18.  map_l / map_r / map_w
 // translate raw operands and targets to work-space indices; partial p goes
-// to part0 + p and padding reads `dummy` and writes nothing.
+// to part0 + p and padding reads `dummy` and writes nothing.  kRulePad
+// padding steps follow the last level.
 template <class ML, class MR, class MW>
 void encode_tables(const RawTables &raw, int part0, int dummy, ML map_l, MR map_r, MW map_w,
                    std::vector<int> &steps, std::vector<int> &level_step, std::vector<int> &comb,
                    std::vector<int> &level_comb)
 {
     auto target = [&](int w) { return w <= -2 ? part0 + (-w - 2) : map_w(w); };
-    steps.assign(raw.steps.size() * 2, 0);
-    const size_t nst = raw.steps.size() / kWave;
-    for (size_t i = 0; i < raw.steps.size(); ++i) {
-        const Ent &e = raw.steps[i];
+    const size_t nraw = raw.steps.size();
+    steps.assign((nraw + (size_t)kRulePad * kWave) * 2, 0);
+    const size_t nst = nraw / kWave;
+    for (size_t i = 0; i < nraw + (size_t)kRulePad * kWave; ++i) {
+        const Ent e = i < nraw ? raw.steps[i] : Ent{-1, -1, 0, -1, 1};
         int l, r, w, last = 0;
         if (e[0] < 0) {
             l = r = w = dummy;

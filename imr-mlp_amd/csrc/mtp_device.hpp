@@ -720,7 +720,9 @@ __device__ __forceinline__ void bwd_shells(const DevModel &m, const double *As, 
 // level at a time.  Steps are taken in groups of four: the entries of the
 // next group are loaded while the current one runs, and every operand of a
 // group is read before any of its results is written (a level never reads
-// what it writes).  A task's sum starts from zero and is stored on the
+// what it writes).  A level's last group holds its last one to four steps;
+// the entries it loads past the level (the next level's, or the padding
+// after the last level) are read but not applied.  A task's sum starts from zero and is stored on the
 // task's last entry: added to its target (kInit: adjoints, which start from
 // their seeds) or written over it (outputs and partial sums, which start at
 // zero).  No task reads or writes another task's target within a level.
@@ -730,6 +732,43 @@ __device__ __forceinline__ void bwd_shells(const DevModel &m, const double *As, 
 // Forward entries then propagate tangents (Q_o += c (Q_l m_r + m_l Q_r));
 // reverse entries, whose l is an adjoint and r a moment, propagate the
 // adjoint of the tangent computation (G_x += c (G_o m_r + A_o Q_r)).
+// One group of up to four steps of a level (cnt of them applied).
+template <bool kDual, bool kInit>
+__device__ __forceinline__ void rule_group(const int2 (&e)[4], int cnt, double *ws, double *wd,
+                                           double &acc, double &acd)
+{
+    double ml[4], mr[4];
+    double dl[4], dr[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const int l = e[k].x & 0xffff, r = (unsigned)e[k].x >> 16;
+        ml[k] = ws[l];
+        mr[k] = ws[r];
+        if constexpr (kDual) {
+            dl[k] = wd[l];
+            dr[k] = wd[r];
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        if (k >= cnt)
+            break;
+        const double c = (double)(e[k].y >> 18);
+        acc = fma(c * ml[k], mr[k], acc);
+        if constexpr (kDual)
+            acd = fma(c * ml[k], dr[k], fma(c * dl[k], mr[k], acd));
+        if (e[k].y & 0x20000) {
+            const int w = e[k].y & 0xffff;
+            ws[w] = kInit ? ws[w] + acc : acc;
+            acc = 0.0;
+            if constexpr (kDual) {
+                wd[w] = kInit ? wd[w] + acd : acd;
+                acd = 0.0;
+            }
+        }
+    }
+}
+
 template <bool kDual, bool kInit>
 __device__ __forceinline__ void run_rules(const int2 *tab, const int *level_step,
                                           const int *level_comb, const int4 *comb, int nlev,
@@ -742,47 +781,16 @@ __device__ __forceinline__ void run_rules(const int2 *tab, const int *level_step
         if (s1 > s0) {
             const int2 *t = tab + (size_t)s0 * kWave + lane;
             int2 e[4] = {t[0], t[kWave], t[2 * kWave], t[3 * kWave]};
-            for (int st = s0; st < s1; st += 4) {
-                int2 nx[4] = {e[0], e[1], e[2], e[3]};
-                if (st + 4 < s1) {
-                    const int2 *u = t + (size_t)(st + 4 - s0) * kWave;
-                    nx[0] = u[0];
-                    nx[1] = u[kWave];
-                    nx[2] = u[2 * kWave];
-                    nx[3] = u[3 * kWave];
-                }
-                double ml[4], mr[4];
-                double dl[4], dr[4];
-#pragma unroll
-                for (int k = 0; k < 4; ++k) {
-                    const int l = e[k].x & 0xffff, r = (unsigned)e[k].x >> 16;
-                    ml[k] = ws[l];
-                    mr[k] = ws[r];
-                    if constexpr (kDual) {
-                        dl[k] = wd[l];
-                        dr[k] = wd[r];
-                    }
-                }
-#pragma unroll
-                for (int k = 0; k < 4; ++k) {
-                    const double c = (double)(e[k].y >> 18);
-                    acc = fma(c * ml[k], mr[k], acc);
-                    if constexpr (kDual)
-                        acd = fma(c * ml[k], dr[k], fma(c * dl[k], mr[k], acd));
-                    if (e[k].y & 0x20000) {
-                        const int w = e[k].y & 0xffff;
-                        ws[w] = kInit ? ws[w] + acc : acc;
-                        acc = 0.0;
-                        if constexpr (kDual) {
-                            wd[w] = kInit ? wd[w] + acd : acd;
-                            acd = 0.0;
-                        }
-                    }
-                }
+            int st = s0;
+            for (; st + 4 < s1; st += 4) {
+                const int2 *u = t + (size_t)(st + 4 - s0) * kWave;
+                const int2 nx[4] = {u[0], u[kWave], u[2 * kWave], u[3 * kWave]};
+                rule_group<kDual, kInit>(e, 4, ws, wd, acc, acd);
 #pragma unroll
                 for (int k = 0; k < 4; ++k)
                     e[k] = nx[k];
             }
+            rule_group<kDual, kInit>(e, s1 - st, ws, wd, acc, acd);
         }
         const int c0 = level_comb[L], c1 = level_comb[L + 1];
         if (c1 > c0) {

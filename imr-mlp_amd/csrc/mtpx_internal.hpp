@@ -18,6 +18,12 @@ constexpr int kMaxR = 16;       // radial basis size
 constexpr int kWave = 64;       // CDNA wavefront
 constexpr int kChunk = 16;      // slots per LDS reduction chunk
 constexpr int kRedStride = 66;  // row stride of the reduction buffer (16-byte rows, no bank conflicts)
+// Product-rule step tables: the shortest piece a task is split into, and
+// the padding steps after the last level (the kernels read the steps in
+// groups of four, so a group that starts in a level's last steps reads at
+// most three steps past it).
+constexpr int kMinPiece = 2;
+constexpr int kRulePad = 3;
 
 // Growable device allocation owned by a context.
 struct DBuf {
@@ -277,7 +283,8 @@ struct Plan {
     // first slot of each (nu, mu) block, -1 where absent: [nu * kMaxMu + mu]
     int slot_base[(kMaxNu + 1) * kMaxMu];
     // Lane-major step tables, one per direction.  Level L owns steps
-    // [level_step[L], level_step[L+1]) (a multiple of 4); step s of lane q is
+    // [level_step[L], level_step[L+1]) and kRulePad padding steps follow
+    // the last level; step s of lane q is
     // entry s * 64 + q, an int2 of work-space indices:
     //   x = l | r << 16,  y = w | first << 16 | last << 17 | c << 18  (c signed)
     //   acc += c * ws[l] * ws[r];  if (last) { ws[w] = init + acc; acc = 0; }
@@ -373,7 +380,7 @@ struct DevModel {
     const DevHead *hd;
     int nradial, ncoef;
     int slot_base[(kMaxNu + 1) * kMaxMu];
-    int fwd_nsteps, bwd_nsteps;                 // steps per lane, all levels
+    int fwd_nsteps, bwd_nsteps;  // steps per lane, all levels and the padding
     const int *fwd_level_step;  // [nfwd+1]
     const int2 *fwd_steps;
     const int *fwd_level_comb;  // [nfwd+1]
