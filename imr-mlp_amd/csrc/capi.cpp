@@ -116,7 +116,6 @@ void fill_model_sizes(const Model &M, const Plan &P, DevModel &dm)
     dm.part0 = P.part0;
     dm.red0 = P.red0;
     dm.priv_doubles = P.priv_doubles;
-    dm.tr_delta = P.tr_delta;
     dm.efs_red = P.efs_red;
     dm.efs_stage = P.efs_stage;
     dm.efs_acc = P.efs_acc;

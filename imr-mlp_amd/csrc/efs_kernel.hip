@@ -97,7 +97,7 @@ __global__ __launch_bounds__(kWave *kMaxWaves) void efs_kernel(DevModel m, DevNe
             ws[k] = 0.0;
         wave_sync();
 
-        run_rules<false, false>(fwd_tab, m.fwd_level_step, m.fwd_level_comb, m.fwd_comb, m.nfwd, ws, lane, 0);
+        run_rules<false, false>(fwd_tab, m.fwd_level_step, m.fwd_level_comb, m.fwd_comb, m.nfwd, ws, lane);
 
         // ---- site energy (potential_mtp.cpp:2966-2970) and adjoint seed ----
         // (an MTP-M head: the head of the descriptors, its seeds per atom)
@@ -123,7 +123,7 @@ __global__ __launch_bounds__(kWave *kMaxWaves) void efs_kernel(DevModel m, DevNe
                 A[k] = L.seed[k];
         wave_sync();
 
-        run_rules<false, true>(bwd_tab, m.bwd_level_step, m.bwd_level_comb, m.bwd_comb, m.nbwd, ws, lane, 0);
+        run_rules<false, true>(bwd_tab, m.bwd_level_step, m.bwd_level_comb, m.bwd_comb, m.nbwd, ws, lane);
         if (lane == 0)
             for (int k = 0; k < m.ndup; ++k)
                 A[m.dup[2 * k + 1]] += A[m.dup[2 * k]];

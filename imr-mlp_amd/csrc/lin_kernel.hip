@@ -378,14 +378,14 @@ __global__ __launch_bounds__(kWave *kMaxWaves) void lin_jac_kernel(DevModel m, D
                 mom[m.dup[2 * k]] = mom[m.dup[2 * k + 1]];
         wave_sync();
         run_rules<false, false>(L.fwd_steps, L.fwd_level_step, L.fwd_level_comb, L.fwd_comb,
-                                L.nfwd, ws, lane, 0);
+                                L.nfwd, ws, lane);
         double *srow = g.site + (size_t)(i - g.a0) * m.S;
         for (int s = lane; s < m.S; s += kWave)
             srow[s] = mom[Ls.map[s]];
         for (int k = L.one + lane; k < L.L0 + L.nL; k += kWave)
             ws[k] = k == L.one ? 1.0 : 0.0;
         wave_sync();
-        run_rules<false, false>(L.steps, L.level_step, L.level_comb, L.comb, L.nlev, ws, lane, 0);
+        run_rules<false, false>(L.steps, L.level_step, L.level_comb, L.comb, L.nlev, ws, lane);
         double *lw = g.lw + (size_t)(i - g.a0) * L.nwalk;
         if (walk_regs) {
 #pragma unroll

@@ -1027,17 +1027,17 @@ bool build_plan(const Model &m, Plan &p, std::string &err)
     encode_tables(bwd, p.part0, p.dummy, adj, same, adj, p.bwd_steps, p.bwd_level_step,
                   p.bwd_comb, p.bwd_level_comb);
 
-    // Training work space: the E/F/S work space (without its transpose
-    // buffer), its dual copy (tangents and second adjoints), the wave's radial
-    // gradient accumulator and the species of the neighbours in flight.
-    // Three more buffers lie over blocks that are dead in the phase that
-    // uses them, where they fit: the first neighbour pass's transpose buffer
-    // over the adjoint block (written with the seeds later), the
-    // slot-ordered {A, G} stage over the moments (dead after the reverse
-    // rules) and the last pass's transpose buffer over the tangents (dead
-    // after the staging).
-    // Otherwise they get room of their own after the gradient accumulator.
-    p.tr_delta = p.red0;
+    // Training work space: the E/F/S work space without its transpose
+    // buffer with its dual copy (tangents and second adjoints) interleaved,
+    // element x's value and dual in doubles 2x and 2x + 1, then the wave's
+    // radial gradient accumulator and the species of the neighbours in
+    // flight.  Three more buffers lie over blocks that are dead in the phase
+    // that uses them, where they fit: the first neighbour pass's transpose
+    // buffer over the adjoint pairs (written with the seeds later), the
+    // slot-ordered {A, G} stage over the moment pairs (dead after the reverse
+    // rules) and the last pass's transpose buffer over the adjoint pairs
+    // (dead after the staging).  Otherwise they get room of their own after
+    // the gradient accumulator.
     p.tr_grad = 2 * p.red0;
     p.tr_ctype = p.tr_grad + ((m.nradial() + 3) & ~3);
     end = p.tr_ctype + kWave / 2;  // 64 ints: neighbour species of a batch
@@ -1049,9 +1049,10 @@ bool build_plan(const Model &m, Plan &p, std::string &err)
         }
         return own_red;
     };
-    p.tr_red1 = p.red0 - K4 >= RB ? K4 : red_region();
-    p.tr_red4 = p.red0 >= RB ? p.tr_delta : red_region();
-    if (2 * N4 <= K4) {
+    const bool over_adjoints = 2 * (p.red0 - K4) >= RB;
+    p.tr_red1 = over_adjoints ? 2 * K4 : red_region();
+    p.tr_red4 = over_adjoints ? 2 * K4 : red_region();
+    if (N4 <= K4) {
         p.tr_stage = 0;
     } else {
         p.tr_stage = end;

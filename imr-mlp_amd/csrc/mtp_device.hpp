@@ -727,27 +727,23 @@ __device__ __forceinline__ void bwd_shells(const DevModel &m, const double *As, 
 // their seeds) or written over it (outputs and partial sums, which start at
 // zero).  No task reads or writes another task's target within a level.
 //
-// kDual also carries a second copy of the work space `delta` doubles further
-// on: for a step  x_w += c x_l x_r  it adds  c (x'_l x_r + x_l x'_r)  to x'_w.
+// kDual carries a dual value beside every element: the work space holds
+// pairs {x, x'} (element x's value in double 2x, its dual in 2x + 1; the
+// tables' indices count pairs), read and written 16 bytes at a time, and
+// for a step  x_w += c x_l x_r  it adds  c (x'_l x_r + x_l x'_r)  to x'_w.
 // Forward entries then propagate tangents (Q_o += c (Q_l m_r + m_l Q_r));
 // reverse entries, whose l is an adjoint and r a moment, propagate the
 // adjoint of the tangent computation (G_x += c (G_o m_r + A_o Q_r)).
 // One group of up to four steps of a level (cnt of them applied).
-template <bool kDual, bool kInit>
-__device__ __forceinline__ void rule_group(const int2 (&e)[4], int cnt, double *ws, double *wd,
-                                           double &acc, double &acd)
+template <bool kInit>
+__device__ __forceinline__ void rule_group(const int2 (&e)[4], int cnt, double *ws, double &acc)
 {
     double ml[4], mr[4];
-    double dl[4], dr[4];
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
         const int l = e[k].x & 0xffff, r = (unsigned)e[k].x >> 16;
         ml[k] = ws[l];
         mr[k] = ws[r];
-        if constexpr (kDual) {
-            dl[k] = wd[l];
-            dr[k] = wd[r];
-        }
     }
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
@@ -755,16 +751,42 @@ __device__ __forceinline__ void rule_group(const int2 (&e)[4], int cnt, double *
             break;
         const double c = (double)(e[k].y >> 18);
         acc = fma(c * ml[k], mr[k], acc);
-        if constexpr (kDual)
-            acd = fma(c * ml[k], dr[k], fma(c * dl[k], mr[k], acd));
         if (e[k].y & 0x20000) {
             const int w = e[k].y & 0xffff;
             ws[w] = kInit ? ws[w] + acc : acc;
             acc = 0.0;
-            if constexpr (kDual) {
-                wd[w] = kInit ? wd[w] + acd : acd;
-                acd = 0.0;
+        }
+    }
+}
+
+// The same over {value, dual} pairs.
+template <bool kInit>
+__device__ __forceinline__ void rule_group_dual(const int2 (&e)[4], int cnt, double2 *wp,
+                                                double &acc, double &acd)
+{
+    double2 vl[4], vr[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        vl[k] = wp[e[k].x & 0xffff];
+        vr[k] = wp[(unsigned)e[k].x >> 16];
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        if (k >= cnt)
+            break;
+        const double c = (double)(e[k].y >> 18);
+        acc = fma(c * vl[k].x, vr[k].x, acc);
+        acd = fma(c * vl[k].x, vr[k].y, fma(c * vl[k].y, vr[k].x, acd));
+        if (e[k].y & 0x20000) {
+            const int w = e[k].y & 0xffff;
+            if (kInit) {
+                const double2 o = wp[w];
+                wp[w] = double2{o.x + acc, o.y + acd};
+            } else {
+                wp[w] = double2{acc, acd};
             }
+            acc = 0.0;
+            acd = 0.0;
         }
     }
 }
@@ -772,12 +794,18 @@ __device__ __forceinline__ void rule_group(const int2 (&e)[4], int cnt, double *
 template <bool kDual, bool kInit>
 __device__ __forceinline__ void run_rules(const int2 *tab, const int *level_step,
                                           const int *level_comb, const int4 *comb, int nlev,
-                                          double *ws, int lane, int delta)
+                                          double *ws, int lane)
 {
-    double *wd = ws + delta;
+    double2 *wp = reinterpret_cast<double2 *>(ws);
     for (int L = 0; L < nlev; ++L) {
         const int s0 = level_step[L], s1 = level_step[L + 1];
         double acc = 0.0, acd = 0.0;
+        auto group = [&](const int2(&e)[4], int cnt) {
+            if constexpr (kDual)
+                rule_group_dual<kInit>(e, cnt, wp, acc, acd);
+            else
+                rule_group<kInit>(e, cnt, ws, acc);
+        };
         if (s1 > s0) {
             const int2 *t = tab + (size_t)s0 * kWave + lane;
             int2 e[4] = {t[0], t[kWave], t[2 * kWave], t[3 * kWave]};
@@ -785,30 +813,35 @@ __device__ __forceinline__ void run_rules(const int2 *tab, const int *level_step
             for (; st + 4 < s1; st += 4) {
                 const int2 *u = t + (size_t)(st + 4 - s0) * kWave;
                 const int2 nx[4] = {u[0], u[kWave], u[2 * kWave], u[3 * kWave]};
-                rule_group<kDual, kInit>(e, 4, ws, wd, acc, acd);
+                group(e, 4);
 #pragma unroll
                 for (int k = 0; k < 4; ++k)
                     e[k] = nx[k];
             }
-            rule_group<kDual, kInit>(e, s1 - st, ws, wd, acc, acd);
+            group(e, s1 - st);
         }
         const int c0 = level_comb[L], c1 = level_comb[L + 1];
         if (c1 > c0) {
             wave_sync();
             for (int c = c0 + lane; c < c1; c += kWave) {
                 const int4 q = comb[c];
-                double sum = ws[q.x], sud = kDual ? wd[q.x] : 0.0;
-                for (int k = 0; k < q.z; ++k) {
-                    sum += ws[q.y + k];
-                    ws[q.y + k] = 0.0;
-                    if constexpr (kDual) {
-                        sud += wd[q.y + k];
-                        wd[q.y + k] = 0.0;
+                if constexpr (kDual) {
+                    double2 sum = wp[q.x];
+                    for (int k = 0; k < q.z; ++k) {
+                        const double2 v = wp[q.y + k];
+                        sum.x += v.x;
+                        sum.y += v.y;
+                        wp[q.y + k] = double2{0.0, 0.0};
                     }
+                    wp[q.x] = sum;
+                } else {
+                    double sum = ws[q.x];
+                    for (int k = 0; k < q.z; ++k) {
+                        sum += ws[q.y + k];
+                        ws[q.y + k] = 0.0;
+                    }
+                    ws[q.x] = sum;
                 }
-                ws[q.x] = sum;
-                if constexpr (kDual)
-                    wd[q.x] = sud;
             }
         }
         wave_sync();

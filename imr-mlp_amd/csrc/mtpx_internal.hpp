@@ -265,15 +265,15 @@ struct Plan {
     //   [0, K4) moments | [K4, 2 K4) adjoints | dummy (a zero slot) |
     //   [part0, red0) partial sums | [red0, priv_doubles) transpose buffer.
     int K4 = 0, dummy = 0, part0 = 0, red0 = 0, priv_doubles = 0;
-    // Training work space (doubles): [0, tr_delta) the E/F/S work space
-    // without its transpose buffer, [tr_delta, tr_grad) its dual copy, the
-    // radial gradient accumulator (tr_grad, nradial) and 64 neighbour species
-    // (tr_ctype, as ints).  The transpose buffers of the first and the last
-    // neighbour pass (tr_red1, tr_red4) and the slot-ordered {A, G} pairs
-    // (tr_stage, nslots4) lie over blocks that are dead in their phase, or
-    // after the species where they do not fit there.
-    int tr_delta = 0, tr_red1 = 0, tr_red4 = 0, tr_stage = 0, tr_grad = 0, tr_ctype = 0,
-        tr_priv = 0;
+    // Training work space (doubles): [0, tr_grad) the E/F/S work space
+    // without its transpose buffer and its dual copy as pairs (element x at
+    // 2x, its dual at 2x + 1), the radial gradient accumulator (tr_grad,
+    // nradial) and 64 neighbour species (tr_ctype, as ints).  The transpose
+    // buffers of the first and the last neighbour pass (tr_red1, tr_red4) and
+    // the slot-ordered {A, G} pairs (tr_stage, nslots4) lie over blocks that
+    // are dead in their phase, or after the species where they do not fit
+    // there.
+    int tr_red1 = 0, tr_red4 = 0, tr_stage = 0, tr_grad = 0, tr_ctype = 0, tr_priv = 0;
     // E/F/S kernel: transpose buffer, slot-ordered adjoints, the wave's
     // energy/virial sums and, with an MTP-M head, the head's work space
     // (descriptors, their adjoints, hidden activations and derivatives, the
@@ -372,7 +372,7 @@ struct DevModel {
     const int *dup;         // [ndup][2]
     int max_partials;
     int K4, dummy, part0, red0, priv_doubles;  // per-wave work space (Plan)
-    int tr_delta, tr_red1, tr_red4, tr_stage, tr_grad, tr_ctype, tr_priv;
+    int tr_red1, tr_red4, tr_stage, tr_grad, tr_ctype, tr_priv;
     int efs_red, efs_stage, efs_acc;
     // MTP-M head (kHeadNone: the linear MTP of species, moment and seed),
     // the per-wave head work space (offset in doubles) and the head itself

@@ -257,10 +257,12 @@ __device__ __forceinline__ GradNbr pair_weight(const DevNeighbors &nb, const Tra
     return g;
 }
 
+// Rows of the first pass alternate m and q of one slot; the sums go to the
+// pair of the slot's basic moment (m at 2b, q at 2b + 1).
 struct DualCtx {
     double *red, *ws;
     const int *slot_basic;
-    int lane, row, delta;
+    int lane, row;
 };
 
 // Powers u_x^k, u_y^k, u_z^k for k = 0 .. N: every monomial of every shell
@@ -308,7 +310,7 @@ __device__ __forceinline__ void fwd_dual_shells(const DevModel &m, DualCtx &cx,
         reduce_rows(cx.red, kChunk, cx.row - kChunk, cx.lane, [&](int r, double acc) {
             const int b = cx.slot_basic[r >> 1];
             if (b >= 0)
-                cx.ws[b + ((r & 1) ? cx.delta : 0)] += acc;
+                cx.ws[2 * b + (r & 1)] += acc;
         });
     };
 #pragma unroll
@@ -380,7 +382,8 @@ __global__ __launch_bounds__(kWave *kMaxWaves) void grad_kernel(DevModel m, DevN
     const int nwaves = blockDim.x / kWave;
     const Shared L = shared_layout(m, lds, false);  // seeds are read from global memory
     double *ws = lds + shared_doubles(m, kTabLds, false) + (size_t)wave * m.tr_priv;
-    double *wd = ws + m.tr_delta;  // tangents Q, second adjoints G
+    // {value, dual} pairs: {m, Q} for the moments, {A, G} for the adjoints
+    double2 *wp = reinterpret_cast<double2 *>(ws);
     double *red1 = ws + m.tr_red1, *red4 = ws + m.tr_red4;
     double2 *AG = reinterpret_cast<double2 *>(ws + m.tr_stage);
     double *grad = ws + m.tr_grad;  // radial part of the gradient
@@ -390,10 +393,8 @@ __global__ __launch_bounds__(kWave *kMaxWaves) void grad_kernel(DevModel m, DevN
     int *ctype = reinterpret_cast<int *>(ws + m.tr_ctype);
 
     stage_shared(m, L, kTabLds, tid, blockDim.x);
-    for (int k = m.dummy + lane; k < m.red0; k += kWave) {
-        ws[k] = 0.0;
-        wd[k] = 0.0;
-    }
+    for (int k = m.dummy + lane; k < m.red0; k += kWave)
+        wp[k] = double2{0.0, 0.0};
     for (int k = lane; k < m.nradial; k += kWave)
         grad[k] = 0.0;
     for (int k = m.nradial + lane; k < m.ncoef; k += kWave)
@@ -416,15 +417,13 @@ __global__ __launch_bounds__(kWave *kMaxWaves) void grad_kernel(DevModel m, DevN
 #pragma unroll
         for (int a = 0; a < 3; ++a)
             fi[a] = t.dLdF[3 * (size_t)i + a];
-        for (int k = lane; k < m.K; k += kWave) {
-            ws[k] = 0.0;
-            wd[k] = 0.0;
-        }
+        for (int k = lane; k < m.K; k += kWave)
+            wp[k] = double2{0.0, 0.0};
         wave_sync();
 
         // ---- 1. basic moments and their tangents ----------------------------
         for (int base = 0; base < n; base += kWave) {
-            DualCtx cx{red1, ws, L.slot_basic, lane, 0, m.tr_delta};
+            DualCtx cx{red1, ws, L.slot_basic, lane, 0};
             Nbr<P::M> q;
             const bool valid = lane < n - base;
             const int64_t p = beg + base + lane;
@@ -438,27 +437,23 @@ __global__ __launch_bounds__(kWave *kMaxWaves) void grad_kernel(DevModel m, DevN
                 reduce_rows(red1, rest, cx.row - rest, lane, [&](int r, double acc) {
                     const int b = L.slot_basic[r >> 1];
                     if (b >= 0)
-                        ws[b + ((r & 1) ? m.tr_delta : 0)] += acc;
+                        ws[2 * b + (r & 1)] += acc;
                 });
         }
         if (lane == 0)
-            for (int k = 0; k < m.ndup; ++k) {
-                ws[m.dup[2 * k]] = ws[m.dup[2 * k + 1]];
-                wd[m.dup[2 * k]] = wd[m.dup[2 * k + 1]];
-            }
+            for (int k = 0; k < m.ndup; ++k)
+                wp[m.dup[2 * k]] = wp[m.dup[2 * k + 1]];
         // the zero slots and partial sums may lie under a transpose buffer
-        for (int k = m.dummy + lane; k < m.red0; k += kWave) {
-            ws[k] = 0.0;
-            wd[k] = 0.0;
-        }
+        for (int k = m.dummy + lane; k < m.red0; k += kWave)
+            wp[k] = double2{0.0, 0.0};
         wave_sync();
 
         // ---- 2. rules forward with tangents; moment and species gradient ----
-        run_rules<true, false>(fwd_tab, m.fwd_level_step, m.fwd_level_comb, m.fwd_comb, m.nfwd, ws, lane,
-                        m.tr_delta);
+        run_rules<true, false>(fwd_tab, m.fwd_level_step, m.fwd_level_comb, m.fwd_comb, m.nfwd, ws,
+                               lane);
         for (int s = lane; s < m.S; s += kWave) {
-            const int x = L.map[s];
-            grow[m.nradial + m.Z + s] += se * ws[x] + wd[x];
+            const double2 x = wp[L.map[s]];
+            grow[m.nradial + m.Z + s] += se * x.x + x.y;
         }
         if (lane == 0)
             grow[m.nradial + ti] += se;
@@ -466,23 +461,23 @@ __global__ __launch_bounds__(kWave *kMaxWaves) void grad_kernel(DevModel m, DevN
         // ---- 3. reverse rules: A with seeds xi, G with seeds dLdE xi --------
         for (int k = lane; k < m.K; k += kWave) {
             const double sd = m.seed[k];
-            ws[m.K4 + k] = sd;
-            wd[m.K4 + k] = se * sd;
+            wp[m.K4 + k] = double2{sd, se * sd};
         }
         wave_sync();
-        run_rules<true, true>(bwd_tab, m.bwd_level_step, m.bwd_level_comb, m.bwd_comb, m.nbwd, ws, lane,
-                        m.tr_delta);
+        run_rules<true, true>(bwd_tab, m.bwd_level_step, m.bwd_level_comb, m.bwd_comb, m.nbwd, ws,
+                              lane);
         if (lane == 0)
             for (int k = 0; k < m.ndup; ++k) {
-                ws[m.K4 + m.dup[2 * k + 1]] += ws[m.K4 + m.dup[2 * k]];
-                wd[m.K4 + m.dup[2 * k + 1]] += wd[m.K4 + m.dup[2 * k]];
+                const double2 v = wp[m.K4 + m.dup[2 * k]];
+                double2 &t = wp[m.K4 + m.dup[2 * k + 1]];
+                t = double2{t.x + v.x, t.y + v.y};
             }
         wave_sync();
-        // slot-ordered {A, G} (the stage may lie over the moments, which are
-        // no longer read; A and G are not under it)
+        // slot-ordered {A, G} (the stage may lie over the moment pairs, which
+        // are no longer read; the adjoint pairs are not under it)
         for (int s = lane; s < m.nslots; s += kWave) {
             const int b = L.slot_basic[s];
-            AG[s] = b >= 0 ? double2{ws[m.K4 + b], wd[m.K4 + b]} : double2{0.0, 0.0};
+            AG[s] = b >= 0 ? wp[m.K4 + b] : double2{0.0, 0.0};
         }
         wave_sync();
 
