@@ -588,7 +588,7 @@ def main():
     # "total": neighbour build from host positions + E/F/S (fastfit total_ns_atom)
     ctx.set_timings(False)
     tot = []
-    for _ in range(5):
+    for _ in range(20):
         t1 = time.perf_counter()
         ctx.build_neighbors(s.cell, s.pbc, pos, s.types, cutoff)
         ctx.efs_device(det)
