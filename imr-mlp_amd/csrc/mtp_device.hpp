@@ -715,25 +715,6 @@ __device__ __forceinline__ void bwd_shells(const DevModel &m, const double *As, 
     }
 }
 
-// Product rules from a lane-major step table (forward: potential_mtp.cpp:
-// 2918-2924; reverse: backpropagate_moments, :3292-3305), one dependency
-// level at a time.  Steps are taken in groups of four: the entries of the
-// next group are loaded while the current one runs, and every operand of a
-// group is read before any of its results is written (a level never reads
-// what it writes).  A level's last group holds its last one to four steps;
-// the entries it loads past the level (the next level's, or the padding
-// after the last level) are read but not applied.  A task's sum starts from zero and is stored on the
-// task's last entry: added to its target (kInit: adjoints, which start from
-// their seeds) or written over it (outputs and partial sums, which start at
-// zero).  No task reads or writes another task's target within a level.
-//
-// kDual carries a dual value beside every element: the work space holds
-// pairs {x, x'} (element x's value in double 2x, its dual in 2x + 1; the
-// tables' indices count pairs), read and written 16 bytes at a time, and
-// for a step  x_w += c x_l x_r  it adds  c (x'_l x_r + x_l x'_r)  to x'_w.
-// Forward entries then propagate tangents (Q_o += c (Q_l m_r + m_l Q_r));
-// reverse entries, whose l is an adjoint and r a moment, propagate the
-// adjoint of the tangent computation (G_x += c (G_o m_r + A_o Q_r)).
 // One group of up to four steps of a level (cnt of them applied).
 template <bool kInit>
 __device__ __forceinline__ void rule_group(const int2 (&e)[4], int cnt, double *ws, double &acc)
@@ -791,6 +772,26 @@ __device__ __forceinline__ void rule_group_dual(const int2 (&e)[4], int cnt, dou
     }
 }
 
+// Product rules from a lane-major step table (forward: potential_mtp.cpp:
+// 2918-2924; reverse: backpropagate_moments, :3292-3305), one dependency
+// level at a time.  Steps are taken in groups of four: the entries of the
+// next group are loaded while the current one runs, and every operand of a
+// group is read before any of its results is written (a level never reads
+// what it writes).  A level's last group holds its last one to four steps;
+// the entries it loads past the level (the next level's, or the padding
+// after the last level) are read but not applied.  A task's sum starts
+// from zero and is stored on the task's last entry: added to its target
+// (kInit: adjoints, which start from their seeds) or written over it
+// (outputs and partial sums, which start at zero).  No task reads or writes
+// another task's target within a level.
+//
+// kDual carries a dual value beside every element: the work space holds
+// pairs {x, x'} (element x's value in double 2x, its dual in 2x + 1; the
+// tables' indices count pairs), read and written 16 bytes at a time, and
+// for a step  x_w += c x_l x_r  it adds  c (x'_l x_r + x_l x'_r)  to x'_w.
+// Forward entries then propagate tangents (Q_o += c (Q_l m_r + m_l Q_r));
+// reverse entries, whose l is an adjoint and r a moment, propagate the
+// adjoint of the tangent computation (G_x += c (G_o m_r + A_o Q_r)).
 template <bool kDual, bool kInit>
 __device__ __forceinline__ void run_rules(const int2 *tab, const int *level_step,
                                           const int *level_comb, const int4 *comb, int nlev,
