@@ -244,3 +244,110 @@ def _check_lin_chunks(text):
     consecutive = sum(len(set().union(*(slots_of[q] for q in range(a, min(a + 6, S)))))
                       for a in range(0, S, 6))
     assert formed < consecutive
+
+
+@pytest.fixture(scope="module")
+def rule_dump(tmp_path_factory):
+    """tests/rule_tables_dump.cpp built against the library's plan code."""
+    import os
+    import shutil
+    import subprocess
+    hipcc = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+    if not os.path.exists(hipcc):
+        pytest.skip("hipcc is not available")
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    pkg = os.path.join(root, "imr-mlp_amd")
+    exe = str(tmp_path_factory.mktemp("rules") / "rule_tables_dump")
+    subprocess.run([hipcc, "-O1", "-std=c++17", "-w", "-I", os.path.join(root, "include"),
+                    "-I", os.path.join(pkg, "csrc"),
+                    os.path.join(root, "tests", "rule_tables_dump.cpp"),
+                    os.path.join(pkg, "csrc", "model.cpp"), os.path.join(pkg, "csrc", "metadata.cpp"),
+                    "-o", exe], check=True)
+    return root, exe
+
+
+def _replay(ws, tab, init):
+    """The rule tables applied level by level as the kernels apply them: a
+    level's operands are read as they stood when the level began, a task's
+    sum goes to its target on the task's last entry, then the level's
+    combines add the partial sums in order and clear them."""
+    nlev, ls, lc, steps, comb = tab
+    for L in range(nlev):
+        snap = ws.copy()
+        for q in range(64):
+            acc = 0.0
+            for st in range(ls[L], ls[L + 1]):
+                x, y = steps[st * 64 + q]
+                acc += (y >> 18) * snap[x & 0xFFFF] * snap[x >> 16]
+                if (y >> 17) & 1:
+                    w = y & 0xFFFF
+                    ws[w] = ws[w] + acc if init else acc
+                    acc = 0.0
+        for tgt, first, cnt in comb[lc[L]:lc[L + 1]]:
+            s = ws[tgt]
+            for j in range(cnt):
+                s += ws[first + j]
+                ws[first + j] = 0.0
+            ws[tgt] = s
+
+
+@pytest.mark.parametrize("name", ["shapeev-10.mtp", "shapeev-16.mtp", "shapeev-20.mtp",
+                                  "pot4b.mtp"])
+def test_rule_tables_apply_the_product_rules(rule_dump, name):
+    """The lane-major rule tables: each level is as long as its longest lane
+    (no step of padding alone), the padding steps after the last level read
+    and write the zero slot only, and the tables replayed on random basic
+    moments and seeds give the moments of the product rules in file order
+    (potential_mtp.cpp:2918-2924) and the adjoints of backpropagate_moments
+    (:3292-3305, reverse file order)."""
+    import os
+    import subprocess
+    root, exe = rule_dump
+    out = subprocess.run([exe, os.path.join("tests", "golden", "templates", name)], cwd=root,
+                         check=True, capture_output=True, text=True).stdout
+    v = [int(t) for t in out.split()]
+    K, B, T, K4, dummy, part0, red0, pad = v[:8]
+    pos = 8
+    times = np.array(v[pos:pos + 4 * T]).reshape(T, 4)
+    pos += 4 * T
+    tabs = []
+    for _ in range(2):
+        nlev, ncomb, nsteps = v[pos:pos + 3]
+        pos += 3
+        ls = v[pos:pos + nlev + 1]
+        pos += nlev + 1
+        lc = v[pos:pos + nlev + 1]
+        pos += nlev + 1
+        steps = [(v[pos + 2 * i], v[pos + 2 * i + 1]) for i in range(nsteps * 64)]
+        pos += 2 * nsteps * 64
+        comb = [tuple(v[pos + 3 * i:pos + 3 * i + 3]) for i in range(ncomb)]
+        pos += 3 * ncomb
+        assert nsteps == ls[-1] + pad
+        pad_entry = (dummy | dummy << 16, dummy | 1 << 16)
+        assert all(s == pad_entry for s in steps[ls[-1] * 64:])
+        for L in range(nlev):
+            if ls[L + 1] > ls[L]:
+                last = steps[(ls[L + 1] - 1) * 64:ls[L + 1] * 64]
+                assert any(s != pad_entry for s in last)
+        tabs.append((nlev, ls, lc, steps, comb))
+    assert pos == len(v)
+
+    rng = np.random.default_rng(11)
+    ws = np.zeros(red0)
+    ws[:B] = rng.uniform(0.5, 1.5, B)
+    m = ws[:K].copy()
+    for l, r, c, o in times:
+        m[o] += c * m[l] * m[r]
+    _replay(ws, tabs[0], init=False)
+    assert np.allclose(ws[:K], m, rtol=1e-12, atol=1e-12 * np.abs(m).max())
+    assert not ws[dummy] and not ws[part0:red0].any()
+
+    seed = rng.uniform(-1.0, 1.0, K)
+    ws[K4:K4 + K] = seed
+    A = seed.copy()
+    for l, r, c, o in times[::-1]:
+        A[r] += c * A[o] * m[l]
+        A[l] += c * A[o] * m[r]
+    _replay(ws, tabs[1], init=True)
+    assert np.allclose(ws[K4:K4 + K], A, rtol=1e-11, atol=1e-12 * np.abs(A).max())
+    assert not ws[dummy] and not ws[part0:red0].any()
