@@ -287,17 +287,17 @@ __global__ __launch_bounds__(256) void force_gather_kernel(DevNeighbors nb, cons
 // mirror's slot), onto the own force the kernel stored.  Sixteen lanes per
 // atom stride over its entries (contiguous reads) and sum over their row
 // (DPP), so the order is fixed and the result repeatable.
-// The last workgroup reduces the per-wave partials instead (one launch for
-// both).
+// The first workgroup reduces the per-wave partials instead (one launch for
+// both; dispatched first, its dependent loads overlap the gather).
 __global__ __launch_bounds__(256) void mirror_gather_kernel(DevNeighbors nb, const double *Dm,
                                                             double *forces, const double *partial,
                                                             int nrows, double *out10)
 {
-    if (blockIdx.x == gridDim.x - 1) {
+    if (blockIdx.x == 0) {
         partial_reduce(partial, nrows, out10);
         return;
     }
-    const int t = blockIdx.x * blockDim.x + threadIdx.x;
+    const int t = (blockIdx.x - 1) * blockDim.x + threadIdx.x;
     const int a = t >> 4, l = t & 15;
     double f0 = 0.0, f1 = 0.0, f2 = 0.0;
     if (a < nb.n) {
