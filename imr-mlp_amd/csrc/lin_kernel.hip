@@ -635,17 +635,22 @@ __global__ __launch_bounds__(kWave) void lin_tile_kernel(DevModel m, DevLin L, D
 #if MTPX_LIN_PART == 1
 // Energy components of a group's structures: ordered sums of the sites'
 // scalar moments over each structure's atoms, and the species counts.
+// Threads [0, nc S) take the sums, one per (structure, scalar), and the
+// next nc Z the counts, so no wave runs both loops.
 __global__ __launch_bounds__(256) void lin_reduce_kernel(int S, int Z, int p, const int *soff,
                                                          const int *center_type, LinGroup g,
                                                          double *ec)
 {
-    const int w = S + Z;
+    const int64_t nc = g.c1 - g.c0;
     const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (t >= (int64_t)(g.c1 - g.c0) * w)
+    if (t >= nc * (S + Z))
         return;
-    const int c = g.c0 + (int)(t / w), r = (int)(t % w);
+    const bool sum = t < nc * S;
+    const int64_t u = sum ? t : t - nc * S;
+    const int c = g.c0 + (int)(sum ? u / S : u / Z);
+    const int r = sum ? (int)(u % S) : S + (int)(u % Z);
     const int i0 = soff[c], i1 = soff[c + 1];
-    if (r < S) {
+    if (sum) {
         // loads of several atoms in flight; the sum stays in atom order
         const double *src = g.site + (size_t)(i0 - g.a0) * S + r;
         const size_t st = (size_t)S;
@@ -665,8 +670,17 @@ __global__ __launch_bounds__(256) void lin_reduce_kernel(int S, int Z, int p, co
         ec[(size_t)c * p + Z + r] = acc;
     } else {
         const int sp = r - S;
-        int cnt = 0;
-        for (int i = i0; i < i1; ++i)
+        int cnt = 0, i = i0;
+        for (; i + 8 <= i1; i += 8) {  // eight loads in flight
+            int v[8];
+#pragma unroll
+            for (int k = 0; k < 8; ++k)
+                v[k] = center_type[i + k];
+#pragma unroll
+            for (int k = 0; k < 8; ++k)
+                cnt += v[k] == sp;
+        }
+        for (; i < i1; ++i)
             cnt += center_type[i] == sp;
         ec[(size_t)c * p + sp] = (double)cnt;
     }
