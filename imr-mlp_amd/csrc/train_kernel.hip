@@ -131,28 +131,43 @@ __global__ __launch_bounds__(kWave) void loss_kernel(LossArgs a)
     row[6] = sqs;
 }
 
-// Ordered column sums of a [rows][cols] array (metrics, gradient rows).
+// Ordered column sums of a [rows][cols] array (metrics, gradient rows).  A
+// workgroup takes kRowCols columns; its kRowGroups row groups each sum a
+// contiguous run of rows in row order (eight loads in flight), and the
+// group sums are added in group order, so the result is the same bits on
+// every run.
+constexpr int kRowCols = 16, kRowGroups = 16;
 __global__ __launch_bounds__(256) void rows_reduce_kernel(const double *rows, int nrows, int cols,
                                                           double *out, int accumulate)
 {
-    const int k = blockIdx.x * blockDim.x + threadIdx.x;
-    if (k >= cols)
-        return;
-    // loads of eight rows in flight; the sum stays in row order
+    __shared__ double part[kRowGroups][kRowCols];
+    const int c = threadIdx.x % kRowCols, g = threadIdx.x / kRowCols;
+    const int k = blockIdx.x * kRowCols + c;
+    const int per = (nrows + kRowGroups - 1) / kRowGroups;
+    const int r1 = min(nrows, (g + 1) * per);
     double s = 0.0;
-    int r = 0;
-    for (; r + 8 <= nrows; r += 8) {
-        double v[8];
+    if (k < cols) {
+        int r = g * per;
+        for (; r + 8 <= r1; r += 8) {
+            double v[8];
 #pragma unroll
-        for (int q = 0; q < 8; ++q)
-            v[q] = rows[(size_t)(r + q) * cols + k];
+            for (int q = 0; q < 8; ++q)
+                v[q] = rows[(size_t)(r + q) * cols + k];
 #pragma unroll
-        for (int q = 0; q < 8; ++q)
-            s += v[q];
+            for (int q = 0; q < 8; ++q)
+                s += v[q];
+        }
+        for (; r < r1; ++r)
+            s += rows[(size_t)r * cols + k];
     }
-    for (; r < nrows; ++r)
-        s += rows[(size_t)r * cols + k];
-    out[k] = accumulate ? out[k] + s : s;
+    part[g][c] = s;
+    __syncthreads();
+    if (g == 0 && k < cols) {
+        double t = part[0][c];
+        for (int q = 1; q < kRowGroups; ++q)
+            t += part[q][c];
+        out[k] = accumulate ? out[k] + t : t;
+    }
 }
 
 // ---- gradient kernel ---------------------------------------------------
@@ -577,8 +592,8 @@ hipError_t launch_rows_reduce(const double *rows, int nrows, int cols, double *o
                               hipStream_t s)
 {
     if (cols > 0)
-        hipLaunchKernelGGL(rows_reduce_kernel, dim3((cols + 255) / 256), dim3(256), 0, s, rows,
-                           nrows, cols, out, accumulate ? 1 : 0);
+        hipLaunchKernelGGL(rows_reduce_kernel, dim3((cols + kRowCols - 1) / kRowCols), dim3(256),
+                           0, s, rows, nrows, cols, out, accumulate ? 1 : 0);
     return hipGetLastError();
 }
 
